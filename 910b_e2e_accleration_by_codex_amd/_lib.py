@@ -1,0 +1,99 @@
+"""ctypes binding of libgdn_mi355x.so, the C-ABI HIP library (declared in include/gdn_mi355x.h).
+
+torch is imported first so that the HIP runtime torch ships is the one already loaded in the
+process; the library then binds to it by soname, and the raw stream handles torch hands out are
+valid for it.  There is no CPU fallback: if the library is missing or no GPU is visible every op
+raises.
+"""
+import ctypes
+import os
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libgdn_mi355x.so")
+
+F32, BF16 = 0, 1
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_L = ctypes.c_int64
+_F = ctypes.c_float
+
+_SIGNATURES = {
+    "gdn_version": ([], _I),
+    "gdn_last_error": ([], ctypes.c_char_p),
+    "gdn_limits": ([_P, _P, _P], _I),
+    "gdn_recurrent_step": ([_P, _L, _P, _L, _P, _L, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P], _I),
+    "gdn_conv_update": ([_P, _L, _P, _P, _P, _P, _L, _I, _I, _I, _P], _I),
+    "gdn_gated_rmsnorm": ([_P, _L, _P, _L, _P, _I, _P, _L, _I, _F, _P], _I),
+    "gdn_decode_fused": ([_P, _L, _P, _L, _P, _P, _L, _P, _P, _P, _P, _P, _P, _I, _F, _P, _P, _I, _I, _I,
+                          _I, _I, _P], _I),
+    "gdn_unit_lower_inv": ([_P, _P, _L, _I, _P], _I),
+    "gdn_chunk_prefill": ([_P, _L, _P, _L, _P, _L, _P, _P, _I, _P, _P, _P, _L, _P, _I, _I, _I, _I, _I, _I,
+                           _I, _P], _I),
+    "gdn_conv_prefill": ([_P, _L, _P, _P, _P, _P, _P, _L, _P, _I, _I, _I, _I, _P], _I),
+    "gdn_gating": ([_P, _P, _L, _P, _P, _P, _P, _L, _I, _P], _I),
+}
+
+_lib = None
+
+
+class GDNError(RuntimeError):
+    """A C-ABI call of the HIP library returned an error code."""
+
+
+def lib():
+    """Load the library once (raises if it was not built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise GDNError(f"{LIB_PATH} is missing: build it first (__graft_entry__.build() or "
+                           f"python -m <package>.build); there is no CPU fallback")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (args, res) in _SIGNATURES.items():
+            fn = getattr(handle, name, None)
+            if fn is None:
+                continue
+            fn.argtypes = args
+            fn.restype = res
+        _lib = handle
+    return _lib
+
+
+def exported_symbols():
+    """Names from the signature table that the loaded library exports."""
+    h = lib()
+    return [n for n in _SIGNATURES if getattr(h, n, None) is not None]
+
+
+def call(name, *args):
+    """Call a C-ABI entry point; raise GDNError with the library's message on failure."""
+    fn = getattr(lib(), name)
+    rc = fn(*args)
+    if rc != 0:
+        msg = lib().gdn_last_error().decode(errors="replace")
+        raise GDNError(f"{name} failed (code {rc}): {msg}")
+
+
+def stream_of(t):
+    """Raw hipStream_t of torch's current stream on t's device."""
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def dtype_code(t):
+    if t.dtype == torch.float32:
+        return F32
+    if t.dtype == torch.bfloat16:
+        return BF16
+    raise TypeError(f"unsupported dtype {t.dtype} (float32 or bfloat16)")
+
+
+def require_cuda(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("GDN HIP ops need tensors on a ROCm GPU device (no CPU fallback)")

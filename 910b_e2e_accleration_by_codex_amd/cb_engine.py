@@ -1,0 +1,213 @@
+"""GDN pieces of the continuous-batching engine on the HIP library.
+
+Mirrors the hot-path parts of the reference engine (src/cb_engine.py):
+  * ``elem_conv_update``      -- src/cb_engine.py:43-51 (decode conv, state shifted in place)
+  * ``causal_conv1d_update``  -- HF name of the same update (HF modeling_qwen3_5.py:200-217)
+  * ``gated_rmsnorm`` / ``fused_gated_rmsnorm`` -- src/cb_engine.py:65-67 (HF formula, HF:175-184)
+  * ``patch_model``           -- src/cb_engine.py:54-77
+  * ``gdn_decode_core``       -- the fused middle of CBEngine._gdn (src/cb_engine.py:325-351)
+  * ``GDNSlots`` / ``gdn_decode_layer`` / ``GDNDecodeGraph`` -- the slot-state layout
+    (src/cb_engine.py:103-113), the decode layer (src/cb_engine.py:318-352) and the graph-captured
+    decode step (src/cb_engine.py:123-187) restricted to the GDN layers.
+Layouts are the reference's: conv state [N, C, K] bf16, recurrent state [N, H_v, d_k, d_v] fp32.
+"""
+import torch
+
+from . import _lib
+from .recurrent_single_step import recurrent_single_step
+
+# The decode conv is always the mul+sum window form (the reference's --elem-conv, cb_run.py:98,160).
+ELEM_CONV = True
+
+
+def _row_view(x2d):
+    """[rows, C] with unit inner stride; returns (tensor, row stride)."""
+    if x2d.stride(-1) != 1:
+        x2d = x2d.contiguous()
+    return x2d, x2d.stride(0)
+
+
+def elem_conv_update(x, state, weight, bias):
+    """x [n,C,1] bf16, state [n,C,K] bf16 (updated in place), weight [C,K] bf16, bias [C] | None.
+    Returns silu(conv) [n,C,1] in x.dtype.  src/cb_engine.py:43-51."""
+    _lib.require_cuda(x, state, weight, bias)
+    n, C, T = x.shape
+    if T != 1:
+        raise ValueError("elem_conv_update: one token per call (x [n,C,1])")
+    K = weight.shape[-1]
+    if tuple(state.shape) != (n, C, K) or tuple(weight.shape) != (C, K):
+        raise ValueError(f"elem_conv_update: state {tuple(state.shape)} / weight {tuple(weight.shape)} "
+                         f"do not match x {tuple(x.shape)}")
+    if not (x.dtype == state.dtype == weight.dtype == torch.bfloat16):
+        raise TypeError("elem_conv_update: x, state and weight must be bfloat16")
+    if not state.is_contiguous():
+        raise ValueError("elem_conv_update: state must be contiguous (it is updated in place)")
+    if bias is not None:
+        bias = bias.to(torch.bfloat16).contiguous()
+    weight = weight.contiguous()
+    xr, xs = _row_view(x[:, :, 0])
+    out = torch.empty(n, C, 1, dtype=x.dtype, device=x.device)
+    _lib.call("gdn_conv_update", _lib.ptr(xr), xs, _lib.ptr(state), _lib.ptr(weight), _lib.ptr(bias),
+              _lib.ptr(out), C, n, C, K, _lib.stream_of(x))
+    return out
+
+
+def causal_conv1d_update(hidden_states, conv_state, weight, bias=None, activation=None):
+    """HF's decode conv update contract (HF:200-217) on the elem_conv_update kernel.  Several new
+    tokens are applied one after another, which gives HF's outputs and final state."""
+    if activation not in ("silu", "swish"):
+        raise NotImplementedError("causal_conv1d_update: only the SiLU activation is fused")
+    T = hidden_states.shape[-1]
+    if T == 1:
+        return elem_conv_update(hidden_states, conv_state, weight, bias)
+    return torch.cat([elem_conv_update(hidden_states[:, :, t:t + 1], conv_state, weight, bias)
+                      for t in range(T)], dim=-1)
+
+
+def gated_rmsnorm(hidden_states, gate, weight, eps=1e-6):
+    """silu(gate) * (weight * bf16(x * rsqrt(mean(x^2) + eps))) over the last dim, HF order
+    (HF:175-184).  hidden_states, gate [..., D] bf16; weight [D] bf16 or fp32."""
+    _lib.require_cuda(hidden_states, gate, weight)
+    if hidden_states.dtype != torch.bfloat16 or gate.dtype != torch.bfloat16:
+        raise TypeError("gated_rmsnorm: hidden_states and gate must be bfloat16")
+    D = hidden_states.shape[-1]
+    if gate.shape != hidden_states.shape or weight.shape != (D,):
+        raise ValueError("gated_rmsnorm: gate must match hidden_states and weight must be [D]")
+    x, xs = _row_view(hidden_states.reshape(-1, D))
+    z, zs = _row_view(gate.reshape(-1, D))
+    w = weight.contiguous()
+    out = torch.empty(hidden_states.shape, dtype=hidden_states.dtype, device=hidden_states.device)
+    _lib.call("gdn_gated_rmsnorm", _lib.ptr(x), xs, _lib.ptr(z), zs, _lib.ptr(w), _lib.dtype_code(w),
+              _lib.ptr(out), x.shape[0], D, float(eps), _lib.stream_of(x))
+    return out
+
+
+def fused_gated_rmsnorm(self, hidden_states, gate=None):
+    """Bound onto Qwen3_5RMSNormGated modules by patch_model (src/cb_engine.py:65-67)."""
+    return gated_rmsnorm(hidden_states, gate, self.weight, self.variance_epsilon)
+
+
+def gdn_decode_core(mixed, z, a, b, conv_state, conv_weight, A_log, dt_bias, norm_weight, rec_state,
+                    num_k_heads, num_v_heads, head_dim, eps=1e-6, conv_bias=None, out=None):
+    """One fused kernel for the GDN decode layer between in_proj_* and out_proj
+    (src/cb_engine.py:325-351 with ELEM_CONV): conv update + SiLU, split, gating, l2norm, recurrent
+    step, gated RMSNorm.  mixed [N, C] bf16 (pre-conv), z [N, H_v*d] bf16, a, b [N, H_v] bf16;
+    conv_state [N, C, K] bf16 and rec_state [N, H_v, d, d] fp32 are updated in place.
+    A_log, dt_bias, norm_weight: the layer's parameters (any float dtype; A_log / dt_bias are read in
+    fp32 exactly as the reference's ``.float()``).  Returns the normed core [N, H_v*d] bf16."""
+    _lib.require_cuda(mixed, z, a, b, conv_state, conv_weight, rec_state)
+    N, C = mixed.shape
+    Hk, Hv, D = num_k_heads, num_v_heads, head_dim
+    K = conv_weight.shape[-1]
+    if C != (2 * Hk + Hv) * D:
+        raise ValueError(f"gdn_decode_core: C={C} != (2*{Hk}+{Hv})*{D}")
+    if tuple(conv_state.shape) != (N, C, K) or not conv_state.is_contiguous():
+        raise ValueError("gdn_decode_core: conv_state must be a contiguous [N, C, K] tensor")
+    if tuple(rec_state.shape) != (N, Hv, D, D) or rec_state.dtype != torch.float32 \
+            or not rec_state.is_contiguous():
+        raise ValueError("gdn_decode_core: rec_state must be a contiguous fp32 [N, H_v, d, d] tensor")
+    for name, t in (("mixed", mixed), ("z", z), ("a", a), ("b", b), ("conv_state", conv_state),
+                    ("conv_weight", conv_weight)):
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"gdn_decode_core: {name} must be bfloat16")
+    mixed, ms = _row_view(mixed)
+    z, zs = _row_view(z.reshape(N, Hv * D))
+    a = a.reshape(N, Hv)
+    b = b.reshape(N, Hv)
+    if a.stride() != b.stride() or a.stride(-1) != 1:
+        a, b = a.contiguous(), b.contiguous()
+    conv_weight = conv_weight.reshape(C, K).contiguous()
+    if conv_bias is not None:
+        conv_bias = conv_bias.to(torch.bfloat16).contiguous()
+    A32 = A_log.to(torch.float32).contiguous()
+    dt32 = dt_bias.to(torch.float32).contiguous()
+    nw = norm_weight if norm_weight.dtype in (torch.float32, torch.bfloat16) else norm_weight.float()
+    nw = nw.contiguous()
+    if out is None:
+        out = torch.empty(N, Hv * D, dtype=torch.bfloat16, device=mixed.device)
+    _lib.call("gdn_decode_fused", _lib.ptr(mixed), ms, _lib.ptr(z), zs, _lib.ptr(a), _lib.ptr(b),
+              a.stride(0), _lib.ptr(conv_state), _lib.ptr(conv_weight), _lib.ptr(conv_bias),
+              _lib.ptr(A32), _lib.ptr(dt32), _lib.ptr(nw), _lib.dtype_code(nw), float(eps),
+              _lib.ptr(rec_state), _lib.ptr(out), N, Hk, Hv, D, K, _lib.stream_of(mixed))
+    return out
+
+
+def patch_model(model, fast_gdn=False, gdn_v2=False):
+    """Install the HIP hot-path functions on a transformers Qwen3.5 model (src/cb_engine.py:54-77):
+    every Qwen3_5GatedDeltaNet gets ``recurrent_gated_delta_rule`` and, with ``fast_gdn``,
+    ``chunk_gated_delta_rule`` (v2 with ``gdn_v2``; v2 is only installed together with fast_gdn,
+    as in the reference); every Qwen3_5RMSNormGated gets the fused gated norm.  transformers >= 5.6
+    calls the module-level functions from GatedDeltaNet.forward, so those names are rebound in the
+    modeling module as well.  Qwen3_5RMSNorm is left to transformers."""
+    from transformers.models.qwen3_5 import modeling_qwen3_5 as M
+    from .gdn_chunk_fast import fast_chunk_gated_delta_rule as v1
+    from .gdn_chunk_fast2 import fast_chunk_gated_delta_rule_v2 as v2
+    chunk_fn = (v2 if gdn_v2 else v1) if fast_gdn else None
+    for m in model.modules():
+        if isinstance(m, M.Qwen3_5RMSNormGated):
+            m.forward = fused_gated_rmsnorm.__get__(m, M.Qwen3_5RMSNormGated)
+        elif isinstance(m, M.Qwen3_5GatedDeltaNet):
+            m.recurrent_gated_delta_rule = recurrent_single_step
+            if chunk_fn is not None:
+                m.chunk_gated_delta_rule = chunk_fn
+    M.torch_recurrent_gated_delta_rule = recurrent_single_step
+    if chunk_fn is not None:
+        M.torch_chunk_gated_delta_rule = chunk_fn
+    M.causal_conv1d_update = causal_conv1d_update
+    return model
+
+
+class GDNSlots:
+    """Per-slot GDN state of every GDN layer, laid out as CBEngine keeps it
+    (src/cb_engine.py:108-112): conv[i] [N, C, K] bf16, rec[i] [N, H_v, d_k, d_v] fp32."""
+
+    def __init__(self, n_slots, layer_ids, conv_dim, conv_kernel, num_v_heads, head_dim, device):
+        self.N = n_slots
+        self.conv = {i: torch.zeros(n_slots, conv_dim, conv_kernel, dtype=torch.bfloat16, device=device)
+                     for i in layer_ids}
+        self.rec = {i: torch.zeros(n_slots, num_v_heads, head_dim, head_dim, dtype=torch.float32,
+                                   device=device) for i in layer_ids}
+
+    def reset(self):
+        for i in self.conv:
+            self.conv[i].zero_()
+            self.rec[i].zero_()
+
+
+def gdn_decode_layer(gd, h, conv_state, rec_state):
+    """CBEngine._gdn (src/cb_engine.py:318-352) for one token per slot: projections (torch GEMMs),
+    the fused HIP core, out_proj.  ``gd`` carries Qwen3_5GatedDeltaNet's attributes
+    (in_proj_qkv, in_proj_z, in_proj_b, in_proj_a, conv1d, A_log, dt_bias, norm, out_proj,
+    num_k_heads, num_v_heads, head_k_dim).  h [N, 1, hidden] bf16 -> [N, 1, hidden]."""
+    n = h.shape[0]
+    mixed = gd.in_proj_qkv(h).reshape(n, -1)
+    z = gd.in_proj_z(h).reshape(n, -1)
+    b = gd.in_proj_b(h).reshape(n, -1)
+    a = gd.in_proj_a(h).reshape(n, -1)
+    w = gd.conv1d.weight
+    core = gdn_decode_core(mixed, z, a, b, conv_state, w.reshape(w.shape[0], w.shape[-1]), gd.A_log,
+                           gd.dt_bias, gd.norm.weight, rec_state, gd.num_k_heads, gd.num_v_heads,
+                           gd.head_k_dim, gd.norm.variance_epsilon, gd.conv1d.bias)
+    return gd.out_proj(core.reshape(n, 1, -1))
+
+
+class GDNDecodeGraph:
+    """A decode step over several GDN layers captured once as a HIP graph and replayed
+    (the GDN part of src/cb_engine.py:123-187).  ``step_fn()`` must read its inputs from static
+    buffers; it is run once eagerly (warm-up), then captured."""
+
+    def __init__(self, step_fn, device=None):
+        self.step_fn = step_fn
+        self.graph = torch.cuda.CUDAGraph()
+        stream = torch.cuda.Stream(device=device)
+        stream.wait_stream(torch.cuda.current_stream(device))
+        with torch.cuda.stream(stream):
+            step_fn()
+        torch.cuda.current_stream(device).wait_stream(stream)
+        torch.cuda.synchronize(device)
+        with torch.cuda.graph(self.graph):
+            self.out = step_fn()
+
+    def replay(self):
+        self.graph.replay()
+        return self.out

@@ -1,0 +1,53 @@
+// Device-side helpers shared by the GDN kernels (gfx950, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gdn {
+
+constexpr int kWave = 64;
+
+// ---- bf16 <-> fp32 -------------------------------------------------------------------------
+// bf16 is the upper half of an IEEE fp32; fp32 -> bf16 rounds to nearest even (torch's rule),
+// NaN stays a quiet NaN.
+__device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
+
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// Round an fp32 value to the nearest bf16 and return it as fp32 (emulates one torch bf16 op).
+__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+
+// Element loads/stores for the two activation dtypes (fp32 or bf16).
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+  __device__ static __forceinline__ float load(const float* p) { return *p; }
+  __device__ static __forceinline__ void store(float* p, float v) { *p = v; }
+  __device__ static __forceinline__ float round(float v) { return v; }
+};
+template <> struct Elem<uint16_t> {
+  __device__ static __forceinline__ float load(const uint16_t* p) { return bf2f(*p); }
+  __device__ static __forceinline__ void store(uint16_t* p, float v) { *p = f2bf(v); }
+  __device__ static __forceinline__ float round(float v) { return rbf(v); }
+};
+
+// ---- scalar math with torch's CPU formulas ------------------------------------------------
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
+// F.softplus(x), beta = 1, threshold = 20.
+__device__ __forceinline__ float softplus_f(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
+// torch.rsqrt = 1 / sqrt(x) with correctly rounded sqrt and divide.
+__device__ __forceinline__ float rsqrt_f(float x) { return 1.0f / sqrtf(x); }
+
+// ---- wavefront reductions ------------------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+}  // namespace gdn

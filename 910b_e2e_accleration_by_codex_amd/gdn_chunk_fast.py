@@ -1,0 +1,179 @@
+"""Chunked gated delta rule prefill on the HIP library.
+
+Drop-in for the reference's ``fast_chunk_gated_delta_rule`` (src/gdn_chunk_fast.py:65-142), whose
+signature is HF's ``torch_chunk_gated_delta_rule`` (HF modeling_qwen3_5.py:249-260); the v2 name
+(src/gdn_chunk_fast2.py:11) runs the same kernel (gdn_chunk_fast2.py).  Semantics kept: q, k are
+l2-normalised in their own dtype when ``use_qk_l2norm_in_kernel``, q is scaled by d^-1/2, the
+sequence is processed in chunks of 64 with an fp32 running state, the output has query's dtype and
+the final state is fp32.  ``chunk_size`` only changes fp32 rounding in the reference (every chunk
+size computes the same recurrence); the kernel always uses 64-token chunks.
+Added beyond the reference: ``cu_seqlens`` (int32 [n_seq+1]) for packed varlen batches
+([1, sum T, H, d] inputs, [n_seq, H_v, d, d] states), the form HF forwards as ``cu_seq_lens_q``.
+
+Also here: the causal conv1d prefill with state capture (src/cb_tp.py:158-164, :236-244, :260),
+the gating, and the fused prefill layer core (src/cb_tp.py:153-181, :230-263).
+"""
+import torch
+
+from . import _lib
+
+CHUNK = 64
+
+
+def _tokens_view(x, name):
+    """[B, T, H, d] -> ([B*T, H, d] tensor with dense (H, d), token stride)."""
+    B, T, H, D = x.shape
+    if x.stride(3) != 1 or x.stride(2) != D or (B > 1 and x.stride(0) != T * x.stride(1)):
+        x = x.contiguous()
+    flat = x.as_strided((B * T, H, D), (x.stride(1), D, 1))
+    return flat, x.stride(1)
+
+
+def _seq_args(B, T, cu_seqlens, device):
+    if cu_seqlens is None:
+        return None, B, T
+    if B != 1:
+        raise ValueError("cu_seqlens needs packed inputs with batch size 1")
+    cu = cu_seqlens.to(device=device, dtype=torch.int32).contiguous()
+    return cu, cu.numel() - 1, 0
+
+
+def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size=64, initial_state=None,
+                           output_final_state=False, use_qk_l2norm_in_kernel=False, cu_seqlens=None,
+                           **kwargs):
+    """query/key [B,T,Hqk,d] (Hqk = Hv after repeat_interleave, or Hv/r key heads read by value
+    head h as h // r), value [B,T,Hv,d] bf16, g [B,T,Hv] (log decay, read in fp32), beta
+    [B,T,Hv], initial_state [B or n_seq, Hv, d, d] | None.
+    Returns (out [B,T,Hv,d] query.dtype, final_state [B or n_seq,Hv,d,d] fp32 | None)."""
+    if chunk_size <= 0:
+        raise ValueError("chunk_size must be positive")
+    _lib.require_cuda(query, key, value, g, beta, initial_state, cu_seqlens)
+    if key.dtype != query.dtype or value.dtype != query.dtype:
+        raise TypeError("chunk_gated_delta_rule: query, key and value must share a dtype")
+    B, T, Hqk, D = query.shape
+    Hv = value.shape[2]
+    if key.shape != query.shape or tuple(value.shape) != (B, T, Hv, D):
+        raise ValueError(f"chunk_gated_delta_rule: shape mismatch q{tuple(query.shape)} "
+                         f"k{tuple(key.shape)} v{tuple(value.shape)}")
+    if tuple(g.shape) != (B, T, Hv) or tuple(beta.shape) != (B, T, Hv):
+        raise ValueError("chunk_gated_delta_rule: g and beta must be [B, T, Hv]")
+    dev = query.device
+    cu, nseq, seq_len = _seq_args(B, T, cu_seqlens, dev)
+    q, qs = _tokens_view(query, "query")
+    k, ks = _tokens_view(key, "key")
+    v, vs = _tokens_view(value, "value")
+    g32 = g.to(torch.float32).contiguous()
+    if beta.dtype not in (torch.float32, torch.bfloat16):
+        beta = beta.to(torch.float32)
+    beta = beta.contiguous()
+    init = None
+    if initial_state is not None:
+        if tuple(initial_state.shape) != (nseq, Hv, D, D):
+            raise ValueError(f"chunk_gated_delta_rule: initial_state must be [{nseq},{Hv},{D},{D}]")
+        init = initial_state.to(torch.float32).contiguous()
+    final = torch.empty(nseq, Hv, D, D, dtype=torch.float32, device=dev) if output_final_state else None
+    out = torch.empty(B, T, Hv, D, dtype=query.dtype, device=dev)
+    _lib.call("gdn_chunk_prefill", _lib.ptr(q), qs, _lib.ptr(k), ks, _lib.ptr(v), vs, _lib.ptr(g32),
+              _lib.ptr(beta), _lib.dtype_code(beta), _lib.ptr(init), _lib.ptr(final), _lib.ptr(out),
+              B * T, _lib.ptr(cu), nseq, seq_len, Hqk, Hv, D, _lib.dtype_code(query),
+              int(bool(use_qk_l2norm_in_kernel)), _lib.stream_of(query))
+    return out, final
+
+
+def fast_chunk_gated_delta_rule(query, key, value, g, beta, chunk_size=64, initial_state=None,
+                                output_final_state=False, use_qk_l2norm_in_kernel=False, **kwargs):
+    """The v1 name (src/gdn_chunk_fast.py:65-75); same kernel as v2."""
+    return chunk_gated_delta_rule(query, key, value, g, beta, chunk_size, initial_state,
+                                  output_final_state, use_qk_l2norm_in_kernel, **kwargs)
+
+
+def _unit_lower_inv(X, base=16):
+    """(I - X)^-1 for strictly lower X [..., 64, 64] fp32 on the GPU: the kernel's blocked inverse
+    (16x16 diagonal blocks by forward substitution, fp32 MFMA block merges), the algorithm of
+    src/gdn_chunk_fast.py:33-62."""
+    _lib.require_cuda(X)
+    if X.shape[-1] != 64 or X.shape[-2] != 64:
+        raise ValueError("_unit_lower_inv: the kernel inverts 64x64 blocks")
+    Xf = X.to(torch.float32).contiguous()
+    out = torch.empty_like(Xf)
+    batch = Xf.numel() // (64 * 64)
+    _lib.call("gdn_unit_lower_inv", _lib.ptr(Xf), _lib.ptr(out), batch, 64, _lib.stream_of(Xf))
+    return out
+
+
+def causal_conv1d_prefill(x, weight, bias=None, history=None, cu_seqlens=None):
+    """Depthwise causal conv (kernel K) + SiLU over prompts, plus the decode conv state they leave.
+    x [B, C, L] bf16 (HF layout; token-major memory such as ``mixed_qkv.transpose(1, 2)`` is read
+    in place); history [n_seq, C, K] | None (None = fresh prompt, zero history: F.conv1d with
+    padding K-1, src/cb_tp.py:163-164; given = the previous K inputs, src/cb_tp.py:236-244).
+    Returns (out [B, C, L] bf16 with token-major memory, state [n_seq, C, K] = the last K inputs,
+    left zero-padded, src/cb_tp.py:158-162, :260)."""
+    _lib.require_cuda(x, weight, bias, history, cu_seqlens)
+    B, C, L = x.shape
+    K = weight.shape[-1]
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise TypeError("causal_conv1d_prefill: x and weight must be bfloat16")
+    xt = x.transpose(1, 2)                                   # [B, L, C]
+    if xt.stride(2) != 1 or (B > 1 and xt.stride(0) != L * xt.stride(1)):
+        xt = xt.contiguous()
+    cu, nseq, seq_len = _seq_args(B, L, cu_seqlens, x.device)
+    w = weight.reshape(C, K).contiguous()
+    if bias is not None:
+        bias = bias.to(torch.bfloat16).contiguous()
+    if history is not None:
+        if tuple(history.shape) != (nseq, C, K):
+            raise ValueError(f"causal_conv1d_prefill: history must be [{nseq},{C},{K}]")
+        history = history.to(torch.bfloat16).contiguous()
+    out = torch.empty(B, L, C, dtype=torch.bfloat16, device=x.device)
+    state = torch.empty(nseq, C, K, dtype=torch.bfloat16, device=x.device)
+    _lib.call("gdn_conv_prefill", _lib.ptr(xt), xt.stride(1), _lib.ptr(w), _lib.ptr(bias),
+              _lib.ptr(history), _lib.ptr(out), _lib.ptr(state), B * L, _lib.ptr(cu), nseq, seq_len,
+              C, K, _lib.stream_of(x))
+    return out.transpose(1, 2), state
+
+
+def gdn_gating(a, b, A_log, dt_bias):
+    """beta = sigmoid(b) (b's dtype, bf16), g = -exp(A_log) * softplus(a + dt_bias) fp32
+    (src/cb_engine.py:337-338).  a, b [..., Hv] bf16."""
+    _lib.require_cuda(a, b)
+    Hv = a.shape[-1]
+    a2 = a.reshape(-1, Hv)
+    b2 = b.reshape(-1, Hv)
+    if a2.stride() != b2.stride() or a2.stride(-1) != 1:
+        a2, b2 = a2.contiguous(), b2.contiguous()
+    beta = torch.empty(a2.shape, dtype=torch.bfloat16, device=a.device)
+    g = torch.empty(a2.shape, dtype=torch.float32, device=a.device)
+    _lib.call("gdn_gating", _lib.ptr(a2), _lib.ptr(b2), a2.stride(0),
+              _lib.ptr(A_log.to(torch.float32).contiguous()), _lib.ptr(dt_bias.to(torch.float32).contiguous()),
+              _lib.ptr(beta), _lib.ptr(g), a2.shape[0], Hv, _lib.stream_of(a))
+    return beta.reshape(b.shape), g.reshape(a.shape)
+
+
+def gdn_prefill_core(mixed_qkv, z, a, b, conv_weight, A_log, dt_bias, norm_weight, num_k_heads,
+                     num_v_heads, head_dim, cu_seqlens=None, conv_history=None, initial_state=None,
+                     eps=1e-6, chunk_size=64, conv_bias=None):
+    """GDN prefill layer between in_proj_* and out_proj for one or more packed prompts
+    (src/cb_tp.py:153-181 fresh, :230-263 continued): conv prefill + SiLU, split q|k|v, gating,
+    chunked rule with l2norm (value head h reads key head h // r, no repeat_interleave copy),
+    gated RMSNorm.  mixed_qkv [T, C] bf16 (pre-conv), z [T, Hv*d], a, b [T, Hv];
+    cu_seqlens int32 [n_seq+1] | None; conv_history [n_seq, C, K] | None;
+    initial_state [n_seq, Hv, d, d] | None.
+    Returns (core [T, Hv*d] bf16, conv_state [n_seq, C, K] bf16, rec_state [n_seq, Hv, d, d] fp32)."""
+    T, C = mixed_qkv.shape
+    Hk, Hv, D = num_k_heads, num_v_heads, head_dim
+    if C != (2 * Hk + Hv) * D:
+        raise ValueError(f"gdn_prefill_core: C={C} != (2*{Hk}+{Hv})*{D}")
+    w = conv_weight.reshape(C, -1)
+    conv_out, conv_state = causal_conv1d_prefill(mixed_qkv.t().unsqueeze(0), w, conv_bias,
+                                                 conv_history, cu_seqlens)
+    qkv = conv_out[0].t()                                     # [T, C] view, dense rows
+    kd = Hk * D
+    q = qkv[:, :kd].reshape(1, T, Hk, D)
+    k = qkv[:, kd:2 * kd].reshape(1, T, Hk, D)
+    v = qkv[:, 2 * kd:].reshape(1, T, Hv, D)
+    beta, g = gdn_gating(a.reshape(1, T, Hv), b.reshape(1, T, Hv), A_log, dt_bias)
+    core, rec = chunk_gated_delta_rule(q, k, v, g, beta, chunk_size, initial_state, True, True,
+                                       cu_seqlens=cu_seqlens)
+    from .cb_engine import gated_rmsnorm
+    core = gated_rmsnorm(core.reshape(T * Hv, D), z.reshape(T * Hv, D), norm_weight, eps)
+    return core.reshape(T, Hv * D), conv_state, rec

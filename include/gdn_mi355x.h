@@ -1,0 +1,107 @@
+/*
+ * gdn_mi355x.h -- C ABI of the MI355X (gfx950) Gated DeltaNet hot-path library
+ * (libgdn_mi355x.so).
+ *
+ * Every entry point takes plain device pointers, sizes and element strides, launches HIP kernels
+ * on the given stream (a hipStream_t passed as void*; NULL = the legacy default stream), never
+ * allocates, never synchronises the host, and is therefore safe inside hipGraph stream capture.
+ * Tensors are dense row-major unless a stride argument says otherwise; strides are in elements.
+ *
+ * Dtype codes: GDN_F32 = 0, GDN_BF16 = 1.  bf16 is stored as the upper 16 bits of an IEEE fp32.
+ * Return value: 0 on success, otherwise a GDN_E* code; gdn_last_error() then returns a message
+ * (thread-local, valid until the next call on the same thread).
+ *
+ * Each declaration names the reference function it replaces (file:line in the reference
+ * repository; "HF:" = transformers models/qwen3_5/modeling_qwen3_5.py, the third-party module the
+ * reference patches).
+ */
+#ifndef GDN_MI355X_H
+#define GDN_MI355X_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { GDN_F32 = 0, GDN_BF16 = 1 };
+enum {
+  GDN_OK = 0,
+  GDN_EINVAL = 1,   /* bad shape, dtype, stride, alignment or null pointer */
+  GDN_EUNSUP = 2,   /* valid but not supported by this build (e.g. head_dim != 128) */
+  GDN_ELAUNCH = 3   /* the HIP launch failed; the message carries hipGetErrorString */
+};
+
+/* Library version (major*10000 + minor*100 + patch). */
+int gdn_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* gdn_last_error(void);
+
+/* Limits of this build: writes head_dim (128), max value heads per key head, max conv kernel. */
+int gdn_limits(int* head_dim, int* max_group_ratio, int* max_conv_kernel);
+
+/*
+ * Single-token recurrent gated delta rule (decode), fp32 state.
+ * Replaces recurrent_single_step (src/recurrent_single_step.py:8-32) for T == 1.
+ *   q, k      [N, Hqk, D]  (dtype in_dtype), row (token) stride q_stride / k_stride; value head h
+ *                          reads key head h / (Hv / Hqk) (Hqk == Hv for repeat_interleave'd input)
+ *   v         [N, Hv, D]   (in_dtype), row stride v_stride
+ *   g         [N, Hv] fp32 (log decay), beta [N, Hv] (beta_dtype)
+ *   state_in  [N, Hv, D, D] fp32 (dk rows, dv columns), NULL = zero state
+ *   state_out [N, Hv, D, D] fp32, may equal state_in (in-place update), NULL = do not write
+ *   out       [N, Hv, D] (in_dtype)
+ *   use_qk_l2norm: apply l2norm(x)=x*rsqrt(sum x^2 + 1e-6) to q, k in in_dtype first.
+ */
+int gdn_recurrent_step(const void* q, int64_t q_stride, const void* k, int64_t k_stride,
+                       const void* v, int64_t v_stride, const float* g, const void* beta,
+                       int beta_dtype, const float* state_in, float* state_out, void* out,
+                       int N, int Hqk, int Hv, int D, int in_dtype, int use_qk_l2norm,
+                       void* stream);
+
+/*
+ * Decode depthwise causal conv update with SiLU, conv state shifted in place.
+ * Replaces elem_conv_update (src/cb_engine.py:43-51); same contract as HF causal_conv1d_update
+ * with activation "silu" (HF:200-217).
+ *   x      [N, C] bf16, row stride x_stride;  state [N, C, K] bf16 (in place)
+ *   weight [C, K] bf16;  bias [C] bf16 or NULL;  out [N, C] bf16, row stride out_stride
+ */
+int gdn_conv_update(const void* x, int64_t x_stride, void* state, const void* weight,
+                    const void* bias, void* out, int64_t out_stride, int N, int C, int K,
+                    void* stream);
+
+/*
+ * Gated RMSNorm: out = silu(gate) * (weight * bf16(x * rsqrt(mean(x^2) + eps))), HF order.
+ * Replaces Qwen3_5RMSNormGated.forward (HF:175-184) / fused_gated_rmsnorm (src/cb_engine.py:65-67).
+ *   x, gate, out [rows, D] bf16 (row strides x_stride, gate_stride; out dense);
+ *   weight [D] (w_dtype: GDN_BF16 or GDN_F32).
+ */
+int gdn_gated_rmsnorm(const void* x, int64_t x_stride, const void* gate, int64_t gate_stride,
+                      const void* weight, int w_dtype, void* out, int64_t rows, int D, float eps,
+                      void* stream);
+
+/*
+ * Fused GDN decode layer core for N slots x 1 token (everything between the input projections
+ * and out_proj of CBEngine._gdn, src/cb_engine.py:318-351, with --elem-conv):
+ *   conv update + SiLU (conv_state shifted in place) -> split q|k|v -> beta = sigmoid(b),
+ *   g = -exp(A_log) * softplus(a + dt_bias) -> l2norm(q), l2norm(k) -> recurrent step with value
+ *   head h reading key head h / (Hv/Hk) -> rec_state updated in place -> gated RMSNorm with z.
+ *   mixed   [N, C] bf16 (pre-conv in_proj_qkv output, channels q(Hk*D) | k(Hk*D) | v(Hv*D)),
+ *           row stride mixed_stride;  C = (2*Hk + Hv) * D
+ *   z       [N, Hv*D] bf16 row stride z_stride;  a, b [N, Hv] bf16 row strides ab_stride
+ *   conv_state [N, C, K] bf16 (in place);  conv_w [C, K] bf16;  conv_b [C] bf16 or NULL
+ *   A_log, dt_bias [Hv] fp32;  norm_w [D] (norm_w_dtype)
+ *   rec_state [N, Hv, D, D] fp32 (in place);  out [N, Hv*D] bf16 (the normed core)
+ */
+int gdn_decode_fused(const void* mixed, int64_t mixed_stride, const void* z, int64_t z_stride,
+                     const void* a, const void* b, int64_t ab_stride, void* conv_state,
+                     const void* conv_w, const void* conv_b, const float* A_log,
+                     const float* dt_bias, const void* norm_w, int norm_w_dtype, float eps,
+                     float* rec_state, void* out, int N, int Hk, int Hv, int D, int K,
+                     void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GDN_MI355X_H */
