@@ -6,9 +6,12 @@
 //     m = gamma * S^T k,   delta = beta * (v - m),   o = gamma * S^T q + (k . q) * delta,
 //     S' = gamma * S + k delta^T,
 // which equals the reference's decay -> read -> delta -> write -> readout sequence
-// (src/recurrent_single_step.py:27-31) up to fp32 rounding order.  256 threads own one 128x128
-// state: thread t holds columns 4*(t%32)..+3 of rows (t/32) + 8*m, m < 16, as 16 float4 loads, so
-// every load instruction of a wave covers two adjacent 512-byte rows (1 KiB contiguous).
+// (src/recurrent_single_step.py:27-31) up to fp32 rounding order.  256 threads (4 waves) own one
+// 128x128 state: thread t holds columns 4*(t%32)..+3 of rows t/32 + 8*m, m < 16, as 16 float4
+// loads, so every load instruction of a wave covers two adjacent 512-byte rows (1 KiB contiguous;
+// measured faster than giving each wave whole columns).  Column sums combine the wave's two row
+// groups with one xor-shuffle and the four waves through LDS; after that each thread derives delta
+// for its own 4 columns and streams its rows straight back.
 #include "gdn_device.h"
 #include "gdn_internal.h"
 
@@ -25,11 +28,16 @@ struct StateRegs {
   f32x4 s[kRowsPerThread];
 };
 
-// Issue the 16 float4 loads of this thread's slice of a [D, D] fp32 state.
+// This thread's first float4 of the state: row t/32, columns 4*(t%32)..+3 (t = 0..255).
+__device__ __forceinline__ int state_f4(int t) { return (t >> 5) * 32 + (t & 31); }
+
+// Issue the 16 float4 loads of this thread's slice of a [D, D] fp32 state (rows t/32 + 8m).  The
+// state is streamed once per step, so loads and stores carry the non-temporal hint (measured ~20%
+// faster than plain accesses for this read-modify-write on MI355X).
 __device__ __forceinline__ void state_load(StateRegs& r, const float* S, int t) {
-  const f32x4* p = reinterpret_cast<const f32x4*>(S) + (t >> 5) * 32 + (t & 31);
+  const f32x4* p = reinterpret_cast<const f32x4*>(S) + state_f4(t);
 #pragma unroll
-  for (int m = 0; m < kRowsPerThread; ++m) r.s[m] = p[m * 8 * 32];
+  for (int m = 0; m < kRowsPerThread; ++m) r.s[m] = __builtin_nontemporal_load(p + m * 8 * 32);
 }
 
 __device__ __forceinline__ void state_zero(StateRegs& r) {
@@ -37,11 +45,11 @@ __device__ __forceinline__ void state_zero(StateRegs& r) {
   for (int m = 0; m < kRowsPerThread; ++m) r.s[m] = f32x4{0.f, 0.f, 0.f, 0.f};
 }
 
-// Column partial sums of S^T k and S^T q over this thread's 16 rows.
+// Column sums of S^T k and S^T q over this thread's 16 rows plus the other row group of its wave
+// (lane ^ 32); lanes 0..31 then publish the wave's partials to red[2][4][D] (k, q).
 __device__ __forceinline__ void state_partials(const StateRegs& r, const float* kn, const float* qs,
-                                               int t, f32x4& pk, f32x4& pq) {
-  pk = f32x4{0.f, 0.f, 0.f, 0.f};
-  pq = f32x4{0.f, 0.f, 0.f, 0.f};
+                                               int t, float (*red)[4][kD]) {
+  f32x4 pk = f32x4{0.f, 0.f, 0.f, 0.f}, pq = f32x4{0.f, 0.f, 0.f, 0.f};
   const int rg = t >> 5;
 #pragma unroll
   for (int m = 0; m < kRowsPerThread; ++m) {
@@ -49,19 +57,35 @@ __device__ __forceinline__ void state_partials(const StateRegs& r, const float* 
     pk += r.s[m] * kr;
     pq += r.s[m] * qr;
   }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    pk[e] += __shfl_xor(pk[e], 32, kWave);
+    pq[e] += __shfl_xor(pq[e], 32, kWave);
+  }
+  const int lane = t & 63, w = t >> 6;
+  if (lane < 32) {
+    *reinterpret_cast<f32x4*>(&red[0][w][4 * lane]) = pk;
+    *reinterpret_cast<f32x4*>(&red[1][w][4 * lane]) = pq;
+  }
 }
 
-// S' = gamma * S + k delta^T, stored to Sout.
-__device__ __forceinline__ void state_update_store(StateRegs& r, float* Sout, const float* kn,
-                                                   const float* delta, float gamma, int t) {
+// Sum of the four waves' partials for column c.
+__device__ __forceinline__ float red_sum(const float (*red)[4][kD], int which, int c) {
+  return red[which][0][c] + red[which][1][c] + red[which][2][c] + red[which][3][c];
+}
+
+// delta for this thread's 4 columns, then S' = gamma S + k delta^T streamed to Sout.
+__device__ __forceinline__ void state_update_store(const StateRegs& r, float* Sout, const float* kn,
+                                                   const float* v, const float (*red)[4][kD],
+                                                   float gamma, float beta, int t) {
   const int rg = t >> 5, cg = t & 31;
-  const f32x4 d = *reinterpret_cast<const f32x4*>(delta + 4 * cg);
-  f32x4* p = reinterpret_cast<f32x4*>(Sout) + rg * 32 + cg;
+  f32x4 d;
 #pragma unroll
-  for (int m = 0; m < kRowsPerThread; ++m) {
-    const float kr = kn[rg + 8 * m];
-    p[m * 8 * 32] = r.s[m] * gamma + d * kr;
-  }
+  for (int e = 0; e < 4; ++e) d[e] = (v[4 * cg + e] - gamma * red_sum(red, 0, 4 * cg + e)) * beta;
+  f32x4* p = reinterpret_cast<f32x4*>(Sout) + state_f4(t);
+#pragma unroll
+  for (int m = 0; m < kRowsPerThread; ++m)
+    __builtin_nontemporal_store(r.s[m] * gamma + d * kn[rg + 8 * m], p + m * 8 * 32);
 }
 
 // l2norm of a D=128 vector held as 2 values per lane, in the input dtype's precision
@@ -85,7 +109,7 @@ __global__ __launch_bounds__(kHeadThreads) void recurrent_step_kernel(
     const InT* __restrict__ v, int64_t v_stride, const float* __restrict__ g,
     const BetaT* __restrict__ beta, const float* state_in, float* state_out, InT* __restrict__ out,
     int Hqk, int Hv, int use_l2) {
-  __shared__ float s_q[kD], s_k[kD], s_v[kD], s_delta[kD];
+  __shared__ float s_q[kD], s_k[kD], s_v[kD];
   __shared__ float s_red[2][4][kD];
   __shared__ float s_sc[4];  // gamma, beta, k.q
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
@@ -124,29 +148,14 @@ __global__ __launch_bounds__(kHeadThreads) void recurrent_step_kernel(
   }
   __syncthreads();
 
-  f32x4 pk, pq;
-  state_partials(S, s_k, s_q, t, pk, pq);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    pk[e] += __shfl_xor(pk[e], 32, kWave);
-    pq[e] += __shfl_xor(pq[e], 32, kWave);
-  }
-  if (lane < 32) {
-    *reinterpret_cast<f32x4*>(&s_red[0][w][4 * lane]) = pk;
-    *reinterpret_cast<f32x4*>(&s_red[1][w][4 * lane]) = pq;
-  }
+  state_partials(S, s_k, s_q, t, s_red);
   __syncthreads();
-
   const float gamma = s_sc[0], bt = s_sc[1], kq = s_sc[2];
+  if (state_out) state_update_store(S, state_out + sidx, s_k, s_v, s_red, gamma, bt, t);
   if (t < kD) {
-    const float mk = s_red[0][0][t] + s_red[0][1][t] + s_red[0][2][t] + s_red[0][3][t];
-    const float mq = s_red[1][0][t] + s_red[1][1][t] + s_red[1][2][t] + s_red[1][3][t];
-    const float delta = (s_v[t] - gamma * mk) * bt;
-    s_delta[t] = delta;
-    Elem<InT>::store(out + ((int64_t)n * Hv + h) * kD + t, gamma * mq + kq * delta);
+    const float delta = (s_v[t] - gamma * red_sum(s_red, 0, t)) * bt;
+    Elem<InT>::store(out + ((int64_t)n * Hv + h) * kD + t, gamma * red_sum(s_red, 1, t) + kq * delta);
   }
-  __syncthreads();
-  if (state_out) state_update_store(S, state_out + sidx, s_k, s_delta, gamma, t);
 }
 
 // ============================================================================================
@@ -175,6 +184,32 @@ __device__ __forceinline__ float conv_channel(uint16_t* st, const uint16_t* wt, 
     for (int i = 0; i < K; ++i) acc += rbf(bf2f(win[i]) * bf2f(wt[i]));
     for (int i = 0; i < K; ++i) st[i] = win[i];
   }
+  float o = rbf(acc);
+  if (has_bias) o = rbf(o + bias);
+  return rbf(silu_f(o));
+}
+
+// K == 4 conv split in two halves so the loads can be issued ahead of the state stream.
+struct Conv4 {
+  uint2 s, w;
+  uint16_t x;
+};
+__device__ __forceinline__ void conv4_load(Conv4& c, const uint16_t* st, const uint16_t* wt, const uint16_t* xp) {
+  c.s = *reinterpret_cast<const uint2*>(st);
+  c.w = *reinterpret_cast<const uint2*>(wt);
+  c.x = *xp;
+}
+__device__ __forceinline__ float conv4_finish(const Conv4& c, uint16_t* st, float bias, bool has_bias) {
+  const uint16_t win[4] = {(uint16_t)(c.s.x >> 16), (uint16_t)(c.s.y & 0xffff), (uint16_t)(c.s.y >> 16), c.x};
+  const uint16_t ww[4] = {(uint16_t)(c.w.x & 0xffff), (uint16_t)(c.w.x >> 16), (uint16_t)(c.w.y & 0xffff),
+                          (uint16_t)(c.w.y >> 16)};
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc += rbf(bf2f(win[i]) * bf2f(ww[i]));
+  uint2 nv;
+  nv.x = (uint32_t)win[0] | ((uint32_t)win[1] << 16);
+  nv.y = (uint32_t)win[2] | ((uint32_t)win[3] << 16);
+  *reinterpret_cast<uint2*>(st) = nv;
   float o = rbf(acc);
   if (has_bias) o = rbf(o + bias);
   return rbf(silu_f(o));
@@ -234,6 +269,9 @@ __global__ __launch_bounds__(256) void gated_rmsnorm_kernel(const uint16_t* __re
 // ============================================================================================
 // Fused decode layer core: one workgroup per (slot, key head) owning its R value heads, so every
 // conv channel it reads is also written by it alone (the in-place conv state needs no grid sync).
+// Wave roles in the prologue: wave 0 convolves + l2-normalises q, wave 1 k, waves 2..R+1 the R v
+// heads, wave R+2 computes the gating; the tiny conv loads are issued before the 64 KiB-per-head
+// state stream so the whole prologue runs while the state is in flight.
 // ============================================================================================
 template <int R, bool kWBf16>
 __global__ __launch_bounds__(kHeadThreads* R) void decode_fused_kernel(
@@ -243,9 +281,9 @@ __global__ __launch_bounds__(kHeadThreads* R) void decode_fused_kernel(
     const uint16_t* __restrict__ conv_b, const float* __restrict__ A_log,
     const float* __restrict__ dt_bias, const void* norm_w, float eps, float* rec_state,
     uint16_t* __restrict__ out, int Hk, int K) {
-  __shared__ float s_q[kD], s_k[kD], s_v[R][kD], s_delta[R][kD];
+  __shared__ float s_q[kD], s_k[kD], s_v[R][kD];
   __shared__ float s_red[R][2][4][kD];
-  __shared__ float s_gamma[R], s_beta[R], s_kq;
+  __shared__ float s_gamma[R], s_beta[R];
   const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
   const int j = t / kHeadThreads, tl = t % kHeadThreads, wl = tl >> 6;  // head in group, local ids
   const int n = blockIdx.x / Hk, hk = blockIdx.x % Hk;
@@ -253,75 +291,81 @@ __global__ __launch_bounds__(kHeadThreads* R) void decode_fused_kernel(
   const int h = hk * R + j;
   const int C = (2 * Hk + Hv) * kD;
   const int64_t sidx = ((int64_t)n * Hv + h) * kD * kD;
-
-  StateRegs S;
-  state_load(S, rec_state + sidx, tl);  // in flight while the prologue runs
-
-  // conv update + SiLU for the q, k and R v heads of this group
   const uint16_t* xr = mixed + n * mixed_stride;
-  for (int e = t; e < (2 + R) * kD; e += kHeadThreads * R) {
-    int ch;
-    float* dst;
-    if (e < kD) { ch = hk * kD + e; dst = &s_q[e]; }
-    else if (e < 2 * kD) { ch = Hk * kD + hk * kD + (e - kD); dst = &s_k[e - kD]; }
-    else { const int vv = e - 2 * kD; ch = 2 * Hk * kD + hk * R * kD + vv; dst = &s_v[0][0] + vv; }
-    const float bb = conv_b ? bf2f(conv_b[ch]) : 0.f;
-    *dst = conv_channel(conv_state + ((int64_t)n * C + ch) * K, conv_w + (int64_t)ch * K, bb,
-                        conv_b != nullptr, xr[ch], K);
-  }
-  if (t < R) {
-    const int hh = hk * R + t;
-    const float bv = bf2f(b[n * ab_stride + hh]);
-    const float av = bf2f(a[n * ab_stride + hh]);
-    s_beta[t] = rbf(sigmoid_f(bv));
-    const float gg = -expf(A_log[hh]) * softplus_f(av + dt_bias[hh]);
-    s_gamma[t] = expf(gg);
-  }
-  __syncthreads();
-  if (wv == 0) {
-    float q0 = s_q[lane], q1 = s_q[lane + 64], k0 = s_k[lane], k1 = s_k[lane + 64];
-    l2norm_pair<true>(q0, q1);
-    l2norm_pair<true>(k0, k1);
-    q0 *= kInvSqrtD;
-    q1 *= kInvSqrtD;
-    const float kq = wave_sum(k0 * q0 + k1 * q1);
-    s_q[lane] = q0; s_q[lane + 64] = q1;
-    s_k[lane] = k0; s_k[lane + 64] = k1;
-    if (lane == 0) s_kq = kq;
-  }
-  __syncthreads();
+  const bool conv_wave = wv < 2 + R;
+  const int ch0 = wv == 0 ? hk * kD : (wv == 1 ? (Hk + hk) * kD : (2 * Hk + hk * R + (wv - 2)) * kD);
 
-  f32x4 pk, pq;
-  state_partials(S, s_k, s_q, tl, pk, pq);
+  // 1. small loads first: conv window / weight / input of this wave's 128 channels, gating inputs
+  Conv4 cv[2];
+  if (conv_wave && K == 4) {
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    pk[e] += __shfl_xor(pk[e], 32, kWave);
-    pq[e] += __shfl_xor(pq[e], 32, kWave);
+    for (int u = 0; u < 2; ++u) {
+      const int ch = ch0 + lane + 64 * u;
+      conv4_load(cv[u], conv_state + ((int64_t)n * C + ch) * 4, conv_w + (int64_t)ch * 4, xr + ch);
+    }
   }
-  if (lane < 32) {
-    *reinterpret_cast<f32x4*>(&s_red[j][0][wl][4 * lane]) = pk;
-    *reinterpret_cast<f32x4*>(&s_red[j][1][wl][4 * lane]) = pq;
+  float g_a = 0.f, g_b = 0.f, g_al = 0.f, g_dt = 0.f;
+  const bool gate_lane = wv == 2 + R && lane < R;
+  if (gate_lane) {
+    const int hh = hk * R + lane;
+    g_b = bf2f(b[n * ab_stride + hh]);
+    g_a = bf2f(a[n * ab_stride + hh]);
+    g_al = A_log[hh];
+    g_dt = dt_bias[hh];
+  }
+  // 2. the state stream
+  StateRegs S;
+  state_load(S, rec_state + sidx, tl);
+
+  // 3. prologue math while the state is in flight
+  if (conv_wave) {
+    float x[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int ch = ch0 + lane + 64 * u;
+      const float bb = conv_b ? bf2f(conv_b[ch]) : 0.f;
+      uint16_t* st = conv_state + ((int64_t)n * C + ch) * K;
+      x[u] = K == 4 ? conv4_finish(cv[u], st, bb, conv_b != nullptr)
+                    : conv_channel(st, conv_w + (int64_t)ch * K, bb, conv_b != nullptr, xr[ch], K);
+    }
+    if (wv < 2) {
+      l2norm_pair<true>(x[0], x[1]);
+      float* dst = wv == 0 ? s_q : s_k;
+      const float sc = wv == 0 ? kInvSqrtD : 1.0f;
+      dst[lane] = x[0] * sc;
+      dst[lane + 64] = x[1] * sc;
+    } else {
+      s_v[wv - 2][lane] = x[0];
+      s_v[wv - 2][lane + 64] = x[1];
+    }
+  }
+  if (gate_lane) {
+    s_beta[lane] = rbf(sigmoid_f(g_b));
+    s_gamma[lane] = expf(-expf(g_al) * softplus_f(g_a + g_dt));
   }
   __syncthreads();
 
-  const float gamma = s_gamma[j];
+  // 4. column sums (two row groups per wave by shuffle, four waves through LDS)
+  state_partials(S, s_k, s_q, tl, s_red[j]);
+  __syncthreads();
+
+  // 5. every thread derives delta for its own 4 columns and streams its rows back at once; wave 0
+  //    of each head also forms the readout o = gamma S^T q + (k.q) delta (bf16, as the reference's
+  //    recurrent output) and the gated RMSNorm of the head's 128 outputs.
+  const float gamma = s_gamma[j], bt = s_beta[j];
+  state_update_store(S, rec_state + sidx, s_k, s_v[j], s_red[j], gamma, bt, tl);
   if (wl == 0) {
-    const float bt = s_beta[j], kq = s_kq;
+    const float kq = wave_sum(s_k[lane] * s_q[lane] + s_k[lane + 64] * s_q[lane + 64]);
     float o[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int c = lane + 64 * u;
-      const float mk = s_red[j][0][0][c] + s_red[j][0][1][c] + s_red[j][0][2][c] + s_red[j][0][3][c];
-      const float mq = s_red[j][1][0][c] + s_red[j][1][1][c] + s_red[j][1][2][c] + s_red[j][1][3][c];
-      const float delta = (s_v[j][c] - gamma * mk) * bt;
-      s_delta[j][c] = delta;
-      o[u] = rbf(gamma * mq + kq * delta);  // the recurrent output is bf16 before the norm
+      const float delta = (s_v[j][c] - gamma * red_sum(s_red[j], 0, c)) * bt;
+      o[u] = rbf(gamma * red_sum(s_red[j], 1, c) + kq * delta);
     }
     gated_norm_row<kWBf16>(o, z + n * z_stride + (int64_t)h * kD, norm_w,
                            out + ((int64_t)n * Hv + h) * kD, kD, eps, lane);
   }
-  __syncthreads();
-  state_update_store(S, rec_state + sidx, s_k, s_delta[j], gamma, tl);
 }
 
 }  // namespace gdn

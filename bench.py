@@ -1,0 +1,243 @@
+"""Benchmark of the GDN hot path on one MI355X.
+
+Default workload (the headline line): the 16-slot GDN decode step over 48 layers -- per layer the
+fused conv update + SiLU + gating + l2norm + recurrent fp32 state read-modify-write + gated RMSNorm
+for 16 slots x 1 token, H_k=16, H_v=32, d=128, conv channels 8192, kernel 4 -- with 48 DISTINCT
+layer states (3.2 GB working set, so the 256 MB Infinity Cache cannot serve them), captured once as
+a HIP graph and replayed.  A "step" is one replay (48 layers).  ``value`` is microseconds per layer.
+
+Also reported (``secondary``): chunked GDN prefill at T=8192 (B=1, H_k=16, H_v=32, d=128, bf16
+inputs, fp32 state) in tokens/s/layer with its bf16-MFMA and HBM fractions.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-prefill]
+"""
+import argparse
+import importlib
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+PKG = "910b_e2e_accleration_by_codex_amd"
+
+HBM_PEAK = 8.0e12          # B/s, MI355X HBM3E
+BF16_PEAK = 2.5e15         # flop/s, dense bf16 MFMA
+
+N_SLOTS, HK, HV, D, KC, LAYERS = 16, 16, 32, 128, 4, 48
+C = (2 * HK + HV) * D
+
+
+def decode_bytes_per_layer():
+    """Algorithmic HBM bytes of one fused decode layer (each tensor touched once)."""
+    state = 2 * N_SLOTS * HV * D * D * 4            # fp32 state read + write
+    conv = 2 * N_SLOTS * C * KC * 2                 # bf16 conv state read + write
+    conv_w = C * KC * 2
+    mixed = N_SLOTS * C * 2
+    z = N_SLOTS * HV * D * 2
+    out = N_SLOTS * HV * D * 2
+    ab = 2 * N_SLOTS * HV * 2
+    params = HV * 4 * 2 + D * 2                     # A_log, dt_bias fp32; norm weight bf16
+    return state + conv + conv_w + mixed + z + out + ab + params
+
+
+def make_decode_layers(dev, seed=0):
+    g_ = torch.Generator(device="cpu").manual_seed(seed)
+    layers = []
+    for _ in range(LAYERS):
+        layers.append(dict(
+            mixed=torch.randn(N_SLOTS, C, generator=g_).to(torch.bfloat16).to(dev),
+            z=torch.randn(N_SLOTS, HV * D, generator=g_).to(torch.bfloat16).to(dev),
+            a=torch.randn(N_SLOTS, HV, generator=g_).to(torch.bfloat16).to(dev),
+            b=torch.randn(N_SLOTS, HV, generator=g_).to(torch.bfloat16).to(dev),
+            conv_state=torch.randn(N_SLOTS, C, KC, generator=g_).to(torch.bfloat16).to(dev),
+            conv_weight=(0.5 * torch.randn(C, KC, generator=g_)).to(torch.bfloat16).to(dev),
+            A_log=torch.full((HV,), -2.302585092994046, device=dev),   # log(0.1)
+            dt_bias=torch.full((HV,), 2.0, device=dev),
+            norm_weight=(1 + 0.02 * torch.randn(D, generator=g_)).to(torch.bfloat16).to(dev),
+            rec_state=(0.02 * torch.randn(N_SLOTS, HV, D, D, generator=g_)).to(dev),
+        ))
+    return layers
+
+
+def decode_step(gdn, layers, outs):
+    for p, o in zip(layers, outs):
+        gdn.gdn_decode_core(p["mixed"], p["z"], p["a"], p["b"], p["conv_state"], p["conv_weight"],
+                            p["A_log"], p["dt_bias"], p["norm_weight"], p["rec_state"], HK, HV, D,
+                            out=o)
+    return outs
+
+
+def bench_decode(gdn, dev, steps, warmup):
+    layers = make_decode_layers(dev)
+    outs = [torch.empty(N_SLOTS, HV * D, dtype=torch.bfloat16, device=dev) for _ in range(LAYERS)]
+    graph = gdn.GDNDecodeGraph(lambda: decode_step(gdn, layers, outs), device=dev)
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    # HIP events on the stream the graph's kernels run on (the current stream at replay)
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1) / steps
+    us_layer = ms * 1000.0 / LAYERS
+    # eager (non-graph) back-to-back launches of the same kernel, for the per-launch duration
+    e2, e3 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e2.record(stream)
+    for _ in range(steps):
+        decode_step(gdn, layers, outs)
+    e3.record(stream)
+    torch.cuda.synchronize()
+    us_eager = e2.elapsed_time(e3) * 1000.0 / (steps * LAYERS)
+    return dict(ms_per_step=ms, us_per_layer=us_layer, us_per_layer_eager=us_eager, wall_s=wall)
+
+
+def prefill_flops(T, hv=HV, d=D, chunk=64):
+    return T * hv * (10 * chunk * d + 6 * d * d)
+
+
+def prefill_bytes(T, nseq=1, hk=HK, hv=HV, d=D):
+    per_tok = 2 * (2 * hk * d) + 2 * hv * d + 6 * hv + 2 * hv * d
+    return T * per_tok + nseq * 2 * hv * d * d * 4
+
+
+def bench_prefill(gdn, dev, T=8192, reps=5, seed=0):
+    g_ = torch.Generator(device="cpu").manual_seed(seed)
+    q = torch.randn(1, T, HK, D, generator=g_).to(torch.bfloat16).to(dev)
+    k = torch.randn(1, T, HK, D, generator=g_).to(torch.bfloat16).to(dev)
+    v = torch.randn(1, T, HV, D, generator=g_).to(torch.bfloat16).to(dev)
+    beta = torch.sigmoid(torch.randn(1, T, HV, generator=g_)).to(torch.bfloat16).to(dev)
+    g = (-torch.nn.functional.softplus(torch.randn(1, T, HV, generator=g_) + 2) * 0.1).to(dev)
+    s0 = (0.02 * torch.randn(1, HV, D, D, generator=g_)).to(dev)
+
+    def run():
+        return gdn.fast_chunk_gated_delta_rule_v2(q, k, v, g, beta, initial_state=s0, output_final_state=True,
+                                                  use_qk_l2norm_in_kernel=True)
+    run()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        run()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / reps
+    F = prefill_flops(T)
+    B = prefill_bytes(T)
+    return dict(workload=f"prefill B=1 T={T} H_k={HK} H_v={HV} d={D} bf16", us_per_layer=us,
+                tokens_per_s_per_layer=T / (us * 1e-6), mfma_frac=F / (us * 1e-6) / BF16_PEAK,
+                hbm_frac=B / (us * 1e-6) / HBM_PEAK, flops=F, bytes=B)
+
+
+def cpu_baseline_decode(layers_cpu=LAYERS, reps=3):
+    """The oracle (torch CPU restatement of the reference decode path) on this host's cores."""
+    oracle = importlib.import_module("oracle.gdn_oracle")
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    g_ = torch.Generator().manual_seed(1)
+    ls = []
+    for _ in range(layers_cpu):
+        ls.append(dict(
+            mixed=torch.randn(N_SLOTS, C, generator=g_).to(torch.bfloat16),
+            z=torch.randn(N_SLOTS, HV * D, generator=g_).to(torch.bfloat16),
+            a=torch.randn(N_SLOTS, HV, generator=g_).to(torch.bfloat16),
+            b=torch.randn(N_SLOTS, HV, generator=g_).to(torch.bfloat16),
+            conv_state=torch.randn(N_SLOTS, C, KC, generator=g_).to(torch.bfloat16),
+            conv_weight=(0.5 * torch.randn(C, KC, generator=g_)).to(torch.bfloat16),
+            A_log=torch.full((HV,), -2.302585092994046), dt_bias=torch.full((HV,), 2.0),
+            norm_weight=(1 + 0.02 * torch.randn(D, generator=g_)).to(torch.bfloat16),
+            rec_state=0.02 * torch.randn(N_SLOTS, HV, D, D, generator=g_)))
+
+    def one():
+        for p in ls:
+            oracle.gdn_decode_core(p["mixed"], p["z"], p["a"], p["b"], p["conv_state"], p["conv_weight"],
+                                   p["A_log"], p["dt_bias"], p["norm_weight"], p["rec_state"], HK, HV, D)
+    one()  # warm-up
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        one()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    us = times[len(times) // 2] * 1e6 / layers_cpu
+    return dict(value=us, unit="us/layer", cores=threads, kind="port",
+                sample=f"oracle gdn_decode_core, {layers_cpu} distinct layers x {reps} timed passes "
+                       f"(median), same shapes as the GPU workload, torch {torch.__version__} CPU, "
+                       f"{threads} threads")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--only", choices=["decode", "prefill"], default=None)
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="first run a 256 MiB device-to-device copy (counter calibration for rocprof)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (the GDN path is benchmarked on a single "
+              "MI355X); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    gdn = importlib.import_module(PKG)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    if args.calib_copy:
+        src = torch.ones(64 << 20, dtype=torch.float32, device=dev)   # 256 MiB
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+    res = {}
+    if args.only in (None, "decode"):
+        res["decode"] = bench_decode(gdn, dev, args.steps, args.warmup)
+    if args.only in (None, "prefill") and not args.no_prefill:
+        try:
+            res["prefill"] = bench_prefill(gdn, dev)
+        except Exception as e:  # prefill kernel absent in this build
+            res["prefill"] = {"error": str(e)[:200]}
+    if args.only == "prefill":
+        print(json.dumps(res["prefill"]))
+        return
+    dec = res["decode"]
+    bpl = decode_bytes_per_layer()
+    achieved = bpl / (dec["us_per_layer"] * 1e-6) / 1e9
+    line = {
+        "metric": "GDN prefill tokens/s/layer (MFMA %); 16-slot decode µs/layer (HBM GB/s %)",
+        "value": round(dec["us_per_layer"], 3),
+        "unit": "us/layer (16-slot GDN decode step, fused conv+gating+recurrent+gated norm)",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(dec["ms_per_step"], 4),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp32 state / bf16 activations", "data": "synthetic (seeded), random-init parameters",
+        "config": {"workload": "GDN decode step, 16 slots x 1 token, H_k=16, H_v=32, d=128, conv 8192x4, "
+                               "48 distinct layers, HIP-graph replay", "slots": N_SLOTS, "layers": LAYERS},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                     "frac": round(achieved * 1e9 / HBM_PEAK, 4), "traffic": None,
+                     "kernel": "decode_fused_kernel<2,true>", "algorithmic_bytes_per_launch": bpl,
+                     "us_per_launch_graph": round(dec["us_per_layer"], 3),
+                     "us_per_launch_eager": round(dec["us_per_layer_eager"], 3)},
+    }
+    if "prefill" in res:
+        line["secondary"] = res["prefill"]
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline_decode()
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()
