@@ -30,12 +30,18 @@ def _tokens_view(x, name):
 
 
 def _seq_args(B, T, cu_seqlens, device):
+    """(device int32 cu_seqlens | None, n_seq, per-sequence length for the uniform case).
+    cu_seqlens is checked on the host (the kernels index memory with it): 1-D, starts at 0,
+    non-decreasing, ends at the packed token count."""
     if cu_seqlens is None:
         return None, B, T
     if B != 1:
         raise ValueError("cu_seqlens needs packed inputs with batch size 1")
+    host = cu_seqlens.detach().to("cpu", torch.int64).reshape(-1)
+    if host.numel() < 2 or int(host[0]) != 0 or int(host[-1]) != T or bool((host[1:] < host[:-1]).any()):
+        raise ValueError(f"cu_seqlens must be non-decreasing from 0 to {T}, got {host.tolist()[:8]}...")
     cu = cu_seqlens.to(device=device, dtype=torch.int32).contiguous()
-    return cu, cu.numel() - 1, 0
+    return cu, host.numel() - 1, 0
 
 
 def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size=64, initial_state=None,

@@ -12,7 +12,9 @@ reference exactly: l2norm runs in the input dtype (bf16), the recurrences run in
 update runs in the weight dtype, the gated norm follows HF's cast order.
 
 How each function is pinned (tests/test_oracle.py):
-  l2norm                      -- HF ``l2norm`` (library routine), bit-exact.
+  l2norm                      -- HF ``l2norm`` (library routine): bit-exact on tensors without a
+                                 scalar tail in torch's vectorised loop, within one bf16 ulp of the
+                                 inverse norm elsewhere (torch double-rounds bf16 rsqrt there).
   unit_lower_inv              -- T (I - X) = I; ``torch.linalg.solve_triangular``; HF's 63-step loop.
   chunk_gated_delta_rule_v2   -- token-by-token recurrence (closed-form equivalence), HF
                                  ``torch_chunk_gated_delta_rule``, padding / split / varlen invariances,
@@ -40,9 +42,26 @@ __all__ = [
 ]
 
 
+def _op(x, dtype):
+    """Round an fp32 result once to ``dtype``: the result of one torch elementwise op on a tensor of
+    that dtype.  (torch's CPU kernels compute bf16 elementwise ops in fp32 and round once in their
+    vectorised body, but double-round some ops such as rsqrt in the scalar tail of the loop, which
+    makes the result depend on the element's position by one bf16 ulp; the oracle uses the
+    single rounding everywhere.)"""
+    return x.to(dtype)
+
+
 def l2norm(x, dim=-1, eps=1e-6):
-    """x * rsqrt(sum(x*x) + eps) in x's dtype.  src/gdn_chunk_fast.py:17-18, HF:242-245."""
-    return x * torch.rsqrt((x * x).sum(dim=dim, keepdim=True) + eps)
+    """x * rsqrt(sum(x*x) + eps) with every op rounded to x's dtype, as torch evaluates it on a
+    bf16 tensor (products rounded, fp32-accumulated sum rounded, +eps, rsqrt, product).
+    src/gdn_chunk_fast.py:17-18, HF:242-245."""
+    dt = x.dtype
+    xf = x.float()
+    sq = _op(xf * xf, dt).float()
+    s = _op(sq.sum(dim=dim, keepdim=True), dt).float()
+    t = _op(s + eps, dt).float()
+    inv = _op(torch.rsqrt(t), dt).float()
+    return _op(xf * inv, dt)
 
 
 def small_unit_lower_inv(X):
@@ -135,7 +154,7 @@ def chunk_gated_delta_rule_v2(query, key, value, g, beta, chunk_size=64, initial
     Kd = (key * (glast.unsqueeze(-1) - g).exp().unsqueeze(-1)).transpose(-1, -2)
     S = (torch.zeros(B, H, dk, dv, dtype=torch.float32) if initial_state is None
          else initial_state.to(torch.float32))
-    outs = []
+    outs = [torch.zeros(B, H, 0, C, dv)] if n == 0 else []   # empty sequence: no chunks
     for i in range(n):
         vn = V[:, :, i] - Kc[:, :, i] @ S
         outs.append(Qg[:, :, i] @ S + QK[:, :, i] @ vn)
@@ -261,7 +280,7 @@ def elem_conv_update(x, state, weight, bias):
     out = (win * weight).sum(-1, keepdim=True)
     if bias is not None:
         out = out + bias.view(1, -1, 1)
-    return F.silu(out).to(x.dtype)
+    return _op(F.silu(out.float()), out.dtype).to(x.dtype)
 
 
 def causal_conv1d_update(hidden_states, conv_state, weight, bias=None, activation=None):
@@ -283,13 +302,17 @@ def causal_conv1d_prefill(x, weight, bias=None, history=None):
     new_state [1,C,K] = last K inputs, left zero-padded, src/cb_tp.py:158-162 and :260)."""
     C, K = weight.shape
     L = x.shape[-1]
+    if L == 0:  # empty prompt: no outputs, the state keeps the history (or zeros)
+        state = torch.zeros(x.shape[0], C, K, dtype=x.dtype) if history is None else history.to(x.dtype)
+        return x.clone(), state.contiguous()
     if history is None:
-        out = F.silu(F.conv1d(x, weight.unsqueeze(1), bias, padding=K - 1, groups=C)[:, :, :L])
+        conv = F.conv1d(x, weight.unsqueeze(1), bias, padding=K - 1, groups=C)[:, :, :L]
         state = x[:, :, -K:] if L >= K else F.pad(x, (K - L, 0))
     else:
         full = torch.cat([history.to(x.dtype), x], dim=-1)
-        out = F.silu(F.conv1d(full[:, :, 1:], weight.unsqueeze(1), bias, groups=C))
+        conv = F.conv1d(full[:, :, 1:], weight.unsqueeze(1), bias, groups=C)
         state = full[:, :, -K:]
+    out = _op(F.silu(conv.float()), conv.dtype)
     return out.to(x.dtype), state.contiguous()
 
 
@@ -308,7 +331,7 @@ def gated_rmsnorm(hidden_states, gate, weight, eps=1e-6):
 def gdn_gating(a, b, A_log, dt_bias):
     """beta = sigmoid(b) (input dtype), g = -exp(A_log) * softplus(a + dt_bias) in fp32.
     src/cb_engine.py:337-338 (HF:497-498)."""
-    beta = b.sigmoid()
+    beta = _op(b.float().sigmoid(), b.dtype)
     g = -A_log.float().exp() * F.softplus(a.float() + dt_bias)
     return beta, g
 

@@ -1,0 +1,211 @@
+"""GPU parity of the prefill kernels against the CPU oracle (same seeded inputs).
+
+Tolerances: output rel-L2 <= 1e-2 (bf16 activations), final fp32 state rel-L2 <= 1e-3; conv state
+capture bit-exact; the 64x64 inverse to fp32 rounding.
+"""
+import pytest
+import torch
+
+from conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+OUT_TOL = 1e-2
+STATE_TOL = 1e-3
+
+
+def _gdn_inputs(T, Hk, Hv, D=128, seed=0, B=1, state=True, decay=0.1):
+    g_ = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, T, Hk, D, generator=g_).to(torch.bfloat16)
+    k = torch.randn(B, T, Hk, D, generator=g_).to(torch.bfloat16)
+    v = torch.randn(B, T, Hv, D, generator=g_).to(torch.bfloat16)
+    beta = torch.sigmoid(torch.randn(B, T, Hv, generator=g_)).to(torch.bfloat16)
+    g = -torch.nn.functional.softplus(torch.randn(B, T, Hv, generator=g_) + 2) * decay
+    s0 = 0.02 * torch.randn(B, Hv, D, D, generator=g_) if state else None
+    return q, k, v, g, beta, s0
+
+
+def _rep(x, r):
+    return x.repeat_interleave(r, dim=2) if r > 1 else x
+
+
+def test_unit_lower_inv(gdn, oracle, dev):
+    """T (I - X) = I to fp32 rounding; equals the oracle's blocked inverse and solve_triangular."""
+    g_ = torch.Generator().manual_seed(0)
+    k = torch.nn.functional.normalize(torch.randn(64, 64, 128, generator=g_), dim=-1)
+    beta = torch.rand(64, 64, generator=g_)
+    G = torch.cumsum(-torch.rand(64, 64, generator=g_) * 0.3, dim=-1)
+    dec = (G.unsqueeze(-1) - G.unsqueeze(-2)).tril().exp().tril()
+    X = -((k * beta.unsqueeze(-1)) @ k.transpose(-1, -2) * dec).tril(-1)
+    T = gdn._unit_lower_inv(X.to(dev)).cpu()
+    I = torch.eye(64)
+    exact = torch.linalg.solve_triangular((I - X).double(), I.double().expand(64, 64, 64), upper=False)
+    assert rel_l2(T, exact) <= 1e-5
+    assert rel_l2(T, oracle.unit_lower_inv(X)) <= 1e-5
+    assert ((T.double() @ (I - X).double()) - I.double()).abs().max().item() <= 1e-4
+
+
+@pytest.mark.parametrize("T,Hk,Hv,repeat", [(150, 2, 2, True), (1, 2, 4, False), (64, 2, 4, False),
+                                            (65, 4, 8, False), (300, 16, 32, False), (129, 2, 6, False)])
+def test_chunk_prefill_vs_oracle(gdn, oracle, dev, T, Hk, Hv, repeat):
+    q, k, v, g, beta, s0 = _gdn_inputs(T, Hk, Hv, seed=T + Hv)
+    r = Hv // Hk
+    o_ref, s_ref = oracle.chunk_gated_delta_rule_v2(_rep(q, r), _rep(k, r), v, g, beta, 64, s0, True, True)
+    qd, kd = (_rep(q, r), _rep(k, r)) if repeat else (q, k)
+    o, s = gdn.fast_chunk_gated_delta_rule_v2(qd.to(dev), kd.to(dev), v.to(dev), g.to(dev), beta.to(dev),
+                                              initial_state=s0.to(dev), output_final_state=True,
+                                              use_qk_l2norm_in_kernel=True)
+    torch.cuda.synchronize()
+    assert o.shape == (1, T, Hv, 128) and o.dtype == torch.bfloat16
+    assert rel_l2(o, o_ref) <= OUT_TOL, rel_l2(o, o_ref)
+    assert rel_l2(s, s_ref) <= STATE_TOL, rel_l2(s, s_ref)
+
+
+def test_chunk_prefill_v1_name_no_state_fp32_beta(gdn, oracle, dev):
+    q, k, v, g, beta, _ = _gdn_inputs(200, 2, 2, seed=11, state=False)
+    beta = beta.float()
+    o_ref, s_ref = oracle.chunk_gated_delta_rule_v1(q, k, v, g, beta, 64, None, True, True)
+    o, s = gdn.fast_chunk_gated_delta_rule(q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta.to(dev),
+                                           output_final_state=True, use_qk_l2norm_in_kernel=True)
+    assert rel_l2(o, o_ref) <= OUT_TOL and rel_l2(s, s_ref) <= STATE_TOL
+    _, none = gdn.fast_chunk_gated_delta_rule(q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta.to(dev),
+                                              use_qk_l2norm_in_kernel=True)
+    assert none is None
+
+
+def test_chunk_prefill_without_l2norm_and_batch(gdn, oracle, dev):
+    """Pre-normalised q, k with use_qk_l2norm_in_kernel=False; B=3 dense batch."""
+    q, k, v, g, beta, _ = _gdn_inputs(130, 2, 2, seed=12, B=3, state=False)
+    q = oracle.l2norm(q)
+    k = oracle.l2norm(k)
+    s0 = 0.02 * torch.randn(3, 2, 128, 128)
+    o_ref, s_ref = oracle.chunk_gated_delta_rule_v2(q, k, v, g, beta, 64, s0, True, False)
+    o, s = gdn.fast_chunk_gated_delta_rule_v2(q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta.to(dev),
+                                              initial_state=s0.to(dev), output_final_state=True)
+    assert rel_l2(o, o_ref) <= OUT_TOL and rel_l2(s, s_ref) <= STATE_TOL
+
+
+def test_chunk_prefill_varlen_matches_per_sequence(gdn, oracle, dev):
+    lens = [100, 64, 0, 236, 1, 65]
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int32)
+    T = int(cu[-1])
+    Hk, Hv = 4, 8
+    q, k, v, g, beta, _ = _gdn_inputs(T, Hk, Hv, seed=13, state=False)
+    s0 = 0.02 * torch.randn(len(lens), Hv, 128, 128)
+    o_ref, s_ref = oracle.chunk_gated_delta_rule_varlen(_rep(q, 2), _rep(k, 2), v, g, beta, cu, 64, s0, True, True)
+    o, s = gdn.fast_chunk_gated_delta_rule_v2(q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta.to(dev),
+                                              initial_state=s0.to(dev), output_final_state=True,
+                                              use_qk_l2norm_in_kernel=True, cu_seqlens=cu.to(dev))
+    assert rel_l2(o, o_ref) <= OUT_TOL and rel_l2(s, s_ref) <= STATE_TOL
+    assert torch.equal(s[2].cpu(), s0[2]), "an empty sequence keeps its initial state"
+    with pytest.raises(ValueError):
+        gdn.fast_chunk_gated_delta_rule_v2(q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta.to(dev),
+                                           cu_seqlens=torch.tensor([0, 5, 3, T], dtype=torch.int32))
+
+
+def test_chunk_prefill_split_invariance(gdn, dev):
+    """Prefill in two pieces with final -> initial state equals one call (prefill_chunk contract)."""
+    q, k, v, g, beta, s0 = _gdn_inputs(320, 2, 4, seed=14)
+    args = lambda a, b: [x[:, a:b].to(dev) for x in (q, k, v, g, beta)]
+    o, s = gdn.fast_chunk_gated_delta_rule_v2(*args(0, 320), initial_state=s0.to(dev), output_final_state=True,
+                                              use_qk_l2norm_in_kernel=True)
+    o1, s1 = gdn.fast_chunk_gated_delta_rule_v2(*args(0, 128), initial_state=s0.to(dev), output_final_state=True,
+                                                use_qk_l2norm_in_kernel=True)
+    o2, s2 = gdn.fast_chunk_gated_delta_rule_v2(*args(128, 320), initial_state=s1, output_final_state=True,
+                                                use_qk_l2norm_in_kernel=True)
+    assert rel_l2(torch.cat([o1, o2], 1), o) <= 1e-3 and rel_l2(s2, s) <= 1e-5
+
+
+def test_chunk_prefill_long_sequence_state_accuracy(gdn, oracle, dev):
+    """T=32768 with 4 value heads (the long-sequence shape at reduced width): final-state rel-L2."""
+    q, k, v, g, beta, s0 = _gdn_inputs(32768, 2, 4, seed=15)
+    o_ref, s_ref = oracle.chunk_gated_delta_rule_v2(_rep(q, 2), _rep(k, 2), v, g, beta, 64, s0, True, True)
+    o, s = gdn.fast_chunk_gated_delta_rule_v2(q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta.to(dev),
+                                              initial_state=s0.to(dev), output_final_state=True,
+                                              use_qk_l2norm_in_kernel=True)
+    assert rel_l2(o, o_ref) <= OUT_TOL and rel_l2(s, s_ref) <= STATE_TOL
+
+
+def test_chunk_prefill_slow_decay_state_accuracy(gdn, oracle, dev):
+    """Slow decay (long memory across chunks) keeps the state within tolerance."""
+    q, k, v, g, beta, s0 = _gdn_inputs(2048, 2, 2, seed=16, decay=0.005)
+    o_ref, s_ref = oracle.chunk_gated_delta_rule_v2(q, k, v, g, beta, 64, s0, True, True)
+    o, s = gdn.fast_chunk_gated_delta_rule_v2(q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta.to(dev),
+                                              initial_state=s0.to(dev), output_final_state=True,
+                                              use_qk_l2norm_in_kernel=True)
+    assert rel_l2(o, o_ref) <= OUT_TOL and rel_l2(s, s_ref) <= STATE_TOL
+
+
+@pytest.mark.parametrize("with_history", [False, True])
+def test_conv_prefill(gdn, oracle, dev, with_history):
+    C, K = 512, 4
+    lens = [37, 2, 0, 130, 64]
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int32)
+    T = int(cu[-1])
+    g_ = torch.Generator().manual_seed(17)
+    x = torch.randn(T, C, generator=g_).to(torch.bfloat16)
+    w = (0.5 * torch.randn(C, K, generator=g_)).to(torch.bfloat16)
+    hist = torch.randn(len(lens), C, K, generator=g_).to(torch.bfloat16) if with_history else None
+    out, st = gdn.causal_conv1d_prefill(x.t().unsqueeze(0).to(dev), w.to(dev), None,
+                                        None if hist is None else hist.to(dev), cu.to(dev))
+    out = out[0].t().cpu()
+    for s in range(len(lens)):
+        a, b = int(cu[s]), int(cu[s + 1])
+        o_ref, st_ref = oracle.causal_conv1d_prefill(x[a:b].t().unsqueeze(0), w, None,
+                                                     None if hist is None else hist[s:s + 1])
+        assert torch.equal(st[s].cpu(), st_ref[0]), f"conv state of sequence {s}"
+        if b > a:
+            d = (out[a:b].float() - o_ref[0].t().float()).abs()
+            assert (d <= o_ref[0].t().float().abs() * 2 ** -7 + 1e-6).all()
+
+
+def test_prefill_core_then_decode_matches_oracle(gdn, oracle, dev):
+    """Fused prefill layer (conv + gating + chunked rule + gated norm) on 3 packed prompts with conv
+    history and initial state, then one fused decode step from the states it left."""
+    Hk, Hv, D, K = 4, 8, 128, 4
+    C = (2 * Hk + Hv) * D
+    lens = [70, 128, 33]
+    cu = torch.tensor([0, 70, 198, 231], dtype=torch.int32)
+    T = 231
+    g_ = torch.Generator().manual_seed(18)
+    mixed = torch.randn(T, C, generator=g_).to(torch.bfloat16)
+    z = torch.randn(T, Hv * D, generator=g_).to(torch.bfloat16)
+    a = torch.randn(T, Hv, generator=g_).to(torch.bfloat16)
+    b = torch.randn(T, Hv, generator=g_).to(torch.bfloat16)
+    cw = (0.5 * torch.randn(C, K, generator=g_)).to(torch.bfloat16)
+    A_log = torch.full((Hv,), -2.302585)
+    dt = torch.full((Hv,), 2.0)
+    nw = (1 + 0.02 * torch.randn(D, generator=g_)).to(torch.bfloat16)
+    hist = torch.randn(3, C, K, generator=g_).to(torch.bfloat16)
+    s0 = 0.02 * torch.randn(3, Hv, D, D, generator=g_)
+    core_ref, conv_ref, rec_ref = oracle.gdn_prefill_core(mixed, z, a, b, cw, A_log, dt, nw, Hk, Hv, D, cu,
+                                                          hist, s0)
+    dv = lambda x: x.to(dev)
+    core, conv, rec = gdn.gdn_prefill_core(dv(mixed), dv(z), dv(a), dv(b), dv(cw), dv(A_log), dv(dt), dv(nw),
+                                           Hk, Hv, D, cu_seqlens=dv(cu), conv_history=dv(hist),
+                                           initial_state=dv(s0))
+    assert torch.equal(conv.cpu(), conv_ref)
+    assert rel_l2(core, core_ref) <= OUT_TOL and rel_l2(rec, rec_ref) <= STATE_TOL
+    # one decode step for the 3 slots from the prefilled states
+    m1 = torch.randn(3, C, generator=g_).to(torch.bfloat16)
+    z1 = torch.randn(3, Hv * D, generator=g_).to(torch.bfloat16)
+    a1 = torch.randn(3, Hv, generator=g_).to(torch.bfloat16)
+    b1 = torch.randn(3, Hv, generator=g_).to(torch.bfloat16)
+    cs_ref, rs_ref = conv_ref.clone(), rec_ref.clone()
+    o_ref = oracle.gdn_decode_core(m1, z1, a1, b1, cs_ref, cw, A_log, dt, nw, rs_ref, Hk, Hv, D)
+    o = gdn.gdn_decode_core(dv(m1), dv(z1), dv(a1), dv(b1), conv, dv(cw), dv(A_log), dv(dt), dv(nw), rec,
+                            Hk, Hv, D)
+    assert torch.equal(conv.cpu(), cs_ref)
+    assert rel_l2(o, o_ref) <= OUT_TOL and rel_l2(rec, rs_ref) <= STATE_TOL
+
+
+def test_gating(gdn, oracle, dev):
+    g_ = torch.Generator().manual_seed(19)
+    a = torch.randn(50, 32, generator=g_).to(torch.bfloat16)
+    b = torch.randn(50, 32, generator=g_).to(torch.bfloat16)
+    A_log = torch.log(torch.rand(32, generator=g_) * 16 + 0.1)
+    dt = torch.rand(32, generator=g_)
+    beta_ref, g_ref = oracle.gdn_gating(a, b, A_log, dt)
+    beta, g = gdn.gdn_gating(a.to(dev), b.to(dev), A_log.to(dev), dt.to(dev))
+    assert torch.equal(beta.cpu(), beta_ref)
+    assert rel_l2(g, g_ref) <= 1e-6
