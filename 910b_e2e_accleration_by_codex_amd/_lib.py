@@ -30,8 +30,9 @@ _SIGNATURES = {
     "gdn_decode_fused": ([_P, _L, _P, _L, _P, _P, _L, _P, _P, _P, _P, _P, _P, _I, _F, _P, _P, _I, _I, _I,
                           _I, _I, _P], _I),
     "gdn_unit_lower_inv": ([_P, _P, _L, _I, _P], _I),
-    "gdn_chunk_prefill": ([_P, _L, _P, _L, _P, _L, _P, _P, _I, _P, _P, _P, _L, _P, _I, _I, _I, _I, _I, _I,
-                           _I, _P], _I),
+    "gdn_chunk_prefill": ([_P, _L, _P, _L, _P, _L, _P, _P, _I, _P, _P, _P, _L, _P, _P, _L, _I, _I, _I, _I,
+                           _I, _I, _I, _P, _L, _P], _I),
+    "gdn_chunk_prefill_workspace_bytes": ([_L, _I], _L),
     "gdn_conv_prefill": ([_P, _L, _P, _P, _P, _P, _P, _L, _P, _I, _I, _I, _I, _P], _I),
     "gdn_gating": ([_P, _P, _L, _P, _P, _P, _P, _L, _I, _P], _I),
 }

@@ -8,15 +8,17 @@ namespace gdn {
 constexpr int kWave = 64;
 
 // ---- bf16 <-> fp32 -------------------------------------------------------------------------
-// bf16 is the upper half of an IEEE fp32; fp32 -> bf16 rounds to nearest even (torch's rule),
-// NaN stays a quiet NaN.
+// bf16 is the upper half of an IEEE fp32; fp32 -> bf16 rounds to nearest even (torch's rule)
+// with gfx950's v_cvt_pk_bf16_f32 (branch-free; NaN stays NaN).
 __device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
 
-__device__ __forceinline__ uint16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+__device__ __forceinline__ uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+
+// Two values -> packed bf16 pair (low half = a), one conversion instruction.
+__device__ __forceinline__ uint32_t f2bf2(float a, float b) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t p = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, p);
 }
 
 // Round an fp32 value to the nearest bf16 and return it as fp32 (emulates one torch bf16 op).

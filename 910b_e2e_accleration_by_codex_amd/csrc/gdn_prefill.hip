@@ -78,34 +78,44 @@ __device__ __forceinline__ void st16_f32(float* M, int ld, f32x4 acc, int lane) 
 }
 
 // ---- (I - X)^{-1} for a strictly lower 64x64 fp32 X (only its strictly lower part is read) ----
-// Same algorithm as src/gdn_chunk_fast.py:33-62: the four 16x16 diagonal blocks by the row
-// recurrence (here: forward substitution, one column per lane group), then the merges
-// [[A,0],[B X21 A, B]] for 32x32 and 64x64, on fp32 MFMA.  All 4 waves must call it (it holds
-// barriers).  sY: 4 x 16 x 16 fp32 scratch.  Writes all of sT (upper blocks zero).
+// Same blocking as src/gdn_chunk_fast.py:33-62 -- the four 16x16 diagonal blocks first, then the
+// merges [[A,0],[B X21 A, B]] for 32x32 and 64x64 -- all on fp32 MFMA.  A diagonal block is
+// inverted as (I+X)(I+X^2)(I+X^4)(I+X^8) (exact for nilpotent X, X^16 = 0) instead of the
+// reference's 16-step row recurrence: six dependent products instead of sixteen dependent steps;
+// with |X_ij| <= 1 (l2-normalised k, beta <= 1, decay <= 1) the powers of a 16x16 block stay far
+// from fp32 overflow (the reference avoids powers of the whole 64x64 block, which can overflow).
+// All 4 waves must call it (it holds barriers).  sY: 4 x 16 x 16 fp32 scratch.  Writes all of sT
+// (upper blocks zero).
 __device__ void unit_lower_inv64(const float* sX, float* sT, float* sY, int w, int lane) {
   using namespace pf;
-  {  // diagonal block w: lane owns column c, rows g + 4m of the block
+  {  // diagonal block w: T = (I+X)(I+X^2)(I+X^4)(I+X^8) (X^16 = 0), six fp32 MFMA products
     const int c = lane & 15, g = lane >> 4;
     const float* Xb = sX + 16 * w * LDF + 16 * w;
-    float acc[4] = {0.f, 0.f, 0.f, 0.f}, tv[4] = {0.f, 0.f, 0.f, 0.f};
+    float* Tb = sT + 16 * w * LDF + 16 * w;
+    float* P = sY + w * 256;  // wave-private 16x16 scratch (pitch 16)
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int gj = j & 3, mj = j >> 2;
-      const float mine = (j == c ? 1.0f : 0.0f) + acc[mj];
-      const float tj = __shfl(mine, c + 16 * gj, kWave);
-      if (g == gj) tv[mj] = tj;
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const int i = g + 4 * m;
-        if (i > j) acc[m] += Xb[i * LDF + j] * tj;
-      }
+    for (int r = 0; r < 4; ++r) {
+      const int i = 4 * g + r;
+      Tb[i * LDF + c] = Xb[i * LDF + c] + (i == c ? 1.0f : 0.0f);
     }
-    float* Tb = sT + 16 * w * LDF;
+    const float* Pin = Xb;
+    int ldp = LDF;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) Tb[(g + 4 * m) * LDF + 16 * w + c] = tv[m];
+    for (int step = 0; step < 3; ++step) {
+      f32x4 p2 = mm16_f32(Pin, ldp, Pin, ldp, f32x4{0.f, 0.f, 0.f, 0.f}, lane);  // X^(2^(step+1))
+      st16_f32(P, 16, p2, lane);
+      __builtin_amdgcn_wave_barrier();
+      f32x4 tp = mm16_f32(Tb, LDF, P, 16, f32x4{0.f, 0.f, 0.f, 0.f}, lane);     // T X^(2^(step+1))
+#pragma unroll
+      for (int r = 0; r < 4; ++r) Tb[(4 * g + r) * LDF + c] += tp[r];
+      __builtin_amdgcn_wave_barrier();
+      Pin = P;
+      ldp = 16;
+    }
+    float* Trow = sT + 16 * w * LDF;
     for (int col = 16 * (w + 1) + c; col < CH; col += 16)
 #pragma unroll
-      for (int m = 0; m < 4; ++m) Tb[(g + 4 * m) * LDF + col] = 0.f;
+      for (int r = 0; r < 4; ++r) Trow[(4 * g + r) * LDF + col] = 0.f;
   }
   __syncthreads();
   // level 1: T10 = T11 (X10 T00), T32 = T33 (X32 T22)
@@ -150,7 +160,7 @@ __global__ __launch_bounds__(pf::NT) void unit_lower_inv_kernel(const float* __r
   __shared__ float sX[CH * LDF], sT[CH * LDF], sY[4 * 256];
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const float* Xm = X + (int64_t)blockIdx.x * CH * CH;
-  for (int i = t; i < CH * CH; i += NT) sX[(i / CH) * LDF + (i % CH)] = Xm[i];
+  for (int i = t; i < CH * CH; i += NT) sX[(i / CH) * LDF + (i % CH)] = (i / CH) > (i % CH) ? Xm[i] : 0.f;
   __syncthreads();
   unit_lower_inv64(sX, sT, sY, w, lane);
   float* Tm = T + (int64_t)blockIdx.x * CH * CH;
@@ -158,399 +168,546 @@ __global__ __launch_bounds__(pf::NT) void unit_lower_inv_kernel(const float* __r
 }
 
 // ============================================================================================
-// Fused chunked prefill.
+// Chunked prefill, part 1: chunk-local quantities (parallel over every (chunk, value head)).
 // ============================================================================================
-template <int BV>
-struct PrefillSmem {
-  uint16_t K[pf::CH * pf::LDK];     // K chunk, row-major (token, feature)
-  uint16_t KT[pf::D * pf::LDT];     // K chunk transposed (feature, token)
-  uint16_t VT[BV * pf::LDT];        // V tile transposed (column, token)
-  uint16_t QK[pf::CH * pf::LDT];    // scale * q.k e^{Gi-Gj}, i >= j
-  uint16_t ST[BV * pf::LDK];        // bf16 copy of the state tile, transposed (column, feature)
-  union {
-    struct {
-      float X[pf::CH * pf::LDF];
-      float T[pf::CH * pf::LDF];
-      float Y[4 * 256];
-    } inv;
-    struct {
-      uint16_t W[pf::CH * pf::LDK];   // W rows (token, feature)
-      uint16_t VN[BV * pf::LDT];      // bf16(vn), transposed (column, token)
-      uint16_t VSH[BV * pf::LDT];     // hi of dec*vn, transposed
-      uint16_t VSL[BV * pf::LDT];     // lo of dec*vn, transposed
-    } upd;
-  } u;
-  float G[pf::CH], EG[pf::CH], B[pf::CH], DEC[pf::CH];
-  float GL;
+// Workspace record per (chunk slot, value head), consumed by the state kernel in exactly the
+// layouts it stages into LDS (so its per-chunk staging is plain copies):
+//   W   [64][128] bf16 = T diag(beta e^G) K          Tb [64][64] bf16 = T diag(beta)
+//   QK  [64][64]  bf16 = scale q.k e^{Gi-Gj}, i>=j    Qg [64][128] bf16 = scale e^{G_t} q_t
+//   KT  [128][64] bf16 = K^T (l2-normalised keys)     DEC [64] fp32 = e^{G_last - G_t}
+//   GL  fp32 = e^{G_last}
+namespace ws {
+constexpr int W = 0;                           // byte offsets inside one record
+constexpr int TB = W + pf::CH * pf::D * 2;     // 16384
+constexpr int QK = TB + pf::CH * pf::CH * 2;   // 24576
+constexpr int QG = QK + pf::CH * pf::CH * 2;   // 32768
+constexpr int KT = QG + pf::CH * pf::D * 2;    // 49152
+constexpr int DEC = KT + pf::D * pf::CH * 2;   // 65536
+constexpr int GL = DEC + pf::CH * 4;           // 65792
+constexpr int BYTES = 66048;                   // record size (multiple of 256)
+}  // namespace ws
+
+struct ChunkPos {
+  int64_t t0;  // first packed token of the chunk
+  int len;     // valid tokens (1..64)
+  int seq, c;  // sequence and chunk index inside it
 };
 
-// Register-staged chunk inputs (prefetched one chunk ahead).
-template <int BV>
-struct ChunkRegs {
-  static constexpr int NV = BV * pf::CH / 8 / pf::NT;  // 16-byte V pieces per thread
-  u16x8 k[4];
-  u16x8 q[4];
-  u16x8 v[NV > 0 ? NV : 1];
-  float g, beta;
-};
-
-struct SeqInfo {
-  int64_t t0;  // first packed token of the sequence
-  int L;       // its length
-};
-
-template <int BV, typename BetaT>
-__device__ __forceinline__ void load_chunk(ChunkRegs<BV>& r, const uint16_t* q, int64_t qs, const uint16_t* k,
-                                           int64_t ks, const uint16_t* v, int64_t vs, const float* g,
-                                           const BetaT* beta, SeqInfo si, int c, int h, int hk, int Hv, int vcol0,
-                                           int t) {
-  using namespace pf;
-  const int base = c * CH;
-  const u16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
-  // K: rows t/16 + 16i, features 8*(t%16)
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = (t >> 4) + 16 * i;
-    const int tok = base + row;
-    r.k[i] = tok < si.L ? *reinterpret_cast<const u16x8*>(k + (si.t0 + tok) * ks + (int64_t)hk * D + 8 * (t & 15))
-                        : zero;
+// Position of chunk `slot` (dense index over all chunks of all sequences).
+__device__ __forceinline__ ChunkPos chunk_pos(int slot, const int32_t* cu, const int32_t* seq_chunk0, int nseq,
+                                              int seq_len) {
+  ChunkPos p;
+  if (cu) {
+    int lo = 0, hi = nseq - 1;  // last sequence whose first chunk slot <= slot
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (seq_chunk0[mid] <= slot) lo = mid;
+      else hi = mid - 1;
+    }
+    p.seq = lo;
+    p.c = slot - seq_chunk0[lo];
+    p.t0 = (int64_t)cu[lo] + (int64_t)p.c * pf::CH;
+    const int64_t left = (int64_t)cu[lo + 1] - p.t0;
+    p.len = left < pf::CH ? (int)left : pf::CH;
+  } else {
+    const int nch = (seq_len + pf::CH - 1) / pf::CH;
+    p.seq = slot / nch;
+    p.c = slot % nch;
+    p.t0 = (int64_t)p.seq * seq_len + (int64_t)p.c * pf::CH;
+    const int left = seq_len - p.c * pf::CH;
+    p.len = left < pf::CH ? left : pf::CH;
   }
-  // Q in MFMA A-fragment order of this wave: row 16w + l%16, features 8(l/16) + 32 ks
-  {
-    const int w = t >> 6, lane = t & 63;
-    const int tok = base + 16 * w + (lane & 15);
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-      r.q[s] = tok < si.L ? *reinterpret_cast<const u16x8*>(q + (si.t0 + tok) * qs + (int64_t)hk * D +
-                                                            32 * s + 8 * (lane >> 4))
-                          : zero;
-  }
-  // V tile: BV columns / 8 pieces per row
-  constexpr int PPR = BV / 8;
-#pragma unroll
-  for (int i = 0; i < ChunkRegs<BV>::NV; ++i) {
-    const int idx = t + NT * i;
-    const int row = idx / PPR, pc = idx % PPR;
-    const int tok = base + row;
-    r.v[i] = tok < si.L ? *reinterpret_cast<const u16x8*>(v + (si.t0 + tok) * vs + (int64_t)h * D + vcol0 + 8 * pc)
-                        : zero;
-  }
-  if (t < CH) {
-    const int tok = base + t;
-    r.g = tok < si.L ? g[(si.t0 + tok) * Hv + h] : 0.f;
-    r.beta = tok < si.L ? Elem<BetaT>::load(beta + (si.t0 + tok) * Hv + h) : 0.f;
-  }
+  return p;
 }
 
-// l2norm (bf16 op rounding) of 8 values whose row is spread over the lanes selected by `mask`.
-__device__ __forceinline__ void l2norm8(u16x8& x, int xor_lo, int xor_hi) {
-  float f[8], ss = 0.f;
+// Load 4 token rows x 8 features (rows 4*tq.., features f0..f0+7) of a [tokens, heads*D] bf16
+// tensor, zero beyond `len`, and l2-normalise each row (a row is spread over 16 consecutive lanes)
+// with the rounding of torch bf16 ops.
+__device__ __forceinline__ void load_rows4(u16x8* x, const uint16_t* base, int64_t stride, int64_t t0, int len,
+                                           int tq, int f0) {
+  const u16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 4 * tq + i;
+    x[i] = row < len ? *reinterpret_cast<const u16x8*>(base + (t0 + row) * stride + f0) : zero;
+  }
+}
+__device__ __forceinline__ void l2norm_rows4(u16x8* x) {
+  float ss[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    ss[i] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float f = bf2f(x[i][e]);
+      ss[i] += rbf(f * f);
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ss[i] += __shfl_xor(ss[i], o, kWave);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float inv = rbf(rsqrt_f(rbf(rbf(ss[i]) + 1e-6f)));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[i][e] = f2bf(bf2f(x[i][e]) * inv);
+  }
+}
+// Write 4 rows x 8 features transposed: dst[(f0+e)*ld + 4tq .. +3] = x[0..3][e] (8-byte stores).
+__device__ __forceinline__ void store_transposed4(uint16_t* dst, int ld, const u16x8* x, int tq, int f0) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    f[e] = bf2f(x[e]);
-    ss += rbf(f[e] * f[e]);
+    const u16x4 v = {x[0][e], x[1][e], x[2][e], x[3][e]};
+    *reinterpret_cast<u16x4*>(dst + (f0 + e) * ld + 4 * tq) = v;
   }
-  for (int o = xor_lo; o <= xor_hi; o <<= 1) ss += __shfl_xor(ss, o, kWave);
-  const float s = rbf(rbf(ss) + 1e-6f);
-  const float inv = rbf(rsqrt_f(s));
-#pragma unroll
-  for (int e = 0; e < 8; ++e) x[e] = f2bf(f[e] * inv);
 }
 
-template <int BV>
-__device__ __forceinline__ void commit_chunk(PrefillSmem<BV>& sm, ChunkRegs<BV>& r, bf16x8* qf, bool use_l2,
-                                             int t) {
+struct LocalSmem {
+  union {
+    uint16_t K[pf::CH * pf::LDK];   // K chunk, row-major (token, feature): A/B of K K^T, B of Q K^T
+    uint16_t W[pf::CH * pf::LDK];   // later: W staged for coalesced stores
+  } a;
+  uint16_t KT[pf::D * pf::LDT];     // K chunk transposed (feature, token): B of W = T' K
+  float X[pf::CH * pf::LDF];
+  float T[pf::CH * pf::LDF];
+  float Y[4 * 256];
+  float G[pf::CH], EG[pf::CH], B[pf::CH];
+};
+
+template <typename BetaT>
+__global__ __launch_bounds__(pf::NT, 2) void chunk_local_kernel(
+    const uint16_t* __restrict__ q, int64_t qs, const uint16_t* __restrict__ k, int64_t ks,
+    const float* __restrict__ g, const BetaT* __restrict__ beta, const int32_t* __restrict__ cu,
+    const int32_t* __restrict__ seq_chunk0, int nseq, int seq_len, int Hqk, int Hv, int use_l2,
+    uint8_t* __restrict__ work) {
   using namespace pf;
-  const int w = t >> 6, lane = t & 63;
+  __shared__ LocalSmem sm;
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  const int slot = blockIdx.x, h = blockIdx.y;
+  const int hk = h / (Hv / Hqk);
+  const ChunkPos cp = chunk_pos(slot, cu, seq_chunk0, nseq, seq_len);
+  uint8_t* rec = work + ((int64_t)slot * Hv + h) * ws::BYTES;
+
+  // K: thread (tq, fb) loads rows 4tq.. x features 8fb..; row-major and transposed copies
+  {
+    const int tq = t >> 4, fb = t & 15;
+    u16x8 x[4];
+    load_rows4(x, k + (int64_t)hk * D, ks, cp.t0, cp.len, tq, 8 * fb);
+    if (use_l2) l2norm_rows4(x);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    if (use_l2) l2norm8(r.k[i], 1, 8);  // a K row is held by 16 consecutive lanes
-    const int row = (t >> 4) + 16 * i, f0 = 8 * (t & 15);
-    *reinterpret_cast<u16x8*>(&sm.K[row * LDK + f0]) = r.k[i];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) sm.KT[(f0 + e) * LDT + row] = r.k[i][e];
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<u16x8*>(&sm.a.K[(4 * tq + i) * LDK + 8 * fb]) = x[i];
+    store_transposed4(sm.KT, LDT, x, tq, 8 * fb);
   }
-  if (use_l2) {
-    // a Q row is held by the 4 lanes l%16 == const of this wave, 4 pieces each
-    float ss = 0.f;
-    float f[4][8];
+  // Q in A-fragment order of this wave (rows 16w + l%16, features 8(l/16) + 32s)
+  bf16x8 qf[4];
+  {
+    const u16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+    const int row = 16 * w + (lane & 15);
+    u16x8 r[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s)
+      r[s] = row < cp.len ? *reinterpret_cast<const u16x8*>(q + (cp.t0 + row) * qs + (int64_t)hk * D + 32 * s +
+                                                            8 * (lane >> 4))
+                          : zero;
+    if (use_l2) {
+      float ss = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        f[s][e] = bf2f(r.q[s][e]);
-        ss += rbf(f[s][e] * f[s][e]);
-      }
-    ss += __shfl_xor(ss, 16, kWave);
-    ss += __shfl_xor(ss, 32, kWave);
-    const float inv = rbf(rsqrt_f(rbf(rbf(ss) + 1e-6f)));
+      for (int s = 0; s < 4; ++s)
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
+        for (int e = 0; e < 8; ++e) {
+          const float f = bf2f(r[s][e]);
+          ss += rbf(f * f);
+        }
+      ss += __shfl_xor(ss, 16, kWave);
+      ss += __shfl_xor(ss, 32, kWave);
+      const float inv = rbf(rsqrt_f(rbf(rbf(ss) + 1e-6f)));
 #pragma unroll
-      for (int e = 0; e < 8; ++e) r.q[s][e] = f2bf(f[s][e] * inv);
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) r[s][e] = f2bf(bf2f(r[s][e]) * inv);
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qf[s] = __builtin_bit_cast(bf16x8, r[s]);
   }
-#pragma unroll
-  for (int s = 0; s < 4; ++s) qf[s] = __builtin_bit_cast(bf16x8, r.q[s]);
-  constexpr int PPR = BV / 8;
-#pragma unroll
-  for (int i = 0; i < ChunkRegs<BV>::NV; ++i) {
-    const int idx = t + NT * i;
-    const int row = idx / PPR, pc = idx % PPR;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) sm.VT[(8 * pc + e) * LDT + row] = r.v[i][e];
-  }
-  if (w == 0) {  // cumulative decay within the chunk
-    float G = r.g;
+  if (w == 0) {  // cumulative decay within the chunk (padding: g = 0, beta = 0)
+    const bool valid = lane < cp.len;
+    float G = valid ? g[(cp.t0 + lane) * Hv + h] : 0.f;
+    const float bt = valid ? Elem<BetaT>::load(beta + (cp.t0 + lane) * Hv + h) : 0.f;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
       const float up = __shfl_up(G, o, kWave);
       if (lane >= o) G += up;
     }
     const float gl = __shfl(G, 63, kWave);
+    const float eg = expf(G), dec = expf(gl - G);
     sm.G[lane] = G;
-    sm.EG[lane] = expf(G);
-    sm.B[lane] = r.beta;
-    sm.DEC[lane] = expf(gl - G);
-    if (lane == 0) sm.GL = expf(gl);
+    sm.EG[lane] = eg;
+    sm.B[lane] = bt;
+    reinterpret_cast<float*>(rec + ws::DEC)[lane] = dec;
+    if (lane == 0) reinterpret_cast<float*>(rec + ws::GL)[0] = expf(gl);
+  }
+  __syncthreads();
+
+  // Qg = scale e^{G_t} q_t -> workspace (this wave's rows, straight from the A fragments);
+  // K^T -> workspace (from LDS)
+  {
+    const int row = 16 * w + (lane & 15);
+    const float f = kScale * sm.EG[row];
+    uint16_t* qg = reinterpret_cast<uint16_t*>(rec + ws::QG) + row * D + 8 * (lane >> 4);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const u16x8 u = __builtin_bit_cast(u16x8, qf[s]);
+      u16x8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = f2bf(bf2f(u[e]) * f);
+      *reinterpret_cast<u16x8*>(qg + 32 * s) = o;
+    }
+    uint16_t* kt = reinterpret_cast<uint16_t*>(rec + ws::KT);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = t + NT * i;  // 1024 pieces of 16 bytes: row idx/8, piece idx%8
+      *reinterpret_cast<u16x8*>(kt + (idx >> 3) * CH + 8 * (idx & 7)) =
+          *reinterpret_cast<const u16x8*>(&sm.KT[(idx >> 3) * LDT + 8 * (idx & 7)]);
+    }
+  }
+  // A = K K^T and QK = Q K^T for this wave's 16 rows; X -> LDS, QK -> workspace
+  {
+    f32x4 accA[4], accQ[4];
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) accA[cb] = accQ[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const bf16x8 ak = frag(sm.a.K, LDK, 16 * w, 32 * s, lane);
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) {
+        if (cb <= w) {
+          const bf16x8 b = frag(sm.a.K, LDK, 16 * cb, 32 * s, lane);
+          accA[cb] = mma(ak, b, accA[cb]);
+          accQ[cb] = mma(qf[s], b, accQ[cb]);
+        }
+      }
+    }
+    uint16_t* qk = reinterpret_cast<uint16_t*>(rec + ws::QK);
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = 16 * w + 4 * (lane >> 4) + r, jj = 16 * cb + (lane & 15);
+        float x = 0.f, v = 0.f;
+        if (cb <= w && i >= jj) {
+          const float dec = expf(sm.G[i] - sm.G[jj]);
+          v = kScale * accQ[cb][r] * dec;
+          if (i > jj) x = -sm.B[i] * accA[cb][r] * dec;
+        }
+        sm.X[i * LDF + jj] = x;
+        qk[i * CH + jj] = f2bf(v);
+      }
+  }
+  __syncthreads();
+
+  unit_lower_inv64(sm.X, sm.T, sm.Y, w, lane);
+
+  // Tb = T diag(beta) -> workspace (row t = 4*(thread/16)..., 16 columns per thread)
+  {
+    const int row = t >> 2, c0 = 16 * (t & 3);
+    u16x8 o[2];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[e >> 3][e & 7] = f2bf(sm.T[row * LDF + c0 + e] * sm.B[c0 + e]);
+    uint16_t* tb = reinterpret_cast<uint16_t*>(rec + ws::TB) + row * CH + c0;
+    *reinterpret_cast<u16x8*>(tb) = o[0];
+    *reinterpret_cast<u16x8*>(tb + 8) = o[1];
+  }
+  // W = T diag(beta e^G) K for this wave's rows
+  f32x4 accW[8];
+  {
+    bf16x8 tbe[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const float* trow = &sm.T[(16 * w + (lane & 15)) * LDF + 32 * s + 8 * (lane >> 4)];
+      float a[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int col = 32 * s + 8 * (lane >> 4) + e;
+        a[e] = trow[e] * sm.B[col] * sm.EG[col];
+      }
+      tbe[s] = pack8(a);
+    }
+#pragma unroll
+    for (int cb = 0; cb < 8; ++cb) {
+      accW[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 2; ++s) accW[cb] = mma(tbe[s], frag(sm.KT, LDT, 16 * cb, 32 * s, lane), accW[cb]);
+    }
+  }
+  // stage W in LDS (the K buffer is free after the K K^T products) and store it coalesced
+#pragma unroll
+  for (int cb = 0; cb < 8; ++cb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      sm.a.W[(16 * w + 4 * (lane >> 4) + r) * LDK + 16 * cb + (lane & 15)] = f2bf(accW[cb][r]);
+  __syncthreads();
+  {
+    uint16_t* wd = reinterpret_cast<uint16_t*>(rec + ws::W);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = t + NT * i;  // 1024 pieces of 16 bytes
+      const int row = idx >> 4, pc = idx & 15;
+      *reinterpret_cast<u16x8*>(wd + row * D + 8 * pc) = *reinterpret_cast<const u16x8*>(&sm.a.W[row * LDK + 8 * pc]);
+    }
   }
 }
 
-template <int BV, typename BetaT>
-__global__ __launch_bounds__(pf::NT) void chunk_prefill_kernel(
-    const uint16_t* __restrict__ q, int64_t qs, const uint16_t* __restrict__ k, int64_t ks,
-    const uint16_t* __restrict__ v, int64_t vs, const float* __restrict__ g, const BetaT* __restrict__ beta,
-    const float* __restrict__ init, float* __restrict__ final_state, uint16_t* __restrict__ out,
-    const int32_t* __restrict__ cu, int seq_len, int Hqk, int Hv, int use_l2) {
+// ============================================================================================
+// Chunked prefill, part 2: the inter-chunk state recurrence.
+// ============================================================================================
+// One workgroup = 4 waves = 64 state columns of one (sequence, value head); wave w owns columns
+// 16w..16w+15 over all 128 rows and all 64 tokens of a chunk, so the dependent chain
+//   U = Tb V,  vn = U - W S,  o = Qg S + QK vn,  S' = GL S + K^T (DEC vn)
+// never waits for another wave: the per-chunk operands shared by the 4 waves (Qg, W, Tb, QK, K^T,
+// V^T) are staged in LDS once per chunk, and the only layout changes inside the chain (S and vn
+// from accumulator layout to B-operand layout) go through wave-private LDS.
+struct StateSmem {
+  uint16_t Qg[pf::CH * pf::LDK];       // scale e^G q (token, feature)
+  uint16_t W[pf::CH * pf::LDK];        // (token, feature)
+  uint16_t Tb[pf::CH * pf::LDT];       // (token, token)
+  uint16_t QK[pf::CH * pf::LDT];       // (token, token)
+  uint16_t KT[pf::D * pf::LDT];        // (feature, token)
+  uint16_t VT[64 * pf::LDT];           // (column, token) for the workgroup's 64 columns
+  uint16_t ST[4][16 * pf::LDK];        // per wave: bf16 S^T (column, feature)
+  uint16_t VN[4][3][16 * pf::LDT];     // per wave: vn, hi(dec vn), lo(dec vn) transposed (column, token)
+  float DEC[pf::CH];
+  float GL;
+};
+
+struct StateStage {  // one chunk's inputs, prefetched into registers
+  u16x8 qg[4], kt[4], w[4], tb[2], qk[2], v[4];
+  float dec, gl;
+};
+
+__device__ __forceinline__ void state_prefetch(StateStage& st, const uint16_t* v, int64_t vs, const uint8_t* rec,
+                                               int64_t t0, int len, int h, int vcol0, int t) {
   using namespace pf;
-  constexpr int NCB = BV / 16;  // 16-wide column blocks of the tile
-  constexpr int NTILE = D / BV;
-  __shared__ PrefillSmem<BV> sm;
-  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
-  int bid = blockIdx.x;
-  const int vt = bid % NTILE;
-  bid /= NTILE;
-  const int h = bid % Hv, seq = bid / Hv;
-  const int hk = h / (Hv / Hqk);
-  const int vcol0 = vt * BV;
-  SeqInfo si;
-  if (cu) {
-    si.t0 = cu[seq];
-    si.L = cu[seq + 1] - cu[seq];
-  } else {
-    si.t0 = (int64_t)seq * seq_len;
-    si.L = seq_len;
+  const uint16_t* wr = reinterpret_cast<const uint16_t*>(rec + ws::W);
+  const uint16_t* qgr = reinterpret_cast<const uint16_t*>(rec + ws::QG);
+  const uint16_t* ktr = reinterpret_cast<const uint16_t*>(rec + ws::KT);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int idx = t + NT * i;  // 1024 pieces of 16 bytes
+    st.w[i] = *reinterpret_cast<const u16x8*>(wr + (idx >> 4) * D + 8 * (idx & 15));
+    st.qg[i] = *reinterpret_cast<const u16x8*>(qgr + (idx >> 4) * D + 8 * (idx & 15));
+    st.kt[i] = *reinterpret_cast<const u16x8*>(ktr + (idx >> 3) * CH + 8 * (idx & 7));
   }
-  const int nch = (si.L + CH - 1) / CH;
-  const int64_t sbase = ((int64_t)seq * Hv + h) * D * D + vcol0;
+  const uint16_t* tbr = reinterpret_cast<const uint16_t*>(rec + ws::TB);
+  const uint16_t* qkr = reinterpret_cast<const uint16_t*>(rec + ws::QK);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int idx = t + NT * i;  // 512 pieces of 16 bytes
+    st.tb[i] = *reinterpret_cast<const u16x8*>(tbr + (idx >> 3) * CH + 8 * (idx & 7));
+    st.qk[i] = *reinterpret_cast<const u16x8*>(qkr + (idx >> 3) * CH + 8 * (idx & 7));
+  }
+  // V: threads 0..127 -> token quad t/8, column block t%8 (8 of the workgroup's 64 columns)
+  if (t < 128) load_rows4(st.v, v + (int64_t)h * D + vcol0, vs, t0, len, t >> 3, 8 * (t & 7));
+  st.dec = reinterpret_cast<const float*>(rec + ws::DEC)[t & 63];
+  st.gl = reinterpret_cast<const float*>(rec + ws::GL)[0];
+}
 
-  // state tile: accS[rb][cb] holds S[16(2w+rb) + 4(l/16) + r][vcol0 + 16cb + l%16]
-  f32x4 accS[2][NCB];
+__device__ __forceinline__ void state_commit(StateSmem& sm, const StateStage& st, int t) {
+  using namespace pf;
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
+  for (int i = 0; i < 4; ++i) {
+    const int idx = t + NT * i;
+    *reinterpret_cast<u16x8*>(&sm.W[(idx >> 4) * LDK + 8 * (idx & 15)]) = st.w[i];
+    *reinterpret_cast<u16x8*>(&sm.Qg[(idx >> 4) * LDK + 8 * (idx & 15)]) = st.qg[i];
+    *reinterpret_cast<u16x8*>(&sm.KT[(idx >> 3) * LDT + 8 * (idx & 7)]) = st.kt[i];
+  }
 #pragma unroll
-    for (int cb = 0; cb < NCB; ++cb) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int d = 16 * (2 * w + rb) + 4 * (lane >> 4) + r;
-        accS[rb][cb][r] = init ? init[sbase + (int64_t)d * D + 16 * cb + (lane & 15)] : 0.f;
-      }
-      u16x4 pk;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) pk[r] = f2bf(accS[rb][cb][r]);
-      *reinterpret_cast<u16x4*>(&sm.ST[(16 * cb + (lane & 15)) * LDK + 16 * (2 * w + rb) + 4 * (lane >> 4)]) = pk;
-    }
+  for (int i = 0; i < 2; ++i) {
+    const int idx = t + NT * i;
+    *reinterpret_cast<u16x8*>(&sm.Tb[(idx >> 3) * LDT + 8 * (idx & 7)]) = st.tb[i];
+    *reinterpret_cast<u16x8*>(&sm.QK[(idx >> 3) * LDT + 8 * (idx & 7)]) = st.qk[i];
+  }
+  if (t < 128) store_transposed4(sm.VT, LDT, st.v, t >> 3, 8 * (t & 7));
+  if (t < 64) sm.DEC[t] = st.dec;
+  if (t == 0) sm.GL = st.gl;
+}
 
-  ChunkRegs<BV> cr;
-  if (nch > 0) load_chunk<BV, BetaT>(cr, q, qs, k, ks, v, vs, g, beta, si, 0, h, hk, Hv, vcol0, t);
-  bf16x8 qf[4];
+template <typename OutT>
+__global__ __launch_bounds__(pf::NT, 1) void chunk_state_kernel(
+    const uint16_t* __restrict__ v, int64_t vs, const float* __restrict__ init, float* __restrict__ final_state,
+    OutT* __restrict__ out, const int32_t* __restrict__ cu, const int32_t* __restrict__ seq_chunk0, int seq_len,
+    int Hv, const uint8_t* __restrict__ work) {
+  using namespace pf;
+  __shared__ StateSmem sm;
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63, g4 = lane >> 4, c16 = lane & 15;
+  const int ntile = D / 64;
+  const int vt = blockIdx.x % ntile;
+  const int h = (blockIdx.x / ntile) % Hv, seq = blockIdx.x / ntile / Hv;
+  const int vcol0 = 64 * vt, j0 = vcol0 + 16 * w;
+  int64_t s0;
+  int L, slot0;
+  if (cu) {
+    s0 = cu[seq];
+    L = cu[seq + 1] - cu[seq];
+    slot0 = seq_chunk0[seq];
+  } else {
+    s0 = (int64_t)seq * seq_len;
+    L = seq_len;
+    slot0 = seq * ((seq_len + CH - 1) / CH);
+  }
+  const int nch = (L + CH - 1) / CH;
+  const int64_t sbase = ((int64_t)seq * Hv + h) * D * D + j0;
+  uint16_t* myST = sm.ST[w];
+  uint16_t* myVN = sm.VN[w][0];
+  uint16_t* myVSH = sm.VN[w][1];
+  uint16_t* myVSL = sm.VN[w][2];
+
+  // S[:, j0..j0+15] as 8 row blocks in accumulator layout: S[rb][r] = S[16rb + 4g + r][j0 + c]
+  f32x4 S[8];
+#pragma unroll
+  for (int rb = 0; rb < 8; ++rb) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      S[rb][r] = init ? init[sbase + (int64_t)(16 * rb + 4 * g4 + r) * D + c16] : 0.f;
+    const u16x4 pk = {f2bf(S[rb][0]), f2bf(S[rb][1]), f2bf(S[rb][2]), f2bf(S[rb][3])};
+    *reinterpret_cast<u16x4*>(&myST[c16 * LDK + 16 * rb + 4 * g4]) = pk;
+  }
+
+  StateStage st;
+  const uint8_t* rec0 = work + (int64_t)slot0 * Hv * ws::BYTES + (int64_t)h * ws::BYTES;
+  if (nch > 0) state_prefetch(st, v, vs, rec0, s0, L < CH ? L : CH, h, vcol0, t);
 
   for (int c = 0; c < nch; ++c) {
-    // ---- 1. chunk inputs into LDS (l2norm, transposes, decay scan); prefetch the next chunk
-    commit_chunk<BV>(sm, cr, qf, use_l2 != 0, t);
-    __syncthreads();
-    if (c + 1 < nch) load_chunk<BV, BetaT>(cr, q, qs, k, ks, v, vs, g, beta, si, c + 1, h, hk, Hv, vcol0, t);
-
-    // ---- 2. A = K K^T and QK = Q K^T for this wave's 16 rows (blocks cb <= w)
-    {
-      f32x4 accA[4], accQ[4];
-#pragma unroll
-      for (int cb = 0; cb < 4; ++cb) accA[cb] = accQ[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const bf16x8 ak = frag(sm.K, LDK, 16 * w, 32 * s, lane);
-#pragma unroll
-        for (int cb = 0; cb < 4; ++cb) {
-          if (cb <= w) {
-            const bf16x8 b = frag(sm.K, LDK, 16 * cb, 32 * s, lane);
-            accA[cb] = mma(ak, b, accA[cb]);
-            accQ[cb] = mma(qf[s], b, accQ[cb]);
-          }
-        }
-      }
-#pragma unroll
-      for (int cb = 0; cb < 4; ++cb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int i = 16 * w + 4 * (lane >> 4) + r, jj = 16 * cb + (lane & 15);
-          float x = 0.f, qk = 0.f;
-          if (cb <= w && i >= jj) {
-            const float dec = expf(sm.G[i] - sm.G[jj]);
-            qk = kScale * accQ[cb][r] * dec;
-            if (i > jj) x = -sm.B[i] * accA[cb][r] * dec;
-          }
-          sm.u.inv.X[i * LDF + jj] = x;
-          sm.QK[i * LDT + jj] = f2bf(qk);
-        }
-    }
+    const int len = L - c * CH < CH ? L - c * CH : CH;
+    const int64_t t0 = s0 + (int64_t)c * CH;
+    state_commit(sm, st, t);
     __syncthreads();
 
-    // ---- 3. T = (I - X)^{-1}
-    unit_lower_inv64(sm.u.inv.X, sm.u.inv.T, sm.u.inv.Y, w, lane);
-
-    // ---- 4. W = T diag(beta e^G) K (64x128) and U = T diag(beta) V (64xBV) for this wave's rows
-    f32x4 accW[8], accU[NCB];
+    // U = Tb V and vn = U - W S for all 4 token blocks of the chunk.  Each phase loads all of its
+    // LDS fragments first and then issues its MFMAs (sched_barrier keeps the compiler from
+    // re-interleaving them into one-load-one-wait pairs).
+    f32x4 U[4];
+    bf16x8 fs[4];  // S^T fragments (B operand of W S and Qg S), reused by the output products
     {
-      bf16x8 tb[2], tbe[2];
+      bf16x8 ft[2][4], fv[2], fw[4][4];
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        const float* trow = &sm.u.inv.T[(16 * w + (lane & 15)) * LDF + 32 * s + 8 * (lane >> 4)];
-        float a[8], b[8];
+        fv[s] = frag(sm.VT, LDT, 16 * w, 32 * s, lane);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int col = 32 * s + 8 * (lane >> 4) + e;
-          a[e] = trow[e] * sm.B[col];
-          b[e] = a[e] * sm.EG[col];
-        }
-        tb[s] = pack8(a);
-        tbe[s] = pack8(b);
+        for (int tb = 0; tb < 4; ++tb) ft[s][tb] = frag(sm.Tb, LDT, 16 * tb, 32 * s, lane);
       }
-#pragma unroll
-      for (int cb = 0; cb < 8; ++cb) {
-        accW[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < 2; ++s) accW[cb] = mma(tbe[s], frag(sm.KT, LDT, 16 * cb, 32 * s, lane), accW[cb]);
-      }
-#pragma unroll
-      for (int cb = 0; cb < NCB; ++cb) {
-        accU[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < 2; ++s) accU[cb] = mma(tb[s], frag(sm.VT, LDT, 16 * cb, 32 * s, lane), accU[cb]);
-      }
-    }
-    __syncthreads();  // T no longer read; its space becomes W / vn
-#pragma unroll
-    for (int cb = 0; cb < 8; ++cb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        sm.u.upd.W[(16 * w + 4 * (lane >> 4) + r) * LDK + 16 * cb + (lane & 15)] = f2bf(accW[cb][r]);
-    __syncthreads();
-
-    // ---- 5. vn = U - W S (fp32 accumulators), published as bf16(vn) and dec*vn = hi + lo
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const bf16x8 a = frag_neg(sm.u.upd.W, LDK, 16 * w, 32 * s, lane);
-#pragma unroll
-      for (int cb = 0; cb < NCB; ++cb) accU[cb] = mma(a, frag(sm.ST, LDK, 16 * cb, 32 * s, lane), accU[cb]);
-    }
-    {
-      const int s0 = 16 * w + 4 * (lane >> 4);
-#pragma unroll
-      for (int cb = 0; cb < NCB; ++cb) {
-        u16x4 vo, vh, vl;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float vn = accU[cb][r];
-          const float vsc = vn * sm.DEC[s0 + r];
-          vo[r] = f2bf(vn);
-          vh[r] = f2bf(vsc);
-          vl[r] = f2bf(vsc - bf2f(vh[r]));
-        }
-        const int off = (16 * cb + (lane & 15)) * LDT + s0;
-        *reinterpret_cast<u16x4*>(&sm.u.upd.VN[off]) = vo;
-        *reinterpret_cast<u16x4*>(&sm.u.upd.VSH[off]) = vh;
-        *reinterpret_cast<u16x4*>(&sm.u.upd.VSL[off]) = vl;
-      }
-    }
-    __syncthreads();
-
-    // ---- 6. o = diag(scale e^G) Q S + QK vn for this wave's 16 rows
-    {
-      bf16x8 qg[4];
-      const float f = kScale * sm.EG[16 * w + (lane & 15)];
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const u16x8 u = __builtin_bit_cast(u16x8, qf[s]);
-        float a[8];
+        fs[s] = frag(myST, LDK, 0, 32 * s, lane);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) a[e] = bf2f(u[e]) * f;
-        qg[s] = pack8(a);
+        for (int tb = 0; tb < 4; ++tb) fw[s][tb] = frag_neg(sm.W, LDK, 16 * tb, 32 * s, lane);
       }
-      f32x4 accO[NCB];
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int cb = 0; cb < NCB; ++cb) {
-        accO[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < 4; ++s) accO[cb] = mma(qg[s], frag(sm.ST, LDK, 16 * cb, 32 * s, lane), accO[cb]);
+      for (int tb = 0; tb < 4; ++tb) {
+        U[tb] = mma(ft[0][tb], fv[0], f32x4{0.f, 0.f, 0.f, 0.f});
+        U[tb] = mma(ft[1][tb], fv[1], U[tb]);
       }
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        if (s == 0 || w >= 2) {
-          const bf16x8 a = frag(sm.QK, LDT, 16 * w, 32 * s, lane);
+      for (int s = 0; s < 4; ++s)
 #pragma unroll
-          for (int cb = 0; cb < NCB; ++cb) accO[cb] = mma(a, frag(sm.u.upd.VN, LDT, 16 * cb, 32 * s, lane), accO[cb]);
-        }
-      }
+        for (int tb = 0; tb < 4; ++tb) U[tb] = mma(fw[s][tb], fs[s], U[tb]);
+    }
+    // publish vn (bf16) and dec*vn = hi + lo, transposed (column, token), wave-private
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+      const int s0r = 16 * tb + 4 * g4;
+      u16x4 vo, vh, vl;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int row = 16 * w + 4 * (lane >> 4) + r;
-        const int tok = c * CH + row;
-        if (tok < si.L) {
-          uint16_t* op = out + ((si.t0 + tok) * Hv + h) * D + vcol0 + (lane & 15);
-#pragma unroll
-          for (int cb = 0; cb < NCB; ++cb) op[16 * cb] = f2bf(accO[cb][r]);
-        }
+        const float vn = U[tb][r];
+        const float vsc = vn * sm.DEC[s0r + r];
+        vo[r] = f2bf(vn);
+        vh[r] = f2bf(vsc);
+        vl[r] = f2bf(vsc - bf2f(vh[r]));
       }
+      *reinterpret_cast<u16x4*>(&myVN[c16 * LDT + s0r]) = vo;
+      *reinterpret_cast<u16x4*>(&myVSH[c16 * LDT + s0r]) = vh;
+      *reinterpret_cast<u16x4*>(&myVSL[c16 * LDT + s0r]) = vl;
     }
-    __syncthreads();  // all reads of the old state copy are done
+    __builtin_amdgcn_wave_barrier();
 
-    // ---- 7. S' = e^{G_last} S + K^T (dec vn), with dec vn = hi + lo
+    // o = Qg S + QK vn
+    {
+      bf16x8 fq[4][4], fk[2][4], fn[2];
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) fq[s][tb] = frag(sm.Qg, LDK, 16 * tb, 32 * s, lane);
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        fn[s] = frag(myVN, LDT, 0, 32 * s, lane);
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb)
+          if (s == 0 || tb >= 2) fk[s][tb] = frag(sm.QK, LDT, 16 * tb, 32 * s, lane);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      f32x4 O[4];
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) O[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) O[tb] = mma(fq[s][tb], fs[s], O[tb]);
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb)
+          if (s == 0 || tb >= 2) O[tb] = mma(fk[s][tb], fn[s], O[tb]);
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = 16 * tb + 4 * g4 + r;
+          if (row < len) Elem<OutT>::store(out + ((t0 + row) * Hv + h) * D + j0 + c16, O[tb][r]);
+        }
+    }
+
+    // next chunk's operands: issued here so their registers are not live during the products above
+    if (c + 1 < nch) {
+      const int len1 = L - (c + 1) * CH < CH ? L - (c + 1) * CH : CH;
+      state_prefetch(st, v, vs, rec0 + (int64_t)(c + 1) * Hv * ws::BYTES, t0 + CH, len1, h, vcol0, t);
+    }
+    // S' = GL S + K^T (hi + lo), then its bf16 transpose for the next chunk
     {
       const float gl = sm.GL;
+      bf16x8 fa[8][2], fh[2], fl[2];
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
+      for (int s = 0; s < 2; ++s) {
+        fh[s] = frag(myVSH, LDT, 0, 32 * s, lane);
+        fl[s] = frag(myVSL, LDT, 0, 32 * s, lane);
 #pragma unroll
-        for (int cb = 0; cb < NCB; ++cb) accS[rb][cb] *= gl;
+        for (int rb = 0; rb < 8; ++rb) fa[rb][s] = frag(sm.KT, LDT, 16 * rb, 32 * s, lane);
+      }
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          const bf16x8 a = frag(sm.KT, LDT, 16 * (2 * w + rb), 32 * s, lane);
+      for (int rb = 0; rb < 8; ++rb) {
+        S[rb] *= gl;
+        S[rb] = mma(fa[rb][0], fh[0], S[rb]);
+        S[rb] = mma(fa[rb][0], fl[0], S[rb]);
+        S[rb] = mma(fa[rb][1], fh[1], S[rb]);
+        S[rb] = mma(fa[rb][1], fl[1], S[rb]);
+      }
+      __builtin_amdgcn_wave_barrier();
 #pragma unroll
-          for (int cb = 0; cb < NCB; ++cb) {
-            accS[rb][cb] = mma(a, frag(sm.u.upd.VSH, LDT, 16 * cb, 32 * s, lane), accS[rb][cb]);
-            accS[rb][cb] = mma(a, frag(sm.u.upd.VSL, LDT, 16 * cb, 32 * s, lane), accS[rb][cb]);
-          }
-        }
-#pragma unroll
-        for (int cb = 0; cb < NCB; ++cb) {
-          u16x4 pk;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) pk[r] = f2bf(accS[rb][cb][r]);
-          *reinterpret_cast<u16x4*>(&sm.ST[(16 * cb + (lane & 15)) * LDK + 16 * (2 * w + rb) + 4 * (lane >> 4)]) = pk;
-        }
+      for (int rb = 0; rb < 8; ++rb) {
+        const u16x4 pk = {f2bf(S[rb][0]), f2bf(S[rb][1]), f2bf(S[rb][2]), f2bf(S[rb][3])};
+        *reinterpret_cast<u16x4*>(&myST[c16 * LDK + 16 * rb + 4 * g4]) = pk;
       }
     }
-    __syncthreads();
+    __syncthreads();  // shared chunk operands are overwritten by the next commit
   }
 
   if (final_state) {
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+    for (int rb = 0; rb < 8; ++rb)
 #pragma unroll
-      for (int cb = 0; cb < NCB; ++cb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int d = 16 * (2 * w + rb) + 4 * (lane >> 4) + r;
-          final_state[sbase + (int64_t)d * D + 16 * cb + (lane & 15)] = accS[rb][cb][r];
-        }
+      for (int r = 0; r < 4; ++r) final_state[sbase + (int64_t)(16 * rb + 4 * g4 + r) * D + c16] = S[rb][r];
   }
 }
 
@@ -657,43 +814,55 @@ extern "C" int gdn_unit_lower_inv(const float* X, float* T, int64_t batch, int n
   return check_launch("gdn_unit_lower_inv");
 }
 
+extern "C" int64_t gdn_chunk_prefill_workspace_bytes(int64_t total_chunks, int Hv) {
+  return total_chunks * (int64_t)Hv * ws::BYTES;
+}
+
 extern "C" int gdn_chunk_prefill(const void* q, int64_t q_stride, const void* k, int64_t k_stride,
                                  const void* v, int64_t v_stride, const float* g, const void* beta,
                                  int beta_dtype, const float* initial_state, float* final_state, void* out,
-                                 int64_t total_tokens, const int32_t* cu_seqlens, int nseq, int seq_len,
-                                 int Hqk, int Hv, int D, int in_dtype, int use_qk_l2norm, void* stream) {
+                                 int64_t total_tokens, const int32_t* cu_seqlens, const int32_t* seq_chunk0,
+                                 int64_t total_chunks, int nseq, int seq_len, int Hqk, int Hv, int D, int in_dtype,
+                                 int use_qk_l2norm, void* workspace, int64_t workspace_bytes, void* stream) {
   clear_error();
   GDN_REQUIRE(q && k && v && g && beta && out, "gdn_chunk_prefill: null input/output pointer");
   GDN_SUPPORT(D == pf::D, "gdn_chunk_prefill: head dim %d unsupported (needs %d)", D, pf::D);
   GDN_SUPPORT(in_dtype == GDN_BF16, "gdn_chunk_prefill: q/k/v must be bfloat16 (MFMA operands)");
   GDN_REQUIRE(beta_dtype == GDN_F32 || beta_dtype == GDN_BF16, "gdn_chunk_prefill: bad beta dtype");
   GDN_REQUIRE(Hqk > 0 && Hv > 0 && Hv % Hqk == 0, "gdn_chunk_prefill: bad heads Hqk=%d Hv=%d", Hqk, Hv);
-  GDN_REQUIRE(nseq >= 0 && total_tokens >= 0, "gdn_chunk_prefill: negative sizes");
-  GDN_REQUIRE(cu_seqlens || (int64_t)nseq * seq_len == total_tokens,
-              "gdn_chunk_prefill: nseq*seq_len != total_tokens without cu_seqlens");
+  GDN_REQUIRE(nseq >= 0 && total_tokens >= 0 && total_chunks >= 0, "gdn_chunk_prefill: negative sizes");
+  GDN_REQUIRE(cu_seqlens ? seq_chunk0 != nullptr : (int64_t)nseq * seq_len == total_tokens,
+              "gdn_chunk_prefill: cu_seqlens needs seq_chunk0; without it nseq*seq_len must be total_tokens");
+  GDN_REQUIRE(cu_seqlens || total_chunks == (int64_t)nseq * ((seq_len + pf::CH - 1) / pf::CH),
+              "gdn_chunk_prefill: total_chunks inconsistent with nseq/seq_len");
   GDN_REQUIRE(aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && q_stride % 8 == 0 && k_stride % 8 == 0 &&
                   v_stride % 8 == 0,
               "gdn_chunk_prefill: q/k/v rows must be 16-byte aligned");
+  GDN_REQUIRE(total_chunks == 0 || (workspace && aligned(workspace, 256) &&
+                                    workspace_bytes >= gdn_chunk_prefill_workspace_bytes(total_chunks, Hv)),
+              "gdn_chunk_prefill: workspace missing, misaligned or smaller than %lld bytes",
+              (long long)gdn_chunk_prefill_workspace_bytes(total_chunks, Hv));
+  GDN_REQUIRE(total_chunks < (1ll << 31) && (int64_t)nseq * Hv * 2 < (1ll << 31), "gdn_chunk_prefill: grid too large");
   if (nseq == 0) return GDN_OK;
   hipStream_t s = (hipStream_t)stream;
-  // Column tile: enough workgroups to cover the chip when there are few (sequence, head) pairs.
-  const int64_t pairs = (int64_t)nseq * Hv;
-  const int BV = pairs >= 256 ? 64 : 32;
-  const int64_t grid = pairs * (pf::D / BV);
-  GDN_REQUIRE(grid < (1ll << 31), "gdn_chunk_prefill: grid too large");
-#define GDN_CP_LAUNCH(BVV, BT)                                                                           \
-  chunk_prefill_kernel<BVV, BT><<<(unsigned)grid, pf::NT, 0, s>>>(                                       \
-      (const uint16_t*)q, q_stride, (const uint16_t*)k, k_stride, (const uint16_t*)v, v_stride, g,       \
-      (const BT*)beta, initial_state, final_state, (uint16_t*)out, cu_seqlens, seq_len, Hqk, Hv, use_qk_l2norm)
-  if (BV == 64) {
-    if (beta_dtype == GDN_BF16) GDN_CP_LAUNCH(64, uint16_t);
-    else GDN_CP_LAUNCH(64, float);
-  } else {
-    if (beta_dtype == GDN_BF16) GDN_CP_LAUNCH(32, uint16_t);
-    else GDN_CP_LAUNCH(32, float);
+  uint8_t* work = (uint8_t*)workspace;
+  if (total_chunks > 0) {
+    dim3 g1((unsigned)total_chunks, (unsigned)Hv);
+    if (beta_dtype == GDN_BF16)
+      chunk_local_kernel<uint16_t><<<g1, pf::NT, 0, s>>>((const uint16_t*)q, q_stride, (const uint16_t*)k, k_stride,
+                                                         g, (const uint16_t*)beta, cu_seqlens, seq_chunk0, nseq,
+                                                         seq_len, Hqk, Hv, use_qk_l2norm, work);
+    else
+      chunk_local_kernel<float><<<g1, pf::NT, 0, s>>>((const uint16_t*)q, q_stride, (const uint16_t*)k, k_stride,
+                                                      g, (const float*)beta, cu_seqlens, seq_chunk0, nseq, seq_len,
+                                                      Hqk, Hv, use_qk_l2norm, work);
+    int rc = check_launch("gdn_chunk_prefill(local)");
+    if (rc) return rc;
   }
-#undef GDN_CP_LAUNCH
-  return check_launch("gdn_chunk_prefill");
+  chunk_state_kernel<uint16_t><<<(unsigned)(nseq * Hv * (pf::D / 64)), pf::NT, 0, s>>>(
+      (const uint16_t*)v, v_stride, initial_state, final_state, (uint16_t*)out, cu_seqlens, seq_chunk0, seq_len, Hv,
+      work);
+  return check_launch("gdn_chunk_prefill(state)");
 }
 
 extern "C" int gdn_conv_prefill(const void* x, int64_t x_stride, const void* weight, const void* bias,

@@ -29,19 +29,38 @@ def _tokens_view(x, name):
     return flat, x.stride(1)
 
 
-def _seq_args(B, T, cu_seqlens, device):
-    """(device int32 cu_seqlens | None, n_seq, per-sequence length for the uniform case).
-    cu_seqlens is checked on the host (the kernels index memory with it): 1-D, starts at 0,
+def _check_cu(cu_seqlens, B, T):
+    """cu_seqlens on the host, checked (the kernels index memory with it): 1-D, starts at 0,
     non-decreasing, ends at the packed token count."""
-    if cu_seqlens is None:
-        return None, B, T
     if B != 1:
         raise ValueError("cu_seqlens needs packed inputs with batch size 1")
     host = cu_seqlens.detach().to("cpu", torch.int64).reshape(-1)
     if host.numel() < 2 or int(host[0]) != 0 or int(host[-1]) != T or bool((host[1:] < host[:-1]).any()):
         raise ValueError(f"cu_seqlens must be non-decreasing from 0 to {T}, got {host.tolist()[:8]}...")
+    return host
+
+
+def _seq_args(B, T, cu_seqlens, device):
+    """(device int32 cu_seqlens | None, n_seq, per-sequence length for the uniform case)."""
+    if cu_seqlens is None:
+        return None, B, T
+    host = _check_cu(cu_seqlens, B, T)
     cu = cu_seqlens.to(device=device, dtype=torch.int32).contiguous()
     return cu, host.numel() - 1, 0
+
+
+def _chunk_table(B, T, cu_seqlens, device):
+    """(device cu_seqlens | None, device seq_chunk0 | None, n_seq, seq_len, total_chunks):
+    seq_chunk0[s] = number of 64-token chunks of the sequences before s (the workspace slot of the
+    first chunk of sequence s)."""
+    if cu_seqlens is None:
+        return None, None, B, T, B * ((T + CHUNK - 1) // CHUNK)
+    host = _check_cu(cu_seqlens, B, T)
+    nch = (host[1:] - host[:-1] + CHUNK - 1) // CHUNK
+    s0 = torch.zeros(host.numel(), dtype=torch.int64)
+    s0[1:] = torch.cumsum(nch, 0)
+    cu = cu_seqlens.to(device=device, dtype=torch.int32).contiguous()
+    return cu, s0.to(device=device, dtype=torch.int32), host.numel() - 1, 0, int(s0[-1])
 
 
 def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size=64, initial_state=None,
@@ -64,7 +83,7 @@ def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size=64, initial_st
     if tuple(g.shape) != (B, T, Hv) or tuple(beta.shape) != (B, T, Hv):
         raise ValueError("chunk_gated_delta_rule: g and beta must be [B, T, Hv]")
     dev = query.device
-    cu, nseq, seq_len = _seq_args(B, T, cu_seqlens, dev)
+    cu, seq_chunk0, nseq, seq_len, total_chunks = _chunk_table(B, T, cu_seqlens, dev)
     q, qs = _tokens_view(query, "query")
     k, ks = _tokens_view(key, "key")
     v, vs = _tokens_view(value, "value")
@@ -79,10 +98,13 @@ def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size=64, initial_st
         init = initial_state.to(torch.float32).contiguous()
     final = torch.empty(nseq, Hv, D, D, dtype=torch.float32, device=dev) if output_final_state else None
     out = torch.empty(B, T, Hv, D, dtype=query.dtype, device=dev)
+    wbytes = int(_lib.lib().gdn_chunk_prefill_workspace_bytes(total_chunks, Hv))
+    work = torch.empty(max(wbytes, 1), dtype=torch.uint8, device=dev)
     _lib.call("gdn_chunk_prefill", _lib.ptr(q), qs, _lib.ptr(k), ks, _lib.ptr(v), vs, _lib.ptr(g32),
               _lib.ptr(beta), _lib.dtype_code(beta), _lib.ptr(init), _lib.ptr(final), _lib.ptr(out),
-              B * T, _lib.ptr(cu), nseq, seq_len, Hqk, Hv, D, _lib.dtype_code(query),
-              int(bool(use_qk_l2norm_in_kernel)), _lib.stream_of(query))
+              B * T, _lib.ptr(cu), _lib.ptr(seq_chunk0), total_chunks, nseq, seq_len, Hqk, Hv, D,
+              _lib.dtype_code(query), int(bool(use_qk_l2norm_in_kernel)), _lib.ptr(work), wbytes,
+              _lib.stream_of(query))
     return out, final
 
 
