@@ -100,6 +100,65 @@ int gdn_decode_fused(const void* mixed, int64_t mixed_stride, const void* z, int
                      float* rec_state, void* out, int N, int Hk, int Hv, int D, int K,
                      void* stream);
 
+/*
+ * (I - X)^{-1} for a batch of strictly lower-triangular 64x64 fp32 matrices (only the strictly
+ * lower part of X is read).  The intra-chunk inverse of the chunked rule.
+ * Replaces _unit_lower_inv / _small_unit_lower_inv (src/gdn_chunk_fast.py:21-62).
+ *   X, T [batch, 64, 64] fp32;  n must be 64.
+ */
+int gdn_unit_lower_inv(const float* X, float* T, int64_t batch, int n, void* stream);
+
+/* Bytes of device workspace gdn_chunk_prefill needs for `total_chunks` 64-token chunks. */
+int64_t gdn_chunk_prefill_workspace_bytes(int64_t total_chunks, int Hv);
+
+/*
+ * Chunked gated delta rule prefill (chunk 64, fp32 state), optionally over packed sequences.
+ * Replaces fast_chunk_gated_delta_rule_v2 (src/gdn_chunk_fast2.py:11-62) and
+ * fast_chunk_gated_delta_rule (src/gdn_chunk_fast.py:65-142), both with HF's signature
+ * torch_chunk_gated_delta_rule (HF:249-260).
+ *   q, k [total_tokens, Hqk, D] bf16, token stride q_stride / k_stride (value head h reads key
+ *        head h / (Hv / Hqk));  v [total_tokens, Hv, D] bf16, token stride v_stride
+ *   g [total_tokens, Hv] fp32 (log decay);  beta [total_tokens, Hv] (beta_dtype)
+ *   initial_state / final_state [nseq, Hv, D, D] fp32, either may be NULL (zero / not written)
+ *   out [total_tokens, Hv, D] bf16 (dense)
+ *   cu_seqlens: device int32 [nseq+1] (packed varlen) with seq_chunk0: device int32 [nseq+1],
+ *     seq_chunk0[s] = sum over earlier sequences of ceil(len/64); or both NULL for nseq
+ *     sequences of seq_len tokens.  total_chunks = sum of ceil(len/64) over sequences.
+ *   workspace: device memory of gdn_chunk_prefill_workspace_bytes(total_chunks, Hv) bytes,
+ *     256-byte aligned (caller-owned; contents are scratch).
+ */
+int gdn_chunk_prefill(const void* q, int64_t q_stride, const void* k, int64_t k_stride,
+                      const void* v, int64_t v_stride, const float* g, const void* beta,
+                      int beta_dtype, const float* initial_state, float* final_state, void* out,
+                      int64_t total_tokens, const int32_t* cu_seqlens, const int32_t* seq_chunk0,
+                      int64_t total_chunks, int nseq, int seq_len, int Hqk, int Hv, int D,
+                      int in_dtype, int use_qk_l2norm, void* workspace, int64_t workspace_bytes,
+                      void* stream);
+
+/*
+ * Depthwise causal conv prefill + SiLU over packed prompts, and the decode conv state they leave
+ * (the last K inputs, left zero-padded).  Replaces the conv of TPEngine.prefill /
+ * TPEngine.prefill_chunk (src/cb_tp.py:158-164, :236-244, :260) and HF causal_conv1d_fn with the
+ * cache conv-state capture (HF:220-239).
+ *   x [total_tokens, C] bf16 (token-major, row stride x_stride); weight [C, K] bf16; bias [C] or NULL
+ *   history [nseq, C, K] bf16 (the previous K inputs of each sequence) or NULL (zero history)
+ *   out [total_tokens, C] bf16 (dense);  state_out [nseq, C, K] bf16 or NULL
+ *   cu_seqlens device int32 [nseq+1] or NULL (nseq sequences of seq_len tokens)
+ */
+int gdn_conv_prefill(const void* x, int64_t x_stride, const void* weight, const void* bias,
+                     const void* history, void* out, void* state_out, int64_t total_tokens,
+                     const int32_t* cu_seqlens, int nseq, int seq_len, int C, int K, void* stream);
+
+/*
+ * GDN gating: beta = sigmoid(b) (bf16), g = -exp(A_log) * softplus(a + dt_bias) (fp32).
+ * Replaces src/cb_engine.py:337-338 (HF:497-498).
+ *   a, b [rows, Hv] bf16 (row stride ab_stride); A_log, dt_bias [Hv] fp32;
+ *   beta_out [rows, Hv] bf16; g_out [rows, Hv] fp32 (dense).
+ */
+int gdn_gating(const void* a, const void* b, int64_t ab_stride, const float* A_log,
+               const float* dt_bias, void* beta_out, float* g_out, int64_t rows, int Hv,
+               void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,60 @@
+"""CPU checks of the C-ABI library: it loads, exports every entry point include/gdn_mi355x.h
+declares, and rejects bad arguments with an error code and message before touching a GPU."""
+import ctypes
+import importlib
+import os
+import re
+
+import pytest
+
+from conftest import PKG_NAME, ROOT
+
+HEADER = os.path.join(ROOT, "include", "gdn_mi355x.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z0-9_]+\*?\s+\*?(gdn_[a-z0-9_]+)\s*\(", text, re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return importlib.import_module(PKG_NAME + "._lib")
+
+
+def test_header_declares_entry_points():
+    syms = declared_symbols()
+    for name in ("gdn_recurrent_step", "gdn_conv_update", "gdn_gated_rmsnorm", "gdn_decode_fused",
+                 "gdn_chunk_prefill", "gdn_conv_prefill", "gdn_gating", "gdn_unit_lower_inv"):
+        assert name in syms
+
+
+def test_library_exports_every_declared_symbol(lib):
+    handle = lib.lib()
+    missing = [s for s in declared_symbols() if getattr(handle, s, None) is None]
+    assert not missing, f"declared but not exported: {missing}"
+    bound = set(lib.exported_symbols())
+    assert set(declared_symbols()) <= bound, "every declared entry point has a ctypes signature"
+
+
+def test_version_limits_and_error_path(lib):
+    h = lib.lib()
+    assert h.gdn_version() >= 100
+    d, r, k = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    assert h.gdn_limits(ctypes.byref(d), ctypes.byref(r), ctypes.byref(k)) == 0
+    assert d.value == 128 and r.value >= 3 and k.value >= 4
+    # argument validation runs on the host, before any HIP call
+    rc = h.gdn_recurrent_step(None, 0, None, 0, None, 0, None, None, 1, None, None, None,
+                              1, 1, 1, 128, 1, 1, None)
+    assert rc == 1 and b"null" in h.gdn_last_error()
+    rc = h.gdn_conv_update(ctypes.c_void_p(16), 0, ctypes.c_void_p(16), ctypes.c_void_p(16), None,
+                           ctypes.c_void_p(16), 0, 1, 8, 9, None)
+    assert rc == 2 and b"kernel size" in h.gdn_last_error()
+    p = ctypes.c_void_p(256)
+    rc = h.gdn_decode_fused(p, 0, p, 0, p, p, 0, p, p, None, p, p, p, 1, ctypes.c_float(1e-6), p, p,
+                            1, 16, 32, 64, 4, None)
+    assert rc == 2 and b"head dim" in h.gdn_last_error()
+    need = h.gdn_chunk_prefill_workspace_bytes(10, 32)
+    assert need > 0 and need % 256 == 0
+    with pytest.raises(lib.GDNError):
+        lib.call("gdn_gated_rmsnorm", None, 0, None, 0, None, 1, None, 1, 128, ctypes.c_float(1e-6), None)

@@ -1,0 +1,56 @@
+"""CPU checks of the host API: the reference-named functions validate their inputs and refuse CPU
+tensors (there is no CPU fallback) before any GPU call."""
+import pytest
+import torch
+
+
+def test_public_names(gdn):
+    for name in ("fast_chunk_gated_delta_rule", "fast_chunk_gated_delta_rule_v2", "recurrent_single_step",
+                 "elem_conv_update", "patch_model", "gated_rmsnorm", "gdn_decode_core", "gdn_prefill_core",
+                 "causal_conv1d_prefill", "causal_conv1d_update", "GDNSlots", "GDNDecodeGraph"):
+        assert hasattr(gdn, name)
+
+
+def test_cpu_tensors_are_refused(gdn):
+    q = torch.zeros(1, 4, 2, 128, dtype=torch.bfloat16)
+    g = torch.zeros(1, 4, 2)
+    with pytest.raises(ValueError, match="no CPU fallback"):
+        gdn.fast_chunk_gated_delta_rule_v2(q, q, q, g, g)
+    with pytest.raises(ValueError, match="no CPU fallback"):
+        gdn.recurrent_single_step(q[:, :1], q[:, :1], q[:, :1], g[:, :1], g[:, :1], None, True)
+    x = torch.zeros(2, 16, 1, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="no CPU fallback"):
+        gdn.elem_conv_update(x, torch.zeros(2, 16, 4, dtype=torch.bfloat16),
+                             torch.zeros(16, 4, dtype=torch.bfloat16), None)
+
+
+def test_cu_seqlens_validation(gdn):
+    from importlib import import_module
+    cf = import_module(gdn.__name__ + ".gdn_chunk_fast")
+    cu, s0, nseq, _, total = cf._chunk_table(1, 200, torch.tensor([0, 64, 64, 130, 200]), "cpu")
+    assert nseq == 4 and total == 1 + 0 + 2 + 2 and s0.tolist() == [0, 1, 1, 3, 5]
+    for bad in ([0, 50, 40, 200], [1, 200], [0, 100], [0]):
+        with pytest.raises(ValueError):
+            cf._chunk_table(1, 200, torch.tensor(bad), "cpu")
+    with pytest.raises(ValueError):
+        cf._chunk_table(2, 100, torch.tensor([0, 100]), "cpu")
+
+
+def test_patch_model_installs_functions(gdn):
+    from transformers.models.qwen3_5 import modeling_qwen3_5 as M
+    from transformers.models.qwen3_5.configuration_qwen3_5 import Qwen3_5TextConfig
+    saved = (M.torch_chunk_gated_delta_rule, M.torch_recurrent_gated_delta_rule, M.causal_conv1d_update)
+    try:
+        cfg = Qwen3_5TextConfig(hidden_size=64, linear_num_key_heads=1, linear_num_value_heads=2,
+                                linear_key_head_dim=128, linear_value_head_dim=128, num_hidden_layers=1,
+                                layer_types=["linear_attention"], intermediate_size=64, num_attention_heads=2,
+                                num_key_value_heads=1, head_dim=64, vocab_size=32)
+        layer = M.Qwen3_5GatedDeltaNet(cfg, 0)
+        holder = torch.nn.ModuleList([layer])
+        gdn.patch_model(holder, fast_gdn=True, gdn_v2=True)
+        assert layer.chunk_gated_delta_rule is gdn.fast_chunk_gated_delta_rule_v2
+        assert layer.recurrent_gated_delta_rule is gdn.recurrent_single_step
+        assert M.torch_chunk_gated_delta_rule is gdn.fast_chunk_gated_delta_rule_v2
+        assert layer.norm.forward.__func__ is gdn.fused_gated_rmsnorm
+    finally:
+        M.torch_chunk_gated_delta_rule, M.torch_recurrent_gated_delta_rule, M.causal_conv1d_update = saved
