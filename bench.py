@@ -102,41 +102,120 @@ def bench_decode(gdn, dev, steps, warmup):
 
 
 def prefill_flops(T, hv=HV, d=D, chunk=64):
+    """Algorithmic flops of the chunked rule: 10*C*d + 6*d^2 per token per value head (the eight
+    contractions of one chunk; inverse and elementwise work excluded)."""
     return T * hv * (10 * chunk * d + 6 * d * d)
 
 
 def prefill_bytes(T, nseq=1, hk=HK, hv=HV, d=D):
+    """Core kernel HBM bytes: q, k (unrepeated) + v in, out, g fp32 + beta bf16, initial + final state."""
     per_tok = 2 * (2 * hk * d) + 2 * hv * d + 6 * hv + 2 * hv * d
     return T * per_tok + nseq * 2 * hv * d * d * 4
 
 
-def bench_prefill(gdn, dev, T=8192, reps=5, seed=0):
+def prefill_layer_bytes(T, nseq, hv=HV, d=D, c=C, k=KC):
+    """Fused layer bytes: mixed_qkv in (C channels) + z + a, b + normed out, states, conv states."""
+    per_tok = 2 * c + 2 * hv * d + 4 * hv + 2 * hv * d
+    return T * per_tok + nseq * (2 * hv * d * d * 4 + c * k * 2)
+
+
+def _time(fn, reps, dev):
+    fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1000.0 / reps
+
+
+def _gdn_inputs(T, seed, dev, nseq=1):
     g_ = torch.Generator(device="cpu").manual_seed(seed)
     q = torch.randn(1, T, HK, D, generator=g_).to(torch.bfloat16).to(dev)
     k = torch.randn(1, T, HK, D, generator=g_).to(torch.bfloat16).to(dev)
     v = torch.randn(1, T, HV, D, generator=g_).to(torch.bfloat16).to(dev)
     beta = torch.sigmoid(torch.randn(1, T, HV, generator=g_)).to(torch.bfloat16).to(dev)
     g = (-torch.nn.functional.softplus(torch.randn(1, T, HV, generator=g_) + 2) * 0.1).to(dev)
-    s0 = (0.02 * torch.randn(1, HV, D, D, generator=g_)).to(dev)
+    s0 = (0.02 * torch.randn(nseq, HV, D, D, generator=g_)).to(dev)
+    return q, k, v, g, beta, s0
 
-    def run():
-        return gdn.fast_chunk_gated_delta_rule_v2(q, k, v, g, beta, initial_state=s0, output_final_state=True,
-                                                  use_qk_l2norm_in_kernel=True)
-    run()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream(dev)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(reps):
-        run()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1000.0 / reps
-    F = prefill_flops(T)
-    B = prefill_bytes(T)
-    return dict(workload=f"prefill B=1 T={T} H_k={HK} H_v={HV} d={D} bf16", us_per_layer=us,
-                tokens_per_s_per_layer=T / (us * 1e-6), mfma_frac=F / (us * 1e-6) / BF16_PEAK,
-                hbm_frac=B / (us * 1e-6) / HBM_PEAK, flops=F, bytes=B)
+
+def _fractions(name, us, F, B, tokens):
+    return dict(workload=name, us_per_layer=round(us, 2), tokens_per_s_per_layer=round(tokens / (us * 1e-6)),
+                mfma_frac=round(F / (us * 1e-6) / BF16_PEAK, 4), hbm_frac=round(B / (us * 1e-6) / HBM_PEAK, 4),
+                flops=F, bytes=B)
+
+
+def bench_prefill(gdn, dev, T=8192, reps=5, seed=0):
+    """Chunked rule alone, B=1, T tokens, H_k=16 key heads read by H_v=32 value heads."""
+    q, k, v, g, beta, s0 = _gdn_inputs(T, seed, dev)
+    us = _time(lambda: gdn.fast_chunk_gated_delta_rule_v2(q, k, v, g, beta, initial_state=s0, output_final_state=True,
+                                                          use_qk_l2norm_in_kernel=True), reps, dev)
+    return _fractions(f"chunked rule B=1 T={T} H_k={HK} H_v={HV} d={D} bf16", us, prefill_flops(T), prefill_bytes(T), T)
+
+
+def bench_prefill_varlen(gdn, dev, reps=5, seed=2):
+    """Fused prefill layer (conv1d prefill + SiLU, l2norm, gating, chunked rule, gated RMSNorm) over
+    16 packed prompts with lengths uniform in [200, 1500], random initial states, zero conv history."""
+    g_ = torch.Generator(device="cpu").manual_seed(seed)
+    lens = torch.randint(200, 1501, (16,), generator=g_)
+    cu = torch.zeros(17, dtype=torch.int32)
+    cu[1:] = torch.cumsum(lens, 0)
+    T = int(cu[-1])
+    mixed = torch.randn(T, C, generator=g_).to(torch.bfloat16).to(dev)
+    z = torch.randn(T, HV * D, generator=g_).to(torch.bfloat16).to(dev)
+    a = torch.randn(T, HV, generator=g_).to(torch.bfloat16).to(dev)
+    b = torch.randn(T, HV, generator=g_).to(torch.bfloat16).to(dev)
+    cw = (0.5 * torch.randn(C, KC, generator=g_)).to(torch.bfloat16).to(dev)
+    A_log = torch.full((HV,), -2.302585092994046, device=dev)
+    dt = torch.full((HV,), 2.0, device=dev)
+    nw = (1 + 0.02 * torch.randn(D, generator=g_)).to(torch.bfloat16).to(dev)
+    s0 = (0.02 * torch.randn(16, HV, D, D, generator=g_)).to(dev)
+    cud = cu.to(dev)
+    us = _time(lambda: gdn.gdn_prefill_core(mixed, z, a, b, cw, A_log, dt, nw, HK, HV, D, cu_seqlens=cud,
+                                            initial_state=s0), reps, dev)
+    return _fractions(f"fused prefill layer, 16 packed prompts ({T} tokens), H_k={HK} H_v={HV} d={D}", us,
+                      prefill_flops(T), prefill_layer_bytes(T, 16), T)
+
+
+def bench_prefill_long(gdn, dev, T=32768, seed=3, check=True):
+    """B=1, T=32768: per-layer time and the final-state rel-L2 against the CPU oracle."""
+    q, k, v, g, beta, s0 = _gdn_inputs(T, seed, dev)
+    run = lambda: gdn.fast_chunk_gated_delta_rule_v2(q, k, v, g, beta, initial_state=s0, output_final_state=True,
+                                                     use_qk_l2norm_in_kernel=True)
+    us = _time(run, 2, dev)
+    res = _fractions(f"chunked rule B=1 T={T} H_k={HK} H_v={HV} d={D} bf16", us, prefill_flops(T),
+                     prefill_bytes(T), T)
+    if check:
+        oracle = importlib.import_module("oracle.gdn_oracle")
+        torch.set_num_threads(len(os.sched_getaffinity(0)))
+        o, s = run()
+        r = HV // HK
+        oc = lambda x: x.cpu().repeat_interleave(r, dim=2)
+        o_ref, s_ref = oracle.chunk_gated_delta_rule_v2(oc(q), oc(k), v.cpu(), g.cpu(), beta.cpu(), 64, s0.cpu(),
+                                                        True, True)
+        rel = lambda x, y: ((x.double().cpu() - y.double()).norm() / y.double().norm()).item()
+        res["out_rel_l2_vs_oracle"] = rel(o, o_ref)
+        res["state_rel_l2_vs_oracle"] = rel(s, s_ref)
+    return res
+
+
+def cpu_baseline_prefill(T=8192, seed=0):
+    """The oracle's chunked rule (torch CPU restatement of src/gdn_chunk_fast2.py) at T=8192."""
+    oracle = importlib.import_module("oracle.gdn_oracle")
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    q, k, v, g, beta, s0 = _gdn_inputs(T, seed, "cpu")
+    r = HV // HK
+    q, k = q.repeat_interleave(r, 2), k.repeat_interleave(r, 2)
+    t0 = time.perf_counter()
+    oracle.chunk_gated_delta_rule_v2(q, k, v, g, beta, 64, s0, True, True)
+    dt = time.perf_counter() - t0
+    return dict(value=round(T / dt), unit="tokens/s/layer", us_per_layer=round(dt * 1e6), cores=threads,
+                kind="port", sample=f"oracle chunk_gated_delta_rule_v2, B=1 T={T} H_v={HV} d={D}, one timed pass")
 
 
 def cpu_baseline_decode(layers_cpu=LAYERS, reps=3):
@@ -206,12 +285,12 @@ def main():
     if args.only in (None, "decode"):
         res["decode"] = bench_decode(gdn, dev, args.steps, args.warmup)
     if args.only in (None, "prefill") and not args.no_prefill:
-        try:
-            res["prefill"] = bench_prefill(gdn, dev)
-        except Exception as e:  # prefill kernel absent in this build
-            res["prefill"] = {"error": str(e)[:200]}
+        res["prefill"] = [bench_prefill(gdn, dev), bench_prefill_varlen(gdn, dev),
+                          bench_prefill_long(gdn, dev, check=not args.no_cpu)]
+        if not args.no_cpu:
+            res["prefill"][0]["cpu_baseline"] = cpu_baseline_prefill()
     if args.only == "prefill":
-        print(json.dumps(res["prefill"]))
+        print(json.dumps({"secondary": res["prefill"]}))
         return
     dec = res["decode"]
     bpl = decode_bytes_per_layer()

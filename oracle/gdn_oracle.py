@@ -1,6 +1,6 @@
 """CPU oracle for the Gated DeltaNet (GDN) hot path -- TEST INFRASTRUCTURE ONLY.
 
-This module is the checker, never the product: only ``tests/``, ``__graft_entry__.smoke()`` and the
+This module is the reference restatement used for verification, never the product: only ``tests/``, ``__graft_entry__.smoke()`` and the
 ``cpu_baseline`` leg of ``bench.py`` may import it.  The shipped package never imports it and has no
 CPU fallback; it fails loudly when its HIP library is missing.
 
