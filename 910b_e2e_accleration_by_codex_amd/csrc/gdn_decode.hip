@@ -252,6 +252,40 @@ __device__ __forceinline__ void gated_norm_row(const float* x, const uint16_t* g
   }
 }
 
+// D = 128 with 16-byte aligned rows: 16 lanes per row, 8 elements per lane, 16 rows per workgroup.
+template <bool kWBf16>
+__global__ __launch_bounds__(256) void gated_rmsnorm128_kernel(const uint16_t* __restrict__ x, int64_t x_stride,
+                                                               const uint16_t* __restrict__ gate, int64_t gate_stride,
+                                                               const void* weight, uint16_t* __restrict__ out,
+                                                               int64_t rows, float eps) {
+  typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+  const int sub = threadIdx.x & 15;
+  const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const bool ok = row < rows;
+  const int64_t r = ok ? row : 0;
+  const u16x8 xv = *reinterpret_cast<const u16x8*>(x + r * x_stride + 8 * sub);
+  const u16x8 zv = *reinterpret_cast<const u16x8*>(gate + r * gate_stride + 8 * sub);
+  float xf[8], ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    xf[e] = bf2f(xv[e]);
+    ss += xf[e] * xf[e];
+  }
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) ss += __shfl_xor(ss, o, kWave);
+  const float inv = rsqrt_f(ss / 128.0f + eps);
+  u16x8 ov;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int c = 8 * sub + e;
+    const float xn = rbf(xf[e] * inv);
+    const float y = kWBf16 ? rbf(bf2f(reinterpret_cast<const uint16_t*>(weight)[c]) * xn)
+                           : reinterpret_cast<const float*>(weight)[c] * xn;
+    ov[e] = f2bf(y * silu_f(bf2f(zv[e])));
+  }
+  if (ok) *reinterpret_cast<u16x8*>(out + row * 128 + 8 * sub) = ov;
+}
+
 template <bool kWBf16>
 __global__ __launch_bounds__(256) void gated_rmsnorm_kernel(const uint16_t* __restrict__ x, int64_t x_stride,
                                                             const uint16_t* __restrict__ gate,
@@ -430,12 +464,25 @@ extern "C" int gdn_gated_rmsnorm(const void* x, int64_t x_stride, const void* ga
   GDN_SUPPORT(D > 0 && D % 64 == 0 && D <= 512, "gdn_gated_rmsnorm: D=%d must be a multiple of 64 <= 512", D);
   GDN_REQUIRE(w_dtype == GDN_F32 || w_dtype == GDN_BF16, "gdn_gated_rmsnorm: bad w_dtype");
   if (rows == 0) return GDN_OK;
+  hipStream_t st = (hipStream_t)stream;
+  const bool vec = D == 128 && x_stride % 8 == 0 && gate_stride % 8 == 0 && aligned(x, 16) && aligned(gate, 16) &&
+                   aligned(out, 16);
+  if (vec) {
+    const unsigned blocks = (unsigned)((rows + 15) / 16);
+    if (w_dtype == GDN_BF16)
+      gated_rmsnorm128_kernel<true><<<blocks, 256, 0, st>>>((const uint16_t*)x, x_stride, (const uint16_t*)gate,
+                                                            gate_stride, weight, (uint16_t*)out, rows, eps);
+    else
+      gated_rmsnorm128_kernel<false><<<blocks, 256, 0, st>>>((const uint16_t*)x, x_stride, (const uint16_t*)gate,
+                                                             gate_stride, weight, (uint16_t*)out, rows, eps);
+    return check_launch("gdn_gated_rmsnorm");
+  }
   const unsigned blocks = (unsigned)((rows + 3) / 4);
   if (w_dtype == GDN_BF16)
-    gated_rmsnorm_kernel<true><<<blocks, 256, 0, (hipStream_t)stream>>>(
+    gated_rmsnorm_kernel<true><<<blocks, 256, 0, st>>>(
         (const uint16_t*)x, x_stride, (const uint16_t*)gate, gate_stride, weight, (uint16_t*)out, rows, D, eps);
   else
-    gated_rmsnorm_kernel<false><<<blocks, 256, 0, (hipStream_t)stream>>>(
+    gated_rmsnorm_kernel<false><<<blocks, 256, 0, st>>>(
         (const uint16_t*)x, x_stride, (const uint16_t*)gate, gate_stride, weight, (uint16_t*)out, rows, D, eps);
   return check_launch("gdn_gated_rmsnorm");
 }

@@ -171,20 +171,21 @@ __global__ __launch_bounds__(pf::NT) void unit_lower_inv_kernel(const float* __r
 // Chunked prefill, part 1: chunk-local quantities (parallel over every (chunk, value head)).
 // ============================================================================================
 // Workspace record per (chunk slot, value head), consumed by the state kernel in exactly the
-// layouts it stages into LDS (so its per-chunk staging is plain copies):
-//   W   [64][128] bf16 = T diag(beta e^G) K          Tb [64][64] bf16 = T diag(beta)
-//   QK  [64][64]  bf16 = scale q.k e^{Gi-Gj}, i>=j    Qg [64][128] bf16 = scale e^{G_t} q_t
-//   KT  [128][64] bf16 = K^T (l2-normalised keys)     DEC [64] fp32 = e^{G_last - G_t}
-//   GL  fp32 = e^{G_last}
+// layouts it uses (so its per-chunk staging is plain copies):
+//   W   [64][128] bf16 = T diag(beta e^G) K          QK [64][64] bf16 = scale q.k e^{Gi-Gj}, i>=j
+//   Qg  [64][128] bf16 = scale e^{G_t} q_t           KT [128][64] bf16 = K^T (l2-normalised keys)
+//   U   fp32 = T diag(beta) V in MFMA accumulator tiles: [col block 8][token block 4][lane 64][4]
+//       (lane l of a tile holds rows 4(l/16)..+3 of column l%16)
+//   DEC [64] fp32 = e^{G_last - G_t}                 GL fp32 = e^{G_last}
 namespace ws {
 constexpr int W = 0;                           // byte offsets inside one record
-constexpr int TB = W + pf::CH * pf::D * 2;     // 16384
-constexpr int QK = TB + pf::CH * pf::CH * 2;   // 24576
-constexpr int QG = QK + pf::CH * pf::CH * 2;   // 32768
-constexpr int KT = QG + pf::CH * pf::D * 2;    // 49152
-constexpr int DEC = KT + pf::D * pf::CH * 2;   // 65536
-constexpr int GL = DEC + pf::CH * 4;           // 65792
-constexpr int BYTES = 66048;                   // record size (multiple of 256)
+constexpr int QK = W + pf::CH * pf::D * 2;     // 16384
+constexpr int QG = QK + pf::CH * pf::CH * 2;   // 24576
+constexpr int KT = QG + pf::CH * pf::D * 2;    // 40960
+constexpr int U = KT + pf::D * pf::CH * 2;     // 57344
+constexpr int DEC = U + pf::CH * pf::D * 4;    // 90112
+constexpr int GL = DEC + pf::CH * 4;           // 90368
+constexpr int BYTES = 90624;                   // record size (multiple of 256)
 }  // namespace ws
 
 struct ChunkPos {
@@ -278,6 +279,7 @@ struct LocalSmem {
 template <typename BetaT>
 __global__ __launch_bounds__(pf::NT, 2) void chunk_local_kernel(
     const uint16_t* __restrict__ q, int64_t qs, const uint16_t* __restrict__ k, int64_t ks,
+    const uint16_t* __restrict__ v, int64_t vs,
     const float* __restrict__ g, const BetaT* __restrict__ beta, const int32_t* __restrict__ cu,
     const int32_t* __restrict__ seq_chunk0, int nseq, int seq_len, int Hqk, int Hv, int use_l2,
     uint8_t* __restrict__ work) {
@@ -299,6 +301,9 @@ __global__ __launch_bounds__(pf::NT, 2) void chunk_local_kernel(
     for (int i = 0; i < 4; ++i) *reinterpret_cast<u16x8*>(&sm.a.K[(4 * tq + i) * LDK + 8 * fb]) = x[i];
     store_transposed4(sm.KT, LDT, x, tq, 8 * fb);
   }
+  // V rows 4tq.. x columns 8fb.. stay in registers until the inverse has freed the X buffer
+  u16x8 vreg[4];
+  load_rows4(vreg, v + (int64_t)h * D, vs, cp.t0, cp.len, t >> 4, 8 * (t & 15));
   // Q in A-fragment order of this wave (rows 16w + l%16, features 8(l/16) + 32s)
   bf16x8 qf[4];
   {
@@ -408,36 +413,44 @@ __global__ __launch_bounds__(pf::NT, 2) void chunk_local_kernel(
 
   unit_lower_inv64(sm.X, sm.T, sm.Y, w, lane);
 
-  // Tb = T diag(beta) -> workspace (row t = 4*(thread/16)..., 16 columns per thread)
-  {
-    const int row = t >> 2, c0 = 16 * (t & 3);
-    u16x8 o[2];
-#pragma unroll
-    for (int e = 0; e < 16; ++e) o[e >> 3][e & 7] = f2bf(sm.T[row * LDF + c0 + e] * sm.B[c0 + e]);
-    uint16_t* tb = reinterpret_cast<uint16_t*>(rec + ws::TB) + row * CH + c0;
-    *reinterpret_cast<u16x8*>(tb) = o[0];
-    *reinterpret_cast<u16x8*>(tb + 8) = o[1];
-  }
-  // W = T diag(beta e^G) K for this wave's rows
+  // W = T diag(beta e^G) K and U = T diag(beta) V for this wave's rows
   f32x4 accW[8];
   {
-    bf16x8 tbe[2];
+    bf16x8 tbe[2], tb[2];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       const float* trow = &sm.T[(16 * w + (lane & 15)) * LDF + 32 * s + 8 * (lane >> 4)];
-      float a[8];
+      float a[8], b[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int col = 32 * s + 8 * (lane >> 4) + e;
-        a[e] = trow[e] * sm.B[col] * sm.EG[col];
+        a[e] = trow[e] * sm.B[col];
+        b[e] = a[e] * sm.EG[col];
       }
-      tbe[s] = pack8(a);
+      tb[s] = pack8(a);
+      tbe[s] = pack8(b);
     }
 #pragma unroll
     for (int cb = 0; cb < 8; ++cb) {
       accW[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < 2; ++s) accW[cb] = mma(tbe[s], frag(sm.KT, LDT, 16 * cb, 32 * s, lane), accW[cb]);
+    }
+    // V^T into the X buffer (dead after the inverse; V^T is 1 KiB larger and runs into T, whose
+    // reads all finished above -- hence the barrier); U tiles go straight to the workspace in
+    // accumulator layout
+    static_assert(pf::D * pf::LDT * 2 <= 2 * pf::CH * pf::LDF * 4, "V^T must fit in X and T");
+    uint16_t* VT = reinterpret_cast<uint16_t*>(sm.X);
+    __syncthreads();
+    store_transposed4(VT, LDT, vreg, t >> 4, 8 * (t & 15));
+    __syncthreads();
+    f32x4* ur = reinterpret_cast<f32x4*>(rec + ws::U);
+#pragma unroll
+    for (int cb = 0; cb < 8; ++cb) {
+      f32x4 u = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 2; ++s) u = mma(tb[s], frag(VT, LDT, 16 * cb, 32 * s, lane), u);
+      ur[(cb * 4 + w) * 64 + lane] = u;
     }
   }
   // stage W in LDS (the K buffer is free after the K K^T products) and store it coalesced
@@ -470,10 +483,8 @@ __global__ __launch_bounds__(pf::NT, 2) void chunk_local_kernel(
 struct StateSmem {
   uint16_t Qg[pf::CH * pf::LDK];       // scale e^G q (token, feature)
   uint16_t W[pf::CH * pf::LDK];        // (token, feature)
-  uint16_t Tb[pf::CH * pf::LDT];       // (token, token)
   uint16_t QK[pf::CH * pf::LDT];       // (token, token)
   uint16_t KT[pf::D * pf::LDT];        // (feature, token)
-  uint16_t VT[64 * pf::LDT];           // (column, token) for the workgroup's 64 columns
   uint16_t ST[4][16 * pf::LDK];        // per wave: bf16 S^T (column, feature)
   uint16_t VN[4][3][16 * pf::LDT];     // per wave: vn, hi(dec vn), lo(dec vn) transposed (column, token)
   float DEC[pf::CH];
@@ -481,12 +492,12 @@ struct StateSmem {
 };
 
 struct StateStage {  // one chunk's inputs, prefetched into registers
-  u16x8 qg[4], kt[4], w[4], tb[2], qk[2], v[4];
+  u16x8 qg[4], kt[4], w[4], qk[2];
+  f32x4 u[4];  // this wave's U tiles (accumulator layout), one per token block
   float dec, gl;
 };
 
-__device__ __forceinline__ void state_prefetch(StateStage& st, const uint16_t* v, int64_t vs, const uint8_t* rec,
-                                               int64_t t0, int len, int h, int vcol0, int t) {
+__device__ __forceinline__ void state_prefetch(StateStage& st, const uint8_t* rec, int j0, int t) {
   using namespace pf;
   const uint16_t* wr = reinterpret_cast<const uint16_t*>(rec + ws::W);
   const uint16_t* qgr = reinterpret_cast<const uint16_t*>(rec + ws::QG);
@@ -498,16 +509,15 @@ __device__ __forceinline__ void state_prefetch(StateStage& st, const uint16_t* v
     st.qg[i] = *reinterpret_cast<const u16x8*>(qgr + (idx >> 4) * D + 8 * (idx & 15));
     st.kt[i] = *reinterpret_cast<const u16x8*>(ktr + (idx >> 3) * CH + 8 * (idx & 7));
   }
-  const uint16_t* tbr = reinterpret_cast<const uint16_t*>(rec + ws::TB);
   const uint16_t* qkr = reinterpret_cast<const uint16_t*>(rec + ws::QK);
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int idx = t + NT * i;  // 512 pieces of 16 bytes
-    st.tb[i] = *reinterpret_cast<const u16x8*>(tbr + (idx >> 3) * CH + 8 * (idx & 7));
     st.qk[i] = *reinterpret_cast<const u16x8*>(qkr + (idx >> 3) * CH + 8 * (idx & 7));
   }
-  // V: threads 0..127 -> token quad t/8, column block t%8 (8 of the workgroup's 64 columns)
-  if (t < 128) load_rows4(st.v, v + (int64_t)h * D + vcol0, vs, t0, len, t >> 3, 8 * (t & 7));
+  const f32x4* ur = reinterpret_cast<const f32x4*>(rec + ws::U) + (j0 >> 4) * 4 * 64 + (t & 63);
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) st.u[tb] = ur[tb * 64];
   st.dec = reinterpret_cast<const float*>(rec + ws::DEC)[t & 63];
   st.gl = reinterpret_cast<const float*>(rec + ws::GL)[0];
 }
@@ -524,17 +534,15 @@ __device__ __forceinline__ void state_commit(StateSmem& sm, const StateStage& st
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int idx = t + NT * i;
-    *reinterpret_cast<u16x8*>(&sm.Tb[(idx >> 3) * LDT + 8 * (idx & 7)]) = st.tb[i];
     *reinterpret_cast<u16x8*>(&sm.QK[(idx >> 3) * LDT + 8 * (idx & 7)]) = st.qk[i];
   }
-  if (t < 128) store_transposed4(sm.VT, LDT, st.v, t >> 3, 8 * (t & 7));
   if (t < 64) sm.DEC[t] = st.dec;
   if (t == 0) sm.GL = st.gl;
 }
 
 template <typename OutT>
 __global__ __launch_bounds__(pf::NT, 1) void chunk_state_kernel(
-    const uint16_t* __restrict__ v, int64_t vs, const float* __restrict__ init, float* __restrict__ final_state,
+    const float* __restrict__ init, float* __restrict__ final_state,
     OutT* __restrict__ out, const int32_t* __restrict__ cu, const int32_t* __restrict__ seq_chunk0, int seq_len,
     int Hv, const uint8_t* __restrict__ work) {
   using namespace pf;
@@ -575,27 +583,23 @@ __global__ __launch_bounds__(pf::NT, 1) void chunk_state_kernel(
 
   StateStage st;
   const uint8_t* rec0 = work + (int64_t)slot0 * Hv * ws::BYTES + (int64_t)h * ws::BYTES;
-  if (nch > 0) state_prefetch(st, v, vs, rec0, s0, L < CH ? L : CH, h, vcol0, t);
+  if (nch > 0) state_prefetch(st, rec0, j0, t);
 
   for (int c = 0; c < nch; ++c) {
     const int len = L - c * CH < CH ? L - c * CH : CH;
     const int64_t t0 = s0 + (int64_t)c * CH;
     state_commit(sm, st, t);
+    f32x4 U[4];
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) U[tb] = st.u[tb];
     __syncthreads();
 
-    // U = Tb V and vn = U - W S for all 4 token blocks of the chunk.  Each phase loads all of its
-    // LDS fragments first and then issues its MFMAs (sched_barrier keeps the compiler from
-    // re-interleaving them into one-load-one-wait pairs).
-    f32x4 U[4];
+    // vn = U - W S for all 4 token blocks of the chunk.  Each phase loads all of its LDS fragments
+    // first and then issues its MFMAs (sched_barrier keeps the compiler from re-interleaving them
+    // into one-load-one-wait pairs).
     bf16x8 fs[4];  // S^T fragments (B operand of W S and Qg S), reused by the output products
     {
-      bf16x8 ft[2][4], fv[2], fw[4][4];
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        fv[s] = frag(sm.VT, LDT, 16 * w, 32 * s, lane);
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb) ft[s][tb] = frag(sm.Tb, LDT, 16 * tb, 32 * s, lane);
-      }
+      bf16x8 fw[4][4];
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         fs[s] = frag(myST, LDK, 0, 32 * s, lane);
@@ -603,11 +607,6 @@ __global__ __launch_bounds__(pf::NT, 1) void chunk_state_kernel(
         for (int tb = 0; tb < 4; ++tb) fw[s][tb] = frag_neg(sm.W, LDK, 16 * tb, 32 * s, lane);
       }
       __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int tb = 0; tb < 4; ++tb) {
-        U[tb] = mma(ft[0][tb], fv[0], f32x4{0.f, 0.f, 0.f, 0.f});
-        U[tb] = mma(ft[1][tb], fv[1], U[tb]);
-      }
 #pragma unroll
       for (int s = 0; s < 4; ++s)
 #pragma unroll
@@ -670,8 +669,7 @@ __global__ __launch_bounds__(pf::NT, 1) void chunk_state_kernel(
 
     // next chunk's operands: issued here so their registers are not live during the products above
     if (c + 1 < nch) {
-      const int len1 = L - (c + 1) * CH < CH ? L - (c + 1) * CH : CH;
-      state_prefetch(st, v, vs, rec0 + (int64_t)(c + 1) * Hv * ws::BYTES, t0 + CH, len1, h, vcol0, t);
+      state_prefetch(st, rec0 + (int64_t)(c + 1) * Hv * ws::BYTES, j0, t);
     }
     // S' = GL S + K^T (hi + lo), then its bf16 transpose for the next chunk
     {
@@ -714,13 +712,13 @@ __global__ __launch_bounds__(pf::NT, 1) void chunk_state_kernel(
 // ============================================================================================
 // Causal depthwise conv prefill + SiLU with decode-state capture.
 // ============================================================================================
-// One thread per (channel, block of TB packed tokens).  x_t for t < 0 (before a sequence) comes
-// from `history` [n_seq, C, K] (x_{-j} = history[K - j]) or is zero.  Numerics of F.conv1d on bf16:
-// fp32 accumulation of the K products (+ bias), one bf16 rounding, SiLU, bf16.
-constexpr int kConvTB = 32;
-
+// One thread per (packed token p, 8 channels): it loads the K input rows p-K+1..p with 16-byte
+// reads (rows before its sequence come from `history` [n_seq, C, K], x_{-j} = history[K - j], or
+// are zero), writes 8 outputs with one 16-byte store, and -- for the last token of a sequence --
+// the sequence's decode conv state (its last K inputs).  Numerics of F.conv1d on bf16: fp32
+// accumulation of the K products (+ bias), one bf16 rounding, SiLU, bf16.
 __device__ __forceinline__ int find_seq(const int32_t* cu, int nseq, int64_t p) {
-  int lo = 0, hi = nseq - 1;
+  int lo = 0, hi = nseq - 1;  // last sequence whose start <= p (skips empty ones)
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
     if (cu[mid] <= p) lo = mid;
@@ -729,47 +727,56 @@ __device__ __forceinline__ int find_seq(const int32_t* cu, int nseq, int64_t p) 
   return lo;
 }
 
+template <int K>
 __global__ __launch_bounds__(256) void conv_prefill_kernel(const uint16_t* __restrict__ x, int64_t x_stride,
                                                            const uint16_t* __restrict__ weight,
                                                            const uint16_t* __restrict__ bias,
                                                            const uint16_t* __restrict__ history,
                                                            uint16_t* __restrict__ out, uint16_t* __restrict__ state,
-                                                           int64_t total, const int32_t* __restrict__ cu, int nseq,
-                                                           int seq_len, int C, int K) {
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t p0 = (int64_t)blockIdx.y * kConvTB;
-  if (c >= C || p0 >= total) return;
-  float w[8];
-  for (int i = 0; i < K; ++i) w[i] = bf2f(weight[(int64_t)c * K + i]);
-  const float b = bias ? bf2f(bias[c]) : 0.f;
-  auto seq_start = [&](int s) -> int64_t { return cu ? (int64_t)cu[s] : (int64_t)s * seq_len; };
-  int s = cu ? find_seq(cu, nseq, p0) : (int)(p0 / seq_len);
-  int64_t s_lo = seq_start(s), s_hi = seq_start(s + 1);
-  // window: win[K-1] is the newest input; prime with the K-1 inputs before p0
-  float win[8];
-  auto input_at = [&](int64_t p) -> float {  // p may precede s_lo
-    if (p >= s_lo) return bf2f(x[p * x_stride + c]);
-    const int64_t back = s_lo - p;  // 1..K
-    if (history && back <= K) return bf2f(history[((int64_t)s * C + c) * K + (K - back)]);
-    return 0.f;
-  };
-  for (int i = 0; i < K - 1; ++i) win[i + 1] = input_at(p0 - (K - 1) + i);
-  const int64_t pend = p0 + kConvTB < total ? p0 + kConvTB : total;
-  for (int64_t p = p0; p < pend; ++p) {
-    while (p >= s_hi) {  // next (non-empty) sequence: re-prime the window from its history
-      ++s;
-      s_lo = seq_start(s);
-      s_hi = seq_start(s + 1);
-      for (int i = 0; i < K - 1; ++i) win[i + 1] = input_at(p - (K - 1) + i);
+                                                           const int32_t* __restrict__ cu, int nseq, int seq_len,
+                                                           int C) {
+  const int cg = blockIdx.x * blockDim.x + threadIdx.x;  // 8-channel group
+  const int64_t p = blockIdx.y;
+  if (8 * cg >= C) return;
+  const int c0 = 8 * cg;
+  const int s = cu ? find_seq(cu, nseq, p) : (int)(p / seq_len);
+  const int64_t s_lo = cu ? (int64_t)cu[s] : (int64_t)s * seq_len;
+  const int64_t s_hi = cu ? (int64_t)cu[s + 1] : s_lo + seq_len;
+  u16x8 win[K];
+#pragma unroll
+  for (int r = 0; r < K; ++r) {
+    const int64_t tok = p - (K - 1) + r;
+    if (tok >= s_lo) {
+      win[r] = *reinterpret_cast<const u16x8*>(x + tok * x_stride + c0);
+    } else {
+      const int back = (int)(s_lo - tok);  // 1..K-1
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        win[r][e] = history ? history[((int64_t)s * C + c0 + e) * K + (K - back)] : (uint16_t)0;
     }
-    for (int i = 0; i < K - 1; ++i) win[i] = win[i + 1];
-    win[K - 1] = bf2f(x[p * x_stride + c]);
-    float acc = b;
-    for (int i = 0; i < K; ++i) acc += win[i] * w[i];
-    out[p * (int64_t)C + c] = f2bf(silu_f(rbf(acc)));
-    if (p == s_hi - 1 && state) {  // last token of the sequence: capture the last K inputs
-      for (int i = 0; i < K; ++i) state[((int64_t)s * C + c) * K + i] = f2bf(win[i]);
-    }
+  }
+  u16x8 wt[K];  // weight[c0 + e][r] -> wt[r][e]
+  {
+    const uint16_t* wp = weight + (int64_t)c0 * K;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+#pragma unroll
+      for (int r = 0; r < K; ++r) wt[r][e] = wp[e * K + r];
+  }
+  u16x8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float acc = bias ? bf2f(bias[c0 + e]) : 0.f;
+#pragma unroll
+    for (int r = 0; r < K; ++r) acc += bf2f(win[r][e]) * bf2f(wt[r][e]);
+    o[e] = f2bf(silu_f(rbf(acc)));
+  }
+  *reinterpret_cast<u16x8*>(out + p * (int64_t)C + c0) = o;
+  if (state && p == s_hi - 1) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+#pragma unroll
+      for (int r = 0; r < K; ++r) state[((int64_t)s * C + c0 + e) * K + r] = win[r][e];
   }
 }
 
@@ -850,18 +857,19 @@ extern "C" int gdn_chunk_prefill(const void* q, int64_t q_stride, const void* k,
     dim3 g1((unsigned)total_chunks, (unsigned)Hv);
     if (beta_dtype == GDN_BF16)
       chunk_local_kernel<uint16_t><<<g1, pf::NT, 0, s>>>((const uint16_t*)q, q_stride, (const uint16_t*)k, k_stride,
+                                                         (const uint16_t*)v, v_stride,
                                                          g, (const uint16_t*)beta, cu_seqlens, seq_chunk0, nseq,
                                                          seq_len, Hqk, Hv, use_qk_l2norm, work);
     else
       chunk_local_kernel<float><<<g1, pf::NT, 0, s>>>((const uint16_t*)q, q_stride, (const uint16_t*)k, k_stride,
+                                                      (const uint16_t*)v, v_stride,
                                                       g, (const float*)beta, cu_seqlens, seq_chunk0, nseq, seq_len,
                                                       Hqk, Hv, use_qk_l2norm, work);
     int rc = check_launch("gdn_chunk_prefill(local)");
     if (rc) return rc;
   }
   chunk_state_kernel<uint16_t><<<(unsigned)(nseq * Hv * (pf::D / 64)), pf::NT, 0, s>>>(
-      (const uint16_t*)v, v_stride, initial_state, final_state, (uint16_t*)out, cu_seqlens, seq_chunk0, seq_len, Hv,
-      work);
+      initial_state, final_state, (uint16_t*)out, cu_seqlens, seq_chunk0, seq_len, Hv, work);
   return check_launch("gdn_chunk_prefill(state)");
 }
 
@@ -876,10 +884,27 @@ extern "C" int gdn_conv_prefill(const void* x, int64_t x_stride, const void* wei
               "gdn_conv_prefill: nseq*seq_len != total_tokens without cu_seqlens");
   hipStream_t s = (hipStream_t)stream;
   if (total_tokens > 0) {
-    dim3 grid((C + 255) / 256, (unsigned)((total_tokens + kConvTB - 1) / kConvTB));
-    conv_prefill_kernel<<<grid, 256, 0, s>>>((const uint16_t*)x, x_stride, (const uint16_t*)weight,
-                                             (const uint16_t*)bias, (const uint16_t*)history, (uint16_t*)out,
-                                             (uint16_t*)state_out, total_tokens, cu_seqlens, nseq, seq_len, C, K);
+    GDN_REQUIRE(C % 8 == 0 && x_stride % 8 == 0 && aligned(x, 16) && aligned(out, 16),
+                "gdn_conv_prefill: C and the row stride must be multiples of 8 with 16-byte aligned rows");
+    GDN_REQUIRE(total_tokens < (1ll << 31), "gdn_conv_prefill: too many tokens");
+    dim3 grid((unsigned)((C / 8 + 255) / 256), (unsigned)total_tokens);
+#define GDN_CONV_PREFILL(KK)                                                                                    \
+  case KK:                                                                                                     \
+    conv_prefill_kernel<KK><<<grid, 256, 0, s>>>((const uint16_t*)x, x_stride, (const uint16_t*)weight,          \
+                                                 (const uint16_t*)bias, (const uint16_t*)history, (uint16_t*)out, \
+                                                 (uint16_t*)state_out, cu_seqlens, nseq, seq_len, C);              \
+    break;
+    switch (K) {
+      GDN_CONV_PREFILL(1)
+      GDN_CONV_PREFILL(2)
+      GDN_CONV_PREFILL(3)
+      GDN_CONV_PREFILL(4)
+      GDN_CONV_PREFILL(5)
+      GDN_CONV_PREFILL(6)
+      GDN_CONV_PREFILL(7)
+      GDN_CONV_PREFILL(8)
+    }
+#undef GDN_CONV_PREFILL
     int rc = check_launch("gdn_conv_prefill");
     if (rc) return rc;
   }

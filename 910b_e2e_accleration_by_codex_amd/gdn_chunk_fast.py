@@ -142,8 +142,9 @@ def causal_conv1d_prefill(x, weight, bias=None, history=None, cu_seqlens=None):
     if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
         raise TypeError("causal_conv1d_prefill: x and weight must be bfloat16")
     xt = x.transpose(1, 2)                                   # [B, L, C]
-    if xt.stride(2) != 1 or (B > 1 and xt.stride(0) != L * xt.stride(1)):
-        xt = xt.contiguous()
+    if (xt.stride(2) != 1 or (B > 1 and xt.stride(0) != L * xt.stride(1)) or xt.stride(1) % 8
+            or xt.data_ptr() % 16):
+        xt = xt.contiguous()                                 # the kernel reads 16-byte row pieces
     cu, nseq, seq_len = _seq_args(B, L, cu_seqlens, x.device)
     w = weight.reshape(C, K).contiguous()
     if bias is not None:
