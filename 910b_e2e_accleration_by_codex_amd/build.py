@@ -20,6 +20,9 @@ HIPCC_FLAGS = [
     "-Wno-unused-variable", "-Wno-unused-but-set-variable",
     # packed fp32 VALU ops stay off in device code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in ordinary VGPRs: the state kernels scale and convert their accumulators
+    # with VALU ops every chunk, which the AGPR form would surround with accvgpr copies
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-I", os.path.join(HERE, "..", "include"),
 ]
 

@@ -24,6 +24,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 namespace pf {
 constexpr int D = 128;          // head dim
@@ -170,23 +171,55 @@ __global__ __launch_bounds__(pf::NT) void unit_lower_inv_kernel(const float* __r
 // ============================================================================================
 // Chunked prefill, part 1: chunk-local quantities (parallel over every (chunk, value head)).
 // ============================================================================================
-// Workspace record per (chunk slot, value head), consumed by the state kernel in exactly the
-// layouts it uses (so its per-chunk staging is plain copies):
-//   W   [64][128] bf16 = T diag(beta e^G) K          QK [64][64] bf16 = scale q.k e^{Gi-Gj}, i>=j
-//   Qg  [64][128] bf16 = scale e^{G_t} q_t           KT [128][64] bf16 = K^T (l2-normalised keys)
-//   U   fp32 = T diag(beta) V in MFMA accumulator tiles: [col block 8][token block 4][lane 64][4]
-//       (lane l of a tile holds rows 4(l/16)..+3 of column l%16)
-//   DEC [64] fp32 = e^{G_last - G_t}                 GL fp32 = e^{G_last}
+// Workspace record per (chunk slot, value head).  Everything the scan kernel multiplies is stored
+// as ready-made MFMA operand fragments: a fragment is 64 lanes x 16 bytes (lane l at byte 16 l), so
+// the scan kernel stages a chunk with plain linear copies and reads each fragment with one
+// conflict-free 16-byte LDS read per lane.
+//
+// k-slot order.  Inside every 32-wide reduction block the scan kernel feeds MFMA B operands straight
+// from accumulator registers: lane (c, g) = (l % 16, l / 16) holds rows 4g..4g+3 of two consecutive
+// 16-row accumulator tiles, and uses them as the 8 k-values of its B fragment.  So B slot s of a
+// block stands for block row kpos(s) = 16 ((s >> 2) & 1) + 4 (s >> 3) + (s & 3), and every A
+// fragment stored here is permuted the same way along k:  A-frag element e of lane (c, g) for tile
+// (m, j) = M[16 m + c][32 j + kpos(8 g + e)].
+//
+//   WN  16 frags [tb 4][j 4]  bf16  M = -W,  W = T diag(beta e^G) K     (tokens x features)
+//   KT  16 frags [rb 8][j 2]  fp16  M = kappa K^T                       (features x tokens)
+//   QG  16 frags [tb 4][j 4]  bf16  M = scale e^{G_t} q_t               (tokens x features)
+//   QK   8 frags [tb 4][j 2]  bf16  M = scale q_i.k_j e^{G_i - G_j}, i >= j, else 0
+//   U   fp16 [slice 8][lane 64][tb 4][r 4] = U[16 tb + 4 g + r][16 slice + c] / USC[tb],
+//       U = T diag(beta) V (accumulator layout of each 16-column slice)
+//   DEC [64] fp32 = e^{G_last - G_t};  USC [4] fp32;  GL = e^{G_last};  KSC = 1 / kappa;  KAP = kappa
+// kappa (per chunk, for |K|) and 1 / USC (per token tile, for |U|) are powers of two chosen by
+// fp16_fit_exp: 1 when the largest magnitude already sits in [2^-4, 2^14), else the power that
+// moves it into [2^14, 2^15) -- inside fp16's range with full relative precision either way.
 namespace ws {
-constexpr int W = 0;                           // byte offsets inside one record
-constexpr int QK = W + pf::CH * pf::D * 2;     // 16384
-constexpr int QG = QK + pf::CH * pf::CH * 2;   // 24576
-constexpr int KT = QG + pf::CH * pf::D * 2;    // 40960
-constexpr int U = KT + pf::D * pf::CH * 2;     // 57344
-constexpr int DEC = U + pf::CH * pf::D * 4;    // 90112
-constexpr int GL = DEC + pf::CH * 4;           // 90368
-constexpr int BYTES = 90624;                   // record size (multiple of 256)
+constexpr int FRAG = 1024;                       // bytes per fragment
+constexpr int WN = 0;                            // byte offsets inside one record
+constexpr int KT = WN + 16 * FRAG;               // 16384
+constexpr int QG = KT + 16 * FRAG;               // 32768
+constexpr int QK = QG + 16 * FRAG;               // 49152
+constexpr int U = QK + 8 * FRAG;                 // 57344
+constexpr int DEC = U + pf::CH * pf::D * 2;      // 73728
+constexpr int USC = DEC + pf::CH * 4;            // 73984 (16-byte aligned: read as one float4)
+constexpr int GL = USC + 16;                     // 74000
+constexpr int KSC = GL + 4;                      // 74004
+constexpr int KAP = KSC + 4;                     // 74008
+constexpr int HDR = DEC;                         // DEC, USC, GL, KSC, KAP: one 512-byte header
+constexpr int BYTES = 74240;                     // record size (multiple of 256)
 }  // namespace ws
+
+// Exponent se such that 2^se max|x| lies in [2^14, 2^15) (0 for 0 / non-finite; clamped to +-60).
+__device__ __forceinline__ int fp16_scale_exp(float amax) {
+  const int e = (int)((__float_as_uint(amax) >> 23) & 0xff) - 127;
+  if (!(amax > 0.f) || e == 128) return 0;
+  const int se = 14 - e;
+  return se < -60 ? -60 : (se > 60 ? 60 : se);
+}
+// As fp16_scale_exp, but 0 whenever max|x| already lies in [2^-4, 2^14).
+__device__ __forceinline__ int fp16_fit_exp(float amax) {
+  return (amax >= 0.0625f && amax < 16384.0f) ? 0 : fp16_scale_exp(amax);
+}
 
 struct ChunkPos {
   int64_t t0;  // first packed token of the chunk
@@ -264,16 +297,43 @@ __device__ __forceinline__ void store_transposed4(uint16_t* dst, int ld, const u
   }
 }
 
+// A-fragment of a bf16 [rows, ld] tile in k-slot order (two 8-byte reads; see the workspace notes).
+__device__ __forceinline__ bf16x8 frag_kperm(const uint16_t* base, int ld, int row0, int k0, int lane) {
+  const uint16_t* p = base + (row0 + (lane & 15)) * ld + k0 + 4 * (lane >> 4);
+  const u16x4 lo = *reinterpret_cast<const u16x4*>(p), hi = *reinterpret_cast<const u16x4*>(p + 16);
+  const u16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(bf16x8, v);
+}
+// 8 accumulator values (rows 4g..4g+3 of tiles a and b) -> one k-slot ordered bf16 fragment.
+__device__ __forceinline__ bf16x8 pack_acc_bf16(f32x4 a, f32x4 b) {
+  const uint32_t w0 = f2bf2(a[0], a[1]), w1 = f2bf2(a[2], a[3]), w2 = f2bf2(b[0], b[1]), w3 = f2bf2(b[2], b[3]);
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 u = {w0, w1, w2, w3};
+  return __builtin_bit_cast(bf16x8, u);
+}
+__device__ __forceinline__ f16x8 pack_acc_f16(f32x4 a, f32x4 b, float sa) {
+  f16x8 h;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    h[r] = (_Float16)(a[r] * sa);
+    h[4 + r] = (_Float16)(b[r] * sa);
+  }
+  return h;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
 struct LocalSmem {
-  union {
-    uint16_t K[pf::CH * pf::LDK];   // K chunk, row-major (token, feature): A/B of K K^T, B of Q K^T
-    uint16_t W[pf::CH * pf::LDK];   // later: W staged for coalesced stores
-  } a;
-  uint16_t KT[pf::D * pf::LDT];     // K chunk transposed (feature, token): B of W = T' K
+  uint16_t K[pf::CH * pf::LDK];     // K chunk, row-major (token, feature)
+  uint16_t KT[pf::D * pf::LDT];     // K chunk transposed (feature, token)
   float X[pf::CH * pf::LDF];
   float T[pf::CH * pf::LDF];
   float Y[4 * 256];
   float G[pf::CH], EG[pf::CH], B[pf::CH];
+  float KMX[4];
 };
 
 template <typename BetaT>
@@ -285,7 +345,7 @@ __global__ __launch_bounds__(pf::NT, 2) void chunk_local_kernel(
     uint8_t* __restrict__ work) {
   using namespace pf;
   __shared__ LocalSmem sm;
-  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
   const int slot = blockIdx.x, h = blockIdx.y;
   const int hk = h / (Hv / Hqk);
   const ChunkPos cp = chunk_pos(slot, cu, seq_chunk0, nseq, seq_len);
@@ -297,24 +357,36 @@ __global__ __launch_bounds__(pf::NT, 2) void chunk_local_kernel(
     u16x8 x[4];
     load_rows4(x, k + (int64_t)hk * D, ks, cp.t0, cp.len, tq, 8 * fb);
     if (use_l2) l2norm_rows4(x);
+    float m = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<u16x8*>(&sm.a.K[(4 * tq + i) * LDK + 8 * fb]) = x[i];
+    for (int i = 0; i < 4; ++i) {
+      *reinterpret_cast<u16x8*>(&sm.K[(4 * tq + i) * LDK + 8 * fb]) = x[i];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(bf2f(x[i][e])));
+    }
     store_transposed4(sm.KT, LDT, x, tq, 8 * fb);
+    m = wave_max(m);
+    if (lane == 0) sm.KMX[w] = m;
   }
   // V rows 4tq.. x columns 8fb.. stay in registers until the inverse has freed the X buffer
   u16x8 vreg[4];
   load_rows4(vreg, v + (int64_t)h * D, vs, cp.t0, cp.len, t >> 4, 8 * (t & 15));
-  // Q in A-fragment order of this wave (rows 16w + l%16, features 8(l/16) + 32s)
+  // Q rows 16w + l%16 in k-slot order: block s holds features 32s + 4g.. and 32s + 16 + 4g..
   bf16x8 qf[4];
   {
     const u16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
-    const int row = 16 * w + (lane & 15);
+    const int row = 16 * w + c16;
     u16x8 r[4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
-      r[s] = row < cp.len ? *reinterpret_cast<const u16x8*>(q + (cp.t0 + row) * qs + (int64_t)hk * D + 32 * s +
-                                                            8 * (lane >> 4))
-                          : zero;
+    for (int s = 0; s < 4; ++s) {
+      if (row < cp.len) {
+        const uint16_t* p = q + (cp.t0 + row) * qs + (int64_t)hk * D + 32 * s + 4 * g4;
+        const u16x4 lo = *reinterpret_cast<const u16x4*>(p), hi = *reinterpret_cast<const u16x4*>(p + 16);
+        r[s] = u16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      } else {
+        r[s] = zero;
+      }
+    }
     if (use_l2) {
       float ss = 0.f;
 #pragma unroll
@@ -354,204 +426,280 @@ __global__ __launch_bounds__(pf::NT, 2) void chunk_local_kernel(
   }
   __syncthreads();
 
-  // Qg = scale e^{G_t} q_t -> workspace (this wave's rows, straight from the A fragments);
-  // K^T -> workspace (from LDS)
+  // QG fragments (this wave's token tile, straight from the k-slot ordered Q fragments) and the
+  // kappa-scaled fp16 K^T fragments
   {
-    const int row = 16 * w + (lane & 15);
-    const float f = kScale * sm.EG[row];
-    uint16_t* qg = reinterpret_cast<uint16_t*>(rec + ws::QG) + row * D + 8 * (lane >> 4);
+    const float f = kScale * sm.EG[16 * w + c16];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const u16x8 u = __builtin_bit_cast(u16x8, qf[s]);
       u16x8 o;
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = f2bf(bf2f(u[e]) * f);
-      *reinterpret_cast<u16x8*>(qg + 32 * s) = o;
+      *reinterpret_cast<u16x8*>(rec + ws::QG + (w * 4 + s) * ws::FRAG + lane * 16) = o;
     }
-    uint16_t* kt = reinterpret_cast<uint16_t*>(rec + ws::KT);
+    const float kmax = fmaxf(fmaxf(sm.KMX[0], sm.KMX[1]), fmaxf(sm.KMX[2], sm.KMX[3]));
+    const int ke = fp16_fit_exp(kmax);
+    const float kappa = ldexpf(1.0f, ke);
+    if (t == 0) {
+      reinterpret_cast<float*>(rec + ws::KSC)[0] = ldexpf(1.0f, -ke);
+      reinterpret_cast<float*>(rec + ws::KAP)[0] = kappa;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int idx = t + NT * i;  // 1024 pieces of 16 bytes: row idx/8, piece idx%8
-      *reinterpret_cast<u16x8*>(kt + (idx >> 3) * CH + 8 * (idx & 7)) =
-          *reinterpret_cast<const u16x8*>(&sm.KT[(idx >> 3) * LDT + 8 * (idx & 7)]);
+      const int idx = t + NT * i;  // fragment idx / 64 = (rb, j), lane idx % 64
+      const int f_ = idx >> 6, l = idx & 63, rb = f_ >> 1, j = f_ & 1;
+      const uint16_t* p = &sm.KT[(16 * rb + (l & 15)) * LDT + 32 * j + 4 * (l >> 4)];
+      const u16x4 lo = *reinterpret_cast<const u16x4*>(p), hi = *reinterpret_cast<const u16x4*>(p + 16);
+      f16x8 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        o[e] = (_Float16)(bf2f(lo[e]) * kappa);
+        o[4 + e] = (_Float16)(bf2f(hi[e]) * kappa);
+      }
+      *reinterpret_cast<f16x8*>(rec + ws::KT + idx * 16) = o;
     }
   }
-  // A = K K^T and QK = Q K^T for this wave's 16 rows; X -> LDS, QK -> workspace
+  // A = K K^T (accumulator layout, rows = this wave's tokens) -> X in LDS; (Q K^T)^T = K Q^T, whose
+  // accumulator layout is exactly the k-slot ordered QK fragment layout -> workspace
   {
     f32x4 accA[4], accQ[4];
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb) accA[cb] = accQ[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const bf16x8 ak = frag(sm.a.K, LDK, 16 * w, 32 * s, lane);
+      const bf16x8 ak = frag(sm.K, LDK, 16 * w, 32 * s, lane);
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb) {
         if (cb <= w) {
-          const bf16x8 b = frag(sm.a.K, LDK, 16 * cb, 32 * s, lane);
-          accA[cb] = mma(ak, b, accA[cb]);
-          accQ[cb] = mma(qf[s], b, accQ[cb]);
+          accA[cb] = mma(ak, frag(sm.K, LDK, 16 * cb, 32 * s, lane), accA[cb]);
+          accQ[cb] = mma(frag_kperm(sm.K, LDK, 16 * cb, 32 * s, lane), qf[s], accQ[cb]);
         }
       }
     }
-    uint16_t* qk = reinterpret_cast<uint16_t*>(rec + ws::QK);
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int i = 16 * w + 4 * (lane >> 4) + r, jj = 16 * cb + (lane & 15);
-        float x = 0.f, v = 0.f;
-        if (cb <= w && i >= jj) {
-          const float dec = expf(sm.G[i] - sm.G[jj]);
-          v = kScale * accQ[cb][r] * dec;
-          if (i > jj) x = -sm.B[i] * accA[cb][r] * dec;
+        {  // X[i][jj], i = 16w + 4g + r, jj = 16cb + c
+          const int i = 16 * w + 4 * g4 + r, jj = 16 * cb + c16;
+          float x = 0.f;
+          if (cb <= w && i > jj) x = -sm.B[i] * accA[cb][r] * expf(sm.G[i] - sm.G[jj]);
+          sm.X[i * LDF + jj] = x;
         }
-        sm.X[i * LDF + jj] = x;
-        qk[i * CH + jj] = f2bf(v);
+        {  // QK[i][jj], i = 16w + c, jj = 16cb + 4g + r
+          const int i = 16 * w + c16, jj = 16 * cb + 4 * g4 + r;
+          accQ[cb][r] = (cb <= w && i >= jj) ? kScale * accQ[cb][r] * expf(sm.G[i] - sm.G[jj]) : 0.f;
+        }
       }
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      *reinterpret_cast<bf16x8*>(rec + ws::QK + (w * 2 + j) * ws::FRAG + lane * 16) =
+          pack_acc_bf16(accQ[2 * j], accQ[2 * j + 1]);
   }
   __syncthreads();
 
   unit_lower_inv64(sm.X, sm.T, sm.Y, w, lane);
 
-  // W = T diag(beta e^G) K and U = T diag(beta) V for this wave's rows
-  f32x4 accW[8];
+  // W^T = K^T (T diag(beta e^G))^T: its accumulator layout is the k-slot ordered W fragment layout.
+  // U = T diag(beta) V in accumulator layout (the scan kernel's initial vn tiles).
   {
     bf16x8 tbe[2], tb[2];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      const float* trow = &sm.T[(16 * w + (lane & 15)) * LDF + 32 * s + 8 * (lane >> 4)];
+      const float* trow = &sm.T[(16 * w + c16) * LDF + 32 * s + 8 * g4];
       float a[8], b[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int col = 32 * s + 8 * (lane >> 4) + e;
+        const int col = 32 * s + 8 * g4 + e;
         a[e] = trow[e] * sm.B[col];
         b[e] = a[e] * sm.EG[col];
       }
       tb[s] = pack8(a);
       tbe[s] = pack8(b);
     }
+    {
+      f32x4 accW[8];
 #pragma unroll
-    for (int cb = 0; cb < 8; ++cb) {
-      accW[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int cb = 0; cb < 8; ++cb) {
+        accW[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < 2; ++s) accW[cb] = mma(tbe[s], frag(sm.KT, LDT, 16 * cb, 32 * s, lane), accW[cb]);
+        for (int s = 0; s < 2; ++s) accW[cb] = mma(frag(sm.KT, LDT, 16 * cb, 32 * s, lane), tbe[s], accW[cb]);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        *reinterpret_cast<bf16x8*>(rec + ws::WN + (w * 4 + j) * ws::FRAG + lane * 16) =
+            pack_acc_bf16(-accW[2 * j], -accW[2 * j + 1]);
     }
     // V^T into the X buffer (dead after the inverse; V^T is 1 KiB larger and runs into T, whose
-    // reads all finished above -- hence the barrier); U tiles go straight to the workspace in
-    // accumulator layout
+    // reads all finished above -- hence the barrier)
     static_assert(pf::D * pf::LDT * 2 <= 2 * pf::CH * pf::LDF * 4, "V^T must fit in X and T");
     uint16_t* VT = reinterpret_cast<uint16_t*>(sm.X);
     __syncthreads();
     store_transposed4(VT, LDT, vreg, t >> 4, 8 * (t & 15));
     __syncthreads();
-    f32x4* ur = reinterpret_cast<f32x4*>(rec + ws::U);
+    f32x4 u[8];
+    float m = 0.f;
 #pragma unroll
     for (int cb = 0; cb < 8; ++cb) {
-      f32x4 u = {0.f, 0.f, 0.f, 0.f};
+      u[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < 2; ++s) u = mma(tb[s], frag(VT, LDT, 16 * cb, 32 * s, lane), u);
-      ur[(cb * 4 + w) * 64 + lane] = u;
+      for (int s = 0; s < 2; ++s) u[cb] = mma(tb[s], frag(VT, LDT, 16 * cb, 32 * s, lane), u[cb]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) m = fmaxf(m, fabsf(u[cb][r]));
     }
-  }
-  // stage W in LDS (the K buffer is free after the K K^T products) and store it coalesced
+    const int ue = fp16_fit_exp(wave_max(m));
+    const float us = ldexpf(1.0f, ue);
+    if (lane == 0) reinterpret_cast<float*>(rec + ws::USC)[w] = ldexpf(1.0f, -ue);
+    typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 #pragma unroll
-  for (int cb = 0; cb < 8; ++cb)
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      sm.a.W[(16 * w + 4 * (lane >> 4) + r) * LDK + 16 * cb + (lane & 15)] = f2bf(accW[cb][r]);
-  __syncthreads();
-  {
-    uint16_t* wd = reinterpret_cast<uint16_t*>(rec + ws::W);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int idx = t + NT * i;  // 1024 pieces of 16 bytes
-      const int row = idx >> 4, pc = idx & 15;
-      *reinterpret_cast<u16x8*>(wd + row * D + 8 * pc) = *reinterpret_cast<const u16x8*>(&sm.a.W[row * LDK + 8 * pc]);
+    for (int cb = 0; cb < 8; ++cb) {
+      const f16x4 hv = {(_Float16)(u[cb][0] * us), (_Float16)(u[cb][1] * us), (_Float16)(u[cb][2] * us),
+                        (_Float16)(u[cb][3] * us)};
+      *reinterpret_cast<f16x4*>(rec + ws::U + ((cb * 64 + lane) * 4 + w) * 8) = hv;
     }
   }
 }
 
 // ============================================================================================
-// Chunked prefill, part 2: the inter-chunk state recurrence.
+// Chunked prefill, part 2: the inter-chunk state recurrence (the scan).
 // ============================================================================================
-// One workgroup = 4 waves = 64 state columns of one (sequence, value head); wave w owns columns
-// 16w..16w+15 over all 128 rows and all 64 tokens of a chunk, so the dependent chain
-//   U = Tb V,  vn = U - W S,  o = Qg S + QK vn,  S' = GL S + K^T (DEC vn)
-// never waits for another wave: the per-chunk operands shared by the 4 waves (Qg, W, Tb, QK, K^T,
-// V^T) are staged in LDS once per chunk, and the only layout changes inside the chain (S and vn
-// from accumulator layout to B-operand layout) go through wave-private LDS.
-struct StateSmem {
-  uint16_t Qg[pf::CH * pf::LDK];       // scale e^G q (token, feature)
-  uint16_t W[pf::CH * pf::LDK];        // (token, feature)
-  uint16_t QK[pf::CH * pf::LDT];       // (token, token)
-  uint16_t KT[pf::D * pf::LDT];        // (feature, token)
-  uint16_t ST[4][16 * pf::LDK];        // per wave: bf16 S^T (column, feature)
-  uint16_t VN[4][3][16 * pf::LDT];     // per wave: vn, hi(dec vn), lo(dec vn) transposed (column, token)
-  float DEC[pf::CH];
-  float GL;
+// One workgroup per (sequence, value head, 16-column slice of the state): 8 workgroups per head,
+// so a single long sequence still spreads over nseq * Hv * 8 workgroups.  The 4 waves specialise:
+//   wave 0 (chain):  vn = U - W S  and  S' = GL S + K^T (DEC vn); the fp32 state slice S [128, 16]
+//                    lives in 8 accumulator tiles for the whole sequence, and both products take
+//                    their B operand straight from accumulator registers (k-slot order)
+//   wave 1 (output): o = Qg S + QK vn one chunk behind the chain, from the S and vn the chain
+//                    published in LDS and Qg / QK fragments it loads itself two chunks ahead
+//   waves 2-3:       stage each chunk's WN and KT fragments, this slice's U tiles and the header
+//                    (34.5 KiB) in a 3-slot LDS ring, loading them from global memory two chunks
+//                    before they are staged
+// One barrier per chunk.  During step c the chain computes chunk c from registers it read out of
+// ring slot c%3 during step c-1, reads chunk c+1 from slot (c+1)%3 into registers, and writes
+// vn(c) and S(c+1) into exchange slots c%3 and (c+1)%3; the output wave reads exchange slot (c-1)%3;
+// the loaders fill ring slot (c+2)%3.  So no LDS read latency sits on the chain's critical path.
+// The state update runs on fp16 MFMA.  Usually DEC vn and K^T fit fp16 as they are (see the fast
+// path); otherwise DEC vn is scaled per column by a power of two sigma into [2^14, 2^15) and K^T
+// by kappa, and the product is folded in as S' = (GL sigma kappa S + P) / (sigma kappa), so the fp32
+// state only ever sees exact power-of-two rescaling besides the MFMA sum.
+namespace rg {  // one ring slot
+constexpr int WN = 0, KT = 16 * ws::FRAG, U = 32 * ws::FRAG, HDR = U + 2048, BYTES = HDR + 512;
+}  // namespace rg
+__device__ __forceinline__ bf16x8 lds_frag(const uint8_t* base, int f, int lane) {
+  return *reinterpret_cast<const bf16x8*>(base + f * ws::FRAG + lane * 16);
+}
+__device__ __forceinline__ f16x8 lds_frag_h(const uint8_t* base, int f, int lane) {
+  return *reinterpret_cast<const f16x8*>(base + f * ws::FRAG + lane * 16);
+}
+struct ScanSmem {
+  uint8_t ring[3][rg::BYTES];
+  uint8_t xch[3][6 * ws::FRAG];  // S (4 k-slot ordered bf16 B fragments) and vn (2)
 };
 
-struct StateStage {  // one chunk's inputs, prefetched into registers
-  u16x8 qg[4], kt[4], w[4], qk[2];
-  f32x4 u[4];  // this wave's U tiles (accumulator layout), one per token block
-  float dec, gl;
+// One chunk's chain operands in registers.
+struct ChainIn {
+  bf16x8 fw[16];  // WN fragments
+  f16x8 fk[16];   // KT fragments
+  f16x8 u[2];     // this lane's U values (tiles 0,1 | 2,3)
+  f32x4 dv[4];    // DEC of this lane's tokens
+  f32x4 usc;
+  float gl, ksc, kap;
 };
+__device__ __forceinline__ void chain_read_w(ChainIn& in, const uint8_t* ring, int lane) {
+  const int g4 = lane >> 4;
+#pragma unroll
+  for (int f = 0; f < 16; ++f) in.fw[f] = lds_frag(ring + rg::WN, f, lane);
+  const float* hdr = reinterpret_cast<const float*>(ring + rg::HDR);
+  in.usc = *reinterpret_cast<const f32x4*>(hdr + (ws::USC - ws::HDR) / 4);
+  in.gl = hdr[(ws::GL - ws::HDR) / 4];
+  in.ksc = hdr[(ws::KSC - ws::HDR) / 4];
+  in.kap = hdr[(ws::KAP - ws::HDR) / 4];
+  in.u[0] = *reinterpret_cast<const f16x8*>(ring + rg::U + lane * 32);
+  in.u[1] = *reinterpret_cast<const f16x8*>(ring + rg::U + lane * 32 + 16);
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) in.dv[tb] = *reinterpret_cast<const f32x4*>(hdr + 16 * tb + 4 * g4);
+}
+__device__ __forceinline__ void chain_read_k(ChainIn& in, const uint8_t* ring, int lane) {
+#pragma unroll
+  for (int f = 0; f < 16; ++f) in.fk[f] = lds_frag_h(ring + rg::KT, f, lane);
+}
+constexpr int kFragPieces = 2 * 16 * ws::FRAG / 16 / 128;  // WN + KT pieces of 16 bytes per loader lane
+constexpr int kLoadPieces = kFragPieces + 2;               // + one piece of U, + one of the header (lanes < 32)
 
-__device__ __forceinline__ void state_prefetch(StateStage& st, const uint8_t* rec, int j0, int t) {
-  using namespace pf;
-  const uint16_t* wr = reinterpret_cast<const uint16_t*>(rec + ws::W);
-  const uint16_t* qgr = reinterpret_cast<const uint16_t*>(rec + ws::QG);
-  const uint16_t* ktr = reinterpret_cast<const uint16_t*>(rec + ws::KT);
+// loader lane lt (0..127): WN/KT pieces lt + 128 i, U piece lt of slice n, header piece lt (< 32)
+__device__ __forceinline__ void scan_load(u16x8 (&r)[kLoadPieces], const uint8_t* rec, int n, int lt) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int idx = t + NT * i;  // 1024 pieces of 16 bytes
-    st.w[i] = *reinterpret_cast<const u16x8*>(wr + (idx >> 4) * D + 8 * (idx & 15));
-    st.qg[i] = *reinterpret_cast<const u16x8*>(qgr + (idx >> 4) * D + 8 * (idx & 15));
-    st.kt[i] = *reinterpret_cast<const u16x8*>(ktr + (idx >> 3) * CH + 8 * (idx & 7));
-  }
-  const uint16_t* qkr = reinterpret_cast<const uint16_t*>(rec + ws::QK);
+  for (int i = 0; i < kFragPieces; ++i) r[i] = *reinterpret_cast<const u16x8*>(rec + ws::WN + (lt + 128 * i) * 16);
+  r[kFragPieces] = *reinterpret_cast<const u16x8*>(rec + ws::U + n * 2048 + lt * 16);
+  if (lt < 32) r[kFragPieces + 1] = *reinterpret_cast<const u16x8*>(rec + ws::HDR + lt * 16);
+}
+__device__ __forceinline__ void scan_store(uint8_t* dst, const u16x8 (&r)[kLoadPieces], int lt) {
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int idx = t + NT * i;  // 512 pieces of 16 bytes
-    st.qk[i] = *reinterpret_cast<const u16x8*>(qkr + (idx >> 3) * CH + 8 * (idx & 7));
-  }
-  const f32x4* ur = reinterpret_cast<const f32x4*>(rec + ws::U) + (j0 >> 4) * 4 * 64 + (t & 63);
-#pragma unroll
-  for (int tb = 0; tb < 4; ++tb) st.u[tb] = ur[tb * 64];
-  st.dec = reinterpret_cast<const float*>(rec + ws::DEC)[t & 63];
-  st.gl = reinterpret_cast<const float*>(rec + ws::GL)[0];
+  for (int i = 0; i < kFragPieces; ++i) *reinterpret_cast<u16x8*>(dst + rg::WN + (lt + 128 * i) * 16) = r[i];
+  *reinterpret_cast<u16x8*>(dst + rg::U + lt * 16) = r[kFragPieces];
+  if (lt < 32) *reinterpret_cast<u16x8*>(dst + rg::HDR + lt * 16) = r[kFragPieces + 1];
 }
 
-__device__ __forceinline__ void state_commit(StateSmem& sm, const StateStage& st, int t) {
+// The output wave's per-chunk operands: QG (16 fragments) and the 6 non-zero QK fragments.
+struct OutFrags {
+  bf16x8 qg[16], qk[6];
+};
+__device__ __forceinline__ void out_load(OutFrags& f, const uint8_t* rec, int lane) {
+  const uint8_t* qg = rec + ws::QG + lane * 16;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) f.qg[i] = *reinterpret_cast<const bf16x8*>(qg + i * ws::FRAG);
+  const uint8_t* qk = rec + ws::QK + lane * 16;
+  const int idx[6] = {0, 2, 4, 5, 6, 7};  // (tb, j) with j <= tb / 2: (0,0) (1,0) (2,0) (2,1) (3,0) (3,1)
+#pragma unroll
+  for (int i = 0; i < 6; ++i) f.qk[i] = *reinterpret_cast<const bf16x8*>(qk + idx[i] * ws::FRAG);
+}
+template <typename OutT>
+__device__ __forceinline__ void out_step(const OutFrags& f, const uint8_t* xch, OutT* out, int64_t t0, int len,
+                                         int Hv, int h, int col, int lane) {
   using namespace pf;
+  bf16x8 sb[4], vb[2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int idx = t + NT * i;
-    *reinterpret_cast<u16x8*>(&sm.W[(idx >> 4) * LDK + 8 * (idx & 15)]) = st.w[i];
-    *reinterpret_cast<u16x8*>(&sm.Qg[(idx >> 4) * LDK + 8 * (idx & 15)]) = st.qg[i];
-    *reinterpret_cast<u16x8*>(&sm.KT[(idx >> 3) * LDT + 8 * (idx & 7)]) = st.kt[i];
-  }
+  for (int j = 0; j < 4; ++j) sb[j] = lds_frag(xch, j, lane);
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int idx = t + NT * i;
-    *reinterpret_cast<u16x8*>(&sm.QK[(idx >> 3) * LDT + 8 * (idx & 7)]) = st.qk[i];
+  for (int j = 0; j < 2; ++j) vb[j] = lds_frag(xch, 4 + j, lane);
+  f32x4 O[4];
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) {
+    O[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) O[tb] = mma(f.qg[tb * 4 + j], sb[j], O[tb]);
   }
-  if (t < 64) sm.DEC[t] = st.dec;
-  if (t == 0) sm.GL = st.gl;
+  O[0] = mma(f.qk[0], vb[0], O[0]);
+  O[1] = mma(f.qk[1], vb[0], O[1]);
+  O[2] = mma(f.qk[2], vb[0], O[2]);
+  O[2] = mma(f.qk[3], vb[1], O[2]);
+  O[3] = mma(f.qk[4], vb[0], O[3]);
+  O[3] = mma(f.qk[5], vb[1], O[3]);
+  const int g4 = lane >> 4;
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * tb + 4 * g4 + r;
+      if (row < len) Elem<OutT>::store(out + ((t0 + row) * Hv + h) * D + col, O[tb][r]);
+    }
 }
 
 template <typename OutT>
-__global__ __launch_bounds__(pf::NT, 1) void chunk_state_kernel(
-    const float* __restrict__ init, float* __restrict__ final_state,
-    OutT* __restrict__ out, const int32_t* __restrict__ cu, const int32_t* __restrict__ seq_chunk0, int seq_len,
-    int Hv, const uint8_t* __restrict__ work) {
+__global__ __launch_bounds__(pf::NT, 1) void chunk_scan_kernel(
+    const float* __restrict__ init, float* __restrict__ final_state, OutT* __restrict__ out,
+    const int32_t* __restrict__ cu, const int32_t* __restrict__ seq_chunk0, int nseq, int seq_len, int Hv,
+    const uint8_t* __restrict__ work) {
   using namespace pf;
-  __shared__ StateSmem sm;
-  const int t = threadIdx.x, w = t >> 6, lane = t & 63, g4 = lane >> 4, c16 = lane & 15;
-  const int ntile = D / 64;
-  const int vt = blockIdx.x % ntile;
-  const int h = (blockIdx.x / ntile) % Hv, seq = blockIdx.x / ntile / Hv;
-  const int vcol0 = 64 * vt, j0 = vcol0 + 16 * w;
+  __shared__ ScanSmem sm;
+  // block -> (sequence-head pair, slice); the 8 slices of a pair share blockIdx % 8 and therefore an
+  // XCD (workgroups are dispatched round-robin over the 8 XCDs), so they share one L2.
+  const int b = blockIdx.x;
+  const int pair = (b >> 6) * 8 + (b & 7), n = (b >> 3) & 7;
+  if (pair >= nseq * Hv) return;
+  const int h = pair % Hv, seq = pair / Hv;
+  const int t = threadIdx.x, lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
+  const int role = __builtin_amdgcn_readfirstlane(t >> 6);
   int64_t s0;
   int L, slot0;
   if (cu) {
@@ -564,148 +712,171 @@ __global__ __launch_bounds__(pf::NT, 1) void chunk_state_kernel(
     slot0 = seq * ((seq_len + CH - 1) / CH);
   }
   const int nch = (L + CH - 1) / CH;
-  const int64_t sbase = ((int64_t)seq * Hv + h) * D * D + j0;
-  uint16_t* myST = sm.ST[w];
-  uint16_t* myVN = sm.VN[w][0];
-  uint16_t* myVSH = sm.VN[w][1];
-  uint16_t* myVSL = sm.VN[w][2];
+  const int64_t rstride = (int64_t)Hv * ws::BYTES;
+  const uint8_t* rec0 = work + (int64_t)slot0 * rstride + (int64_t)h * ws::BYTES;
+  const int col = 16 * n + c16;
 
-  // S[:, j0..j0+15] as 8 row blocks in accumulator layout: S[rb][r] = S[16rb + 4g + r][j0 + c]
-  f32x4 S[8];
+  if (role == 0) {
+    // ---------------- chain wave ----------------
+    const int64_t sbase = ((int64_t)seq * Hv + h) * D * D + col;
+    f32x4 S[8];
 #pragma unroll
-  for (int rb = 0; rb < 8; ++rb) {
+    for (int rb = 0; rb < 8; ++rb)
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      S[rb][r] = init ? init[sbase + (int64_t)(16 * rb + 4 * g4 + r) * D + c16] : 0.f;
-    const u16x4 pk = {f2bf(S[rb][0]), f2bf(S[rb][1]), f2bf(S[rb][2]), f2bf(S[rb][3])};
-    *reinterpret_cast<u16x4*>(&myST[c16 * LDK + 16 * rb + 4 * g4]) = pk;
-  }
-
-  StateStage st;
-  const uint8_t* rec0 = work + (int64_t)slot0 * Hv * ws::BYTES + (int64_t)h * ws::BYTES;
-  if (nch > 0) state_prefetch(st, rec0, j0, t);
-
-  for (int c = 0; c < nch; ++c) {
-    const int len = L - c * CH < CH ? L - c * CH : CH;
-    const int64_t t0 = s0 + (int64_t)c * CH;
-    state_commit(sm, st, t);
-    f32x4 U[4];
+      for (int r = 0; r < 4; ++r) S[rb][r] = init ? init[sbase + (int64_t)(16 * rb + 4 * g4 + r) * D] : 0.f;
+    bf16x8 Sb[4];
 #pragma unroll
-    for (int tb = 0; tb < 4; ++tb) U[tb] = st.u[tb];
-    __syncthreads();
-
-    // vn = U - W S for all 4 token blocks of the chunk.  Each phase loads all of its LDS fragments
-    // first and then issues its MFMAs (sched_barrier keeps the compiler from re-interleaving them
-    // into one-load-one-wait pairs).
-    bf16x8 fs[4];  // S^T fragments (B operand of W S and Qg S), reused by the output products
-    {
-      bf16x8 fw[4][4];
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        fs[s] = frag(myST, LDK, 0, 32 * s, lane);
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb) fw[s][tb] = frag_neg(sm.W, LDK, 16 * tb, 32 * s, lane);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb) U[tb] = mma(fw[s][tb], fs[s], U[tb]);
+    for (int j = 0; j < 4; ++j) {
+      Sb[j] = pack_acc_bf16(S[2 * j], S[2 * j + 1]);
+      *reinterpret_cast<bf16x8*>(&sm.xch[0][j * ws::FRAG + lane * 16]) = Sb[j];
     }
-    // publish vn (bf16) and dec*vn = hi + lo, transposed (column, token), wave-private
-#pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
-      const int s0r = 16 * tb + 4 * g4;
-      u16x4 vo, vh, vl;
+    __syncthreads();  // prologue
+    ChainIn in;
+    if (nch > 0) {
+      chain_read_w(in, sm.ring[0], lane);
+      chain_read_k(in, sm.ring[0], lane);
+    }
+    int x0 = 0;  // c % 3
+    for (int c = 0; c < nch; ++c) {
+      uint8_t* xch = sm.xch[x0];
+      const int x1 = x0 == 2 ? 0 : x0 + 1;
+      const uint8_t* nxt = sm.ring[x1];  // chunk c+1 sits in ring slot (c+1) % 3
+      f32x4 vn[4], dv[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float vn = U[tb][r];
-        const float vsc = vn * sm.DEC[s0r + r];
-        vo[r] = f2bf(vn);
-        vh[r] = f2bf(vsc);
-        vl[r] = f2bf(vsc - bf2f(vh[r]));
+        vn[0][r] = (float)in.u[0][r];
+        vn[1][r] = (float)in.u[0][4 + r];
+        vn[2][r] = (float)in.u[1][r];
+        vn[3][r] = (float)in.u[1][4 + r];
       }
-      *reinterpret_cast<u16x4*>(&myVN[c16 * LDT + s0r]) = vo;
-      *reinterpret_cast<u16x4*>(&myVSH[c16 * LDT + s0r]) = vh;
-      *reinterpret_cast<u16x4*>(&myVSL[c16 * LDT + s0r]) = vl;
-    }
-    __builtin_amdgcn_wave_barrier();
-
-    // o = Qg S + QK vn
-    {
-      bf16x8 fq[4][4], fk[2][4], fn[2];
+      {  // the tile scales are 1 unless |U| left [2^-4, 2^14) (same value in every lane)
+        const bool unit = in.usc[0] == 1.0f && in.usc[1] == 1.0f && in.usc[2] == 1.0f && in.usc[3] == 1.0f;
+        if (!__builtin_amdgcn_readfirstlane((int)unit)) {
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb) fq[s][tb] = frag(sm.Qg, LDK, 16 * tb, 32 * s, lane);
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        fn[s] = frag(myVN, LDT, 0, 32 * s, lane);
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb)
-          if (s == 0 || tb >= 2) fk[s][tb] = frag(sm.QK, LDT, 16 * tb, 32 * s, lane);
+          for (int tb = 0; tb < 4; ++tb) vn[tb] *= in.usc[tb];
+        }
       }
-      __builtin_amdgcn_sched_barrier(0);
-      f32x4 O[4];
 #pragma unroll
-      for (int tb = 0; tb < 4; ++tb) O[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
+        for (int tb = 0; tb < 4; ++tb) vn[tb] = mma(in.fw[tb * 4 + j], Sb[j], vn[tb]);
 #pragma unroll
-        for (int tb = 0; tb < 4; ++tb) O[tb] = mma(fq[s][tb], fs[s], O[tb]);
-#pragma unroll
-      for (int s = 0; s < 2; ++s)
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb)
-          if (s == 0 || tb >= 2) O[tb] = mma(fk[s][tb], fn[s], O[tb]);
+      for (int tb = 0; tb < 4; ++tb) dv[tb] = in.dv[tb];
+      const float gl = in.gl, ksc = in.ksc, kap = in.kap;
+      if (c + 1 < nch) chain_read_w(in, nxt, lane);
+      // publish vn (bf16, for the output wave); DEC vn -> fp16
+      float m = 0.f;
 #pragma unroll
       for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int row = 16 * tb + 4 * g4 + r;
-          if (row < len) Elem<OutT>::store(out + ((t0 + row) * Hv + h) * D + j0 + c16, O[tb][r]);
+          dv[tb][r] *= vn[tb][r];
+          m = fmaxf(m, fabsf(dv[tb][r]));
         }
-    }
-
-    // next chunk's operands: issued here so their registers are not live during the products above
-    if (c + 1 < nch) {
-      state_prefetch(st, rec0 + (int64_t)(c + 1) * Hv * ws::BYTES, j0, t);
-    }
-    // S' = GL S + K^T (hi + lo), then its bf16 transpose for the next chunk
-    {
-      const float gl = sm.GL;
-      bf16x8 fa[8][2], fh[2], fl[2];
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        fh[s] = frag(myVSH, LDT, 0, 32 * s, lane);
-        fl[s] = frag(myVSL, LDT, 0, 32 * s, lane);
+      for (int j = 0; j < 2; ++j)
+        *reinterpret_cast<bf16x8*>(&xch[(4 + j) * ws::FRAG + lane * 16]) = pack_acc_bf16(vn[2 * j], vn[2 * j + 1]);
+      // Fast path (the usual case): kappa = 1 and every |DEC vn| below 2^14 with the largest at
+      // least 2^-4, so DEC vn goes to fp16 unscaled.  Otherwise: per-column power-of-two scaling.
+      const bool fast = kap == 1.0f && __builtin_amdgcn_ballot_w64(m >= 16384.0f) == 0 &&
+                        __builtin_amdgcn_ballot_w64(m >= 0.0625f) != 0;
+      if (__builtin_amdgcn_readfirstlane((int)fast)) {
+        f16x8 vh[2];
 #pragma unroll
-        for (int rb = 0; rb < 8; ++rb) fa[rb][s] = frag(sm.KT, LDT, 16 * rb, 32 * s, lane);
+        for (int j = 0; j < 2; ++j) vh[j] = pack_acc_f16(dv[2 * j], dv[2 * j + 1], 1.0f);
+#pragma unroll
+        for (int rb = 0; rb < 8; ++rb) {
+          S[rb] *= gl;
+          S[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(in.fk[rb * 2], vh[0], S[rb], 0, 0, 0);
+          S[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(in.fk[rb * 2 + 1], vh[1], S[rb], 0, 0, 0);
+        }
+      } else {
+        m = fmaxf(m, __shfl_xor(m, 16, kWave));
+        m = fmaxf(m, __shfl_xor(m, 32, kWave));
+        const int se = fp16_scale_exp(m);
+        f16x8 vh[2];
+        const float sigma = ldexpf(1.0f, se);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) vh[j] = pack_acc_f16(dv[2 * j], dv[2 * j + 1], sigma);
+        const float pre = gl * sigma * kap;  // GL * sigma * kappa (exact powers of two)
+        const float post = ldexpf(ksc, -se); // 1 / (sigma * kappa)
+#pragma unroll
+        for (int rb = 0; rb < 8; ++rb) {
+          S[rb] *= pre;
+          S[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(in.fk[rb * 2], vh[0], S[rb], 0, 0, 0);
+          S[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(in.fk[rb * 2 + 1], vh[1], S[rb], 0, 0, 0);
+          S[rb] *= post;
+        }
       }
-      __builtin_amdgcn_sched_barrier(0);
+      if (c + 1 < nch) chain_read_k(in, nxt, lane);
+      uint8_t* xn = sm.xch[x1];
 #pragma unroll
-      for (int rb = 0; rb < 8; ++rb) {
-        S[rb] *= gl;
-        S[rb] = mma(fa[rb][0], fh[0], S[rb]);
-        S[rb] = mma(fa[rb][0], fl[0], S[rb]);
-        S[rb] = mma(fa[rb][1], fh[1], S[rb]);
-        S[rb] = mma(fa[rb][1], fl[1], S[rb]);
+      for (int j = 0; j < 4; ++j) {
+        Sb[j] = pack_acc_bf16(S[2 * j], S[2 * j + 1]);
+        *reinterpret_cast<bf16x8*>(&xn[j * ws::FRAG + lane * 16]) = Sb[j];
       }
-      __builtin_amdgcn_wave_barrier();
+      x0 = x1;
+      __syncthreads();  // end of step c
+    }
+    __syncthreads();  // step nch (the output wave's last chunk)
+    if (final_state) {
 #pragma unroll
-      for (int rb = 0; rb < 8; ++rb) {
-        const u16x4 pk = {f2bf(S[rb][0]), f2bf(S[rb][1]), f2bf(S[rb][2]), f2bf(S[rb][3])};
-        *reinterpret_cast<u16x4*>(&myST[c16 * LDK + 16 * rb + 4 * g4]) = pk;
+      for (int rb = 0; rb < 8; ++rb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) final_state[sbase + (int64_t)(16 * rb + 4 * g4 + r) * D] = S[rb][r];
+    }
+  } else if (role == 1) {
+    // ---------------- output wave: step c computes chunk c-1 ----------------
+    OutFrags F0, F1;  // even / odd chunks
+    if (nch > 0) out_load(F0, rec0, lane);
+    __syncthreads();  // prologue
+    if (nch > 1) out_load(F1, rec0 + rstride, lane);
+    __syncthreads();  // step 0
+    int xp = 0;       // (c - 1) % 3
+    for (int c = 1; c <= nch; c += 2) {
+      {
+        const int cc = c - 1;  // even
+        const int len = L - cc * CH < CH ? L - cc * CH : CH;
+        out_step<OutT>(F0, sm.xch[xp], out, s0 + (int64_t)cc * CH, len, Hv, h, col, lane);
+        if (c + 1 < nch) out_load(F0, rec0 + (int64_t)(c + 1) * rstride, lane);
+        xp = xp == 2 ? 0 : xp + 1;
+        __syncthreads();  // end of step c
+      }
+      if (c + 1 <= nch) {
+        const int cc = c;  // odd
+        const int len = L - cc * CH < CH ? L - cc * CH : CH;
+        out_step<OutT>(F1, sm.xch[xp], out, s0 + (int64_t)cc * CH, len, Hv, h, col, lane);
+        if (c + 2 < nch) out_load(F1, rec0 + (int64_t)(c + 2) * rstride, lane);
+        xp = xp == 2 ? 0 : xp + 1;
+        __syncthreads();  // end of step c+1
       }
     }
-    __syncthreads();  // shared chunk operands are overwritten by the next commit
-  }
-
-  if (final_state) {
-#pragma unroll
-    for (int rb = 0; rb < 8; ++rb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) final_state[sbase + (int64_t)(16 * rb + 4 * g4 + r) * D + c16] = S[rb][r];
+  } else {
+    // ---------------- loader waves ----------------
+    const int lt = t - 128;
+    u16x8 R0[kLoadPieces], R1[kLoadPieces];  // even / odd chunks
+    if (nch > 0) scan_load(R0, rec0, n, lt);
+    if (nch > 1) scan_load(R1, rec0 + rstride, n, lt);
+    if (nch > 0) scan_store(sm.ring[0], R0, lt);
+    if (nch > 1) scan_store(sm.ring[1], R1, lt);
+    if (nch > 2) scan_load(R0, rec0 + 2 * rstride, n, lt);
+    if (nch > 3) scan_load(R1, rec0 + 3 * rstride, n, lt);
+    __syncthreads();  // prologue
+    // step c: stage chunk c+2 (held in R[c&1]) into ring slot (c+2)%3, then load chunk c+4
+    int slot = 2;  // (c + 2) % 3
+    for (int c = 0; c < nch; c += 2) {
+      if (c + 2 < nch) scan_store(sm.ring[slot], R0, lt);
+      if (c + 4 < nch) scan_load(R0, rec0 + (int64_t)(c + 4) * rstride, n, lt);
+      slot = slot == 2 ? 0 : slot + 1;
+      __syncthreads();  // end of step c
+      if (c + 1 < nch) {
+        if (c + 3 < nch) scan_store(sm.ring[slot], R1, lt);
+        if (c + 5 < nch) scan_load(R1, rec0 + (int64_t)(c + 5) * rstride, n, lt);
+        slot = slot == 2 ? 0 : slot + 1;
+        __syncthreads();  // end of step c+1
+      }
+    }
+    __syncthreads();  // step nch
   }
 }
 
@@ -849,7 +1020,8 @@ extern "C" int gdn_chunk_prefill(const void* q, int64_t q_stride, const void* k,
                                     workspace_bytes >= gdn_chunk_prefill_workspace_bytes(total_chunks, Hv)),
               "gdn_chunk_prefill: workspace missing, misaligned or smaller than %lld bytes",
               (long long)gdn_chunk_prefill_workspace_bytes(total_chunks, Hv));
-  GDN_REQUIRE(total_chunks < (1ll << 31) && (int64_t)nseq * Hv * 2 < (1ll << 31), "gdn_chunk_prefill: grid too large");
+  GDN_REQUIRE(total_chunks < (1ll << 31) && ((int64_t)nseq * Hv + 7) / 8 * 64 < (1ll << 31),
+              "gdn_chunk_prefill: grid too large");
   if (nseq == 0) return GDN_OK;
   hipStream_t s = (hipStream_t)stream;
   uint8_t* work = (uint8_t*)workspace;
@@ -868,8 +1040,10 @@ extern "C" int gdn_chunk_prefill(const void* q, int64_t q_stride, const void* k,
     int rc = check_launch("gdn_chunk_prefill(local)");
     if (rc) return rc;
   }
-  chunk_state_kernel<uint16_t><<<(unsigned)(nseq * Hv * (pf::D / 64)), pf::NT, 0, s>>>(
-      initial_state, final_state, (uint16_t*)out, cu_seqlens, seq_chunk0, seq_len, Hv, work);
+  const int64_t pairs = (int64_t)nseq * Hv;
+  const int64_t scan_blocks = (pairs + 7) / 8 * 64;
+  chunk_scan_kernel<uint16_t><<<(unsigned)scan_blocks, pf::NT, 0, s>>>(
+      initial_state, final_state, (uint16_t*)out, cu_seqlens, seq_chunk0, nseq, seq_len, Hv, work);
   return check_launch("gdn_chunk_prefill(state)");
 }
 
