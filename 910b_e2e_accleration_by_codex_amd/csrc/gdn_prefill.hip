@@ -31,7 +31,6 @@ constexpr int D = 128;          // head dim
 constexpr int CH = 64;          // chunk length
 constexpr int NT = 256;         // threads per workgroup (4 waves)
 constexpr int LDK = D + 8;      // row pitch (bf16) of [*, 128] tiles
-constexpr int LDT = CH + 8;     // row pitch (bf16) of [*, 64] tiles
 constexpr int LDF = CH + 4;     // row pitch (fp32) of [64, 64] matrices
 constexpr float kScale = 0.08838834764831845f;  // (float)(1 / sqrt(128))
 }  // namespace pf
@@ -85,33 +84,36 @@ __device__ __forceinline__ void st16_f32(float* M, int ld, f32x4 acc, int lane) 
 // reference's 16-step row recurrence: six dependent products instead of sixteen dependent steps;
 // with |X_ij| <= 1 (l2-normalised k, beta <= 1, decay <= 1) the powers of a 16x16 block stay far
 // from fp32 overflow (the reference avoids powers of the whole 64x64 block, which can overflow).
-// All 4 waves must call it (it holds barriers).  sY: 4 x 16 x 16 fp32 scratch.  Writes all of sT
-// (upper blocks zero).
-__device__ void unit_lower_inv64(const float* sX, float* sT, float* sY, int w, int lane) {
+// All 4 waves must call it (it holds barriers).  Its four 16x16 scratch blocks live in the upper
+// blocks (0,1) (0,2) (0,3) (1,2) of sX, which the inverse never reads.  Writes all of sT (upper
+// blocks zero).
+__device__ __forceinline__ float* inv_scratch(float* sX, int k) {
+  return sX + (k == 3 ? 16 * pf::LDF + 32 : 16 * (k + 1));
+}
+__device__ void unit_lower_inv64(float* sX, float* sT, int w, int lane) {
   using namespace pf;
   {  // diagonal block w: T = (I+X)(I+X^2)(I+X^4)(I+X^8) (X^16 = 0), six fp32 MFMA products
     const int c = lane & 15, g = lane >> 4;
     const float* Xb = sX + 16 * w * LDF + 16 * w;
     float* Tb = sT + 16 * w * LDF + 16 * w;
-    float* P = sY + w * 256;  // wave-private 16x16 scratch (pitch 16)
+    float* P = inv_scratch(sX, w);  // wave-private 16x16 scratch
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = 4 * g + r;
       Tb[i * LDF + c] = Xb[i * LDF + c] + (i == c ? 1.0f : 0.0f);
     }
     const float* Pin = Xb;
-    int ldp = LDF;
+    const int ldp = LDF;
 #pragma unroll
     for (int step = 0; step < 3; ++step) {
       f32x4 p2 = mm16_f32(Pin, ldp, Pin, ldp, f32x4{0.f, 0.f, 0.f, 0.f}, lane);  // X^(2^(step+1))
-      st16_f32(P, 16, p2, lane);
+      st16_f32(P, LDF, p2, lane);
       __builtin_amdgcn_wave_barrier();
-      f32x4 tp = mm16_f32(Tb, LDF, P, 16, f32x4{0.f, 0.f, 0.f, 0.f}, lane);     // T X^(2^(step+1))
+      f32x4 tp = mm16_f32(Tb, LDF, P, LDF, f32x4{0.f, 0.f, 0.f, 0.f}, lane);    // T X^(2^(step+1))
 #pragma unroll
       for (int r = 0; r < 4; ++r) Tb[(4 * g + r) * LDF + c] += tp[r];
       __builtin_amdgcn_wave_barrier();
       Pin = P;
-      ldp = 16;
     }
     float* Trow = sT + 16 * w * LDF;
     for (int col = 16 * (w + 1) + c; col < CH; col += 16)
@@ -120,18 +122,18 @@ __device__ void unit_lower_inv64(const float* sX, float* sT, float* sY, int w, i
   }
   __syncthreads();
   // level 1: T10 = T11 (X10 T00), T32 = T33 (X32 T22)
-  float* Y = sY + w * 256;
+  float* Y = inv_scratch(sX, w);
   if (w < 2) {
     const int b0 = 32 * w;  // block row/col offsets: rows b0+16.., cols b0..
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     acc = mm16_f32(sX + (b0 + 16) * LDF + b0, LDF, sT + b0 * LDF + b0, LDF, acc, lane);
-    st16_f32(Y, 16, acc, lane);
+    st16_f32(Y, LDF, acc, lane);
   }
   __syncthreads();
   if (w < 2) {
     const int b0 = 32 * w;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    acc = mm16_f32(sT + (b0 + 16) * LDF + b0 + 16, LDF, Y, 16, acc, lane);
+    acc = mm16_f32(sT + (b0 + 16) * LDF + b0 + 16, LDF, Y, LDF, acc, lane);
     st16_f32(sT + (b0 + 16) * LDF + b0, LDF, acc, lane);
   }
   __syncthreads();
@@ -141,16 +143,16 @@ __device__ void unit_lower_inv64(const float* sX, float* sT, float* sY, int w, i
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     if (jb == 0) acc = mm16_f32(sX + 16 * ib * LDF + 0, LDF, sT + 0 * LDF + 0, LDF, acc, lane);
     acc = mm16_f32(sX + 16 * ib * LDF + 16, LDF, sT + 16 * LDF + 16 * jb, LDF, acc, lane);
-    st16_f32(Y, 16, acc, lane);
+    st16_f32(Y, LDF, acc, lane);
   }
   __syncthreads();
   {  // T20 = T22 Y20, T30 = T32 Y20 + T33 Y30, T21 = T22 Y21, T31 = T32 Y21 + T33 Y31
     const int ib = 2 + (w & 1), jb = w >> 1;
-    const float* Ya = sY + (2 * jb) * 256;      // Y2jb
-    const float* Yb = sY + (2 * jb + 1) * 256;  // Y3jb
+    const float* Ya = inv_scratch(sX, 2 * jb);      // Y2jb
+    const float* Yb = inv_scratch(sX, 2 * jb + 1);  // Y3jb
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    acc = mm16_f32(sT + 16 * ib * LDF + 32, LDF, Ya, 16, acc, lane);
-    if (ib == 3) acc = mm16_f32(sT + 48 * LDF + 48, LDF, Yb, 16, acc, lane);
+    acc = mm16_f32(sT + 16 * ib * LDF + 32, LDF, Ya, LDF, acc, lane);
+    if (ib == 3) acc = mm16_f32(sT + 48 * LDF + 48, LDF, Yb, LDF, acc, lane);
     st16_f32(sT + 16 * ib * LDF + 16 * jb, LDF, acc, lane);
   }
   __syncthreads();
@@ -158,12 +160,12 @@ __device__ void unit_lower_inv64(const float* sX, float* sT, float* sY, int w, i
 
 __global__ __launch_bounds__(pf::NT) void unit_lower_inv_kernel(const float* __restrict__ X, float* __restrict__ T) {
   using namespace pf;
-  __shared__ float sX[CH * LDF], sT[CH * LDF], sY[4 * 256];
+  __shared__ float sX[CH * LDF], sT[CH * LDF];
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const float* Xm = X + (int64_t)blockIdx.x * CH * CH;
   for (int i = t; i < CH * CH; i += NT) sX[(i / CH) * LDF + (i % CH)] = (i / CH) > (i % CH) ? Xm[i] : 0.f;
   __syncthreads();
-  unit_lower_inv64(sX, sT, sY, w, lane);
+  unit_lower_inv64(sX, sT, w, lane);
   float* Tm = T + (int64_t)blockIdx.x * CH * CH;
   for (int i = t; i < CH * CH; i += NT) Tm[i] = sT[(i / CH) * LDF + (i % CH)];
 }
@@ -185,11 +187,15 @@ __global__ __launch_bounds__(pf::NT) void unit_lower_inv_kernel(const float* __r
 //
 //   WN  16 frags [tb 4][j 4]  bf16  M = -W,  W = T diag(beta e^G) K     (tokens x features)
 //   KT  16 frags [rb 8][j 2]  fp16  M = kappa K^T                       (features x tokens)
-//   QG  16 frags [tb 4][j 4]  bf16  M = scale e^{G_t} q_t               (tokens x features)
-//   QK   8 frags [tb 4][j 2]  bf16  M = scale q_i.k_j e^{G_i - G_j}, i >= j, else 0
+//   QG  16 frags [tb 4][j 4]  bf16  M = q (l2-normalised)               (tokens x features)
+//   QK   8 frags [tb 4][j 2]  bf16  M = scale q_i.k_j e^{G_i - G_j}, i >= j, else 0 (the two
+//                                   all-zero fragments (tb, j) = (0, 1), (1, 1) are not written)
+// KT and QG depend on the key head only: they are written into the record of the first value
+// head of each key head (h % (Hv / Hk) == 0) and read from there.
 //   U   fp16 [slice 8][lane 64][tb 4][r 4] = U[16 tb + 4 g + r][16 slice + c] / USC[tb],
 //       U = T diag(beta) V (accumulator layout of each 16-column slice)
-//   DEC [64] fp32 = e^{G_last - G_t};  USC [4] fp32;  GL = e^{G_last};  KSC = 1 / kappa;  KAP = kappa
+//   DEC [64] fp32 = e^{G_last - G_t};  USC [4] fp32;  GL = e^{G_last};  KSC = 1 / kappa;  KAP = kappa;
+//   EGS [64] fp32 = scale e^{G_t} (the output rows' factor for q S)
 // kappa (per chunk, for |K|) and 1 / USC (per token tile, for |U|) are powers of two chosen by
 // fp16_fit_exp: 1 when the largest magnitude already sits in [2^-4, 2^14), else the power that
 // moves it into [2^14, 2^15) -- inside fp16's range with full relative precision either way.
@@ -205,8 +211,9 @@ constexpr int USC = DEC + pf::CH * 4;            // 73984 (16-byte aligned: read
 constexpr int GL = USC + 16;                     // 74000
 constexpr int KSC = GL + 4;                      // 74004
 constexpr int KAP = KSC + 4;                     // 74008
-constexpr int HDR = DEC;                         // DEC, USC, GL, KSC, KAP: one 512-byte header
-constexpr int BYTES = 74240;                     // record size (multiple of 256)
+constexpr int HDR = DEC;                         // DEC, USC, GL, KSC, KAP: the 512 bytes the scan stages
+constexpr int EGS = HDR + 512;                   // 74240
+constexpr int BYTES = EGS + pf::CH * 4;          // 74496 (multiple of 256)
 }  // namespace ws
 
 // Exponent se such that 2^se max|x| lies in [2^14, 2^15) (0 for 0 / non-finite; clamped to +-60).
@@ -288,14 +295,6 @@ __device__ __forceinline__ void l2norm_rows4(u16x8* x) {
     for (int e = 0; e < 8; ++e) x[i][e] = f2bf(bf2f(x[i][e]) * inv);
   }
 }
-// Write 4 rows x 8 features transposed: dst[(f0+e)*ld + 4tq .. +3] = x[0..3][e] (8-byte stores).
-__device__ __forceinline__ void store_transposed4(uint16_t* dst, int ld, const u16x8* x, int tq, int f0) {
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const u16x4 v = {x[0][e], x[1][e], x[2][e], x[3][e]};
-    *reinterpret_cast<u16x4*>(dst + (f0 + e) * ld + 4 * tq) = v;
-  }
-}
 
 // A-fragment of a bf16 [rows, ld] tile in k-slot order (two 8-byte reads; see the workspace notes).
 __device__ __forceinline__ bf16x8 frag_kperm(const uint16_t* base, int ld, int row0, int k0, int lane) {
@@ -303,6 +302,28 @@ __device__ __forceinline__ bf16x8 frag_kperm(const uint16_t* base, int ld, int r
   const u16x4 lo = *reinterpret_cast<const u16x4*>(p), hi = *reinterpret_cast<const u16x4*>(p + 16);
   const u16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   return __builtin_bit_cast(bf16x8, v);
+}
+// ds_read_b64_tr_b16: within each 16-lane group, lane j supplies the address of 4 consecutive
+// 16-bit values L[j][0..3]; lane i receives L[4e + (i >> 2)][i & 3] for e = 0..3.
+__device__ __forceinline__ u16x4 lds_tr16(const uint16_t* p) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p);
+  return __builtin_bit_cast(u16x4, v);
+}
+// Fragment with k along the rows of a row-major [k][m] bf16 tile: lane (c, g) = (l % 16, l / 16)
+// gets M[k0 + 8g + e][m0 + c], e < 8 -- the A operand of M^T or the B operand of M.
+__device__ __forceinline__ u16x8 frag_tr(const uint16_t* base, int ld, int k0, int m0, int lane) {
+  const int j = lane & 15, g = lane >> 4;
+  const uint16_t* p = base + (k0 + 8 * g + (j >> 2)) * ld + m0 + 4 * (j & 3);
+  const u16x4 lo = lds_tr16(p), hi = lds_tr16(p + 4 * ld);
+  return u16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+// The same in k-slot order: element e of lane (c, g) is M[k0 + kpos(8g + e)][m0 + c].
+__device__ __forceinline__ u16x8 frag_tr_kperm(const uint16_t* base, int ld, int k0, int m0, int lane) {
+  const int j = lane & 15, g = lane >> 4;
+  const uint16_t* p = base + (k0 + 4 * g + (j >> 2)) * ld + m0 + 4 * (j & 3);
+  const u16x4 lo = lds_tr16(p), hi = lds_tr16(p + 16 * ld);
+  return u16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 // 8 accumulator values (rows 4g..4g+3 of tiles a and b) -> one k-slot ordered bf16 fragment.
 __device__ __forceinline__ bf16x8 pack_acc_bf16(f32x4 a, f32x4 b) {
@@ -327,17 +348,16 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 
 struct LocalSmem {
-  uint16_t K[pf::CH * pf::LDK];     // K chunk, row-major (token, feature)
-  uint16_t KT[pf::D * pf::LDT];     // K chunk transposed (feature, token)
-  float X[pf::CH * pf::LDF];
+  uint16_t K[pf::CH * pf::LDK];     // K chunk, row-major (token, feature); K^T operands via transpose reads
+  float X[pf::CH * pf::LDF];        // then V, row-major (token, feature), once the inverse is done
   float T[pf::CH * pf::LDF];
-  float Y[4 * 256];
   float G[pf::CH], EG[pf::CH], B[pf::CH];
   float KMX[4];
 };
+static_assert(pf::CH * pf::LDK * 2 <= pf::CH * pf::LDF * 4, "V must fit in the X buffer");
 
 template <typename BetaT>
-__global__ __launch_bounds__(pf::NT, 2) void chunk_local_kernel(
+__global__ __launch_bounds__(pf::NT, 3) void chunk_local_kernel(
     const uint16_t* __restrict__ q, int64_t qs, const uint16_t* __restrict__ k, int64_t ks,
     const uint16_t* __restrict__ v, int64_t vs,
     const float* __restrict__ g, const BetaT* __restrict__ beta, const int32_t* __restrict__ cu,
@@ -350,50 +370,58 @@ __global__ __launch_bounds__(pf::NT, 2) void chunk_local_kernel(
   const int hk = h / (Hv / Hqk);
   const ChunkPos cp = chunk_pos(slot, cu, seq_chunk0, nseq, seq_len);
   uint8_t* rec = work + ((int64_t)slot * Hv + h) * ws::BYTES;
+  const bool kq_owner = h % (Hv / Hqk) == 0;  // writes the key-head fragments KT and QG
 
-  // K: thread (tq, fb) loads rows 4tq.. x features 8fb..; row-major and transposed copies
-  {
-    const int tq = t >> 4, fb = t & 15;
-    u16x8 x[4];
-    load_rows4(x, k + (int64_t)hk * D, ks, cp.t0, cp.len, tq, 8 * fb);
-    if (use_l2) l2norm_rows4(x);
-    float m = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      *reinterpret_cast<u16x8*>(&sm.K[(4 * tq + i) * LDK + 8 * fb]) = x[i];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(bf2f(x[i][e])));
-    }
-    store_transposed4(sm.KT, LDT, x, tq, 8 * fb);
-    m = wave_max(m);
-    if (lane == 0) sm.KMX[w] = m;
-  }
-  // V rows 4tq.. x columns 8fb.. stay in registers until the inverse has freed the X buffer
-  u16x8 vreg[4];
-  load_rows4(vreg, v + (int64_t)h * D, vs, cp.t0, cp.len, t >> 4, 8 * (t & 15));
-  // Q rows 16w + l%16 in k-slot order: block s holds features 32s + 4g.. and 32s + 16 + 4g..
-  bf16x8 qf[4];
+  // Every global load of the chunk is issued up front, so the chunk costs one memory round trip:
+  // K and V rows 4tq.. x features 8fb.. (thread (tq, fb)), Q rows 16w + l%16 in k-slot order
+  // (block s holds features 32s + 4g.. and 32s + 16 + 4g..), g and beta (wave 0, lane = token).
+  const int tq = t >> 4, fb = t & 15;
+  u16x8 kx[4], vreg[4], qr[4];
+  load_rows4(kx, k + (int64_t)hk * D, ks, cp.t0, cp.len, tq, 8 * fb);
+  load_rows4(vreg, v + (int64_t)h * D, vs, cp.t0, cp.len, tq, 8 * fb);
   {
     const u16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
     const int row = 16 * w + c16;
-    u16x8 r[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       if (row < cp.len) {
         const uint16_t* p = q + (cp.t0 + row) * qs + (int64_t)hk * D + 32 * s + 4 * g4;
         const u16x4 lo = *reinterpret_cast<const u16x4*>(p), hi = *reinterpret_cast<const u16x4*>(p + 16);
-        r[s] = u16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        qr[s] = u16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       } else {
-        r[s] = zero;
+        qr[s] = zero;
       }
     }
+  }
+  float graw = 0.f, braw = 0.f;  // padding: g = 0, beta = 0
+  if (w == 0 && lane < cp.len) {
+    graw = g[(cp.t0 + lane) * Hv + h];
+    braw = Elem<BetaT>::load(beta + (cp.t0 + lane) * Hv + h);
+  }
+
+  // K: l2norm, row-major LDS copy, largest |K|
+  {
+    if (use_l2) l2norm_rows4(kx);
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      *reinterpret_cast<u16x8*>(&sm.K[(4 * tq + i) * LDK + 8 * fb]) = kx[i];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(bf2f(kx[i][e])));
+    }
+    m = wave_max(m);
+    if (lane == 0) sm.KMX[w] = m;
+  }
+  // Q: l2norm in registers (a row is spread over lanes l%16 + 16g' and the 4 blocks)
+  bf16x8 qf[4];
+  {
     if (use_l2) {
       float ss = 0.f;
 #pragma unroll
       for (int s = 0; s < 4; ++s)
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float f = bf2f(r[s][e]);
+          const float f = bf2f(qr[s][e]);
           ss += rbf(f * f);
         }
       ss += __shfl_xor(ss, 16, kWave);
@@ -402,15 +430,13 @@ __global__ __launch_bounds__(pf::NT, 2) void chunk_local_kernel(
 #pragma unroll
       for (int s = 0; s < 4; ++s)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) r[s][e] = f2bf(bf2f(r[s][e]) * inv);
+        for (int e = 0; e < 8; ++e) qr[s][e] = f2bf(bf2f(qr[s][e]) * inv);
     }
 #pragma unroll
-    for (int s = 0; s < 4; ++s) qf[s] = __builtin_bit_cast(bf16x8, r[s]);
+    for (int s = 0; s < 4; ++s) qf[s] = __builtin_bit_cast(bf16x8, qr[s]);
   }
-  if (w == 0) {  // cumulative decay within the chunk (padding: g = 0, beta = 0)
-    const bool valid = lane < cp.len;
-    float G = valid ? g[(cp.t0 + lane) * Hv + h] : 0.f;
-    const float bt = valid ? Elem<BetaT>::load(beta + (cp.t0 + lane) * Hv + h) : 0.f;
+  if (w == 0) {  // cumulative decay within the chunk
+    float G = graw;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
       const float up = __shfl_up(G, o, kWave);
@@ -420,23 +446,20 @@ __global__ __launch_bounds__(pf::NT, 2) void chunk_local_kernel(
     const float eg = expf(G), dec = expf(gl - G);
     sm.G[lane] = G;
     sm.EG[lane] = eg;
-    sm.B[lane] = bt;
+    sm.B[lane] = braw;
     reinterpret_cast<float*>(rec + ws::DEC)[lane] = dec;
+    reinterpret_cast<float*>(rec + ws::EGS)[lane] = kScale * eg;
     if (lane == 0) reinterpret_cast<float*>(rec + ws::GL)[0] = expf(gl);
   }
   __syncthreads();
 
   // QG fragments (this wave's token tile, straight from the k-slot ordered Q fragments) and the
-  // kappa-scaled fp16 K^T fragments
+  // kappa-scaled fp16 K^T fragments, written once per key head
   {
-    const float f = kScale * sm.EG[16 * w + c16];
+    if (kq_owner) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const u16x8 u = __builtin_bit_cast(u16x8, qf[s]);
-      u16x8 o;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = f2bf(bf2f(u[e]) * f);
-      *reinterpret_cast<u16x8*>(rec + ws::QG + (w * 4 + s) * ws::FRAG + lane * 16) = o;
+      for (int s = 0; s < 4; ++s)
+        *reinterpret_cast<bf16x8*>(rec + ws::QG + (w * 4 + s) * ws::FRAG + lane * 16) = qf[s];
     }
     const float kmax = fmaxf(fmaxf(sm.KMX[0], sm.KMX[1]), fmaxf(sm.KMX[2], sm.KMX[3]));
     const int ke = fp16_fit_exp(kmax);
@@ -446,17 +469,13 @@ __global__ __launch_bounds__(pf::NT, 2) void chunk_local_kernel(
       reinterpret_cast<float*>(rec + ws::KAP)[0] = kappa;
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 4 && kq_owner; ++i) {
       const int idx = t + NT * i;  // fragment idx / 64 = (rb, j), lane idx % 64
-      const int f_ = idx >> 6, l = idx & 63, rb = f_ >> 1, j = f_ & 1;
-      const uint16_t* p = &sm.KT[(16 * rb + (l & 15)) * LDT + 32 * j + 4 * (l >> 4)];
-      const u16x4 lo = *reinterpret_cast<const u16x4*>(p), hi = *reinterpret_cast<const u16x4*>(p + 16);
+      const int f_ = idx >> 6, rb = f_ >> 1, j = f_ & 1;  // idx % 64 == lane (idx = t + 256 i)
+      const u16x8 kt = frag_tr_kperm(sm.K, LDK, 32 * j, 16 * rb, lane);
       f16x8 o;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        o[e] = (_Float16)(bf2f(lo[e]) * kappa);
-        o[4 + e] = (_Float16)(bf2f(hi[e]) * kappa);
-      }
+      for (int e = 0; e < 8; ++e) o[e] = (_Float16)(bf2f(kt[e]) * kappa);
       *reinterpret_cast<f16x8*>(rec + ws::KT + idx * 16) = o;
     }
   }
@@ -484,22 +503,23 @@ __global__ __launch_bounds__(pf::NT, 2) void chunk_local_kernel(
         {  // X[i][jj], i = 16w + 4g + r, jj = 16cb + c
           const int i = 16 * w + 4 * g4 + r, jj = 16 * cb + c16;
           float x = 0.f;
-          if (cb <= w && i > jj) x = -sm.B[i] * accA[cb][r] * expf(sm.G[i] - sm.G[jj]);
+          if (cb <= w && i > jj) x = -sm.B[i] * accA[cb][r] * __expf(sm.G[i] - sm.G[jj]);
           sm.X[i * LDF + jj] = x;
         }
         {  // QK[i][jj], i = 16w + c, jj = 16cb + 4g + r
           const int i = 16 * w + c16, jj = 16 * cb + 4 * g4 + r;
-          accQ[cb][r] = (cb <= w && i >= jj) ? kScale * accQ[cb][r] * expf(sm.G[i] - sm.G[jj]) : 0.f;
+          accQ[cb][r] = (cb <= w && i >= jj) ? kScale * accQ[cb][r] * __expf(sm.G[i] - sm.G[jj]) : 0.f;
         }
       }
 #pragma unroll
     for (int j = 0; j < 2; ++j)
-      *reinterpret_cast<bf16x8*>(rec + ws::QK + (w * 2 + j) * ws::FRAG + lane * 16) =
-          pack_acc_bf16(accQ[2 * j], accQ[2 * j + 1]);
+      if (2 * j <= w)  // fragment (w, j) is non-zero only when its first column block 2j <= w
+        *reinterpret_cast<bf16x8*>(rec + ws::QK + (w * 2 + j) * ws::FRAG + lane * 16) =
+            pack_acc_bf16(accQ[2 * j], accQ[2 * j + 1]);
   }
   __syncthreads();
 
-  unit_lower_inv64(sm.X, sm.T, sm.Y, w, lane);
+  unit_lower_inv64(sm.X, sm.T, w, lane);
 
   // W^T = K^T (T diag(beta e^G))^T: its accumulator layout is the k-slot ordered W fragment layout.
   // U = T diag(beta) V in accumulator layout (the scan kernel's initial vn tiles).
@@ -524,19 +544,20 @@ __global__ __launch_bounds__(pf::NT, 2) void chunk_local_kernel(
       for (int cb = 0; cb < 8; ++cb) {
         accW[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < 2; ++s) accW[cb] = mma(frag(sm.KT, LDT, 16 * cb, 32 * s, lane), tbe[s], accW[cb]);
+        for (int s = 0; s < 2; ++s)
+          accW[cb] = mma(__builtin_bit_cast(bf16x8, frag_tr(sm.K, LDK, 32 * s, 16 * cb, lane)), tbe[s], accW[cb]);
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         *reinterpret_cast<bf16x8*>(rec + ws::WN + (w * 4 + j) * ws::FRAG + lane * 16) =
             pack_acc_bf16(-accW[2 * j], -accW[2 * j + 1]);
     }
-    // V^T into the X buffer (dead after the inverse; V^T is 1 KiB larger and runs into T, whose
-    // reads all finished above -- hence the barrier)
-    static_assert(pf::D * pf::LDT * 2 <= 2 * pf::CH * pf::LDF * 4, "V^T must fit in X and T");
-    uint16_t* VT = reinterpret_cast<uint16_t*>(sm.X);
+    // V row-major into the X buffer (dead after the inverse; its scratch blocks were read by the
+    // inverse's last step -- hence the barrier)
+    uint16_t* sV = reinterpret_cast<uint16_t*>(sm.X);
     __syncthreads();
-    store_transposed4(VT, LDT, vreg, t >> 4, 8 * (t & 15));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<u16x8*>(&sV[(4 * tq + i) * LDK + 8 * fb]) = vreg[i];
     __syncthreads();
     f32x4 u[8];
     float m = 0.f;
@@ -544,7 +565,8 @@ __global__ __launch_bounds__(pf::NT, 2) void chunk_local_kernel(
     for (int cb = 0; cb < 8; ++cb) {
       u[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < 2; ++s) u[cb] = mma(tb[s], frag(VT, LDT, 16 * cb, 32 * s, lane), u[cb]);
+      for (int s = 0; s < 2; ++s)
+        u[cb] = mma(tb[s], __builtin_bit_cast(bf16x8, frag_tr(sV, LDK, 32 * s, 16 * cb, lane)), u[cb]);
 #pragma unroll
       for (int r = 0; r < 4; ++r) m = fmaxf(m, fabsf(u[cb][r]));
     }
@@ -626,10 +648,15 @@ __device__ __forceinline__ void chain_read_k(ChainIn& in, const uint8_t* ring, i
 constexpr int kFragPieces = 2 * 16 * ws::FRAG / 16 / 128;  // WN + KT pieces of 16 bytes per loader lane
 constexpr int kLoadPieces = kFragPieces + 2;               // + one piece of U, + one of the header (lanes < 32)
 
-// loader lane lt (0..127): WN/KT pieces lt + 128 i, U piece lt of slice n, header piece lt (< 32)
-__device__ __forceinline__ void scan_load(u16x8 (&r)[kLoadPieces], const uint8_t* rec, int n, int lt) {
+// loader lane lt (0..127): WN/KT pieces lt + 128 i (KT from the key head's record rec_kq), U piece lt
+// of slice n, header piece lt (< 32)
+__device__ __forceinline__ void scan_load(u16x8 (&r)[kLoadPieces], const uint8_t* rec, const uint8_t* rec_kq,
+                                          int n, int lt) {
 #pragma unroll
-  for (int i = 0; i < kFragPieces; ++i) r[i] = *reinterpret_cast<const u16x8*>(rec + ws::WN + (lt + 128 * i) * 16);
+  for (int i = 0; i < kFragPieces / 2; ++i) r[i] = *reinterpret_cast<const u16x8*>(rec + ws::WN + (lt + 128 * i) * 16);
+#pragma unroll
+  for (int i = kFragPieces / 2; i < kFragPieces; ++i)
+    r[i] = *reinterpret_cast<const u16x8*>(rec_kq + ws::WN + (lt + 128 * i) * 16);
   r[kFragPieces] = *reinterpret_cast<const u16x8*>(rec + ws::U + n * 2048 + lt * 16);
   if (lt < 32) r[kFragPieces + 1] = *reinterpret_cast<const u16x8*>(rec + ws::HDR + lt * 16);
 }
@@ -640,12 +667,17 @@ __device__ __forceinline__ void scan_store(uint8_t* dst, const u16x8 (&r)[kLoadP
   if (lt < 32) *reinterpret_cast<u16x8*>(dst + rg::HDR + lt * 16) = r[kFragPieces + 1];
 }
 
-// The output wave's per-chunk operands: QG (16 fragments) and the 6 non-zero QK fragments.
+// The output wave's per-chunk operands: QG (16 fragments, from the key head's record), the 6
+// non-zero QK fragments and the row factors scale e^{G_t} of this lane's tokens.
 struct OutFrags {
   bf16x8 qg[16], qk[6];
+  f32x4 egs[4];
 };
-__device__ __forceinline__ void out_load(OutFrags& f, const uint8_t* rec, int lane) {
-  const uint8_t* qg = rec + ws::QG + lane * 16;
+__device__ __forceinline__ void out_load(OutFrags& f, const uint8_t* rec, const uint8_t* rec_kq, int lane) {
+  const f32x4* eg = reinterpret_cast<const f32x4*>(rec + ws::EGS) + (lane >> 4);
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) f.egs[tb] = eg[4 * tb];
+  const uint8_t* qg = rec_kq + ws::QG + lane * 16;
 #pragma unroll
   for (int i = 0; i < 16; ++i) f.qg[i] = *reinterpret_cast<const bf16x8*>(qg + i * ws::FRAG);
   const uint8_t* qk = rec + ws::QK + lane * 16;
@@ -668,6 +700,7 @@ __device__ __forceinline__ void out_step(const OutFrags& f, const uint8_t* xch, 
     O[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < 4; ++j) O[tb] = mma(f.qg[tb * 4 + j], sb[j], O[tb]);
+    O[tb] *= f.egs[tb];
   }
   O[0] = mma(f.qk[0], vb[0], O[0]);
   O[1] = mma(f.qk[1], vb[0], O[1]);
@@ -688,8 +721,8 @@ __device__ __forceinline__ void out_step(const OutFrags& f, const uint8_t* xch, 
 template <typename OutT>
 __global__ __launch_bounds__(pf::NT, 1) void chunk_scan_kernel(
     const float* __restrict__ init, float* __restrict__ final_state, OutT* __restrict__ out,
-    const int32_t* __restrict__ cu, const int32_t* __restrict__ seq_chunk0, int nseq, int seq_len, int Hv,
-    const uint8_t* __restrict__ work) {
+    const int32_t* __restrict__ cu, const int32_t* __restrict__ seq_chunk0, int nseq, int seq_len, int Hqk,
+    int Hv, const uint8_t* __restrict__ work) {
   using namespace pf;
   __shared__ ScanSmem sm;
   // block -> (sequence-head pair, slice); the 8 slices of a pair share blockIdx % 8 and therefore an
@@ -714,6 +747,7 @@ __global__ __launch_bounds__(pf::NT, 1) void chunk_scan_kernel(
   const int nch = (L + CH - 1) / CH;
   const int64_t rstride = (int64_t)Hv * ws::BYTES;
   const uint8_t* rec0 = work + (int64_t)slot0 * rstride + (int64_t)h * ws::BYTES;
+  const int64_t kq_off = -(int64_t)(h % (Hv / Hqk)) * ws::BYTES;  // record of the key head's owner
   const int col = 16 * n + c16;
 
   if (role == 0) {
@@ -828,9 +862,9 @@ __global__ __launch_bounds__(pf::NT, 1) void chunk_scan_kernel(
   } else if (role == 1) {
     // ---------------- output wave: step c computes chunk c-1 ----------------
     OutFrags F0, F1;  // even / odd chunks
-    if (nch > 0) out_load(F0, rec0, lane);
+    if (nch > 0) out_load(F0, rec0, rec0 + kq_off, lane);
     __syncthreads();  // prologue
-    if (nch > 1) out_load(F1, rec0 + rstride, lane);
+    if (nch > 1) out_load(F1, rec0 + rstride, rec0 + rstride + kq_off, lane);
     __syncthreads();  // step 0
     int xp = 0;       // (c - 1) % 3
     for (int c = 1; c <= nch; c += 2) {
@@ -838,7 +872,7 @@ __global__ __launch_bounds__(pf::NT, 1) void chunk_scan_kernel(
         const int cc = c - 1;  // even
         const int len = L - cc * CH < CH ? L - cc * CH : CH;
         out_step<OutT>(F0, sm.xch[xp], out, s0 + (int64_t)cc * CH, len, Hv, h, col, lane);
-        if (c + 1 < nch) out_load(F0, rec0 + (int64_t)(c + 1) * rstride, lane);
+        if (c + 1 < nch) out_load(F0, rec0 + (int64_t)(c + 1) * rstride, rec0 + (int64_t)(c + 1) * rstride + kq_off, lane);
         xp = xp == 2 ? 0 : xp + 1;
         __syncthreads();  // end of step c
       }
@@ -846,7 +880,7 @@ __global__ __launch_bounds__(pf::NT, 1) void chunk_scan_kernel(
         const int cc = c;  // odd
         const int len = L - cc * CH < CH ? L - cc * CH : CH;
         out_step<OutT>(F1, sm.xch[xp], out, s0 + (int64_t)cc * CH, len, Hv, h, col, lane);
-        if (c + 2 < nch) out_load(F1, rec0 + (int64_t)(c + 2) * rstride, lane);
+        if (c + 2 < nch) out_load(F1, rec0 + (int64_t)(c + 2) * rstride, rec0 + (int64_t)(c + 2) * rstride + kq_off, lane);
         xp = xp == 2 ? 0 : xp + 1;
         __syncthreads();  // end of step c+1
       }
@@ -855,23 +889,23 @@ __global__ __launch_bounds__(pf::NT, 1) void chunk_scan_kernel(
     // ---------------- loader waves ----------------
     const int lt = t - 128;
     u16x8 R0[kLoadPieces], R1[kLoadPieces];  // even / odd chunks
-    if (nch > 0) scan_load(R0, rec0, n, lt);
-    if (nch > 1) scan_load(R1, rec0 + rstride, n, lt);
+    if (nch > 0) scan_load(R0, rec0, rec0 + kq_off, n, lt);
+    if (nch > 1) scan_load(R1, rec0 + rstride, rec0 + rstride + kq_off, n, lt);
     if (nch > 0) scan_store(sm.ring[0], R0, lt);
     if (nch > 1) scan_store(sm.ring[1], R1, lt);
-    if (nch > 2) scan_load(R0, rec0 + 2 * rstride, n, lt);
-    if (nch > 3) scan_load(R1, rec0 + 3 * rstride, n, lt);
+    if (nch > 2) scan_load(R0, rec0 + 2 * rstride, rec0 + 2 * rstride + kq_off, n, lt);
+    if (nch > 3) scan_load(R1, rec0 + 3 * rstride, rec0 + 3 * rstride + kq_off, n, lt);
     __syncthreads();  // prologue
     // step c: stage chunk c+2 (held in R[c&1]) into ring slot (c+2)%3, then load chunk c+4
     int slot = 2;  // (c + 2) % 3
     for (int c = 0; c < nch; c += 2) {
       if (c + 2 < nch) scan_store(sm.ring[slot], R0, lt);
-      if (c + 4 < nch) scan_load(R0, rec0 + (int64_t)(c + 4) * rstride, n, lt);
+      if (c + 4 < nch) scan_load(R0, rec0 + (int64_t)(c + 4) * rstride, rec0 + (int64_t)(c + 4) * rstride + kq_off, n, lt);
       slot = slot == 2 ? 0 : slot + 1;
       __syncthreads();  // end of step c
       if (c + 1 < nch) {
         if (c + 3 < nch) scan_store(sm.ring[slot], R1, lt);
-        if (c + 5 < nch) scan_load(R1, rec0 + (int64_t)(c + 5) * rstride, n, lt);
+        if (c + 5 < nch) scan_load(R1, rec0 + (int64_t)(c + 5) * rstride, rec0 + (int64_t)(c + 5) * rstride + kq_off, n, lt);
         slot = slot == 2 ? 0 : slot + 1;
         __syncthreads();  // end of step c+1
       }
@@ -1043,7 +1077,7 @@ extern "C" int gdn_chunk_prefill(const void* q, int64_t q_stride, const void* k,
   const int64_t pairs = (int64_t)nseq * Hv;
   const int64_t scan_blocks = (pairs + 7) / 8 * 64;
   chunk_scan_kernel<uint16_t><<<(unsigned)scan_blocks, pf::NT, 0, s>>>(
-      initial_state, final_state, (uint16_t*)out, cu_seqlens, seq_chunk0, nseq, seq_len, Hv, work);
+      initial_state, final_state, (uint16_t*)out, cu_seqlens, seq_chunk0, nseq, seq_len, Hqk, Hv, work);
   return check_launch("gdn_chunk_prefill(state)");
 }
 
