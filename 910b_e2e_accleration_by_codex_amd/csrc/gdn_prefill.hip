@@ -668,15 +668,15 @@ __device__ __forceinline__ void scan_store(uint8_t* dst, const u16x8 (&r)[kLoadP
 }
 
 // The output wave's per-chunk operands: QG (16 fragments, from the key head's record), the 6
-// non-zero QK fragments and the row factors scale e^{G_t} of this lane's tokens.
+// non-zero QK fragments and the row factors scale e^{G_t} of this lane's token in each tile.
 struct OutFrags {
   bf16x8 qg[16], qk[6];
-  f32x4 egs[4];
+  float egs[4];
 };
 __device__ __forceinline__ void out_load(OutFrags& f, const uint8_t* rec, const uint8_t* rec_kq, int lane) {
-  const f32x4* eg = reinterpret_cast<const f32x4*>(rec + ws::EGS) + (lane >> 4);
+  const float* eg = reinterpret_cast<const float*>(rec + ws::EGS) + (lane & 15);
 #pragma unroll
-  for (int tb = 0; tb < 4; ++tb) f.egs[tb] = eg[4 * tb];
+  for (int tb = 0; tb < 4; ++tb) f.egs[tb] = eg[16 * tb];
   const uint8_t* qg = rec_kq + ws::QG + lane * 16;
 #pragma unroll
   for (int i = 0; i < 16; ++i) f.qg[i] = *reinterpret_cast<const bf16x8*>(qg + i * ws::FRAG);
@@ -685,9 +685,13 @@ __device__ __forceinline__ void out_load(OutFrags& f, const uint8_t* rec, const 
 #pragma unroll
   for (int i = 0; i < 6; ++i) f.qk[i] = *reinterpret_cast<const bf16x8*>(qk + idx[i] * ws::FRAG);
 }
+// o^T = S^T Qg^T + vn^T QK^T, tile by tile.  The k-slot ordered B fragments of S and vn are A
+// fragments of S^T and vn^T, and the QG / QK A fragments are B fragments of their transposes, so
+// the transposed products need no data movement -- and their accumulator layout gives each lane 4
+// consecutive output columns of one token: lane (c, g) holds o[16 tb + c][16 n + 4g .. 4g + 3].
 template <typename OutT>
 __device__ __forceinline__ void out_step(const OutFrags& f, const uint8_t* xch, OutT* out, int64_t t0, int len,
-                                         int Hv, int h, int col, int lane) {
+                                         int Hv, int h, int col0, int lane) {
   using namespace pf;
   bf16x8 sb[4], vb[2];
 #pragma unroll
@@ -699,23 +703,31 @@ __device__ __forceinline__ void out_step(const OutFrags& f, const uint8_t* xch, 
   for (int tb = 0; tb < 4; ++tb) {
     O[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) O[tb] = mma(f.qg[tb * 4 + j], sb[j], O[tb]);
+    for (int j = 0; j < 4; ++j) O[tb] = mma(sb[j], f.qg[tb * 4 + j], O[tb]);
     O[tb] *= f.egs[tb];
   }
-  O[0] = mma(f.qk[0], vb[0], O[0]);
-  O[1] = mma(f.qk[1], vb[0], O[1]);
-  O[2] = mma(f.qk[2], vb[0], O[2]);
-  O[2] = mma(f.qk[3], vb[1], O[2]);
-  O[3] = mma(f.qk[4], vb[0], O[3]);
-  O[3] = mma(f.qk[5], vb[1], O[3]);
-  const int g4 = lane >> 4;
+  O[0] = mma(vb[0], f.qk[0], O[0]);
+  O[1] = mma(vb[0], f.qk[1], O[1]);
+  O[2] = mma(vb[0], f.qk[2], O[2]);
+  O[2] = mma(vb[1], f.qk[3], O[2]);
+  O[3] = mma(vb[0], f.qk[4], O[3]);
+  O[3] = mma(vb[1], f.qk[5], O[3]);
+  const int c16 = lane & 15, g4 = lane >> 4;
 #pragma unroll
-  for (int tb = 0; tb < 4; ++tb)
+  for (int tb = 0; tb < 4; ++tb) {
+    const int row = 16 * tb + c16;
+    if (row < len) {
+      OutT* o = out + ((t0 + row) * Hv + h) * D + col0 + 4 * g4;
+      if constexpr (sizeof(OutT) == 2) {
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 pk = {f2bf2(O[tb][0], O[tb][1]), f2bf2(O[tb][2], O[tb][3])};
+        *reinterpret_cast<u32x2*>(o) = pk;
+      } else {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = 16 * tb + 4 * g4 + r;
-      if (row < len) Elem<OutT>::store(out + ((t0 + row) * Hv + h) * D + col, O[tb][r]);
+        for (int r = 0; r < 4; ++r) Elem<OutT>::store(o + r, O[tb][r]);
+      }
     }
+  }
 }
 
 template <typename OutT>
@@ -871,7 +883,7 @@ __global__ __launch_bounds__(pf::NT, 1) void chunk_scan_kernel(
       {
         const int cc = c - 1;  // even
         const int len = L - cc * CH < CH ? L - cc * CH : CH;
-        out_step<OutT>(F0, sm.xch[xp], out, s0 + (int64_t)cc * CH, len, Hv, h, col, lane);
+        out_step<OutT>(F0, sm.xch[xp], out, s0 + (int64_t)cc * CH, len, Hv, h, 16 * n, lane);
         if (c + 1 < nch) out_load(F0, rec0 + (int64_t)(c + 1) * rstride, rec0 + (int64_t)(c + 1) * rstride + kq_off, lane);
         xp = xp == 2 ? 0 : xp + 1;
         __syncthreads();  // end of step c
@@ -879,7 +891,7 @@ __global__ __launch_bounds__(pf::NT, 1) void chunk_scan_kernel(
       if (c + 1 <= nch) {
         const int cc = c;  // odd
         const int len = L - cc * CH < CH ? L - cc * CH : CH;
-        out_step<OutT>(F1, sm.xch[xp], out, s0 + (int64_t)cc * CH, len, Hv, h, col, lane);
+        out_step<OutT>(F1, sm.xch[xp], out, s0 + (int64_t)cc * CH, len, Hv, h, 16 * n, lane);
         if (c + 2 < nch) out_load(F1, rec0 + (int64_t)(c + 2) * rstride, rec0 + (int64_t)(c + 2) * rstride + kq_off, lane);
         xp = xp == 2 ? 0 : xp + 1;
         __syncthreads();  // end of step c+1
@@ -1050,6 +1062,7 @@ extern "C" int gdn_chunk_prefill(const void* q, int64_t q_stride, const void* k,
   GDN_REQUIRE(aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && q_stride % 8 == 0 && k_stride % 8 == 0 &&
                   v_stride % 8 == 0,
               "gdn_chunk_prefill: q/k/v rows must be 16-byte aligned");
+  GDN_REQUIRE(aligned(out, 8), "gdn_chunk_prefill: out must be 8-byte aligned");
   GDN_REQUIRE(total_chunks == 0 || (workspace && aligned(workspace, 256) &&
                                     workspace_bytes >= gdn_chunk_prefill_workspace_bytes(total_chunks, Hv)),
               "gdn_chunk_prefill: workspace missing, misaligned or smaller than %lld bytes",
