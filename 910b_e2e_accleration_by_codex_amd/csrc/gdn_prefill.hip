@@ -366,7 +366,7 @@ __global__ __launch_bounds__(pf::NT, 3) void chunk_local_kernel(
   using namespace pf;
   __shared__ LocalSmem sm;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
-  const int slot = blockIdx.x, h = blockIdx.y;
+  const int h = blockIdx.x, slot = blockIdx.y;  // value heads fastest: the heads sharing a key head run together
   const int hk = h / (Hv / Hqk);
   const ChunkPos cp = chunk_pos(slot, cu, seq_chunk0, nseq, seq_len);
   uint8_t* rec = work + ((int64_t)slot * Hv + h) * ws::BYTES;
@@ -1073,7 +1073,7 @@ extern "C" int gdn_chunk_prefill(const void* q, int64_t q_stride, const void* k,
   hipStream_t s = (hipStream_t)stream;
   uint8_t* work = (uint8_t*)workspace;
   if (total_chunks > 0) {
-    dim3 g1((unsigned)total_chunks, (unsigned)Hv);
+    dim3 g1((unsigned)Hv, (unsigned)total_chunks);
     if (beta_dtype == GDN_BF16)
       chunk_local_kernel<uint16_t><<<g1, pf::NT, 0, s>>>((const uint16_t*)q, q_stride, (const uint16_t*)k, k_stride,
                                                          (const uint16_t*)v, v_stride,

@@ -262,7 +262,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill"], default=None)
+    ap.add_argument("--only", choices=["decode", "prefill", "prefill8192"], default=None,
+                    help="run one workload group (prefill8192: the T=8192 chunked rule alone, for profiling)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first run a 256 MiB device-to-device copy (counter calibration for rocprof)")
     args = ap.parse_args()
@@ -284,12 +285,14 @@ def main():
     res = {}
     if args.only in (None, "decode"):
         res["decode"] = bench_decode(gdn, dev, args.steps, args.warmup)
-    if args.only in (None, "prefill") and not args.no_prefill:
+    if args.only == "prefill8192":
+        res["prefill"] = [bench_prefill(gdn, dev, reps=args.steps)]
+    elif args.only in (None, "prefill") and not args.no_prefill:
         res["prefill"] = [bench_prefill(gdn, dev), bench_prefill_varlen(gdn, dev),
                           bench_prefill_long(gdn, dev, check=not args.no_cpu)]
         if not args.no_cpu:
             res["prefill"][0]["cpu_baseline"] = cpu_baseline_prefill()
-    if args.only == "prefill":
+    if args.only in ("prefill", "prefill8192"):
         print(json.dumps({"secondary": res["prefill"]}))
         return
     dec = res["decode"]
