@@ -8,13 +8,13 @@
 //   vn  = U - W S,   o = diag(scale e^G) Q S + QK vn,   S' = e^{G_last} S + K^T diag(e^{G_last - G}) vn
 // which is src/gdn_chunk_fast2.py:31-59 (and HF torch_chunk_gated_delta_rule) written per chunk.
 //
-// One workgroup (4 waves) owns (sequence, value head, BV-column tile of the state) and walks its
-// chunks in order; the fp32 state tile S [128, BV] lives in MFMA accumulators across chunks.  Every
-// product runs on v_mfma_f32_16x16x32_bf16 with fp32 accumulation; precision is spent where the
-// fp32 state needs it: U and vn stay fp32 in accumulators, and the state update K^T (dec*vn) uses
-// vn split into bf16 hi + lo (two MFMAs), so the running state never sees a bf16 rounding of its
-// increment.  K, V and l2-normalised q, k are exact in bf16.  The 64x64 inverse is fp32 throughout:
-// 16x16 diagonal blocks by forward substitution, block merges on v_mfma_f32_16x16x4_f32.
+// Two kernels: chunk_local_kernel does every state-independent part of a chunk in parallel over all
+// (chunk, value head) pairs and writes ready-made MFMA operand fragments to a workspace;
+// chunk_scan_kernel walks the chunks of each sequence in order with the fp32 state held in MFMA
+// accumulators (one workgroup per 16-column slice of a head's state).  Products run on
+// v_mfma_f32_16x16x32_bf16 / _f16 with fp32 accumulation; the 64x64 inverse is fp32 throughout
+// (v_mfma_f32_16x16x4_f32).  The state update uses fp16 operands (DEC vn and K^T) with power-of-two
+// range scaling, so the running state never sees a bf16 rounding of its increment.
 #include "gdn_device.h"
 #include "gdn_internal.h"
 
