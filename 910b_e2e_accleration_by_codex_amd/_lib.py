@@ -35,6 +35,11 @@ _SIGNATURES = {
     "gdn_chunk_prefill_workspace_bytes": ([_L, _I], _L),
     "gdn_conv_prefill": ([_P, _L, _P, _P, _P, _P, _P, _L, _P, _I, _I, _I, _I, _P], _I),
     "gdn_gating": ([_P, _P, _L, _P, _P, _P, _P, _L, _I, _P], _I),
+    "gdn_decode_fused_masked": ([_P, _L, _P, _L, _P, _P, _L, _P, _P, _P, _P, _P, _P, _I, _F, _P, _P, _P, _I,
+                                 _I, _I, _I, _I, _P], _I),
+    "gdn_chunk_prefill_rows": ([_P, _L, _P, _L, _P, _L, _P, _P, _I, _P, _P, _P, _I, _P, _L, _P, _P, _L, _I,
+                                _I, _I, _I, _I, _I, _I, _P, _L, _P], _I),
+    "gdn_conv_prefill_rows": ([_P, _L, _P, _P, _P, _P, _P, _P, _I, _L, _P, _I, _I, _I, _I, _P], _I),
 }
 
 _lib = None

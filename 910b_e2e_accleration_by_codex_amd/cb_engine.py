@@ -88,13 +88,16 @@ def fused_gated_rmsnorm(self, hidden_states, gate=None):
 
 
 def gdn_decode_core(mixed, z, a, b, conv_state, conv_weight, A_log, dt_bias, norm_weight, rec_state,
-                    num_k_heads, num_v_heads, head_dim, eps=1e-6, conv_bias=None, out=None):
+                    num_k_heads, num_v_heads, head_dim, eps=1e-6, conv_bias=None, out=None, active=None):
     """One fused kernel for the GDN decode layer between in_proj_* and out_proj
     (src/cb_engine.py:325-351 with ELEM_CONV): conv update + SiLU, split, gating, l2norm, recurrent
     step, gated RMSNorm.  mixed [N, C] bf16 (pre-conv), z [N, H_v*d] bf16, a, b [N, H_v] bf16;
     conv_state [N, C, K] bf16 and rec_state [N, H_v, d, d] fp32 are updated in place.
     A_log, dt_bias, norm_weight: the layer's parameters (any float dtype; A_log / dt_bias are read in
-    fp32 exactly as the reference's ``.float()``).  Returns the normed core [N, H_v*d] bf16."""
+    fp32 exactly as the reference's ``.float()``).  ``active`` (bool / uint8 [N] on the device, or
+    None = all): slots that advance; the others keep their conv and recurrent state and get zero
+    output rows -- the held slots of src/cb_tp.py:274-285 without the save / restore copies.
+    Returns the normed core [N, H_v*d] bf16."""
     _lib.require_cuda(mixed, z, a, b, conv_state, conv_weight, rec_state)
     N, C = mixed.shape
     Hk, Hv, D = num_k_heads, num_v_heads, head_dim
@@ -125,10 +128,15 @@ def gdn_decode_core(mixed, z, a, b, conv_state, conv_weight, A_log, dt_bias, nor
     nw = nw.contiguous()
     if out is None:
         out = torch.empty(N, Hv * D, dtype=torch.bfloat16, device=mixed.device)
-    _lib.call("gdn_decode_fused", _lib.ptr(mixed), ms, _lib.ptr(z), zs, _lib.ptr(a), _lib.ptr(b),
+    if active is not None:
+        _lib.require_cuda(active)
+        if active.numel() != N:
+            raise ValueError(f"gdn_decode_core: active must have N={N} entries")
+        active = active.reshape(N).to(torch.uint8).contiguous()
+    _lib.call("gdn_decode_fused_masked", _lib.ptr(mixed), ms, _lib.ptr(z), zs, _lib.ptr(a), _lib.ptr(b),
               a.stride(0), _lib.ptr(conv_state), _lib.ptr(conv_weight), _lib.ptr(conv_bias),
               _lib.ptr(A32), _lib.ptr(dt32), _lib.ptr(nw), _lib.dtype_code(nw), float(eps),
-              _lib.ptr(rec_state), _lib.ptr(out), N, Hk, Hv, D, K, _lib.stream_of(mixed))
+              _lib.ptr(rec_state), _lib.ptr(out), _lib.ptr(active), N, Hk, Hv, D, K, _lib.stream_of(mixed))
     return out
 
 

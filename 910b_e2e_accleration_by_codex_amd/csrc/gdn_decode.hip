@@ -314,7 +314,7 @@ __global__ __launch_bounds__(kHeadThreads* R) void decode_fused_kernel(
     uint16_t* __restrict__ conv_state, const uint16_t* __restrict__ conv_w,
     const uint16_t* __restrict__ conv_b, const float* __restrict__ A_log,
     const float* __restrict__ dt_bias, const void* norm_w, float eps, float* rec_state,
-    uint16_t* __restrict__ out, int Hk, int K) {
+    uint16_t* __restrict__ out, const uint8_t* __restrict__ active, int Hk, int K) {
   __shared__ float s_q[kD], s_k[kD], s_v[R][kD];
   __shared__ float s_red[R][2][4][kD];
   __shared__ float s_gamma[R], s_beta[R];
@@ -322,6 +322,10 @@ __global__ __launch_bounds__(kHeadThreads* R) void decode_fused_kernel(
   const int j = t / kHeadThreads, tl = t % kHeadThreads, wl = tl >> 6;  // head in group, local ids
   const int n = blockIdx.x / Hk, hk = blockIdx.x % Hk;
   const int Hv = Hk * R;
+  if (active && !active[n]) {  // a held or idle slot: states untouched, output rows zero
+    if (tl < kD) out[((int64_t)n * Hv + hk * R + j) * kD + tl] = 0;
+    return;
+  }
   const int h = hk * R + j;
   const int C = (2 * Hk + Hv) * kD;
   const int64_t sidx = ((int64_t)n * Hv + h) * kD * kD;
@@ -487,12 +491,12 @@ extern "C" int gdn_gated_rmsnorm(const void* x, int64_t x_stride, const void* ga
   return check_launch("gdn_gated_rmsnorm");
 }
 
-extern "C" int gdn_decode_fused(const void* mixed, int64_t mixed_stride, const void* z, int64_t z_stride,
-                                const void* a, const void* b, int64_t ab_stride, void* conv_state,
-                                const void* conv_w, const void* conv_b, const float* A_log,
-                                const float* dt_bias, const void* norm_w, int norm_w_dtype, float eps,
-                                float* rec_state, void* out, int N, int Hk, int Hv, int D, int K,
-                                void* stream) {
+extern "C" int gdn_decode_fused_masked(const void* mixed, int64_t mixed_stride, const void* z, int64_t z_stride,
+                                       const void* a, const void* b, int64_t ab_stride, void* conv_state,
+                                       const void* conv_w, const void* conv_b, const float* A_log,
+                                       const float* dt_bias, const void* norm_w, int norm_w_dtype, float eps,
+                                       float* rec_state, void* out, const uint8_t* active, int N, int Hk, int Hv,
+                                       int D, int K, void* stream) {
   clear_error();
   GDN_REQUIRE(mixed && z && a && b && conv_state && conv_w && A_log && dt_bias && norm_w && rec_state && out,
               "gdn_decode_fused: null pointer");
@@ -512,7 +516,7 @@ extern "C" int gdn_decode_fused(const void* mixed, int64_t mixed_stride, const v
   decode_fused_kernel<RR, WB><<<grid, kHeadThreads * RR, 0, s>>>(                                     \
       (const uint16_t*)mixed, mixed_stride, (const uint16_t*)z, z_stride, (const uint16_t*)a,         \
       (const uint16_t*)b, ab_stride, (uint16_t*)conv_state, (const uint16_t*)conv_w,                  \
-      (const uint16_t*)conv_b, A_log, dt_bias, norm_w, eps, rec_state, (uint16_t*)out, Hk, K)
+      (const uint16_t*)conv_b, A_log, dt_bias, norm_w, eps, rec_state, (uint16_t*)out, active, Hk, K)
 #define GDN_DF_R(WB)                      \
   switch (R) {                            \
     case 1: GDN_DF_LAUNCH(1, WB); break;  \
@@ -525,4 +529,15 @@ extern "C" int gdn_decode_fused(const void* mixed, int64_t mixed_stride, const v
 #undef GDN_DF_R
 #undef GDN_DF_LAUNCH
   return check_launch("gdn_decode_fused");
+}
+
+extern "C" int gdn_decode_fused(const void* mixed, int64_t mixed_stride, const void* z, int64_t z_stride,
+                                const void* a, const void* b, int64_t ab_stride, void* conv_state,
+                                const void* conv_w, const void* conv_b, const float* A_log,
+                                const float* dt_bias, const void* norm_w, int norm_w_dtype, float eps,
+                                float* rec_state, void* out, int N, int Hk, int Hv, int D, int K,
+                                void* stream) {
+  return gdn_decode_fused_masked(mixed, mixed_stride, z, z_stride, a, b, ab_stride, conv_state, conv_w, conv_b,
+                                 A_log, dt_bias, norm_w, norm_w_dtype, eps, rec_state, out, nullptr, N, Hk, Hv, D, K,
+                                 stream);
 }

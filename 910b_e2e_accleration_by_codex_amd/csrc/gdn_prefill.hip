@@ -228,6 +228,12 @@ __device__ __forceinline__ int fp16_fit_exp(float amax) {
   return (amax >= 0.0625f && amax < 16384.0f) ? 0 : fp16_scale_exp(amax);
 }
 
+// Slot row of sequence s for state I/O: rows[s] (or s without rows); -1 if outside [0, n_rows).
+__device__ __forceinline__ int state_row(const int32_t* rows, int n_rows, int s) {
+  const int r = rows ? rows[s] : s;
+  return (r >= 0 && r < n_rows) ? r : -1;
+}
+
 struct ChunkPos {
   int64_t t0;  // first packed token of the chunk
   int len;     // valid tokens (1..64)
@@ -733,8 +739,8 @@ __device__ __forceinline__ void out_step(const OutFrags& f, const uint8_t* xch, 
 template <typename OutT>
 __global__ __launch_bounds__(pf::NT, 1) void chunk_scan_kernel(
     const float* __restrict__ init, float* __restrict__ final_state, OutT* __restrict__ out,
-    const int32_t* __restrict__ cu, const int32_t* __restrict__ seq_chunk0, int nseq, int seq_len, int Hqk,
-    int Hv, const uint8_t* __restrict__ work) {
+    const int32_t* __restrict__ cu, const int32_t* __restrict__ seq_chunk0, const int32_t* __restrict__ rows,
+    int n_rows, int nseq, int seq_len, int Hqk, int Hv, const uint8_t* __restrict__ work) {
   using namespace pf;
   __shared__ ScanSmem sm;
   // block -> (sequence-head pair, slice); the 8 slices of a pair share blockIdx % 8 and therefore an
@@ -764,12 +770,14 @@ __global__ __launch_bounds__(pf::NT, 1) void chunk_scan_kernel(
 
   if (role == 0) {
     // ---------------- chain wave ----------------
-    const int64_t sbase = ((int64_t)seq * Hv + h) * D * D + col;
+    const int srow = state_row(rows, n_rows, seq);  // slot row of this sequence's states (-1: none)
+    const int64_t sbase = ((int64_t)(srow < 0 ? 0 : srow) * Hv + h) * D * D + col;
     f32x4 S[8];
 #pragma unroll
     for (int rb = 0; rb < 8; ++rb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) S[rb][r] = init ? init[sbase + (int64_t)(16 * rb + 4 * g4 + r) * D] : 0.f;
+      for (int r = 0; r < 4; ++r)
+        S[rb][r] = (init && srow >= 0) ? init[sbase + (int64_t)(16 * rb + 4 * g4 + r) * D] : 0.f;
     bf16x8 Sb[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -865,7 +873,7 @@ __global__ __launch_bounds__(pf::NT, 1) void chunk_scan_kernel(
       __syncthreads();  // end of step c
     }
     __syncthreads();  // step nch (the output wave's last chunk)
-    if (final_state) {
+    if (final_state && srow >= 0) {
 #pragma unroll
       for (int rb = 0; rb < 8; ++rb)
 #pragma unroll
@@ -930,10 +938,11 @@ __global__ __launch_bounds__(pf::NT, 1) void chunk_scan_kernel(
 // Causal depthwise conv prefill + SiLU with decode-state capture.
 // ============================================================================================
 // One thread per (packed token p, 8 channels): it loads the K input rows p-K+1..p with 16-byte
-// reads (rows before its sequence come from `history` [n_seq, C, K], x_{-j} = history[K - j], or
-// are zero), writes 8 outputs with one 16-byte store, and -- for the last token of a sequence --
-// the sequence's decode conv state (its last K inputs).  Numerics of F.conv1d on bf16: fp32
-// accumulation of the K products (+ bias), one bf16 rounding, SiLU, bf16.
+// reads (rows before its sequence come from the sequence's history row [C, K], x_{-j} = history[K - j],
+// or are zero) and writes 8 outputs with one 16-byte store.  Numerics of F.conv1d on bf16: fp32
+// accumulation of the K products (+ bias), one bf16 rounding, SiLU, bf16.  The decode conv state a
+// sequence leaves (its last K inputs) is written afterwards by conv_state_capture_kernel, so the
+// history may be the same slot rows the state goes to.
 __device__ __forceinline__ int find_seq(const int32_t* cu, int nseq, int64_t p) {
   int lo = 0, hi = nseq - 1;  // last sequence whose start <= p (skips empty ones)
   while (lo < hi) {
@@ -949,7 +958,8 @@ __global__ __launch_bounds__(256) void conv_prefill_kernel(const uint16_t* __res
                                                            const uint16_t* __restrict__ weight,
                                                            const uint16_t* __restrict__ bias,
                                                            const uint16_t* __restrict__ history,
-                                                           uint16_t* __restrict__ out, uint16_t* __restrict__ state,
+                                                           const int32_t* __restrict__ rows, int n_rows,
+                                                           uint16_t* __restrict__ out,
                                                            const int32_t* __restrict__ cu, int nseq, int seq_len,
                                                            int C) {
   const int cg = blockIdx.x * blockDim.x + threadIdx.x;  // 8-channel group
@@ -959,6 +969,7 @@ __global__ __launch_bounds__(256) void conv_prefill_kernel(const uint16_t* __res
   const int s = cu ? find_seq(cu, nseq, p) : (int)(p / seq_len);
   const int64_t s_lo = cu ? (int64_t)cu[s] : (int64_t)s * seq_len;
   const int64_t s_hi = cu ? (int64_t)cu[s + 1] : s_lo + seq_len;
+  const int hrow = history ? state_row(rows, n_rows, s) : -1;
   u16x8 win[K];
 #pragma unroll
   for (int r = 0; r < K; ++r) {
@@ -969,7 +980,7 @@ __global__ __launch_bounds__(256) void conv_prefill_kernel(const uint16_t* __res
       const int back = (int)(s_lo - tok);  // 1..K-1
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        win[r][e] = history ? history[((int64_t)s * C + c0 + e) * K + (K - back)] : (uint16_t)0;
+        win[r][e] = hrow >= 0 ? history[((int64_t)hrow * C + c0 + e) * K + (K - back)] : (uint16_t)0;
     }
   }
   u16x8 wt[K];  // weight[c0 + e][r] -> wt[r][e]
@@ -989,25 +1000,31 @@ __global__ __launch_bounds__(256) void conv_prefill_kernel(const uint16_t* __res
     o[e] = f2bf(silu_f(rbf(acc)));
   }
   *reinterpret_cast<u16x8*>(out + p * (int64_t)C + c0) = o;
-  if (state && p == s_hi - 1) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-#pragma unroll
-      for (int r = 0; r < K; ++r) state[((int64_t)s * C + c0 + e) * K + r] = win[r][e];
-  }
 }
 
-// Sequences shorter than K keep part of their history; empty sequences keep all of it.  The main
-// kernel writes the state of every non-empty sequence (its window already holds the history);
-// this pass fills the state of empty ones.
-__global__ void conv_prefill_empty_kernel(const uint16_t* __restrict__ history, uint16_t* __restrict__ state,
+// The decode conv state each sequence leaves: its last K inputs, the front filled from its history
+// row (or zeros) when the sequence is shorter than K -- an empty sequence keeps its history.  One
+// thread per (sequence, channel) reads its old row entries before writing them, so `history` and
+// `state` may be the same slot rows.
+__global__ void conv_state_capture_kernel(const uint16_t* __restrict__ x, int64_t x_stride,
+                                          const uint16_t* history, const int32_t* __restrict__ hist_rows,
+                                          uint16_t* state, const int32_t* __restrict__ state_rows, int n_rows,
                                           const int32_t* __restrict__ cu, int nseq, int seq_len, int C, int K) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= (int64_t)nseq * C) return;
-  const int s = (int)(i / C);
-  const int L = cu ? cu[s + 1] - cu[s] : seq_len;
-  if (L != 0) return;
-  for (int j = 0; j < K; ++j) state[i * K + j] = history ? history[i * K + j] : (uint16_t)0;
+  const int s = (int)(i / C), c = (int)(i % C);
+  const int orow = state_row(state_rows, n_rows, s);
+  if (orow < 0) return;
+  const int hrow = history ? state_row(hist_rows, n_rows, s) : -1;
+  const int64_t s_lo = cu ? (int64_t)cu[s] : (int64_t)s * seq_len;
+  const int64_t L = cu ? (int64_t)cu[s + 1] - s_lo : seq_len;
+  uint16_t win[8];
+  for (int j = 0; j < K; ++j) {  // win[j] = input K - j before the end of the sequence
+    const int64_t tok = L - K + j;  // position inside the sequence
+    if (tok >= 0) win[j] = x[(s_lo + tok) * x_stride + c];
+    else win[j] = hrow >= 0 ? history[((int64_t)hrow * C + c) * K + (K + tok)] : (uint16_t)0;
+  }
+  for (int j = 0; j < K; ++j) state[((int64_t)orow * C + c) * K + j] = win[j];
 }
 
 // ============================================================================================
@@ -1042,13 +1059,16 @@ extern "C" int64_t gdn_chunk_prefill_workspace_bytes(int64_t total_chunks, int H
   return total_chunks * (int64_t)Hv * ws::BYTES;
 }
 
-extern "C" int gdn_chunk_prefill(const void* q, int64_t q_stride, const void* k, int64_t k_stride,
-                                 const void* v, int64_t v_stride, const float* g, const void* beta,
-                                 int beta_dtype, const float* initial_state, float* final_state, void* out,
-                                 int64_t total_tokens, const int32_t* cu_seqlens, const int32_t* seq_chunk0,
-                                 int64_t total_chunks, int nseq, int seq_len, int Hqk, int Hv, int D, int in_dtype,
-                                 int use_qk_l2norm, void* workspace, int64_t workspace_bytes, void* stream) {
+extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const void* k, int64_t k_stride,
+                                      const void* v, int64_t v_stride, const float* g, const void* beta,
+                                      int beta_dtype, const float* initial_state, float* final_state,
+                                      const int32_t* state_rows, int n_rows, void* out, int64_t total_tokens,
+                                      const int32_t* cu_seqlens, const int32_t* seq_chunk0, int64_t total_chunks,
+                                      int nseq, int seq_len, int Hqk, int Hv, int D, int in_dtype,
+                                      int use_qk_l2norm, void* workspace, int64_t workspace_bytes, void* stream) {
   clear_error();
+  GDN_REQUIRE(state_rows ? n_rows >= 0 : n_rows == nseq,
+              "gdn_chunk_prefill: without state_rows, n_rows must equal nseq");
   GDN_REQUIRE(q && k && v && g && beta && out, "gdn_chunk_prefill: null input/output pointer");
   GDN_SUPPORT(D == pf::D, "gdn_chunk_prefill: head dim %d unsupported (needs %d)", D, pf::D);
   GDN_SUPPORT(in_dtype == GDN_BF16, "gdn_chunk_prefill: q/k/v must be bfloat16 (MFMA operands)");
@@ -1090,19 +1110,35 @@ extern "C" int gdn_chunk_prefill(const void* q, int64_t q_stride, const void* k,
   const int64_t pairs = (int64_t)nseq * Hv;
   const int64_t scan_blocks = (pairs + 7) / 8 * 64;
   chunk_scan_kernel<uint16_t><<<(unsigned)scan_blocks, pf::NT, 0, s>>>(
-      initial_state, final_state, (uint16_t*)out, cu_seqlens, seq_chunk0, nseq, seq_len, Hqk, Hv, work);
+      initial_state, final_state, (uint16_t*)out, cu_seqlens, seq_chunk0, state_rows, n_rows, nseq, seq_len, Hqk,
+      Hv, work);
   return check_launch("gdn_chunk_prefill(state)");
 }
 
-extern "C" int gdn_conv_prefill(const void* x, int64_t x_stride, const void* weight, const void* bias,
-                                const void* history, void* out, void* state_out, int64_t total_tokens,
-                                const int32_t* cu_seqlens, int nseq, int seq_len, int C, int K, void* stream) {
+extern "C" int gdn_chunk_prefill(const void* q, int64_t q_stride, const void* k, int64_t k_stride,
+                                 const void* v, int64_t v_stride, const float* g, const void* beta,
+                                 int beta_dtype, const float* initial_state, float* final_state, void* out,
+                                 int64_t total_tokens, const int32_t* cu_seqlens, const int32_t* seq_chunk0,
+                                 int64_t total_chunks, int nseq, int seq_len, int Hqk, int Hv, int D, int in_dtype,
+                                 int use_qk_l2norm, void* workspace, int64_t workspace_bytes, void* stream) {
+  return gdn_chunk_prefill_rows(q, q_stride, k, k_stride, v, v_stride, g, beta, beta_dtype, initial_state,
+                                final_state, nullptr, nseq, out, total_tokens, cu_seqlens, seq_chunk0, total_chunks,
+                                nseq, seq_len, Hqk, Hv, D, in_dtype, use_qk_l2norm, workspace, workspace_bytes,
+                                stream);
+}
+
+extern "C" int gdn_conv_prefill_rows(const void* x, int64_t x_stride, const void* weight, const void* bias,
+                                     const void* history, void* out, void* state_out, const int32_t* state_rows,
+                                     int n_rows, int64_t total_tokens, const int32_t* cu_seqlens, int nseq,
+                                     int seq_len, int C, int K, void* stream) {
   clear_error();
   GDN_REQUIRE(x && weight && out, "gdn_conv_prefill: null pointer");
   GDN_REQUIRE(C > 0 && K >= 1 && nseq >= 0 && total_tokens >= 0, "gdn_conv_prefill: bad sizes");
   GDN_SUPPORT(K <= 8, "gdn_conv_prefill: kernel size %d > 8", K);
   GDN_REQUIRE(cu_seqlens || (int64_t)nseq * seq_len == total_tokens,
               "gdn_conv_prefill: nseq*seq_len != total_tokens without cu_seqlens");
+  GDN_REQUIRE(state_rows ? n_rows >= 0 : n_rows == nseq,
+              "gdn_conv_prefill: without state_rows, n_rows must equal nseq");
   hipStream_t s = (hipStream_t)stream;
   if (total_tokens > 0) {
     GDN_REQUIRE(C % 8 == 0 && x_stride % 8 == 0 && aligned(x, 16) && aligned(out, 16),
@@ -1112,8 +1148,8 @@ extern "C" int gdn_conv_prefill(const void* x, int64_t x_stride, const void* wei
 #define GDN_CONV_PREFILL(KK)                                                                                    \
   case KK:                                                                                                     \
     conv_prefill_kernel<KK><<<grid, 256, 0, s>>>((const uint16_t*)x, x_stride, (const uint16_t*)weight,          \
-                                                 (const uint16_t*)bias, (const uint16_t*)history, (uint16_t*)out, \
-                                                 (uint16_t*)state_out, cu_seqlens, nseq, seq_len, C);              \
+                                                 (const uint16_t*)bias, (const uint16_t*)history, state_rows,      \
+                                                 n_rows, (uint16_t*)out, cu_seqlens, nseq, seq_len, C);            \
     break;
     switch (K) {
       GDN_CONV_PREFILL(1)
@@ -1131,11 +1167,19 @@ extern "C" int gdn_conv_prefill(const void* x, int64_t x_stride, const void* wei
   }
   if (state_out && nseq > 0) {
     const int64_t n = (int64_t)nseq * C;
-    conv_prefill_empty_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(
-        (const uint16_t*)history, (uint16_t*)state_out, cu_seqlens, nseq, seq_len, C, K);
-    return check_launch("gdn_conv_prefill(empty)");
+    conv_state_capture_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(
+        (const uint16_t*)x, x_stride, (const uint16_t*)history, state_rows, (uint16_t*)state_out, state_rows,
+        n_rows, cu_seqlens, nseq, seq_len, C, K);
+    return check_launch("gdn_conv_prefill(state)");
   }
   return GDN_OK;
+}
+
+extern "C" int gdn_conv_prefill(const void* x, int64_t x_stride, const void* weight, const void* bias,
+                                const void* history, void* out, void* state_out, int64_t total_tokens,
+                                const int32_t* cu_seqlens, int nseq, int seq_len, int C, int K, void* stream) {
+  return gdn_conv_prefill_rows(x, x_stride, weight, bias, history, out, state_out, nullptr, nseq, total_tokens,
+                               cu_seqlens, nseq, seq_len, C, K, stream);
 }
 
 extern "C" int gdn_gating(const void* a, const void* b, int64_t ab_stride, const float* A_log,

@@ -63,13 +63,28 @@ def _chunk_table(B, T, cu_seqlens, device):
     return cu, s0.to(device=device, dtype=torch.int32), host.numel() - 1, 0, int(s0[-1])
 
 
+def _check_rows(state_rows, nseq, n_rows, device):
+    """Slot rows (int32 [n_seq] on the device), checked on the host: every row in [0, n_rows)."""
+    rows = torch.as_tensor(state_rows).reshape(-1)
+    if rows.numel() != nseq:
+        raise ValueError(f"state_rows must hold one row per sequence ({nseq})")
+    host = rows.detach().to("cpu", torch.int64)
+    if nseq and (int(host.min()) < 0 or int(host.max()) >= n_rows):
+        raise ValueError(f"state_rows must lie in [0, {n_rows})")
+    return rows.to(device=device, dtype=torch.int32).contiguous()
+
+
 def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size=64, initial_state=None,
                            output_final_state=False, use_qk_l2norm_in_kernel=False, cu_seqlens=None,
-                           **kwargs):
+                           state_rows=None, final_state_out=None, **kwargs):
     """query/key [B,T,Hqk,d] (Hqk = Hv after repeat_interleave, or Hv/r key heads read by value
     head h as h // r), value [B,T,Hv,d] bf16, g [B,T,Hv] (log decay, read in fp32), beta
     [B,T,Hv], initial_state [B or n_seq, Hv, d, d] | None.
-    Returns (out [B,T,Hv,d] query.dtype, final_state [B or n_seq,Hv,d,d] fp32 | None)."""
+    Returns (out [B,T,Hv,d] query.dtype, final_state [B or n_seq,Hv,d,d] fp32 | None).
+    Slot rows (added for a continuous-batching engine): with ``state_rows`` (int [n_seq]) the states
+    live in slot buffers -- ``initial_state`` (or None = zero) and ``final_state_out`` are fp32
+    [n_rows, Hv, d, d], sequence s uses row state_rows[s], and the two may be the same tensor; the
+    final state is then written there and returned."""
     if chunk_size <= 0:
         raise ValueError("chunk_size must be positive")
     _lib.require_cuda(query, key, value, g, beta, initial_state, cu_seqlens)
@@ -91,19 +106,32 @@ def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size=64, initial_st
     if beta.dtype not in (torch.float32, torch.bfloat16):
         beta = beta.to(torch.float32)
     beta = beta.contiguous()
-    init = None
-    if initial_state is not None:
-        if tuple(initial_state.shape) != (nseq, Hv, D, D):
-            raise ValueError(f"chunk_gated_delta_rule: initial_state must be [{nseq},{Hv},{D},{D}]")
-        init = initial_state.to(torch.float32).contiguous()
-    final = torch.empty(nseq, Hv, D, D, dtype=torch.float32, device=dev) if output_final_state else None
+    rows, n_rows = None, nseq
+    if state_rows is not None:
+        if final_state_out is None:
+            raise ValueError("chunk_gated_delta_rule: state_rows needs final_state_out (the slot buffer)")
+        n_rows = final_state_out.shape[0]
+        for name, t in (("final_state_out", final_state_out), ("initial_state", initial_state)):
+            if t is not None and (tuple(t.shape) != (n_rows, Hv, D, D) or t.dtype != torch.float32
+                                  or not t.is_contiguous() or t.device != dev):
+                raise ValueError(f"chunk_gated_delta_rule: {name} must be a contiguous fp32 "
+                                 f"[{n_rows},{Hv},{D},{D}] slot buffer on {dev}")
+        rows = _check_rows(state_rows, nseq, n_rows, dev)
+        init, final = initial_state, final_state_out
+    else:
+        init = None
+        if initial_state is not None:
+            if tuple(initial_state.shape) != (nseq, Hv, D, D):
+                raise ValueError(f"chunk_gated_delta_rule: initial_state must be [{nseq},{Hv},{D},{D}]")
+            init = initial_state.to(torch.float32).contiguous()
+        final = torch.empty(nseq, Hv, D, D, dtype=torch.float32, device=dev) if output_final_state else None
     out = torch.empty(B, T, Hv, D, dtype=query.dtype, device=dev)
     wbytes = int(_lib.lib().gdn_chunk_prefill_workspace_bytes(total_chunks, Hv))
     work = torch.empty(max(wbytes, 1), dtype=torch.uint8, device=dev)
-    _lib.call("gdn_chunk_prefill", _lib.ptr(q), qs, _lib.ptr(k), ks, _lib.ptr(v), vs, _lib.ptr(g32),
-              _lib.ptr(beta), _lib.dtype_code(beta), _lib.ptr(init), _lib.ptr(final), _lib.ptr(out),
-              B * T, _lib.ptr(cu), _lib.ptr(seq_chunk0), total_chunks, nseq, seq_len, Hqk, Hv, D,
-              _lib.dtype_code(query), int(bool(use_qk_l2norm_in_kernel)), _lib.ptr(work), wbytes,
+    _lib.call("gdn_chunk_prefill_rows", _lib.ptr(q), qs, _lib.ptr(k), ks, _lib.ptr(v), vs, _lib.ptr(g32),
+              _lib.ptr(beta), _lib.dtype_code(beta), _lib.ptr(init), _lib.ptr(final), _lib.ptr(rows), n_rows,
+              _lib.ptr(out), B * T, _lib.ptr(cu), _lib.ptr(seq_chunk0), total_chunks, nseq, seq_len, Hqk, Hv,
+              D, _lib.dtype_code(query), int(bool(use_qk_l2norm_in_kernel)), _lib.ptr(work), wbytes,
               _lib.stream_of(query))
     return out, final
 
@@ -129,13 +157,16 @@ def _unit_lower_inv(X, base=16):
     return out
 
 
-def causal_conv1d_prefill(x, weight, bias=None, history=None, cu_seqlens=None):
+def causal_conv1d_prefill(x, weight, bias=None, history=None, cu_seqlens=None, state_rows=None, state_out=None):
     """Depthwise causal conv (kernel K) + SiLU over prompts, plus the decode conv state they leave.
     x [B, C, L] bf16 (HF layout; token-major memory such as ``mixed_qkv.transpose(1, 2)`` is read
     in place); history [n_seq, C, K] | None (None = fresh prompt, zero history: F.conv1d with
     padding K-1, src/cb_tp.py:163-164; given = the previous K inputs, src/cb_tp.py:236-244).
     Returns (out [B, C, L] bf16 with token-major memory, state [n_seq, C, K] = the last K inputs,
-    left zero-padded, src/cb_tp.py:158-162, :260)."""
+    left zero-padded, src/cb_tp.py:158-162, :260).
+    Slot rows: with ``state_rows`` (int [n_seq]) ``history`` (or None = zero) and ``state_out`` are
+    bf16 [n_rows, C, K] slot buffers, sequence s uses row state_rows[s], and the two may be the same
+    tensor; the new states are written there and ``state_out`` is returned."""
     _lib.require_cuda(x, weight, bias, history, cu_seqlens)
     B, C, L = x.shape
     K = weight.shape[-1]
@@ -149,15 +180,28 @@ def causal_conv1d_prefill(x, weight, bias=None, history=None, cu_seqlens=None):
     w = weight.reshape(C, K).contiguous()
     if bias is not None:
         bias = bias.to(torch.bfloat16).contiguous()
-    if history is not None:
-        if tuple(history.shape) != (nseq, C, K):
-            raise ValueError(f"causal_conv1d_prefill: history must be [{nseq},{C},{K}]")
-        history = history.to(torch.bfloat16).contiguous()
+    rows, n_rows = None, nseq
+    if state_rows is not None:
+        if state_out is None:
+            raise ValueError("causal_conv1d_prefill: state_rows needs state_out (the slot buffer)")
+        n_rows = state_out.shape[0]
+        for name, t in (("state_out", state_out), ("history", history)):
+            if t is not None and (tuple(t.shape) != (n_rows, C, K) or t.dtype != torch.bfloat16
+                                  or not t.is_contiguous() or t.device != x.device):
+                raise ValueError(f"causal_conv1d_prefill: {name} must be a contiguous bf16 [{n_rows},{C},{K}] "
+                                 f"slot buffer on {x.device}")
+        rows = _check_rows(state_rows, nseq, n_rows, x.device)
+        state = state_out
+    else:
+        if history is not None:
+            if tuple(history.shape) != (nseq, C, K):
+                raise ValueError(f"causal_conv1d_prefill: history must be [{nseq},{C},{K}]")
+            history = history.to(torch.bfloat16).contiguous()
+        state = torch.empty(nseq, C, K, dtype=torch.bfloat16, device=x.device)
     out = torch.empty(B, L, C, dtype=torch.bfloat16, device=x.device)
-    state = torch.empty(nseq, C, K, dtype=torch.bfloat16, device=x.device)
-    _lib.call("gdn_conv_prefill", _lib.ptr(xt), xt.stride(1), _lib.ptr(w), _lib.ptr(bias),
-              _lib.ptr(history), _lib.ptr(out), _lib.ptr(state), B * L, _lib.ptr(cu), nseq, seq_len,
-              C, K, _lib.stream_of(x))
+    _lib.call("gdn_conv_prefill_rows", _lib.ptr(xt), xt.stride(1), _lib.ptr(w), _lib.ptr(bias),
+              _lib.ptr(history), _lib.ptr(out), _lib.ptr(state), _lib.ptr(rows), n_rows, B * L, _lib.ptr(cu),
+              nseq, seq_len, C, K, _lib.stream_of(x))
     return out.transpose(1, 2), state
 
 
@@ -180,29 +224,47 @@ def gdn_gating(a, b, A_log, dt_bias):
 
 def gdn_prefill_core(mixed_qkv, z, a, b, conv_weight, A_log, dt_bias, norm_weight, num_k_heads,
                      num_v_heads, head_dim, cu_seqlens=None, conv_history=None, initial_state=None,
-                     eps=1e-6, chunk_size=64, conv_bias=None):
+                     eps=1e-6, chunk_size=64, conv_bias=None, slots=None, conv_slots=None, rec_slots=None,
+                     continuation=False):
     """GDN prefill layer between in_proj_* and out_proj for one or more packed prompts
     (src/cb_tp.py:153-181 fresh, :230-263 continued): conv prefill + SiLU, split q|k|v, gating,
     chunked rule with l2norm (value head h reads key head h // r, no repeat_interleave copy),
     gated RMSNorm.  mixed_qkv [T, C] bf16 (pre-conv), z [T, Hv*d], a, b [T, Hv];
     cu_seqlens int32 [n_seq+1] | None; conv_history [n_seq, C, K] | None;
     initial_state [n_seq, Hv, d, d] | None.
-    Returns (core [T, Hv*d] bf16, conv_state [n_seq, C, K] bf16, rec_state [n_seq, Hv, d, d] fp32)."""
+    Returns (core [T, Hv*d] bf16, conv_state [n_seq, C, K] bf16, rec_state [n_seq, Hv, d, d] fp32).
+    Slot rows (the engine's state buffers, src/cb_engine.py:198-205, src/cb_tp.py:178-179, :256-262):
+    with ``slots`` (int [n_seq]) the states go straight into rows slots[s] of ``conv_slots``
+    [N, C, K] bf16 and ``rec_slots`` [N, Hv, d, d] fp32, and with ``continuation`` each sequence
+    first reads its conv history and initial state from those rows (a later chunk of a prompt);
+    then (core, conv_slots, rec_slots) is returned and conv_history / initial_state are not used."""
     T, C = mixed_qkv.shape
     Hk, Hv, D = num_k_heads, num_v_heads, head_dim
     if C != (2 * Hk + Hv) * D:
         raise ValueError(f"gdn_prefill_core: C={C} != (2*{Hk}+{Hv})*{D}")
     w = conv_weight.reshape(C, -1)
-    conv_out, conv_state = causal_conv1d_prefill(mixed_qkv.t().unsqueeze(0), w, conv_bias,
-                                                 conv_history, cu_seqlens)
+    if slots is not None:
+        if conv_slots is None or rec_slots is None:
+            raise ValueError("gdn_prefill_core: slots needs conv_slots and rec_slots")
+        conv_out, conv_state = causal_conv1d_prefill(mixed_qkv.t().unsqueeze(0), w, conv_bias,
+                                                     conv_slots if continuation else None, cu_seqlens,
+                                                     state_rows=slots, state_out=conv_slots)
+    else:
+        conv_out, conv_state = causal_conv1d_prefill(mixed_qkv.t().unsqueeze(0), w, conv_bias,
+                                                     conv_history, cu_seqlens)
     qkv = conv_out[0].t()                                     # [T, C] view, dense rows
     kd = Hk * D
     q = qkv[:, :kd].reshape(1, T, Hk, D)
     k = qkv[:, kd:2 * kd].reshape(1, T, Hk, D)
     v = qkv[:, 2 * kd:].reshape(1, T, Hv, D)
     beta, g = gdn_gating(a.reshape(1, T, Hv), b.reshape(1, T, Hv), A_log, dt_bias)
-    core, rec = chunk_gated_delta_rule(q, k, v, g, beta, chunk_size, initial_state, True, True,
-                                       cu_seqlens=cu_seqlens)
+    if slots is not None:
+        core, rec = chunk_gated_delta_rule(q, k, v, g, beta, chunk_size, rec_slots if continuation else None,
+                                           True, True, cu_seqlens=cu_seqlens, state_rows=slots,
+                                           final_state_out=rec_slots)
+    else:
+        core, rec = chunk_gated_delta_rule(q, k, v, g, beta, chunk_size, initial_state, True, True,
+                                           cu_seqlens=cu_seqlens)
     from .cb_engine import gated_rmsnorm
     core = gated_rmsnorm(core.reshape(T * Hv, D), z.reshape(T * Hv, D), norm_weight, eps)
     return core.reshape(T, Hv * D), conv_state, rec

@@ -159,6 +159,55 @@ int gdn_gating(const void* a, const void* b, int64_t ab_stride, const float* A_l
                const float* dt_bias, void* beta_out, float* g_out, int64_t rows, int Hv,
                void* stream);
 
+/*
+ * Slot-row variants for a continuous-batching engine's state buffers.  The engine keeps one row per
+ * slot: conv state [n_rows, C, K] bf16, recurrent state [n_rows, Hv, D, D] fp32
+ * (src/cb_engine.py:108-112).
+ */
+
+/*
+ * gdn_decode_fused for a dense step over all N slots where only some advance.  active [N] uint8
+ * (device): nonzero = advance the slot; a zero slot's conv and recurrent state are left untouched
+ * and its output rows are zero.  NULL = every slot advances (that is gdn_decode_fused).  Replaces
+ * the save / restore of held slots around the dense decode step (src/cb_tp.py:274-285).
+ */
+int gdn_decode_fused_masked(const void* mixed, int64_t mixed_stride, const void* z, int64_t z_stride,
+                            const void* a, const void* b, int64_t ab_stride, void* conv_state,
+                            const void* conv_w, const void* conv_b, const float* A_log,
+                            const float* dt_bias, const void* norm_w, int norm_w_dtype, float eps,
+                            float* rec_state, void* out, const uint8_t* active, int N, int Hk, int Hv,
+                            int D, int K, void* stream);
+
+/*
+ * gdn_chunk_prefill with the sequences' states in slot rows.  initial_state / final_state are
+ * [n_rows, Hv, D, D] fp32 and sequence s reads and writes row state_rows[s] (device int32 [nseq]);
+ * a row outside [0, n_rows) is neither read nor written (zero initial state, no final state).
+ * initial_state and final_state may be the same buffer (a continuation chunk updates its slot in
+ * place).  state_rows NULL: row s, and n_rows must equal nseq (that is gdn_chunk_prefill).
+ * Replaces the slot copies after prefill, self.rec[i][slot] = last (src/cb_tp.py:179, :262;
+ * src/cb_engine.py:198-205), and the continuation's initial_state = self.rec[i][slot]
+ * (src/cb_tp.py:256).
+ */
+int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const void* k, int64_t k_stride,
+                           const void* v, int64_t v_stride, const float* g, const void* beta,
+                           int beta_dtype, const float* initial_state, float* final_state,
+                           const int32_t* state_rows, int n_rows, void* out, int64_t total_tokens,
+                           const int32_t* cu_seqlens, const int32_t* seq_chunk0, int64_t total_chunks,
+                           int nseq, int seq_len, int Hqk, int Hv, int D, int in_dtype,
+                           int use_qk_l2norm, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * gdn_conv_prefill with history and decode conv state in slot rows [n_rows, C, K] bf16: sequence
+ * s reads its history from row state_rows[s] and writes its new state there (rows outside
+ * [0, n_rows): zero history, no state).  history and state_out may be the same buffer.
+ * Replaces self.conv[i][slot] = conv_state / full_in[..., -K:] and the continuation's
+ * prev = self.conv[i][slot] (src/cb_tp.py:178, :240, :260).
+ */
+int gdn_conv_prefill_rows(const void* x, int64_t x_stride, const void* weight, const void* bias,
+                          const void* history, void* out, void* state_out, const int32_t* state_rows,
+                          int n_rows, int64_t total_tokens, const int32_t* cu_seqlens, int nseq,
+                          int seq_len, int C, int K, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -25,7 +25,8 @@ def lib():
 def test_header_declares_entry_points():
     syms = declared_symbols()
     for name in ("gdn_recurrent_step", "gdn_conv_update", "gdn_gated_rmsnorm", "gdn_decode_fused",
-                 "gdn_chunk_prefill", "gdn_conv_prefill", "gdn_gating", "gdn_unit_lower_inv"):
+                 "gdn_chunk_prefill", "gdn_conv_prefill", "gdn_gating", "gdn_unit_lower_inv",
+                 "gdn_decode_fused_masked", "gdn_chunk_prefill_rows", "gdn_conv_prefill_rows"):
         assert name in syms
 
 
@@ -54,6 +55,15 @@ def test_version_limits_and_error_path(lib):
     rc = h.gdn_decode_fused(p, 0, p, 0, p, p, 0, p, p, None, p, p, p, 1, ctypes.c_float(1e-6), p, p,
                             1, 16, 32, 64, 4, None)
     assert rc == 2 and b"head dim" in h.gdn_last_error()
+    rc = h.gdn_decode_fused_masked(p, 0, p, 0, p, p, 0, p, p, None, p, p, p, 1, ctypes.c_float(1e-6), p, p,
+                                   None, 1, 16, 32, 64, 4, None)
+    assert rc == 2 and b"head dim" in h.gdn_last_error()
+    # without state_rows the slot-row variants need n_rows == nseq
+    rc = h.gdn_chunk_prefill_rows(p, 0, p, 0, p, 0, p, p, 1, None, None, None, 3, p, 64, None, None, 1, 2, 32,
+                                  16, 32, 128, 1, 1, p, 1 << 30, None)
+    assert rc == 1 and b"n_rows" in h.gdn_last_error()
+    rc = h.gdn_conv_prefill_rows(p, 8, p, None, None, p, None, None, 5, 8, None, 1, 8, 8, 4, None)
+    assert rc == 1 and b"n_rows" in h.gdn_last_error()
     need = h.gdn_chunk_prefill_workspace_bytes(10, 32)
     assert need > 0 and need % 256 == 0
     with pytest.raises(lib.GDNError):

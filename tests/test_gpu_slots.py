@@ -1,0 +1,102 @@
+"""GPU tests of the continuous-batching slot paths: prefill whose conv and recurrent states go
+straight into slot rows (fresh and continuation chunks, src/cb_tp.py:153-263), and the masked
+decode step that leaves held slots untouched (src/cb_tp.py:274-285)."""
+import pytest
+import torch
+
+from conftest import rel_l2
+
+OUT_TOL, STATE_TOL = 1e-2, 1e-3
+Hk, Hv, D, K = 4, 8, 128, 4
+C = (2 * Hk + Hv) * D
+
+
+def _layer_inputs(T, seed):
+    g_ = torch.Generator().manual_seed(seed)
+    mixed = torch.randn(T, C, generator=g_).to(torch.bfloat16)
+    z = torch.randn(T, Hv * D, generator=g_).to(torch.bfloat16)
+    a = torch.randn(T, Hv, generator=g_).to(torch.bfloat16)
+    b = torch.randn(T, Hv, generator=g_).to(torch.bfloat16)
+    return mixed, z, a, b
+
+
+def _params(seed):
+    g_ = torch.Generator().manual_seed(seed)
+    cw = (0.5 * torch.randn(C, K, generator=g_)).to(torch.bfloat16)
+    A_log = torch.full((Hv,), -2.302585)
+    dt = torch.full((Hv,), 2.0)
+    nw = (1 + 0.02 * torch.randn(D, generator=g_)).to(torch.bfloat16)
+    return cw, A_log, dt, nw
+
+
+@pytest.mark.gpu
+def test_prefill_into_slot_rows(gdn, dev):
+    """3 packed prompts into slots [5, 0, 3] of an 8-slot engine: those rows equal the plain call's
+    states bit for bit, every other row is untouched."""
+    cu = torch.tensor([0, 70, 198, 231], dtype=torch.int32)
+    T = 231
+    mixed, z, a, b = (x.to(dev) for x in _layer_inputs(T, 30))
+    cw, A_log, dt, nw = (x.to(dev) for x in _params(31))
+    cud = cu.to(dev)
+    core_ref, conv_ref, rec_ref = gdn.gdn_prefill_core(mixed, z, a, b, cw, A_log, dt, nw, Hk, Hv, D,
+                                                       cu_seqlens=cud)
+    g_ = torch.Generator().manual_seed(32)
+    conv_slots = torch.randn(8, C, K, generator=g_).to(torch.bfloat16).to(dev)
+    rec_slots = torch.randn(8, Hv, D, D, generator=g_).to(dev)
+    conv0, rec0 = conv_slots.clone(), rec_slots.clone()
+    slots = torch.tensor([5, 0, 3], dtype=torch.int32, device=dev)
+    core, cs, rs = gdn.gdn_prefill_core(mixed, z, a, b, cw, A_log, dt, nw, Hk, Hv, D, cu_seqlens=cud,
+                                        slots=slots, conv_slots=conv_slots, rec_slots=rec_slots)
+    assert cs is conv_slots and rs is rec_slots
+    assert torch.equal(core, core_ref)
+    for i, r in enumerate([5, 0, 3]):
+        assert torch.equal(conv_slots[r], conv_ref[i]) and torch.equal(rec_slots[r], rec_ref[i])
+    for r in (1, 2, 4, 6, 7):
+        assert torch.equal(conv_slots[r], conv0[r]) and torch.equal(rec_slots[r], rec0[r])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("split", [1, 2, 64, 100])
+def test_prefill_continuation_through_slots(gdn, dev, split):
+    """A prompt prefilled in two chunks through its slot row (the second chunk reads the conv history
+    and recurrent state the first left there, src/cb_tp.py:230-263) matches one pass."""
+    T = 150
+    mixed, z, a, b = (x.to(dev) for x in _layer_inputs(T, 33))
+    cw, A_log, dt, nw = (x.to(dev) for x in _params(34))
+    core_ref, conv_ref, rec_ref = gdn.gdn_prefill_core(mixed, z, a, b, cw, A_log, dt, nw, Hk, Hv, D)
+    conv_slots = torch.zeros(4, C, K, dtype=torch.bfloat16, device=dev)
+    rec_slots = torch.zeros(4, Hv, D, D, device=dev)
+    slots = torch.tensor([2], dtype=torch.int32, device=dev)
+    parts = []
+    for lo, hi, cont in ((0, split, False), (split, T, True)):
+        c, _, _ = gdn.gdn_prefill_core(mixed[lo:hi], z[lo:hi], a[lo:hi], b[lo:hi], cw, A_log, dt, nw, Hk, Hv, D,
+                                       slots=slots, conv_slots=conv_slots, rec_slots=rec_slots,
+                                       continuation=cont)
+        parts.append(c)
+    core = torch.cat(parts)
+    assert torch.equal(conv_slots[2], conv_ref[0])  # the conv window is pure data movement
+    assert rel_l2(core, core_ref) <= OUT_TOL and rel_l2(rec_slots[2], rec_ref[0]) <= STATE_TOL
+    assert torch.count_nonzero(conv_slots[[0, 1, 3]]) == 0 and torch.count_nonzero(rec_slots[[0, 1, 3]]) == 0
+
+
+@pytest.mark.gpu
+def test_decode_masked_slots(gdn, dev):
+    """A dense decode step with held slots: held rows keep their conv and recurrent state bit for bit
+    and output zeros; active rows equal the unmasked step's."""
+    N = 5
+    mixed, z, a, b = (x.to(dev) for x in _layer_inputs(N, 35))
+    cw, A_log, dt, nw = (x.to(dev) for x in _params(36))
+    g_ = torch.Generator().manual_seed(37)
+    conv0 = torch.randn(N, C, K, generator=g_).to(torch.bfloat16).to(dev)
+    rec0 = (0.02 * torch.randn(N, Hv, D, D, generator=g_)).to(dev)
+    cs_ref, rs_ref = conv0.clone(), rec0.clone()
+    o_ref = gdn.gdn_decode_core(mixed, z, a, b, cs_ref, cw, A_log, dt, nw, rs_ref, Hk, Hv, D)
+    active = torch.tensor([1, 0, 1, 1, 0], dtype=torch.bool, device=dev)
+    cs, rs = conv0.clone(), rec0.clone()
+    o = gdn.gdn_decode_core(mixed, z, a, b, cs, cw, A_log, dt, nw, rs, Hk, Hv, D, active=active)
+    for n in range(N):
+        if active[n]:
+            assert torch.equal(o[n], o_ref[n]) and torch.equal(cs[n], cs_ref[n]) and torch.equal(rs[n], rs_ref[n])
+        else:
+            assert torch.count_nonzero(o[n]) == 0
+            assert torch.equal(cs[n], conv0[n]) and torch.equal(rs[n], rec0[n])
