@@ -593,26 +593,33 @@ __global__ __launch_bounds__(pf::NT, 3) void chunk_local_kernel(
 // Chunked prefill, part 2: the inter-chunk state recurrence (the scan).
 // ============================================================================================
 // One workgroup per (sequence, value head, 16-column slice of the state): 8 workgroups per head,
-// so a single long sequence still spreads over nseq * Hv * 8 workgroups.  The 4 waves specialise:
-//   wave 0 (chain):  vn = U - W S  and  S' = GL S + K^T (DEC vn); the fp32 state slice S [128, 16]
-//                    lives in 8 accumulator tiles for the whole sequence, and both products take
-//                    their B operand straight from accumulator registers (k-slot order)
-//   wave 1 (output): o = Qg S + QK vn one chunk behind the chain, from the S and vn the chain
-//                    published in LDS and Qg / QK fragments it loads itself two chunks ahead
-//   waves 2-3:       stage each chunk's WN and KT fragments, this slice's U tiles and the header
+// so a single long sequence still spreads over nseq * Hv * 8 workgroups.  The 6 waves specialise:
+//   waves 0-1 (chain): vn = U - W S  and  S' = GL S + K^T (DEC vn) with the fp32 state slice
+//                    S [128, 16] split by rows: wave 0 holds S rows 0-63, wave 1 rows 64-127, each in
+//                    4 accumulator tiles for the whole sequence.  Each wave forms its half of the
+//                    k-sum W S (8 MFMAs; wave 0 starts from U), the two partial sums are swapped
+//                    through LDS with a per-wave step flag, and each wave then updates its own rows
+//                    (8 MFMAs).  Both products take their B operand straight from accumulator
+//                    registers (k-slot order)
+//   waves 2-3 (output): o = Qg S + QK vn one chunk behind the chain (two token tiles each), from
+//                    the S and vn the chain published in LDS and Qg / QK fragments they load
+//                    themselves two chunks ahead
+//   waves 4-5:       stage each chunk's WN and KT fragments, this slice's U tiles and the header
 //                    (34.5 KiB) in a 3-slot LDS ring, loading them from global memory two chunks
 //                    before they are staged
 // One barrier per chunk.  During step c the chain computes chunk c from registers it read out of
 // ring slot c%3 during step c-1, reads chunk c+1 from slot (c+1)%3 into registers, and writes
-// vn(c) and S(c+1) into exchange slots c%3 and (c+1)%3; the output wave reads exchange slot (c-1)%3;
-// the loaders fill ring slot (c+2)%3.  So no LDS read latency sits on the chain's critical path.
+// vn(c) and S(c+1) into exchange slots c%3 and (c+1)%3; the output waves read exchange slot (c-1)%3;
+// the loaders fill ring slot (c+2)%3.  So no LDS read latency sits on the chain's critical path
+// beyond the partial-sum swap.
 // The state update runs on fp16 MFMA.  Usually DEC vn and K^T fit fp16 as they are (see the fast
 // path); otherwise DEC vn is scaled per column by a power of two sigma into [2^14, 2^15) and K^T
-// by kappa, and the product is folded in as S' = (GL sigma kappa S + P) / (sigma kappa), so the fp32
+// by kappa, and the product is folded in as S' = (GL S sigma kappa + P) / (sigma kappa), so the fp32
 // state only ever sees exact power-of-two rescaling besides the MFMA sum.
 namespace rg {  // one ring slot
 constexpr int WN = 0, KT = 16 * ws::FRAG, U = 32 * ws::FRAG, HDR = U + 2048, BYTES = HDR + 512;
 }  // namespace rg
+constexpr int kScanThreads = 384;  // 2 chain waves, 2 output waves, 2 loader waves
 __device__ __forceinline__ bf16x8 lds_frag(const uint8_t* base, int f, int lane) {
   return *reinterpret_cast<const bf16x8*>(base + f * ws::FRAG + lane * 16);
 }
@@ -622,34 +629,56 @@ __device__ __forceinline__ f16x8 lds_frag_h(const uint8_t* base, int f, int lane
 struct ScanSmem {
   uint8_t ring[3][rg::BYTES];
   uint8_t xch[3][6 * ws::FRAG];  // S (4 k-slot ordered bf16 B fragments) and vn (2)
+  f32x4 part[2][4][64];          // the chain waves' partial sums of vn, [wave][token tile][lane]
+  int flag[2];                   // step counter of each chain wave's published partial sum
 };
 
-// One chunk's chain operands in registers.
+// One chunk's operands for one chain wave (half = 0: S rows 0-63, 1: rows 64-127).
+// The KT fragments live outside: they are double-buffered, so that the next chunk's are read while
+// this chunk's update MFMAs still use theirs.
 struct ChainIn {
-  bf16x8 fw[16];  // WN fragments
-  f16x8 fk[16];   // KT fragments
-  f16x8 u[2];     // this lane's U values (tiles 0,1 | 2,3)
-  f32x4 dv[4];    // DEC of this lane's tokens
-  f32x4 usc;
+  bf16x8 fw[8];  // WN fragments (tb, k-block 2 half + j) at [tb * 2 + j]
+  f16x8 u[2];    // this lane's U values (tiles 0,1 | 2,3); wave 0 only
+  f32x4 dv[4];   // DEC of this lane's tokens
+  f32x4 usc;     // wave 0 only
   float gl, ksc, kap;
 };
+typedef f16x8 KFrags[8];  // KT fragments of row tiles 4 half .. 4 half + 3 (2 k-blocks each)
+template <int HALF>
 __device__ __forceinline__ void chain_read_w(ChainIn& in, const uint8_t* ring, int lane) {
   const int g4 = lane >> 4;
 #pragma unroll
-  for (int f = 0; f < 16; ++f) in.fw[f] = lds_frag(ring + rg::WN, f, lane);
+  for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) in.fw[tb * 2 + j] = lds_frag(ring + rg::WN, tb * 4 + 2 * HALF + j, lane);
   const float* hdr = reinterpret_cast<const float*>(ring + rg::HDR);
-  in.usc = *reinterpret_cast<const f32x4*>(hdr + (ws::USC - ws::HDR) / 4);
+  if (HALF == 0) {
+    in.usc = *reinterpret_cast<const f32x4*>(hdr + (ws::USC - ws::HDR) / 4);
+    in.u[0] = *reinterpret_cast<const f16x8*>(ring + rg::U + lane * 32);
+    in.u[1] = *reinterpret_cast<const f16x8*>(ring + rg::U + lane * 32 + 16);
+  }
   in.gl = hdr[(ws::GL - ws::HDR) / 4];
   in.ksc = hdr[(ws::KSC - ws::HDR) / 4];
   in.kap = hdr[(ws::KAP - ws::HDR) / 4];
-  in.u[0] = *reinterpret_cast<const f16x8*>(ring + rg::U + lane * 32);
-  in.u[1] = *reinterpret_cast<const f16x8*>(ring + rg::U + lane * 32 + 16);
 #pragma unroll
   for (int tb = 0; tb < 4; ++tb) in.dv[tb] = *reinterpret_cast<const f32x4*>(hdr + 16 * tb + 4 * g4);
 }
-__device__ __forceinline__ void chain_read_k(ChainIn& in, const uint8_t* ring, int lane) {
+template <int HALF>
+__device__ __forceinline__ void chain_read_k(KFrags& fk, const uint8_t* ring, int lane) {
 #pragma unroll
-  for (int f = 0; f < 16; ++f) in.fk[f] = lds_frag_h(ring + rg::KT, f, lane);
+  for (int f = 0; f < 8; ++f) fk[f] = lds_frag_h(ring + rg::KT, 8 * HALF + f, lane);
+}
+// Wait until the other chain wave has published step `target` (it always publishes before it waits
+// itself, so the wait ends; the bound only keeps a broken invariant from hanging the GPU).
+__device__ __forceinline__ void wait_flag(int* flag, int target) {
+  for (int i = 0; i < (1 << 18); ++i) {
+    const int v = __hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (__builtin_amdgcn_readfirstlane(v) == target) break;
+  }
+}
+// Publish step `value` after this wave's earlier LDS writes (release).
+__device__ __forceinline__ void set_flag(int* flag, int value, int lane) {
+  if (lane == 0) __hip_atomic_store(flag, value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 constexpr int kFragPieces = 2 * 16 * ws::FRAG / 16 / 128;  // WN + KT pieces of 16 bytes per loader lane
 constexpr int kLoadPieces = kFragPieces + 2;               // + one piece of U, + one of the header (lanes < 32)
@@ -673,71 +702,264 @@ __device__ __forceinline__ void scan_store(uint8_t* dst, const u16x8 (&r)[kLoadP
   if (lt < 32) *reinterpret_cast<u16x8*>(dst + rg::HDR + lt * 16) = r[kFragPieces + 1];
 }
 
-// The output wave's per-chunk operands: QG (16 fragments, from the key head's record), the 6
-// non-zero QK fragments and the row factors scale e^{G_t} of this lane's token in each tile.
+// An output wave's per-chunk operands.  Output wave P handles token tiles A = P and B = 3 - P (one
+// and two non-zero QK fragments: tile tb has QK fragments (tb, j) for j <= tb / 2), so the two
+// output waves do equal work: its QG fragments (8, from the key head's record), its 3 QK fragments
+// and the row factors scale e^{G_t} of this lane's token in each of its tiles.
 struct OutFrags {
-  bf16x8 qg[16], qk[6];
-  float egs[4];
+  bf16x8 qg[8], qk[3];
+  float egs[2];
 };
+template <int P>
 __device__ __forceinline__ void out_load(OutFrags& f, const uint8_t* rec, const uint8_t* rec_kq, int lane) {
+  constexpr int A = P, B = 3 - P;
   const float* eg = reinterpret_cast<const float*>(rec + ws::EGS) + (lane & 15);
-#pragma unroll
-  for (int tb = 0; tb < 4; ++tb) f.egs[tb] = eg[16 * tb];
+  f.egs[0] = eg[16 * A];
+  f.egs[1] = eg[16 * B];
   const uint8_t* qg = rec_kq + ws::QG + lane * 16;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) f.qg[i] = *reinterpret_cast<const bf16x8*>(qg + i * ws::FRAG);
+  for (int j = 0; j < 4; ++j) {
+    f.qg[j] = *reinterpret_cast<const bf16x8*>(qg + (A * 4 + j) * ws::FRAG);
+    f.qg[4 + j] = *reinterpret_cast<const bf16x8*>(qg + (B * 4 + j) * ws::FRAG);
+  }
   const uint8_t* qk = rec + ws::QK + lane * 16;
-  const int idx[6] = {0, 2, 4, 5, 6, 7};  // (tb, j) with j <= tb / 2: (0,0) (1,0) (2,0) (2,1) (3,0) (3,1)
-#pragma unroll
-  for (int i = 0; i < 6; ++i) f.qk[i] = *reinterpret_cast<const bf16x8*>(qk + idx[i] * ws::FRAG);
+  f.qk[0] = *reinterpret_cast<const bf16x8*>(qk + (A * 2) * ws::FRAG);
+  f.qk[1] = *reinterpret_cast<const bf16x8*>(qk + (B * 2) * ws::FRAG);
+  f.qk[2] = *reinterpret_cast<const bf16x8*>(qk + (B * 2 + 1) * ws::FRAG);
 }
 // o^T = S^T Qg^T + vn^T QK^T, tile by tile.  The k-slot ordered B fragments of S and vn are A
 // fragments of S^T and vn^T, and the QG / QK A fragments are B fragments of their transposes, so
 // the transposed products need no data movement -- and their accumulator layout gives each lane 4
 // consecutive output columns of one token: lane (c, g) holds o[16 tb + c][16 n + 4g .. 4g + 3].
-template <typename OutT>
+template <int P, typename OutT>
 __device__ __forceinline__ void out_step(const OutFrags& f, const uint8_t* xch, OutT* out, int64_t t0, int len,
                                          int Hv, int h, int col0, int lane) {
   using namespace pf;
+  constexpr int A = P, B = 3 - P;
   bf16x8 sb[4], vb[2];
 #pragma unroll
   for (int j = 0; j < 4; ++j) sb[j] = lds_frag(xch, j, lane);
 #pragma unroll
   for (int j = 0; j < 2; ++j) vb[j] = lds_frag(xch, 4 + j, lane);
-  f32x4 O[4];
+  f32x4 O[2];
 #pragma unroll
-  for (int tb = 0; tb < 4; ++tb) {
-    O[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < 2; ++i) {
+    O[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) O[tb] = mma(sb[j], f.qg[tb * 4 + j], O[tb]);
-    O[tb] *= f.egs[tb];
+    for (int j = 0; j < 4; ++j) O[i] = mma(sb[j], f.qg[i * 4 + j], O[i]);
+    O[i] *= f.egs[i];
   }
   O[0] = mma(vb[0], f.qk[0], O[0]);
   O[1] = mma(vb[0], f.qk[1], O[1]);
-  O[2] = mma(vb[0], f.qk[2], O[2]);
-  O[2] = mma(vb[1], f.qk[3], O[2]);
-  O[3] = mma(vb[0], f.qk[4], O[3]);
-  O[3] = mma(vb[1], f.qk[5], O[3]);
+  O[1] = mma(vb[1], f.qk[2], O[1]);
   const int c16 = lane & 15, g4 = lane >> 4;
 #pragma unroll
-  for (int tb = 0; tb < 4; ++tb) {
-    const int row = 16 * tb + c16;
+  for (int i = 0; i < 2; ++i) {
+    const int row = 16 * (i == 0 ? A : B) + c16;
     if (row < len) {
       OutT* o = out + ((t0 + row) * Hv + h) * D + col0 + 4 * g4;
       if constexpr (sizeof(OutT) == 2) {
         typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-        const u32x2 pk = {f2bf2(O[tb][0], O[tb][1]), f2bf2(O[tb][2], O[tb][3])};
+        const u32x2 pk = {f2bf2(O[i][0], O[i][1]), f2bf2(O[i][2], O[i][3])};
         *reinterpret_cast<u32x2*>(o) = pk;
       } else {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) Elem<OutT>::store(o + r, O[tb][r]);
+        for (int r = 0; r < 4; ++r) Elem<OutT>::store(o + r, O[i][r]);
       }
     }
   }
 }
+// An output wave: step c computes chunk c-1 (F0 / F1: even / odd chunks, loaded two chunks ahead).
+template <int P, typename OutT>
+__device__ __forceinline__ void output_wave(const ScanSmem& sm, const uint8_t* rec0, int64_t rstride,
+                                            int64_t kq_off, OutT* out, int64_t s0, int L, int nch, int Hv, int h,
+                                            int col0, int lane) {
+  using namespace pf;
+  OutFrags F0, F1;
+  if (nch > 0) out_load<P>(F0, rec0, rec0 + kq_off, lane);
+  __syncthreads();  // prologue
+  if (nch > 1) out_load<P>(F1, rec0 + rstride, rec0 + rstride + kq_off, lane);
+  __syncthreads();  // step 0
+  int xp = 0;       // (c - 1) % 3
+  for (int c = 1; c <= nch; c += 2) {
+    {
+      const int cc = c - 1;  // even
+      const int len = L - cc * CH < CH ? L - cc * CH : CH;
+      out_step<P, OutT>(F0, sm.xch[xp], out, s0 + (int64_t)cc * CH, len, Hv, h, col0, lane);
+      if (c + 1 < nch) out_load<P>(F0, rec0 + (int64_t)(c + 1) * rstride, rec0 + (int64_t)(c + 1) * rstride + kq_off, lane);
+      xp = xp == 2 ? 0 : xp + 1;
+      __syncthreads();  // end of step c
+    }
+    if (c + 1 <= nch) {
+      const int cc = c;  // odd
+      const int len = L - cc * CH < CH ? L - cc * CH : CH;
+      out_step<P, OutT>(F1, sm.xch[xp], out, s0 + (int64_t)cc * CH, len, Hv, h, col0, lane);
+      if (c + 2 < nch) out_load<P>(F1, rec0 + (int64_t)(c + 2) * rstride, rec0 + (int64_t)(c + 2) * rstride + kq_off, lane);
+      xp = xp == 2 ? 0 : xp + 1;
+      __syncthreads();  // end of step c+1
+    }
+  }
+}
+
+// One chain step for chunk c: `in` and `fk` hold chunk c's operands on entry; chunk c+1's are read
+// into `in` and `fk_next` once the partial sums are swapped (ring slot `nxt`).
+template <int HALF>
+__device__ __forceinline__ void chain_step(ScanSmem& sm, f32x4 (&S)[4], bf16x8 (&Sb)[2], ChainIn& in, KFrags& fk,
+                                           KFrags& fk_next, int c, int nch, int& x0, int lane) {
+  uint8_t* xch = sm.xch[x0];
+  const int x1 = x0 == 2 ? 0 : x0 + 1;
+  const uint8_t* nxt = sm.ring[x1];  // chunk c+1 sits in ring slot (c+1) % 3
+  // this wave's half of the k-sum: U (wave 0) + sum over S rows 64 HALF.. of WN S
+  f32x4 acc[4];
+  if (HALF == 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      acc[0][r] = (float)in.u[0][r];
+      acc[1][r] = (float)in.u[0][4 + r];
+      acc[2][r] = (float)in.u[1][r];
+      acc[3][r] = (float)in.u[1][4 + r];
+    }
+    // the tile scales are 1 unless |U| left [2^-4, 2^14) (same value in every lane)
+    const bool unit = in.usc[0] == 1.0f && in.usc[1] == 1.0f && in.usc[2] == 1.0f && in.usc[3] == 1.0f;
+    if (!__builtin_amdgcn_readfirstlane((int)unit)) {
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) acc[tb] *= in.usc[tb];
+    }
+  } else {
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) acc[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) acc[tb] = mma(in.fw[tb * 2 + j], Sb[j], acc[tb]);
+  // publish the partial sum, then the step flag (one wave's LDS writes complete in order)
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) sm.part[HALF][tb][lane] = acc[tb];
+  set_flag(&sm.flag[HALF], c + 1, lane);
+  f32x4 dv[4];
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) dv[tb] = in.dv[tb];
+  const float gl = in.gl, ksc = in.ksc, kap = in.kap;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    S[i] *= gl;
+    asm volatile("" : "+v"(S[i]));  // done while the other wave finishes its half
+  }
+  wait_flag(&sm.flag[1 - HALF], c + 1);
+  // vn = U - W S: both waves add the same two partial sums (a + b == b + a exactly)
+  f32x4 vn[4];
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) vn[tb] = acc[tb] + sm.part[1 - HALF][tb][lane];
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) asm volatile("" : "+v"(vn[tb]));  // complete before the reads below
+  // chunk c+1's operands: issued behind the partial-sum reads (whose completion the chain waits
+  // for; LDS returns in order and the wait counter saturates at 15), so they arrive while this
+  // chunk's update runs
+  __builtin_amdgcn_sched_barrier(0);
+  if (c + 1 < nch) {
+    chain_read_w<HALF>(in, nxt, lane);
+    chain_read_k<HALF>(fk_next, nxt, lane);
+  }
+  // DEC vn -> fp16; wave 1 publishes vn (bf16) for the output waves
+  float m = 0.f;
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      dv[tb][r] *= vn[tb][r];
+      m = fmaxf(m, fabsf(dv[tb][r]));
+    }
+  if (HALF == 1) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      *reinterpret_cast<bf16x8*>(&xch[(4 + j) * ws::FRAG + lane * 16]) = pack_acc_bf16(vn[2 * j], vn[2 * j + 1]);
+  }
+  // Fast path (the usual case): kappa = 1 and every |DEC vn| below 2^14 with the largest at
+  // least 2^-4, so DEC vn goes to fp16 unscaled.  Otherwise: per-column power-of-two scaling.
+  // Both waves hold the same DEC vn, so they take the same path.
+  const bool fast = kap == 1.0f && __builtin_amdgcn_ballot_w64(m >= 16384.0f) == 0 &&
+                    __builtin_amdgcn_ballot_w64(m >= 0.0625f) != 0;
+  if (__builtin_amdgcn_readfirstlane((int)fast)) {
+    f16x8 vh[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) vh[j] = pack_acc_f16(dv[2 * j], dv[2 * j + 1], 1.0f);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      S[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fk[i * 2], vh[0], S[i], 0, 0, 0);
+      S[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fk[i * 2 + 1], vh[1], S[i], 0, 0, 0);
+    }
+  } else {
+    m = fmaxf(m, __shfl_xor(m, 16, kWave));
+    m = fmaxf(m, __shfl_xor(m, 32, kWave));
+    const int se = fp16_scale_exp(m);
+    f16x8 vh[2];
+    const float sigma = ldexpf(1.0f, se);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) vh[j] = pack_acc_f16(dv[2 * j], dv[2 * j + 1], sigma);
+    const float pre = sigma * kap;        // exact powers of two
+    const float post = ldexpf(ksc, -se);  // 1 / (sigma * kappa)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      S[i] *= pre;
+      S[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fk[i * 2], vh[0], S[i], 0, 0, 0);
+      S[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fk[i * 2 + 1], vh[1], S[i], 0, 0, 0);
+      S[i] *= post;
+    }
+  }
+  uint8_t* xn = sm.xch[x1];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    Sb[j] = pack_acc_bf16(S[2 * j], S[2 * j + 1]);
+    *reinterpret_cast<bf16x8*>(&xn[(2 * HALF + j) * ws::FRAG + lane * 16]) = Sb[j];
+  }
+  x0 = x1;
+  __syncthreads();  // end of step c
+}
+
+// The chain wave holding S rows 64 HALF .. 64 HALF + 63 (4 accumulator tiles).
+template <int HALF>
+__device__ __forceinline__ void chain_wave(ScanSmem& sm, const float* __restrict__ init,
+                                           float* __restrict__ final_state, int srow, int64_t sbase, int nch,
+                                           int lane) {
+  using namespace pf;
+  const int g4 = lane >> 4;
+  f32x4 S[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      S[i][r] = (init && srow >= 0) ? init[sbase + (int64_t)(64 * HALF + 16 * i + 4 * g4 + r) * D] : 0.f;
+  bf16x8 Sb[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    Sb[j] = pack_acc_bf16(S[2 * j], S[2 * j + 1]);
+    *reinterpret_cast<bf16x8*>(&sm.xch[0][(2 * HALF + j) * ws::FRAG + lane * 16]) = Sb[j];
+  }
+  if (lane == 0) sm.flag[HALF] = 0;
+  __syncthreads();  // prologue
+  ChainIn in;
+  KFrags fk0, fk1;  // chunks c even / odd
+  if (nch > 0) {
+    chain_read_w<HALF>(in, sm.ring[0], lane);
+    chain_read_k<HALF>(fk0, sm.ring[0], lane);
+  }
+  int x0 = 0;  // c % 3
+  for (int c = 0; c < nch; c += 2) {
+    chain_step<HALF>(sm, S, Sb, in, fk0, fk1, c, nch, x0, lane);
+    if (c + 1 < nch) chain_step<HALF>(sm, S, Sb, in, fk1, fk0, c + 1, nch, x0, lane);
+  }
+  __syncthreads();  // step nch (the output waves' last chunk)
+  if (final_state && srow >= 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) final_state[sbase + (int64_t)(64 * HALF + 16 * i + 4 * g4 + r) * D] = S[i][r];
+  }
+}
 
 template <typename OutT>
-__global__ __launch_bounds__(pf::NT, 1) void chunk_scan_kernel(
+__global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(
     const float* __restrict__ init, float* __restrict__ final_state, OutT* __restrict__ out,
     const int32_t* __restrict__ cu, const int32_t* __restrict__ seq_chunk0, const int32_t* __restrict__ rows,
     int n_rows, int nseq, int seq_len, int Hqk, int Hv, const uint8_t* __restrict__ work) {
@@ -768,146 +990,19 @@ __global__ __launch_bounds__(pf::NT, 1) void chunk_scan_kernel(
   const int64_t kq_off = -(int64_t)(h % (Hv / Hqk)) * ws::BYTES;  // record of the key head's owner
   const int col = 16 * n + c16;
 
-  if (role == 0) {
-    // ---------------- chain wave ----------------
+  if (role < 2) {
+    // ---------------- chain waves ----------------
     const int srow = state_row(rows, n_rows, seq);  // slot row of this sequence's states (-1: none)
     const int64_t sbase = ((int64_t)(srow < 0 ? 0 : srow) * Hv + h) * D * D + col;
-    f32x4 S[8];
-#pragma unroll
-    for (int rb = 0; rb < 8; ++rb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        S[rb][r] = (init && srow >= 0) ? init[sbase + (int64_t)(16 * rb + 4 * g4 + r) * D] : 0.f;
-    bf16x8 Sb[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      Sb[j] = pack_acc_bf16(S[2 * j], S[2 * j + 1]);
-      *reinterpret_cast<bf16x8*>(&sm.xch[0][j * ws::FRAG + lane * 16]) = Sb[j];
-    }
-    __syncthreads();  // prologue
-    ChainIn in;
-    if (nch > 0) {
-      chain_read_w(in, sm.ring[0], lane);
-      chain_read_k(in, sm.ring[0], lane);
-    }
-    int x0 = 0;  // c % 3
-    for (int c = 0; c < nch; ++c) {
-      uint8_t* xch = sm.xch[x0];
-      const int x1 = x0 == 2 ? 0 : x0 + 1;
-      const uint8_t* nxt = sm.ring[x1];  // chunk c+1 sits in ring slot (c+1) % 3
-      f32x4 vn[4], dv[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        vn[0][r] = (float)in.u[0][r];
-        vn[1][r] = (float)in.u[0][4 + r];
-        vn[2][r] = (float)in.u[1][r];
-        vn[3][r] = (float)in.u[1][4 + r];
-      }
-      {  // the tile scales are 1 unless |U| left [2^-4, 2^14) (same value in every lane)
-        const bool unit = in.usc[0] == 1.0f && in.usc[1] == 1.0f && in.usc[2] == 1.0f && in.usc[3] == 1.0f;
-        if (!__builtin_amdgcn_readfirstlane((int)unit)) {
-#pragma unroll
-          for (int tb = 0; tb < 4; ++tb) vn[tb] *= in.usc[tb];
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb) vn[tb] = mma(in.fw[tb * 4 + j], Sb[j], vn[tb]);
-#pragma unroll
-      for (int tb = 0; tb < 4; ++tb) dv[tb] = in.dv[tb];
-      const float gl = in.gl, ksc = in.ksc, kap = in.kap;
-      if (c + 1 < nch) chain_read_w(in, nxt, lane);
-      // publish vn (bf16, for the output wave); DEC vn -> fp16
-      float m = 0.f;
-#pragma unroll
-      for (int tb = 0; tb < 4; ++tb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          dv[tb][r] *= vn[tb][r];
-          m = fmaxf(m, fabsf(dv[tb][r]));
-        }
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        *reinterpret_cast<bf16x8*>(&xch[(4 + j) * ws::FRAG + lane * 16]) = pack_acc_bf16(vn[2 * j], vn[2 * j + 1]);
-      // Fast path (the usual case): kappa = 1 and every |DEC vn| below 2^14 with the largest at
-      // least 2^-4, so DEC vn goes to fp16 unscaled.  Otherwise: per-column power-of-two scaling.
-      const bool fast = kap == 1.0f && __builtin_amdgcn_ballot_w64(m >= 16384.0f) == 0 &&
-                        __builtin_amdgcn_ballot_w64(m >= 0.0625f) != 0;
-      if (__builtin_amdgcn_readfirstlane((int)fast)) {
-        f16x8 vh[2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) vh[j] = pack_acc_f16(dv[2 * j], dv[2 * j + 1], 1.0f);
-#pragma unroll
-        for (int rb = 0; rb < 8; ++rb) {
-          S[rb] *= gl;
-          S[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(in.fk[rb * 2], vh[0], S[rb], 0, 0, 0);
-          S[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(in.fk[rb * 2 + 1], vh[1], S[rb], 0, 0, 0);
-        }
-      } else {
-        m = fmaxf(m, __shfl_xor(m, 16, kWave));
-        m = fmaxf(m, __shfl_xor(m, 32, kWave));
-        const int se = fp16_scale_exp(m);
-        f16x8 vh[2];
-        const float sigma = ldexpf(1.0f, se);
-#pragma unroll
-        for (int j = 0; j < 2; ++j) vh[j] = pack_acc_f16(dv[2 * j], dv[2 * j + 1], sigma);
-        const float pre = gl * sigma * kap;  // GL * sigma * kappa (exact powers of two)
-        const float post = ldexpf(ksc, -se); // 1 / (sigma * kappa)
-#pragma unroll
-        for (int rb = 0; rb < 8; ++rb) {
-          S[rb] *= pre;
-          S[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(in.fk[rb * 2], vh[0], S[rb], 0, 0, 0);
-          S[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(in.fk[rb * 2 + 1], vh[1], S[rb], 0, 0, 0);
-          S[rb] *= post;
-        }
-      }
-      if (c + 1 < nch) chain_read_k(in, nxt, lane);
-      uint8_t* xn = sm.xch[x1];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        Sb[j] = pack_acc_bf16(S[2 * j], S[2 * j + 1]);
-        *reinterpret_cast<bf16x8*>(&xn[j * ws::FRAG + lane * 16]) = Sb[j];
-      }
-      x0 = x1;
-      __syncthreads();  // end of step c
-    }
-    __syncthreads();  // step nch (the output wave's last chunk)
-    if (final_state && srow >= 0) {
-#pragma unroll
-      for (int rb = 0; rb < 8; ++rb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) final_state[sbase + (int64_t)(16 * rb + 4 * g4 + r) * D] = S[rb][r];
-    }
-  } else if (role == 1) {
-    // ---------------- output wave: step c computes chunk c-1 ----------------
-    OutFrags F0, F1;  // even / odd chunks
-    if (nch > 0) out_load(F0, rec0, rec0 + kq_off, lane);
-    __syncthreads();  // prologue
-    if (nch > 1) out_load(F1, rec0 + rstride, rec0 + rstride + kq_off, lane);
-    __syncthreads();  // step 0
-    int xp = 0;       // (c - 1) % 3
-    for (int c = 1; c <= nch; c += 2) {
-      {
-        const int cc = c - 1;  // even
-        const int len = L - cc * CH < CH ? L - cc * CH : CH;
-        out_step<OutT>(F0, sm.xch[xp], out, s0 + (int64_t)cc * CH, len, Hv, h, 16 * n, lane);
-        if (c + 1 < nch) out_load(F0, rec0 + (int64_t)(c + 1) * rstride, rec0 + (int64_t)(c + 1) * rstride + kq_off, lane);
-        xp = xp == 2 ? 0 : xp + 1;
-        __syncthreads();  // end of step c
-      }
-      if (c + 1 <= nch) {
-        const int cc = c;  // odd
-        const int len = L - cc * CH < CH ? L - cc * CH : CH;
-        out_step<OutT>(F1, sm.xch[xp], out, s0 + (int64_t)cc * CH, len, Hv, h, 16 * n, lane);
-        if (c + 2 < nch) out_load(F1, rec0 + (int64_t)(c + 2) * rstride, rec0 + (int64_t)(c + 2) * rstride + kq_off, lane);
-        xp = xp == 2 ? 0 : xp + 1;
-        __syncthreads();  // end of step c+1
-      }
-    }
+    if (role == 0) chain_wave<0>(sm, init, final_state, srow, sbase, nch, lane);
+    else chain_wave<1>(sm, init, final_state, srow, sbase, nch, lane);
+  } else if (role < 4) {
+    // ---------------- output waves: step c computes chunk c-1 ----------------
+    if (role == 2) output_wave<0, OutT>(sm, rec0, rstride, kq_off, out, s0, L, nch, Hv, h, 16 * n, lane);
+    else output_wave<1, OutT>(sm, rec0, rstride, kq_off, out, s0, L, nch, Hv, h, 16 * n, lane);
   } else {
     // ---------------- loader waves ----------------
-    const int lt = t - 128;
+    const int lt = t - 256;
     u16x8 R0[kLoadPieces], R1[kLoadPieces];  // even / odd chunks
     if (nch > 0) scan_load(R0, rec0, rec0 + kq_off, n, lt);
     if (nch > 1) scan_load(R1, rec0 + rstride, rec0 + rstride + kq_off, n, lt);
@@ -1109,7 +1204,7 @@ extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const voi
   }
   const int64_t pairs = (int64_t)nseq * Hv;
   const int64_t scan_blocks = (pairs + 7) / 8 * 64;
-  chunk_scan_kernel<uint16_t><<<(unsigned)scan_blocks, pf::NT, 0, s>>>(
+  chunk_scan_kernel<uint16_t><<<(unsigned)scan_blocks, kScanThreads, 0, s>>>(
       initial_state, final_state, (uint16_t*)out, cu_seqlens, seq_chunk0, state_rows, n_rows, nseq, seq_len, Hqk,
       Hv, work);
   return check_launch("gdn_chunk_prefill(state)");

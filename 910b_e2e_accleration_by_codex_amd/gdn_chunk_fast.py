@@ -29,49 +29,89 @@ def _tokens_view(x, name):
     return flat, x.stride(1)
 
 
-def _check_cu(cu_seqlens, B, T):
-    """cu_seqlens on the host, checked (the kernels index memory with it): 1-D, starts at 0,
-    non-decreasing, ends at the packed token count."""
+def _to_device_int32(host, device):
+    """int64 host tensor -> int32 device tensor through pinned memory, without waiting for the GPU."""
+    if torch.device(device).type == "cpu":
+        return host.to(torch.int32)
+    staged = torch.empty(host.shape, dtype=torch.int32, pin_memory=True)
+    staged.copy_(host)
+    return staged.to(device, non_blocking=True)
+
+
+class Varlen:
+    """A packed batch's sequence table, checked once on the host (the kernels index memory with it):
+    cu_seqlens 1-D, starting at 0, non-decreasing, ending at the packed token count.  Holds the
+    device copies of cu_seqlens and of seq_chunk0 (seq_chunk0[s] = number of 64-token chunks of the
+    sequences before s: the workspace slot of the first chunk of sequence s).
+    cu_seqlens given on the host (a CPU tensor or a list, as a scheduler holds it) costs no GPU
+    wait: the tables go up through pinned memory on the stream.  A device tensor is read back once.
+    Build one per layer call and hand it to every op of that call."""
+
+    def __init__(self, cu_seqlens, T, device):
+        if isinstance(cu_seqlens, Varlen):
+            raise TypeError("already a Varlen")
+        host = torch.as_tensor(cu_seqlens).detach().to("cpu", torch.int64).reshape(-1)
+        if host.numel() < 2 or int(host[0]) != 0 or int(host[-1]) != T or bool((host[1:] < host[:-1]).any()):
+            raise ValueError(f"cu_seqlens must be non-decreasing from 0 to {T}, got {host.tolist()[:8]}...")
+        self.T = T
+        self.host = host
+        self.nseq = host.numel() - 1
+        nch = (host[1:] - host[:-1] + CHUNK - 1) // CHUNK
+        s0 = torch.zeros(host.numel(), dtype=torch.int64)
+        s0[1:] = torch.cumsum(nch, 0)
+        self.total_chunks = int(s0[-1])
+        self.cu = _to_device_int32(host, device)
+        self.seq_chunk0 = _to_device_int32(s0, device)
+
+
+def _varlen(cu_seqlens, B, T, device):
     if B != 1:
         raise ValueError("cu_seqlens needs packed inputs with batch size 1")
-    host = cu_seqlens.detach().to("cpu", torch.int64).reshape(-1)
-    if host.numel() < 2 or int(host[0]) != 0 or int(host[-1]) != T or bool((host[1:] < host[:-1]).any()):
-        raise ValueError(f"cu_seqlens must be non-decreasing from 0 to {T}, got {host.tolist()[:8]}...")
-    return host
+    if isinstance(cu_seqlens, Varlen):
+        if cu_seqlens.T != T:
+            raise ValueError(f"Varlen built for {cu_seqlens.T} tokens, inputs hold {T}")
+        return cu_seqlens
+    return Varlen(cu_seqlens, T, device)
 
 
 def _seq_args(B, T, cu_seqlens, device):
     """(device int32 cu_seqlens | None, n_seq, per-sequence length for the uniform case)."""
     if cu_seqlens is None:
         return None, B, T
-    host = _check_cu(cu_seqlens, B, T)
-    cu = cu_seqlens.to(device=device, dtype=torch.int32).contiguous()
-    return cu, host.numel() - 1, 0
+    vl = _varlen(cu_seqlens, B, T, device)
+    return vl.cu, vl.nseq, 0
 
 
 def _chunk_table(B, T, cu_seqlens, device):
-    """(device cu_seqlens | None, device seq_chunk0 | None, n_seq, seq_len, total_chunks):
-    seq_chunk0[s] = number of 64-token chunks of the sequences before s (the workspace slot of the
-    first chunk of sequence s)."""
+    """(device cu_seqlens | None, device seq_chunk0 | None, n_seq, seq_len, total_chunks)."""
     if cu_seqlens is None:
         return None, None, B, T, B * ((T + CHUNK - 1) // CHUNK)
-    host = _check_cu(cu_seqlens, B, T)
-    nch = (host[1:] - host[:-1] + CHUNK - 1) // CHUNK
-    s0 = torch.zeros(host.numel(), dtype=torch.int64)
-    s0[1:] = torch.cumsum(nch, 0)
-    cu = cu_seqlens.to(device=device, dtype=torch.int32).contiguous()
-    return cu, s0.to(device=device, dtype=torch.int32), host.numel() - 1, 0, int(s0[-1])
+    vl = _varlen(cu_seqlens, B, T, device)
+    return vl.cu, vl.seq_chunk0, vl.nseq, 0, vl.total_chunks
+
+
+class Rows:
+    """Slot rows of a batch's sequences (int [n_seq]), checked once on the host: every row in
+    [0, n_rows).  Host input (CPU tensor / list) costs no GPU wait; a device tensor is read back once."""
+
+    def __init__(self, state_rows, nseq, n_rows, device):
+        host = torch.as_tensor(state_rows).detach().to("cpu", torch.int64).reshape(-1)
+        if host.numel() != nseq:
+            raise ValueError(f"state_rows must hold one row per sequence ({nseq})")
+        if nseq and (int(host.min()) < 0 or int(host.max()) >= n_rows):
+            raise ValueError(f"state_rows must lie in [0, {n_rows})")
+        self.nseq, self.n_rows = nseq, n_rows
+        self.dev = _to_device_int32(host, device)
 
 
 def _check_rows(state_rows, nseq, n_rows, device):
-    """Slot rows (int32 [n_seq] on the device), checked on the host: every row in [0, n_rows)."""
-    rows = torch.as_tensor(state_rows).reshape(-1)
-    if rows.numel() != nseq:
-        raise ValueError(f"state_rows must hold one row per sequence ({nseq})")
-    host = rows.detach().to("cpu", torch.int64)
-    if nseq and (int(host.min()) < 0 or int(host.max()) >= n_rows):
-        raise ValueError(f"state_rows must lie in [0, {n_rows})")
-    return rows.to(device=device, dtype=torch.int32).contiguous()
+    """Device int32 slot rows, checked (see Rows)."""
+    if isinstance(state_rows, Rows):
+        if state_rows.nseq != nseq or state_rows.n_rows != n_rows:
+            raise ValueError(f"Rows built for {state_rows.nseq} sequences / {state_rows.n_rows} rows, "
+                             f"call has {nseq} / {n_rows}")
+        return state_rows.dev
+    return Rows(state_rows, nseq, n_rows, device).dev
 
 
 def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size=64, initial_state=None,
@@ -87,7 +127,7 @@ def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size=64, initial_st
     final state is then written there and returned."""
     if chunk_size <= 0:
         raise ValueError("chunk_size must be positive")
-    _lib.require_cuda(query, key, value, g, beta, initial_state, cu_seqlens)
+    _lib.require_cuda(query, key, value, g, beta, initial_state)
     if key.dtype != query.dtype or value.dtype != query.dtype:
         raise TypeError("chunk_gated_delta_rule: query, key and value must share a dtype")
     B, T, Hqk, D = query.shape
@@ -167,7 +207,7 @@ def causal_conv1d_prefill(x, weight, bias=None, history=None, cu_seqlens=None, s
     Slot rows: with ``state_rows`` (int [n_seq]) ``history`` (or None = zero) and ``state_out`` are
     bf16 [n_rows, C, K] slot buffers, sequence s uses row state_rows[s], and the two may be the same
     tensor; the new states are written there and ``state_out`` is returned."""
-    _lib.require_cuda(x, weight, bias, history, cu_seqlens)
+    _lib.require_cuda(x, weight, bias, history)
     B, C, L = x.shape
     K = weight.shape[-1]
     if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
@@ -230,7 +270,8 @@ def gdn_prefill_core(mixed_qkv, z, a, b, conv_weight, A_log, dt_bias, norm_weigh
     (src/cb_tp.py:153-181 fresh, :230-263 continued): conv prefill + SiLU, split q|k|v, gating,
     chunked rule with l2norm (value head h reads key head h // r, no repeat_interleave copy),
     gated RMSNorm.  mixed_qkv [T, C] bf16 (pre-conv), z [T, Hv*d], a, b [T, Hv];
-    cu_seqlens int32 [n_seq+1] | None; conv_history [n_seq, C, K] | None;
+    cu_seqlens int [n_seq+1] (host or device) | Varlen | None -- host lengths, as the scheduler
+    holds them, keep the call free of GPU waits; conv_history [n_seq, C, K] | None;
     initial_state [n_seq, Hv, d, d] | None.
     Returns (core [T, Hv*d] bf16, conv_state [n_seq, C, K] bf16, rec_state [n_seq, Hv, d, d] fp32).
     Slot rows (the engine's state buffers, src/cb_engine.py:198-205, src/cb_tp.py:178-179, :256-262):
@@ -243,9 +284,15 @@ def gdn_prefill_core(mixed_qkv, z, a, b, conv_weight, A_log, dt_bias, norm_weigh
     if C != (2 * Hk + Hv) * D:
         raise ValueError(f"gdn_prefill_core: C={C} != (2*{Hk}+{Hv})*{D}")
     w = conv_weight.reshape(C, -1)
+    if cu_seqlens is not None:  # checked and uploaded once for both kernels
+        cu_seqlens = _varlen(cu_seqlens, 1, T, mixed_qkv.device)
     if slots is not None:
         if conv_slots is None or rec_slots is None:
             raise ValueError("gdn_prefill_core: slots needs conv_slots and rec_slots")
+        if conv_slots.shape[0] != rec_slots.shape[0]:
+            raise ValueError("gdn_prefill_core: conv_slots and rec_slots must hold the same slot count")
+        nseq = cu_seqlens.nseq if cu_seqlens is not None else 1
+        slots = slots if isinstance(slots, Rows) else Rows(slots, nseq, conv_slots.shape[0], mixed_qkv.device)
         conv_out, conv_state = causal_conv1d_prefill(mixed_qkv.t().unsqueeze(0), w, conv_bias,
                                                      conv_slots if continuation else None, cu_seqlens,
                                                      state_rows=slots, state_out=conv_slots)

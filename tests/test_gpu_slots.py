@@ -44,9 +44,9 @@ def test_prefill_into_slot_rows(gdn, dev):
     conv_slots = torch.randn(8, C, K, generator=g_).to(torch.bfloat16).to(dev)
     rec_slots = torch.randn(8, Hv, D, D, generator=g_).to(dev)
     conv0, rec0 = conv_slots.clone(), rec_slots.clone()
-    slots = torch.tensor([5, 0, 3], dtype=torch.int32, device=dev)
-    core, cs, rs = gdn.gdn_prefill_core(mixed, z, a, b, cw, A_log, dt, nw, Hk, Hv, D, cu_seqlens=cud,
-                                        slots=slots, conv_slots=conv_slots, rec_slots=rec_slots)
+    # host lengths and rows (no GPU wait) must give what device ones give
+    core, cs, rs = gdn.gdn_prefill_core(mixed, z, a, b, cw, A_log, dt, nw, Hk, Hv, D, cu_seqlens=cu,
+                                        slots=[5, 0, 3], conv_slots=conv_slots, rec_slots=rec_slots)
     assert cs is conv_slots and rs is rec_slots
     assert torch.equal(core, core_ref)
     for i, r in enumerate([5, 0, 3]):
