@@ -1032,12 +1032,18 @@ __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(
 // ============================================================================================
 // Causal depthwise conv prefill + SiLU with decode-state capture.
 // ============================================================================================
-// One thread per (packed token p, 8 channels): it loads the K input rows p-K+1..p with 16-byte
-// reads (rows before its sequence come from the sequence's history row [C, K], x_{-j} = history[K - j],
-// or are zero) and writes 8 outputs with one 16-byte store.  Numerics of F.conv1d on bf16: fp32
+// One thread per (run of kConvRun consecutive packed tokens, 8 channels): it loads the input rows
+// p0-K+1 .. p0+kConvRun-1 once with 16-byte reads and slides the K-tap window over them (rows before a
+// token's sequence come from the sequence's history row [C, K], x_{-j} = history[K - j], or are
+// zero), then writes 8 outputs per token with one 16-byte store.  A workgroup covers one token run
+// and 2048 channels, so the sequence walk is uniform across it.  Numerics of F.conv1d on bf16: fp32
 // accumulation of the K products (+ bias), one bf16 rounding, SiLU, bf16.  The decode conv state a
 // sequence leaves (its last K inputs) is written afterwards by conv_state_capture_kernel, so the
 // history may be the same slot rows the state goes to.
+constexpr int kConvRun = 8;
+// SiLU with the hardware exp and reciprocal (each within about 1 ulp in fp32, so the bf16 result
+// is within one bf16 ulp of the exactly rounded x / (1 + e^-x)).
+__device__ __forceinline__ float silu_fast(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 __device__ __forceinline__ int find_seq(const int32_t* cu, int nseq, int64_t p) {
   int lo = 0, hi = nseq - 1;  // last sequence whose start <= p (skips empty ones)
   while (lo < hi) {
@@ -1054,47 +1060,82 @@ __global__ __launch_bounds__(256) void conv_prefill_kernel(const uint16_t* __res
                                                            const uint16_t* __restrict__ bias,
                                                            const uint16_t* __restrict__ history,
                                                            const int32_t* __restrict__ rows, int n_rows,
-                                                           uint16_t* __restrict__ out,
+                                                           uint16_t* __restrict__ out, int64_t total_tokens,
                                                            const int32_t* __restrict__ cu, int nseq, int seq_len,
                                                            int C) {
   const int cg = blockIdx.x * blockDim.x + threadIdx.x;  // 8-channel group
-  const int64_t p = blockIdx.y;
+  const int64_t p0 = (int64_t)blockIdx.y * kConvRun;
   if (8 * cg >= C) return;
   const int c0 = 8 * cg;
-  const int s = cu ? find_seq(cu, nseq, p) : (int)(p / seq_len);
-  const int64_t s_lo = cu ? (int64_t)cu[s] : (int64_t)s * seq_len;
-  const int64_t s_hi = cu ? (int64_t)cu[s + 1] : s_lo + seq_len;
-  const int hrow = history ? state_row(rows, n_rows, s) : -1;
-  u16x8 win[K];
+  const int nrun = total_tokens - p0 < kConvRun ? (int)(total_tokens - p0) : kConvRun;
+  // rows p0-K+1 .. p0+nrun-1 (only those inside [0, total_tokens) are read)
+  u16x8 xr[kConvRun + K - 1];
+  const u16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-  for (int r = 0; r < K; ++r) {
-    const int64_t tok = p - (K - 1) + r;
-    if (tok >= s_lo) {
-      win[r] = *reinterpret_cast<const u16x8*>(x + tok * x_stride + c0);
-    } else {
-      const int back = (int)(s_lo - tok);  // 1..K-1
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        win[r][e] = hrow >= 0 ? history[((int64_t)hrow * C + c0 + e) * K + (K - back)] : (uint16_t)0;
-    }
+  for (int i = 0; i < kConvRun + K - 1; ++i) {
+    const int64_t tok = p0 - (K - 1) + i;
+    xr[i] = (tok >= 0 && i < nrun + K - 1) ? *reinterpret_cast<const u16x8*>(x + tok * x_stride + c0) : zero;
   }
   u16x8 wt[K];  // weight[c0 + e][r] -> wt[r][e]
   {
-    const uint16_t* wp = weight + (int64_t)c0 * K;
+    const u16x8* wp = reinterpret_cast<const u16x8*>(weight + (int64_t)c0 * K);  // 8 K contiguous values
+    uint16_t w[8 * K];
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      const u16x8 v = wp[i];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) w[8 * i + e] = v[e];
+    }
 #pragma unroll
     for (int e = 0; e < 8; ++e)
 #pragma unroll
-      for (int r = 0; r < K; ++r) wt[r][e] = wp[e * K + r];
+      for (int r = 0; r < K; ++r) wt[r][e] = w[e * K + r];
   }
-  u16x8 o;
+  float bv[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    float acc = bias ? bf2f(bias[c0 + e]) : 0.f;
+  for (int e = 0; e < 8; ++e) bv[e] = bias ? bf2f(bias[c0 + e]) : 0.f;
+  // sequence of p0, then walk forward (uniform across the workgroup)
+  int s = cu ? find_seq(cu, nseq, p0) : (int)(p0 / seq_len);
+  int64_t s_lo = cu ? (int64_t)cu[s] : (int64_t)s * seq_len;
+  int64_t s_hi = cu ? (int64_t)cu[s + 1] : s_lo + seq_len;
 #pragma unroll
-    for (int r = 0; r < K; ++r) acc += bf2f(win[r][e]) * bf2f(wt[r][e]);
-    o[e] = f2bf(silu_f(rbf(acc)));
+  for (int i = 0; i < kConvRun; ++i) {
+    if (i >= nrun) break;  // (uniform: the last run of the batch)
+    const int64_t p = p0 + i;
+    while (p >= s_hi) {  // next non-empty sequence
+      ++s;
+      s_lo = cu ? (int64_t)cu[s] : (int64_t)s * seq_len;
+      s_hi = cu ? (int64_t)cu[s + 1] : s_lo + seq_len;
+    }
+    u16x8 win[K];
+    if (p - (K - 1) >= s_lo) {
+#pragma unroll
+      for (int r = 0; r < K; ++r) win[r] = xr[i + r];
+    } else {
+      const int hrow = history ? state_row(rows, n_rows, s) : -1;
+#pragma unroll
+      for (int r = 0; r < K; ++r) {
+        const int64_t tok = p - (K - 1) + r;
+        if (tok >= s_lo) {
+          win[r] = xr[i + r];
+        } else {
+          const int back = (int)(s_lo - tok);  // 1..K-1
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            win[r][e] = hrow >= 0 ? history[((int64_t)hrow * C + c0 + e) * K + (K - back)] : (uint16_t)0;
+        }
+      }
+    }
+    u16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float acc = bv[e];
+#pragma unroll
+      for (int r = 0; r < K; ++r) acc += bf2f(win[r][e]) * bf2f(wt[r][e]);
+      o[e] = f2bf(silu_fast(rbf(acc)));
+    }
+    *reinterpret_cast<u16x8*>(out + p * (int64_t)C + c0) = o;
   }
-  *reinterpret_cast<u16x8*>(out + p * (int64_t)C + c0) = o;
 }
 
 // The decode conv state each sequence leaves: its last K inputs, the front filled from its history
@@ -1239,12 +1280,14 @@ extern "C" int gdn_conv_prefill_rows(const void* x, int64_t x_stride, const void
     GDN_REQUIRE(C % 8 == 0 && x_stride % 8 == 0 && aligned(x, 16) && aligned(out, 16),
                 "gdn_conv_prefill: C and the row stride must be multiples of 8 with 16-byte aligned rows");
     GDN_REQUIRE(total_tokens < (1ll << 31), "gdn_conv_prefill: too many tokens");
-    dim3 grid((unsigned)((C / 8 + 255) / 256), (unsigned)total_tokens);
+    GDN_REQUIRE(aligned(weight, 16), "gdn_conv_prefill: weight must be 16-byte aligned");
+    dim3 grid((unsigned)((C / 8 + 255) / 256), (unsigned)((total_tokens + kConvRun - 1) / kConvRun));
 #define GDN_CONV_PREFILL(KK)                                                                                    \
   case KK:                                                                                                     \
     conv_prefill_kernel<KK><<<grid, 256, 0, s>>>((const uint16_t*)x, x_stride, (const uint16_t*)weight,          \
                                                  (const uint16_t*)bias, (const uint16_t*)history, state_rows,      \
-                                                 n_rows, (uint16_t*)out, cu_seqlens, nseq, seq_len, C);            \
+                                                 n_rows, (uint16_t*)out, total_tokens, cu_seqlens, nseq, seq_len, \
+                                                 C);                                                           \
     break;
     switch (K) {
       GDN_CONV_PREFILL(1)
