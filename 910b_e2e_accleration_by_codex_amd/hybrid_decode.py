@@ -1,0 +1,192 @@
+"""Hybrid (GDN + full-attention) decode step of a Qwen3.5-shaped model, graph-captured.
+
+The decode side of the reference's engine (src/cb_engine.py:123-187 graph capture, :246-250 dense
+decode over all slots, :318-352 the GDN layer) for a whole layer stack: every GDN layer runs its
+in-projections as one GEMM, the fused HIP decode core (conv update + gating + l2norm + recurrent
+step + gated RMSNorm, one kernel) and out_proj; every fourth layer is GQA full attention
+(HF Qwen3_5Attention: gated q, per-head q/k RMSNorm, partial rotary, modeling_qwen3_5.py) over a
+per-slot KV cache; each layer ends with the SwiGLU MLP.  Weights are random (no checkpoints), the
+slots' GDN states and KV caches are pre-filled with random values at per-slot context lengths.
+
+Only the GDN layers are this library's kernels; projections, attention and MLP are torch ops on
+hipBLASLt GEMMs.  The KV cache keeps K transposed ([slot, kv head, head_dim, position]) so both
+batched attention products take a contiguous right operand.
+"""
+from dataclasses import dataclass
+from types import SimpleNamespace
+
+import torch
+
+from .cb_engine import GDNSlots, gdn_decode_core
+
+
+@dataclass
+class HybridConfig:
+    """Layer shapes.  The defaults are Qwen3.5-27B's (src/cb_tp.py:7-10, HF configuration_qwen3_5.py):
+    hidden 5120, 64 layers with every fourth one full attention, GDN H_k=16 / H_v=48 / d=128 with a
+    4-tap conv, attention 24 q / 4 kv heads of 256 with a quarter of each head rotary, MLP 17408."""
+    hidden: int = 5120
+    layers: int = 64
+    full_every: int = 4  # 0: GDN layers only
+    gdn_k_heads: int = 16
+    gdn_v_heads: int = 48
+    gdn_head: int = 128
+    conv_k: int = 4
+    attn_heads: int = 24
+    kv_heads: int = 4
+    attn_head: int = 256
+    rotary_frac: float = 0.25
+    rope_theta: float = 10000.0
+    mlp: int = 17408     # 0: no MLP (the token mixers alone)
+    vocab: int = 248320  # 0: no LM head (the step returns the final hidden state)
+    eps: float = 1e-6
+
+    def is_full(self, i):
+        return self.full_every > 0 and (i + 1) % self.full_every == 0
+
+    @property
+    def conv_dim(self):
+        return (2 * self.gdn_k_heads + self.gdn_v_heads) * self.gdn_head
+
+
+def rms_norm(x, w, eps):
+    """Qwen3_5RMSNorm: fp32 x * rsqrt(mean(x^2) + eps) * (1 + w), cast back (modeling_qwen3_5.py)."""
+    xf = x.float()
+    y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return (y * (1.0 + w.float())).to(x.dtype)
+
+
+def _rotate_half(x):
+    h = x.shape[-1] // 2
+    return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
+
+
+class HybridDecoder:
+    """Random-weight hybrid stack with slot state for ``n_slots`` sequences.  ``ctx`` (int [N], host)
+    are the per-slot context lengths already in the caches; each ``step`` appends one token per slot."""
+
+    def __init__(self, cfg, n_slots, ctx, max_steps, device, seed=0, weight_std=0.02):
+        self.cfg, self.N, self.dev = cfg, n_slots, device
+        g_ = torch.Generator(device=device).manual_seed(seed)
+        bf = torch.bfloat16
+
+        def w(*shape, std=weight_std):
+            return (torch.randn(*shape, generator=g_, device=device) * std).to(bf)
+
+        H, D = cfg.hidden, cfg.gdn_head
+        self.layers = []
+        gdn_ids = [i for i in range(cfg.layers) if not cfg.is_full(i)]
+        self.slots = GDNSlots(n_slots, gdn_ids, cfg.conv_dim, cfg.conv_k, cfg.gdn_v_heads, D, device)
+        ctx = torch.as_tensor(ctx, dtype=torch.int64)
+        self.max_ctx = int(ctx.max()) + max_steps
+        self.pos = ctx.to(device=device, dtype=torch.int64)  # position of the next token per slot
+        kv, hd = cfg.kv_heads, cfg.attn_head
+        for i in range(cfg.layers):
+            L = SimpleNamespace(full=cfg.is_full(i), in_norm=w(H), post_norm=w(H),
+                                gate_up=w(2 * cfg.mlp, H) if cfg.mlp else None,
+                                down=w(H, cfg.mlp) if cfg.mlp else None)
+            if L.full:
+                L.qkv = w(cfg.attn_heads * hd * 2 + 2 * kv * hd, H)
+                L.o = w(H, cfg.attn_heads * hd)
+                L.q_norm, L.k_norm = w(hd), w(hd)
+                # cache: K transposed [N, kv, hd, T], V [N, kv, T, hd]; random history below each ctx
+                L.kt = torch.randn(n_slots, kv, hd, self.max_ctx, generator=g_, device=device).to(bf)
+                L.v = torch.randn(n_slots, kv, self.max_ctx, hd, generator=g_, device=device).to(bf)
+            else:
+                Hv, Hk, C = cfg.gdn_v_heads, cfg.gdn_k_heads, cfg.conv_dim
+                L.in_proj = w(C + Hv * D + 2 * Hv, H)  # in_proj_qkv | in_proj_z | in_proj_b | in_proj_a
+                L.conv_w = (0.5 * torch.randn(C, cfg.conv_k, generator=g_, device=device)).to(bf)
+                L.A_log = torch.full((Hv,), -2.302585092994046, device=device)
+                L.dt_bias = torch.full((Hv,), 2.0, device=device)
+                L.norm_w = (1 + 0.02 * torch.randn(D, generator=g_, device=device)).to(bf)
+                L.out = w(H, Hv * D)
+                self.slots.conv[i].copy_(torch.randn(n_slots, C, cfg.conv_k, generator=g_, device=device).to(bf))
+                self.slots.rec[i].copy_(0.02 * torch.randn(n_slots, Hv, D, D, generator=g_, device=device))
+            self.layers.append(L)
+        self.final_norm = w(H)
+        self.lm_head = w(cfg.vocab, H) if cfg.vocab else None
+        rd = int(hd * cfg.rotary_frac)
+        self.inv_freq = 1.0 / (cfg.rope_theta ** (torch.arange(0, rd, 2, device=device, dtype=torch.float32) / rd))
+        self.t_idx = torch.arange(self.max_ctx, device=device)
+        self.slot_idx = torch.arange(n_slots, device=device)
+
+    # -- layers ------------------------------------------------------------------------------
+    def gdn(self, i, L, x):
+        cfg, n = self.cfg, x.shape[0]
+        Hv, D, C = cfg.gdn_v_heads, cfg.gdn_head, cfg.conv_dim
+        proj = x @ L.in_proj.t()                       # one GEMM for qkv | z | b | a
+        mixed = proj[:, :C]
+        z = proj[:, C:C + Hv * D]
+        b = proj[:, C + Hv * D:C + Hv * D + Hv]
+        a = proj[:, C + Hv * D + Hv:]
+        core = gdn_decode_core(mixed, z, a, b, self.slots.conv[i], L.conv_w, L.A_log, L.dt_bias, L.norm_w,
+                               self.slots.rec[i], cfg.gdn_k_heads, Hv, D, cfg.eps)
+        return core.reshape(n, Hv * D) @ L.out.t()
+
+    def attention(self, L, x):
+        cfg, n = self.cfg, x.shape[0]
+        nh, kv, hd = cfg.attn_heads, cfg.kv_heads, cfg.attn_head
+        proj = x @ L.qkv.t()
+        qg = proj[:, :nh * hd * 2].reshape(n, nh, 2 * hd)
+        q, gate = qg[..., :hd], qg[..., hd:].reshape(n, nh * hd)
+        k = proj[:, nh * hd * 2:nh * hd * 2 + kv * hd].reshape(n, kv, hd)
+        v = proj[:, nh * hd * 2 + kv * hd:].reshape(n, kv, hd)
+        q, k = rms_norm(q, L.q_norm, cfg.eps), rms_norm(k, L.k_norm, cfg.eps)
+        # partial rotary at each slot's position (HF apply_rotary_pos_emb on the first rd dims)
+        freqs = self.pos.float()[:, None] * self.inv_freq[None, :]
+        emb = torch.cat((freqs, freqs), dim=-1)
+        cos, sin = emb.cos()[:, None, :], emb.sin()[:, None, :]
+        rd = emb.shape[-1]
+
+        def rope(t):
+            tr = t[..., :rd].float()
+            return torch.cat(((tr * cos + _rotate_half(tr) * sin).to(t.dtype), t[..., rd:]), dim=-1)
+
+        q, k = rope(q), rope(k)
+        L.kt[self.slot_idx, :, :, self.pos] = k
+        L.v[self.slot_idx, :, self.pos, :] = v
+        grp = nh // kv
+        s = torch.matmul(q.reshape(n, kv, grp, hd), L.kt).float() * (hd ** -0.5)  # [n, kv, grp, T]
+        s = s.masked_fill((self.t_idx[None, :] > self.pos[:, None])[:, None, None, :], float("-inf"))
+        p = torch.softmax(s, dim=-1).to(x.dtype)
+        o = torch.matmul(p, L.v).reshape(n, nh * hd)                               # [n, kv, grp, hd]
+        return (o * torch.sigmoid(gate)) @ L.o.t()
+
+    def mlp(self, L, x):
+        gu = x @ L.gate_up.t()
+        m = self.cfg.mlp
+        return (torch.nn.functional.silu(gu[:, :m]) * gu[:, m:]) @ L.down.t()
+
+    def step(self, h):
+        """h [N, hidden] bf16 (the step's token embeddings) -> logits [N, vocab] (or the final hidden
+        state without an LM head).  Advances every slot by one token."""
+        for i, L in enumerate(self.layers):
+            x = rms_norm(h, L.in_norm, self.cfg.eps)
+            h = h + (self.attention(L, x) if L.full else self.gdn(i, L, x))
+            if L.gate_up is not None:
+                h = h + self.mlp(L, rms_norm(h, L.post_norm, self.cfg.eps))
+        self.pos += 1
+        h = rms_norm(h, self.final_norm, self.cfg.eps)
+        return h @ self.lm_head.t() if self.lm_head is not None else h
+
+
+class HybridDecodeGraph:
+    """The whole decode step captured once as a HIP graph and replayed (src/cb_engine.py:123-187):
+    ``inp`` is the static input buffer, ``replay()`` returns the static output."""
+
+    def __init__(self, model, inp):
+        self.model, self.inp = model, inp
+        self.graph = torch.cuda.CUDAGraph()
+        dev = inp.device
+        stream = torch.cuda.Stream(device=dev)
+        stream.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(stream):
+            model.step(inp)  # warm-up (advances the slots by one token)
+        torch.cuda.current_stream(dev).wait_stream(stream)
+        torch.cuda.synchronize(dev)
+        with torch.cuda.graph(self.graph):
+            self.out = model.step(inp)
+
+    def replay(self):
+        self.graph.replay()
+        return self.out

@@ -7,9 +7,12 @@ layer states (3.2 GB working set, so the 256 MB Infinity Cache cannot serve them
 a HIP graph and replayed.  A "step" is one replay (48 layers).  ``value`` is microseconds per layer.
 
 Also reported (``secondary``): chunked GDN prefill at T=8192 (B=1, H_k=16, H_v=32, d=128, bf16
-inputs, fp32 state) in tokens/s/layer with its bf16-MFMA and HBM fractions.
+inputs, fp32 state) in tokens/s/layer with its bf16-MFMA and HBM fractions, the fused varlen
+prefill layer, T=32768, and whole decode steps at Qwen3.5-27B shape (the hybrid 64-layer stack,
+and its 48 GDN layers with projections) in tokens/s.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-prefill]
+                      [--only decode|prefill|prefill8192|hybrid]
 """
 import argparse
 import importlib
@@ -255,6 +258,50 @@ def cpu_baseline_decode(layers_cpu=LAYERS, reps=3):
                        f"{threads} threads")
 
 
+def bench_hybrid(gdn, dev, steps=10, warmup=2, seed=4):
+    """Whole decode steps at Qwen3.5-27B shape, 16 slots, contexts uniform in [512, 4096] with random
+    GDN states and KV caches, HIP-graph replay (random-init bf16 weights):
+      * the 64-layer hybrid stack (48 GDN + 16 GQA attention layers, SwiGLU MLPs, LM head 248320);
+      * the 48 GDN layers alone with their projections (in_proj GEMM -> fused HIP core -> out_proj).
+    HBM bytes: every weight read once per step, GDN states read + written, KV caches read."""
+    hd = importlib.import_module(PKG + ".hybrid_decode")
+    out = []
+    for name, cfg in (("hybrid 64-layer stack (48 GDN + 16 attention, MLPs, LM head)", hd.HybridConfig()),
+                      ("48 GDN layers with projections (no attention / MLP / LM head)",
+                       hd.HybridConfig(layers=48, full_every=0, mlp=0, vocab=0))):
+        g_ = torch.Generator().manual_seed(seed)
+        ctx = torch.randint(512, 4097, (N_SLOTS,), generator=g_)
+        model = hd.HybridDecoder(cfg, N_SLOTS, ctx, steps + warmup + 2, dev, seed=seed)
+        inp = torch.randn(N_SLOTS, cfg.hidden, generator=g_).to(torch.bfloat16).to(dev)
+        graph = hd.HybridDecodeGraph(model, inp)
+        for _ in range(warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        wbytes = sum(t.numel() * t.element_size() for L in model.layers for t in vars(L).values()
+                     if torch.is_tensor(t) and t.dtype == torch.bfloat16 and t.dim() == 2)
+        wbytes += model.lm_head.numel() * 2 if model.lm_head is not None else 0
+        sbytes = sum(2 * (model.slots.conv[i].numel() * 2 + model.slots.rec[i].numel() * 4) for i in model.slots.rec)
+        kvbytes = sum(L.kt.numel() * 2 + L.v.numel() * 2 for L in model.layers if L.full)
+        total = wbytes + sbytes + kvbytes
+        n_gdn = len(model.slots.rec)
+        out.append({"workload": f"decode step, Qwen3.5-27B shape, {name}, 16 slots, ctx U[512,4096], HIP graph",
+                    "ms_per_step": round(ms, 3), "tokens_per_s": round(N_SLOTS / ms * 1e3, 1),
+                    "us_per_gdn_layer": round(ms * 1e3 / n_gdn, 2) if not cfg.full_every else None,
+                    "hbm_bytes_per_step": total, "weight_bytes": wbytes, "gdn_state_bytes": sbytes,
+                    "kv_cache_bytes_read": kvbytes,
+                    "hbm_frac": round(total / (ms * 1e-3) / HBM_PEAK, 4)})
+        del graph, model, inp
+        torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -262,7 +309,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill", "prefill8192"], default=None,
+    ap.add_argument("--only", choices=["decode", "prefill", "prefill8192", "hybrid"], default=None,
                     help="run one workload group (prefill8192: the T=8192 chunked rule alone, for profiling)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first run a 256 MiB device-to-device copy (counter calibration for rocprof)")
@@ -292,8 +339,10 @@ def main():
                           bench_prefill_long(gdn, dev, check=not args.no_cpu)]
         if not args.no_cpu:
             res["prefill"][0]["cpu_baseline"] = cpu_baseline_prefill()
-    if args.only in ("prefill", "prefill8192"):
-        print(json.dumps({"secondary": res["prefill"]}))
+    if args.only in (None, "hybrid"):
+        res["hybrid"] = bench_hybrid(gdn, dev)
+    if args.only in ("prefill", "prefill8192", "hybrid"):
+        print(json.dumps({"secondary": res.get("prefill", []) + res.get("hybrid", [])}))
         return
     dec = res["decode"]
     bpl = decode_bytes_per_layer()
@@ -314,8 +363,7 @@ def main():
                      "us_per_launch_graph": round(dec["us_per_layer"], 3),
                      "us_per_launch_eager": round(dec["us_per_layer_eager"], 3)},
     }
-    if "prefill" in res:
-        line["secondary"] = res["prefill"]
+    line["secondary"] = res.get("prefill", []) + res.get("hybrid", [])
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline_decode()
     print(json.dumps(line))

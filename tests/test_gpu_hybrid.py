@@ -1,0 +1,109 @@
+"""GPU tests of the whole-layer decode path: a GDN layer with its projections against an fp32
+composition around the oracle (src/cb_engine.py:318-352), the full-attention layer against a
+per-slot fp32 reference, and the graph-captured hybrid step (src/cb_engine.py:123-187) against
+eager steps."""
+import pytest
+import torch
+
+from conftest import PKG_NAME, rel_l2
+
+OUT_TOL = 1e-2
+
+
+def _hybrid(gdn):
+    from importlib import import_module
+    return import_module(PKG_NAME + ".hybrid_decode")
+
+
+def _small_cfg(hd_mod):
+    return hd_mod.HybridConfig(hidden=256, layers=4, full_every=4, gdn_k_heads=2, gdn_v_heads=4, gdn_head=128,
+                               conv_k=4, attn_heads=4, kv_heads=2, attn_head=64, mlp=512, vocab=128)
+
+
+@pytest.mark.gpu
+def test_gdn_layer_with_projections_vs_oracle(gdn, oracle, dev):
+    """in_proj (one GEMM) -> fused HIP core -> out_proj equals the fp32 composition of the same
+    weights around the oracle's decode core; the layer's states match too."""
+    hd = _hybrid(gdn)
+    cfg = _small_cfg(hd)
+    model = hd.HybridDecoder(cfg, 3, [5, 17, 9], 4, dev, seed=40)
+    L = model.layers[0]
+    g_ = torch.Generator().manual_seed(41)
+    x = torch.randn(3, cfg.hidden, generator=g_).to(torch.bfloat16)
+    conv0, rec0 = model.slots.conv[0].cpu(), model.slots.rec[0].cpu()
+    out = model.gdn(0, L, x.to(dev)).cpu()
+    Hv, D, C = cfg.gdn_v_heads, cfg.gdn_head, cfg.conv_dim
+    proj = (x.float() @ L.in_proj.cpu().float().t()).to(torch.bfloat16)
+    mixed, z = proj[:, :C], proj[:, C:C + Hv * D]
+    b, a = proj[:, C + Hv * D:C + Hv * D + Hv], proj[:, C + Hv * D + Hv:]
+    conv_ref, rec_ref = conv0.clone(), rec0.clone()
+    core = oracle.gdn_decode_core(mixed, z, a, b, conv_ref, L.conv_w.cpu(), L.A_log.cpu(), L.dt_bias.cpu(),
+                                  L.norm_w.cpu(), rec_ref, cfg.gdn_k_heads, Hv, D, cfg.eps)
+    ref = core.float() @ L.out.cpu().float().t()
+    assert rel_l2(out, ref) <= OUT_TOL
+    assert rel_l2(model.slots.rec[0], rec_ref) <= 1e-3
+    # the conv state is the pre-conv inputs shifted in: exact up to the GEMM's own bf16 rounding
+    assert rel_l2(model.slots.conv[0], conv_ref) <= 1e-2
+
+
+@pytest.mark.gpu
+def test_attention_layer_vs_fp32_reference(gdn, dev):
+    """GQA decode attention (gated q, q/k RMSNorm, partial rotary, KV cache at each slot's position)
+    against a per-slot fp32 loop over the same cache."""
+    hd = _hybrid(gdn)
+    cfg = _small_cfg(hd)
+    ctx = [5, 17, 9]
+    model = hd.HybridDecoder(cfg, 3, ctx, 4, dev, seed=42)
+    L = model.layers[3]
+    g_ = torch.Generator().manual_seed(43)
+    x = torch.randn(3, cfg.hidden, generator=g_).to(torch.bfloat16)
+    out = model.attention(L, x.to(dev)).cpu().float()
+    nh, kv, hdim = cfg.attn_heads, cfg.kv_heads, cfg.attn_head
+    rd = int(hdim * cfg.rotary_frac)
+    kt, vc = L.kt.cpu().float(), L.v.cpu().float()   # the cache after the layer wrote this token
+    proj = (x.float() @ L.qkv.cpu().float().t())
+    ref = torch.zeros(3, cfg.hidden)
+    for n in range(3):
+        p = ctx[n]
+        qg = proj[n, :nh * hdim * 2].reshape(nh, 2 * hdim)
+        q, gate = qg[:, :hdim], qg[:, hdim:].reshape(-1)
+        q = hd.rms_norm(q, L.q_norm.cpu(), cfg.eps)
+        inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, rd, 2).float() / rd))
+        emb = torch.cat((p * inv, p * inv))
+        qr = q[:, :rd] * emb.cos() + hd._rotate_half(q[:, :rd]) * emb.sin()
+        q = torch.cat((qr, q[:, rd:]), dim=-1)
+        o = torch.zeros(nh, hdim)
+        for h in range(nh):
+            j = h // (nh // kv)
+            s = (q[h] @ kt[n, j, :, :p + 1]) * hdim ** -0.5
+            o[h] = torch.softmax(s, -1) @ vc[n, j, :p + 1, :]
+        ref[n] = (o.reshape(-1) * torch.sigmoid(gate)) @ L.o.cpu().float().t()
+    assert rel_l2(out, ref) <= OUT_TOL
+    # the new key / value landed at each slot's position and nowhere else
+    kproj = proj[:, nh * hdim * 2:nh * hdim * 2 + kv * hdim].reshape(3, kv, hdim)
+    for n in range(3):
+        k_ref = hd.rms_norm(kproj[n], L.k_norm.cpu(), cfg.eps)
+        assert rel_l2(kt[n, :, rd:, ctx[n]], k_ref[:, rd:]) <= 1e-2
+
+
+@pytest.mark.gpu
+def test_hybrid_graph_replay_matches_eager(gdn, dev):
+    """Three replays of the captured 4-layer hybrid step give the eager steps' logits and states."""
+    hd = _hybrid(gdn)
+    cfg = _small_cfg(hd)
+    ctx = [5, 17, 9]
+    eager = hd.HybridDecoder(cfg, 3, ctx, 8, dev, seed=44)
+    graphed = hd.HybridDecoder(cfg, 3, ctx, 8, dev, seed=44)
+    g_ = torch.Generator().manual_seed(45)
+    inp = torch.randn(3, cfg.hidden, generator=g_).to(torch.bfloat16).to(dev)
+    graph = hd.HybridDecodeGraph(graphed, inp)        # runs one eager warm-up step
+    eager.step(inp)
+    for _ in range(3):
+        out_g = graph.replay().clone()
+        out_e = eager.step(inp)
+        torch.cuda.synchronize()
+        assert rel_l2(out_g, out_e) <= 1e-3
+        for i in eager.slots.rec:
+            assert rel_l2(graphed.slots.rec[i], eager.slots.rec[i]) <= 1e-5
+            assert torch.equal(graphed.slots.conv[i], eager.slots.conv[i])
+        assert torch.equal(graphed.pos, eager.pos)
