@@ -33,6 +33,12 @@ _SIGNATURES = {
     "gdn_chunk_prefill": ([_P, _L, _P, _L, _P, _L, _P, _P, _I, _P, _P, _P, _L, _P, _P, _L, _I, _I, _I, _I,
                            _I, _I, _I, _P, _L, _P], _I),
     "gdn_chunk_prefill_workspace_bytes": ([_L, _I], _L),
+    "gdn_decode_linear_workspace_bytes": ([_I, _L, _L], _L),
+    "gdn_decode_linear": ([_P, _L, _P, _L, _P, _L, _I, _L, _L, _P, _L, _P], _I),
+    "gdn_decode_linear_packed_elems": ([_L, _L], _L),
+    "gdn_decode_linear_pack": ([_P, _L, _P, _L, _L, _P], _I),
+    "gdn_decode_linear_packed": ([_P, _L, _P, _P, _L, _I, _L, _L, _P, _L, _P], _I),
+    "gdn_add_rmsnorm": ([_P, _P, _P, _P, _P, _I, _I, _F, _P], _I),
     "gdn_conv_prefill": ([_P, _L, _P, _P, _P, _P, _P, _L, _P, _I, _I, _I, _I, _P], _I),
     "gdn_gating": ([_P, _P, _L, _P, _P, _P, _P, _L, _I, _P], _I),
     "gdn_decode_fused_masked": ([_P, _L, _P, _L, _P, _P, _L, _P, _P, _P, _P, _P, _P, _I, _F, _P, _P, _P, _I,

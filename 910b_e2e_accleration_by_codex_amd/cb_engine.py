@@ -165,6 +165,75 @@ def patch_model(model, fast_gdn=False, gdn_v2=False):
     return model
 
 
+class PackedWeight:
+    """A linear weight [N, K] bf16 (nn.Linear layout) repacked once into the decode projection
+    kernel's fragment-major layout (every load of the kernel then reads 1 KB contiguous)."""
+
+    def __init__(self, weight):
+        _lib.require_cuda(weight)
+        N, K = weight.shape
+        if weight.dtype != torch.bfloat16 or K % 128:
+            raise ValueError("PackedWeight: bf16 [N, K] with K a multiple of 128")
+        w = weight.contiguous()
+        self.N, self.K = N, K
+        self.data = torch.empty(int(_lib.lib().gdn_decode_linear_packed_elems(N, K)), dtype=torch.bfloat16,
+                                device=weight.device)
+        _lib.call("gdn_decode_linear_pack", _lib.ptr(w), w.stride(0), _lib.ptr(self.data), N, K,
+                  _lib.stream_of(w))
+
+
+def decode_linear(x, weight):
+    """x [M, K] bf16 @ weight[N, K]^T (nn.Linear layout, or a PackedWeight) -> [M, N] bf16 for a
+    decode step's M <= 16 rows (one token per slot): the GDN layer's in_proj_* / out_proj
+    (src/cb_engine.py:320-323, :352) on the weight-streaming projection kernel.  Plain weights of
+    shapes it does not take (more rows, K not a multiple of 128, rows not 16-byte aligned) run on
+    torch's GEMM."""
+    if isinstance(weight, PackedWeight):
+        _lib.require_cuda(x)
+        M, K = x.shape
+        if K != weight.K or M > 16 or x.dtype != torch.bfloat16:
+            raise ValueError(f"decode_linear: x {tuple(x.shape)} {x.dtype} does not fit the packed weight "
+                             f"[{weight.N}, {weight.K}] (at most 16 bf16 rows)")
+        if x.stride(1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
+            x = x.contiguous()
+        out = torch.empty(M, weight.N, dtype=torch.bfloat16, device=x.device)
+        wb = int(_lib.lib().gdn_decode_linear_workspace_bytes(M, weight.N, K))
+        ws = torch.empty(max(wb // 4, 1), dtype=torch.float32, device=x.device) if wb else None
+        _lib.call("gdn_decode_linear_packed", _lib.ptr(x), x.stride(0), _lib.ptr(weight.data), _lib.ptr(out),
+                  out.stride(0), M, weight.N, K, _lib.ptr(ws), wb, _lib.stream_of(x))
+        return out
+    _lib.require_cuda(x, weight)
+    M, K = x.shape
+    N = weight.shape[0]
+    if (M > 16 or K % 128 or weight.shape[1] != K or x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16
+            or x.stride(1) != 1 or weight.stride(1) != 1 or x.stride(0) % 8 or weight.stride(0) % 8
+            or x.data_ptr() % 16 or weight.data_ptr() % 16):
+        return x @ weight.t()
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=x.device)
+    wb = int(_lib.lib().gdn_decode_linear_workspace_bytes(M, N, K))
+    ws = torch.empty(max(wb // 4, 1), dtype=torch.float32, device=x.device) if wb else None
+    _lib.call("gdn_decode_linear", _lib.ptr(x), x.stride(0), _lib.ptr(weight), weight.stride(0), _lib.ptr(out),
+              out.stride(0), M, N, K, _lib.ptr(ws), wb, _lib.stream_of(x))
+    return out
+
+
+def add_rms_norm(h, delta, weight, eps=1e-6):
+    """Residual add + Qwen3_5RMSNorm between decode-step layers (HF modeling_qwen3_5.py):
+    h, delta [M, H] bf16 (delta None: norm only), weight [H] bf16.  Returns (h + delta, norm of it);
+    one kernel instead of the add and the norm's chain of elementwise ops."""
+    _lib.require_cuda(h, delta, weight)
+    M, H = h.shape
+    for name, t in (("h", h), ("delta", delta)):
+        if t is not None and (t.dtype != torch.bfloat16 or t.shape != (M, H) or not t.is_contiguous()):
+            raise ValueError(f"add_rms_norm: {name} must be a contiguous bf16 [{M}, {H}] tensor")
+    w = weight.to(torch.bfloat16).contiguous()
+    x = torch.empty_like(h)
+    h_out = torch.empty_like(h) if delta is not None else h
+    _lib.call("gdn_add_rmsnorm", _lib.ptr(h), _lib.ptr(delta), _lib.ptr(w), _lib.ptr(h_out), _lib.ptr(x), M, H,
+              float(eps), _lib.stream_of(h))
+    return h_out, x
+
+
 class GDNSlots:
     """Per-slot GDN state of every GDN layer, laid out as CBEngine keeps it
     (src/cb_engine.py:108-112): conv[i] [N, C, K] bf16, rec[i] [N, H_v, d_k, d_v] fp32."""

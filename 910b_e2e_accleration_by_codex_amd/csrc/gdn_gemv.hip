@@ -1,0 +1,320 @@
+// Decode-step projections: out[M, N] = x[M, K] W[N, K]^T with M <= 16 slots (the GDN layer's
+// in_proj_* and out_proj in nn.Linear layout, bf16 in / bf16 out, fp32 accumulation).
+//
+// At 16 rows the product is a weight stream: W is read once (2 N K bytes) and x is tiny, so the
+// kernel is HBM-bound and is built to keep W loads long and in flight.  It runs on bf16 MFMA with
+// the roles turned around -- out^T = W x^T -- so the 16 slots are the MFMA's N dimension and each
+// 16-row tile of W is an A operand:
+//   * v_mfma_f32_16x16x32_bf16, lane (r, g) = (l % 16, l / 16).  Per 128-wide k step a lane loads
+//     64 contiguous bytes of W row r (k + 32 g .. k + 32 g + 31) and the same 32 k of x row r; the
+//     4 MFMAs of the step take 8 of those k each (A and B permuted alike, so the sum over the step
+//     is the plain dot product).  4 lanes cover 256 contiguous bytes of a W row.
+//   * a wave owns RT row tiles (16 RT output features) and reuses each x fragment RT times; a
+//     workgroup is 4 waves.  When N alone gives too few waves to fill the chip, K is split over
+//     blockIdx.y and fp32 partial sums go through a workspace and a small reduction kernel.
+//   * each wave keeps PF k steps of loads in flight ahead of its MFMAs (a ring of register buffers).
+#include "gdn_device.h"
+#include "gdn_internal.h"
+
+namespace gdn {
+namespace gv {
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+constexpr int RT = 2;               // row tiles per wave
+constexpr int WAVES = 4;            // waves per workgroup
+constexpr int ROWS = 16 * RT * WAVES;  // output features per workgroup
+constexpr int KSTEP = 128;
+constexpr int TARGET_WAVES = 2048;  // with PF steps in flight per wave: enough loads in flight for HBM
+constexpr int PF = 3;               // k steps loaded ahead (a ring of PF + 1 register buffers)
+
+struct Frag4 {
+  u16x8 v[4];
+};
+__device__ __forceinline__ void load4(Frag4& f, const uint16_t* p) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) f.v[j] = *reinterpret_cast<const u16x8*>(p + 8 * j);
+}
+}  // namespace gv
+
+// grid (ceil(N / ROWS), ksplit); workgroup (4 waves).  Split s covers k steps [s * steps_per, ...).
+// PACKED: W is in the fragment-major layout of gdn_decode_linear_pack (w_stride unused).
+template <bool PACKED>
+__global__ __launch_bounds__(64 * gv::WAVES) void decode_linear_kernel(
+    const uint16_t* __restrict__ x, int64_t x_stride, const uint16_t* __restrict__ W, int64_t w_stride,
+    uint16_t* __restrict__ out, int64_t out_stride, float* __restrict__ part, int M, int64_t N, int64_t K,
+    int steps_per) {
+  using namespace gv;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, r = lane & 15, g = lane >> 4;
+  const int64_t f0 = (int64_t)blockIdx.x * ROWS + (int64_t)w * 16 * RT;
+  const int64_t nsteps = K / KSTEP;
+  const int64_t s_lo = (int64_t)blockIdx.y * steps_per;
+  const int64_t s_hi = s_lo + steps_per < nsteps ? s_lo + steps_per : nsteps;
+  const uint16_t* wrow[RT];
+  const int64_t ntiles = (N + 15) / 16;
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    if (PACKED) {
+      // tile f / 16 (clamped: tiles past the last load a valid tile; their results are not stored)
+      int64_t tile = (f0 >> 4) + t;
+      tile = tile < ntiles ? tile : ntiles - 1;
+      wrow[t] = W + tile * nsteps * (KSTEP * 16) + lane * 8;
+    } else {
+      int64_t row = f0 + 16 * t + r;
+      row = row < N ? row : N - 1;  // rows past N load a valid row; their results are not stored
+      wrow[t] = W + row * w_stride + 32 * g;
+    }
+  }
+  const bool xrow = r < M;
+  const uint16_t* xp = x + (int64_t)(xrow ? r : 0) * x_stride + 32 * g;
+  f32x4 acc[RT];
+#pragma unroll
+  for (int t = 0; t < RT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  Frag4 a[PF + 1][RT], b[PF + 1];
+  const u16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+  auto load_step = [&](int buf, int64_t s) {
+    const int64_t k = s * KSTEP;
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+      if (PACKED) {  // block (tile, s): 4 fragments of 64 lanes x 16 bytes, fragment j contiguous
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          a[buf][t].v[j] = *reinterpret_cast<const u16x8*>(wrow[t] + s * (KSTEP * 16) + j * 512);
+      } else {
+        load4(a[buf][t], wrow[t] + k);
+      }
+    }
+    if (xrow) load4(b[buf], xp + k);
+    else
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[buf].v[j] = zero;
+  };
+  auto mma_step = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int t = 0; t < RT; ++t)
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[buf][t].v[j]),
+                                                         __builtin_bit_cast(bf16x8, b[buf].v[j]), acc[t], 0, 0, 0);
+  };
+  // step s_lo + i lives in buffer i % (PF + 1); the loop is unrolled over the ring so every buffer
+  // index is static
+#pragma unroll
+  for (int u = 0; u < PF; ++u)
+    if (s_lo + u < s_hi) load_step(u, s_lo + u);
+  for (int64_t s = s_lo; s < s_hi; s += PF + 1) {
+#pragma unroll
+    for (int u = 0; u <= PF; ++u) {
+      if (s + u + PF < s_hi) load_step((u + PF) % (PF + 1), s + u + PF);
+      if (s + u < s_hi) mma_step(u);
+    }
+  }
+  // lane (c, g) holds out^T[f0 + 16 t + 4 g + i][slot c], i < 4
+  const int c = r;
+  if (c >= M) return;
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    const int64_t f = f0 + 16 * t + 4 * g;
+    if (f >= N) continue;
+    if (part) {
+      float* pp = part + ((int64_t)blockIdx.y * M + c) * N + f;
+      if (f + 4 <= N && (N & 3) == 0) *reinterpret_cast<f32x4*>(pp) = acc[t];
+      else
+        for (int i = 0; i < 4 && f + i < N; ++i) pp[i] = acc[t][i];
+    } else {
+      uint16_t* op = out + (int64_t)c * out_stride + f;
+      if (f + 4 <= N && (out_stride & 3) == 0 && ((uintptr_t)out & 7) == 0) {
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        *reinterpret_cast<u32x2*>(op) = u32x2{f2bf2(acc[t][0], acc[t][1]), f2bf2(acc[t][2], acc[t][3])};
+      } else {
+        for (int i = 0; i < 4 && f + i < N; ++i) op[i] = f2bf(acc[t][i]);
+      }
+    }
+  }
+}
+
+// out[c][f] = bf16(sum over splits of part[s][c][f]), 4 features per thread.
+__global__ __launch_bounds__(256) void decode_linear_reduce_kernel(const float* __restrict__ part, int splits,
+                                                                   uint16_t* __restrict__ out, int64_t out_stride,
+                                                                   int M, int64_t N) {
+  const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // quad index over M x ceil(N / 4)
+  const int64_t nq = (N + 3) / 4;
+  if (q >= (int64_t)M * nq) return;
+  const int c = (int)(q / nq);
+  const int64_t f = (q % nq) * 4;
+  float s[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int sp = 0; sp < splits; ++sp) {
+    const float* pp = part + ((int64_t)sp * M + c) * N + f;
+    for (int i = 0; i < 4; ++i)
+      if (f + i < N) s[i] += pp[i];
+  }
+  for (int i = 0; i < 4; ++i)
+    if (f + i < N) out[(int64_t)c * out_stride + f + i] = f2bf(s[i]);
+}
+
+// Fragment-major copy of W [N, K] for the packed kernel: for 16-row tile T, k step s, fragment j,
+// lane l = 16 g + r and element e: P[(((T * nsteps + s) * 4 + j) * 64 + l) * 8 + e] =
+// W[16 T + r][128 s + 32 g + 8 j + e] (zero past row N).  Every load of the packed kernel then
+// reads 1 KB contiguous and a tile's k steps follow each other in memory.
+__global__ __launch_bounds__(256) void decode_linear_pack_kernel(const uint16_t* __restrict__ W, int64_t w_stride,
+                                                                 uint16_t* __restrict__ P, int64_t N, int64_t K) {
+  using namespace gv;
+  const int64_t nsteps = K / KSTEP;
+  const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // one 16-byte piece of P
+  const int64_t total = (N + 15) / 16 * nsteps * 4 * 64;
+  if (q >= total) return;
+  const int l = (int)(q & 63), j = (int)((q >> 6) & 3);
+  const int64_t ts = q >> 8, s = ts % nsteps, T = ts / nsteps;
+  const int64_t row = 16 * T + (l & 15), k = 128 * s + 32 * (l >> 4) + 8 * j;
+  u16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (row < N) v = *reinterpret_cast<const u16x8*>(W + row * w_stride + k);
+  *reinterpret_cast<u16x8*>(P + q * 8) = v;
+}
+
+namespace gv {
+// (blocks along N, k splits, k steps per split)
+inline void plan(int64_t N, int64_t K, int64_t* nb, int* splits, int* steps_per) {
+  *nb = (N + ROWS - 1) / ROWS;
+  const int64_t nsteps = K / KSTEP;
+  int64_t sp = (TARGET_WAVES + *nb * WAVES - 1) / (*nb * WAVES);
+  if (sp < 1) sp = 1;
+  if (sp > nsteps) sp = nsteps;
+  const int64_t per = (nsteps + sp - 1) / sp;
+  *steps_per = (int)per;
+  *splits = (int)((nsteps + per - 1) / per);
+}
+}  // namespace gv
+
+}  // namespace gdn
+
+using namespace gdn;
+
+namespace {
+int64_t workspace_bytes(int M, int64_t N, int64_t K) {
+  int64_t nb;
+  int splits, per;
+  gv::plan(N, K, &nb, &splits, &per);
+  return splits > 1 ? (int64_t)splits * M * N * (int64_t)sizeof(float) : 0;
+}
+
+int decode_linear_launch(bool packed, const void* x, int64_t x_stride, const void* W, int64_t w_stride, void* out,
+                         int64_t out_stride, int M, int64_t N, int64_t K, float* workspace, int64_t ws_bytes,
+                         void* stream) {
+  GDN_REQUIRE(x && W && out, "gdn_decode_linear: null pointer");
+  GDN_SUPPORT(M >= 1 && M <= 16, "gdn_decode_linear: %d rows (1..16 supported)", M);
+  GDN_REQUIRE(N > 0 && N < (1ll << 31) && K > 0, "gdn_decode_linear: bad sizes N=%lld K=%lld", (long long)N,
+              (long long)K);
+  GDN_SUPPORT(K % gv::KSTEP == 0, "gdn_decode_linear: K=%lld must be a multiple of %d", (long long)K, gv::KSTEP);
+  GDN_REQUIRE(aligned(x, 16) && aligned(W, 16) && x_stride % 8 == 0 && x_stride >= K &&
+                  (packed || (w_stride % 8 == 0 && w_stride >= K)),
+              "gdn_decode_linear: x and W rows must be 16-byte aligned and hold K values");
+  GDN_REQUIRE(aligned(out, 2) && out_stride >= N, "gdn_decode_linear: out rows must hold N values");
+  int64_t nb;
+  int splits, per;
+  gv::plan(N, K, &nb, &splits, &per);
+  const int64_t need = workspace_bytes(M, N, K);
+  GDN_REQUIRE(need == 0 || (workspace && aligned(workspace, 16) && ws_bytes >= need),
+              "gdn_decode_linear: needs a 16-byte aligned fp32 workspace of %lld bytes", (long long)need);
+  hipStream_t s = (hipStream_t)stream;
+  float* part = splits > 1 ? workspace : nullptr;
+  if (packed)
+    decode_linear_kernel<true><<<dim3((unsigned)nb, (unsigned)splits), 64 * gv::WAVES, 0, s>>>(
+        (const uint16_t*)x, x_stride, (const uint16_t*)W, w_stride, (uint16_t*)out, out_stride, part, M, N, K, per);
+  else
+    decode_linear_kernel<false><<<dim3((unsigned)nb, (unsigned)splits), 64 * gv::WAVES, 0, s>>>(
+        (const uint16_t*)x, x_stride, (const uint16_t*)W, w_stride, (uint16_t*)out, out_stride, part, M, N, K, per);
+  int rc = check_launch("gdn_decode_linear");
+  if (rc || !part) return rc;
+  const int64_t quads = (int64_t)M * ((N + 3) / 4);
+  decode_linear_reduce_kernel<<<(unsigned)((quads + 255) / 256), 256, 0, s>>>(part, splits, (uint16_t*)out,
+                                                                               out_stride, M, N);
+  return check_launch("gdn_decode_linear(reduce)");
+}
+}  // namespace
+
+extern "C" int64_t gdn_decode_linear_workspace_bytes(int M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K < gv::KSTEP || K % gv::KSTEP) return 0;
+  return workspace_bytes(M, N, K);
+}
+
+extern "C" int gdn_decode_linear(const void* x, int64_t x_stride, const void* W, int64_t w_stride, void* out,
+                                 int64_t out_stride, int M, int64_t N, int64_t K, float* workspace,
+                                 int64_t workspace_bytes, void* stream) {
+  clear_error();
+  return decode_linear_launch(false, x, x_stride, W, w_stride, out, out_stride, M, N, K, workspace,
+                              workspace_bytes, stream);
+}
+
+extern "C" int64_t gdn_decode_linear_packed_elems(int64_t N, int64_t K) {
+  if (N <= 0 || K <= 0 || K % gv::KSTEP) return 0;
+  return (N + 15) / 16 * 16 * K;
+}
+
+extern "C" int gdn_decode_linear_pack(const void* W, int64_t w_stride, void* packed, int64_t N, int64_t K,
+                                      void* stream) {
+  clear_error();
+  GDN_REQUIRE(W && packed, "gdn_decode_linear_pack: null pointer");
+  GDN_REQUIRE(N > 0 && N < (1ll << 31) && K > 0, "gdn_decode_linear_pack: bad sizes");
+  GDN_SUPPORT(K % gv::KSTEP == 0, "gdn_decode_linear_pack: K=%lld must be a multiple of %d", (long long)K,
+              gv::KSTEP);
+  GDN_REQUIRE(aligned(W, 16) && aligned(packed, 16) && w_stride % 8 == 0 && w_stride >= K,
+              "gdn_decode_linear_pack: W rows must be 16-byte aligned and hold K values");
+  const int64_t pieces = gdn_decode_linear_packed_elems(N, K) / 8;
+  GDN_REQUIRE((pieces + 255) / 256 < (1ll << 31), "gdn_decode_linear_pack: too large");
+  decode_linear_pack_kernel<<<(unsigned)((pieces + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+      (const uint16_t*)W, w_stride, (uint16_t*)packed, N, K);
+  return check_launch("gdn_decode_linear_pack");
+}
+
+extern "C" int gdn_decode_linear_packed(const void* x, int64_t x_stride, const void* packed, void* out,
+                                        int64_t out_stride, int M, int64_t N, int64_t K, float* workspace,
+                                        int64_t workspace_bytes, void* stream) {
+  clear_error();
+  return decode_linear_launch(true, x, x_stride, packed, 0, out, out_stride, M, N, K, workspace, workspace_bytes,
+                              stream);
+}
+
+// ============================================================================================
+// Residual add + RMSNorm between the decode step's layers (Qwen3_5RMSNorm, modeling_qwen3_5.py:
+// fp32 x * rsqrt(mean(x^2) + eps) * (1 + w), cast to bf16): h_out = bf16(h + delta) (delta may be
+// null: h_out = h), x_out = norm(h_out).  One workgroup per row; h_out may alias h.
+// ============================================================================================
+namespace gdn {
+__global__ __launch_bounds__(256) void add_rmsnorm_kernel(const uint16_t* h, const uint16_t* __restrict__ delta,
+                                                          const uint16_t* __restrict__ w, uint16_t* h_out,
+                                                          uint16_t* __restrict__ x_out, int H, float eps) {
+  const int64_t row = blockIdx.x;
+  const uint16_t* hr = h + row * H;
+  const uint16_t* dr = delta ? delta + row * H : nullptr;
+  uint16_t* hor = h_out + row * H;
+  __shared__ float red[4];
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < H; i += 256) {
+    float v = bf2f(hr[i]);
+    if (dr) v = rbf(v + bf2f(dr[i]));
+    ss += v * v;
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float inv = rsqrtf((red[0] + red[1] + red[2] + red[3]) / (float)H + eps);
+  for (int i = threadIdx.x; i < H; i += 256) {
+    float v = bf2f(hr[i]);
+    if (dr) v = rbf(v + bf2f(dr[i]));
+    x_out[row * H + i] = f2bf(v * inv * (1.0f + bf2f(w[i])));
+    if (dr) hor[i] = f2bf(v);
+  }
+}
+}  // namespace gdn
+
+extern "C" int gdn_add_rmsnorm(const void* h, const void* delta, const void* w, void* h_out, void* x_out, int M,
+                               int H, float eps, void* stream) {
+  clear_error();
+  GDN_REQUIRE(h && w && x_out && (!delta || h_out), "gdn_add_rmsnorm: null pointer");
+  GDN_REQUIRE(M >= 0 && H > 0, "gdn_add_rmsnorm: bad sizes");
+  if (M == 0) return GDN_OK;
+  add_rmsnorm_kernel<<<M, 256, 0, (hipStream_t)stream>>>((const uint16_t*)h, (const uint16_t*)delta,
+                                                         (const uint16_t*)w, (uint16_t*)h_out, (uint16_t*)x_out, H,
+                                                         eps);
+  return check_launch("gdn_add_rmsnorm");
+}

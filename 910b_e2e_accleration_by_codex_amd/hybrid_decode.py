@@ -8,16 +8,17 @@ step + gated RMSNorm, one kernel) and out_proj; every fourth layer is GQA full a
 per-slot KV cache; each layer ends with the SwiGLU MLP.  Weights are random (no checkpoints), the
 slots' GDN states and KV caches are pre-filled with random values at per-slot context lengths.
 
-Only the GDN layers are this library's kernels; projections, attention and MLP are torch ops on
-hipBLASLt GEMMs.  The KV cache keeps K transposed ([slot, kv head, head_dim, position]) so both
-batched attention products take a contiguous right operand.
+The GDN layer core and every linear of the step (the weight-streaming decode projection kernel,
+gdn_decode_linear) are this library's kernels; attention scores, softmax, norms and activations are
+torch ops.  The KV cache keeps K transposed ([slot, kv head, head_dim, position]) so both batched
+attention products take a contiguous right operand.
 """
 from dataclasses import dataclass
 from types import SimpleNamespace
 
 import torch
 
-from .cb_engine import GDNSlots, gdn_decode_core
+from .cb_engine import GDNSlots, PackedWeight, add_rms_norm, decode_linear, gdn_decode_core
 
 
 @dataclass
@@ -63,9 +64,11 @@ def _rotate_half(x):
 
 class HybridDecoder:
     """Random-weight hybrid stack with slot state for ``n_slots`` sequences.  ``ctx`` (int [N], host)
-    are the per-slot context lengths already in the caches; each ``step`` appends one token per slot."""
+    are the per-slot context lengths already in the caches; each ``step`` appends one token per slot.
+    Every linear weight is packed once for the decode projection kernel (``L.<name>_p``); the plain
+    [N, K] weights are kept only with ``keep_plain`` (for checks against a reference)."""
 
-    def __init__(self, cfg, n_slots, ctx, max_steps, device, seed=0, weight_std=0.02):
+    def __init__(self, cfg, n_slots, ctx, max_steps, device, seed=0, weight_std=0.02, keep_plain=False):
         self.cfg, self.N, self.dev = cfg, n_slots, device
         g_ = torch.Generator(device=device).manual_seed(seed)
         bf = torch.bfloat16
@@ -84,7 +87,7 @@ class HybridDecoder:
         for i in range(cfg.layers):
             L = SimpleNamespace(full=cfg.is_full(i), in_norm=w(H), post_norm=w(H),
                                 gate_up=w(2 * cfg.mlp, H) if cfg.mlp else None,
-                                down=w(H, cfg.mlp) if cfg.mlp else None)
+                                down=w(H, cfg.mlp) if cfg.mlp else None, gate_up_p=None)
             if L.full:
                 L.qkv = w(cfg.attn_heads * hd * 2 + 2 * kv * hd, H)
                 L.o = w(H, cfg.attn_heads * hd)
@@ -102,9 +105,18 @@ class HybridDecoder:
                 L.out = w(H, Hv * D)
                 self.slots.conv[i].copy_(torch.randn(n_slots, C, cfg.conv_k, generator=g_, device=device).to(bf))
                 self.slots.rec[i].copy_(0.02 * torch.randn(n_slots, Hv, D, D, generator=g_, device=device))
+            for name in ("in_proj", "out", "qkv", "o", "gate_up", "down"):
+                wt = getattr(L, name, None)
+                if wt is not None:
+                    setattr(L, name + "_p", PackedWeight(wt))
+                    if not keep_plain:
+                        setattr(L, name, None)
             self.layers.append(L)
         self.final_norm = w(H)
         self.lm_head = w(cfg.vocab, H) if cfg.vocab else None
+        self.lm_head_p = PackedWeight(self.lm_head) if cfg.vocab else None
+        if not keep_plain:
+            self.lm_head = None
         rd = int(hd * cfg.rotary_frac)
         self.inv_freq = 1.0 / (cfg.rope_theta ** (torch.arange(0, rd, 2, device=device, dtype=torch.float32) / rd))
         self.t_idx = torch.arange(self.max_ctx, device=device)
@@ -114,19 +126,19 @@ class HybridDecoder:
     def gdn(self, i, L, x):
         cfg, n = self.cfg, x.shape[0]
         Hv, D, C = cfg.gdn_v_heads, cfg.gdn_head, cfg.conv_dim
-        proj = x @ L.in_proj.t()                       # one GEMM for qkv | z | b | a
+        proj = decode_linear(x, L.in_proj_p)           # one product for qkv | z | b | a
         mixed = proj[:, :C]
         z = proj[:, C:C + Hv * D]
         b = proj[:, C + Hv * D:C + Hv * D + Hv]
         a = proj[:, C + Hv * D + Hv:]
         core = gdn_decode_core(mixed, z, a, b, self.slots.conv[i], L.conv_w, L.A_log, L.dt_bias, L.norm_w,
                                self.slots.rec[i], cfg.gdn_k_heads, Hv, D, cfg.eps)
-        return core.reshape(n, Hv * D) @ L.out.t()
+        return decode_linear(core.reshape(n, Hv * D), L.out_p)
 
     def attention(self, L, x):
         cfg, n = self.cfg, x.shape[0]
         nh, kv, hd = cfg.attn_heads, cfg.kv_heads, cfg.attn_head
-        proj = x @ L.qkv.t()
+        proj = decode_linear(x, L.qkv_p)
         qg = proj[:, :nh * hd * 2].reshape(n, nh, 2 * hd)
         q, gate = qg[..., :hd], qg[..., hd:].reshape(n, nh * hd)
         k = proj[:, nh * hd * 2:nh * hd * 2 + kv * hd].reshape(n, kv, hd)
@@ -150,24 +162,34 @@ class HybridDecoder:
         s = s.masked_fill((self.t_idx[None, :] > self.pos[:, None])[:, None, None, :], float("-inf"))
         p = torch.softmax(s, dim=-1).to(x.dtype)
         o = torch.matmul(p, L.v).reshape(n, nh * hd)                               # [n, kv, grp, hd]
-        return (o * torch.sigmoid(gate)) @ L.o.t()
+        return decode_linear(o * torch.sigmoid(gate), L.o_p)
 
     def mlp(self, L, x):
-        gu = x @ L.gate_up.t()
+        gu = decode_linear(x, L.gate_up_p)
         m = self.cfg.mlp
-        return (torch.nn.functional.silu(gu[:, :m]) * gu[:, m:]) @ L.down.t()
+        return decode_linear(torch.nn.functional.silu(gu[:, :m]) * gu[:, m:], L.down_p)
 
     def step(self, h):
         """h [N, hidden] bf16 (the step's token embeddings) -> logits [N, vocab] (or the final hidden
-        state without an LM head).  Advances every slot by one token."""
+        state without an LM head).  Advances every slot by one token.  Each residual add is fused
+        with the RMSNorm that follows it (Qwen3_5DecoderLayer.forward's order)."""
+        eps = self.cfg.eps
+        norms = []
+        for L in self.layers:
+            norms.append(L.in_norm)
+            if L.gate_up_p is not None:
+                norms.append(L.post_norm)
+        norms.append(self.final_norm)
+        h, x = add_rms_norm(h, None, norms[0], eps)
+        k = 1
         for i, L in enumerate(self.layers):
-            x = rms_norm(h, L.in_norm, self.cfg.eps)
-            h = h + (self.attention(L, x) if L.full else self.gdn(i, L, x))
-            if L.gate_up is not None:
-                h = h + self.mlp(L, rms_norm(h, L.post_norm, self.cfg.eps))
+            h, x = add_rms_norm(h, self.attention(L, x) if L.full else self.gdn(i, L, x), norms[k], eps)
+            k += 1
+            if L.gate_up_p is not None:
+                h, x = add_rms_norm(h, self.mlp(L, x), norms[k], eps)
+                k += 1
         self.pos += 1
-        h = rms_norm(h, self.final_norm, self.cfg.eps)
-        return h @ self.lm_head.t() if self.lm_head is not None else h
+        return decode_linear(x, self.lm_head_p) if self.lm_head_p is not None else x
 
 
 class HybridDecodeGraph:

@@ -265,6 +265,7 @@ def bench_hybrid(gdn, dev, steps=10, warmup=2, seed=4):
       * the 48 GDN layers alone with their projections (in_proj GEMM -> fused HIP core -> out_proj).
     HBM bytes: every weight read once per step, GDN states read + written, KV caches read."""
     hd = importlib.import_module(PKG + ".hybrid_decode")
+    cb = importlib.import_module(PKG + ".cb_engine")
     out = []
     for name, cfg in (("hybrid 64-layer stack (48 GDN + 16 attention, MLPs, LM head)", hd.HybridConfig()),
                       ("48 GDN layers with projections (no attention / MLP / LM head)",
@@ -284,9 +285,10 @@ def bench_hybrid(gdn, dev, steps=10, warmup=2, seed=4):
         e1.record()
         torch.cuda.synchronize()
         ms = e0.elapsed_time(e1) / steps
-        wbytes = sum(t.numel() * t.element_size() for L in model.layers for t in vars(L).values()
-                     if torch.is_tensor(t) and t.dtype == torch.bfloat16 and t.dim() == 2)
-        wbytes += model.lm_head.numel() * 2 if model.lm_head is not None else 0
+        packed = [v for L in model.layers for v in vars(L).values() if isinstance(v, cb.PackedWeight)]
+        packed += [model.lm_head_p] if model.lm_head_p is not None else []
+        wbytes = sum(p.N * p.K * 2 for p in packed)                     # the weights' own bytes
+        wbytes += sum(L.conv_w.numel() * 2 for L in model.layers if not L.full)
         sbytes = sum(2 * (model.slots.conv[i].numel() * 2 + model.slots.rec[i].numel() * 4) for i in model.slots.rec)
         kvbytes = sum(L.kt.numel() * 2 + L.v.numel() * 2 for L in model.layers if L.full)
         total = wbytes + sbytes + kvbytes

@@ -208,6 +208,43 @@ int gdn_conv_prefill_rows(const void* x, int64_t x_stride, const void* weight, c
                           int n_rows, int64_t total_tokens, const int32_t* cu_seqlens, int nseq,
                           int seq_len, int C, int K, void* stream);
 
+/*
+ * Decode-step projections: out[M, N] = x[M, K] W[N, K]^T, M <= 16 rows (one token per slot), bf16 x,
+ * W (nn.Linear weight layout [out_features, in_features]) and out, fp32 accumulation.  Replaces the
+ * GDN layer's in_proj_qkv / in_proj_z / in_proj_b / in_proj_a and out_proj calls of the decode step
+ * (src/cb_engine.py:320-323, :352; torch nn.Linear on the reference's device); the rest of a decode
+ * step's linears (attention, MLP, LM head) take it too.  K must be a multiple of 128; x and W rows
+ * 16-byte aligned.  workspace: fp32, gdn_decode_linear_workspace_bytes(M, N, K) bytes (0: none is
+ * needed -- K is split over workgroups, through the workspace, only when N is small).
+ */
+int64_t gdn_decode_linear_workspace_bytes(int M, int64_t N, int64_t K);
+int gdn_decode_linear(const void* x, int64_t x_stride, const void* W, int64_t w_stride, void* out,
+                      int64_t out_stride, int M, int64_t N, int64_t K, float* workspace,
+                      int64_t workspace_bytes, void* stream);
+
+/*
+ * The same product on a weight packed once (at load time) by gdn_decode_linear_pack into the
+ * kernel's fragment-major layout (gdn_decode_linear_packed_elems(N, K) bf16 values, rows padded to
+ * a multiple of 16 with zeros), so that every weight load reads 1 KB contiguous.
+ */
+int64_t gdn_decode_linear_packed_elems(int64_t N, int64_t K);
+int gdn_decode_linear_pack(const void* W, int64_t w_stride, void* packed, int64_t N, int64_t K, void* stream);
+int gdn_decode_linear_packed(const void* x, int64_t x_stride, const void* packed, void* out, int64_t out_stride,
+                             int M, int64_t N, int64_t K, float* workspace, int64_t workspace_bytes,
+                             void* stream);
+
+/*
+ * Residual add + RMSNorm between the layers of a decode step (HF Qwen3_5RMSNorm: fp32
+ * x * rsqrt(mean(x^2) + eps) * (1 + w), cast to bf16; the residual h + delta rounded to bf16 as
+ * torch does).  h, delta, h_out, x_out [M, H] bf16 rows, w [H] bf16.  delta NULL: x_out = norm(h)
+ * and h_out is not written; otherwise h_out = h + delta (h_out may be h) and x_out = norm(h_out).
+ * Replaces the residual adds and the input / post-attention layernorms around each layer
+ * (HF modeling_qwen3_5.py Qwen3_5DecoderLayer.forward) in the graph-captured decode step
+ * (src/cb_engine.py:153-172).
+ */
+int gdn_add_rmsnorm(const void* h, const void* delta, const void* w, void* h_out, void* x_out, int M, int H,
+                    float eps, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

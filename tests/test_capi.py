@@ -26,7 +26,9 @@ def test_header_declares_entry_points():
     syms = declared_symbols()
     for name in ("gdn_recurrent_step", "gdn_conv_update", "gdn_gated_rmsnorm", "gdn_decode_fused",
                  "gdn_chunk_prefill", "gdn_conv_prefill", "gdn_gating", "gdn_unit_lower_inv",
-                 "gdn_decode_fused_masked", "gdn_chunk_prefill_rows", "gdn_conv_prefill_rows"):
+                 "gdn_decode_fused_masked", "gdn_chunk_prefill_rows", "gdn_conv_prefill_rows",
+                 "gdn_decode_linear", "gdn_decode_linear_workspace_bytes", "gdn_decode_linear_pack",
+                 "gdn_decode_linear_packed", "gdn_add_rmsnorm"):
         assert name in syms
 
 
@@ -64,6 +66,22 @@ def test_version_limits_and_error_path(lib):
     assert rc == 1 and b"n_rows" in h.gdn_last_error()
     rc = h.gdn_conv_prefill_rows(p, 8, p, None, None, p, None, None, 5, 8, None, 1, 8, 8, 4, None)
     assert rc == 1 and b"n_rows" in h.gdn_last_error()
+    # decode projections: at most 16 rows, K a multiple of 128, packed size = padded rows x K
+    rc = h.gdn_decode_linear(p, 256, p, 256, p, 256, 17, 256, 256, None, 0, None)
+    assert rc == 2 and b"rows" in h.gdn_last_error()
+    rc = h.gdn_decode_linear(p, 256, p, 256, p, 256, 16, 256, 100, None, 0, None)
+    assert rc == 2 and b"multiple" in h.gdn_last_error()
+    rc = h.gdn_decode_linear_packed(p, 256, p, p, 256, 16, 256, 100, None, 0, None)
+    assert rc == 2 and b"multiple" in h.gdn_last_error()
+    assert h.gdn_decode_linear_workspace_bytes(16, 248320, 5120) == 0
+    small = h.gdn_decode_linear_workspace_bytes(16, 5120, 17408)
+    assert small > 0 and small % (16 * 5120 * 4) == 0
+    rc = h.gdn_decode_linear(p, 17408, p, 17408, p, 5120, 16, 5120, 17408, None, 0, None)
+    assert rc == 1 and b"workspace" in h.gdn_last_error()
+    assert h.gdn_decode_linear_packed_elems(98, 256) == 112 * 256
+    assert h.gdn_decode_linear_packed_elems(98, 100) == 0
+    rc = h.gdn_add_rmsnorm(p, p, p, None, p, 4, 256, ctypes.c_float(1e-6), None)
+    assert rc == 1 and b"null" in h.gdn_last_error()
     need = h.gdn_chunk_prefill_workspace_bytes(10, 32)
     assert need > 0 and need % 256 == 0
     with pytest.raises(lib.GDNError):

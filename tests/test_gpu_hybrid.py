@@ -26,7 +26,7 @@ def test_gdn_layer_with_projections_vs_oracle(gdn, oracle, dev):
     weights around the oracle's decode core; the layer's states match too."""
     hd = _hybrid(gdn)
     cfg = _small_cfg(hd)
-    model = hd.HybridDecoder(cfg, 3, [5, 17, 9], 4, dev, seed=40)
+    model = hd.HybridDecoder(cfg, 3, [5, 17, 9], 4, dev, seed=40, keep_plain=True)
     L = model.layers[0]
     g_ = torch.Generator().manual_seed(41)
     x = torch.randn(3, cfg.hidden, generator=g_).to(torch.bfloat16)
@@ -53,7 +53,7 @@ def test_attention_layer_vs_fp32_reference(gdn, dev):
     hd = _hybrid(gdn)
     cfg = _small_cfg(hd)
     ctx = [5, 17, 9]
-    model = hd.HybridDecoder(cfg, 3, ctx, 4, dev, seed=42)
+    model = hd.HybridDecoder(cfg, 3, ctx, 4, dev, seed=42, keep_plain=True)
     L = model.layers[3]
     g_ = torch.Generator().manual_seed(43)
     x = torch.randn(3, cfg.hidden, generator=g_).to(torch.bfloat16)
@@ -107,3 +107,42 @@ def test_hybrid_graph_replay_matches_eager(gdn, dev):
             assert rel_l2(graphed.slots.rec[i], eager.slots.rec[i]) <= 1e-5
             assert torch.equal(graphed.slots.conv[i], eager.slots.conv[i])
         assert torch.equal(graphed.pos, eager.pos)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("packed", [False, True])
+@pytest.mark.parametrize("M,N,K", [(16, 16480, 5120), (16, 5120, 6144), (3, 98, 256), (16, 1000, 17408),
+                                   (1, 4096, 1024)])
+def test_decode_linear_vs_fp32(gdn, dev, M, N, K, packed):
+    """The decode-projection kernel, on plain and on packed weights (split and unsplit K, row tails,
+    N not a multiple of 4 or 16), against an fp32 product of the same bf16 operands."""
+    from importlib import import_module
+    cb = import_module(PKG_NAME + ".cb_engine")
+    g_ = torch.Generator().manual_seed(M * 7 + N + K)
+    x = torch.randn(M, K, generator=g_).to(torch.bfloat16)
+    w = (0.02 * torch.randn(N, K, generator=g_)).to(torch.bfloat16)
+    wd = w.to(dev)
+    out = cb.decode_linear(x.to(dev), cb.PackedWeight(wd) if packed else wd).cpu()
+    ref = x.float() @ w.float().t()
+    assert out.shape == (M, N) and out.dtype == torch.bfloat16
+    # fp32 accumulation, one bf16 rounding: within a bf16 ulp of each element plus summation order
+    assert ((out.float() - ref).abs() <= ref.abs() * 2 ** -7 + 1e-3).all()
+
+
+@pytest.mark.gpu
+def test_add_rms_norm_vs_torch(gdn, dev):
+    """Fused residual add + Qwen3_5RMSNorm against the torch formula (residual rounded to bf16 first)."""
+    from importlib import import_module
+    cb = import_module(PKG_NAME + ".cb_engine")
+    hd = _hybrid(gdn)
+    g_ = torch.Generator().manual_seed(46)
+    h = torch.randn(5, 5120, generator=g_).to(torch.bfloat16)
+    d = torch.randn(5, 5120, generator=g_).to(torch.bfloat16)
+    w = (0.02 * torch.randn(5120, generator=g_)).to(torch.bfloat16)
+    h2, x = cb.add_rms_norm(h.to(dev), d.to(dev), w.to(dev))
+    assert torch.equal(h2.cpu(), h + d)
+    x_ref = hd.rms_norm(h + d, w, 1e-6)
+    assert ((x.cpu().float() - x_ref.float()).abs() <= x_ref.float().abs() * 2 ** -7 + 1e-6).all()
+    h3, x0 = cb.add_rms_norm(h.to(dev), None, w.to(dev))
+    assert torch.equal(h3.cpu(), h)
+    assert rel_l2(x0, hd.rms_norm(h, w, 1e-6)) <= 1e-3
