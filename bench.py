@@ -31,6 +31,9 @@ HBM_PEAK = 8.0e12          # B/s, MI355X HBM3E
 BF16_PEAK = 2.5e15         # flop/s, dense bf16 MFMA
 
 N_SLOTS, HK, HV, D, KC, LAYERS = 16, 16, 32, 128, 4, 48
+# HBM bytes per decode_fused_kernel launch at this workload, measured with two rocprofv3 --pmc runs
+# (FETCH_SIZE, WRITE_SIZE) scaled by what the counters read for a 256 MiB device copy
+DECODE_TRAFFIC = 69_988_966
 C = (2 * HK + HV) * D
 
 
@@ -360,7 +363,9 @@ def main():
         "config": {"workload": "GDN decode step, 16 slots x 1 token, H_k=16, H_v=32, d=128, conv 8192x4, "
                                "48 distinct layers, HIP-graph replay", "slots": N_SLOTS, "layers": LAYERS},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                     "frac": round(achieved * 1e9 / HBM_PEAK, 4), "traffic": None,
+                     "frac": round(achieved * 1e9 / HBM_PEAK, 4), "traffic": DECODE_TRAFFIC,
+                     "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, copy-calibrated "
+                                       "(profiles/decode_fused_kernel_16slot_Hv32_48layer.md)",
                      "kernel": "decode_fused_kernel<2,true>", "algorithmic_bytes_per_launch": bpl,
                      "us_per_launch_graph": round(dec["us_per_layer"], 3),
                      "us_per_launch_eager": round(dec["us_per_layer_eager"], 3)},
