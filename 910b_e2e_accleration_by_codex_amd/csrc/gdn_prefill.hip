@@ -279,27 +279,47 @@ __device__ __forceinline__ void load_rows4(u16x8* x, const uint16_t* base, int64
     x[i] = row < len ? *reinterpret_cast<const u16x8*>(base + (t0 + row) * stride + f0) : zero;
   }
 }
+// The pieces of torch's bf16 l2norm x * rsqrt(sum(x^2) + eps) (each op rounded to bf16), two
+// values at a time: the squares are exact in fp32, rounded to bf16 as a pair (v_cvt_pk_bf16_f32)
+// and added with one v_dot2 against (1, 1).
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float sumsq_bf16(u16x8 x, float acc) {
+  const u32x4v w = __builtin_bit_cast(u32x4v, x);
+  const bf16x2 one = __builtin_bit_cast(bf16x2, 0x3f803f80u);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float lo = __uint_as_float(w[i] << 16), hi = __uint_as_float(w[i] & 0xffff0000u);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, f2bf2(lo * lo, hi * hi)), one, acc, false);
+  }
+  return acc;
+}
+__device__ __forceinline__ u16x8 scale_bf16(u16x8 x, float s) {
+  const u32x4v w = __builtin_bit_cast(u32x4v, x);
+  u32x4v o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    o[i] = f2bf2(__uint_as_float(w[i] << 16) * s, __uint_as_float(w[i] & 0xffff0000u) * s);
+  return __builtin_bit_cast(u16x8, o);
+}
+// bf16(rsqrt(bf16(bf16(ss) + 1e-6))): hardware rsqrt and one Newton step (within an ulp of the
+// exact fp32 value before the bf16 rounding).
+__device__ __forceinline__ float l2norm_inv(float ss) {
+  const float x = rbf(rbf(ss) + 1e-6f);
+  float y = __builtin_amdgcn_rsqf(x);
+  y = y * (1.5f - 0.5f * x * y * y);
+  return rbf(y);
+}
 __device__ __forceinline__ void l2norm_rows4(u16x8* x) {
   float ss[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    ss[i] = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float f = bf2f(x[i][e]);
-      ss[i] += rbf(f * f);
-    }
-  }
+  for (int i = 0; i < 4; ++i) ss[i] = sumsq_bf16(x[i], 0.f);
 #pragma unroll
   for (int o = 1; o < 16; o <<= 1)
 #pragma unroll
     for (int i = 0; i < 4; ++i) ss[i] += __shfl_xor(ss[i], o, kWave);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float inv = rbf(rsqrt_f(rbf(rbf(ss[i]) + 1e-6f)));
-#pragma unroll
-    for (int e = 0; e < 8; ++e) x[i][e] = f2bf(bf2f(x[i][e]) * inv);
-  }
+  for (int i = 0; i < 4; ++i) x[i] = scale_bf16(x[i], l2norm_inv(ss[i]));
 }
 
 // A-fragment of a bf16 [rows, ld] tile in k-slot order (two 8-byte reads; see the workspace notes).
@@ -362,59 +382,90 @@ struct LocalSmem {
 };
 static_assert(pf::CH * pf::LDK * 2 <= pf::CH * pf::LDF * 4, "V must fit in the X buffer");
 
-template <typename BetaT>
-__global__ __launch_bounds__(pf::NT, 3) void chunk_local_kernel(
-    const uint16_t* __restrict__ q, int64_t qs, const uint16_t* __restrict__ k, int64_t ks,
-    const uint16_t* __restrict__ v, int64_t vs,
-    const float* __restrict__ g, const BetaT* __restrict__ beta, const int32_t* __restrict__ cu,
-    const int32_t* __restrict__ seq_chunk0, int nseq, int seq_len, int Hqk, int Hv, int use_l2,
-    uint8_t* __restrict__ work) {
-  using namespace pf;
-  __shared__ LocalSmem sm;
-  const int t = threadIdx.x, w = t >> 6, lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
-  const int h = blockIdx.x, slot = blockIdx.y;  // value heads fastest: the heads sharing a key head run together
-  const int hk = h / (Hv / Hqk);
-  const ChunkPos cp = chunk_pos(slot, cu, seq_chunk0, nseq, seq_len);
-  uint8_t* rec = work + ((int64_t)slot * Hv + h) * ws::BYTES;
-  const bool kq_owner = h % (Hv / Hqk) == 0;  // writes the key-head fragments KT and QG
-
-  // Every global load of the chunk is issued up front, so the chunk costs one memory round trip:
-  // K and V rows 4tq.. x features 8fb.. (thread (tq, fb)), Q rows 16w + l%16 in k-slot order
-  // (block s holds features 32s + 4g.. and 32s + 16 + 4g..), g and beta (wave 0, lane = token).
-  const int tq = t >> 4, fb = t & 15;
+// One (chunk, value head) item's global inputs in registers, all loads issued up front so the
+// item costs one memory round trip: K and V rows 4tq.. x features 8fb.. (thread (tq, fb)), Q rows
+// 16w + l%16 in k-slot order (block s holds features 32s + 4g.. and 32s + 16 + 4g..), g and beta
+// (wave 0, lane = token).
+struct LocalLoads {
   u16x8 kx[4], vreg[4], qr[4];
-  load_rows4(kx, k + (int64_t)hk * D, ks, cp.t0, cp.len, tq, 8 * fb);
-  load_rows4(vreg, v + (int64_t)h * D, vs, cp.t0, cp.len, tq, 8 * fb);
-  {
-    const u16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
-    const int row = 16 * w + c16;
+  float graw, braw;
+  ChunkPos cp;
+  int h, slot;
+};
+template <typename BetaT>
+__device__ __forceinline__ void local_loads(LocalLoads& L, int64_t item, const uint16_t* __restrict__ q, int64_t qs,
+                                            const uint16_t* __restrict__ k, int64_t ks,
+                                            const uint16_t* __restrict__ v, int64_t vs,
+                                            const float* __restrict__ g, const BetaT* __restrict__ beta,
+                                            const int32_t* __restrict__ cu, const int32_t* __restrict__ seq_chunk0,
+                                            int nseq, int seq_len, int Hqk, int Hv) {
+  using namespace pf;
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
+  // value heads fastest: the heads sharing a key head run next to each other
+  L.h = (int)(item % Hv);
+  L.slot = (int)(item / Hv);
+  L.cp = chunk_pos(L.slot, cu, seq_chunk0, nseq, seq_len);
+  const ChunkPos& cp = L.cp;
+  const int hk = L.h / (Hv / Hqk);
+  const int tq = t >> 4, fb = t & 15;
+  load_rows4(L.kx, k + (int64_t)hk * D, ks, cp.t0, cp.len, tq, 8 * fb);
+  load_rows4(L.vreg, v + (int64_t)L.h * D, vs, cp.t0, cp.len, tq, 8 * fb);
+  const u16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+  const int row = 16 * w + c16;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      if (row < cp.len) {
-        const uint16_t* p = q + (cp.t0 + row) * qs + (int64_t)hk * D + 32 * s + 4 * g4;
-        const u16x4 lo = *reinterpret_cast<const u16x4*>(p), hi = *reinterpret_cast<const u16x4*>(p + 16);
-        qr[s] = u16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      } else {
-        qr[s] = zero;
-      }
+  for (int s = 0; s < 4; ++s) {
+    if (row < cp.len) {
+      const uint16_t* p = q + (cp.t0 + row) * qs + (int64_t)hk * D + 32 * s + 4 * g4;
+      const u16x4 lo = *reinterpret_cast<const u16x4*>(p), hi = *reinterpret_cast<const u16x4*>(p + 16);
+      L.qr[s] = u16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    } else {
+      L.qr[s] = zero;
     }
   }
-  float graw = 0.f, braw = 0.f;  // padding: g = 0, beta = 0
+  L.graw = 0.f;  // padding: g = 0, beta = 0
+  L.braw = 0.f;
   if (w == 0 && lane < cp.len) {
-    graw = g[(cp.t0 + lane) * Hv + h];
-    braw = Elem<BetaT>::load(beta + (cp.t0 + lane) * Hv + h);
+    L.graw = g[(cp.t0 + lane) * Hv + L.h];
+    L.braw = Elem<BetaT>::load(beta + (cp.t0 + lane) * Hv + L.h);
   }
+}
+
+// Everything state-independent about one item, from its loaded inputs to its workspace record.
+__device__ __forceinline__ void local_item(LocalSmem& sm, const LocalLoads& L, int Hqk, int Hv, int use_l2,
+                                           uint8_t* __restrict__ work) {
+  using namespace pf;
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
+  const int h = L.h, slot = L.slot;
+  const ChunkPos& cp = L.cp;
+  uint8_t* rec = work + ((int64_t)slot * Hv + h) * ws::BYTES;
+  const bool kq_owner = h % (Hv / Hqk) == 0;  // writes the key-head fragments KT and QG
+  const int tq = t >> 4, fb = t & 15;
+  u16x8 kx[4], vreg[4], qr[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    kx[i] = L.kx[i];
+    vreg[i] = L.vreg[i];
+    qr[i] = L.qr[i];
+  }
+  const float graw = L.graw, braw = L.braw;
 
   // K: l2norm, row-major LDS copy, largest |K|
   {
     if (use_l2) l2norm_rows4(kx);
-    float m = 0.f;
+    // largest |K|: bf16 bit patterns with the sign cleared order like their magnitudes (NaN aside)
+    typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+    u16x2 mx = {0, 0};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       *reinterpret_cast<u16x8*>(&sm.K[(4 * tq + i) * LDK + 8 * fb]) = kx[i];
+      const u32x4v wv = __builtin_bit_cast(u32x4v, kx[i]);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(bf2f(kx[i][e])));
+      for (int e = 0; e < 4; ++e) {
+        const u16x2 a = __builtin_bit_cast(u16x2, wv[e] & 0x7fff7fffu);
+        mx = __builtin_elementwise_max(mx, a);
+      }
     }
+    float m = fmaxf(bf2f(mx[0]), bf2f(mx[1]));
     m = wave_max(m);
     if (lane == 0) sm.KMX[w] = m;
   }
@@ -424,19 +475,12 @@ __global__ __launch_bounds__(pf::NT, 3) void chunk_local_kernel(
     if (use_l2) {
       float ss = 0.f;
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float f = bf2f(qr[s][e]);
-          ss += rbf(f * f);
-        }
+      for (int s = 0; s < 4; ++s) ss = sumsq_bf16(qr[s], ss);
       ss += __shfl_xor(ss, 16, kWave);
       ss += __shfl_xor(ss, 32, kWave);
-      const float inv = rbf(rsqrt_f(rbf(rbf(ss) + 1e-6f)));
+      const float inv = l2norm_inv(ss);
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) qr[s][e] = f2bf(bf2f(qr[s][e]) * inv);
+      for (int s = 0; s < 4; ++s) qr[s] = scale_bf16(qr[s], inv);
     }
 #pragma unroll
     for (int s = 0; s < 4; ++s) qf[s] = __builtin_bit_cast(bf16x8, qr[s]);
@@ -485,31 +529,32 @@ __global__ __launch_bounds__(pf::NT, 3) void chunk_local_kernel(
       *reinterpret_cast<f16x8*>(rec + ws::KT + idx * 16) = o;
     }
   }
-  // A = K K^T (accumulator layout, rows = this wave's tokens) -> X in LDS; (Q K^T)^T = K Q^T, whose
-  // accumulator layout is exactly the k-slot ordered QK fragment layout -> workspace
+  // A = K K^T -> X in LDS, and (Q K^T)^T = K Q^T, whose accumulator layout is exactly the k-slot
+  // ordered QK fragment layout -> workspace.  Both are lower triangles of 16x16 blocks; wave w takes
+  // the A blocks of row tile 3 - w and the QK blocks of its own row tile w (whose q it holds), so
+  // every wave computes 5 blocks.
   {
+    const int ta = 3 - w;  // A row tile
     f32x4 accA[4], accQ[4];
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb) accA[cb] = accQ[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const bf16x8 ak = frag(sm.K, LDK, 16 * w, 32 * s, lane);
+      const bf16x8 ak = frag(sm.K, LDK, 16 * ta, 32 * s, lane);
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb) {
-        if (cb <= w) {
-          accA[cb] = mma(ak, frag(sm.K, LDK, 16 * cb, 32 * s, lane), accA[cb]);
-          accQ[cb] = mma(frag_kperm(sm.K, LDK, 16 * cb, 32 * s, lane), qf[s], accQ[cb]);
-        }
+        if (cb <= ta) accA[cb] = mma(ak, frag(sm.K, LDK, 16 * cb, 32 * s, lane), accA[cb]);
+        if (cb <= w) accQ[cb] = mma(frag_kperm(sm.K, LDK, 16 * cb, 32 * s, lane), qf[s], accQ[cb]);
       }
     }
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        {  // X[i][jj], i = 16w + 4g + r, jj = 16cb + c
-          const int i = 16 * w + 4 * g4 + r, jj = 16 * cb + c16;
+        {  // X[i][jj], i = 16 ta + 4g + r, jj = 16cb + c
+          const int i = 16 * ta + 4 * g4 + r, jj = 16 * cb + c16;
           float x = 0.f;
-          if (cb <= w && i > jj) x = -sm.B[i] * accA[cb][r] * __expf(sm.G[i] - sm.G[jj]);
+          if (cb <= ta && i > jj) x = -sm.B[i] * accA[cb][r] * __expf(sm.G[i] - sm.G[jj]);
           sm.X[i * LDF + jj] = x;
         }
         {  // QK[i][jj], i = 16w + c, jj = 16cb + 4g + r
@@ -587,6 +632,22 @@ __global__ __launch_bounds__(pf::NT, 3) void chunk_local_kernel(
       *reinterpret_cast<f16x4*>(rec + ws::U + ((cb * 64 + lane) * 4 + w) * 8) = hv;
     }
   }
+}
+
+// Grid (value heads, chunks): item = chunk slot x Hv + value head, value heads fastest so the heads
+// sharing a key head run next to each other.
+template <typename BetaT>
+__global__ __launch_bounds__(pf::NT, 3) void chunk_local_kernel(
+    const uint16_t* __restrict__ q, int64_t qs, const uint16_t* __restrict__ k, int64_t ks,
+    const uint16_t* __restrict__ v, int64_t vs,
+    const float* __restrict__ g, const BetaT* __restrict__ beta, const int32_t* __restrict__ cu,
+    const int32_t* __restrict__ seq_chunk0, int nseq, int seq_len, int Hqk, int Hv, int use_l2,
+    uint8_t* __restrict__ work) {
+  __shared__ LocalSmem sm;
+  LocalLoads L;
+  local_loads<BetaT>(L, (int64_t)blockIdx.y * gridDim.x + blockIdx.x, q, qs, k, ks, v, vs, g, beta, cu, seq_chunk0,
+                     nseq, seq_len, Hqk, Hv);
+  local_item(sm, L, Hqk, Hv, use_l2, work);
 }
 
 // ============================================================================================
