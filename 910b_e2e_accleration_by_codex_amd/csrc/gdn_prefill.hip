@@ -691,8 +691,65 @@ struct ScanSmem {
   uint8_t ring[3][rg::BYTES];
   uint8_t xch[3][6 * ws::FRAG];  // S (4 k-slot ordered bf16 B fragments) and vn (2)
   f32x4 part[2][4][64];          // the chain waves' partial sums of vn, [wave][token tile][lane]
+  float init_buf[2][pf::D * 16]; // the next sequences' initial state slices [row][16 columns]
   int flag[2];                   // step counter of each chain wave's published partial sum
 };
+
+// The sequences a scan workgroup walks: packed (cu / seq_chunk0) or uniform (seq_len tokens and
+// nch_u chunks each), and their state rows.  Indices are wave-uniform, so these are scalar loads.
+struct SeqTable {
+  const int32_t* cu;
+  const int32_t* chunk0;
+  const int32_t* rows;
+  int n_rows, seq_len, nch_u;
+  __device__ __forceinline__ int64_t start(int s) const { return cu ? (int64_t)cu[s] : (int64_t)s * seq_len; }
+  __device__ __forceinline__ int len(int s) const { return cu ? cu[s + 1] - cu[s] : seq_len; }
+  __device__ __forceinline__ int first_chunk(int s) const { return cu ? chunk0[s] : s * nch_u; }
+};
+// First sequence of group g when `groups` groups share the chunk stream: the first sequence whose
+// first chunk lies at or past g * total / groups (so groups hold whole sequences and differ by
+// at most one sequence's chunks).
+__device__ __forceinline__ int group_start(const SeqTable& t, int nseq, int64_t total, int groups, int g) {
+  if (g <= 0) return 0;
+  if (g >= groups) return nseq;
+  const int64_t q = total * g / groups;
+  int lo = 0, hi = nseq;  // first_chunk(nseq) == total >= q
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (t.first_chunk(mid) >= q) hi = mid;
+    else lo = mid + 1;
+  }
+  return lo;
+}
+// A position in a group's chunk stream: chunk c of the nch chunks of sequence s (which starts at
+// packed token t0, holds L tokens and keeps its states in slot row `row`, -1: none), k = the
+// ordinal of s among the group's non-empty sequences.
+struct Walk {
+  int s, c, nch, k, L, row;
+  int64_t t0;
+};
+__device__ __forceinline__ int next_nonempty(const SeqTable& t, int s, int s_hi) {
+  while (s < s_hi && t.len(s) == 0) ++s;
+  return s;
+}
+__device__ __forceinline__ void walk_open(Walk& w, const SeqTable& t, int s, int s_hi) {
+  w.s = s;
+  w.c = 0;
+  w.L = s < s_hi ? t.len(s) : 0;
+  w.nch = (w.L + pf::CH - 1) / pf::CH;
+  w.t0 = s < s_hi ? t.start(s) : 0;
+  w.row = s < s_hi ? state_row(t.rows, t.n_rows, s) : -1;
+}
+__device__ __forceinline__ void walk_begin(Walk& w, const SeqTable& t, int s_lo, int s_hi) {
+  walk_open(w, t, next_nonempty(t, s_lo, s_hi), s_hi);
+  w.k = 0;
+}
+__device__ __forceinline__ bool walk_last(const Walk& w) { return w.c == w.nch - 1; }
+__device__ __forceinline__ void walk_next(Walk& w, const SeqTable& t, int s_hi) {
+  if (++w.c < w.nch) return;
+  walk_open(w, t, next_nonempty(t, w.s + 1, s_hi), s_hi);
+  ++w.k;
+}
 
 // One chunk's operands for one chain wave (half = 0: S rows 0-63, 1: rows 64-127).
 // The KT fragments live outside: they are double-buffered, so that the next chunk's are read while
@@ -741,26 +798,62 @@ __device__ __forceinline__ void wait_flag(int* flag, int target) {
 __device__ __forceinline__ void set_flag(int* flag, int value, int lane) {
   if (lane == 0) __hip_atomic_store(flag, value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
-constexpr int kFragPieces = 2 * 16 * ws::FRAG / 16 / 128;  // WN + KT pieces of 16 bytes per loader lane
-constexpr int kLoadPieces = kFragPieces + 2;               // + one piece of U, + one of the header (lanes < 32)
-
-// loader lane lt (0..127): WN/KT pieces lt + 128 i (KT from the key head's record rec_kq), U piece lt
-// of slice n, header piece lt (< 32)
-__device__ __forceinline__ void scan_load(u16x8 (&r)[kLoadPieces], const uint8_t* rec, const uint8_t* rec_kq,
-                                          int n, int lt) {
-#pragma unroll
-  for (int i = 0; i < kFragPieces / 2; ++i) r[i] = *reinterpret_cast<const u16x8*>(rec + ws::WN + (lt + 128 * i) * 16);
-#pragma unroll
-  for (int i = kFragPieces / 2; i < kFragPieces; ++i)
-    r[i] = *reinterpret_cast<const u16x8*>(rec_kq + ws::WN + (lt + 128 * i) * 16);
-  r[kFragPieces] = *reinterpret_cast<const u16x8*>(rec + ws::U + n * 2048 + lt * 16);
-  if (lt < 32) r[kFragPieces + 1] = *reinterpret_cast<const u16x8*>(rec + ws::HDR + lt * 16);
+// The loader waves move a chunk's ring operands straight from L2 into LDS with global_load_lds
+// (16 bytes per lane: one wave instruction fills one 1 KiB fragment, lane l at byte 16 l), so the
+// data never passes through registers and the loaders issue no LDS stores.  Fragments of one
+// chunk: WN 0..15 and KT 0..15 (KT from the key head's record rec_kq), U fragments 2n, 2n+1 of
+// slice n, and the 512-byte header (lanes < 32).  Loader wave 0 issues WN 0-7, KT 0-7, U 0 and
+// the header (kDmaOps0 instructions), wave 1 WN 8-15, KT 8-15 and U 1 (kDmaOps1).
+constexpr int kDmaOps0 = 18, kDmaOps1 = 17;
+__device__ __forceinline__ void dma_frag(uint8_t* lds, const uint8_t* src, int lane) {
+  __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(src + lane * 16),
+                                   reinterpret_cast<uint32_t*>(lds), 16, 0, 0);
 }
-__device__ __forceinline__ void scan_store(uint8_t* dst, const u16x8 (&r)[kLoadPieces], int lt) {
+// The 128 x 16 fp32 initial-state slice at src (row pitch D floats) into an init_buf (row-major,
+// 64 bytes a row): 8 instructions, loader wave wl issues 4 (kInitOps).
+constexpr int kInitOps = 4;
+__device__ __forceinline__ void init_dma(float* dst, const float* src, int wl, int lane) {
 #pragma unroll
-  for (int i = 0; i < kFragPieces; ++i) *reinterpret_cast<u16x8*>(dst + rg::WN + (lt + 128 * i) * 16) = r[i];
-  *reinterpret_cast<u16x8*>(dst + rg::U + lt * 16) = r[kFragPieces];
-  if (lt < 32) *reinterpret_cast<u16x8*>(dst + rg::HDR + lt * 16) = r[kFragPieces + 1];
+  for (int i = kInitOps * wl; i < kInitOps * wl + kInitOps; ++i) {
+    const int p = 64 * i + lane;  // 16-byte piece: row p / 4, columns 4 (p % 4) ..
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(src + (p >> 2) * pf::D + 4 * (p & 3)),
+                                     reinterpret_cast<uint32_t*>(dst + 256 * i), 16, 0, 0);
+  }
+}
+__device__ __forceinline__ void scan_dma(uint8_t* dst, const uint8_t* rec, const uint8_t* rec_kq, int n, int wl,
+                                         int lane) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) dma_frag(dst + rg::WN + (8 * wl + i) * ws::FRAG, rec + ws::WN + (8 * wl + i) * ws::FRAG, lane);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) dma_frag(dst + rg::KT + (8 * wl + i) * ws::FRAG, rec_kq + ws::KT + (8 * wl + i) * ws::FRAG, lane);
+  dma_frag(dst + rg::U + wl * ws::FRAG, rec + ws::U + n * 2048 + wl * ws::FRAG, lane);
+  if (wl == 0 && lane < 32) dma_frag(dst + rg::HDR, rec + ws::HDR, lane);
+}
+// Wait until every chunk but the most recently issued one has landed in LDS (keep: the newest
+// chunk's copies may stay in flight) -- per-wave instruction counts, the loaders issue nothing else.
+__device__ __forceinline__ void dma_wait(int wl, bool keep) {
+  if (!keep) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  else if (wl == 0) asm volatile("s_waitcnt vmcnt(18)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(17)" ::: "memory");
+}
+static_assert(kDmaOps0 == 18 && kDmaOps1 == 17, "dma_wait's counts follow scan_dma");
+// The loaders' workgroup barrier.  __syncthreads() would also wait for every copy in flight (its
+// release fence covers the LDS the copies write); the loaders order their copies themselves with
+// dma_wait, so they meet the other waves at the bare barrier.  The LDS reads of a slot by the
+// other waves complete before those waves reach the barrier (their __syncthreads waits for them),
+// so a copy issued after the barrier cannot overtake them.
+__device__ __forceinline__ void loader_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+// The chain and output waves' workgroup barrier: it waits for their own LDS accesses (lgkmcnt 0),
+// which is all the other waves depend on; their global loads and stores (the output waves' next
+// operands, the rows of o and of final states) stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 // An output wave's per-chunk operands.  Output wave P handles token tiles A = P and B = 3 - P (one
@@ -830,43 +923,52 @@ __device__ __forceinline__ void out_step(const OutFrags& f, const uint8_t* xch, 
     }
   }
 }
-// An output wave: step c computes chunk c-1 (F0 / F1: even / odd chunks, loaded two chunks ahead).
+// An output wave: step c computes chunk c-1 of the stream (F0 / F1: even / odd chunks, loaded two
+// chunks ahead; the walk follows chunk c-1 for its sequence position).
 template <int P, typename OutT>
 __device__ __forceinline__ void output_wave(const ScanSmem& sm, const uint8_t* rec0, int64_t rstride,
-                                            int64_t kq_off, OutT* out, int64_t s0, int L, int nch, int Hv, int h,
-                                            int col0, int lane) {
+                                            int64_t kq_off, OutT* out, const SeqTable& tab, int s_lo, int s_hi,
+                                            int nch, int Hv, int h, int col0, int lane) {
   using namespace pf;
+  Walk w;
+  walk_begin(w, tab, s_lo, s_hi);
   OutFrags F0, F1;
   if (nch > 0) out_load<P>(F0, rec0, rec0 + kq_off, lane);
-  __syncthreads();  // prologue
+  lds_barrier();  // prologue
   if (nch > 1) out_load<P>(F1, rec0 + rstride, rec0 + rstride + kq_off, lane);
-  __syncthreads();  // step 0
-  int xp = 0;       // (c - 1) % 3
+  lds_barrier();  // step 0
+  int xp = 0;        // (c - 1) % 3
   for (int c = 1; c <= nch; c += 2) {
     {
-      const int cc = c - 1;  // even
-      const int len = L - cc * CH < CH ? L - cc * CH : CH;
-      out_step<P, OutT>(F0, sm.xch[xp], out, s0 + (int64_t)cc * CH, len, Hv, h, col0, lane);
+      const int len = w.L - w.c * CH < CH ? w.L - w.c * CH : CH;
+      out_step<P, OutT>(F0, sm.xch[xp], out, w.t0 + (int64_t)w.c * CH, len, Hv, h, col0, lane);
+      walk_next(w, tab, s_hi);
       if (c + 1 < nch) out_load<P>(F0, rec0 + (int64_t)(c + 1) * rstride, rec0 + (int64_t)(c + 1) * rstride + kq_off, lane);
       xp = xp == 2 ? 0 : xp + 1;
-      __syncthreads();  // end of step c
+      lds_barrier();  // end of step c
     }
     if (c + 1 <= nch) {
-      const int cc = c;  // odd
-      const int len = L - cc * CH < CH ? L - cc * CH : CH;
-      out_step<P, OutT>(F1, sm.xch[xp], out, s0 + (int64_t)cc * CH, len, Hv, h, col0, lane);
+      const int len = w.L - w.c * CH < CH ? w.L - w.c * CH : CH;
+      out_step<P, OutT>(F1, sm.xch[xp], out, w.t0 + (int64_t)w.c * CH, len, Hv, h, col0, lane);
+      walk_next(w, tab, s_hi);
       if (c + 2 < nch) out_load<P>(F1, rec0 + (int64_t)(c + 2) * rstride, rec0 + (int64_t)(c + 2) * rstride + kq_off, lane);
       xp = xp == 2 ? 0 : xp + 1;
-      __syncthreads();  // end of step c+1
+      lds_barrier();  // end of step c+1
     }
   }
 }
 
-// One chain step for chunk c: `in` and `fk` hold chunk c's operands on entry; chunk c+1's are read
-// into `in` and `fk_next` once the partial sums are swapped (ring slot `nxt`).
+// What a chain step does after its update when its chunk ends a sequence: store this lane's final
+// state column (fin; nullptr: not kept) and continue from the next sequence's initial state (nxt:
+// this lane's column of an init_buf; nullptr: zeros).
+struct Swap {
+  bool last;
+  float* fin;
+  const float* nxt;
+};
 template <int HALF>
 __device__ __forceinline__ void chain_step(ScanSmem& sm, f32x4 (&S)[4], bf16x8 (&Sb)[2], ChainIn& in, KFrags& fk,
-                                           KFrags& fk_next, int c, int nch, int& x0, int lane) {
+                                           KFrags& fk_next, int c, int nch, int& x0, const Swap& sw, int lane) {
   uint8_t* xch = sm.xch[x0];
   const int x1 = x0 == 2 ? 0 : x0 + 1;
   const uint8_t* nxt = sm.ring[x1];  // chunk c+1 sits in ring slot (c+1) % 3
@@ -968,6 +1070,19 @@ __device__ __forceinline__ void chain_step(ScanSmem& sm, f32x4 (&S)[4], bf16x8 (
       S[i] *= post;
     }
   }
+  if (sw.last) {
+    const int g4 = lane >> 4;
+    if (sw.fin) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sw.fin[(64 * HALF + 16 * i + 4 * g4 + r) * pf::D] = S[i][r];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) S[i][r] = sw.nxt ? sw.nxt[(64 * HALF + 16 * i + 4 * g4 + r) * 16] : 0.f;
+  }
   uint8_t* xn = sm.xch[x1];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -975,22 +1090,35 @@ __device__ __forceinline__ void chain_step(ScanSmem& sm, f32x4 (&S)[4], bf16x8 (
     *reinterpret_cast<bf16x8*>(&xn[(2 * HALF + j) * ws::FRAG + lane * 16]) = Sb[j];
   }
   x0 = x1;
-  __syncthreads();  // end of step c
+  lds_barrier();  // end of step c
 }
 
-// The chain wave holding S rows 64 HALF .. 64 HALF + 63 (4 accumulator tiles).
+// The chain wave holding S rows 64 HALF .. 64 HALF + 63 (4 accumulator tiles) of one 16-column
+// slice (this lane: column col) through every chunk of its group's sequences: at a sequence's last
+// chunk the step stores the final state and continues from the next sequence's initial state,
+// which the loader waves have staged in init_buf[(k + 1) & 1].  The walk runs one chunk ahead
+// (wn), so its table reads are in flight a whole step before they are needed.  The chain's
+// barriers wait only for its LDS accesses: its final-state stores need no ordering with the
+// other waves.
 template <int HALF>
 __device__ __forceinline__ void chain_wave(ScanSmem& sm, const float* __restrict__ init,
-                                           float* __restrict__ final_state, int srow, int64_t sbase, int nch,
-                                           int lane) {
+                                           float* __restrict__ final_state, int Hv, int h, int col,
+                                           const SeqTable& tab, int s_lo, int s_hi, int nch, int lane) {
   using namespace pf;
   const int g4 = lane >> 4;
+  auto state_col = [&](const float* base, int row) -> const float* {  // this lane's column of a state
+    return (base && row >= 0) ? base + ((int64_t)row * Hv + h) * D * D + col : nullptr;
+  };
+  Walk w, wn;  // chunk c, chunk c+1
+  walk_begin(w, tab, s_lo, s_hi);
+  wn = w;
+  walk_next(wn, tab, s_hi);
   f32x4 S[4];
+  const float* s0 = state_col(init, w.row);
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      S[i][r] = (init && srow >= 0) ? init[sbase + (int64_t)(64 * HALF + 16 * i + 4 * g4 + r) * D] : 0.f;
+    for (int r = 0; r < 4; ++r) S[i][r] = s0 ? s0[(64 * HALF + 16 * i + 4 * g4 + r) * D] : 0.f;
   bf16x8 Sb[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -998,54 +1126,68 @@ __device__ __forceinline__ void chain_wave(ScanSmem& sm, const float* __restrict
     *reinterpret_cast<bf16x8*>(&sm.xch[0][(2 * HALF + j) * ws::FRAG + lane * 16]) = Sb[j];
   }
   if (lane == 0) sm.flag[HALF] = 0;
-  __syncthreads();  // prologue
+  lds_barrier();  // prologue
   ChainIn in;
   KFrags fk0, fk1;  // chunks c even / odd
   if (nch > 0) {
     chain_read_w<HALF>(in, sm.ring[0], lane);
     chain_read_k<HALF>(fk0, sm.ring[0], lane);
   }
+  auto swap_of = [&]() {
+    Swap sw{false, nullptr, nullptr};
+    if (walk_last(w)) {  // then wn is the first chunk of the next non-empty sequence (if any)
+      sw.last = true;
+      sw.fin = const_cast<float*>(state_col(final_state, w.row));
+      if (state_col(init, wn.row)) sw.nxt = sm.init_buf[(w.k + 1) & 1] + (lane & 15);
+    }
+    return sw;
+  };
   int x0 = 0;  // c % 3
   for (int c = 0; c < nch; c += 2) {
-    chain_step<HALF>(sm, S, Sb, in, fk0, fk1, c, nch, x0, lane);
-    if (c + 1 < nch) chain_step<HALF>(sm, S, Sb, in, fk1, fk0, c + 1, nch, x0, lane);
+    chain_step<HALF>(sm, S, Sb, in, fk0, fk1, c, nch, x0, swap_of(), lane);
+    w = wn;
+    walk_next(wn, tab, s_hi);
+    if (c + 1 < nch) {
+      chain_step<HALF>(sm, S, Sb, in, fk1, fk0, c + 1, nch, x0, swap_of(), lane);
+      w = wn;
+      walk_next(wn, tab, s_hi);
+    }
   }
-  __syncthreads();  // step nch (the output waves' last chunk)
-  if (final_state && srow >= 0) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) final_state[sbase + (int64_t)(64 * HALF + 16 * i + 4 * g4 + r) * D] = S[i][r];
-  }
+  lds_barrier();  // step nch (the output waves' last chunk)
 }
 
+// The scan: one workgroup per (sequence group, value head, 16-column slice).  A group is a run of
+// whole sequences; its chunk records are consecutive workspace slots, so the workgroup streams
+// them in order and carries the state across sequence boundaries (groups == nseq: one sequence per
+// workgroup).
 template <typename OutT>
 __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(
     const float* __restrict__ init, float* __restrict__ final_state, OutT* __restrict__ out,
     const int32_t* __restrict__ cu, const int32_t* __restrict__ seq_chunk0, const int32_t* __restrict__ rows,
-    int n_rows, int nseq, int seq_len, int Hqk, int Hv, const uint8_t* __restrict__ work) {
+    int n_rows, int nseq, int seq_len, int Hqk, int Hv, int groups, int64_t total_chunks,
+    const uint8_t* __restrict__ work) {
   using namespace pf;
   __shared__ ScanSmem sm;
-  // block -> (sequence-head pair, slice); the 8 slices of a pair share blockIdx % 8 and therefore an
+  // block -> (group-head pair, slice); the 8 slices of a pair share blockIdx % 8 and therefore an
   // XCD (workgroups are dispatched round-robin over the 8 XCDs), so they share one L2.
   const int b = blockIdx.x;
   const int pair = (b >> 6) * 8 + (b & 7), n = (b >> 3) & 7;
-  if (pair >= nseq * Hv) return;
-  const int h = pair % Hv, seq = pair / Hv;
-  const int t = threadIdx.x, lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
-  const int role = __builtin_amdgcn_readfirstlane(t >> 6);
-  int64_t s0;
-  int L, slot0;
-  if (cu) {
-    s0 = cu[seq];
-    L = cu[seq + 1] - cu[seq];
-    slot0 = seq_chunk0[seq];
+  if (pair >= groups * Hv) return;
+  const int h = pair % Hv, grp = pair / Hv;
+  const SeqTable tab{cu, seq_chunk0, rows, n_rows, seq_len, (seq_len + CH - 1) / CH};
+  int s_lo, s_hi;
+  if (groups == nseq) {
+    s_lo = grp;
+    s_hi = grp + 1;
   } else {
-    s0 = (int64_t)seq * seq_len;
-    L = seq_len;
-    slot0 = seq * ((seq_len + CH - 1) / CH);
+    s_lo = group_start(tab, nseq, total_chunks, groups, grp);
+    s_hi = group_start(tab, nseq, total_chunks, groups, grp + 1);
   }
-  const int nch = (L + CH - 1) / CH;
+  if (s_lo >= s_hi) return;
+  const int slot0 = tab.first_chunk(s_lo);
+  const int nch = tab.first_chunk(s_hi) - slot0;  // chunks of the group's stream
+  const int t = threadIdx.x, lane = t & 63, c16 = lane & 15;
+  const int role = __builtin_amdgcn_readfirstlane(t >> 6);
   const int64_t rstride = (int64_t)Hv * ws::BYTES;
   const uint8_t* rec0 = work + (int64_t)slot0 * rstride + (int64_t)h * ws::BYTES;
   const int64_t kq_off = -(int64_t)(h % (Hv / Hqk)) * ws::BYTES;  // record of the key head's owner
@@ -1053,40 +1195,69 @@ __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(
 
   if (role < 2) {
     // ---------------- chain waves ----------------
-    const int srow = state_row(rows, n_rows, seq);  // slot row of this sequence's states (-1: none)
-    const int64_t sbase = ((int64_t)(srow < 0 ? 0 : srow) * Hv + h) * D * D + col;
-    if (role == 0) chain_wave<0>(sm, init, final_state, srow, sbase, nch, lane);
-    else chain_wave<1>(sm, init, final_state, srow, sbase, nch, lane);
+    if (role == 0) chain_wave<0>(sm, init, final_state, Hv, h, col, tab, s_lo, s_hi, nch, lane);
+    else chain_wave<1>(sm, init, final_state, Hv, h, col, tab, s_lo, s_hi, nch, lane);
   } else if (role < 4) {
     // ---------------- output waves: step c computes chunk c-1 ----------------
-    if (role == 2) output_wave<0, OutT>(sm, rec0, rstride, kq_off, out, s0, L, nch, Hv, h, 16 * n, lane);
-    else output_wave<1, OutT>(sm, rec0, rstride, kq_off, out, s0, L, nch, Hv, h, 16 * n, lane);
+    if (role == 2) output_wave<0, OutT>(sm, rec0, rstride, kq_off, out, tab, s_lo, s_hi, nch, Hv, h, 16 * n, lane);
+    else output_wave<1, OutT>(sm, rec0, rstride, kq_off, out, tab, s_lo, s_hi, nch, Hv, h, 16 * n, lane);
   } else {
     // ---------------- loader waves ----------------
-    const int lt = t - 256;
-    u16x8 R0[kLoadPieces], R1[kLoadPieces];  // even / odd chunks
-    if (nch > 0) scan_load(R0, rec0, rec0 + kq_off, n, lt);
-    if (nch > 1) scan_load(R1, rec0 + rstride, rec0 + rstride + kq_off, n, lt);
-    if (nch > 0) scan_store(sm.ring[0], R0, lt);
-    if (nch > 1) scan_store(sm.ring[1], R1, lt);
-    if (nch > 2) scan_load(R0, rec0 + 2 * rstride, rec0 + 2 * rstride + kq_off, n, lt);
-    if (nch > 3) scan_load(R1, rec0 + 3 * rstride, rec0 + 3 * rstride + kq_off, n, lt);
-    __syncthreads();  // prologue
-    // step c: stage chunk c+2 (held in R[c&1]) into ring slot (c+2)%3, then load chunk c+4
-    int slot = 2;  // (c + 2) % 3
-    for (int c = 0; c < nch; c += 2) {
-      if (c + 2 < nch) scan_store(sm.ring[slot], R0, lt);
-      if (c + 4 < nch) scan_load(R0, rec0 + (int64_t)(c + 4) * rstride, rec0 + (int64_t)(c + 4) * rstride + kq_off, n, lt);
-      slot = slot == 2 ? 0 : slot + 1;
-      __syncthreads();  // end of step c
-      if (c + 1 < nch) {
-        if (c + 3 < nch) scan_store(sm.ring[slot], R1, lt);
-        if (c + 5 < nch) scan_load(R1, rec0 + (int64_t)(c + 5) * rstride, rec0 + (int64_t)(c + 5) * rstride + kq_off, n, lt);
-        slot = slot == 2 ? 0 : slot + 1;
-        __syncthreads();  // end of step c+1
+    const int wl = role - 4, lt = t - 256;
+    // Empty sequences have no chunks: their final state is their initial state (zeros without
+    // one).  Loader lane lt copies row lt of the slice.
+    if (final_state) {
+      for (int s = s_lo; s < s_hi; ++s) {
+        if (tab.len(s) != 0) continue;
+        const int r = state_row(rows, n_rows, s);
+        if (r < 0) continue;
+        const int64_t off = ((int64_t)r * Hv + h) * D * D + (int64_t)lt * D + 16 * n;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f32x4 x = init ? *reinterpret_cast<const f32x4*>(init + off + 4 * q) : f32x4{0.f, 0.f, 0.f, 0.f};
+          *reinterpret_cast<f32x4*>(final_state + off + 4 * q) = x;
+        }
       }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the copies below count their own loads
     }
-    __syncthreads();  // step nch
+    // Chunk j sits in ring slot j % 3.  The chain reads chunk j's operands during step j-1 (chunk 0:
+    // after the prologue barrier), so from step j on that slot is free: step j (>= 1) starts the
+    // copy of chunk j+3 into it, and the copy has steps j and j+1 to land (chunk 3, started at
+    // step 1, has one step).  Before the barrier that ends step j, chunk j+2 must be complete.
+    // When chunk j+1 ends the k-th sequence, step j (the prologue for j+1 = 0) also copies the
+    // next sequence's initial state slice into init_buf[(k + 1) & 1], issued before the chunk
+    // copy, so it is complete at the same barrier; the chain reads it at the end of step j+1.
+    // The other buffer may still be read during that step, and a buffer is reused two sequences
+    // later, after the step that read it ended.
+    auto dma_chunk = [&](int c) {
+      const uint8_t* rec = rec0 + (int64_t)c * rstride;
+      scan_dma(sm.ring[c % 3], rec, rec + kq_off, n, wl, lane);
+    };
+    Walk w;  // follows chunk j+1
+    walk_begin(w, tab, s_lo, s_hi);
+    auto dma_next_init = [&]() {
+      if (!init || !walk_last(w)) return;
+      Walk w2 = w;  // the next non-empty sequence's first chunk
+      walk_next(w2, tab, s_hi);
+      if (w2.row >= 0) init_dma(sm.init_buf[(w.k + 1) & 1], init + ((int64_t)w2.row * Hv + h) * D * D + 16 * n, wl, lane);
+    };
+    if (nch > 0) dma_next_init();
+    if (nch > 0) dma_chunk(0);
+    if (nch > 1) dma_chunk(1);
+    if (nch > 2) dma_chunk(2);
+    dma_wait(wl, nch > 2);  // chunks 0 and 1 (and the initial state after chunk 0)
+    loader_barrier();       // prologue
+    for (int c = 0; c < nch; ++c) {
+      walk_next(w, tab, s_hi);
+      if (c + 1 < nch) dma_next_init();
+      if (c == 1 && 3 < nch) dma_chunk(3);
+      const bool issued = c >= 1 && c + 3 < nch;
+      if (issued) dma_chunk(c + 3);
+      dma_wait(wl, issued);  // chunk c+2 (and the initial state after chunk c+1)
+      loader_barrier();      // end of step c
+    }
+    dma_wait(wl, false);
+    loader_barrier();  // step nch
   }
 }
 
@@ -1252,6 +1423,27 @@ extern "C" int gdn_unit_lower_inv(const float* X, float* T, int64_t batch, int n
   return check_launch("gdn_unit_lower_inv");
 }
 
+namespace {
+// Compute units of the current device (cached per device).
+int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+int scan_groups(int nseq, int Hv) {
+  const int per_group = 8 * Hv, cus = device_cus();
+  if (nseq <= 1 || per_group > cus) return nseq;
+  const int g = cus / per_group;
+  return g < nseq ? g : nseq;
+}
+}  // namespace
+
 extern "C" int64_t gdn_chunk_prefill_workspace_bytes(int64_t total_chunks, int Hv) {
   return total_chunks * (int64_t)Hv * ws::BYTES;
 }
@@ -1280,6 +1472,8 @@ extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const voi
                   v_stride % 8 == 0,
               "gdn_chunk_prefill: q/k/v rows must be 16-byte aligned");
   GDN_REQUIRE(aligned(out, 8), "gdn_chunk_prefill: out must be 8-byte aligned");
+  GDN_REQUIRE((!initial_state || aligned(initial_state, 16)) && (!final_state || aligned(final_state, 16)),
+              "gdn_chunk_prefill: initial/final state must be 16-byte aligned");
   GDN_REQUIRE(total_chunks == 0 || (workspace && aligned(workspace, 256) &&
                                     workspace_bytes >= gdn_chunk_prefill_workspace_bytes(total_chunks, Hv)),
               "gdn_chunk_prefill: workspace missing, misaligned or smaller than %lld bytes",
@@ -1304,11 +1498,15 @@ extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const voi
     int rc = check_launch("gdn_chunk_prefill(local)");
     if (rc) return rc;
   }
-  const int64_t pairs = (int64_t)nseq * Hv;
+  // Sequence groups: when the Hv x 8 workgroups of one group leave CUs free, split the sequences
+  // into as many groups (balanced by chunks) as fill the CUs once; each workgroup then streams its
+  // group's sequences back to back.  Otherwise one sequence per workgroup.
+  const int groups = scan_groups(nseq, Hv);
+  const int64_t pairs = (int64_t)groups * Hv;
   const int64_t scan_blocks = (pairs + 7) / 8 * 64;
   chunk_scan_kernel<uint16_t><<<(unsigned)scan_blocks, kScanThreads, 0, s>>>(
       initial_state, final_state, (uint16_t*)out, cu_seqlens, seq_chunk0, state_rows, n_rows, nseq, seq_len, Hqk,
-      Hv, work);
+      Hv, groups, total_chunks, work);
   return check_launch("gdn_chunk_prefill(state)");
 }
 

@@ -103,6 +103,31 @@ def test_chunk_prefill_varlen_matches_per_sequence(gdn, oracle, dev):
                                            cu_seqlens=torch.tensor([0, 5, 3, T], dtype=torch.int32))
 
 
+@pytest.mark.parametrize("with_state", [True, False])
+def test_chunk_prefill_many_sequences_grouped(gdn, oracle, dev, with_state):
+    """40 packed sequences at H_v=4: the scan streams several whole sequences per workgroup and
+    carries the state across their boundaries (lengths 0, 1, 63, 64, 65 and random up to 200)."""
+    g_ = torch.Generator().manual_seed(31)
+    lens = [0, 1, 63, 64, 65, 0, 0, 130] + torch.randint(0, 201, (32,), generator=g_).tolist()
+    lens[20] = 0
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int32)
+    T = int(cu[-1])
+    Hk, Hv = 2, 4
+    q, k, v, g, beta, _ = _gdn_inputs(T, Hk, Hv, seed=32, state=False)
+    s0 = 0.02 * torch.randn(len(lens), Hv, 128, 128, generator=g_) if with_state else None
+    o_ref, s_ref = oracle.chunk_gated_delta_rule_varlen(_rep(q, 2), _rep(k, 2), v, g, beta, cu, 64, s0, True, True)
+    o, s = gdn.fast_chunk_gated_delta_rule_v2(q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta.to(dev),
+                                              initial_state=s0.to(dev) if with_state else None,
+                                              output_final_state=True, use_qk_l2norm_in_kernel=True,
+                                              cu_seqlens=cu.tolist())
+    assert rel_l2(o, o_ref) <= OUT_TOL
+    for i, L in enumerate(lens):
+        if L == 0:  # an empty sequence keeps its initial state exactly (zeros without one)
+            assert torch.equal(s[i].cpu(), s0[i] if with_state else torch.zeros(Hv, 128, 128))
+        else:
+            assert rel_l2(s[i], s_ref[i]) <= STATE_TOL, (i, L)
+
+
 def test_chunk_prefill_split_invariance(gdn, dev):
     """Prefill in two pieces with final -> initial state equals one call (prefill_chunk contract)."""
     q, k, v, g, beta, s0 = _gdn_inputs(320, 2, 4, seed=14)
