@@ -665,14 +665,15 @@ __global__ __launch_bounds__(pf::NT, 3) void chunk_local_kernel(
 //   waves 2-3 (output): o = Qg S + QK vn one chunk behind the chain (two token tiles each), from
 //                    the S and vn the chain published in LDS and Qg / QK fragments they load
 //                    themselves two chunks ahead
-//   waves 4-5:       stage each chunk's WN and KT fragments, this slice's U tiles and the header
-//                    (34.5 KiB) in a 3-slot LDS ring, loading them from global memory two chunks
-//                    before they are staged
+//   waves 4-5:       copy each chunk's WN and KT fragments, this slice's U tiles and the header
+//                    (34.5 KiB) from L2 into a 3-slot LDS ring, two steps ahead
+//   wave 6:          touches the records of the chunk kPrefetchAhead steps ahead, so they are in
+//                    L2 (fetched from HBM once for the head's 8 slices) before they are copied
 // One barrier per chunk.  During step c the chain computes chunk c from registers it read out of
 // ring slot c%3 during step c-1, reads chunk c+1 from slot (c+1)%3 into registers, and writes
 // vn(c) and S(c+1) into exchange slots c%3 and (c+1)%3; the output waves read exchange slot (c-1)%3;
-// the loaders fill ring slot (c+2)%3.  So no LDS read latency sits on the chain's critical path
-// beyond the partial-sum swap.
+// the loaders fill ring slot c%3 with chunk c+3.  So no LDS read latency sits on the chain's
+// critical path beyond the partial-sum swap.
 // The state update runs on fp16 MFMA.  Usually DEC vn and K^T fit fp16 as they are (see the fast
 // path); otherwise DEC vn is scaled per column by a power of two sigma into [2^14, 2^15) and K^T
 // by kappa, and the product is folded in as S' = (GL S sigma kappa + P) / (sigma kappa), so the fp32
@@ -680,7 +681,8 @@ __global__ __launch_bounds__(pf::NT, 3) void chunk_local_kernel(
 namespace rg {  // one ring slot
 constexpr int WN = 0, KT = 16 * ws::FRAG, U = 32 * ws::FRAG, HDR = U + 2048, BYTES = HDR + 512;
 }  // namespace rg
-constexpr int kScanThreads = 384;  // 2 chain waves, 2 output waves, 2 loader waves
+constexpr int kScanThreads = 448;  // 2 chain waves, 2 output waves, 2 loader waves, 1 prefetch wave
+constexpr int kPrefetchAhead = 6;  // chunks between the L2 prefetch and the chain step
 __device__ __forceinline__ bf16x8 lds_frag(const uint8_t* base, int f, int lane) {
   return *reinterpret_cast<const bf16x8*>(base + f * ws::FRAG + lane * 16);
 }
@@ -692,6 +694,7 @@ struct ScanSmem {
   uint8_t xch[3][6 * ws::FRAG];  // S (4 k-slot ordered bf16 B fragments) and vn (2)
   f32x4 part[2][4][64];          // the chain waves' partial sums of vn, [wave][token tile][lane]
   float init_buf[2][pf::D * 16]; // the next sequences' initial state slices [row][16 columns]
+  uint32_t pf_sink[64];          // landing place of the prefetch wave's copies (never read)
   int flag[2];                   // step counter of each chain wave's published partial sum
 };
 
@@ -818,6 +821,27 @@ __device__ __forceinline__ void init_dma(float* dst, const float* src, int wl, i
     const int p = 64 * i + lane;  // 16-byte piece: row p / 4, columns 4 (p % 4) ..
     __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(src + (p >> 2) * pf::D + 4 * (p & 3)),
                                      reinterpret_cast<uint32_t*>(dst + 256 * i), 16, 0, 0);
+  }
+}
+// L2 prefetch of the lines slice n of a head reads from one chunk's records: its eighth of WN, KT
+// (key head's record) and QG (key head's record), its U tiles, an eighth of QK, the header and
+// the row factors -- 78 lines of 128 bytes, 2 instructions.  Each lane copies one dword of its
+// line into pf_sink (4-byte global_load_lds), so nothing lands in registers; the lines stay in the
+// XCD's L2 for the other slices, which run on the same XCD.
+__device__ __forceinline__ void scan_prefetch(uint32_t* sink, const uint8_t* rec, const uint8_t* rec_kq, int n,
+                                              int lane) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int x = 64 * i + lane;
+    const uint8_t* p = nullptr;
+    if (x < 16) p = rec + ws::WN + (16 * n + x) * 128;
+    else if (x < 32) p = rec_kq + ws::KT + (16 * n + x - 16) * 128;
+    else if (x < 48) p = rec + ws::U + n * 2048 + (x - 32) * 128;
+    else if (x < 64) p = rec_kq + ws::QG + (16 * n + x - 48) * 128;
+    else if (x < 72) p = rec + ws::QK + (8 * n + x - 64) * 128;
+    else if (x < 76) p = rec + ws::HDR + (x - 72) * 128;
+    else if (x < 78) p = rec + ws::EGS + (x - 76) * 128;
+    if (p) __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(p), sink, 4, 0, 0);
   }
 }
 __device__ __forceinline__ void scan_dma(uint8_t* dst, const uint8_t* rec, const uint8_t* rec_kq, int n, int wl,
@@ -1201,6 +1225,22 @@ __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(
     // ---------------- output waves: step c computes chunk c-1 ----------------
     if (role == 2) output_wave<0, OutT>(sm, rec0, rstride, kq_off, out, tab, s_lo, s_hi, nch, Hv, h, 16 * n, lane);
     else output_wave<1, OutT>(sm, rec0, rstride, kq_off, out, tab, s_lo, s_hi, nch, Hv, h, 16 * n, lane);
+  } else if (role == 6) {
+    // ---------------- prefetch wave: chunk c + kPrefetchAhead at step c ----------------
+    // Its copies are never waited for until the end (their own wave's counter), so a slow HBM
+    // fetch delays nothing; at most a few dozen are in flight.
+    auto touch = [&](int c) {
+      const uint8_t* rec = rec0 + (int64_t)c * rstride;
+      scan_prefetch(sm.pf_sink, rec, rec + kq_off, n, lane);
+    };
+    for (int c = 3; c < kPrefetchAhead && c < nch; ++c) touch(c);
+    loader_barrier();  // prologue
+    for (int c = 0; c < nch; ++c) {
+      if (c + kPrefetchAhead < nch) touch(c + kPrefetchAhead);
+      loader_barrier();  // end of step c
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no copy may land after the workgroup ends
+    loader_barrier();  // step nch
   } else {
     // ---------------- loader waves ----------------
     const int wl = role - 4, lt = t - 256;
