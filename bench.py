@@ -126,10 +126,14 @@ def prefill_layer_bytes(T, nseq, hv=HV, d=D, c=C, k=KC):
 
 
 def _time(fn, reps, dev):
+    """GPU time per call with the host enqueueing ahead (as a serving loop does): a spin kernel of
+    ~20 ms keeps the GPU busy while the timed calls are queued, so the event window holds only
+    their GPU work, not the host's time to issue the first call."""
     fn()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(50_000_000)
     e0.record(stream)
     for _ in range(reps):
         fn()

@@ -119,7 +119,8 @@ int64_t gdn_chunk_prefill_workspace_bytes(int64_t total_chunks, int Hv);
  *   q, k [total_tokens, Hqk, D] bf16, token stride q_stride / k_stride (value head h reads key
  *        head h / (Hv / Hqk));  v [total_tokens, Hv, D] bf16, token stride v_stride
  *   g [total_tokens, Hv] fp32 (log decay);  beta [total_tokens, Hv] (beta_dtype)
- *   initial_state / final_state [nseq, Hv, D, D] fp32, either may be NULL (zero / not written)
+ *   initial_state / final_state [nseq, Hv, D, D] fp32, 16-byte aligned, either may be NULL
+ *     (zero / not written)
  *   out [total_tokens, Hv, D] bf16 (dense)
  *   cu_seqlens: device int32 [nseq+1] (packed varlen) with seq_chunk0: device int32 [nseq+1],
  *     seq_chunk0[s] = sum over earlier sequences of ceil(len/64); or both NULL for nseq
