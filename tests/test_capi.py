@@ -66,6 +66,10 @@ def test_version_limits_and_error_path(lib):
     assert rc == 1 and b"n_rows" in h.gdn_last_error()
     rc = h.gdn_conv_prefill_rows(p, 8, p, None, None, p, None, None, 5, 8, None, 1, 8, 8, 4, None)
     assert rc == 1 and b"n_rows" in h.gdn_last_error()
+    # the scan copies 16-byte pieces of initial states: states must be 16-byte aligned
+    rc = h.gdn_chunk_prefill(p, 0, p, 0, p, 0, p, p, 1, ctypes.c_void_p(256 + 4), None, p, 64, None, None, 1, 1,
+                             64, 16, 32, 128, 1, 1, p, 1 << 30, None)
+    assert rc == 1 and b"16-byte" in h.gdn_last_error()
     # decode projections: at most 16 rows, K a multiple of 128, packed size = padded rows x K
     rc = h.gdn_decode_linear(p, 256, p, 256, p, 256, 17, 256, 256, None, 0, None)
     assert rc == 2 and b"rows" in h.gdn_last_error()
