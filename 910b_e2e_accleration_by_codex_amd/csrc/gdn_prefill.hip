@@ -382,73 +382,73 @@ struct LocalSmem {
 };
 static_assert(pf::CH * pf::LDK * 2 <= pf::CH * pf::LDF * 4, "V must fit in the X buffer");
 
-// One (chunk, value head) item's global inputs in registers, all loads issued up front so the
-// item costs one memory round trip: K and V rows 4tq.. x features 8fb.. (thread (tq, fb)), Q rows
-// 16w + l%16 in k-slot order (block s holds features 32s + 4g.. and 32s + 16 + 4g..), g and beta
-// (wave 0, lane = token).
-struct LocalLoads {
-  u16x8 kx[4], vreg[4], qr[4];
-  float graw, braw;
+// One (chunk, key head) item's inputs shared by the key head's value heads, all loads issued up
+// front: K rows 4tq.. x features 8fb.. (thread (tq, fb)) and Q rows 16w + l%16 in k-slot order
+// (block s holds features 32s + 4g.. and 32s + 16 + 4g..).
+struct KeyLoads {
+  u16x8 kx[4], qr[4];
   ChunkPos cp;
-  int h, slot;
+  int hk, slot;
 };
-template <typename BetaT>
-__device__ __forceinline__ void local_loads(LocalLoads& L, int64_t item, const uint16_t* __restrict__ q, int64_t qs,
-                                            const uint16_t* __restrict__ k, int64_t ks,
-                                            const uint16_t* __restrict__ v, int64_t vs,
-                                            const float* __restrict__ g, const BetaT* __restrict__ beta,
-                                            const int32_t* __restrict__ cu, const int32_t* __restrict__ seq_chunk0,
-                                            int nseq, int seq_len, int Hqk, int Hv) {
+// One value head's inputs for that chunk: V rows like K, g and beta (wave 0, lane = token).
+struct HeadLoads {
+  u16x8 vreg[4];
+  float graw, braw;
+};
+__device__ __forceinline__ void key_loads(KeyLoads& L, int64_t item, const uint16_t* __restrict__ q, int64_t qs,
+                                          const uint16_t* __restrict__ k, int64_t ks,
+                                          const int32_t* __restrict__ cu, const int32_t* __restrict__ seq_chunk0,
+                                          int nseq, int seq_len, int Hqk) {
   using namespace pf;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
-  // value heads fastest: the heads sharing a key head run next to each other
-  L.h = (int)(item % Hv);
-  L.slot = (int)(item / Hv);
+  L.hk = (int)(item % Hqk);
+  L.slot = (int)(item / Hqk);
   L.cp = chunk_pos(L.slot, cu, seq_chunk0, nseq, seq_len);
   const ChunkPos& cp = L.cp;
-  const int hk = L.h / (Hv / Hqk);
   const int tq = t >> 4, fb = t & 15;
-  load_rows4(L.kx, k + (int64_t)hk * D, ks, cp.t0, cp.len, tq, 8 * fb);
-  load_rows4(L.vreg, v + (int64_t)L.h * D, vs, cp.t0, cp.len, tq, 8 * fb);
+  load_rows4(L.kx, k + (int64_t)L.hk * D, ks, cp.t0, cp.len, tq, 8 * fb);
   const u16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
   const int row = 16 * w + c16;
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     if (row < cp.len) {
-      const uint16_t* p = q + (cp.t0 + row) * qs + (int64_t)hk * D + 32 * s + 4 * g4;
+      const uint16_t* p = q + (cp.t0 + row) * qs + (int64_t)L.hk * D + 32 * s + 4 * g4;
       const u16x4 lo = *reinterpret_cast<const u16x4*>(p), hi = *reinterpret_cast<const u16x4*>(p + 16);
       L.qr[s] = u16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     } else {
       L.qr[s] = zero;
     }
   }
-  L.graw = 0.f;  // padding: g = 0, beta = 0
-  L.braw = 0.f;
+}
+template <typename BetaT>
+__device__ __forceinline__ void head_loads(HeadLoads& H, const ChunkPos& cp, int h, const uint16_t* __restrict__ v,
+                                           int64_t vs, const float* __restrict__ g, const BetaT* __restrict__ beta,
+                                           int Hv) {
+  using namespace pf;
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  load_rows4(H.vreg, v + (int64_t)h * D, vs, cp.t0, cp.len, t >> 4, 8 * (t & 15));
+  H.graw = 0.f;  // padding: g = 0, beta = 0
+  H.braw = 0.f;
   if (w == 0 && lane < cp.len) {
-    L.graw = g[(cp.t0 + lane) * Hv + L.h];
-    L.braw = Elem<BetaT>::load(beta + (cp.t0 + lane) * Hv + L.h);
+    H.graw = g[(cp.t0 + lane) * Hv + h];
+    H.braw = Elem<BetaT>::load(beta + (cp.t0 + lane) * Hv + h);
   }
 }
 
-// Everything state-independent about one item, from its loaded inputs to its workspace record.
-__device__ __forceinline__ void local_item(LocalSmem& sm, const LocalLoads& L, int Hqk, int Hv, int use_l2,
-                                           uint8_t* __restrict__ work) {
+// The key head's part of an item: l2norm of K (row-major LDS copy, largest |K| -> kappa) and of Q
+// (k-slot ordered fragments qf, kept in registers), and the key-head fragments QG and kappa K^T,
+// written into the record of the key head's first value head (rec).  Returns kappa's exponent.
+__device__ __forceinline__ int local_key(LocalSmem& sm, const KeyLoads& L, int use_l2, bf16x8 (&qf)[4],
+                                         uint8_t* __restrict__ rec) {
   using namespace pf;
-  const int t = threadIdx.x, w = t >> 6, lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
-  const int h = L.h, slot = L.slot;
-  const ChunkPos& cp = L.cp;
-  uint8_t* rec = work + ((int64_t)slot * Hv + h) * ws::BYTES;
-  const bool kq_owner = h % (Hv / Hqk) == 0;  // writes the key-head fragments KT and QG
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const int tq = t >> 4, fb = t & 15;
-  u16x8 kx[4], vreg[4], qr[4];
+  u16x8 kx[4], qr[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     kx[i] = L.kx[i];
-    vreg[i] = L.vreg[i];
     qr[i] = L.qr[i];
   }
-  const float graw = L.graw, braw = L.braw;
-
   // K: l2norm, row-major LDS copy, largest |K|
   {
     if (use_l2) l2norm_rows4(kx);
@@ -470,7 +470,6 @@ __device__ __forceinline__ void local_item(LocalSmem& sm, const LocalLoads& L, i
     if (lane == 0) sm.KMX[w] = m;
   }
   // Q: l2norm in registers (a row is spread over lanes l%16 + 16g' and the 4 blocks)
-  bf16x8 qf[4];
   {
     if (use_l2) {
       float ss = 0.f;
@@ -484,6 +483,48 @@ __device__ __forceinline__ void local_item(LocalSmem& sm, const LocalLoads& L, i
     }
 #pragma unroll
     for (int s = 0; s < 4; ++s) qf[s] = __builtin_bit_cast(bf16x8, qr[s]);
+  }
+  __syncthreads();
+  // QG fragments (this wave's token tile, straight from the k-slot ordered Q fragments) and the
+  // kappa-scaled fp16 K^T fragments
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+    *reinterpret_cast<bf16x8*>(rec + ws::QG + (w * 4 + s) * ws::FRAG + lane * 16) = qf[s];
+  const float kmax = fmaxf(fmaxf(sm.KMX[0], sm.KMX[1]), fmaxf(sm.KMX[2], sm.KMX[3]));
+  const int ke = fp16_fit_exp(kmax);
+  const float kappa = ldexpf(1.0f, ke);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int idx = t + NT * i;  // fragment idx / 64 = (rb, j), lane idx % 64
+    const int f_ = idx >> 6, rb = f_ >> 1, j = f_ & 1;  // idx % 64 == lane (idx = t + 256 i)
+    const u16x8 kt = frag_tr_kperm(sm.K, LDK, 32 * j, 16 * rb, lane);
+    f16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = (_Float16)(bf2f(kt[e]) * kappa);
+    *reinterpret_cast<f16x8*>(rec + ws::KT + idx * 16) = o;
+  }
+  return ke;
+}
+
+// One value head's part: cumulative decay, X = -(beta K K^T o decay) and the QK fragments, the
+// inverse, W and U -- everything state-independent about (chunk, value head), into its record.
+// sm.K holds the key head's normalised K; the caller has synchronised since the last value head.
+__device__ __forceinline__ void local_head(LocalSmem& sm, const HeadLoads& H, const bf16x8 (&qf)[4], int ke,
+                                           uint8_t* __restrict__ rec) {
+  using namespace pf;
+  // the thread index through an opaque move: the caller loops over value heads, and addresses
+  // derived from it would otherwise be hoisted out of that loop and held in registers
+  int t;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"((int)threadIdx.x));
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
+  const int tq = t >> 4, fb = t & 15;
+  u16x8 vreg[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) vreg[i] = H.vreg[i];
+  const float graw = H.graw, braw = H.braw;
+  if (t == 0) {
+    reinterpret_cast<float*>(rec + ws::KSC)[0] = ldexpf(1.0f, -ke);
+    reinterpret_cast<float*>(rec + ws::KAP)[0] = ldexpf(1.0f, ke);
   }
   if (w == 0) {  // cumulative decay within the chunk
     float G = graw;
@@ -503,32 +544,6 @@ __device__ __forceinline__ void local_item(LocalSmem& sm, const LocalLoads& L, i
   }
   __syncthreads();
 
-  // QG fragments (this wave's token tile, straight from the k-slot ordered Q fragments) and the
-  // kappa-scaled fp16 K^T fragments, written once per key head
-  {
-    if (kq_owner) {
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-        *reinterpret_cast<bf16x8*>(rec + ws::QG + (w * 4 + s) * ws::FRAG + lane * 16) = qf[s];
-    }
-    const float kmax = fmaxf(fmaxf(sm.KMX[0], sm.KMX[1]), fmaxf(sm.KMX[2], sm.KMX[3]));
-    const int ke = fp16_fit_exp(kmax);
-    const float kappa = ldexpf(1.0f, ke);
-    if (t == 0) {
-      reinterpret_cast<float*>(rec + ws::KSC)[0] = ldexpf(1.0f, -ke);
-      reinterpret_cast<float*>(rec + ws::KAP)[0] = kappa;
-    }
-#pragma unroll
-    for (int i = 0; i < 4 && kq_owner; ++i) {
-      const int idx = t + NT * i;  // fragment idx / 64 = (rb, j), lane idx % 64
-      const int f_ = idx >> 6, rb = f_ >> 1, j = f_ & 1;  // idx % 64 == lane (idx = t + 256 i)
-      const u16x8 kt = frag_tr_kperm(sm.K, LDK, 32 * j, 16 * rb, lane);
-      f16x8 o;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = (_Float16)(bf2f(kt[e]) * kappa);
-      *reinterpret_cast<f16x8*>(rec + ws::KT + idx * 16) = o;
-    }
-  }
   // A = K K^T -> X in LDS, and (Q K^T)^T = K Q^T, whose accumulator layout is exactly the k-slot
   // ordered QK fragment layout -> workspace.  Both are lower triangles of 16x16 blocks; wave w takes
   // the A blocks of row tile 3 - w and the QK blocks of its own row tile w (whose q it holds), so
@@ -634,8 +649,9 @@ __device__ __forceinline__ void local_item(LocalSmem& sm, const LocalLoads& L, i
   }
 }
 
-// Grid (value heads, chunks): item = chunk slot x Hv + value head, value heads fastest so the heads
-// sharing a key head run next to each other.
+// Grid (key heads, chunks): one workgroup per (chunk, key head) does the key head's shared work
+// once and then each of its Hv / Hqk value heads in turn (the next head's inputs load while the
+// current one is computed).
 template <typename BetaT>
 __global__ __launch_bounds__(pf::NT, 3) void chunk_local_kernel(
     const uint16_t* __restrict__ q, int64_t qs, const uint16_t* __restrict__ k, int64_t ks,
@@ -644,10 +660,22 @@ __global__ __launch_bounds__(pf::NT, 3) void chunk_local_kernel(
     const int32_t* __restrict__ seq_chunk0, int nseq, int seq_len, int Hqk, int Hv, int use_l2,
     uint8_t* __restrict__ work) {
   __shared__ LocalSmem sm;
-  LocalLoads L;
-  local_loads<BetaT>(L, (int64_t)blockIdx.y * gridDim.x + blockIdx.x, q, qs, k, ks, v, vs, g, beta, cu, seq_chunk0,
-                     nseq, seq_len, Hqk, Hv);
-  local_item(sm, L, Hqk, Hv, use_l2, work);
+  const int r = Hv / Hqk;
+  KeyLoads KL;
+  key_loads(KL, (int64_t)blockIdx.y * gridDim.x + blockIdx.x, q, qs, k, ks, cu, seq_chunk0, nseq, seq_len, Hqk);
+  const int h0 = KL.hk * r;
+  HeadLoads H;
+  head_loads<BetaT>(H, KL.cp, h0, v, vs, g, beta, Hv);
+  uint8_t* rec0 = work + ((int64_t)KL.slot * Hv + h0) * ws::BYTES;
+  bf16x8 qf[4];
+  const int ke = local_key(sm, KL, use_l2, qf, rec0);
+  for (int j = 0; j < r; ++j) {
+    if (j > 0) {
+      head_loads<BetaT>(H, KL.cp, h0 + j, v, vs, g, beta, Hv);
+      __syncthreads();  // this head rewrites the decay arrays and X
+    }
+    local_head(sm, H, qf, ke, rec0 + (int64_t)j * ws::BYTES);
+  }
 }
 
 // ============================================================================================
@@ -1524,7 +1552,7 @@ extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const voi
   hipStream_t s = (hipStream_t)stream;
   uint8_t* work = (uint8_t*)workspace;
   if (total_chunks > 0) {
-    dim3 g1((unsigned)Hv, (unsigned)total_chunks);
+    dim3 g1((unsigned)Hqk, (unsigned)total_chunks);
     if (beta_dtype == GDN_BF16)
       chunk_local_kernel<uint16_t><<<g1, pf::NT, 0, s>>>((const uint16_t*)q, q_stride, (const uint16_t*)k, k_stride,
                                                          (const uint16_t*)v, v_stride,
