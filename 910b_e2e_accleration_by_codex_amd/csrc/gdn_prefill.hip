@@ -506,6 +506,54 @@ __device__ __forceinline__ int local_key(LocalSmem& sm, const KeyLoads& L, int u
   return ke;
 }
 
+// A = K K^T -> X in LDS, and (Q K^T)^T = K Q^T, whose accumulator layout is exactly the k-slot
+// ordered QK fragment layout -> workspace.  Both are lower triangles of 16x16 blocks; wave W takes
+// the A blocks of row tile 3 - W and the QK blocks of its own row tile W (whose q it holds), so
+// every wave computes 5 blocks.  X carries -beta_i and the decay e^{G_i - G_j}, QK the scale and
+// the decay; sm.G and sm.B hold the value head's cumulative decay and beta.
+template <int W>
+__device__ __forceinline__ void aqk_blocks(LocalSmem& sm, const bf16x8 (&qf)[4], uint8_t* __restrict__ rec,
+                                           int lane) {
+  using namespace pf;
+  constexpr int TA = 3 - W;  // A row tile
+  const int c16 = lane & 15, g4 = lane >> 4;
+  f32x4 accA[TA + 1], accQ[W + 1];
+#pragma unroll
+  for (int cb = 0; cb <= TA; ++cb) accA[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int cb = 0; cb <= W; ++cb) accQ[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const bf16x8 ak = frag(sm.K, LDK, 16 * TA, 32 * s, lane);
+#pragma unroll
+    for (int cb = 0; cb <= TA; ++cb) accA[cb] = mma(ak, frag(sm.K, LDK, 16 * cb, 32 * s, lane), accA[cb]);
+#pragma unroll
+    for (int cb = 0; cb <= W; ++cb) accQ[cb] = mma(frag_kperm(sm.K, LDK, 16 * cb, 32 * s, lane), qf[s], accQ[cb]);
+  }
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {  // X[i][jj], i = 16 TA + 4g + r, jj = 16cb + c
+      const int i = 16 * TA + 4 * g4 + r, jj = 16 * cb + c16;
+      float x = 0.f;
+      if (cb <= TA && i > jj) x = -sm.B[i] * accA[cb <= TA ? cb : 0][r] * __expf(sm.G[i] - sm.G[jj]);
+      sm.X[i * LDF + jj] = x;
+    }
+  f32x4 qk[4];
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {  // QK[i][jj], i = 16W + c, jj = 16cb + 4g + r
+      const int i = 16 * W + c16, jj = 16 * cb + 4 * g4 + r;
+      qk[cb][r] = (cb <= W && i >= jj) ? kScale * accQ[cb <= W ? cb : 0][r] * __expf(sm.G[i] - sm.G[jj]) : 0.f;
+    }
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    if (2 * j <= W)  // fragment (W, j) is non-zero only when its first column block 2j <= W
+      *reinterpret_cast<bf16x8*>(rec + ws::QK + (W * 2 + j) * ws::FRAG + lane * 16) =
+          pack_acc_bf16(qk[2 * j], qk[2 * j + 1]);
+}
+
 // One value head's part: cumulative decay, X = -(beta K K^T o decay) and the QK fragments, the
 // inverse, W and U -- everything state-independent about (chunk, value head), into its record.
 // sm.K holds the key head's normalised K; the caller has synchronised since the last value head.
@@ -544,44 +592,13 @@ __device__ __forceinline__ void local_head(LocalSmem& sm, const HeadLoads& H, co
   }
   __syncthreads();
 
-  // A = K K^T -> X in LDS, and (Q K^T)^T = K Q^T, whose accumulator layout is exactly the k-slot
-  // ordered QK fragment layout -> workspace.  Both are lower triangles of 16x16 blocks; wave w takes
-  // the A blocks of row tile 3 - w and the QK blocks of its own row tile w (whose q it holds), so
-  // every wave computes 5 blocks.
-  {
-    const int ta = 3 - w;  // A row tile
-    f32x4 accA[4], accQ[4];
-#pragma unroll
-    for (int cb = 0; cb < 4; ++cb) accA[cb] = accQ[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const bf16x8 ak = frag(sm.K, LDK, 16 * ta, 32 * s, lane);
-#pragma unroll
-      for (int cb = 0; cb < 4; ++cb) {
-        if (cb <= ta) accA[cb] = mma(ak, frag(sm.K, LDK, 16 * cb, 32 * s, lane), accA[cb]);
-        if (cb <= w) accQ[cb] = mma(frag_kperm(sm.K, LDK, 16 * cb, 32 * s, lane), qf[s], accQ[cb]);
-      }
-    }
-#pragma unroll
-    for (int cb = 0; cb < 4; ++cb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        {  // X[i][jj], i = 16 ta + 4g + r, jj = 16cb + c
-          const int i = 16 * ta + 4 * g4 + r, jj = 16 * cb + c16;
-          float x = 0.f;
-          if (cb <= ta && i > jj) x = -sm.B[i] * accA[cb][r] * __expf(sm.G[i] - sm.G[jj]);
-          sm.X[i * LDF + jj] = x;
-        }
-        {  // QK[i][jj], i = 16w + c, jj = 16cb + 4g + r
-          const int i = 16 * w + c16, jj = 16 * cb + 4 * g4 + r;
-          accQ[cb][r] = (cb <= w && i >= jj) ? kScale * accQ[cb][r] * __expf(sm.G[i] - sm.G[jj]) : 0.f;
-        }
-      }
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-      if (2 * j <= w)  // fragment (w, j) is non-zero only when its first column block 2j <= w
-        *reinterpret_cast<bf16x8*>(rec + ws::QK + (w * 2 + j) * ws::FRAG + lane * 16) =
-            pack_acc_bf16(accQ[2 * j], accQ[2 * j + 1]);
+  // A = K K^T -> X in LDS and the QK fragments -> workspace (aqk_blocks), with the wave index as a
+  // compile-time constant so every block bound is static
+  switch (w) {
+    case 0: aqk_blocks<0>(sm, qf, rec, lane); break;
+    case 1: aqk_blocks<1>(sm, qf, rec, lane); break;
+    case 2: aqk_blocks<2>(sm, qf, rec, lane); break;
+    default: aqk_blocks<3>(sm, qf, rec, lane); break;
   }
   __syncthreads();
 
