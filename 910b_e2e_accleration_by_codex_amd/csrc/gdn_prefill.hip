@@ -270,13 +270,16 @@ __device__ __forceinline__ ChunkPos chunk_pos(int slot, const int32_t* cu, const
 // Load 4 token rows x 8 features (rows 4*tq.., features f0..f0+7) of a [tokens, heads*D] bf16
 // tensor, zero beyond `len`, and l2-normalise each row (a row is spread over 16 consecutive lanes)
 // with the rounding of torch bf16 ops.
+// Rows past the chunk's end (len >= 1) read its last row and are zeroed afterwards: every load is
+// issued unconditionally, so the group goes out back to back with no branch around it.
 __device__ __forceinline__ void load_rows4(u16x8* x, const uint16_t* base, int64_t stride, int64_t t0, int len,
                                            int tq, int f0) {
   const u16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = 4 * tq + i;
-    x[i] = row < len ? *reinterpret_cast<const u16x8*>(base + (t0 + row) * stride + f0) : zero;
+    const u16x8 r = *reinterpret_cast<const u16x8*>(base + (t0 + (row < len ? row : len - 1)) * stride + f0);
+    x[i] = row < len ? r : zero;
   }
 }
 // The pieces of torch's bf16 l2norm x * rsqrt(sum(x^2) + eps) (each op rounded to bf16), two
@@ -408,16 +411,13 @@ __device__ __forceinline__ void key_loads(KeyLoads& L, int64_t item, const uint1
   const int tq = t >> 4, fb = t & 15;
   load_rows4(L.kx, k + (int64_t)L.hk * D, ks, cp.t0, cp.len, tq, 8 * fb);
   const u16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
-  const int row = 16 * w + c16;
+  const int row = 16 * w + c16, rowc = row < cp.len ? row : cp.len - 1;
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    if (row < cp.len) {
-      const uint16_t* p = q + (cp.t0 + row) * qs + (int64_t)L.hk * D + 32 * s + 4 * g4;
-      const u16x4 lo = *reinterpret_cast<const u16x4*>(p), hi = *reinterpret_cast<const u16x4*>(p + 16);
-      L.qr[s] = u16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-    } else {
-      L.qr[s] = zero;
-    }
+    const uint16_t* p = q + (cp.t0 + rowc) * qs + (int64_t)L.hk * D + 32 * s + 4 * g4;
+    const u16x4 lo = *reinterpret_cast<const u16x4*>(p), hi = *reinterpret_cast<const u16x4*>(p + 16);
+    const u16x8 x = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    L.qr[s] = row < cp.len ? x : zero;
   }
 }
 template <typename BetaT>
@@ -427,12 +427,12 @@ __device__ __forceinline__ void head_loads(HeadLoads& H, const ChunkPos& cp, int
   using namespace pf;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   load_rows4(H.vreg, v + (int64_t)h * D, vs, cp.t0, cp.len, t >> 4, 8 * (t & 15));
-  H.graw = 0.f;  // padding: g = 0, beta = 0
-  H.braw = 0.f;
-  if (w == 0 && lane < cp.len) {
-    H.graw = g[(cp.t0 + lane) * Hv + h];
-    H.braw = Elem<BetaT>::load(beta + (cp.t0 + lane) * Hv + h);
-  }
+  // padding tokens: g = 0, beta = 0 (their loads read the chunk's last token)
+  const int tok = lane < cp.len ? lane : cp.len - 1;
+  const float gr = g[(cp.t0 + tok) * Hv + h];
+  const float br = Elem<BetaT>::load(beta + (cp.t0 + tok) * Hv + h);
+  H.graw = w == 0 && lane < cp.len ? gr : 0.f;
+  H.braw = w == 0 && lane < cp.len ? br : 0.f;
 }
 
 // The key head's part of an item: l2norm of K (row-major LDS copy, largest |K| -> kappa) and of Q
