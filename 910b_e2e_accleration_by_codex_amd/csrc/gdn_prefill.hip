@@ -805,6 +805,7 @@ __device__ __forceinline__ void walk_next(Walk& w, const SeqTable& t, int s_hi) 
 struct ChainIn {
   bf16x8 fw[8];  // WN fragments (tb, k-block 2 half + j) at [tb * 2 + j]
   f16x8 u[2];    // this lane's U values (tiles 0,1 | 2,3); wave 0 only
+  f32x4 uf[4];   // the same, scaled to fp32 (chain_u_convert); wave 0 only
   f32x4 dv[4];   // DEC of this lane's tokens
   f32x4 usc;     // wave 0 only
   float gl, ksc, kap;
@@ -829,22 +830,44 @@ __device__ __forceinline__ void chain_read_w(ChainIn& in, const uint8_t* ring, i
 #pragma unroll
   for (int tb = 0; tb < 4; ++tb) in.dv[tb] = *reinterpret_cast<const f32x4*>(hdr + 16 * tb + 4 * g4);
 }
+// U -> fp32 with its tile scales (1 unless |U| left [2^-4, 2^14); same value in every lane), done
+// once the reads have landed, off the next step's critical path.
+__device__ __forceinline__ void chain_u_convert(ChainIn& in) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    in.uf[0][r] = (float)in.u[0][r];
+    in.uf[1][r] = (float)in.u[0][4 + r];
+    in.uf[2][r] = (float)in.u[1][r];
+    in.uf[3][r] = (float)in.u[1][4 + r];
+  }
+  const bool unit = in.usc[0] == 1.0f && in.usc[1] == 1.0f && in.usc[2] == 1.0f && in.usc[3] == 1.0f;
+  if (!__builtin_amdgcn_readfirstlane((int)unit)) {
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) in.uf[tb] *= in.usc[tb];
+  }
+}
 template <int HALF>
 __device__ __forceinline__ void chain_read_k(KFrags& fk, const uint8_t* ring, int lane) {
 #pragma unroll
   for (int f = 0; f < 8; ++f) fk[f] = lds_frag_h(ring + rg::KT, 8 * HALF + f, lane);
 }
 // Wait until the other chain wave has published step `target` (it always publishes before it waits
-// itself, so the wait ends; the bound only keeps a broken invariant from hanging the GPU).
+// itself, so the wait ends; the bound only keeps a broken invariant from hanging the GPU).  Program
+// order suffices after it for the same reason as in set_flag.
 __device__ __forceinline__ void wait_flag(int* flag, int target) {
   for (int i = 0; i < (1 << 18); ++i) {
-    const int v = __hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    const int v = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     if (__builtin_amdgcn_readfirstlane(v) == target) break;
   }
+  asm volatile("" ::: "memory");  // the partial-sum reads stay behind the flag read
 }
-// Publish step `value` after this wave's earlier LDS writes (release).
+// Publish step `value` after this wave's earlier LDS writes.  LDS performs a CU's operations in one
+// global order, one wave's in program order, so a reader that sees the flag and then reads the
+// partial sums sees them written: no fence (and no wait for the writes) is needed, only program
+// order, which the compiler barriers keep.
 __device__ __forceinline__ void set_flag(int* flag, int value, int lane) {
-  if (lane == 0) __hip_atomic_store(flag, value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+  asm volatile("" ::: "memory");
+  if (lane == 0) __hip_atomic_store(flag, value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 // The loader waves move a chunk's ring operands straight from L2 into LDS with global_load_lds
 // (16 bytes per lane: one wave instruction fills one 1 KiB fragment, lane l at byte 16 l), so the
@@ -1045,18 +1068,7 @@ __device__ __forceinline__ void chain_step(ScanSmem& sm, f32x4 (&S)[4], bf16x8 (
   f32x4 acc[4];
   if (HALF == 0) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      acc[0][r] = (float)in.u[0][r];
-      acc[1][r] = (float)in.u[0][4 + r];
-      acc[2][r] = (float)in.u[1][r];
-      acc[3][r] = (float)in.u[1][4 + r];
-    }
-    // the tile scales are 1 unless |U| left [2^-4, 2^14) (same value in every lane)
-    const bool unit = in.usc[0] == 1.0f && in.usc[1] == 1.0f && in.usc[2] == 1.0f && in.usc[3] == 1.0f;
-    if (!__builtin_amdgcn_readfirstlane((int)unit)) {
-#pragma unroll
-      for (int tb = 0; tb < 4; ++tb) acc[tb] *= in.usc[tb];
-    }
+    for (int tb = 0; tb < 4; ++tb) acc[tb] = in.uf[tb];
   } else {
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb) acc[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1139,6 +1151,8 @@ __device__ __forceinline__ void chain_step(ScanSmem& sm, f32x4 (&S)[4], bf16x8 (
       S[i] *= post;
     }
   }
+  // next chunk's U to fp32 while the update's MFMAs run
+  if (HALF == 0) chain_u_convert(in);
   if (sw.last) {
     const int g4 = lane >> 4;
     if (sw.fin) {
@@ -1200,6 +1214,7 @@ __device__ __forceinline__ void chain_wave(ScanSmem& sm, const float* __restrict
   KFrags fk0, fk1;  // chunks c even / odd
   if (nch > 0) {
     chain_read_w<HALF>(in, sm.ring[0], lane);
+    if (HALF == 0) chain_u_convert(in);
     chain_read_k<HALF>(fk0, sm.ring[0], lane);
   }
   auto swap_of = [&]() {
