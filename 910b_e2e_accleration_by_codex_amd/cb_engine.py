@@ -115,6 +115,8 @@ def gdn_decode_core(mixed, z, a, b, conv_state, conv_weight, A_log, dt_bias, nor
             raise TypeError(f"gdn_decode_core: {name} must be bfloat16")
     mixed, ms = _row_view(mixed)
     z, zs = _row_view(z.reshape(N, Hv * D))
+    if zs % 4 or z.data_ptr() % 8:          # the kernel reads 4 gate values per 8-byte load
+        z, zs = z.contiguous(), Hv * D
     a = a.reshape(N, Hv)
     b = b.reshape(N, Hv)
     if a.stride() != b.stride() or a.stride(-1) != 1:
@@ -126,8 +128,12 @@ def gdn_decode_core(mixed, z, a, b, conv_state, conv_weight, A_log, dt_bias, nor
     dt32 = dt_bias.to(torch.float32).contiguous()
     nw = norm_weight if norm_weight.dtype in (torch.float32, torch.bfloat16) else norm_weight.float()
     nw = nw.contiguous()
+    if nw.data_ptr() % 16:
+        nw = nw.clone()
     if out is None:
         out = torch.empty(N, Hv * D, dtype=torch.bfloat16, device=mixed.device)
+    elif not out.is_contiguous() or out.data_ptr() % 8:
+        raise ValueError("gdn_decode_core: out must be a contiguous, 8-byte aligned bf16 [N, H_v*d] tensor")
     if active is not None:
         _lib.require_cuda(active)
         if active.numel() != N:

@@ -10,8 +10,8 @@
 // 128x128 state: thread t holds columns 4*(t%32)..+3 of rows t/32 + 8*m, m < 16, as 16 float4
 // loads, so every load instruction of a wave covers two adjacent 512-byte rows (1 KiB contiguous;
 // measured faster than giving each wave whole columns).  Column sums combine the wave's two row
-// groups with one xor-shuffle and the four waves through LDS; after that each thread derives delta
-// for its own 4 columns and streams its rows straight back.
+// groups with one register swap (v_permlane32_swap) and the four waves through LDS; after that
+// each thread derives delta for its own 4 columns and streams its rows straight back.
 #include "gdn_device.h"
 #include "gdn_internal.h"
 
@@ -37,7 +37,11 @@ __device__ __forceinline__ int state_f4(int t) { return (t >> 5) * 32 + (t & 31)
 __device__ __forceinline__ void state_load(StateRegs& r, const float* S, int t) {
   const f32x4* p = reinterpret_cast<const f32x4*>(S) + state_f4(t);
 #pragma unroll
-  for (int m = 0; m < kRowsPerThread; ++m) r.s[m] = __builtin_nontemporal_load(p + m * 8 * 32);
+  for (int m = 0; m < kRowsPerThread; ++m) {
+    r.s[m] = __builtin_nontemporal_load(p + m * 8 * 32);
+    // keep the loads in row order, so column sums taken in row order wait for one row at a time
+    __builtin_amdgcn_sched_barrier(0);
+  }
 }
 
 __device__ __forceinline__ void state_zero(StateRegs& r) {
@@ -45,28 +49,32 @@ __device__ __forceinline__ void state_zero(StateRegs& r) {
   for (int m = 0; m < kRowsPerThread; ++m) r.s[m] = f32x4{0.f, 0.f, 0.f, 0.f};
 }
 
-// Column sums of S^T k and S^T q over this thread's 16 rows plus the other row group of its wave
-// (lane ^ 32); lanes 0..31 then publish the wave's partials to red[2][4][D] (k, q).
+// Column sums of S^T x over this thread's 16 rows plus the other row group of its wave
+// (lane ^ 32, a register swap); lanes 0..31 then publish the wave's partials to red[4][D].
+__device__ __forceinline__ void state_partial(const StateRegs& r, const float* xr, int t, float (*red)[kD]) {
+  f32x4 p = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int m = 0; m < kRowsPerThread; ++m) p += r.s[m] * xr[m];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) p[e] = xor32_sum(p[e]);
+  const int lane = t & 63, w = t >> 6;
+  if (lane < 32) *reinterpret_cast<f32x4*>(&red[w][4 * lane]) = p;
+}
+
+// This thread's 16 entries of a length-D vector in LDS (rows t/32 + 8m).
+__device__ __forceinline__ void row_values(const float* x, int t, float* xr) {
+#pragma unroll
+  for (int m = 0; m < kRowsPerThread; ++m) xr[m] = x[(t >> 5) + 8 * m];
+}
+
+// Both column sums (k and q) of the standalone step, published to red[2][4][D].
 __device__ __forceinline__ void state_partials(const StateRegs& r, const float* kn, const float* qs,
                                                int t, float (*red)[4][kD]) {
-  f32x4 pk = f32x4{0.f, 0.f, 0.f, 0.f}, pq = f32x4{0.f, 0.f, 0.f, 0.f};
-  const int rg = t >> 5;
-#pragma unroll
-  for (int m = 0; m < kRowsPerThread; ++m) {
-    const float kr = kn[rg + 8 * m], qr = qs[rg + 8 * m];
-    pk += r.s[m] * kr;
-    pq += r.s[m] * qr;
-  }
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    pk[e] += __shfl_xor(pk[e], 32, kWave);
-    pq[e] += __shfl_xor(pq[e], 32, kWave);
-  }
-  const int lane = t & 63, w = t >> 6;
-  if (lane < 32) {
-    *reinterpret_cast<f32x4*>(&red[0][w][4 * lane]) = pk;
-    *reinterpret_cast<f32x4*>(&red[1][w][4 * lane]) = pq;
-  }
+  float xr[kRowsPerThread];
+  row_values(kn, t, xr);
+  state_partial(r, xr, t, red[0]);
+  row_values(qs, t, xr);
+  state_partial(r, xr, t, red[1]);
 }
 
 // Sum of the four waves' partials for column c.
@@ -199,7 +207,8 @@ __device__ __forceinline__ void conv4_load(Conv4& c, const uint16_t* st, const u
   c.w = *reinterpret_cast<const uint2*>(wt);
   c.x = *xp;
 }
-__device__ __forceinline__ float conv4_finish(const Conv4& c, uint16_t* st, float bias, bool has_bias) {
+// The shifted window is returned in *nw (the caller stores it, possibly much later).
+__device__ __forceinline__ float conv4_finish(const Conv4& c, uint2* nw, float bias, bool has_bias) {
   const uint16_t win[4] = {(uint16_t)(c.s.x >> 16), (uint16_t)(c.s.y & 0xffff), (uint16_t)(c.s.y >> 16), c.x};
   const uint16_t ww[4] = {(uint16_t)(c.w.x & 0xffff), (uint16_t)(c.w.x >> 16), (uint16_t)(c.w.y & 0xffff),
                           (uint16_t)(c.w.y >> 16)};
@@ -209,7 +218,7 @@ __device__ __forceinline__ float conv4_finish(const Conv4& c, uint16_t* st, floa
   uint2 nv;
   nv.x = (uint32_t)win[0] | ((uint32_t)win[1] << 16);
   nv.y = (uint32_t)win[2] | ((uint32_t)win[3] << 16);
-  *reinterpret_cast<uint2*>(st) = nv;
+  *nw = nv;
   float o = rbf(acc);
   if (has_bias) o = rbf(o + bias);
   return rbf(silu_f(o));
@@ -233,23 +242,24 @@ __global__ __launch_bounds__(256) void conv_update_kernel(const uint16_t* __rest
 // ============================================================================================
 // Gated RMSNorm (HF Qwen3_5RMSNormGated): one wave per row, D % 64 == 0, D <= 512.
 // ============================================================================================
-template <bool kWBf16>
-__device__ __forceinline__ void gated_norm_row(const float* x, const uint16_t* gate, const void* weight,
+// x, gate and weight hold this lane's D/64 values (element j*64 + lane; x bf16-rounded), all
+// loaded beforehand so a caller can fetch them long before the row is ready.
+__device__ __forceinline__ void gated_norm_row(const float* x, const float* gate, const float* weight, bool w_bf16,
                                                uint16_t* out, int D, float eps, int lane) {
-  // x: this lane's D/64 values (bf16-rounded); element j*64 + lane.
   float ss = 0.f;
   const int nper = D / 64;
   for (int j = 0; j < nper; ++j) ss += x[j] * x[j];
   ss = wave_sum(ss);
   const float inv = rsqrt_f(ss / (float)D + eps);
   for (int j = 0; j < nper; ++j) {
-    const int c = j * 64 + lane;
     const float xn = rbf(x[j] * inv);
-    float y;
-    if (kWBf16) y = rbf(bf2f(reinterpret_cast<const uint16_t*>(weight)[c]) * xn);
-    else y = reinterpret_cast<const float*>(weight)[c] * xn;
-    out[c] = f2bf(y * silu_f(bf2f(gate[c])));
+    const float y = w_bf16 ? rbf(weight[j] * xn) : weight[j] * xn;
+    out[j * 64 + lane] = f2bf(y * silu_f(gate[j]));
   }
+}
+
+__device__ __forceinline__ float load_weight(const void* w, bool w_bf16, int c) {
+  return w_bf16 ? bf2f(reinterpret_cast<const uint16_t*>(w)[c]) : reinterpret_cast<const float*>(w)[c];
 }
 
 // D = 128 with 16-byte aligned rows: 16 lanes per row, 8 elements per lane, 16 rows per workgroup.
@@ -295,26 +305,43 @@ __global__ __launch_bounds__(256) void gated_rmsnorm_kernel(const uint16_t* __re
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
-  float xv[8];
-  for (int j = 0; j < D / 64; ++j) xv[j] = bf2f(x[row * x_stride + j * 64 + lane]);
-  gated_norm_row<kWBf16>(xv, gate + row * gate_stride, weight, out + row * D, D, eps, lane);
+  float xv[8], gv[8], wv[8];
+  for (int j = 0; j < D / 64; ++j) {
+    const int c = j * 64 + lane;
+    xv[j] = bf2f(x[row * x_stride + c]);
+    gv[j] = bf2f(gate[row * gate_stride + c]);
+    wv[j] = load_weight(weight, kWBf16, c);
+  }
+  gated_norm_row(xv, gv, wv, kWBf16, out + row * D, D, eps, lane);
 }
 
 // ============================================================================================
 // Fused decode layer core: one workgroup per (slot, key head) owning its R value heads, so every
 // conv channel it reads is also written by it alone (the in-place conv state needs no grid sync).
-// Wave roles in the prologue: wave 0 convolves + l2-normalises q, wave 1 k, waves 2..R+1 the R v
-// heads, wave R+2 computes the gating; the tiny conv loads are issued before the 64 KiB-per-head
-// state stream so the whole prologue runs while the state is in flight.
+// 256 threads stream each value head's state: load, column sums, delta, store.  Waves 0..R+1 also
+// convolve the group's q, k and R v channel blocks (conv update + SiLU, l2norm), wave R+2 computes
+// the gating, and wave 0 of each head forms the readout o = gamma S^T q + (k.q) delta with its
+// gated RMSNorm.  Their small loads (conv window / weight / input, gating inputs, the readout's
+// gate and norm weight) are issued first and kept as raw bits until the wave's 64 KiB state loads
+// are out, so the prologue runs while the state is in flight; the readout and the K = 4 conv
+// window write-back come after the state stores, so no write sits in the read phase and nothing
+// but delta sits between a wave's last state load and its first store.
+// (A separate control wave doing all of the prologue and readout was measured 18% slower: one
+// wave convolving all (R+2)*128 channels puts the prologue on the critical path.)
 // ============================================================================================
+__device__ __forceinline__ int conv_group_ch0(int g, int hk, int Hk, int R) {
+  return g == 0 ? hk * kD : (g == 1 ? (Hk + hk) * kD : (2 * Hk + hk * R + (g - 2)) * kD);
+}
+
 template <int R, bool kWBf16>
-__global__ __launch_bounds__(kHeadThreads* R) void decode_fused_kernel(
+__global__ __launch_bounds__(kHeadThreads * R) void decode_fused_kernel(
     const uint16_t* __restrict__ mixed, int64_t mixed_stride, const uint16_t* __restrict__ z,
     int64_t z_stride, const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, int64_t ab_stride,
     uint16_t* __restrict__ conv_state, const uint16_t* __restrict__ conv_w,
     const uint16_t* __restrict__ conv_b, const float* __restrict__ A_log,
     const float* __restrict__ dt_bias, const void* norm_w, float eps, float* rec_state,
     uint16_t* __restrict__ out, const uint8_t* __restrict__ active, int Hk, int K) {
+  constexpr int kGroups = R + 2;  // conv channel blocks of 128: q, k, v_0..v_{R-1}
   __shared__ float s_q[kD], s_k[kD], s_v[R][kD];
   __shared__ float s_red[R][2][4][kD];
   __shared__ float s_gamma[R], s_beta[R];
@@ -330,41 +357,74 @@ __global__ __launch_bounds__(kHeadThreads* R) void decode_fused_kernel(
   const int C = (2 * Hk + Hv) * kD;
   const int64_t sidx = ((int64_t)n * Hv + h) * kD * kD;
   const uint16_t* xr = mixed + n * mixed_stride;
-  const bool conv_wave = wv < 2 + R;
-  const int ch0 = wv == 0 ? hk * kD : (wv == 1 ? (Hk + hk) * kD : (2 * Hk + hk * R + (wv - 2)) * kD);
+  const bool k4 = K == 4;
+  const bool bias_on = conv_b != nullptr;
+  const bool conv_wave = wv < kGroups;
+  const int ch0 = conv_wave ? conv_group_ch0(wv, hk, Hk, R) : 0;
+  const bool gate_lane = wv == kGroups && lane < R;
+  const bool read_wave = wl == 0;
+  const int oc = 4 * (lane & 31);  // readout lane l owns output columns 4(l % 32)..+3 (both half-waves)
 
-  // 1. small loads first: conv window / weight / input of this wave's 128 channels, gating inputs
+  // ---- phase A: small loads (raw bits), the state stream, the prologue -----------------------
   Conv4 cv[2];
-  if (conv_wave && K == 4) {
+  uint32_t cx[2] = {0u, 0u};
+  if (conv_wave && k4) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int ch = ch0 + lane + 64 * u;
-      conv4_load(cv[u], conv_state + ((int64_t)n * C + ch) * 4, conv_w + (int64_t)ch * 4, xr + ch);
+      cv[u].s = *reinterpret_cast<const uint2*>(conv_state + ((int64_t)n * C + ch) * 4);
+      cv[u].w = *reinterpret_cast<const uint2*>(conv_w + (int64_t)ch * 4);
+      cx[u] = xr[ch];
     }
   }
-  float g_a = 0.f, g_b = 0.f, g_al = 0.f, g_dt = 0.f;
-  const bool gate_lane = wv == 2 + R && lane < R;
+  uint32_t g_a = 0u, g_b = 0u;
+  float g_al = 0.f, g_dt = 0.f;
   if (gate_lane) {
     const int hh = hk * R + lane;
-    g_b = bf2f(b[n * ab_stride + hh]);
-    g_a = bf2f(a[n * ab_stride + hh]);
+    g_b = b[n * ab_stride + hh];
+    g_a = a[n * ab_stride + hh];
     g_al = A_log[hh];
     g_dt = dt_bias[hh];
   }
-  // 2. the state stream
+  uint32_t zr[2] = {0u, 0u}, nwr[4] = {0u, 0u, 0u, 0u};
+  if (read_wave) {
+    const uint2 zz = *reinterpret_cast<const uint2*>(z + n * z_stride + (int64_t)h * kD + oc);
+    zr[0] = zz.x;
+    zr[1] = zz.y;
+    if (kWBf16) {
+      const uint2 ww = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(norm_w) + oc);
+      nwr[0] = ww.x;
+      nwr[1] = ww.y;
+    } else {
+      const uint4 ww = *reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(norm_w) + oc);
+      nwr[0] = ww.x; nwr[1] = ww.y; nwr[2] = ww.z; nwr[3] = ww.w;
+    }
+  }
   StateRegs S;
   state_load(S, rec_state + sidx, tl);
+  // nothing derived from the small loads may be computed before this point
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    pin(cv[u].s.x); pin(cv[u].s.y); pin(cv[u].w.x); pin(cv[u].w.y); pin(cx[u]);
+    pin(zr[u]);
+  }
+  pin(g_a); pin(g_b); pin(g_al); pin(g_dt);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) pin(nwr[e]);
 
-  // 3. prologue math while the state is in flight
+  uint2 cnew[2];
   if (conv_wave) {
     float x[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int ch = ch0 + lane + 64 * u;
-      const float bb = conv_b ? bf2f(conv_b[ch]) : 0.f;
-      uint16_t* st = conv_state + ((int64_t)n * C + ch) * K;
-      x[u] = K == 4 ? conv4_finish(cv[u], st, bb, conv_b != nullptr)
-                    : conv_channel(st, conv_w + (int64_t)ch * K, bb, conv_b != nullptr, xr[ch], K);
+      const float bb = bias_on ? bf2f(conv_b[ch]) : 0.f;
+      if (k4) {
+        cv[u].x = (uint16_t)cx[u];
+        x[u] = conv4_finish(cv[u], &cnew[u], bb, bias_on);
+      } else {  // general K: window updated in place here
+        x[u] = conv_channel(conv_state + ((int64_t)n * C + ch) * K, conv_w + (int64_t)ch * K, bb, bias_on, xr[ch], K);
+      }
     }
     if (wv < 2) {
       l2norm_pair<true>(x[0], x[1]);
@@ -378,31 +438,65 @@ __global__ __launch_bounds__(kHeadThreads* R) void decode_fused_kernel(
     }
   }
   if (gate_lane) {
-    s_beta[lane] = rbf(sigmoid_f(g_b));
-    s_gamma[lane] = expf(-expf(g_al) * softplus_f(g_a + g_dt));
+    s_beta[lane] = rbf(sigmoid_f(bf2f((uint16_t)g_b)));
+    s_gamma[lane] = expf(-expf(g_al) * softplus_f(bf2f((uint16_t)g_a) + g_dt));
   }
   __syncthreads();
 
-  // 4. column sums (two row groups per wave by shuffle, four waves through LDS)
-  state_partials(S, s_k, s_q, tl, s_red[j]);
+  // ---- phase B: column sums S^T k and S^T q (two row groups per wave by register swap, four
+  //      waves through LDS); k.q on the readout waves ----------------------------------------------
+  float kq = 0.f;
+  if (read_wave) kq = wave_sum_fast(s_k[lane] * s_q[lane] + s_k[lane + 64] * s_q[lane + 64]);
+  float kr[kRowsPerThread], qr[kRowsPerThread];
+  row_values(s_k, tl, kr);
+  row_values(s_q, tl, qr);
+  state_partial(S, kr, tl, s_red[j][0]);
+  state_partial(S, qr, tl, s_red[j][1]);
   __syncthreads();
 
-  // 5. every thread derives delta for its own 4 columns and streams its rows back at once; wave 0
-  //    of each head also forms the readout o = gamma S^T q + (k.q) delta (bf16, as the reference's
-  //    recurrent output) and the gated RMSNorm of the head's 128 outputs.
+  // ---- phase C: every thread derives delta for its own 4 columns and streams its rows back; then
+  //      the conv windows go back and the readout waves form o (bf16, as the reference's recurrent
+  //      output) and the gated RMSNorm of the head's 128 outputs --------------------------------
   const float gamma = s_gamma[j], bt = s_beta[j];
-  state_update_store(S, rec_state + sidx, s_k, s_v[j], s_red[j], gamma, bt, tl);
-  if (wl == 0) {
-    const float kq = wave_sum(s_k[lane] * s_q[lane] + s_k[lane + 64] * s_q[lane + 64]);
-    float o[2];
+  // (measured: 16-byte reads of the partials and k kept in registers for the stores are both slower)
+  f32x4 d;
+  const int cg = tl & 31;
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int c = lane + 64 * u;
-      const float delta = (s_v[j][c] - gamma * red_sum(s_red[j], 0, c)) * bt;
-      o[u] = rbf(gamma * red_sum(s_red[j], 1, c) + kq * delta);
+  for (int e = 0; e < 4; ++e) d[e] = (s_v[j][4 * cg + e] - gamma * red_sum(s_red[j], 0, 4 * cg + e)) * bt;
+  {
+    f32x4* p = reinterpret_cast<f32x4*>(rec_state + sidx) + state_f4(tl);
+#pragma unroll
+    for (int m = 0; m < kRowsPerThread; ++m)
+      __builtin_nontemporal_store(S.s[m] * gamma + d * s_k[(tl >> 5) + 8 * m], p + m * 8 * 32);
+  }
+  if (conv_wave && k4) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      *reinterpret_cast<uint2*>(conv_state + ((int64_t)n * C + ch0 + lane + 64 * u) * 4) = cnew[u];
+  }
+  if (read_wave) {  // lanes l and l + 32 hold the same columns (tl & 31 == l & 31)
+    float o[4], ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      o[e] = rbf(gamma * red_sum(s_red[j], 1, oc + e) + kq * d[e]);
+      ss += o[e] * o[e];
     }
-    gated_norm_row<kWBf16>(o, z + n * z_stride + (int64_t)h * kD, norm_w,
-                           out + ((int64_t)n * Hv + h) * kD, kD, eps, lane);
+    ss = half_sum(ss);
+    const float inv = rsqrt_f(ss / (float)kD + eps);
+    uint16_t ov[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float xn = rbf(o[e] * inv);
+      const float wt = kWBf16 ? bf2f((uint16_t)(nwr[e >> 1] >> (16 * (e & 1)))) : __uint_as_float(nwr[e]);
+      const float y = kWBf16 ? rbf(wt * xn) : wt * xn;
+      ov[e] = f2bf(y * silu_f(bf2f((uint16_t)(zr[e >> 1] >> (16 * (e & 1))))));
+    }
+    if (lane < 32) {
+      uint2 pk;
+      pk.x = (uint32_t)ov[0] | ((uint32_t)ov[1] << 16);
+      pk.y = (uint32_t)ov[2] | ((uint32_t)ov[3] << 16);
+      *reinterpret_cast<uint2*>(out + ((int64_t)n * Hv + h) * kD + oc) = pk;
+    }
   }
 }
 
@@ -505,6 +599,9 @@ extern "C" int gdn_decode_fused_masked(const void* mixed, int64_t mixed_stride, 
   GDN_SUPPORT(K >= 1 && K <= 8, "gdn_decode_fused: conv kernel %d unsupported", K);
   GDN_REQUIRE(norm_w_dtype == GDN_F32 || norm_w_dtype == GDN_BF16, "gdn_decode_fused: bad norm_w_dtype");
   GDN_REQUIRE(aligned(rec_state, 16), "gdn_decode_fused: rec_state must be 16-byte aligned");
+  GDN_REQUIRE(aligned(z, 8) && z_stride % 4 == 0 && aligned(out, 8),
+              "gdn_decode_fused: z (and its row stride) and out must be 8-byte aligned");
+  GDN_REQUIRE(aligned(norm_w, norm_w_dtype == GDN_BF16 ? 8 : 16), "gdn_decode_fused: norm_w misaligned");
   GDN_REQUIRE(K != 4 || (aligned(conv_state, 8) && aligned(conv_w, 8)),
               "gdn_decode_fused: conv state/weight must be 8-byte aligned");
   const int R = Hv / Hk;

@@ -52,4 +52,40 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Register-only reductions with DPP row permutes and gfx950's permlane swaps (no LDS round trip
+// per step).  Every step adds a lane's value to its partner's, so all lanes of a group end with
+// the bit-identical sum.  The whole wave must be active.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), kCtrl, 0xf, 0xf, true));
+}
+// Sum over each aligned group of 16 lanes.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]: lane ^ 1
+  v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]: lane ^ 2
+  v += dpp_mov<0x141>(v);  // row_half_mirror: the other quad of each 8
+  v += dpp_mov<0x140>(v);  // row_mirror: the other 8 of each 16
+  return v;
+}
+// Sum over lanes 0..31 and, separately, over lanes 32..63.
+__device__ __forceinline__ float half_sum(float v) {
+  v = row16_sum(v);
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);  // rows (0,1), (2,3) exchanged
+  return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
+}
+// v plus the value of lane ^ 32, in every lane.
+__device__ __forceinline__ float xor32_sum(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);  // halves exchanged
+  return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
+}
+// Sum over the whole wave.
+__device__ __forceinline__ float wave_sum_fast(float v) { return xor32_sum(half_sum(v)); }
+
+// Treat v as produced at this point: no use of a loaded value can be hoisted above it, so a load
+// issued earlier is not waited for before the loads issued between the two.
+__device__ __forceinline__ void pin(uint32_t& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void pin(float& v) { asm volatile("" : "+v"(v)); }
+
 }  // namespace gdn

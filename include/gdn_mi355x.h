@@ -88,10 +88,12 @@ int gdn_gated_rmsnorm(const void* x, int64_t x_stride, const void* gate, int64_t
  *   head h reading key head h / (Hv/Hk) -> rec_state updated in place -> gated RMSNorm with z.
  *   mixed   [N, C] bf16 (pre-conv in_proj_qkv output, channels q(Hk*D) | k(Hk*D) | v(Hv*D)),
  *           row stride mixed_stride;  C = (2*Hk + Hv) * D
- *   z       [N, Hv*D] bf16 row stride z_stride;  a, b [N, Hv] bf16 row strides ab_stride
+ *   z       [N, Hv*D] bf16 row stride z_stride (8-byte aligned, z_stride % 4 == 0);
+ *           a, b [N, Hv] bf16 row strides ab_stride
  *   conv_state [N, C, K] bf16 (in place);  conv_w [C, K] bf16;  conv_b [C] bf16 or NULL
- *   A_log, dt_bias [Hv] fp32;  norm_w [D] (norm_w_dtype)
- *   rec_state [N, Hv, D, D] fp32 (in place);  out [N, Hv*D] bf16 (the normed core)
+ *   A_log, dt_bias [Hv] fp32;  norm_w [D] (norm_w_dtype; 8-byte aligned bf16 / 16-byte fp32)
+ *   rec_state [N, Hv, D, D] fp32 (in place, 16-byte aligned);  out [N, Hv*D] bf16 (the normed
+ *           core, 8-byte aligned)
  */
 int gdn_decode_fused(const void* mixed, int64_t mixed_stride, const void* z, int64_t z_stride,
                      const void* a, const void* b, int64_t ab_stride, void* conv_state,

@@ -147,10 +147,29 @@ def _layer_inputs(N, Hk, Hv, D, K, seed):
     return p
 
 
-@pytest.mark.parametrize("Hk,Hv", [(16, 32), (16, 48), (8, 8)])
+@pytest.mark.parametrize("Hk,Hv", [(16, 32), (16, 48), (8, 8), (4, 16)])
 def test_decode_fused_layer(gdn, oracle, dev, Hk, Hv):
     N, D, K = 16, 128, 4
     p = _layer_inputs(N, Hk, Hv, D, K, seed=6)
+    ref_conv, ref_rec = p["conv_state"].clone(), p["rec_state"].clone()
+    ref = oracle.gdn_decode_core(p["mixed"], p["z"], p["a"], p["b"], ref_conv, p["conv_weight"],
+                                 p["A_log"], p["dt_bias"], p["norm_weight"], ref_rec, Hk, Hv, D)
+    d = {k: v.to(dev) for k, v in p.items()}
+    out = gdn.gdn_decode_core(d["mixed"], d["z"], d["a"], d["b"], d["conv_state"], d["conv_weight"],
+                              d["A_log"], d["dt_bias"], d["norm_weight"], d["rec_state"], Hk, Hv, D)
+    torch.cuda.synchronize()
+    assert torch.equal(d["conv_state"].cpu(), ref_conv), "conv state must be bit-exact"
+    assert rel_l2(out, ref) <= OUT_TOL
+    assert rel_l2(d["rec_state"], ref_rec) <= STATE_TOL
+
+
+@pytest.mark.parametrize("Hk,Hv,K,wdtype", [(16, 48, 3, torch.float32), (4, 16, 2, torch.float32),
+                                             (8, 8, 4, torch.float32)])
+def test_decode_fused_layer_conv_k_and_fp32_norm(gdn, oracle, dev, Hk, Hv, K, wdtype):
+    """Conv kernel sizes other than 4 (window updated in place in the prologue) and an fp32 norm weight."""
+    N, D = 16, 128
+    p = _layer_inputs(N, Hk, Hv, D, K, seed=8)
+    p["norm_weight"] = p["norm_weight"].to(wdtype)
     ref_conv, ref_rec = p["conv_state"].clone(), p["rec_state"].clone()
     ref = oracle.gdn_decode_core(p["mixed"], p["z"], p["a"], p["b"], ref_conv, p["conv_weight"],
                                  p["A_log"], p["dt_bias"], p["norm_weight"], ref_rec, Hk, Hv, D)
