@@ -280,6 +280,69 @@ extern "C" int gdn_decode_linear_packed(const void* x, int64_t x_stride, const v
 // null: h_out = h), x_out = norm(h_out).  One workgroup per row; h_out may alias h.
 // ============================================================================================
 namespace gdn {
+typedef uint16_t u16x8v __attribute__((ext_vector_type(8)));
+
+// Sum of v over the workgroup's 4 waves (every thread gets it).
+__device__ __forceinline__ float block_sum4(float v, float* red) {
+  v = wave_sum_fast(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return red[0] + red[1] + red[2] + red[3];
+}
+
+// H % 8 == 0 with 16-byte aligned rows and H <= 256 * 8 * kMaxV: each thread issues all of its
+// 16-byte row pieces at once (a row is one memory round trip, not one per element) and keeps them
+// in registers for the output pass.
+template <int kMaxV>
+__global__ __launch_bounds__(256) void add_rmsnorm_vec_kernel(const uint16_t* h, const uint16_t* __restrict__ delta,
+                                                              const uint16_t* __restrict__ w, uint16_t* h_out,
+                                                              uint16_t* __restrict__ x_out, int H, float eps) {
+  __shared__ float red[4];
+  const int64_t base = (int64_t)blockIdx.x * H;
+  const int nv = H / 8;
+  u16x8v hv[kMaxV], dv[kMaxV];
+#pragma unroll
+  for (int j = 0; j < kMaxV; ++j) {
+    const int v = threadIdx.x + 256 * j;
+    if (v < nv) {
+      hv[j] = *reinterpret_cast<const u16x8v*>(h + base + 8 * v);
+      if (delta) dv[j] = *reinterpret_cast<const u16x8v*>(delta + base + 8 * v);
+    }
+  }
+  float x[kMaxV][8], ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < kMaxV; ++j) {
+    const int v = threadIdx.x + 256 * j;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float val = 0.f;
+      if (v < nv) {
+        val = bf2f(hv[j][e]);
+        if (delta) val = rbf(val + bf2f(dv[j][e]));
+      }
+      x[j][e] = val;
+      ss += val * val;
+    }
+  }
+  const float inv = rsqrtf(block_sum4(ss, red) / (float)H + eps);
+#pragma unroll
+  for (int j = 0; j < kMaxV; ++j) {
+    const int v = threadIdx.x + 256 * j;
+    if (v < nv) {
+      const u16x8v wv = *reinterpret_cast<const u16x8v*>(w + 8 * v);
+      u16x8v o, hn;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        o[e] = f2bf(x[j][e] * inv * (1.0f + bf2f(wv[e])));
+        hn[e] = f2bf(x[j][e]);
+      }
+      *reinterpret_cast<u16x8v*>(x_out + base + 8 * v) = o;
+      if (delta) *reinterpret_cast<u16x8v*>(h_out + base + 8 * v) = hn;
+    }
+  }
+}
+
+// Any H (rows of other widths or alignments): element loop.
 __global__ __launch_bounds__(256) void add_rmsnorm_kernel(const uint16_t* h, const uint16_t* __restrict__ delta,
                                                           const uint16_t* __restrict__ w, uint16_t* h_out,
                                                           uint16_t* __restrict__ x_out, int H, float eps) {
@@ -294,10 +357,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(const uint16_t* h, con
     if (dr) v = rbf(v + bf2f(dr[i]));
     ss += v * v;
   }
-  ss = wave_sum(ss);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
-  __syncthreads();
-  const float inv = rsqrtf((red[0] + red[1] + red[2] + red[3]) / (float)H + eps);
+  const float inv = rsqrtf(block_sum4(ss, red) / (float)H + eps);
   for (int i = threadIdx.x; i < H; i += 256) {
     float v = bf2f(hr[i]);
     if (dr) v = rbf(v + bf2f(dr[i]));
@@ -313,8 +373,17 @@ extern "C" int gdn_add_rmsnorm(const void* h, const void* delta, const void* w, 
   GDN_REQUIRE(h && w && x_out && (!delta || h_out), "gdn_add_rmsnorm: null pointer");
   GDN_REQUIRE(M >= 0 && H > 0, "gdn_add_rmsnorm: bad sizes");
   if (M == 0) return GDN_OK;
-  add_rmsnorm_kernel<<<M, 256, 0, (hipStream_t)stream>>>((const uint16_t*)h, (const uint16_t*)delta,
-                                                         (const uint16_t*)w, (uint16_t*)h_out, (uint16_t*)x_out, H,
-                                                         eps);
+  hipStream_t s = (hipStream_t)stream;
+  const bool vec = H % 8 == 0 && aligned(h, 16) && aligned(w, 16) && aligned(x_out, 16) &&
+                   (!delta || (aligned(delta, 16) && aligned(h_out, 16)));
+  if (vec && H <= 256 * 8 * 2)
+    add_rmsnorm_vec_kernel<2><<<M, 256, 0, s>>>((const uint16_t*)h, (const uint16_t*)delta, (const uint16_t*)w,
+                                                (uint16_t*)h_out, (uint16_t*)x_out, H, eps);
+  else if (vec && H <= 256 * 8 * 4)
+    add_rmsnorm_vec_kernel<4><<<M, 256, 0, s>>>((const uint16_t*)h, (const uint16_t*)delta, (const uint16_t*)w,
+                                                (uint16_t*)h_out, (uint16_t*)x_out, H, eps);
+  else
+    add_rmsnorm_kernel<<<M, 256, 0, s>>>((const uint16_t*)h, (const uint16_t*)delta, (const uint16_t*)w,
+                                         (uint16_t*)h_out, (uint16_t*)x_out, H, eps);
   return check_launch("gdn_add_rmsnorm");
 }

@@ -130,15 +130,17 @@ def test_decode_linear_vs_fp32(gdn, dev, M, N, K, packed):
 
 
 @pytest.mark.gpu
-def test_add_rms_norm_vs_torch(gdn, dev):
-    """Fused residual add + Qwen3_5RMSNorm against the torch formula (residual rounded to bf16 first)."""
+@pytest.mark.parametrize("H", [5120, 4096, 5121, 12288])
+def test_add_rms_norm_vs_torch(gdn, dev, H):
+    """Fused residual add + Qwen3_5RMSNorm against the torch formula (residual rounded to bf16 first);
+    H = 4096 / 5120: the vector kernel (2 / 4 pieces per thread), 5121 and 12288: the element loop."""
     from importlib import import_module
     cb = import_module(PKG_NAME + ".cb_engine")
     hd = _hybrid(gdn)
     g_ = torch.Generator().manual_seed(46)
-    h = torch.randn(5, 5120, generator=g_).to(torch.bfloat16)
-    d = torch.randn(5, 5120, generator=g_).to(torch.bfloat16)
-    w = (0.02 * torch.randn(5120, generator=g_)).to(torch.bfloat16)
+    h = torch.randn(5, H, generator=g_).to(torch.bfloat16)
+    d = torch.randn(5, H, generator=g_).to(torch.bfloat16)
+    w = (0.02 * torch.randn(H, generator=g_)).to(torch.bfloat16)
     h2, x = cb.add_rms_norm(h.to(dev), d.to(dev), w.to(dev))
     assert torch.equal(h2.cpu(), h + d)
     x_ref = hd.rms_norm(h + d, w, 1e-6)
