@@ -223,12 +223,67 @@ def decode_linear(x, weight):
     return out
 
 
+class Partials:
+    """The fp32 split-K partial sums [splits, M, N] of a decode projection (decode_linear_partial):
+    the projection's bf16 output is bf16(data.sum(0)) summed in split order, which the consumer
+    (add_rms_norm, swiglu) forms itself."""
+
+    def __init__(self, data, splits, M, N):
+        self.data, self.splits, self.M, self.N = data, splits, M, N
+
+    def to_bf16(self):
+        out = self.data[0].clone()
+        for s in range(1, self.splits):
+            out += self.data[s]
+        return out.to(torch.bfloat16)
+
+
+def decode_linear_partial(x, weight):
+    """decode_linear on a PackedWeight, returning its split-K partial sums (Partials) instead of the
+    reduced bf16 output: for a consumer that reduces them itself."""
+    _lib.require_cuda(x)
+    M, K = x.shape
+    if not isinstance(weight, PackedWeight) or K != weight.K or M > 16 or x.dtype != torch.bfloat16:
+        raise ValueError("decode_linear_partial: bf16 x [M <= 16, K] and a PackedWeight [N, K]")
+    if x.stride(1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
+        x = x.contiguous()
+    splits = int(_lib.lib().gdn_decode_linear_splits(M, weight.N, K))
+    part = torch.empty(splits, M, weight.N, dtype=torch.float32, device=x.device)
+    _lib.call("gdn_decode_linear_packed_partial", _lib.ptr(x), x.stride(0), _lib.ptr(weight.data), _lib.ptr(part),
+              M, weight.N, K, part.numel() * 4, _lib.stream_of(x))
+    return Partials(part, splits, M, weight.N)
+
+
+def swiglu(gate_up):
+    """HF Qwen3_5MLP's act_fn(gate) * up with gate | up as one projection [M, 2m]: a bf16 tensor, or the
+    Partials of the gate_up projection (reduced here, no separate reduction)."""
+    if isinstance(gate_up, Partials):
+        M, m = gate_up.M, gate_up.N // 2
+        out = torch.empty(M, m, dtype=torch.bfloat16, device=gate_up.data.device)
+        _lib.call("gdn_swiglu_partial", _lib.ptr(gate_up.data), gate_up.splits, _lib.ptr(out), M, m,
+                  _lib.stream_of(out))
+        return out
+    m = gate_up.shape[-1] // 2
+    return torch.nn.functional.silu(gate_up[:, :m]) * gate_up[:, m:]
+
+
 def add_rms_norm(h, delta, weight, eps=1e-6):
     """Residual add + Qwen3_5RMSNorm between decode-step layers (HF modeling_qwen3_5.py):
-    h, delta [M, H] bf16 (delta None: norm only), weight [H] bf16.  Returns (h + delta, norm of it);
-    one kernel instead of the add and the norm's chain of elementwise ops."""
-    _lib.require_cuda(h, delta, weight)
+    h, delta [M, H] bf16 (delta None: norm only; or the Partials of the projection that produced it),
+    weight [H] bf16.  Returns (h + delta, norm of it); one kernel instead of the add and the norm's
+    chain of elementwise ops."""
+    _lib.require_cuda(h, weight)
     M, H = h.shape
+    if isinstance(delta, Partials):
+        if (delta.M, delta.N) != (M, H) or h.dtype != torch.bfloat16 or not h.is_contiguous():
+            raise ValueError(f"add_rms_norm: h must be a contiguous bf16 [{M}, {H}] tensor matching the partials")
+        w = weight.to(torch.bfloat16).contiguous()
+        x = torch.empty_like(h)
+        h_out = torch.empty_like(h)
+        _lib.call("gdn_add_rmsnorm_partial", _lib.ptr(h), _lib.ptr(delta.data), delta.splits, _lib.ptr(w),
+                  _lib.ptr(h_out), _lib.ptr(x), M, H, float(eps), _lib.stream_of(h))
+        return h_out, x
+    _lib.require_cuda(delta)
     for name, t in (("h", h), ("delta", delta)):
         if t is not None and (t.dtype != torch.bfloat16 or t.shape != (M, H) or not t.is_contiguous()):
             raise ValueError(f"add_rms_norm: {name} must be a contiguous bf16 [{M}, {H}] tensor")

@@ -197,10 +197,12 @@ int64_t workspace_bytes(int M, int64_t N, int64_t K) {
   return splits > 1 ? (int64_t)splits * M * N * (int64_t)sizeof(float) : 0;
 }
 
+// partial_only: write the fp32 split-K partial sums [splits][M][N] into workspace (even with one
+// split) and skip the reduction; out is unused.
 int decode_linear_launch(bool packed, const void* x, int64_t x_stride, const void* W, int64_t w_stride, void* out,
                          int64_t out_stride, int M, int64_t N, int64_t K, float* workspace, int64_t ws_bytes,
-                         void* stream) {
-  GDN_REQUIRE(x && W && out, "gdn_decode_linear: null pointer");
+                         void* stream, bool partial_only = false) {
+  GDN_REQUIRE(x && W && (out || partial_only), "gdn_decode_linear: null pointer");
   GDN_SUPPORT(M >= 1 && M <= 16, "gdn_decode_linear: %d rows (1..16 supported)", M);
   GDN_REQUIRE(N > 0 && N < (1ll << 31) && K > 0, "gdn_decode_linear: bad sizes N=%lld K=%lld", (long long)N,
               (long long)K);
@@ -208,15 +210,15 @@ int decode_linear_launch(bool packed, const void* x, int64_t x_stride, const voi
   GDN_REQUIRE(aligned(x, 16) && aligned(W, 16) && x_stride % 8 == 0 && x_stride >= K &&
                   (packed || (w_stride % 8 == 0 && w_stride >= K)),
               "gdn_decode_linear: x and W rows must be 16-byte aligned and hold K values");
-  GDN_REQUIRE(aligned(out, 2) && out_stride >= N, "gdn_decode_linear: out rows must hold N values");
+  GDN_REQUIRE(partial_only || (aligned(out, 2) && out_stride >= N), "gdn_decode_linear: out rows must hold N values");
   int64_t nb;
   int splits, per;
   gv::plan(N, K, &nb, &splits, &per);
-  const int64_t need = workspace_bytes(M, N, K);
+  const int64_t need = partial_only ? (int64_t)splits * M * N * (int64_t)sizeof(float) : workspace_bytes(M, N, K);
   GDN_REQUIRE(need == 0 || (workspace && aligned(workspace, 16) && ws_bytes >= need),
               "gdn_decode_linear: needs a 16-byte aligned fp32 workspace of %lld bytes", (long long)need);
   hipStream_t s = (hipStream_t)stream;
-  float* part = splits > 1 ? workspace : nullptr;
+  float* part = (splits > 1 || partial_only) ? workspace : nullptr;
   if (packed)
     decode_linear_kernel<true><<<dim3((unsigned)nb, (unsigned)splits), 64 * gv::WAVES, 0, s>>>(
         (const uint16_t*)x, x_stride, (const uint16_t*)W, w_stride, (uint16_t*)out, out_stride, part, M, N, K, per);
@@ -224,7 +226,7 @@ int decode_linear_launch(bool packed, const void* x, int64_t x_stride, const voi
     decode_linear_kernel<false><<<dim3((unsigned)nb, (unsigned)splits), 64 * gv::WAVES, 0, s>>>(
         (const uint16_t*)x, x_stride, (const uint16_t*)W, w_stride, (uint16_t*)out, out_stride, part, M, N, K, per);
   int rc = check_launch("gdn_decode_linear");
-  if (rc || !part) return rc;
+  if (rc || !part || partial_only) return rc;
   const int64_t quads = (int64_t)M * ((N + 3) / 4);
   decode_linear_reduce_kernel<<<(unsigned)((quads + 255) / 256), 256, 0, s>>>(part, splits, (uint16_t*)out,
                                                                                out_stride, M, N);
@@ -342,6 +344,88 @@ __global__ __launch_bounds__(256) void add_rmsnorm_vec_kernel(const uint16_t* h,
   }
 }
 
+// The same with delta given as the fp32 split-K partial sums of the projection that produced it
+// (part [splits][M][H], gdn_decode_linear_packed_partial): delta = bf16(sum over splits, in split
+// order) -- exactly what decode_linear_reduce_kernel would have stored -- so the reduction costs no
+// launch and no bf16 round trip.  The split loads of one row piece are issued together.
+template <int kMaxV>
+__global__ __launch_bounds__(256) void add_rmsnorm_part_kernel(const uint16_t* h, const float* __restrict__ part,
+                                                               int splits, int M, const uint16_t* __restrict__ w,
+                                                               uint16_t* h_out, uint16_t* __restrict__ x_out, int H,
+                                                               float eps) {
+  typedef float f32x4v __attribute__((ext_vector_type(4)));
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x, base = row * H;
+  const int nv = H / 8;
+  float x[kMaxV][8], ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < kMaxV; ++j) {
+    const int v = threadIdx.x + 256 * j;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[j][e] = 0.f;
+    if (v < nv) {
+      const u16x8v hv = *reinterpret_cast<const u16x8v*>(h + base + 8 * v);
+      f32x4v d0 = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+      for (int sp = 0; sp < splits; ++sp) {
+        const float* pp = part + ((int64_t)sp * M + row) * H + 8 * v;
+        d0 += *reinterpret_cast<const f32x4v*>(pp);
+        d1 += *reinterpret_cast<const f32x4v*>(pp + 4);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float d = rbf(e < 4 ? d0[e] : d1[e - 4]);
+        x[j][e] = rbf(bf2f(hv[e]) + d);
+        ss += x[j][e] * x[j][e];
+      }
+    }
+  }
+  const float inv = rsqrtf(block_sum4(ss, red) / (float)H + eps);
+#pragma unroll
+  for (int j = 0; j < kMaxV; ++j) {
+    const int v = threadIdx.x + 256 * j;
+    if (v < nv) {
+      const u16x8v wv = *reinterpret_cast<const u16x8v*>(w + 8 * v);
+      u16x8v o, hn;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        o[e] = f2bf(x[j][e] * inv * (1.0f + bf2f(wv[e])));
+        hn[e] = f2bf(x[j][e]);
+      }
+      *reinterpret_cast<u16x8v*>(x_out + base + 8 * v) = o;
+      *reinterpret_cast<u16x8v*>(h_out + base + 8 * v) = hn;
+    }
+  }
+}
+
+// SwiGLU of a decode step's MLP from the fp32 split-K partials of its gate_up projection
+// (part [splits][M][2m], gate columns first): g, u = bf16(sum over splits), then torch's
+// bf16(bf16(silu(g)) * u) (F.silu(gu[:, :m]) * gu[:, m:]).  8 outputs per thread.
+__global__ __launch_bounds__(256) void swiglu_part_kernel(const float* __restrict__ part, int splits, int M,
+                                                          int64_t m, uint16_t* __restrict__ out) {
+  typedef float f32x4v __attribute__((ext_vector_type(4)));
+  const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // 8-column piece over M x m / 8
+  const int64_t per_row = m / 8;
+  if (q >= (int64_t)M * per_row) return;
+  const int64_t row = q / per_row, col = (q % per_row) * 8;
+  f32x4v g0 = {0.f, 0.f, 0.f, 0.f}, g1 = g0, u0 = g0, u1 = g0;
+#pragma unroll 4
+  for (int sp = 0; sp < splits; ++sp) {
+    const float* pp = part + ((int64_t)sp * M + row) * (2 * m) + col;
+    g0 += *reinterpret_cast<const f32x4v*>(pp);
+    g1 += *reinterpret_cast<const f32x4v*>(pp + 4);
+    u0 += *reinterpret_cast<const f32x4v*>(pp + m);
+    u1 += *reinterpret_cast<const f32x4v*>(pp + m + 4);
+  }
+  u16x8v o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float g = rbf(e < 4 ? g0[e] : g1[e - 4]), u = rbf(e < 4 ? u0[e] : u1[e - 4]);
+    o[e] = f2bf(rbf(silu_f(g)) * u);
+  }
+  *reinterpret_cast<u16x8v*>(out + row * m + col) = o;
+}
+
 // Any H (rows of other widths or alignments): element loop.
 __global__ __launch_bounds__(256) void add_rmsnorm_kernel(const uint16_t* h, const uint16_t* __restrict__ delta,
                                                           const uint16_t* __restrict__ w, uint16_t* h_out,
@@ -386,4 +470,50 @@ extern "C" int gdn_add_rmsnorm(const void* h, const void* delta, const void* w, 
     add_rmsnorm_kernel<<<M, 256, 0, s>>>((const uint16_t*)h, (const uint16_t*)delta, (const uint16_t*)w,
                                          (uint16_t*)h_out, (uint16_t*)x_out, H, eps);
   return check_launch("gdn_add_rmsnorm");
+}
+
+extern "C" int gdn_decode_linear_splits(int M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K < gv::KSTEP || K % gv::KSTEP) return 0;
+  int64_t nb;
+  int splits, per;
+  gv::plan(N, K, &nb, &splits, &per);
+  return splits;
+}
+
+extern "C" int gdn_decode_linear_packed_partial(const void* x, int64_t x_stride, const void* packed, float* part,
+                                                int M, int64_t N, int64_t K, int64_t part_bytes, void* stream) {
+  clear_error();
+  return decode_linear_launch(true, x, x_stride, packed, 0, nullptr, 0, M, N, K, part, part_bytes, stream, true);
+}
+
+extern "C" int gdn_add_rmsnorm_partial(const void* h, const float* part, int splits, const void* w, void* h_out,
+                                       void* x_out, int M, int H, float eps, void* stream) {
+  clear_error();
+  GDN_REQUIRE(h && part && w && h_out && x_out, "gdn_add_rmsnorm_partial: null pointer");
+  GDN_REQUIRE(M >= 0 && splits >= 1, "gdn_add_rmsnorm_partial: bad sizes");
+  GDN_SUPPORT(H > 0 && H % 8 == 0 && H <= 256 * 8 * 4, "gdn_add_rmsnorm_partial: H=%d must be a multiple of 8 <= 8192",
+              H);
+  GDN_REQUIRE(aligned(h, 16) && aligned(part, 16) && aligned(w, 16) && aligned(h_out, 16) && aligned(x_out, 16),
+              "gdn_add_rmsnorm_partial: rows must be 16-byte aligned");
+  if (M == 0) return GDN_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (H <= 256 * 8 * 2)
+    add_rmsnorm_part_kernel<2><<<M, 256, 0, s>>>((const uint16_t*)h, part, splits, M, (const uint16_t*)w,
+                                                 (uint16_t*)h_out, (uint16_t*)x_out, H, eps);
+  else
+    add_rmsnorm_part_kernel<4><<<M, 256, 0, s>>>((const uint16_t*)h, part, splits, M, (const uint16_t*)w,
+                                                 (uint16_t*)h_out, (uint16_t*)x_out, H, eps);
+  return check_launch("gdn_add_rmsnorm_partial");
+}
+
+extern "C" int gdn_swiglu_partial(const float* part, int splits, void* out, int M, int64_t m, void* stream) {
+  clear_error();
+  GDN_REQUIRE(part && out, "gdn_swiglu_partial: null pointer");
+  GDN_REQUIRE(M >= 0 && splits >= 1 && m > 0 && m % 8 == 0, "gdn_swiglu_partial: bad sizes (m a multiple of 8)");
+  GDN_REQUIRE(aligned(part, 16) && aligned(out, 16), "gdn_swiglu_partial: part and out must be 16-byte aligned");
+  if (M == 0) return GDN_OK;
+  const int64_t pieces = (int64_t)M * (m / 8);
+  swiglu_part_kernel<<<(unsigned)((pieces + 255) / 256), 256, 0, (hipStream_t)stream>>>(part, splits, M, m,
+                                                                                        (uint16_t*)out);
+  return check_launch("gdn_swiglu_partial");
 }

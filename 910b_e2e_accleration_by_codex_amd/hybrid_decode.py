@@ -8,9 +8,11 @@ step + gated RMSNorm, one kernel) and out_proj; every fourth layer is GQA full a
 per-slot KV cache; each layer ends with the SwiGLU MLP.  Weights are random (no checkpoints), the
 slots' GDN states and KV caches are pre-filled with random values at per-slot context lengths.
 
-The GDN layer core and every linear of the step (the weight-streaming decode projection kernel,
-gdn_decode_linear) are this library's kernels; attention scores, softmax, norms and activations are
-torch ops.  The KV cache keeps K transposed ([slot, kv head, head_dim, position]) so both batched
+The GDN layer core, every linear of the step (the weight-streaming decode projection kernel,
+gdn_decode_linear), the residual adds with their RMSNorms and the SwiGLU products are this library's
+kernels; the output projections hand their split-K partial sums straight to the residual add + norm,
+and gate_up its partials to SwiGLU.  Attention scores, softmax and the q/k norms and rotary are torch
+ops.  The KV cache keeps K transposed ([slot, kv head, head_dim, position]) so both batched
 attention products take a contiguous right operand.
 """
 from dataclasses import dataclass
@@ -18,7 +20,8 @@ from types import SimpleNamespace
 
 import torch
 
-from .cb_engine import GDNSlots, PackedWeight, add_rms_norm, decode_linear, gdn_decode_core
+from .cb_engine import (GDNSlots, PackedWeight, add_rms_norm, decode_linear, decode_linear_partial, gdn_decode_core,
+                        swiglu)
 
 
 @dataclass
@@ -123,7 +126,7 @@ class HybridDecoder:
         self.slot_idx = torch.arange(n_slots, device=device)
 
     # -- layers ------------------------------------------------------------------------------
-    def gdn(self, i, L, x):
+    def gdn(self, i, L, x, partial=False):
         cfg, n = self.cfg, x.shape[0]
         Hv, D, C = cfg.gdn_v_heads, cfg.gdn_head, cfg.conv_dim
         proj = decode_linear(x, L.in_proj_p)           # one product for qkv | z | b | a
@@ -133,9 +136,9 @@ class HybridDecoder:
         a = proj[:, C + Hv * D + Hv:]
         core = gdn_decode_core(mixed, z, a, b, self.slots.conv[i], L.conv_w, L.A_log, L.dt_bias, L.norm_w,
                                self.slots.rec[i], cfg.gdn_k_heads, Hv, D, cfg.eps)
-        return decode_linear(core.reshape(n, Hv * D), L.out_p)
+        return (decode_linear_partial if partial else decode_linear)(core.reshape(n, Hv * D), L.out_p)
 
-    def attention(self, L, x):
+    def attention(self, L, x, partial=False):
         cfg, n = self.cfg, x.shape[0]
         nh, kv, hd = cfg.attn_heads, cfg.kv_heads, cfg.attn_head
         proj = decode_linear(x, L.qkv_p)
@@ -162,12 +165,11 @@ class HybridDecoder:
         s = s.masked_fill((self.t_idx[None, :] > self.pos[:, None])[:, None, None, :], float("-inf"))
         p = torch.softmax(s, dim=-1).to(x.dtype)
         o = torch.matmul(p, L.v).reshape(n, nh * hd)                               # [n, kv, grp, hd]
-        return decode_linear(o * torch.sigmoid(gate), L.o_p)
+        return (decode_linear_partial if partial else decode_linear)(o * torch.sigmoid(gate), L.o_p)
 
-    def mlp(self, L, x):
-        gu = decode_linear(x, L.gate_up_p)
-        m = self.cfg.mlp
-        return decode_linear(torch.nn.functional.silu(gu[:, :m]) * gu[:, m:], L.down_p)
+    def mlp(self, L, x, partial=False):
+        act = swiglu(decode_linear_partial(x, L.gate_up_p))
+        return (decode_linear_partial if partial else decode_linear)(act, L.down_p)
 
     def step(self, h):
         """h [N, hidden] bf16 (the step's token embeddings) -> logits [N, vocab] (or the final hidden
@@ -183,10 +185,13 @@ class HybridDecoder:
         h, x = add_rms_norm(h, None, norms[0], eps)
         k = 1
         for i, L in enumerate(self.layers):
-            h, x = add_rms_norm(h, self.attention(L, x) if L.full else self.gdn(i, L, x), norms[k], eps)
+            # the token mixer's and the MLP's output projections hand their split-K partial sums
+            # straight to the residual add + norm
+            mix = self.attention(L, x, partial=True) if L.full else self.gdn(i, L, x, partial=True)
+            h, x = add_rms_norm(h, mix, norms[k], eps)
             k += 1
             if L.gate_up_p is not None:
-                h, x = add_rms_norm(h, self.mlp(L, x), norms[k], eps)
+                h, x = add_rms_norm(h, self.mlp(L, x, partial=True), norms[k], eps)
                 k += 1
         self.pos += 1
         return decode_linear(x, self.lm_head_p) if self.lm_head_p is not None else x

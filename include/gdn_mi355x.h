@@ -248,6 +248,27 @@ int gdn_decode_linear_packed(const void* x, int64_t x_stride, const void* packed
 int gdn_add_rmsnorm(const void* h, const void* delta, const void* w, void* h_out, void* x_out, int M, int H,
                     float eps, void* stream);
 
+/*
+ * Split-K partial sums of a decode projection, for a consumer that reduces them itself (no reduction
+ * launch, no bf16 round trip of the projection's output).  The reference's nn.Linear outputs
+ * (o_proj / out_proj / mlp.down_proj feeding the residual add, mlp.gate_up feeding SwiGLU) are
+ * exactly bf16(sum over splits, in split order) of these partials.
+ *   gdn_decode_linear_splits: the number of K splits gdn_decode_linear(_packed) uses for (M, N, K).
+ *   gdn_decode_linear_packed_partial: part [splits][M][N] fp32 (16-byte aligned, part_bytes >=
+ *     splits * M * N * 4), written even with one split; otherwise as gdn_decode_linear_packed.
+ *   gdn_add_rmsnorm_partial: gdn_add_rmsnorm with delta = bf16(sum of part [splits][M][H]);
+ *     H % 8 == 0, H <= 8192, 16-byte aligned rows; h_out may alias h.
+ *   gdn_swiglu_partial: out[M, m] = bf16(bf16(silu(g)) * u) with g, u = bf16(sum of part
+ *     [splits][M][2m]) columns j and m + j (HF Qwen3_5MLP: act_fn(gate_proj(x)) * up_proj(x) with
+ *     gate|up as one projection); m % 8 == 0, part and out 16-byte aligned.
+ */
+int gdn_decode_linear_splits(int M, int64_t N, int64_t K);
+int gdn_decode_linear_packed_partial(const void* x, int64_t x_stride, const void* packed, float* part, int M,
+                                     int64_t N, int64_t K, int64_t part_bytes, void* stream);
+int gdn_add_rmsnorm_partial(const void* h, const float* part, int splits, const void* w, void* h_out, void* x_out,
+                            int M, int H, float eps, void* stream);
+int gdn_swiglu_partial(const float* part, int splits, void* out, int M, int64_t m, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -148,3 +148,32 @@ def test_add_rms_norm_vs_torch(gdn, dev, H):
     h3, x0 = cb.add_rms_norm(h.to(dev), None, w.to(dev))
     assert torch.equal(h3.cpu(), h)
     assert rel_l2(x0, hd.rms_norm(h, w, 1e-6)) <= 1e-3
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("N,K", [(5120, 6144), (512, 1024), (34816, 5120)])
+def test_split_k_partials_feed_norm_and_swiglu(gdn, dev, N, K):
+    """The split-K partial sums of a projection, reduced by their consumers, give exactly the reduced
+    projection's values: residual add + norm from partials == from the bf16 output, SwiGLU from the
+    gate_up partials == bf16(bf16(silu(g)) * u) of the reduced output."""
+    from importlib import import_module
+    cb = import_module(PKG_NAME + ".cb_engine")
+    g_ = torch.Generator().manual_seed(47)
+    M = 16
+    x = torch.randn(M, K, generator=g_).to(torch.bfloat16).to(dev)
+    w = cb.PackedWeight((0.02 * torch.randn(N, K, generator=g_)).to(torch.bfloat16).to(dev))
+    y = cb.decode_linear(x, w)
+    p = cb.decode_linear_partial(x, w)
+    assert torch.equal(p.to_bf16(), y), "partials must reduce to the projection's output"
+    if N <= 8192:
+        h = torch.randn(M, N, generator=g_).to(torch.bfloat16).to(dev)
+        nw = (0.02 * torch.randn(N, generator=g_)).to(torch.bfloat16).to(dev)
+        h_ref, x_ref = cb.add_rms_norm(h, y, nw)
+        h_p, x_p = cb.add_rms_norm(h, p, nw)
+        assert torch.equal(h_p, h_ref) and torch.equal(x_p, x_ref)
+    if N % 16 == 0:
+        m = N // 2
+        act = cb.swiglu(p)
+        ref = torch.nn.functional.silu(y[:, :m]) * y[:, m:]
+        assert torch.equal(act, cb.swiglu(y))
+        assert ((act.float() - ref.float()).abs() <= ref.float().abs() * 2 ** -7).all()
