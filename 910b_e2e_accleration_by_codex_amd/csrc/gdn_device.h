@@ -54,7 +54,9 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 // Register-only reductions with DPP row permutes and gfx950's permlane swaps (no LDS round trip
 // per step).  Every step adds a lane's value to its partner's, so all lanes of a group end with
-// the bit-identical sum.  The whole wave must be active.
+// the bit-identical sum -- and the same sum as the xor butterfly over the same lane groups
+// (lane ^ 1, ^ 2, ^ 4, ^ 8 for row16_sum; the later steps pair lanes whose values are already
+// equal within their group).  The whole wave must be active.
 template <int kCtrl>
 __device__ __forceinline__ float dpp_mov(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), kCtrl, 0xf, 0xf, true));
@@ -73,6 +75,25 @@ __device__ __forceinline__ float half_sum(float v) {
   const uint32_t u = __builtin_bit_cast(uint32_t, v);
   const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);  // rows (0,1), (2,3) exchanged
   return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
+}
+// v plus the value of lane ^ 16, in every lane.
+__device__ __forceinline__ float xor16_sum(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);  // rows (0,1), (2,3) exchanged
+  return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
+}
+// Maximum over the whole wave.
+__device__ __forceinline__ float wave_max_fast(float v) {
+  v = fmaxf(v, dpp_mov<0xB1>(v));
+  v = fmaxf(v, dpp_mov<0x4E>(v));
+  v = fmaxf(v, dpp_mov<0x141>(v));
+  v = fmaxf(v, dpp_mov<0x140>(v));
+  uint32_t u = __builtin_bit_cast(uint32_t, v);
+  auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  v = fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
+  u = __builtin_bit_cast(uint32_t, v);
+  r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
 }
 // v plus the value of lane ^ 32, in every lane.
 __device__ __forceinline__ float xor32_sum(float v) {

@@ -318,9 +318,7 @@ __device__ __forceinline__ void l2norm_rows4(u16x8* x) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) ss[i] = sumsq_bf16(x[i], 0.f);
 #pragma unroll
-  for (int o = 1; o < 16; o <<= 1)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) ss[i] += __shfl_xor(ss[i], o, kWave);
+  for (int i = 0; i < 4; ++i) ss[i] = row16_sum(ss[i]);
 #pragma unroll
   for (int i = 0; i < 4; ++i) x[i] = scale_bf16(x[i], l2norm_inv(ss[i]));
 }
@@ -370,11 +368,7 @@ __device__ __forceinline__ f16x8 pack_acc_f16(f32x4 a, f32x4 b, float sa) {
   }
   return h;
 }
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-  return v;
-}
+__device__ __forceinline__ float wave_max(float v) { return wave_max_fast(v); }
 
 struct LocalSmem {
   uint16_t K[pf::CH * pf::LDK];     // K chunk, row-major (token, feature); K^T operands via transpose reads
@@ -475,8 +469,7 @@ __device__ __forceinline__ int local_key(LocalSmem& sm, const KeyLoads& L, int u
       float ss = 0.f;
 #pragma unroll
       for (int s = 0; s < 4; ++s) ss = sumsq_bf16(qr[s], ss);
-      ss += __shfl_xor(ss, 16, kWave);
-      ss += __shfl_xor(ss, 32, kWave);
+      ss = xor32_sum(xor16_sum(ss));
       const float inv = l2norm_inv(ss);
 #pragma unroll
       for (int s = 0; s < 4; ++s) qr[s] = scale_bf16(qr[s], inv);
