@@ -267,6 +267,44 @@ def swiglu(gate_up):
     return torch.nn.functional.silu(gate_up[:, :m]) * gate_up[:, m:]
 
 
+def attn_decode_workspace(n_slots, n_heads, head_dim, cache_len, device):
+    """The fp32 workspace gqa_decode_attention needs for these sizes (allocate once, reuse per layer)."""
+    nbytes = int(_lib.lib().gdn_attn_decode_workspace_bytes(n_slots, n_heads, head_dim, cache_len))
+    if nbytes < 0:
+        raise ValueError("attn_decode_workspace: bad sizes")
+    return torch.empty(max(nbytes, 4) // 4, dtype=torch.float32, device=device)
+
+
+def gqa_decode_attention(proj, pos, q_norm, k_norm, inv_freq, k_cache_t, v_cache, n_heads, kv_heads, head_dim,
+                         rotary_dim, eps=1e-6, work=None):
+    """HF Qwen3_5Attention.forward at decode (modeling_qwen3_5.py:629-700) after its one fused q|gate|k|v
+    projection: q/k Qwen3_5RMSNorm, partial rotary at each slot's position, K and V written into the
+    per-slot cache (K transposed [N, kv, hd, T], V [N, kv, T, hd]) at ``pos``, softmax attention over
+    positions 0..pos, times sigmoid(gate).  proj [N, (2 nh + 2 kv) hd] bf16 (per head q then gate, then
+    k, then v), pos [N] int64 on the device.  Returns the gated output [N, nh * hd] bf16 (o_proj's
+    input).  Three HIP launches, capturable in a graph."""
+    _lib.require_cuda(proj, pos, q_norm, k_norm, k_cache_t, v_cache)
+    N = proj.shape[0]
+    nh, kv, hd = n_heads, kv_heads, head_dim
+    T = k_cache_t.shape[-1]
+    if (proj.dtype != torch.bfloat16 or proj.stride(1) != 1 or pos.dtype != torch.int64 or pos.numel() != N
+            or tuple(k_cache_t.shape) != (N, kv, hd, T) or tuple(v_cache.shape) != (N, kv, T, hd)
+            or not (k_cache_t.is_contiguous() and v_cache.is_contiguous())
+            or k_cache_t.dtype != torch.bfloat16 or v_cache.dtype != torch.bfloat16):
+        raise ValueError("gqa_decode_attention: bf16 proj [N, (2 nh + 2 kv) hd], int64 pos [N], contiguous bf16 "
+                         "caches K^T [N, kv, hd, T] and V [N, kv, T, hd]")
+    qn = q_norm.to(torch.bfloat16).contiguous()
+    kn = k_norm.to(torch.bfloat16).contiguous()
+    inv = inv_freq.to(torch.float32).contiguous() if rotary_dim else None
+    if work is None:
+        work = attn_decode_workspace(N, nh, hd, T, proj.device)
+    out = torch.empty(N, nh * hd, dtype=torch.bfloat16, device=proj.device)
+    _lib.call("gdn_attn_decode", _lib.ptr(proj), proj.stride(0), _lib.ptr(pos.contiguous()), _lib.ptr(qn),
+              _lib.ptr(kn), _lib.ptr(inv), _lib.ptr(k_cache_t), _lib.ptr(v_cache), _lib.ptr(out), out.stride(0),
+              _lib.ptr(work), work.numel() * 4, N, nh, kv, hd, rotary_dim, T, float(eps), _lib.stream_of(proj))
+    return out
+
+
 def add_rms_norm(h, delta, weight, eps=1e-6):
     """Residual add + Qwen3_5RMSNorm between decode-step layers (HF modeling_qwen3_5.py):
     h, delta [M, H] bf16 (delta None: norm only; or the Partials of the projection that produced it),

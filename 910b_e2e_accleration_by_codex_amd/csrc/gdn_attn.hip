@@ -1,0 +1,342 @@
+// GQA decode attention of the hybrid stack's full-attention layers, for N slots of one new token
+// each, over a per-slot KV cache: HF Qwen3_5Attention.forward (modeling_qwen3_5.py:629-700) with
+// its q/k Qwen3_5RMSNorm, partial rotary (apply_rotary_pos_emb, :554-580), eager attention
+// (:604-626) and the sigmoid output gate (:698), as the reference's engine runs it at decode.
+//
+// Three launches, all HBM- or latency-bound (the cache is read once):
+//   1. attn_prep_kernel: one wave per (slot, head row).  RMSNorm (fp32, (1 + w), bf16) of the q and
+//      k rows, rotary on the first rd dims (fp32, bf16), q kept in fp32 for the scores, k and v
+//      written into the cache at the slot's position.
+//   2. attn_split_kernel: one workgroup per (256-token split, kv head, slot) with the kv head's G
+//      query heads.  Scores (fp32) from the transposed K cache [hd, T] with tokens along the lanes
+//      (8-byte loads of 4 tokens per lane, each wave a quarter of the head dims), the split's max
+//      and exp-sum per query head, then P V from the V cache [T, hd] (16-byte loads of 8 dims per
+//      lane, row groups of tokens), reduced across the row groups in LDS.
+//   3. attn_combine_kernel: per (slot, query head): the splits merged with their max (flash
+//      decoding), o rounded to bf16 and multiplied by bf16(sigmoid(gate)).
+// Rounding: scores, softmax and P V accumulate in fp32 (the eager path rounds the scores and the
+// probabilities to bf16); the test holds the result to an fp32 reference.
+#include "gdn_device.h"
+#include "gdn_internal.h"
+
+namespace gdn {
+namespace at {
+constexpr int SPLIT = 256;   // tokens per split workgroup
+constexpr int THREADS = 256;
+typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+
+__host__ __device__ inline int64_t round256(int64_t b) { return (b + 255) / 256 * 256; }
+// workspace: q (fp32 [N, nh, hd]) | m, l (fp32 [N, nh, S, 2]) | partial o (fp32 [N, nh, S, hd])
+struct Work {
+  float* q;
+  float* ml;
+  float* o;
+};
+__host__ __device__ inline int splits_of(int T) { return (T + SPLIT - 1) / SPLIT; }
+__host__ __device__ inline int64_t work_bytes(int N, int nh, int hd, int T) {
+  const int64_t S = splits_of(T);
+  return round256((int64_t)N * nh * hd * 4) + round256((int64_t)N * nh * S * 2 * 4) +
+         round256((int64_t)N * nh * S * hd * 4);
+}
+__host__ __device__ inline Work work_of(float* base, int N, int nh, int hd, int T) {
+  const int64_t S = splits_of(T);
+  char* p = reinterpret_cast<char*>(base);
+  Work w;
+  w.q = reinterpret_cast<float*>(p);
+  p += round256((int64_t)N * nh * hd * 4);
+  w.ml = reinterpret_cast<float*>(p);
+  p += round256((int64_t)N * nh * S * 2 * 4);
+  w.o = reinterpret_cast<float*>(p);
+  return w;
+}
+}  // namespace at
+
+// One wave per (slot n, row r): r < nh are query heads, nh <= r < nh + kv key heads.  Lane l holds
+// dims l + 64 e.  The rotary partner of dim d < rd is d +- rd / 2, exchanged through LDS.
+template <int HD>
+__global__ __launch_bounds__(256) void attn_prep_kernel(const uint16_t* __restrict__ proj, int64_t ps,
+                                                        const int64_t* __restrict__ pos,
+                                                        const uint16_t* __restrict__ q_w,
+                                                        const uint16_t* __restrict__ k_w,
+                                                        const float* __restrict__ inv_freq, uint16_t* __restrict__ kt,
+                                                        uint16_t* __restrict__ vc, float* __restrict__ qf, int N,
+                                                        int nh, int kv, int rd, int T, float eps) {
+  constexpr int E = HD / 64;
+  __shared__ float row[4][HD];
+  const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t w = (int64_t)blockIdx.x * 4 + wid;
+  if (w >= (int64_t)N * (nh + kv)) return;  // whole waves only: no barrier below
+  const int n = (int)(w / (nh + kv)), r = (int)(w % (nh + kv));
+  const bool is_q = r < nh;
+  const int j = r - nh;
+  const uint16_t* src = proj + n * ps + (is_q ? (int64_t)r * 2 * HD : (int64_t)2 * nh * HD + (int64_t)j * HD);
+  const uint16_t* wt = is_q ? q_w : k_w;
+  float x[E];
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    x[e] = bf2f(src[lane + 64 * e]);
+    ss += x[e] * x[e];
+  }
+  ss = wave_sum(ss);
+  const float inv = rsqrt_f(ss / (float)HD + eps);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const float y = rbf((x[e] * inv) * (1.0f + bf2f(wt[lane + 64 * e])));
+    x[e] = y;
+    row[wid][lane + 64 * e] = y;
+  }
+  // one wave's LDS accesses complete in program order: the partner reads below see the writes
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  const int64_t p = pos[n];
+  const float fp = (float)p;
+  const int half = rd / 2;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int d = lane + 64 * e;
+    if (d < rd) {
+      const int i = d < half ? d : d - half;
+      const float ang = fp * inv_freq[i];
+      const float c = cosf(ang), s = sinf(ang);
+      const float rot = d < half ? -row[wid][d + half] : row[wid][d - half];
+      x[e] = rbf(x[e] * c + rot * s);
+    }
+  }
+  if (is_q) {
+    float* q = qf + ((int64_t)n * nh + r) * HD;
+#pragma unroll
+    for (int e = 0; e < E; ++e) q[lane + 64 * e] = x[e];
+  } else if (p >= 0 && p < T) {
+    const uint16_t* vs = proj + n * ps + (int64_t)2 * nh * HD + (int64_t)kv * HD + (int64_t)j * HD;
+    uint16_t* kd = kt + ((int64_t)n * kv + j) * HD * T + p;
+    uint16_t* vd = vc + (((int64_t)n * kv + j) * T + p) * HD;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      kd[(int64_t)(lane + 64 * e) * T] = f2bf(x[e]);
+      vd[lane + 64 * e] = vs[lane + 64 * e];
+    }
+  }
+}
+
+// grid (S, kv, N), 256 threads.  Split s covers tokens [256 s, 256 s + 256) of the slot's
+// len = pos + 1 (the new token included).
+template <int HD, int G>
+__global__ __launch_bounds__(256) void attn_split_kernel(const int64_t* __restrict__ pos,
+                                                         const uint16_t* __restrict__ kt,
+                                                         const uint16_t* __restrict__ vc, at::Work wk, int nh,
+                                                         int kv, int T, float scale) {
+  using namespace at;
+  constexpr int CG = HD / 8;          // 16-byte column groups of a V row
+  constexpr int RG = THREADS / CG;    // token row groups in P V
+  constexpr int QROWS = HD / 4;       // head dims per wave in the scores
+  __shared__ float qs[HD][G];                            // q of the G heads, dim-major
+  __shared__ float big[(4 * G * SPLIT > RG * G * HD) ? 4 * G * SPLIT : RG * G * HD];
+  __shared__ float pl[SPLIT][G];                         // probabilities, token-major
+  __shared__ float red[2][4][G];
+  const int split = blockIdx.x, j = blockIdx.y, n = blockIdx.z;
+  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
+  const int64_t p = pos[n];
+  const int len = (int)(p + 1 < T ? p + 1 : T);
+  const int t0 = split * SPLIT;
+  if (t0 >= len) return;  // uniform over the workgroup
+  const int S = splits_of(T);
+  const int h0 = j * G;
+  for (int i = tid; i < G * HD; i += THREADS) {
+    const int g = i / HD, d = i % HD;
+    qs[d][g] = wk.q[((int64_t)n * nh + h0 + g) * HD + d];
+  }
+  __syncthreads();
+  // ---- scores: wave wid sums dims [QROWS wid, QROWS wid + QROWS) for tokens t0 + 4 lane .. + 3
+  {
+    float acc[G][4];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[g][i] = 0.f;
+    const int tl = t0 + 4 * lane;
+    const int len4 = (len + 3) & ~3;  // <= T: T is a multiple of 4
+    if (tl < len4) {
+      const uint16_t* kp = kt + ((int64_t)n * kv + j) * HD * T + (int64_t)(QROWS * wid) * T + tl;
+#pragma unroll 8
+      for (int d = 0; d < QROWS; ++d) {
+        const u16x4 k4 = *reinterpret_cast<const u16x4*>(kp + (int64_t)d * T);
+        const int dd = QROWS * wid + d;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float q = qs[dd][g];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[g][i] += q * bf2f(k4[i]);
+        }
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) big[(wid * G + g) * SPLIT + 4 * lane + i] = acc[g][i];
+  }
+  __syncthreads();
+  // ---- split softmax: thread tid = token t0 + tid
+  const bool valid = t0 + tid < len;
+  float s[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float v = ((big[(0 * G + g) * SPLIT + tid] + big[(1 * G + g) * SPLIT + tid]) +
+                     (big[(2 * G + g) * SPLIT + tid] + big[(3 * G + g) * SPLIT + tid])) * scale;
+    s[g] = valid ? v : -INFINITY;
+    const float m = wave_max_fast(s[g]);
+    if (lane == 0) red[0][wid][g] = m;
+  }
+  __syncthreads();
+  float e[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float m = fmaxf(fmaxf(red[0][0][g], red[0][1][g]), fmaxf(red[0][2][g], red[0][3][g]));
+    e[g] = valid ? expf(s[g] - m) : 0.f;
+    pl[tid][g] = e[g];
+    const float l = wave_sum(e[g]);
+    if (lane == 0) red[1][wid][g] = l;
+  }
+  __syncthreads();
+  if (tid < G) {
+    const int g = tid;
+    const float m = fmaxf(fmaxf(red[0][0][g], red[0][1][g]), fmaxf(red[0][2][g], red[0][3][g]));
+    const float l = (red[1][0][g] + red[1][1][g]) + (red[1][2][g] + red[1][3][g]);
+    float* ml = wk.ml + (((int64_t)n * nh + h0 + g) * S + split) * 2;
+    ml[0] = m;
+    ml[1] = l;
+  }
+  // ---- P V: thread (rg, cg) sums tokens t0 + rg + RG i over dims 8 cg .. 8 cg + 7
+  {
+    const int cg = tid % CG, rg = tid / CG;
+    float acc[G][8];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
+    const uint16_t* vp = vc + (((int64_t)n * kv + j) * T + t0) * HD + 8 * cg;
+    const int cnt = len - t0 < SPLIT ? len - t0 : SPLIT;
+#pragma unroll 4
+    for (int t = rg; t < cnt; t += RG) {
+      const u16x8 v8 = *reinterpret_cast<const u16x8*>(vp + (int64_t)t * HD);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float pr = pl[t][g];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[g][i] += pr * bf2f(v8[i]);
+      }
+    }
+    __syncthreads();  // every score read of `big` is done: reuse it for the row groups' sums
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) big[(rg * G + g) * HD + 8 * cg + i] = acc[g][i];
+  }
+  __syncthreads();
+  for (int i = tid; i < G * HD; i += THREADS) {
+    const int g = i / HD, d = i % HD;
+    float o = 0.f;
+#pragma unroll
+    for (int r = 0; r < RG; ++r) o += big[(r * G + g) * HD + d];
+    wk.o[(((int64_t)n * nh + h0 + g) * S + split) * HD + d] = o;
+  }
+}
+
+// grid (N * nh), HD threads: thread d of (slot n, query head h).
+template <int HD>
+__global__ __launch_bounds__(256) void attn_combine_kernel(const int64_t* __restrict__ pos,
+                                                           const uint16_t* __restrict__ proj, int64_t ps,
+                                                           at::Work wk, uint16_t* __restrict__ out,
+                                                           int64_t out_stride, int nh, int T) {
+  using namespace at;
+  const int n = blockIdx.x / nh, h = blockIdx.x % nh, d = threadIdx.x;
+  const int64_t p = pos[n];
+  const int len = (int)(p + 1 < T ? p + 1 : T);
+  const int ns = (len + SPLIT - 1) / SPLIT, S = splits_of(T);
+  const float* ml = wk.ml + ((int64_t)n * nh + h) * S * 2;
+  const float* op = wk.o + ((int64_t)n * nh + h) * S * HD + d;
+  float M = -INFINITY;
+  for (int s = 0; s < ns; ++s) M = fmaxf(M, ml[2 * s]);
+  float L = 0.f, o = 0.f;
+  for (int s = 0; s < ns; ++s) {
+    const float f = expf(ml[2 * s] - M);
+    L += ml[2 * s + 1] * f;
+    o += op[(int64_t)s * HD] * f;
+  }
+  const float a = rbf(o / L);
+  const float gate = bf2f(proj[n * ps + (int64_t)h * 2 * HD + HD + d]);
+  out[n * out_stride + (int64_t)h * HD + d] = f2bf(a * rbf(sigmoid_f(gate)));
+}
+
+template <int HD, int G>
+static void launch_split(dim3 grid, hipStream_t st, const int64_t* pos, const uint16_t* kt, const uint16_t* vc,
+                         at::Work wk, int nh, int kv, int T, float scale) {
+  attn_split_kernel<HD, G><<<grid, at::THREADS, 0, st>>>(pos, kt, vc, wk, nh, kv, T, scale);
+}
+template <int HD>
+static bool launch_split_g(int G, dim3 grid, hipStream_t st, const int64_t* pos, const uint16_t* kt,
+                           const uint16_t* vc, at::Work wk, int nh, int kv, int T, float scale) {
+  switch (G) {
+    case 1: launch_split<HD, 1>(grid, st, pos, kt, vc, wk, nh, kv, T, scale); return true;
+    case 2: launch_split<HD, 2>(grid, st, pos, kt, vc, wk, nh, kv, T, scale); return true;
+    case 4: launch_split<HD, 4>(grid, st, pos, kt, vc, wk, nh, kv, T, scale); return true;
+    case 6: launch_split<HD, 6>(grid, st, pos, kt, vc, wk, nh, kv, T, scale); return true;
+    case 8: launch_split<HD, 8>(grid, st, pos, kt, vc, wk, nh, kv, T, scale); return true;
+    default: return false;
+  }
+}
+template <int HD>
+static int launch_all(const uint16_t* proj, int64_t ps, const int64_t* pos, const uint16_t* q_w, const uint16_t* k_w,
+                      const float* inv_freq, uint16_t* kt, uint16_t* vc, uint16_t* out, int64_t os, float* work, int N,
+                      int nh, int kv, int rd, int T, float eps, hipStream_t st) {
+  const at::Work wk = at::work_of(work, N, nh, HD, T);
+  const int64_t waves = (int64_t)N * (nh + kv);
+  attn_prep_kernel<HD><<<(unsigned)((waves + 3) / 4), 256, 0, st>>>(proj, ps, pos, q_w, k_w, inv_freq, kt, vc, wk.q,
+                                                                     N, nh, kv, rd, T, eps);
+  const dim3 grid(at::splits_of(T), kv, N);
+  if (!launch_split_g<HD>(nh / kv, grid, st, pos, kt, vc, wk, nh, kv, T, 1.0f / sqrtf((float)HD)))
+    return set_error(GDN_EUNSUP, "gdn_attn_decode: query heads per kv head must be 1, 2, 4, 6 or 8");
+  attn_combine_kernel<HD><<<N * nh, HD, 0, st>>>(pos, proj, ps, wk, out, os, nh, T);
+  return check_launch("gdn_attn_decode");
+}
+
+}  // namespace gdn
+
+using namespace gdn;
+
+extern "C" int64_t gdn_attn_decode_workspace_bytes(int N, int nh, int hd, int T) {
+  if (N < 0 || nh < 1 || hd < 1 || T < 1) return -1;
+  return at::work_bytes(N, nh, hd, T);
+}
+
+extern "C" int gdn_attn_decode(const void* proj, int64_t proj_stride, const int64_t* pos, const void* q_norm_w,
+                               const void* k_norm_w, const float* inv_freq, void* k_cache_t, void* v_cache,
+                               void* out, int64_t out_stride, float* work, int64_t work_bytes, int N, int nh, int kv,
+                               int hd, int rd, int T, float eps, void* stream) {
+  clear_error();
+  GDN_REQUIRE(proj && pos && q_norm_w && k_norm_w && k_cache_t && v_cache && out && work && (inv_freq || rd == 0),
+              "gdn_attn_decode: null pointer");
+  GDN_REQUIRE(N >= 0 && nh >= 1 && kv >= 1 && nh % kv == 0, "gdn_attn_decode: bad head counts");
+  GDN_SUPPORT(hd == 64 || hd == 128 || hd == 256, "gdn_attn_decode: head_dim must be 64, 128 or 256");
+  GDN_REQUIRE(rd >= 0 && rd <= hd && rd % 2 == 0, "gdn_attn_decode: rotary dims must be even and <= head_dim");
+  GDN_REQUIRE(T >= 4 && T % 4 == 0, "gdn_attn_decode: cache length must be a positive multiple of 4");
+  GDN_REQUIRE(proj_stride >= (int64_t)(2 * nh + 2 * kv) * hd && out_stride >= (int64_t)nh * hd,
+              "gdn_attn_decode: row strides too small");
+  GDN_REQUIRE(work_bytes >= at::work_bytes(N, nh, hd, T), "gdn_attn_decode: workspace too small (%lld bytes needed)",
+              (long long)at::work_bytes(N, nh, hd, T));
+  GDN_REQUIRE(aligned(k_cache_t, 8) && aligned(v_cache, 16) && aligned(work, 256) && aligned(pos, 8),
+              "gdn_attn_decode: K cache 8-byte, V cache 16-byte, workspace 256-byte aligned");
+  if (N == 0) return GDN_OK;
+  const auto* P = static_cast<const uint16_t*>(proj);
+  const auto* qw = static_cast<const uint16_t*>(q_norm_w);
+  const auto* kw = static_cast<const uint16_t*>(k_norm_w);
+  auto* kt = static_cast<uint16_t*>(k_cache_t);
+  auto* vc = static_cast<uint16_t*>(v_cache);
+  auto* o = static_cast<uint16_t*>(out);
+  const hipStream_t st = (hipStream_t)stream;
+  switch (hd) {
+    case 64: return launch_all<64>(P, proj_stride, pos, qw, kw, inv_freq, kt, vc, o, out_stride, work, N, nh, kv, rd, T, eps, st);
+    case 128: return launch_all<128>(P, proj_stride, pos, qw, kw, inv_freq, kt, vc, o, out_stride, work, N, nh, kv, rd, T, eps, st);
+    default: return launch_all<256>(P, proj_stride, pos, qw, kw, inv_freq, kt, vc, o, out_stride, work, N, nh, kv, rd, T, eps, st);
+  }
+}

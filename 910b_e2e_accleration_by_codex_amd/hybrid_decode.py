@@ -11,17 +11,17 @@ slots' GDN states and KV caches are pre-filled with random values at per-slot co
 The GDN layer core, every linear of the step (the weight-streaming decode projection kernel,
 gdn_decode_linear), the residual adds with their RMSNorms and the SwiGLU products are this library's
 kernels; the output projections hand their split-K partial sums straight to the residual add + norm,
-and gate_up its partials to SwiGLU.  Attention scores, softmax and the q/k norms and rotary are torch
-ops.  The KV cache keeps K transposed ([slot, kv head, head_dim, position]) so both batched
-attention products take a contiguous right operand.
+and gate_up its partials to SwiGLU.  The attention layer (q/k norms, rotary, cache writes, softmax
+attention, gate) is this library's three-launch decode attention.  The KV cache keeps K transposed
+([slot, kv head, head_dim, position]) so the score loads run along positions.
 """
 from dataclasses import dataclass
 from types import SimpleNamespace
 
 import torch
 
-from .cb_engine import (GDNSlots, PackedWeight, add_rms_norm, decode_linear, decode_linear_partial, gdn_decode_core,
-                        swiglu)
+from .cb_engine import (GDNSlots, PackedWeight, add_rms_norm, attn_decode_workspace, decode_linear, decode_linear_partial,
+                        gdn_decode_core, gqa_decode_attention, swiglu)
 
 
 @dataclass
@@ -53,18 +53,6 @@ class HybridConfig:
         return (2 * self.gdn_k_heads + self.gdn_v_heads) * self.gdn_head
 
 
-def rms_norm(x, w, eps):
-    """Qwen3_5RMSNorm: fp32 x * rsqrt(mean(x^2) + eps) * (1 + w), cast back (modeling_qwen3_5.py)."""
-    xf = x.float()
-    y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
-    return (y * (1.0 + w.float())).to(x.dtype)
-
-
-def _rotate_half(x):
-    h = x.shape[-1] // 2
-    return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
-
-
 class HybridDecoder:
     """Random-weight hybrid stack with slot state for ``n_slots`` sequences.  ``ctx`` (int [N], host)
     are the per-slot context lengths already in the caches; each ``step`` appends one token per slot.
@@ -84,7 +72,7 @@ class HybridDecoder:
         gdn_ids = [i for i in range(cfg.layers) if not cfg.is_full(i)]
         self.slots = GDNSlots(n_slots, gdn_ids, cfg.conv_dim, cfg.conv_k, cfg.gdn_v_heads, D, device)
         ctx = torch.as_tensor(ctx, dtype=torch.int64)
-        self.max_ctx = int(ctx.max()) + max_steps
+        self.max_ctx = (int(ctx.max()) + max_steps + 3) // 4 * 4  # the attention kernels read 4 positions at once
         self.pos = ctx.to(device=device, dtype=torch.int64)  # position of the next token per slot
         kv, hd = cfg.kv_heads, cfg.attn_head
         for i in range(cfg.layers):
@@ -121,9 +109,10 @@ class HybridDecoder:
         if not keep_plain:
             self.lm_head = None
         rd = int(hd * cfg.rotary_frac)
+        self.rotary_dim = rd
         self.inv_freq = 1.0 / (cfg.rope_theta ** (torch.arange(0, rd, 2, device=device, dtype=torch.float32) / rd))
-        self.t_idx = torch.arange(self.max_ctx, device=device)
-        self.slot_idx = torch.arange(n_slots, device=device)
+        self.attn_work = (attn_decode_workspace(n_slots, cfg.attn_heads, hd, self.max_ctx, device)
+                          if any(L.full for L in self.layers) else None)
 
     # -- layers ------------------------------------------------------------------------------
     def gdn(self, i, L, x, partial=False):
@@ -139,33 +128,14 @@ class HybridDecoder:
         return (decode_linear_partial if partial else decode_linear)(core.reshape(n, Hv * D), L.out_p)
 
     def attention(self, L, x, partial=False):
-        cfg, n = self.cfg, x.shape[0]
+        cfg = self.cfg
         nh, kv, hd = cfg.attn_heads, cfg.kv_heads, cfg.attn_head
-        proj = decode_linear(x, L.qkv_p)
-        qg = proj[:, :nh * hd * 2].reshape(n, nh, 2 * hd)
-        q, gate = qg[..., :hd], qg[..., hd:].reshape(n, nh * hd)
-        k = proj[:, nh * hd * 2:nh * hd * 2 + kv * hd].reshape(n, kv, hd)
-        v = proj[:, nh * hd * 2 + kv * hd:].reshape(n, kv, hd)
-        q, k = rms_norm(q, L.q_norm, cfg.eps), rms_norm(k, L.k_norm, cfg.eps)
-        # partial rotary at each slot's position (HF apply_rotary_pos_emb on the first rd dims)
-        freqs = self.pos.float()[:, None] * self.inv_freq[None, :]
-        emb = torch.cat((freqs, freqs), dim=-1)
-        cos, sin = emb.cos()[:, None, :], emb.sin()[:, None, :]
-        rd = emb.shape[-1]
-
-        def rope(t):
-            tr = t[..., :rd].float()
-            return torch.cat(((tr * cos + _rotate_half(tr) * sin).to(t.dtype), t[..., rd:]), dim=-1)
-
-        q, k = rope(q), rope(k)
-        L.kt[self.slot_idx, :, :, self.pos] = k
-        L.v[self.slot_idx, :, self.pos, :] = v
-        grp = nh // kv
-        s = torch.matmul(q.reshape(n, kv, grp, hd), L.kt).float() * (hd ** -0.5)  # [n, kv, grp, T]
-        s = s.masked_fill((self.t_idx[None, :] > self.pos[:, None])[:, None, None, :], float("-inf"))
-        p = torch.softmax(s, dim=-1).to(x.dtype)
-        o = torch.matmul(p, L.v).reshape(n, nh * hd)                               # [n, kv, grp, hd]
-        return (decode_linear_partial if partial else decode_linear)(o * torch.sigmoid(gate), L.o_p)
+        proj = decode_linear(x, L.qkv_p)   # per head q | gate, then k, then v
+        # q/k norms, partial rotary, the cache writes at each slot's position, softmax attention and
+        # the sigmoid gate: three HIP launches
+        o = gqa_decode_attention(proj, self.pos, L.q_norm, L.k_norm, self.inv_freq, L.kt, L.v, nh, kv, hd,
+                                 self.rotary_dim, cfg.eps, work=self.attn_work)
+        return (decode_linear_partial if partial else decode_linear)(o, L.o_p)
 
     def mlp(self, L, x, partial=False):
         act = swiglu(decode_linear_partial(x, L.gate_up_p))

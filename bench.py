@@ -270,7 +270,8 @@ def bench_hybrid(gdn, dev, steps=10, warmup=2, seed=4):
     GDN states and KV caches, HIP-graph replay (random-init bf16 weights):
       * the 64-layer hybrid stack (48 GDN + 16 GQA attention layers, SwiGLU MLPs, LM head 248320);
       * the 48 GDN layers alone with their projections (in_proj GEMM -> fused HIP core -> out_proj).
-    HBM bytes: every weight read once per step, GDN states read + written, KV caches read."""
+    HBM bytes: every weight read once per step, GDN states read + written, each slot's KV cache read
+    up to its position."""
     hd = importlib.import_module(PKG + ".hybrid_decode")
     cb = importlib.import_module(PKG + ".cb_engine")
     out = []
@@ -297,7 +298,11 @@ def bench_hybrid(gdn, dev, steps=10, warmup=2, seed=4):
         wbytes = sum(p.N * p.K * 2 for p in packed)                     # the weights' own bytes
         wbytes += sum(L.conv_w.numel() * 2 for L in model.layers if not L.full)
         sbytes = sum(2 * (model.slots.conv[i].numel() * 2 + model.slots.rec[i].numel() * 4) for i in model.slots.rec)
-        kvbytes = sum(L.kt.numel() * 2 + L.v.numel() * 2 for L in model.layers if L.full)
+        # the attention reads each slot's K and V at positions 0..pos: the graph's eager warm-up step
+        # and the warmup replays advanced pos to ctx + 1 + warmup before the timed steps
+        n_attn = sum(1 for L in model.layers if L.full)
+        mean_len = float(ctx.double().mean()) + 2 + warmup + (steps - 1) / 2
+        kvbytes = int(n_attn * N_SLOTS * mean_len * cfg.kv_heads * cfg.attn_head * 2 * 2)
         total = wbytes + sbytes + kvbytes
         n_gdn = len(model.slots.rec)
         out.append({"workload": f"decode step, Qwen3.5-27B shape, {name}, 16 slots, ctx U[512,4096], HIP graph",

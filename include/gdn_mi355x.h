@@ -269,6 +269,29 @@ int gdn_add_rmsnorm_partial(const void* h, const float* part, int splits, const 
                             int M, int H, float eps, void* stream);
 int gdn_swiglu_partial(const float* part, int splits, void* out, int M, int64_t m, void* stream);
 
+/*
+ * GQA decode attention of the hybrid stack's full-attention layers, one new token for each of N
+ * slots.  It has no counterpart inside the reference's GDN path: it is the attention layer the
+ * reference's engine runs between its GDN layers, HF Qwen3_5Attention.forward
+ * (transformers modeling_qwen3_5.py:629-700: gated q, q/k Qwen3_5RMSNorm, partial rotary,
+ * softmax(q k^T / sqrt(hd)) v, times sigmoid(gate)), here in three launches on a per-slot cache.
+ *   proj [N, proj_stride] bf16: per query head h its q (hd) then its gate (hd) at h * 2hd, then the
+ *     kv key rows (hd each) at 2 nh hd, then the kv value rows at (2 nh + kv) hd.
+ *   pos [N] int64 (device): the position of the new token; it is written to the caches there and
+ *     attends to positions 0..pos (positions >= T are not written, the attended range is clamped).
+ *   q_norm_w, k_norm_w [hd] bf16 (the norm multiplies by 1 + w); inv_freq [rd / 2] fp32 (the rotary
+ *     angle of pair i is float(pos) * inv_freq[i], applied to the first rd dims).
+ *   k_cache_t [N, kv, hd, T] bf16 (K transposed), v_cache [N, kv, T, hd] bf16; T % 4 == 0.
+ *   out [N, out_stride] bf16: the gated attention output, nh * hd columns (o_proj's input).
+ *   work: gdn_attn_decode_workspace_bytes(N, nh, hd, T) bytes, 256-byte aligned.
+ * hd in {64, 128, 256}; nh / kv in {1, 2, 4, 6, 8}.  Scores, softmax and P V run in fp32.
+ */
+int64_t gdn_attn_decode_workspace_bytes(int N, int nh, int hd, int T);
+int gdn_attn_decode(const void* proj, int64_t proj_stride, const int64_t* pos, const void* q_norm_w,
+                    const void* k_norm_w, const float* inv_freq, void* k_cache_t, void* v_cache, void* out,
+                    int64_t out_stride, float* work, int64_t work_bytes, int N, int nh, int kv, int hd, int rd, int T,
+                    float eps, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

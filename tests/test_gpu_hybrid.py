@@ -10,6 +10,18 @@ from conftest import PKG_NAME, rel_l2
 OUT_TOL = 1e-2
 
 
+def rms_norm(x, w, eps):
+    """Qwen3_5RMSNorm (HF modeling_qwen3_5.py): fp32 x * rsqrt(mean(x^2) + eps) * (1 + w), cast back."""
+    xf = x.float()
+    y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return (y * (1.0 + w.float())).to(x.dtype)
+
+
+def rotate_half(x):
+    h = x.shape[-1] // 2
+    return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
+
+
 def _hybrid(gdn):
     from importlib import import_module
     return import_module(PKG_NAME + ".hybrid_decode")
@@ -67,10 +79,10 @@ def test_attention_layer_vs_fp32_reference(gdn, dev):
         p = ctx[n]
         qg = proj[n, :nh * hdim * 2].reshape(nh, 2 * hdim)
         q, gate = qg[:, :hdim], qg[:, hdim:].reshape(-1)
-        q = hd.rms_norm(q, L.q_norm.cpu(), cfg.eps)
+        q = rms_norm(q, L.q_norm.cpu(), cfg.eps)
         inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, rd, 2).float() / rd))
         emb = torch.cat((p * inv, p * inv))
-        qr = q[:, :rd] * emb.cos() + hd._rotate_half(q[:, :rd]) * emb.sin()
+        qr = q[:, :rd] * emb.cos() + rotate_half(q[:, :rd]) * emb.sin()
         q = torch.cat((qr, q[:, rd:]), dim=-1)
         o = torch.zeros(nh, hdim)
         for h in range(nh):
@@ -82,8 +94,73 @@ def test_attention_layer_vs_fp32_reference(gdn, dev):
     # the new key / value landed at each slot's position and nowhere else
     kproj = proj[:, nh * hdim * 2:nh * hdim * 2 + kv * hdim].reshape(3, kv, hdim)
     for n in range(3):
-        k_ref = hd.rms_norm(kproj[n], L.k_norm.cpu(), cfg.eps)
+        k_ref = rms_norm(kproj[n], L.k_norm.cpu(), cfg.eps)
         assert rel_l2(kt[n, :, rd:, ctx[n]], k_ref[:, rd:]) <= 1e-2
+
+
+def _attn_reference(proj, pos, qn, kn, inv_freq, kt, vc, nh, kv, hd, rd, eps):
+    """Per-slot fp32 loop of HF Qwen3_5Attention at decode on the CPU; updates kt / vc in place."""
+    N = proj.shape[0]
+    out = torch.zeros(N, nh * hd)
+    for n in range(N):
+        p = int(pos[n])
+        emb = torch.cat((p * inv_freq, p * inv_freq))
+        cos, sin = emb.cos(), emb.sin()
+
+        def rope(t):
+            tr = t[..., :rd].float()
+            return torch.cat(((tr * cos + rotate_half(tr) * sin).to(t.dtype), t[..., rd:]), dim=-1)
+
+        qg = proj[n, :nh * 2 * hd].reshape(nh, 2 * hd)
+        q = rope(rms_norm(qg[:, :hd], qn, eps))
+        gate = qg[:, hd:].reshape(-1)
+        k = rope(rms_norm(proj[n, 2 * nh * hd:(2 * nh + kv) * hd].reshape(kv, hd), kn, eps))
+        v = proj[n, (2 * nh + kv) * hd:(2 * nh + 2 * kv) * hd].reshape(kv, hd)
+        kt[n, :, :, p] = k
+        vc[n, :, p, :] = v
+        o = torch.zeros(nh, hd)
+        for h in range(nh):
+            j = h // (nh // kv)
+            s = (q[h].float() @ kt[n, j, :, :p + 1].float()) * hd ** -0.5
+            o[h] = torch.softmax(s, -1) @ vc[n, j, :p + 1, :].float()
+        out[n] = (o.reshape(-1).to(torch.bfloat16) * torch.sigmoid(gate)).float()
+    return out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("nh,kv,hd,pos,T", [
+    (24, 4, 256, [0, 255, 256, 1300], 1304),   # 27B shape; split edges at 256 positions
+    (4, 2, 64, [5, 17, 9], 24),
+    (8, 1, 128, [700, 3], 704),
+    (2, 2, 128, [511, 515], 516),
+])
+def test_gqa_decode_attention_vs_fp32(gdn, dev, nh, kv, hd, pos, T):
+    """The three-launch decode attention (q/k norm, partial rotary, cache writes at each slot's
+    position, split softmax attention, gate) against a per-slot fp32 loop; the caches hold the new
+    key and value at each position and are unchanged elsewhere."""
+    from importlib import import_module
+    cb = import_module(PKG_NAME + ".cb_engine")
+    N, rd, eps = len(pos), hd // 4, 1e-6
+    g_ = torch.Generator().manual_seed(hd + nh + T)
+    bf = torch.bfloat16
+    proj = torch.randn(N, (2 * nh + 2 * kv) * hd, generator=g_).to(bf)
+    qn = (0.1 * torch.randn(hd, generator=g_)).to(bf)
+    kn = (0.1 * torch.randn(hd, generator=g_)).to(bf)
+    inv = 1.0 / (10000.0 ** (torch.arange(0, rd, 2).float() / rd))
+    kt = torch.randn(N, kv, hd, T, generator=g_).to(bf)
+    vc = torch.randn(N, kv, T, hd, generator=g_).to(bf)
+    pos_t = torch.tensor(pos, dtype=torch.int64)
+    kt_d, vc_d = kt.to(dev), vc.to(dev)
+    out = cb.gqa_decode_attention(proj.to(dev), pos_t.to(dev), qn.to(dev), kn.to(dev), inv.to(dev), kt_d, vc_d,
+                                  nh, kv, hd, rd, eps).cpu().float()
+    ref = _attn_reference(proj, pos_t, qn, kn, inv, kt, vc, nh, kv, hd, rd, eps)
+    assert rel_l2(out, ref) <= OUT_TOL
+    kt_g, vc_g = kt_d.cpu(), vc_d.cpu()
+    assert torch.equal(vc_g, vc)                       # values copied exactly, nothing else touched
+    for n, p in enumerate(pos):
+        assert rel_l2(kt_g[n, :, :, p], kt[n, :, :, p]) <= 1e-2
+        kt_g[n, :, :, p] = kt[n, :, :, p]
+    assert torch.equal(kt_g, kt)
 
 
 @pytest.mark.gpu
@@ -143,11 +220,11 @@ def test_add_rms_norm_vs_torch(gdn, dev, H):
     w = (0.02 * torch.randn(H, generator=g_)).to(torch.bfloat16)
     h2, x = cb.add_rms_norm(h.to(dev), d.to(dev), w.to(dev))
     assert torch.equal(h2.cpu(), h + d)
-    x_ref = hd.rms_norm(h + d, w, 1e-6)
+    x_ref = rms_norm(h + d, w, 1e-6)
     assert ((x.cpu().float() - x_ref.float()).abs() <= x_ref.float().abs() * 2 ** -7 + 1e-6).all()
     h3, x0 = cb.add_rms_norm(h.to(dev), None, w.to(dev))
     assert torch.equal(h3.cpu(), h)
-    assert rel_l2(x0, hd.rms_norm(h, w, 1e-6)) <= 1e-3
+    assert rel_l2(x0, rms_norm(h, w, 1e-6)) <= 1e-3
 
 
 @pytest.mark.gpu
