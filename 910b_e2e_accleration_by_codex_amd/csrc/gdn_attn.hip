@@ -158,7 +158,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const int64_t* __restri
     const int len4 = (len + 3) & ~3;  // <= T: T is a multiple of 4
     if (tl < len4) {
       const uint16_t* kp = kt + ((int64_t)n * kv + j) * HD * T + (int64_t)(QROWS * wid) * T + tl;
-#pragma unroll 8
+#pragma unroll 16
       for (int d = 0; d < QROWS; ++d) {
         const u16x4 k4 = *reinterpret_cast<const u16x4*>(kp + (int64_t)d * T);
         const int dd = QROWS * wid + d;
@@ -216,7 +216,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const int64_t* __restri
       for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
     const uint16_t* vp = vc + (((int64_t)n * kv + j) * T + t0) * HD + 8 * cg;
     const int cnt = len - t0 < SPLIT ? len - t0 : SPLIT;
-#pragma unroll 4
+#pragma unroll 8
     for (int t = rg; t < cnt; t += RG) {
       const u16x8 v8 = *reinterpret_cast<const u16x8*>(vp + (int64_t)t * HD);
 #pragma unroll

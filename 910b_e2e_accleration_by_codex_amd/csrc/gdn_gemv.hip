@@ -292,55 +292,54 @@ __device__ __forceinline__ float block_sum4(float v, float* red) {
   return red[0] + red[1] + red[2] + red[3];
 }
 
-// H % 8 == 0 with 16-byte aligned rows and H <= 256 * 8 * kMaxV: each thread issues all of its
-// 16-byte row pieces at once (a row is one memory round trip, not one per element) and keeps them
-// in registers for the output pass.
-template <int kMaxV>
-__global__ __launch_bounds__(256) void add_rmsnorm_vec_kernel(const uint16_t* h, const uint16_t* __restrict__ delta,
-                                                              const uint16_t* __restrict__ w, uint16_t* h_out,
-                                                              uint16_t* __restrict__ x_out, int H, float eps) {
-  __shared__ float red[4];
+// Row reductions of the add + norm kernels: 1024 threads, one 16-byte row piece each (H <= 8192).
+// Both kernels below sum the squares in this same order, so they give bit-identical norms.
+constexpr int kPartThreads = 1024;
+__device__ __forceinline__ float block_sum_1k(float v, float* red) {
+  v = wave_sum_fast(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < kPartThreads / 64; ++i) tot += red[i];
+  return tot;
+}
+
+// H % 8 == 0 with 16-byte aligned rows and H <= 8192: each thread loads its row piece once and keeps
+// it in registers for the output pass (a row is one memory round trip).
+__global__ __launch_bounds__(kPartThreads) void add_rmsnorm_vec_kernel(const uint16_t* h,
+                                                                       const uint16_t* __restrict__ delta,
+                                                                       const uint16_t* __restrict__ w, uint16_t* h_out,
+                                                                       uint16_t* __restrict__ x_out, int H, float eps) {
+  __shared__ float red[kPartThreads / 64];
   const int64_t base = (int64_t)blockIdx.x * H;
-  const int nv = H / 8;
-  u16x8v hv[kMaxV], dv[kMaxV];
+  const int v = threadIdx.x, nv = H / 8;
+  float x[8], ss = 0.f;
 #pragma unroll
-  for (int j = 0; j < kMaxV; ++j) {
-    const int v = threadIdx.x + 256 * j;
-    if (v < nv) {
-      hv[j] = *reinterpret_cast<const u16x8v*>(h + base + 8 * v);
-      if (delta) dv[j] = *reinterpret_cast<const u16x8v*>(delta + base + 8 * v);
-    }
-  }
-  float x[kMaxV][8], ss = 0.f;
-#pragma unroll
-  for (int j = 0; j < kMaxV; ++j) {
-    const int v = threadIdx.x + 256 * j;
+  for (int e = 0; e < 8; ++e) x[e] = 0.f;
+  if (v < nv) {
+    const u16x8v hv = *reinterpret_cast<const u16x8v*>(h + base + 8 * v);
+    u16x8v dv = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (delta) dv = *reinterpret_cast<const u16x8v*>(delta + base + 8 * v);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      float val = 0.f;
-      if (v < nv) {
-        val = bf2f(hv[j][e]);
-        if (delta) val = rbf(val + bf2f(dv[j][e]));
-      }
-      x[j][e] = val;
+      float val = bf2f(hv[e]);
+      if (delta) val = rbf(val + bf2f(dv[e]));
+      x[e] = val;
       ss += val * val;
     }
   }
-  const float inv = rsqrtf(block_sum4(ss, red) / (float)H + eps);
+  const float inv = rsqrtf(block_sum_1k(ss, red) / (float)H + eps);
+  if (v < nv) {
+    const u16x8v wv = *reinterpret_cast<const u16x8v*>(w + 8 * v);
+    u16x8v o, hn;
 #pragma unroll
-  for (int j = 0; j < kMaxV; ++j) {
-    const int v = threadIdx.x + 256 * j;
-    if (v < nv) {
-      const u16x8v wv = *reinterpret_cast<const u16x8v*>(w + 8 * v);
-      u16x8v o, hn;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        o[e] = f2bf(x[j][e] * inv * (1.0f + bf2f(wv[e])));
-        hn[e] = f2bf(x[j][e]);
-      }
-      *reinterpret_cast<u16x8v*>(x_out + base + 8 * v) = o;
-      if (delta) *reinterpret_cast<u16x8v*>(h_out + base + 8 * v) = hn;
+    for (int e = 0; e < 8; ++e) {
+      o[e] = f2bf(x[e] * inv * (1.0f + bf2f(wv[e])));
+      hn[e] = f2bf(x[e]);
     }
+    *reinterpret_cast<u16x8v*>(x_out + base + 8 * v) = o;
+    if (delta) *reinterpret_cast<u16x8v*>(h_out + base + 8 * v) = hn;
   }
 }
 
@@ -348,53 +347,46 @@ __global__ __launch_bounds__(256) void add_rmsnorm_vec_kernel(const uint16_t* h,
 // (part [splits][M][H], gdn_decode_linear_packed_partial): delta = bf16(sum over splits, in split
 // order) -- exactly what decode_linear_reduce_kernel would have stored -- so the reduction costs no
 // launch and no bf16 round trip.  The split loads of one row piece are issued together.
-template <int kMaxV>
-__global__ __launch_bounds__(256) void add_rmsnorm_part_kernel(const uint16_t* h, const float* __restrict__ part,
-                                                               int splits, int M, const uint16_t* __restrict__ w,
-                                                               uint16_t* h_out, uint16_t* __restrict__ x_out, int H,
-                                                               float eps) {
+__global__ __launch_bounds__(kPartThreads) void add_rmsnorm_part_kernel(const uint16_t* h,
+                                                                        const float* __restrict__ part, int splits,
+                                                                        int M, const uint16_t* __restrict__ w,
+                                                                        uint16_t* h_out, uint16_t* __restrict__ x_out,
+                                                                        int H, float eps) {
   typedef float f32x4v __attribute__((ext_vector_type(4)));
-  __shared__ float red[4];
+  __shared__ float red[kPartThreads / 64];
   const int64_t row = blockIdx.x, base = row * H;
-  const int nv = H / 8;
-  float x[kMaxV][8], ss = 0.f;
+  const int v = threadIdx.x, nv = H / 8;
+  float x[8], ss = 0.f;
 #pragma unroll
-  for (int j = 0; j < kMaxV; ++j) {
-    const int v = threadIdx.x + 256 * j;
+  for (int e = 0; e < 8; ++e) x[e] = 0.f;
+  if (v < nv) {
+    const u16x8v hv = *reinterpret_cast<const u16x8v*>(h + base + 8 * v);
+    f32x4v d0 = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
+    // the loads of 16 splits are issued before their in-order sums
+#pragma unroll 16
+    for (int sp = 0; sp < splits; ++sp) {
+      const float* pp = part + ((int64_t)sp * M + row) * H + 8 * v;
+      d0 += *reinterpret_cast<const f32x4v*>(pp);
+      d1 += *reinterpret_cast<const f32x4v*>(pp + 4);
+    }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) x[j][e] = 0.f;
-    if (v < nv) {
-      const u16x8v hv = *reinterpret_cast<const u16x8v*>(h + base + 8 * v);
-      f32x4v d0 = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-      for (int sp = 0; sp < splits; ++sp) {
-        const float* pp = part + ((int64_t)sp * M + row) * H + 8 * v;
-        d0 += *reinterpret_cast<const f32x4v*>(pp);
-        d1 += *reinterpret_cast<const f32x4v*>(pp + 4);
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float d = rbf(e < 4 ? d0[e] : d1[e - 4]);
-        x[j][e] = rbf(bf2f(hv[e]) + d);
-        ss += x[j][e] * x[j][e];
-      }
+    for (int e = 0; e < 8; ++e) {
+      const float d = rbf(e < 4 ? d0[e] : d1[e - 4]);
+      x[e] = rbf(bf2f(hv[e]) + d);
+      ss += x[e] * x[e];
     }
   }
-  const float inv = rsqrtf(block_sum4(ss, red) / (float)H + eps);
+  const float inv = rsqrtf(block_sum_1k(ss, red) / (float)H + eps);
+  if (v < nv) {
+    const u16x8v wv = *reinterpret_cast<const u16x8v*>(w + 8 * v);
+    u16x8v o, hn;
 #pragma unroll
-  for (int j = 0; j < kMaxV; ++j) {
-    const int v = threadIdx.x + 256 * j;
-    if (v < nv) {
-      const u16x8v wv = *reinterpret_cast<const u16x8v*>(w + 8 * v);
-      u16x8v o, hn;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        o[e] = f2bf(x[j][e] * inv * (1.0f + bf2f(wv[e])));
-        hn[e] = f2bf(x[j][e]);
-      }
-      *reinterpret_cast<u16x8v*>(x_out + base + 8 * v) = o;
-      *reinterpret_cast<u16x8v*>(h_out + base + 8 * v) = hn;
+    for (int e = 0; e < 8; ++e) {
+      o[e] = f2bf(x[e] * inv * (1.0f + bf2f(wv[e])));
+      hn[e] = f2bf(x[e]);
     }
+    *reinterpret_cast<u16x8v*>(x_out + base + 8 * v) = o;
+    *reinterpret_cast<u16x8v*>(h_out + base + 8 * v) = hn;
   }
 }
 
@@ -460,12 +452,9 @@ extern "C" int gdn_add_rmsnorm(const void* h, const void* delta, const void* w, 
   hipStream_t s = (hipStream_t)stream;
   const bool vec = H % 8 == 0 && aligned(h, 16) && aligned(w, 16) && aligned(x_out, 16) &&
                    (!delta || (aligned(delta, 16) && aligned(h_out, 16)));
-  if (vec && H <= 256 * 8 * 2)
-    add_rmsnorm_vec_kernel<2><<<M, 256, 0, s>>>((const uint16_t*)h, (const uint16_t*)delta, (const uint16_t*)w,
-                                                (uint16_t*)h_out, (uint16_t*)x_out, H, eps);
-  else if (vec && H <= 256 * 8 * 4)
-    add_rmsnorm_vec_kernel<4><<<M, 256, 0, s>>>((const uint16_t*)h, (const uint16_t*)delta, (const uint16_t*)w,
-                                                (uint16_t*)h_out, (uint16_t*)x_out, H, eps);
+  if (vec && H <= kPartThreads * 8)
+    add_rmsnorm_vec_kernel<<<M, kPartThreads, 0, s>>>((const uint16_t*)h, (const uint16_t*)delta, (const uint16_t*)w,
+                                                      (uint16_t*)h_out, (uint16_t*)x_out, H, eps);
   else
     add_rmsnorm_kernel<<<M, 256, 0, s>>>((const uint16_t*)h, (const uint16_t*)delta, (const uint16_t*)w,
                                          (uint16_t*)h_out, (uint16_t*)x_out, H, eps);
@@ -491,18 +480,14 @@ extern "C" int gdn_add_rmsnorm_partial(const void* h, const float* part, int spl
   clear_error();
   GDN_REQUIRE(h && part && w && h_out && x_out, "gdn_add_rmsnorm_partial: null pointer");
   GDN_REQUIRE(M >= 0 && splits >= 1, "gdn_add_rmsnorm_partial: bad sizes");
-  GDN_SUPPORT(H > 0 && H % 8 == 0 && H <= 256 * 8 * 4, "gdn_add_rmsnorm_partial: H=%d must be a multiple of 8 <= 8192",
+  GDN_SUPPORT(H > 0 && H % 8 == 0 && H <= kPartThreads * 8, "gdn_add_rmsnorm_partial: H=%d must be a multiple of 8 <= 8192",
               H);
   GDN_REQUIRE(aligned(h, 16) && aligned(part, 16) && aligned(w, 16) && aligned(h_out, 16) && aligned(x_out, 16),
               "gdn_add_rmsnorm_partial: rows must be 16-byte aligned");
   if (M == 0) return GDN_OK;
   hipStream_t s = (hipStream_t)stream;
-  if (H <= 256 * 8 * 2)
-    add_rmsnorm_part_kernel<2><<<M, 256, 0, s>>>((const uint16_t*)h, part, splits, M, (const uint16_t*)w,
-                                                 (uint16_t*)h_out, (uint16_t*)x_out, H, eps);
-  else
-    add_rmsnorm_part_kernel<4><<<M, 256, 0, s>>>((const uint16_t*)h, part, splits, M, (const uint16_t*)w,
-                                                 (uint16_t*)h_out, (uint16_t*)x_out, H, eps);
+  add_rmsnorm_part_kernel<<<M, kPartThreads, 0, s>>>((const uint16_t*)h, part, splits, M, (const uint16_t*)w,
+                                                     (uint16_t*)h_out, (uint16_t*)x_out, H, eps);
   return check_launch("gdn_add_rmsnorm_partial");
 }
 
