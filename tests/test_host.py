@@ -54,3 +54,20 @@ def test_patch_model_installs_functions(gdn):
         assert layer.norm.forward.__func__ is gdn.fused_gated_rmsnorm
     finally:
         M.torch_chunk_gated_delta_rule, M.torch_recurrent_gated_delta_rule, M.causal_conv1d_update = saved
+
+
+def test_decode_step_ops_refuse_cpu_tensors(gdn):
+    """The decode-step ops around the core (attention, residual add + norm) have no CPU path either."""
+    from importlib import import_module
+    from conftest import PKG_NAME
+    cb = import_module(PKG_NAME + ".cb_engine")
+    N, nh, kv, hd, T = 2, 4, 2, 64, 8
+    bf = torch.bfloat16
+    proj = torch.zeros(N, (2 * nh + 2 * kv) * hd, dtype=bf)
+    with pytest.raises(ValueError, match="no CPU fallback"):
+        cb.gqa_decode_attention(proj, torch.zeros(N, dtype=torch.int64), torch.zeros(hd, dtype=bf),
+                                torch.zeros(hd, dtype=bf), torch.ones(hd // 8), torch.zeros(N, kv, hd, T, dtype=bf),
+                                torch.zeros(N, kv, T, hd, dtype=bf), nh, kv, hd, hd // 4)
+    h = torch.zeros(N, 256, dtype=bf)
+    with pytest.raises(ValueError, match="no CPU fallback"):
+        cb.add_rms_norm(h, h, torch.zeros(256, dtype=bf))
