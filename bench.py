@@ -12,7 +12,7 @@ prefill layer, T=32768, and whole decode steps at Qwen3.5-27B shape (the hybrid 
 and its 48 GDN layers with projections) in tokens/s.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-prefill]
-                      [--only decode|prefill|prefill8192|hybrid]
+                      [--only decode|prefill|prefill8192|hybrid|attention]
 """
 import argparse
 import importlib
@@ -265,6 +265,39 @@ def cpu_baseline_decode(layers_cpu=LAYERS, reps=3):
                        f"{threads} threads")
 
 
+def bench_attention(gdn, dev, reps=3, seed=4):
+    """The decode attention of the hybrid stack's full-attention layers alone, at Qwen3.5-27B's
+    attention shape: 16 slots, 24 q / 4 kv heads of 256, quarter rotary, positions = contexts uniform
+    in [512, 4096].  Sixteen layers' KV caches are cycled so the cache reads come from HBM.  Bytes:
+    each slot's K and V at positions 0..pos (the kernels' algorithmic reads)."""
+    cb = importlib.import_module(PKG + ".cb_engine")
+    nh, kv, hd, rd, T, L = 24, 4, 256, 64, 4112, 16
+    g_ = torch.Generator().manual_seed(seed)
+    ctx = torch.randint(512, 4097, (N_SLOTS,), generator=g_)
+    bf = torch.bfloat16
+    proj = torch.randn(N_SLOTS, (2 * nh + 2 * kv) * hd, generator=g_).to(bf).to(dev)
+    qn = (0.1 * torch.randn(hd, generator=g_)).to(bf).to(dev)
+    kn = (0.1 * torch.randn(hd, generator=g_)).to(bf).to(dev)
+    inv = (1.0 / (10000.0 ** (torch.arange(0, rd, 2).float() / rd))).to(dev)
+    kts = [torch.randn(N_SLOTS, kv, hd, T, device=dev).to(bf) for _ in range(L)]
+    vcs = [torch.randn(N_SLOTS, kv, T, hd, device=dev).to(bf) for _ in range(L)]
+    pos = ctx.to(dev)
+    work = cb.attn_decode_workspace(N_SLOTS, nh, hd, T, dev)
+
+    def layers():
+        for i in range(L):
+            cb.gqa_decode_attention(proj, pos, qn, kn, inv, kts[i], vcs[i], nh, kv, hd, rd, 1e-6, work=work)
+
+    us = _time(layers, reps, dev) / L
+    nbytes = int((ctx.double() + 1).sum()) * kv * hd * 2 * 2
+    del kts, vcs
+    torch.cuda.empty_cache()
+    return {"workload": f"decode attention, 27B shape (24 q / 4 kv heads of 256), 16 slots, ctx U[512,4096] "
+                        f"(mean {float(ctx.double().mean()):.1f})",
+            "us_per_layer": round(us, 2), "kv_bytes_per_layer": nbytes,
+            "hbm_frac": round(nbytes / (us * 1e-6) / HBM_PEAK, 4)}
+
+
 def bench_hybrid(gdn, dev, steps=10, warmup=2, seed=4):
     """Whole decode steps at Qwen3.5-27B shape, 16 slots, contexts uniform in [512, 4096] with random
     GDN states and KV caches, HIP-graph replay (random-init bf16 weights):
@@ -323,7 +356,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill", "prefill8192", "hybrid"], default=None,
+    ap.add_argument("--only", choices=["decode", "prefill", "prefill8192", "hybrid", "attention"], default=None,
                     help="run one workload group (prefill8192: the T=8192 chunked rule alone, for profiling)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first run a 256 MiB device-to-device copy (counter calibration for rocprof)")
@@ -355,7 +388,9 @@ def main():
             res["prefill"][0]["cpu_baseline"] = cpu_baseline_prefill()
     if args.only in (None, "hybrid"):
         res["hybrid"] = bench_hybrid(gdn, dev)
-    if args.only in ("prefill", "prefill8192", "hybrid"):
+    if args.only in (None, "attention"):
+        res["hybrid"] = res.get("hybrid", []) + [bench_attention(gdn, dev, reps=args.steps if args.only else 3)]
+    if args.only in ("prefill", "prefill8192", "hybrid", "attention"):
         print(json.dumps({"secondary": res.get("prefill", []) + res.get("hybrid", [])}))
         return
     dec = res["decode"]
