@@ -23,10 +23,18 @@ namespace gdn {
 namespace at {
 constexpr int SPLIT = 256;   // tokens per split workgroup
 constexpr int THREADS = 256;
-typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
-typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 __host__ __device__ inline int64_t round256(int64_t b) { return (b + 255) / 256 * 256; }
+// Two bf16 values a, b (dwords holding two bf16 each) paired as (a.lo, b.lo) / (a.hi, b.hi).
+__device__ __forceinline__ uint32_t pair_lo(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
+__device__ __forceinline__ uint32_t pair_hi(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
+// acc + x.lo * y.lo + x.hi * y.hi (bf16 pairs, fp32 sum: v_dot2_f32_bf16).
+__device__ __forceinline__ float dot2_bf16(uint32_t x, uint32_t y, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x), __builtin_bit_cast(bf16x2, y), acc, false);
+}
 // workspace: q (fp32 [N, nh, hd]) | m, l (fp32 [N, nh, S, 2]) | partial o (fp32 [N, nh, S, hd])
 struct Work {
   float* q;
@@ -130,9 +138,9 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const int64_t* __restri
   constexpr int CG = HD / 8;          // 16-byte column groups of a V row
   constexpr int RG = THREADS / CG;    // token row groups in P V
   constexpr int QROWS = HD / 4;       // head dims per wave in the scores
-  __shared__ float qs[HD][G];                            // q of the G heads, dim-major
+  __shared__ uint32_t qp[HD / 2][G];                     // q of the G heads as bf16 pairs (dims 2i, 2i+1)
   __shared__ float big[(4 * G * SPLIT > RG * G * HD) ? 4 * G * SPLIT : RG * G * HD];
-  __shared__ float pl[SPLIT][G];                         // probabilities, token-major
+  __shared__ uint32_t pl[SPLIT / 2 * G];                 // bf16 probability pairs (positions 2i, 2i+1) per head
   __shared__ float red[2][4][G];
   const int split = blockIdx.x, j = blockIdx.y, n = blockIdx.z;
   const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
@@ -142,9 +150,10 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const int64_t* __restri
   if (t0 >= len) return;  // uniform over the workgroup
   const int S = splits_of(T);
   const int h0 = j * G;
-  for (int i = tid; i < G * HD; i += THREADS) {
-    const int g = i / HD, d = i % HD;
-    qs[d][g] = wk.q[((int64_t)n * nh + h0 + g) * HD + d];
+  for (int i = tid; i < G * HD / 2; i += THREADS) {  // q is bf16-exact: the pairs lose nothing
+    const int g = i / (HD / 2), dp = i % (HD / 2);
+    const float* qg = wk.q + ((int64_t)n * nh + h0 + g) * HD + 2 * dp;
+    qp[dp][g] = (uint32_t)f2bf(qg[0]) | ((uint32_t)f2bf(qg[1]) << 16);
   }
   __syncthreads();
   // ---- scores: wave wid sums dims [QROWS wid, QROWS wid + QROWS) for tokens t0 + 4 lane .. + 3
@@ -158,15 +167,19 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const int64_t* __restri
     const int len4 = (len + 3) & ~3;  // <= T: T is a multiple of 4
     if (tl < len4) {
       const uint16_t* kp = kt + ((int64_t)n * kv + j) * HD * T + (int64_t)(QROWS * wid) * T + tl;
-#pragma unroll 16
-      for (int d = 0; d < QROWS; ++d) {
-        const u16x4 k4 = *reinterpret_cast<const u16x4*>(kp + (int64_t)d * T);
-        const int dd = QROWS * wid + d;
+      // rows d, d + 1 at a time: per position the pair (k[d], k[d+1]) against q's pair, on v_dot2
+#pragma unroll 8
+      for (int d = 0; d < QROWS; d += 2) {
+        const u32x2 ka = *reinterpret_cast<const u32x2*>(kp + (int64_t)d * T);
+        const u32x2 kb = *reinterpret_cast<const u32x2*>(kp + (int64_t)(d + 1) * T);
+        const uint32_t kk[4] = {pair_lo(ka[0], kb[0]), pair_hi(ka[0], kb[0]), pair_lo(ka[1], kb[1]),
+                                pair_hi(ka[1], kb[1])};
+        const int dp = (QROWS * wid + d) >> 1;
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-          const float q = qs[dd][g];
+          const uint32_t q2 = qp[dp][g];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) acc[g][i] += q * bf2f(k4[i]);
+          for (int i = 0; i < 4; ++i) acc[g][i] = dot2_bf16(q2, kk[i], acc[g][i]);
         }
       }
     }
@@ -192,8 +205,9 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const int64_t* __restri
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const float m = fmaxf(fmaxf(red[0][0][g], red[0][1][g]), fmaxf(red[0][2][g], red[0][3][g]));
-    e[g] = valid ? expf(s[g] - m) : 0.f;
-    pl[tid][g] = e[g];
+    const uint16_t eb = f2bf(valid ? expf(s[g] - m) : 0.f);  // P V runs on bf16 probabilities
+    e[g] = bf2f(eb);
+    reinterpret_cast<uint16_t*>(pl)[((tid >> 1) * G + g) * 2 + (tid & 1)] = eb;
     const float l = wave_sum(e[g]);
     if (lane == 0) red[1][wid][g] = l;
   }
@@ -206,7 +220,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const int64_t* __restri
     ml[0] = m;
     ml[1] = l;
   }
-  // ---- P V: thread (rg, cg) sums tokens t0 + rg + RG i over dims 8 cg .. 8 cg + 7
+  // ---- P V: thread (rg, cg) sums position pairs (2 q, 2 q + 1), q = rg + RG i, over dims 8 cg .. 8 cg + 7
   {
     const int cg = tid % CG, rg = tid / CG;
     float acc[G][8];
@@ -216,14 +230,23 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const int64_t* __restri
       for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
     const uint16_t* vp = vc + (((int64_t)n * kv + j) * T + t0) * HD + 8 * cg;
     const int cnt = len - t0 < SPLIT ? len - t0 : SPLIT;
-#pragma unroll 8
-    for (int t = rg; t < cnt; t += RG) {
-      const u16x8 v8 = *reinterpret_cast<const u16x8*>(vp + (int64_t)t * HD);
+#pragma unroll 4
+    for (int q = rg; 2 * q < cnt; q += RG) {
+      // position 2q + 1 past the range reads the last valid row instead (its probability is 0)
+      const int t1 = 2 * q + 1 < cnt ? 2 * q + 1 : 2 * q;
+      const u32x4 va = *reinterpret_cast<const u32x4*>(vp + (int64_t)(2 * q) * HD);
+      const u32x4 vb = *reinterpret_cast<const u32x4*>(vp + (int64_t)t1 * HD);
+      uint32_t vv[8];
+#pragma unroll
+      for (int e2 = 0; e2 < 4; ++e2) {
+        vv[2 * e2] = pair_lo(va[e2], vb[e2]);
+        vv[2 * e2 + 1] = pair_hi(va[e2], vb[e2]);
+      }
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        const float pr = pl[t][g];
+        const uint32_t p2 = pl[q * G + g];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[g][i] += pr * bf2f(v8[i]);
+        for (int i = 0; i < 8; ++i) acc[g][i] = dot2_bf16(p2, vv[i], acc[g][i]);
       }
     }
     __syncthreads();  // every score read of `big` is done: reuse it for the row groups' sums
