@@ -278,9 +278,12 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const int64_t* __rest
   const int ns = (len + SPLIT - 1) / SPLIT, S = splits_of(T);
   const float* ml = wk.ml + ((int64_t)n * nh + h) * S * 2;
   const float* op = wk.o + ((int64_t)n * nh + h) * S * HD + d;
+  // the loads of 4 splits at a time are issued together (a slot has up to S splits)
   float M = -INFINITY;
+#pragma unroll 4
   for (int s = 0; s < ns; ++s) M = fmaxf(M, ml[2 * s]);
   float L = 0.f, o = 0.f;
+#pragma unroll 4
   for (int s = 0; s < ns; ++s) {
     const float f = expf(ml[2 * s] - M);
     L += ml[2 * s + 1] * f;
