@@ -289,7 +289,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const int64_t* __rest
     L += ml[2 * s + 1] * f;
     o += op[(int64_t)s * HD] * f;
   }
-  const float a = rbf(o / L);
+  const float a = ns > 0 ? rbf(o / L) : 0.f;  // a negative position attends to nothing: zero output
   const float gate = bf2f(proj[n * ps + (int64_t)h * 2 * HD + HD + d]);
   out[n * out_stride + (int64_t)h * HD + d] = f2bf(a * rbf(sigmoid_f(gate)));
 }

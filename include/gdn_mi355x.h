@@ -278,7 +278,8 @@ int gdn_swiglu_partial(const float* part, int splits, void* out, int M, int64_t 
  *   proj [N, proj_stride] bf16: per query head h its q (hd) then its gate (hd) at h * 2hd, then the
  *     kv key rows (hd each) at 2 nh hd, then the kv value rows at (2 nh + kv) hd.
  *   pos [N] int64 (device): the position of the new token; it is written to the caches there and
- *     attends to positions 0..pos (positions >= T are not written, the attended range is clamped).
+ *     attends to positions 0..pos.  The caller keeps 0 <= pos < T: a position >= T is not written and
+ *     the attended range is clamped to T; a negative position writes nothing and gives a zero output.
  *   q_norm_w, k_norm_w [hd] bf16 (the norm multiplies by 1 + w); inv_freq [rd / 2] fp32 (the rotary
  *     angle of pair i is float(pos) * inv_freq[i], applied to the first rd dims).
  *   k_cache_t [N, kv, hd, T] bf16 (K transposed), v_cache [N, kv, T, hd] bf16; T % 4 == 0.

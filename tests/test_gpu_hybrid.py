@@ -164,6 +164,31 @@ def test_gqa_decode_attention_vs_fp32(gdn, dev, nh, kv, hd, pos, T):
 
 
 @pytest.mark.gpu
+def test_gqa_decode_attention_negative_position(gdn, dev):
+    """A slot at position -1 attends to nothing: zero output and no cache write; the other slots are
+    unaffected."""
+    from importlib import import_module
+    cb = import_module(PKG_NAME + ".cb_engine")
+    nh, kv, hd, T, rd, eps = 4, 2, 64, 16, 16, 1e-6
+    g_ = torch.Generator().manual_seed(49)
+    bf = torch.bfloat16
+    proj = torch.randn(2, (2 * nh + 2 * kv) * hd, generator=g_).to(bf)
+    qn = (0.1 * torch.randn(hd, generator=g_)).to(bf)
+    kn = (0.1 * torch.randn(hd, generator=g_)).to(bf)
+    inv = 1.0 / (10000.0 ** (torch.arange(0, rd, 2).float() / rd))
+    kt = torch.randn(2, kv, hd, T, generator=g_).to(bf)
+    vc = torch.randn(2, kv, T, hd, generator=g_).to(bf)
+    kt_d, vc_d = kt.to(dev), vc.to(dev)
+    out = cb.gqa_decode_attention(proj.to(dev), torch.tensor([-1, 5], device=dev), qn.to(dev), kn.to(dev),
+                                  inv.to(dev), kt_d, vc_d, nh, kv, hd, rd, eps).cpu().float()
+    assert torch.equal(out[0], torch.zeros(nh * hd))
+    assert torch.equal(kt_d[0].cpu(), kt[0]) and torch.equal(vc_d[0].cpu(), vc[0])
+    ref = _attn_reference(proj[1:], torch.tensor([5]), qn, kn, inv, kt[1:].clone(), vc[1:].clone(), nh, kv, hd, rd,
+                          eps)
+    assert rel_l2(out[1:], ref) <= OUT_TOL
+
+
+@pytest.mark.gpu
 def test_hybrid_graph_replay_matches_eager(gdn, dev):
     """Three replays of the captured 4-layer hybrid step give the eager steps' logits and states."""
     hd = _hybrid(gdn)
