@@ -20,7 +20,7 @@
 #include "gdn_internal.h"
 
 namespace gdn {
-namespace at {
+namespace attn {
 constexpr int SPLIT = 256;   // tokens per split workgroup
 constexpr int THREADS = 256;
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -58,7 +58,7 @@ __host__ __device__ inline Work work_of(float* base, int N, int nh, int hd, int 
   w.o = reinterpret_cast<float*>(p);
   return w;
 }
-}  // namespace at
+}  // namespace attn
 
 // One wave per (slot n, row r): r < nh are query heads, nh <= r < nh + kv key heads.  Lane l holds
 // dims l + 64 e.  The rotary partner of dim d < rd is d +- rd / 2, exchanged through LDS.
@@ -132,9 +132,9 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(const uint16_t* __restri
 template <int HD, int G>
 __global__ __launch_bounds__(256) void attn_split_kernel(const int64_t* __restrict__ pos,
                                                          const uint16_t* __restrict__ kt,
-                                                         const uint16_t* __restrict__ vc, at::Work wk, int nh,
+                                                         const uint16_t* __restrict__ vc, attn::Work wk, int nh,
                                                          int kv, int T, float scale) {
-  using namespace at;
+  using namespace attn;
   constexpr int CG = HD / 8;          // 16-byte column groups of a V row
   constexpr int RG = THREADS / CG;    // token row groups in P V
   constexpr int QROWS = HD / 4;       // head dims per wave in the scores
@@ -269,9 +269,9 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const int64_t* __restri
 template <int HD>
 __global__ __launch_bounds__(256) void attn_combine_kernel(const int64_t* __restrict__ pos,
                                                            const uint16_t* __restrict__ proj, int64_t ps,
-                                                           at::Work wk, uint16_t* __restrict__ out,
+                                                           attn::Work wk, uint16_t* __restrict__ out,
                                                            int64_t out_stride, int nh, int T) {
-  using namespace at;
+  using namespace attn;
   const int n = blockIdx.x / nh, h = blockIdx.x % nh, d = threadIdx.x;
   const int64_t p = pos[n];
   const int len = (int)(p + 1 < T ? p + 1 : T);
@@ -296,12 +296,12 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const int64_t* __rest
 
 template <int HD, int G>
 static void launch_split(dim3 grid, hipStream_t st, const int64_t* pos, const uint16_t* kt, const uint16_t* vc,
-                         at::Work wk, int nh, int kv, int T, float scale) {
-  attn_split_kernel<HD, G><<<grid, at::THREADS, 0, st>>>(pos, kt, vc, wk, nh, kv, T, scale);
+                         attn::Work wk, int nh, int kv, int T, float scale) {
+  attn_split_kernel<HD, G><<<grid, attn::THREADS, 0, st>>>(pos, kt, vc, wk, nh, kv, T, scale);
 }
 template <int HD>
 static bool launch_split_g(int G, dim3 grid, hipStream_t st, const int64_t* pos, const uint16_t* kt,
-                           const uint16_t* vc, at::Work wk, int nh, int kv, int T, float scale) {
+                           const uint16_t* vc, attn::Work wk, int nh, int kv, int T, float scale) {
   switch (G) {
     case 1: launch_split<HD, 1>(grid, st, pos, kt, vc, wk, nh, kv, T, scale); return true;
     case 2: launch_split<HD, 2>(grid, st, pos, kt, vc, wk, nh, kv, T, scale); return true;
@@ -315,11 +315,11 @@ template <int HD>
 static int launch_all(const uint16_t* proj, int64_t ps, const int64_t* pos, const uint16_t* q_w, const uint16_t* k_w,
                       const float* inv_freq, uint16_t* kt, uint16_t* vc, uint16_t* out, int64_t os, float* work, int N,
                       int nh, int kv, int rd, int T, float eps, hipStream_t st) {
-  const at::Work wk = at::work_of(work, N, nh, HD, T);
+  const attn::Work wk = attn::work_of(work, N, nh, HD, T);
   const int64_t waves = (int64_t)N * (nh + kv);
   attn_prep_kernel<HD><<<(unsigned)((waves + 3) / 4), 256, 0, st>>>(proj, ps, pos, q_w, k_w, inv_freq, kt, vc, wk.q,
                                                                      N, nh, kv, rd, T, eps);
-  const dim3 grid(at::splits_of(T), kv, N);
+  const dim3 grid(attn::splits_of(T), kv, N);
   if (!launch_split_g<HD>(nh / kv, grid, st, pos, kt, vc, wk, nh, kv, T, 1.0f / sqrtf((float)HD)))
     return set_error(GDN_EUNSUP, "gdn_attn_decode: query heads per kv head must be 1, 2, 4, 6 or 8");
   attn_combine_kernel<HD><<<N * nh, HD, 0, st>>>(pos, proj, ps, wk, out, os, nh, T);
@@ -332,7 +332,7 @@ using namespace gdn;
 
 extern "C" int64_t gdn_attn_decode_workspace_bytes(int N, int nh, int hd, int T) {
   if (N < 0 || nh < 1 || hd < 1 || T < 1) return -1;
-  return at::work_bytes(N, nh, hd, T);
+  return attn::work_bytes(N, nh, hd, T);
 }
 
 extern "C" int gdn_attn_decode(const void* proj, int64_t proj_stride, const int64_t* pos, const void* q_norm_w,
@@ -348,8 +348,8 @@ extern "C" int gdn_attn_decode(const void* proj, int64_t proj_stride, const int6
   GDN_REQUIRE(T >= 4 && T % 4 == 0, "gdn_attn_decode: cache length must be a positive multiple of 4");
   GDN_REQUIRE(proj_stride >= (int64_t)(2 * nh + 2 * kv) * hd && out_stride >= (int64_t)nh * hd,
               "gdn_attn_decode: row strides too small");
-  GDN_REQUIRE(work_bytes >= at::work_bytes(N, nh, hd, T), "gdn_attn_decode: workspace too small (%lld bytes needed)",
-              (long long)at::work_bytes(N, nh, hd, T));
+  GDN_REQUIRE(work_bytes >= attn::work_bytes(N, nh, hd, T), "gdn_attn_decode: workspace too small (%lld bytes needed)",
+              (long long)attn::work_bytes(N, nh, hd, T));
   GDN_REQUIRE(aligned(k_cache_t, 8) && aligned(v_cache, 16) && aligned(work, 256) && aligned(pos, 8),
               "gdn_attn_decode: K cache 8-byte, V cache 16-byte, workspace 256-byte aligned");
   if (N == 0) return GDN_OK;
