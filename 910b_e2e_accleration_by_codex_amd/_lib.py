@@ -45,6 +45,8 @@ _SIGNATURES = {
     "gdn_swiglu_partial": ([_P, _I, _P, _I, _L, _P], _I),
     "gdn_attn_decode_workspace_bytes": ([_I, _I, _I, _I], _L),
     "gdn_attn_decode": ([_P, _L, _P, _P, _P, _P, _P, _P, _P, _L, _P, _L, _I, _I, _I, _I, _I, _I, _F, _P], _I),
+    "gdn_attn_decode_partial": ([_P, _I, _P, _P, _P, _P, _P, _P, _P, _L, _P, _L, _I, _I, _I, _I, _I, _I, _F, _P],
+                                _I),
     "gdn_conv_prefill": ([_P, _L, _P, _P, _P, _P, _P, _L, _P, _I, _I, _I, _I, _P], _I),
     "gdn_gating": ([_P, _P, _L, _P, _P, _P, _P, _L, _I, _P], _I),
     "gdn_decode_fused_masked": ([_P, _L, _P, _L, _P, _P, _L, _P, _P, _P, _P, _P, _P, _I, _F, _P, _P, _P, _I,

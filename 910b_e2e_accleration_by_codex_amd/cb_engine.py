@@ -281,13 +281,20 @@ def gqa_decode_attention(proj, pos, q_norm, k_norm, inv_freq, k_cache_t, v_cache
     projection: q/k Qwen3_5RMSNorm, partial rotary at each slot's position, K and V written into the
     per-slot cache (K transposed [N, kv, hd, T], V [N, kv, T, hd]) at ``pos``, softmax attention over
     positions 0..pos, times sigmoid(gate).  proj [N, (2 nh + 2 kv) hd] bf16 (per head q then gate, then
-    k, then v), pos [N] int64 on the device.  Returns the gated output [N, nh * hd] bf16 (o_proj's
+    k, then v), or that projection's Partials (decode_linear_partial: reduced here, no reduction
+    launch), pos [N] int64 on the device.  Returns the gated output [N, nh * hd] bf16 (o_proj's
     input).  Three HIP launches, capturable in a graph."""
+    nh, kv, hd = n_heads, kv_heads, head_dim
+    part = proj if isinstance(proj, Partials) else None
+    if part is not None:
+        if part.N != (2 * nh + 2 * kv) * hd:
+            raise ValueError("gqa_decode_attention: partials of a [(2 nh + 2 kv) hd]-wide projection expected")
+        proj = part.data[0]                      # device, dtype and row count for the checks below
     _lib.require_cuda(proj, pos, q_norm, k_norm, k_cache_t, v_cache)
     N = proj.shape[0]
-    nh, kv, hd = n_heads, kv_heads, head_dim
     T = k_cache_t.shape[-1]
-    if (proj.dtype != torch.bfloat16 or proj.stride(1) != 1 or pos.dtype != torch.int64 or pos.numel() != N
+    if ((proj.dtype != torch.bfloat16 and part is None) or proj.stride(1) != 1 or pos.dtype != torch.int64
+            or pos.numel() != N
             or tuple(k_cache_t.shape) != (N, kv, hd, T) or tuple(v_cache.shape) != (N, kv, T, hd)
             or not (k_cache_t.is_contiguous() and v_cache.is_contiguous())
             or k_cache_t.dtype != torch.bfloat16 or v_cache.dtype != torch.bfloat16):
@@ -299,9 +306,13 @@ def gqa_decode_attention(proj, pos, q_norm, k_norm, inv_freq, k_cache_t, v_cache
     if work is None:
         work = attn_decode_workspace(N, nh, hd, T, proj.device)
     out = torch.empty(N, nh * hd, dtype=torch.bfloat16, device=proj.device)
-    _lib.call("gdn_attn_decode", _lib.ptr(proj), proj.stride(0), _lib.ptr(pos.contiguous()), _lib.ptr(qn),
-              _lib.ptr(kn), _lib.ptr(inv), _lib.ptr(k_cache_t), _lib.ptr(v_cache), _lib.ptr(out), out.stride(0),
-              _lib.ptr(work), work.numel() * 4, N, nh, kv, hd, rotary_dim, T, float(eps), _lib.stream_of(proj))
+    rest = (_lib.ptr(pos.contiguous()), _lib.ptr(qn), _lib.ptr(kn), _lib.ptr(inv), _lib.ptr(k_cache_t),
+            _lib.ptr(v_cache), _lib.ptr(out), out.stride(0), _lib.ptr(work), work.numel() * 4, N, nh, kv, hd,
+            rotary_dim, T, float(eps), _lib.stream_of(proj))
+    if part is not None:
+        _lib.call("gdn_attn_decode_partial", _lib.ptr(part.data), part.splits, *rest)
+    else:
+        _lib.call("gdn_attn_decode", _lib.ptr(proj), proj.stride(0), *rest)
     return out
 
 

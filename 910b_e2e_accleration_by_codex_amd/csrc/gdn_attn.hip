@@ -58,13 +58,27 @@ __host__ __device__ inline Work work_of(float* base, int N, int nh, int hd, int 
   w.o = reinterpret_cast<float*>(p);
   return w;
 }
+// The fused projection's row n, column col: a bf16 matrix, or bf16(sum of fp32 split-K partials
+// [splits][N][width] in split order) -- the same value the reduced projection holds.
+struct Src {
+  const uint16_t* bf;
+  int64_t stride;
+  const float* part;
+  int splits, N;
+  int64_t width;
+  __device__ __forceinline__ float operator()(int n, int64_t col) const {
+    if (!part) return bf2f(bf[n * stride + col]);
+    float s = 0.f;
+    for (int sp = 0; sp < splits; ++sp) s += part[((int64_t)sp * N + n) * width + col];
+    return rbf(s);
+  }
+};
 }  // namespace attn
 
 // One wave per (slot n, row r): r < nh are query heads, nh <= r < nh + kv key heads.  Lane l holds
 // dims l + 64 e.  The rotary partner of dim d < rd is d +- rd / 2, exchanged through LDS.
 template <int HD>
-__global__ __launch_bounds__(256) void attn_prep_kernel(const uint16_t* __restrict__ proj, int64_t ps,
-                                                        const int64_t* __restrict__ pos,
+__global__ __launch_bounds__(256) void attn_prep_kernel(attn::Src proj, const int64_t* __restrict__ pos,
                                                         const uint16_t* __restrict__ q_w,
                                                         const uint16_t* __restrict__ k_w,
                                                         const float* __restrict__ inv_freq, uint16_t* __restrict__ kt,
@@ -78,13 +92,13 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(const uint16_t* __restri
   const int n = (int)(w / (nh + kv)), r = (int)(w % (nh + kv));
   const bool is_q = r < nh;
   const int j = r - nh;
-  const uint16_t* src = proj + n * ps + (is_q ? (int64_t)r * 2 * HD : (int64_t)2 * nh * HD + (int64_t)j * HD);
+  const int64_t src = is_q ? (int64_t)r * 2 * HD : (int64_t)2 * nh * HD + (int64_t)j * HD;  // row n's column
   const uint16_t* wt = is_q ? q_w : k_w;
   float x[E];
   float ss = 0.f;
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    x[e] = bf2f(src[lane + 64 * e]);
+    x[e] = proj(n, src + lane + 64 * e);
     ss += x[e] * x[e];
   }
   ss = wave_sum(ss);
@@ -116,13 +130,13 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(const uint16_t* __restri
 #pragma unroll
     for (int e = 0; e < E; ++e) q[lane + 64 * e] = x[e];
   } else if (p >= 0 && p < T) {
-    const uint16_t* vs = proj + n * ps + (int64_t)2 * nh * HD + (int64_t)kv * HD + (int64_t)j * HD;
+    const int64_t vs = (int64_t)2 * nh * HD + (int64_t)kv * HD + (int64_t)j * HD;
     uint16_t* kd = kt + ((int64_t)n * kv + j) * HD * T + p;
     uint16_t* vd = vc + (((int64_t)n * kv + j) * T + p) * HD;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
       kd[(int64_t)(lane + 64 * e) * T] = f2bf(x[e]);
-      vd[lane + 64 * e] = vs[lane + 64 * e];
+      vd[lane + 64 * e] = f2bf(proj(n, vs + lane + 64 * e));  // exact: the value is bf16
     }
   }
 }
@@ -267,8 +281,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(const int64_t* __restri
 
 // grid (N * nh), HD threads: thread d of (slot n, query head h).
 template <int HD>
-__global__ __launch_bounds__(256) void attn_combine_kernel(const int64_t* __restrict__ pos,
-                                                           const uint16_t* __restrict__ proj, int64_t ps,
+__global__ __launch_bounds__(256) void attn_combine_kernel(const int64_t* __restrict__ pos, attn::Src proj,
                                                            attn::Work wk, uint16_t* __restrict__ out,
                                                            int64_t out_stride, int nh, int T) {
   using namespace attn;
@@ -290,7 +303,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const int64_t* __rest
     o += op[(int64_t)s * HD] * f;
   }
   const float a = ns > 0 ? rbf(o / L) : 0.f;  // a negative position attends to nothing: zero output
-  const float gate = bf2f(proj[n * ps + (int64_t)h * 2 * HD + HD + d]);
+  const float gate = proj(n, (int64_t)h * 2 * HD + HD + d);
   out[n * out_stride + (int64_t)h * HD + d] = f2bf(a * rbf(sigmoid_f(gate)));
 }
 
@@ -312,17 +325,17 @@ static bool launch_split_g(int G, dim3 grid, hipStream_t st, const int64_t* pos,
   }
 }
 template <int HD>
-static int launch_all(const uint16_t* proj, int64_t ps, const int64_t* pos, const uint16_t* q_w, const uint16_t* k_w,
+static int launch_all(attn::Src proj, const int64_t* pos, const uint16_t* q_w, const uint16_t* k_w,
                       const float* inv_freq, uint16_t* kt, uint16_t* vc, uint16_t* out, int64_t os, float* work, int N,
                       int nh, int kv, int rd, int T, float eps, hipStream_t st) {
   const attn::Work wk = attn::work_of(work, N, nh, HD, T);
   const int64_t waves = (int64_t)N * (nh + kv);
-  attn_prep_kernel<HD><<<(unsigned)((waves + 3) / 4), 256, 0, st>>>(proj, ps, pos, q_w, k_w, inv_freq, kt, vc, wk.q,
-                                                                     N, nh, kv, rd, T, eps);
+  attn_prep_kernel<HD><<<(unsigned)((waves + 3) / 4), 256, 0, st>>>(proj, pos, q_w, k_w, inv_freq, kt, vc, wk.q, N,
+                                                                     nh, kv, rd, T, eps);
   const dim3 grid(attn::splits_of(T), kv, N);
   if (!launch_split_g<HD>(nh / kv, grid, st, pos, kt, vc, wk, nh, kv, T, 1.0f / sqrtf((float)HD)))
     return set_error(GDN_EUNSUP, "gdn_attn_decode: query heads per kv head must be 1, 2, 4, 6 or 8");
-  attn_combine_kernel<HD><<<N * nh, HD, 0, st>>>(pos, proj, ps, wk, out, os, nh, T);
+  attn_combine_kernel<HD><<<N * nh, HD, 0, st>>>(pos, proj, wk, out, os, nh, T);
   return check_launch("gdn_attn_decode");
 }
 
@@ -335,25 +348,23 @@ extern "C" int64_t gdn_attn_decode_workspace_bytes(int N, int nh, int hd, int T)
   return attn::work_bytes(N, nh, hd, T);
 }
 
-extern "C" int gdn_attn_decode(const void* proj, int64_t proj_stride, const int64_t* pos, const void* q_norm_w,
-                               const void* k_norm_w, const float* inv_freq, void* k_cache_t, void* v_cache,
-                               void* out, int64_t out_stride, float* work, int64_t work_bytes, int N, int nh, int kv,
-                               int hd, int rd, int T, float eps, void* stream) {
-  clear_error();
-  GDN_REQUIRE(proj && pos && q_norm_w && k_norm_w && k_cache_t && v_cache && out && work && (inv_freq || rd == 0),
-              "gdn_attn_decode: null pointer");
-  GDN_REQUIRE(N >= 0 && nh >= 1 && kv >= 1 && nh % kv == 0, "gdn_attn_decode: bad head counts");
-  GDN_SUPPORT(hd == 64 || hd == 128 || hd == 256, "gdn_attn_decode: head_dim must be 64, 128 or 256");
-  GDN_REQUIRE(rd >= 0 && rd <= hd && rd % 2 == 0, "gdn_attn_decode: rotary dims must be even and <= head_dim");
-  GDN_REQUIRE(T >= 4 && T % 4 == 0, "gdn_attn_decode: cache length must be a positive multiple of 4");
-  GDN_REQUIRE(proj_stride >= (int64_t)(2 * nh + 2 * kv) * hd && out_stride >= (int64_t)nh * hd,
-              "gdn_attn_decode: row strides too small");
-  GDN_REQUIRE(work_bytes >= attn::work_bytes(N, nh, hd, T), "gdn_attn_decode: workspace too small (%lld bytes needed)",
+namespace {
+int attn_entry(const char* name, attn::Src src, const int64_t* pos, const void* q_norm_w, const void* k_norm_w,
+               const float* inv_freq, void* k_cache_t, void* v_cache, void* out, int64_t out_stride, float* work,
+               int64_t work_bytes, int N, int nh, int kv, int hd, int rd, int T, float eps, void* stream) {
+  GDN_REQUIRE(pos && q_norm_w && k_norm_w && k_cache_t && v_cache && out && work && (inv_freq || rd == 0),
+              "%s: null pointer", name);
+  GDN_REQUIRE(N >= 0 && nh >= 1 && kv >= 1 && nh % kv == 0, "%s: bad head counts", name);
+  GDN_SUPPORT(hd == 64 || hd == 128 || hd == 256, "%s: head_dim must be 64, 128 or 256", name);
+  GDN_REQUIRE(rd >= 0 && rd <= hd && rd % 2 == 0, "%s: rotary dims must be even and <= head_dim", name);
+  GDN_REQUIRE(T >= 4 && T % 4 == 0, "%s: cache length must be a positive multiple of 4", name);
+  GDN_REQUIRE(out_stride >= (int64_t)nh * hd, "%s: output row stride too small", name);
+  GDN_REQUIRE(work_bytes >= attn::work_bytes(N, nh, hd, T), "%s: workspace too small (%lld bytes needed)", name,
               (long long)attn::work_bytes(N, nh, hd, T));
   GDN_REQUIRE(aligned(k_cache_t, 8) && aligned(v_cache, 16) && aligned(work, 256) && aligned(pos, 8),
-              "gdn_attn_decode: K cache 8-byte, V cache 16-byte, workspace 256-byte aligned");
+              "%s: K cache 8-byte, V cache 16-byte, workspace 256-byte aligned", name);
   if (N == 0) return GDN_OK;
-  const auto* P = static_cast<const uint16_t*>(proj);
+  src.N = N;
   const auto* qw = static_cast<const uint16_t*>(q_norm_w);
   const auto* kw = static_cast<const uint16_t*>(k_norm_w);
   auto* kt = static_cast<uint16_t*>(k_cache_t);
@@ -361,8 +372,32 @@ extern "C" int gdn_attn_decode(const void* proj, int64_t proj_stride, const int6
   auto* o = static_cast<uint16_t*>(out);
   const hipStream_t st = (hipStream_t)stream;
   switch (hd) {
-    case 64: return launch_all<64>(P, proj_stride, pos, qw, kw, inv_freq, kt, vc, o, out_stride, work, N, nh, kv, rd, T, eps, st);
-    case 128: return launch_all<128>(P, proj_stride, pos, qw, kw, inv_freq, kt, vc, o, out_stride, work, N, nh, kv, rd, T, eps, st);
-    default: return launch_all<256>(P, proj_stride, pos, qw, kw, inv_freq, kt, vc, o, out_stride, work, N, nh, kv, rd, T, eps, st);
+    case 64: return launch_all<64>(src, pos, qw, kw, inv_freq, kt, vc, o, out_stride, work, N, nh, kv, rd, T, eps, st);
+    case 128: return launch_all<128>(src, pos, qw, kw, inv_freq, kt, vc, o, out_stride, work, N, nh, kv, rd, T, eps, st);
+    default: return launch_all<256>(src, pos, qw, kw, inv_freq, kt, vc, o, out_stride, work, N, nh, kv, rd, T, eps, st);
   }
+}
+}  // namespace
+
+extern "C" int gdn_attn_decode(const void* proj, int64_t proj_stride, const int64_t* pos, const void* q_norm_w,
+                               const void* k_norm_w, const float* inv_freq, void* k_cache_t, void* v_cache,
+                               void* out, int64_t out_stride, float* work, int64_t work_bytes, int N, int nh, int kv,
+                               int hd, int rd, int T, float eps, void* stream) {
+  clear_error();
+  GDN_REQUIRE(proj, "gdn_attn_decode: null pointer");
+  GDN_REQUIRE(proj_stride >= (int64_t)(2 * nh + 2 * kv) * hd, "gdn_attn_decode: projection row stride too small");
+  const attn::Src src{static_cast<const uint16_t*>(proj), proj_stride, nullptr, 0, N, 0};
+  return attn_entry("gdn_attn_decode", src, pos, q_norm_w, k_norm_w, inv_freq, k_cache_t, v_cache, out, out_stride,
+                    work, work_bytes, N, nh, kv, hd, rd, T, eps, stream);
+}
+
+extern "C" int gdn_attn_decode_partial(const float* part, int splits, const int64_t* pos, const void* q_norm_w,
+                                       const void* k_norm_w, const float* inv_freq, void* k_cache_t, void* v_cache,
+                                       void* out, int64_t out_stride, float* work, int64_t work_bytes, int N, int nh,
+                                       int kv, int hd, int rd, int T, float eps, void* stream) {
+  clear_error();
+  GDN_REQUIRE(part && splits >= 1 && aligned(part, 4), "gdn_attn_decode_partial: bad partials");
+  const attn::Src src{nullptr, 0, part, splits, N, (int64_t)(2 * nh + 2 * kv) * hd};
+  return attn_entry("gdn_attn_decode_partial", src, pos, q_norm_w, k_norm_w, inv_freq, k_cache_t, v_cache, out,
+                    out_stride, work, work_bytes, N, nh, kv, hd, rd, T, eps, stream);
 }

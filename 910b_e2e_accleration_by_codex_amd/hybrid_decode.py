@@ -130,7 +130,7 @@ class HybridDecoder:
     def attention(self, L, x, partial=False):
         cfg = self.cfg
         nh, kv, hd = cfg.attn_heads, cfg.kv_heads, cfg.attn_head
-        proj = decode_linear(x, L.qkv_p)   # per head q | gate, then k, then v
+        proj = decode_linear_partial(x, L.qkv_p)   # per head q | gate, then k, then v: split-K partials
         # q/k norms, partial rotary, the cache writes at each slot's position, softmax attention and
         # the sigmoid gate: three HIP launches
         o = gqa_decode_attention(proj, self.pos, L.q_norm, L.k_norm, self.inv_freq, L.kt, L.v, nh, kv, hd,

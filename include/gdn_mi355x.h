@@ -292,6 +292,13 @@ int gdn_attn_decode(const void* proj, int64_t proj_stride, const int64_t* pos, c
                     const void* k_norm_w, const float* inv_freq, void* k_cache_t, void* v_cache, void* out,
                     int64_t out_stride, float* work, int64_t work_bytes, int N, int nh, int kv, int hd, int rd, int T,
                     float eps, void* stream);
+/* The same with the projection given as its split-K partial sums (gdn_decode_linear_packed_partial):
+ * part [splits][N][(2 nh + 2 kv) hd] fp32; every value is bf16(sum over splits, in split order), as in
+ * the reduced projection, so the result is identical and the reduction launch disappears. */
+int gdn_attn_decode_partial(const float* part, int splits, const int64_t* pos, const void* q_norm_w,
+                            const void* k_norm_w, const float* inv_freq, void* k_cache_t, void* v_cache, void* out,
+                            int64_t out_stride, float* work, int64_t work_bytes, int N, int nh, int kv, int hd, int rd,
+                            int T, float eps, void* stream);
 
 #ifdef __cplusplus
 }

@@ -164,6 +164,32 @@ def test_gqa_decode_attention_vs_fp32(gdn, dev, nh, kv, hd, pos, T):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("nh,kv,hd,H", [(4, 2, 64, 512), (24, 4, 256, 5120)])
+def test_gqa_decode_attention_from_partials(gdn, dev, nh, kv, hd, H):
+    """The attention fed the q|gate|k|v projection's split-K partials gives exactly what it gives on the
+    reduced projection: the same output and the same cache writes."""
+    from importlib import import_module
+    cb = import_module(PKG_NAME + ".cb_engine")
+    g_ = torch.Generator().manual_seed(50)
+    bf = torch.bfloat16
+    N, T, rd = 16, 520, hd // 4
+    x = torch.randn(N, H, generator=g_).to(bf).to(dev)
+    w = cb.PackedWeight((0.05 * torch.randn((2 * nh + 2 * kv) * hd, H, generator=g_)).to(bf).to(dev))
+    qn = (0.1 * torch.randn(hd, generator=g_)).to(bf).to(dev)
+    kn = (0.1 * torch.randn(hd, generator=g_)).to(bf).to(dev)
+    inv = (1.0 / (10000.0 ** (torch.arange(0, rd, 2).float() / rd))).to(dev)
+    kt = torch.randn(N, kv, hd, T, generator=g_).to(bf).to(dev)
+    vc = torch.randn(N, kv, T, hd, generator=g_).to(bf).to(dev)
+    pos = torch.randint(0, T, (N,), generator=g_).to(dev)
+    p = cb.decode_linear_partial(x, w)
+    assert p.splits > 1
+    kt1, vc1, kt2, vc2 = kt.clone(), vc.clone(), kt.clone(), vc.clone()
+    o1 = cb.gqa_decode_attention(cb.decode_linear(x, w), pos, qn, kn, inv, kt1, vc1, nh, kv, hd, rd)
+    o2 = cb.gqa_decode_attention(p, pos, qn, kn, inv, kt2, vc2, nh, kv, hd, rd)
+    assert torch.equal(o1, o2) and torch.equal(kt1, kt2) and torch.equal(vc1, vc2)
+
+
+@pytest.mark.gpu
 def test_gqa_decode_attention_negative_position(gdn, dev):
     """A slot at position -1 attends to nothing: zero output and no cache write; the other slots are
     unaffected."""
