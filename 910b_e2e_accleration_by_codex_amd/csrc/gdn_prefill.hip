@@ -844,14 +844,22 @@ __device__ __forceinline__ void chain_read_k(KFrags& fk, const uint8_t* ring, in
 #pragma unroll
   for (int f = 0; f < 8; ++f) fk[f] = lds_frag_h(ring + rg::KT, 8 * HALF + f, lane);
 }
+// Bounded waits: `limit` polls, then the wait gives up and raises the device status word (read
+// back by gdn_device_status), so a broken invariant neither hangs the GPU nor passes silently.
+struct WaitCtl {
+  int limit;
+  int* status;
+};
 // Wait until the other chain wave has published step `target` (it always publishes before it waits
 // itself, so the wait ends; the bound only keeps a broken invariant from hanging the GPU).  Program
 // order suffices after it for the same reason as in set_flag.
-__device__ __forceinline__ void wait_flag(int* flag, int target) {
-  for (int i = 0; i < (1 << 18); ++i) {
+__device__ __forceinline__ void wait_flag(int* flag, int target, const WaitCtl& wc, int lane) {
+  int i = 0;
+  for (; i < wc.limit; ++i) {
     const int v = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     if (__builtin_amdgcn_readfirstlane(v) == target) break;
   }
+  if (i == wc.limit && lane == 0) __hip_atomic_fetch_or(wc.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   asm volatile("" ::: "memory");  // the partial-sum reads stay behind the flag read
 }
 // Publish step `value` after this wave's earlier LDS writes.  LDS performs a CU's operations in one
@@ -1053,7 +1061,8 @@ struct Swap {
 };
 template <int HALF>
 __device__ __forceinline__ void chain_step(ScanSmem& sm, f32x4 (&S)[4], bf16x8 (&Sb)[2], ChainIn& in, KFrags& fk,
-                                           KFrags& fk_next, int c, int nch, int& x0, const Swap& sw, int lane) {
+                                           KFrags& fk_next, int c, int nch, int& x0, const Swap& sw,
+                                           const WaitCtl& wc, int lane) {
   uint8_t* xch = sm.xch[x0];
   const int x1 = x0 == 2 ? 0 : x0 + 1;
   const uint8_t* nxt = sm.ring[x1];  // chunk c+1 sits in ring slot (c+1) % 3
@@ -1083,7 +1092,7 @@ __device__ __forceinline__ void chain_step(ScanSmem& sm, f32x4 (&S)[4], bf16x8 (
     S[i] *= gl;
     asm volatile("" : "+v"(S[i]));  // done while the other wave finishes its half
   }
-  wait_flag(&sm.flag[1 - HALF], c + 1);
+  wait_flag(&sm.flag[1 - HALF], c + 1, wc, lane);
   // vn = U - W S: both waves add the same two partial sums (a + b == b + a exactly)
   f32x4 vn[4];
 #pragma unroll
@@ -1179,7 +1188,8 @@ __device__ __forceinline__ void chain_step(ScanSmem& sm, f32x4 (&S)[4], bf16x8 (
 template <int HALF>
 __device__ __forceinline__ void chain_wave(ScanSmem& sm, const float* __restrict__ init,
                                            float* __restrict__ final_state, int Hv, int h, int col,
-                                           const SeqTable& tab, int s_lo, int s_hi, int nch, int lane) {
+                                           const SeqTable& tab, int s_lo, int s_hi, int nch, const WaitCtl& wc,
+                                           int lane) {
   using namespace pf;
   const int g4 = lane >> 4;
   auto state_col = [&](const float* base, int row) -> const float* {  // this lane's column of a state
@@ -1221,11 +1231,11 @@ __device__ __forceinline__ void chain_wave(ScanSmem& sm, const float* __restrict
   };
   int x0 = 0;  // c % 3
   for (int c = 0; c < nch; c += 2) {
-    chain_step<HALF>(sm, S, Sb, in, fk0, fk1, c, nch, x0, swap_of(), lane);
+    chain_step<HALF>(sm, S, Sb, in, fk0, fk1, c, nch, x0, swap_of(), wc, lane);
     w = wn;
     walk_next(wn, tab, s_hi);
     if (c + 1 < nch) {
-      chain_step<HALF>(sm, S, Sb, in, fk1, fk0, c + 1, nch, x0, swap_of(), lane);
+      chain_step<HALF>(sm, S, Sb, in, fk1, fk0, c + 1, nch, x0, swap_of(), wc, lane);
       w = wn;
       walk_next(wn, tab, s_hi);
     }
@@ -1242,7 +1252,7 @@ __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(
     const float* __restrict__ init, float* __restrict__ final_state, OutT* __restrict__ out,
     const int32_t* __restrict__ cu, const int32_t* __restrict__ seq_chunk0, const int32_t* __restrict__ rows,
     int n_rows, int nseq, int seq_len, int Hqk, int Hv, int groups, int64_t total_chunks,
-    const uint8_t* __restrict__ work) {
+    const uint8_t* __restrict__ work, WaitCtl wc) {
   using namespace pf;
   __shared__ ScanSmem sm;
   // block -> (group-head pair, slice); the 8 slices of a pair share blockIdx % 8 and therefore an
@@ -1272,8 +1282,8 @@ __global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(
 
   if (role < 2) {
     // ---------------- chain waves ----------------
-    if (role == 0) chain_wave<0>(sm, init, final_state, Hv, h, col, tab, s_lo, s_hi, nch, lane);
-    else chain_wave<1>(sm, init, final_state, Hv, h, col, tab, s_lo, s_hi, nch, lane);
+    if (role == 0) chain_wave<0>(sm, init, final_state, Hv, h, col, tab, s_lo, s_hi, nch, wc, lane);
+    else chain_wave<1>(sm, init, final_state, Hv, h, col, tab, s_lo, s_hi, nch, wc, lane);
   } else if (role < 4) {
     // ---------------- output waves: step c computes chunk c-1 ----------------
     if (role == 2) output_wave<0, OutT>(sm, rec0, rstride, kq_off, out, tab, s_lo, s_hi, nch, Hv, h, 16 * n, lane);
@@ -1502,9 +1512,52 @@ __global__ void gating_kernel(const uint16_t* __restrict__ a, const uint16_t* __
   g[i] = -expf(A_log[h]) * softplus_f(bf2f(a[r * ab_stride + h]) + dt_bias[h]);
 }
 
+// Status word of the bounded waits (bit 0: a wait gave up), one per device.
+__device__ int g_wait_status;
+
 }  // namespace gdn
 
 using namespace gdn;
+
+namespace {
+constexpr int kDefaultWaitLimit = 1 << 18;
+int g_wait_limit = kDefaultWaitLimit;
+// Device address of g_wait_status on the current device (looked up once per device); null on failure.
+int* wait_status_ptr() {
+  static int* cached[64] = {nullptr};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  if (!cached[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_wait_status)) != hipSuccess) return nullptr;
+    cached[dev] = (int*)p;
+  }
+  return cached[dev];
+}
+}  // namespace
+
+extern "C" int gdn_device_status(int clear) {
+  clear_error();
+  int* p = wait_status_ptr();
+  if (!p) return set_error(GDN_ELAUNCH, "gdn_device_status: no device status word on the current device");
+  int v = 0;
+  if (hipMemcpy(&v, p, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess)
+    return set_error(GDN_ELAUNCH, "gdn_device_status: reading the status word failed");
+  if (clear) {
+    const int zero = 0;
+    if (hipMemcpy(p, &zero, sizeof(int), hipMemcpyHostToDevice) != hipSuccess)
+      return set_error(GDN_ELAUNCH, "gdn_device_status: clearing the status word failed");
+  }
+  if (v) return set_error(GDN_EWAIT, "a bounded inter-wave wait of the chunked prefill gave up: the outputs and "
+                                     "final states of the calls since the last status check are wrong");
+  return GDN_OK;
+}
+
+extern "C" int gdn_set_wait_limit(int64_t polls) {
+  clear_error();
+  g_wait_limit = polls < 0 ? kDefaultWaitLimit : (polls > (1ll << 30) ? (1 << 30) : (int)polls);
+  return GDN_OK;
+}
 
 extern "C" int gdn_unit_lower_inv(const float* X, float* T, int64_t batch, int n, void* stream) {
   clear_error();
@@ -1594,12 +1647,14 @@ extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const voi
   // Sequence groups: when the Hv x 8 workgroups of one group leave CUs free, split the sequences
   // into as many groups (balanced by chunks) as fill the CUs once; each workgroup then streams its
   // group's sequences back to back.  Otherwise one sequence per workgroup.
+  const WaitCtl wc{g_wait_limit, wait_status_ptr()};
+  if (!wc.status) return set_error(GDN_ELAUNCH, "gdn_chunk_prefill: no device status word on the current device");
   const int groups = scan_groups(nseq, Hv);
   const int64_t pairs = (int64_t)groups * Hv;
   const int64_t scan_blocks = (pairs + 7) / 8 * 64;
   chunk_scan_kernel<uint16_t><<<(unsigned)scan_blocks, kScanThreads, 0, s>>>(
       initial_state, final_state, (uint16_t*)out, cu_seqlens, seq_chunk0, state_rows, n_rows, nseq, seq_len, Hqk,
-      Hv, groups, total_chunks, work);
+      Hv, groups, total_chunks, work, wc);
   return check_launch("gdn_chunk_prefill(state)");
 }
 

@@ -5,8 +5,10 @@ signature is HF's ``torch_chunk_gated_delta_rule`` (HF modeling_qwen3_5.py:249-2
 (src/gdn_chunk_fast2.py:11) runs the same kernel (gdn_chunk_fast2.py).  Semantics kept: q, k are
 l2-normalised in their own dtype when ``use_qk_l2norm_in_kernel``, q is scaled by d^-1/2, the
 sequence is processed in chunks of 64 with an fp32 running state, the output has query's dtype and
-the final state is fp32.  ``chunk_size`` only changes fp32 rounding in the reference (every chunk
-size computes the same recurrence); the kernel always uses 64-token chunks.
+the final state is fp32.  Supported subset of the reference's arguments: chunk_size 64, bf16
+query/key/value, head dim 128 (the kernels' bf16 MFMA tiles); anything else raises ValueError
+before any GPU work (the reference also takes fp32 inputs, other head dims and chunk sizes --
+every chunk size computes the same recurrence, so a caller passes 64).
 Added beyond the reference: ``cu_seqlens`` (int32 [n_seq+1]) for packed varlen batches
 ([1, sum T, H, d] inputs, [n_seq, H_v, d, d] states), the form HF forwards as ``cu_seq_lens_q``.
 
@@ -114,6 +116,24 @@ def _check_rows(state_rows, nseq, n_rows, device):
     return Rows(state_rows, nseq, n_rows, device).dev
 
 
+SUPPORTED = "chunk_size 64, bfloat16 query/key/value, head dim 128"
+
+
+def check_chunk_args(query, key, value, chunk_size):
+    """The supported subset of the reference's arguments (src/gdn_chunk_fast2.py:11-19 accepts any
+    float dtype, head dim and chunk size): the kernels take 64-token chunks of bf16 q/k/v with
+    head dim 128 (bf16 MFMA operands).  Anything else raises ValueError before any GPU work."""
+    if chunk_size != CHUNK:
+        raise ValueError(f"chunk_gated_delta_rule: chunk_size={chunk_size} is not supported ({SUPPORTED}); "
+                         f"every chunk size computes the same recurrence, call it with chunk_size=64")
+    if not (query.dtype == key.dtype == value.dtype == torch.bfloat16):
+        raise ValueError(f"chunk_gated_delta_rule: query/key/value dtypes {query.dtype}/{key.dtype}/{value.dtype} "
+                         f"are not supported ({SUPPORTED})")
+    if query.dim() != 4 or query.shape[-1] != 128 or value.shape[-1] != 128:
+        raise ValueError(f"chunk_gated_delta_rule: head dim {query.shape[-1]} / {value.shape[-1]} is not supported "
+                         f"({SUPPORTED})")
+
+
 def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size=64, initial_state=None,
                            output_final_state=False, use_qk_l2norm_in_kernel=False, cu_seqlens=None,
                            state_rows=None, final_state_out=None, **kwargs):
@@ -125,11 +145,8 @@ def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size=64, initial_st
     live in slot buffers -- ``initial_state`` (or None = zero) and ``final_state_out`` are fp32
     [n_rows, Hv, d, d], sequence s uses row state_rows[s], and the two may be the same tensor; the
     final state is then written there and returned."""
-    if chunk_size <= 0:
-        raise ValueError("chunk_size must be positive")
+    check_chunk_args(query, key, value, chunk_size)
     _lib.require_cuda(query, key, value, g, beta, initial_state)
-    if key.dtype != query.dtype or value.dtype != query.dtype:
-        raise TypeError("chunk_gated_delta_rule: query, key and value must share a dtype")
     B, T, Hqk, D = query.shape
     Hv = value.shape[2]
     if key.shape != query.shape or tuple(value.shape) != (B, T, Hv, D):

@@ -29,7 +29,8 @@ enum {
   GDN_OK = 0,
   GDN_EINVAL = 1,   /* bad shape, dtype, stride, alignment or null pointer */
   GDN_EUNSUP = 2,   /* valid but not supported by this build (e.g. head_dim != 128) */
-  GDN_ELAUNCH = 3   /* the HIP launch failed; the message carries hipGetErrorString */
+  GDN_ELAUNCH = 3,  /* the HIP launch failed; the message carries hipGetErrorString */
+  GDN_EWAIT = 4     /* a kernel's bounded wait gave up (gdn_device_status): results are wrong */
 };
 
 /* Library version (major*10000 + minor*100 + patch). */
@@ -40,6 +41,23 @@ const char* gdn_last_error(void);
 
 /* Limits of this build: writes head_dim (128), max value heads per key head, max conv kernel. */
 int gdn_limits(int* head_dim, int* max_group_ratio, int* max_conv_kernel);
+
+/*
+ * Device status of the current device: GDN_OK, or GDN_EWAIT when a kernel's bounded inter-wave
+ * wait (the chunked prefill's two-wave state chain) gave up since the last clearing check -- the
+ * outputs and final states of the calls launched since then are wrong.  clear != 0 resets the
+ * status.  Waits for the device (a synchronous copy of one word): call it where a check is wanted,
+ * not inside stream capture.  No reference counterpart: the reference's device ops have no bounded
+ * waits (fail-loud contract of src/cb_engine.py:327).
+ */
+int gdn_device_status(int clear);
+
+/*
+ * Poll bound of the kernels' bounded waits for launches that follow (default 262144 polls;
+ * polls < 0 restores the default).  A small bound makes a wait give up while every kernel still
+ * runs to its end: it exists to test the status plumbing.
+ */
+int gdn_set_wait_limit(int64_t polls);
 
 /*
  * Single-token recurrent gated delta rule (decode), fp32 state.

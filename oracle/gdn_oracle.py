@@ -27,9 +27,12 @@ How each function is pinned (tests/test_oracle.py):
                                  ``causal_conv1d_update`` within bf16 rounding; state shift exact.
   causal_conv1d_prefill       -- equals repeated decode updates from a zero / given history.
   gated_rmsnorm               -- HF ``Qwen3_5RMSNormGated`` module, bit-exact.
-  gdn_gating                  -- closed form in float64.
-  gdn_decode_core / gdn_prefill_core -- compositions of the above; chunked prefill of a sequence
-                                 followed by decode equals decode of every token.
+  gdn_gating, expand_key_heads, gdn_decode_core, gdn_prefill_core
+                              -- transformers' own ``Qwen3_5GatedDeltaNet.forward`` (the layer the
+                                 reference patches) fed the same weights: a fresh prompt, a continued
+                                 prompt and cached decode steps, outputs and both states; planted
+                                 mistakes (a/b swapped, q/k split swapped, h % r head map, z heads
+                                 permuted) are caught.  gdn_gating also against float64.
 """
 import torch
 import torch.nn.functional as F
@@ -38,7 +41,7 @@ __all__ = [
     "l2norm", "small_unit_lower_inv", "unit_lower_inv", "chunk_gated_delta_rule_v1",
     "chunk_gated_delta_rule_v2", "chunk_gated_delta_rule_varlen", "recurrent_gated_delta_rule",
     "recurrent_single_step", "elem_conv_update", "causal_conv1d_update", "causal_conv1d_prefill",
-    "gated_rmsnorm", "gdn_gating", "gdn_decode_core", "gdn_prefill_core",
+    "gated_rmsnorm", "gdn_gating", "expand_key_heads", "gdn_decode_core", "gdn_prefill_core",
 ]
 
 
@@ -336,6 +339,12 @@ def gdn_gating(a, b, A_log, dt_bias):
     return beta, g
 
 
+def expand_key_heads(x, r):
+    """[.., H_k, d] -> [.., H_k * r, d] with value head h reading key head h // r
+    (``repeat_interleave(r, dim=2)``, src/cb_engine.py:339-342, HF:499-502)."""
+    return x.repeat_interleave(r, dim=2) if r > 1 else x
+
+
 def gdn_decode_core(mixed_qkv, z, a, b, conv_state, conv_weight, A_log, dt_bias, norm_weight,
                     rec_state, num_k_heads, num_v_heads, head_dim, eps=1e-6, conv_bias=None):
     """The GDN decode layer between the input projections and out_proj:
@@ -353,9 +362,7 @@ def gdn_decode_core(mixed_qkv, z, a, b, conv_state, conv_weight, A_log, dt_bias,
     value = value.reshape(n, 1, -1, head_dim)
     beta, g = gdn_gating(a.reshape(n, 1, -1), b.reshape(n, 1, -1), A_log, dt_bias)
     r = num_v_heads // num_k_heads
-    if r > 1:
-        query = query.repeat_interleave(r, dim=2)
-        key = key.repeat_interleave(r, dim=2)
+    query, key = expand_key_heads(query, r), expand_key_heads(key, r)
     core, new_rs = recurrent_single_step(query, key, value, g, beta, rec_state, True, True)
     rec_state.copy_(new_rs.to(rec_state.dtype))
     core = gated_rmsnorm(core.reshape(-1, head_dim), z.reshape(-1, head_dim), norm_weight, eps)
@@ -388,9 +395,7 @@ def gdn_prefill_core(mixed_qkv, z, a, b, conv_weight, A_log, dt_bias, norm_weigh
         key = key.reshape(1, L, -1, head_dim)
         value = value.reshape(1, L, -1, head_dim)
         beta, g = gdn_gating(a[lo:hi].unsqueeze(0), b[lo:hi].unsqueeze(0), A_log, dt_bias)
-        if r > 1:
-            query = query.repeat_interleave(r, dim=2)
-            key = key.repeat_interleave(r, dim=2)
+        query, key = expand_key_heads(query, r), expand_key_heads(key, r)
         init = None if initial_state is None else initial_state[s:s + 1]
         core, last = chunk_gated_delta_rule_v2(query, key, value, g, beta, chunk_size, init, True, True)
         core = gated_rmsnorm(core.reshape(-1, head_dim), z[lo:hi].reshape(-1, head_dim),

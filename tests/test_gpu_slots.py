@@ -1,6 +1,10 @@
 """GPU tests of the continuous-batching slot paths: prefill whose conv and recurrent states go
-straight into slot rows (fresh and continuation chunks, src/cb_tp.py:153-263), and the masked
-decode step that leaves held slots untouched (src/cb_tp.py:274-285)."""
+straight into slot rows (fresh and continuation chunks, src/cb_engine.py:198-205,
+src/cb_tp.py:153-263), and the masked decode step that leaves held slots untouched
+(src/cb_tp.py:274-285).  Each path is checked against the oracle's compositions on the same inputs
+(outputs rel-L2 <= 1e-2, fp32 states <= 1e-3, conv states bit for bit), and against the plain HIP
+call for the properties of the slot layout itself (rows written bit-identical to the plain call's
+states, other rows untouched)."""
 import pytest
 import torch
 
@@ -29,8 +33,12 @@ def _params(seed):
     return cw, A_log, dt, nw
 
 
+def _cpu(*ts):
+    return [t.cpu() for t in ts]
+
+
 @pytest.mark.gpu
-def test_prefill_into_slot_rows(gdn, dev):
+def test_prefill_into_slot_rows(gdn, oracle, dev):
     """3 packed prompts into slots [5, 0, 3] of an 8-slot engine: those rows equal the plain call's
     states bit for bit, every other row is untouched."""
     cu = torch.tensor([0, 70, 198, 231], dtype=torch.int32)
@@ -53,11 +61,17 @@ def test_prefill_into_slot_rows(gdn, dev):
         assert torch.equal(conv_slots[r], conv_ref[i]) and torch.equal(rec_slots[r], rec_ref[i])
     for r in (1, 2, 4, 6, 7):
         assert torch.equal(conv_slots[r], conv0[r]) and torch.equal(rec_slots[r], rec0[r])
+    # the oracle's composition (src/cb_tp.py:153-181 per prompt) on the same inputs
+    o_core, o_conv, o_rec = oracle.gdn_prefill_core(*_cpu(mixed, z, a, b, cw, A_log, dt, nw), Hk, Hv, D,
+                                                    cu_seqlens=cu)
+    assert rel_l2(core, o_core) <= OUT_TOL
+    for i, r in enumerate([5, 0, 3]):
+        assert torch.equal(conv_slots[r].cpu(), o_conv[i]) and rel_l2(rec_slots[r], o_rec[i]) <= STATE_TOL
 
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("split", [1, 2, 64, 100])
-def test_prefill_continuation_through_slots(gdn, dev, split):
+def test_prefill_continuation_through_slots(gdn, oracle, dev, split):
     """A prompt prefilled in two chunks through its slot row (the second chunk reads the conv history
     and recurrent state the first left there, src/cb_tp.py:230-263) matches one pass."""
     T = 150
@@ -77,10 +91,19 @@ def test_prefill_continuation_through_slots(gdn, dev, split):
     assert torch.equal(conv_slots[2], conv_ref[0])  # the conv window is pure data movement
     assert rel_l2(core, core_ref) <= OUT_TOL and rel_l2(rec_slots[2], rec_ref[0]) <= STATE_TOL
     assert torch.count_nonzero(conv_slots[[0, 1, 3]]) == 0 and torch.count_nonzero(rec_slots[[0, 1, 3]]) == 0
+    # the oracle's continuation (src/cb_tp.py:230-263): the second chunk starts from the first's conv
+    # window and recurrent state
+    xs = _cpu(mixed, z, a, b)
+    ps = _cpu(cw, A_log, dt, nw)
+    c1, cs1, rs1 = oracle.gdn_prefill_core(*(x[:split] for x in xs), *ps, Hk, Hv, D)
+    c2, cs2, rs2 = oracle.gdn_prefill_core(*(x[split:] for x in xs), *ps, Hk, Hv, D, conv_history=cs1,
+                                           initial_state=rs1)
+    assert rel_l2(parts[0], c1) <= OUT_TOL and rel_l2(parts[1], c2) <= OUT_TOL
+    assert torch.equal(conv_slots[2].cpu(), cs2[0]) and rel_l2(rec_slots[2], rs2[0]) <= STATE_TOL
 
 
 @pytest.mark.gpu
-def test_decode_masked_slots(gdn, dev):
+def test_decode_masked_slots(gdn, oracle, dev):
     """A dense decode step with held slots: held rows keep their conv and recurrent state bit for bit
     and output zeros; active rows equal the unmasked step's."""
     N = 5
@@ -100,3 +123,10 @@ def test_decode_masked_slots(gdn, dev):
         else:
             assert torch.count_nonzero(o[n]) == 0
             assert torch.equal(cs[n], conv0[n]) and torch.equal(rs[n], rec0[n])
+    # the active rows against the oracle's decode layer on those rows alone
+    act = [n for n in range(N) if active[n]]
+    c_o, r_o = conv0[act].cpu(), rec0[act].cpu()
+    o_o = oracle.gdn_decode_core(*(x[act].cpu() for x in (mixed, z, a, b)), c_o, *_cpu(cw, A_log, dt, nw), r_o,
+                                 Hk, Hv, D)
+    assert rel_l2(o[act], o_o) <= OUT_TOL
+    assert torch.equal(cs[act].cpu(), c_o) and rel_l2(rs[act], r_o) <= STATE_TOL

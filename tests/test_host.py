@@ -71,3 +71,22 @@ def test_decode_step_ops_refuse_cpu_tensors(gdn):
     h = torch.zeros(N, 256, dtype=bf)
     with pytest.raises(ValueError, match="no CPU fallback"):
         cb.add_rms_norm(h, h, torch.zeros(256, dtype=bf))
+
+
+def test_chunk_rule_refuses_unsupported_arguments(gdn):
+    """chunk_size != 64, non-bf16 q/k/v and head dims other than 128 raise a ValueError naming the
+    supported subset, before any device work (the reference's v2 accepts them, src/gdn_chunk_fast2.py:11-19)."""
+    bf = torch.bfloat16
+    q = torch.zeros(1, 4, 2, 128, dtype=bf)
+    g = torch.zeros(1, 4, 2)
+    for fn in (gdn.fast_chunk_gated_delta_rule, gdn.fast_chunk_gated_delta_rule_v2):
+        with pytest.raises(ValueError, match="chunk_size=128 is not supported"):
+            fn(q, q, q, g, g, chunk_size=128)
+        qf = q.float()
+        with pytest.raises(ValueError, match="dtypes .* are not supported"):
+            fn(qf, qf, qf, g, g)
+        with pytest.raises(ValueError, match="dtypes .* are not supported"):
+            fn(q, q, qf, g, g)
+        q64 = torch.zeros(1, 4, 2, 64, dtype=bf)
+        with pytest.raises(ValueError, match="head dim 64"):
+            fn(q64, q64, q64, g, g)
