@@ -1515,6 +1515,10 @@ __global__ void gating_kernel(const uint16_t* __restrict__ a, const uint16_t* __
 // Status word of the bounded waits (bit 0: a wait gave up), one per device.
 __device__ int g_wait_status;
 
+// Workspace of gdn_chunk_prefill_noalloc: one static array per device (host code reaches it only
+// through the address hipGetSymbolAddress returns on that device).
+static __device__ __align__(256) uint8_t scratch[GDN_NOALLOC_SCRATCH_BYTES];
+
 }  // namespace gdn
 
 using namespace gdn;
@@ -1535,6 +1539,19 @@ int* wait_status_ptr() {
   return cached[dev];
 }
 }  // namespace
+
+// Device address of `scratch` on the current device, looked up once per device (null on failure).
+static uint8_t* scratch_ptr() {
+  static uint8_t* cached[64] = {nullptr};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  if (!cached[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+    cached[dev] = (uint8_t*)p;
+  }
+  return cached[dev];
+}
 
 extern "C" int gdn_device_status(int clear) {
   clear_error();
@@ -1668,6 +1685,28 @@ extern "C" int gdn_chunk_prefill(const void* q, int64_t q_stride, const void* k,
                                 final_state, nullptr, nseq, out, total_tokens, cu_seqlens, seq_chunk0, total_chunks,
                                 nseq, seq_len, Hqk, Hv, D, in_dtype, use_qk_l2norm, workspace, workspace_bytes,
                                 stream);
+}
+
+extern "C" int gdn_chunk_prefill_noalloc(const void* q, int64_t q_stride, const void* k, int64_t k_stride,
+                                         const void* v, int64_t v_stride, const float* g, const void* beta,
+                                         int beta_dtype, const float* initial_state, float* final_state,
+                                         const int32_t* state_rows, int n_rows, void* out, int64_t total_tokens,
+                                         const int32_t* cu_seqlens, const int32_t* seq_chunk0, int64_t total_chunks,
+                                         int nseq, int seq_len, int Hqk, int Hv, int D, int in_dtype,
+                                         int use_qk_l2norm, void* stream) {
+  clear_error();
+  GDN_REQUIRE(total_chunks >= 0 && Hv > 0, "gdn_chunk_prefill_noalloc: bad sizes");
+  const int64_t need = gdn_chunk_prefill_workspace_bytes(total_chunks, Hv);
+  GDN_REQUIRE(need <= GDN_NOALLOC_SCRATCH_BYTES,
+              "gdn_chunk_prefill_noalloc: the call needs %lld bytes of workspace, the static scratch holds %lld "
+              "(%lld chunks x %d value heads is too many; use gdn_chunk_prefill_rows with a workspace)",
+              (long long)need, (long long)GDN_NOALLOC_SCRATCH_BYTES, (long long)total_chunks, Hv);
+  uint8_t* ws_ptr = scratch_ptr();
+  if (!ws_ptr) return set_error(GDN_ELAUNCH, "gdn_chunk_prefill_noalloc: no static scratch on the current device");
+  return gdn_chunk_prefill_rows(q, q_stride, k, k_stride, v, v_stride, g, beta, beta_dtype, initial_state,
+                                final_state, state_rows, n_rows, out, total_tokens, cu_seqlens, seq_chunk0,
+                                total_chunks, nseq, seq_len, Hqk, Hv, D, in_dtype, use_qk_l2norm, ws_ptr,
+                                GDN_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 extern "C" int gdn_conv_prefill_rows(const void* x, int64_t x_stride, const void* weight, const void* bias,

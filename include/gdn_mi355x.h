@@ -218,6 +218,27 @@ int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const void* k, int64
                            int use_qk_l2norm, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * gdn_chunk_prefill_rows without a workspace argument and without any allocation: the kernels'
+ * workspace is a static device array of GDN_NOALLOC_SCRATCH_BYTES (64 MiB) that the library holds on
+ * every GPU it runs on until the process ends.  A call whose
+ * gdn_chunk_prefill_workspace_bytes(total_chunks, Hv) exceeds it is rejected with GDN_EINVAL before
+ * any launch (64 MiB holds 900 (chunk, value head) records, e.g. 1792 tokens at Hv = 32).  Every
+ * call on one GPU shares that GPU's array: calls that overlap on one GPU (other streams, other host
+ * threads) race and give wrong results -- order them on one stream.  The array needs no clearing
+ * (every record a call reads, the same call writes first).
+ * No counterpart in the reference: for callers that cannot allocate (code under HIP graph capture,
+ * serving loops, harnesses that forbid hipMalloc).
+ */
+#define GDN_NOALLOC_SCRATCH_BYTES (64ll << 20)
+int gdn_chunk_prefill_noalloc(const void* q, int64_t q_stride, const void* k, int64_t k_stride,
+                              const void* v, int64_t v_stride, const float* g, const void* beta,
+                              int beta_dtype, const float* initial_state, float* final_state,
+                              const int32_t* state_rows, int n_rows, void* out, int64_t total_tokens,
+                              const int32_t* cu_seqlens, const int32_t* seq_chunk0, int64_t total_chunks,
+                              int nseq, int seq_len, int Hqk, int Hv, int D, int in_dtype,
+                              int use_qk_l2norm, void* stream);
+
+/*
  * gdn_conv_prefill with history and decode conv state in slot rows [n_rows, C, K] bf16: sequence
  * s reads its history from row state_rows[s] and writes its new state there (rows outside
  * [0, n_rows): zero history, no state).  history and state_out may be the same buffer.
