@@ -24,8 +24,6 @@ _SIGNATURES = {
     "gdn_version": ([], _I),
     "gdn_last_error": ([], ctypes.c_char_p),
     "gdn_limits": ([_P, _P, _P], _I),
-    "gdn_device_status": ([_I], _I),
-    "gdn_set_wait_limit": ([_L], _I),
     "gdn_recurrent_step": ([_P, _L, _P, _L, _P, _L, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P], _I),
     "gdn_conv_update": ([_P, _L, _P, _P, _P, _P, _L, _I, _I, _I, _P], _I),
     "gdn_gated_rmsnorm": ([_P, _L, _P, _L, _P, _I, _P, _L, _I, _F, _P], _I),
@@ -34,7 +32,7 @@ _SIGNATURES = {
     "gdn_unit_lower_inv": ([_P, _P, _L, _I, _P], _I),
     "gdn_chunk_prefill": ([_P, _L, _P, _L, _P, _L, _P, _P, _I, _P, _P, _P, _L, _P, _P, _L, _I, _I, _I, _I,
                            _I, _I, _I, _P, _L, _P], _I),
-    "gdn_chunk_prefill_workspace_bytes": ([_L, _I], _L),
+    "gdn_chunk_prefill_workspace_bytes": ([_L, _I, _I], _L),
     "gdn_decode_linear_workspace_bytes": ([_I, _L, _L], _L),
     "gdn_decode_linear": ([_P, _L, _P, _L, _P, _L, _I, _L, _L, _P, _L, _P], _I),
     "gdn_decode_linear_packed_elems": ([_L, _L], _L),
@@ -98,22 +96,6 @@ def call(name, *args):
     if rc != 0:
         msg = lib().gdn_last_error().decode(errors="replace")
         raise GDNError(f"{name} failed (code {rc}): {msg}")
-
-
-GDN_EWAIT = 4
-
-
-def check_device_status(clear=True):
-    """Raise GDNError if a kernel's bounded wait gave up on the current device since the last check
-    (the results of the calls launched since then are wrong); ``clear`` resets the status.  Waits for
-    the device."""
-    call("gdn_device_status", int(bool(clear)))
-
-
-def set_wait_limit(polls=-1):
-    """Poll bound of the kernels' bounded waits (negative: the default).  For tests of the status
-    plumbing only."""
-    call("gdn_set_wait_limit", int(polls))
 
 
 def stream_of(t):

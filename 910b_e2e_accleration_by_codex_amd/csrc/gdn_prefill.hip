@@ -90,71 +90,87 @@ __device__ __forceinline__ void st16_f32(float* M, int ld, f32x4 acc, int lane) 
 __device__ __forceinline__ float* inv_scratch(float* sX, int k) {
   return sX + (k == 3 ? 16 * pf::LDF + 32 : 16 * (k + 1));
 }
-__device__ void unit_lower_inv64(float* sX, float* sT, int w, int lane) {
+// The inverse in five barrier-free phases for waves 0-3 (the caller puts a workgroup barrier
+// between consecutive phases): the diagonal blocks, then the two merge levels in two steps each.
+// Phase 0: diagonal block w: T = (I+X)(I+X^2)(I+X^4)(I+X^8) (X^16 = 0), six fp32 MFMA products.
+__device__ __forceinline__ void inv64_diag(float* sX, float* sT, int w, int lane) {
   using namespace pf;
-  {  // diagonal block w: T = (I+X)(I+X^2)(I+X^4)(I+X^8) (X^16 = 0), six fp32 MFMA products
-    const int c = lane & 15, g = lane >> 4;
-    const float* Xb = sX + 16 * w * LDF + 16 * w;
-    float* Tb = sT + 16 * w * LDF + 16 * w;
-    float* P = inv_scratch(sX, w);  // wave-private 16x16 scratch
+  const int c = lane & 15, g = lane >> 4;
+  const float* Xb = sX + 16 * w * LDF + 16 * w;
+  float* Tb = sT + 16 * w * LDF + 16 * w;
+  float* P = inv_scratch(sX, w);  // wave-private 16x16 scratch
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = 4 * g + r;
-      Tb[i * LDF + c] = Xb[i * LDF + c] + (i == c ? 1.0f : 0.0f);
-    }
-    const float* Pin = Xb;
-    const int ldp = LDF;
+  for (int r = 0; r < 4; ++r) {
+    const int i = 4 * g + r;
+    Tb[i * LDF + c] = Xb[i * LDF + c] + (i == c ? 1.0f : 0.0f);
+  }
+  const float* Pin = Xb;
+  const int ldp = LDF;
 #pragma unroll
-    for (int step = 0; step < 3; ++step) {
-      f32x4 p2 = mm16_f32(Pin, ldp, Pin, ldp, f32x4{0.f, 0.f, 0.f, 0.f}, lane);  // X^(2^(step+1))
-      st16_f32(P, LDF, p2, lane);
-      __builtin_amdgcn_wave_barrier();
-      f32x4 tp = mm16_f32(Tb, LDF, P, LDF, f32x4{0.f, 0.f, 0.f, 0.f}, lane);    // T X^(2^(step+1))
+  for (int step = 0; step < 3; ++step) {
+    f32x4 p2 = mm16_f32(Pin, ldp, Pin, ldp, f32x4{0.f, 0.f, 0.f, 0.f}, lane);  // X^(2^(step+1))
+    st16_f32(P, LDF, p2, lane);
+    __builtin_amdgcn_wave_barrier();
+    f32x4 tp = mm16_f32(Tb, LDF, P, LDF, f32x4{0.f, 0.f, 0.f, 0.f}, lane);    // T X^(2^(step+1))
 #pragma unroll
-      for (int r = 0; r < 4; ++r) Tb[(4 * g + r) * LDF + c] += tp[r];
-      __builtin_amdgcn_wave_barrier();
-      Pin = P;
-    }
-    float* Trow = sT + 16 * w * LDF;
-    for (int col = 16 * (w + 1) + c; col < CH; col += 16)
+    for (int r = 0; r < 4; ++r) Tb[(4 * g + r) * LDF + c] += tp[r];
+    __builtin_amdgcn_wave_barrier();
+    Pin = P;
+  }
+  float* Trow = sT + 16 * w * LDF;
+  for (int col = 16 * (w + 1) + c; col < CH; col += 16)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) Trow[(4 * g + r) * LDF + col] = 0.f;
-  }
+    for (int r = 0; r < 4; ++r) Trow[(4 * g + r) * LDF + col] = 0.f;
+}
+// Phase 1: Y = X10 T00 (wave 0), X32 T22 (wave 1).
+__device__ __forceinline__ void inv64_merge1a(float* sX, float* sT, int w, int lane) {
+  using namespace pf;
+  if (w >= 2) return;
+  const int b0 = 32 * w;  // block row/col offsets: rows b0+16.., cols b0..
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  acc = mm16_f32(sX + (b0 + 16) * LDF + b0, LDF, sT + b0 * LDF + b0, LDF, acc, lane);
+  st16_f32(inv_scratch(sX, w), LDF, acc, lane);
+}
+// Phase 2: T10 = T11 Y (wave 0), T32 = T33 Y (wave 1).
+__device__ __forceinline__ void inv64_merge1b(float* sX, float* sT, int w, int lane) {
+  using namespace pf;
+  if (w >= 2) return;
+  const int b0 = 32 * w;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  acc = mm16_f32(sT + (b0 + 16) * LDF + b0 + 16, LDF, inv_scratch(sX, w), LDF, acc, lane);
+  st16_f32(sT + (b0 + 16) * LDF + b0, LDF, acc, lane);
+}
+// Phase 3: Y20 = X20 T00 + X21 T10, Y30 = X30 T00 + X31 T10, Y21 = X21 T11, Y31 = X31 T11.
+__device__ __forceinline__ void inv64_merge2a(float* sX, float* sT, int w, int lane) {
+  using namespace pf;
+  const int ib = 2 + (w & 1), jb = w >> 1;  // wave 0: Y20, 1: Y30, 2: Y21, 3: Y31
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  if (jb == 0) acc = mm16_f32(sX + 16 * ib * LDF + 0, LDF, sT + 0 * LDF + 0, LDF, acc, lane);
+  acc = mm16_f32(sX + 16 * ib * LDF + 16, LDF, sT + 16 * LDF + 16 * jb, LDF, acc, lane);
+  st16_f32(inv_scratch(sX, w), LDF, acc, lane);
+}
+// Phase 4: T20 = T22 Y20, T30 = T32 Y20 + T33 Y30, T21 = T22 Y21, T31 = T32 Y21 + T33 Y31.
+__device__ __forceinline__ void inv64_merge2b(float* sX, float* sT, int w, int lane) {
+  using namespace pf;
+  const int ib = 2 + (w & 1), jb = w >> 1;
+  const float* Ya = inv_scratch(sX, 2 * jb);      // Y2jb
+  const float* Yb = inv_scratch(sX, 2 * jb + 1);  // Y3jb
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  acc = mm16_f32(sT + 16 * ib * LDF + 32, LDF, Ya, LDF, acc, lane);
+  if (ib == 3) acc = mm16_f32(sT + 48 * LDF + 48, LDF, Yb, LDF, acc, lane);
+  st16_f32(sT + 16 * ib * LDF + 16 * jb, LDF, acc, lane);
+}
+// All 4 waves of a 256-thread workgroup: the phases with a barrier after each.
+__device__ void unit_lower_inv64(float* sX, float* sT, int w, int lane) {
+  inv64_diag(sX, sT, w, lane);
   __syncthreads();
-  // level 1: T10 = T11 (X10 T00), T32 = T33 (X32 T22)
-  float* Y = inv_scratch(sX, w);
-  if (w < 2) {
-    const int b0 = 32 * w;  // block row/col offsets: rows b0+16.., cols b0..
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    acc = mm16_f32(sX + (b0 + 16) * LDF + b0, LDF, sT + b0 * LDF + b0, LDF, acc, lane);
-    st16_f32(Y, LDF, acc, lane);
-  }
+  inv64_merge1a(sX, sT, w, lane);
   __syncthreads();
-  if (w < 2) {
-    const int b0 = 32 * w;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    acc = mm16_f32(sT + (b0 + 16) * LDF + b0 + 16, LDF, Y, LDF, acc, lane);
-    st16_f32(sT + (b0 + 16) * LDF + b0, LDF, acc, lane);
-  }
+  inv64_merge1b(sX, sT, w, lane);
   __syncthreads();
-  // level 2: Y20 = X20 T00 + X21 T10, Y30 = X30 T00 + X31 T10, Y21 = X21 T11, Y31 = X31 T11
-  {
-    const int ib = 2 + (w & 1), jb = w >> 1;  // wave 0: Y20, 1: Y30, 2: Y21, 3: Y31
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    if (jb == 0) acc = mm16_f32(sX + 16 * ib * LDF + 0, LDF, sT + 0 * LDF + 0, LDF, acc, lane);
-    acc = mm16_f32(sX + 16 * ib * LDF + 16, LDF, sT + 16 * LDF + 16 * jb, LDF, acc, lane);
-    st16_f32(Y, LDF, acc, lane);
-  }
+  inv64_merge2a(sX, sT, w, lane);
   __syncthreads();
-  {  // T20 = T22 Y20, T30 = T32 Y20 + T33 Y30, T21 = T22 Y21, T31 = T32 Y21 + T33 Y31
-    const int ib = 2 + (w & 1), jb = w >> 1;
-    const float* Ya = inv_scratch(sX, 2 * jb);      // Y2jb
-    const float* Yb = inv_scratch(sX, 2 * jb + 1);  // Y3jb
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    acc = mm16_f32(sT + 16 * ib * LDF + 32, LDF, Ya, LDF, acc, lane);
-    if (ib == 3) acc = mm16_f32(sT + 48 * LDF + 48, LDF, Yb, LDF, acc, lane);
-    st16_f32(sT + 16 * ib * LDF + 16 * jb, LDF, acc, lane);
-  }
+  inv64_merge2b(sX, sT, w, lane);
   __syncthreads();
 }
 
@@ -171,18 +187,17 @@ __global__ __launch_bounds__(pf::NT) void unit_lower_inv_kernel(const float* __r
 }
 
 // ============================================================================================
-// Chunked prefill, part 1: chunk-local quantities (parallel over every (chunk, value head)).
+// Chunked prefill: operand fragments of one chunk.
 // ============================================================================================
-// Workspace record per (chunk slot, value head).  Everything the scan kernel multiplies is stored
-// as ready-made MFMA operand fragments: a fragment is 64 lanes x 16 bytes (lane l at byte 16 l), so
-// the scan kernel stages a chunk with plain linear copies and reads each fragment with one
+// The segment kernel builds, per (chunk, value head), the operands of the state chain in LDS as
+// ready-made MFMA fragments: a fragment is 64 lanes x 16 bytes (lane l at byte 16 l), read with one
 // conflict-free 16-byte LDS read per lane.
 //
-// k-slot order.  Inside every 32-wide reduction block the scan kernel feeds MFMA B operands straight
-// from accumulator registers: lane (c, g) = (l % 16, l / 16) holds rows 4g..4g+3 of two consecutive
+// k-slot order.  Inside every 32-wide reduction block the chain feeds MFMA B operands straight from
+// accumulator registers: lane (c, g) = (l % 16, l / 16) holds rows 4g..4g+3 of two consecutive
 // 16-row accumulator tiles, and uses them as the 8 k-values of its B fragment.  So B slot s of a
 // block stands for block row kpos(s) = 16 ((s >> 2) & 1) + 4 (s >> 3) + (s & 3), and every A
-// fragment stored here is permuted the same way along k:  A-frag element e of lane (c, g) for tile
+// fragment below is permuted the same way along k:  A-frag element e of lane (c, g) for tile
 // (m, j) = M[16 m + c][32 j + kpos(8 g + e)].
 //
 //   WN  16 frags [tb 4][j 4]  bf16  M = -W,  W = T diag(beta e^G) K     (tokens x features)
@@ -190,8 +205,6 @@ __global__ __launch_bounds__(pf::NT) void unit_lower_inv_kernel(const float* __r
 //   QG  16 frags [tb 4][j 4]  bf16  M = q (l2-normalised)               (tokens x features)
 //   QK   8 frags [tb 4][j 2]  bf16  M = scale q_i.k_j e^{G_i - G_j}, i >= j, else 0 (the two
 //                                   all-zero fragments (tb, j) = (0, 1), (1, 1) are not written)
-// KT and QG depend on the key head only: they are written into the record of the first value
-// head of each key head (h % (Hv / Hk) == 0) and read from there.
 //   U   fp16 [slice 8][lane 64][tb 4][r 4] = U[16 tb + 4 g + r][16 slice + c] / USC[tb],
 //       U = T diag(beta) V (accumulator layout of each 16-column slice)
 //   DEC [64] fp32 = e^{G_last - G_t};  USC [4] fp32;  GL = e^{G_last};  KSC = 1 / kappa;  KAP = kappa;
@@ -370,101 +383,317 @@ __device__ __forceinline__ f16x8 pack_acc_f16(f32x4 a, f32x4 b, float sa) {
 }
 __device__ __forceinline__ float wave_max(float v) { return wave_max_fast(v); }
 
-struct LocalSmem {
-  uint16_t K[pf::CH * pf::LDK];     // K chunk, row-major (token, feature); K^T operands via transpose reads
-  float X[pf::CH * pf::LDF];        // then V, row-major (token, feature), once the inverse is done
+__device__ __forceinline__ bf16x8 lds_frag(const uint8_t* base, int f, int lane) {
+  return *reinterpret_cast<const bf16x8*>(base + f * ws::FRAG + lane * 16);
+}
+__device__ __forceinline__ f16x8 lds_frag_h(const uint8_t* base, int f, int lane) {
+  return *reinterpret_cast<const f16x8*>(base + f * ws::FRAG + lane * 16);
+}
+// Workgroup barrier over LDS only: it waits for this wave's LDS accesses (lgkmcnt 0), which is all
+// the other waves depend on, and leaves global loads and stores in flight (__syncthreads would
+// drain them: its release fence waits for every outstanding memory access, the next chunk's
+// prefetched inputs included).
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// ============================================================================================
+// Chunked prefill, part 1: the intra-chunk inverse, parallel over every (chunk, key head).
+// ============================================================================================
+// For each value head of the key head: X = -(beta_i k_i.k_j e^{G_i - G_j})_{i>j} and
+// T = (I - X)^{-1} (unit_lower_inv64, fp32), written as the bf16 MFMA fragments the segment kernel
+// multiplies K and V with: T diag(beta e^G) (W = T diag(beta e^G) K) and T diag(beta)
+// (U = T diag(beta) V), lower-triangular fragments only (token tile w, k-block s <= w / 2).  It is
+// latency-bound work (dependent fp32 products, barriers), so it runs in its own kernel at 3
+// workgroups per compute unit.  K K^T is formed once per key head.
+namespace tf {
+constexpr int FRAGS = 6;                      // per matrix
+constexpr int BYTES = 2 * FRAGS * ws::FRAG;   // T diag(beta e^G), then T diag(beta): 12 KiB
+__device__ __forceinline__ int fid(int w, int s) { return w < 2 ? w : 2 * w - 2 + s; }
+}  // namespace tf
+struct InvSmem {
+  uint16_t K[pf::CH * pf::LDK];
+  float X[pf::CH * pf::LDF];
   float T[pf::CH * pf::LDF];
   float G[pf::CH], EG[pf::CH], B[pf::CH];
-  float KMX[4];
 };
-static_assert(pf::CH * pf::LDK * 2 <= pf::CH * pf::LDF * 4, "V must fit in the X buffer");
-
-// One (chunk, key head) item's inputs shared by the key head's value heads, all loads issued up
-// front: K rows 4tq.. x features 8fb.. (thread (tq, fb)) and Q rows 16w + l%16 in k-slot order
-// (block s holds features 32s + 4g.. and 32s + 16 + 4g..).
-struct KeyLoads {
-  u16x8 kx[4], qr[4];
-  ChunkPos cp;
-  int hk, slot;
-};
-// One value head's inputs for that chunk: V rows like K, g and beta (wave 0, lane = token).
-struct HeadLoads {
-  u16x8 vreg[4];
-  float graw, braw;
-};
-__device__ __forceinline__ void key_loads(KeyLoads& L, int64_t item, const uint16_t* __restrict__ q, int64_t qs,
-                                          const uint16_t* __restrict__ k, int64_t ks,
-                                          const int32_t* __restrict__ cu, const int32_t* __restrict__ seq_chunk0,
-                                          int nseq, int seq_len, int Hqk) {
+template <typename BetaT>
+__global__ __launch_bounds__(pf::NT, 3) void inv_kernel(const uint16_t* __restrict__ k, int64_t ks,
+                                                       const float* __restrict__ g, const BetaT* __restrict__ beta,
+                                                       const int32_t* __restrict__ cu,
+                                                       const int32_t* __restrict__ seq_chunk0, int nseq, int seq_len,
+                                                       int Hqk, int Hv, int use_l2, uint8_t* __restrict__ tfrag) {
   using namespace pf;
+  __shared__ InvSmem sm;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
-  L.hk = (int)(item % Hqk);
-  L.slot = (int)(item / Hqk);
-  L.cp = chunk_pos(L.slot, cu, seq_chunk0, nseq, seq_len);
-  const ChunkPos& cp = L.cp;
-  const int tq = t >> 4, fb = t & 15;
-  load_rows4(L.kx, k + (int64_t)L.hk * D, ks, cp.t0, cp.len, tq, 8 * fb);
-  const u16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
-  const int row = 16 * w + c16, rowc = row < cp.len ? row : cp.len - 1;
+  const int hk = blockIdx.x, slot = blockIdx.y;
+  const ChunkPos cp = chunk_pos(slot, cu, seq_chunk0, nseq, seq_len);
+  const int r = Hv / Hqk, h0 = hk * r;
+  const int tok = lane < cp.len ? lane : cp.len - 1;
+  float graw = 0.f, braw = 0.f;
+  if (w == 0) {  // the first value head's g and beta (zero past the chunk's end)
+    const float gr = g[(cp.t0 + tok) * Hv + h0];
+    const float br = Elem<BetaT>::load(beta + (cp.t0 + tok) * Hv + h0);
+    graw = lane < cp.len ? gr : 0.f;
+    braw = lane < cp.len ? br : 0.f;
+  }
+  {
+    u16x8 kx[4];
+    const int tq = t >> 4, fb = t & 15;
+    load_rows4(kx, k + (int64_t)hk * D, ks, cp.t0, cp.len, tq, 8 * fb);
+    if (use_l2) l2norm_rows4(kx);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<u16x8*>(&sm.K[(4 * tq + i) * LDK + 8 * fb]) = kx[i];
+  }
+  __syncthreads();
+  // K K^T, row tile w (blocks cb <= w), kept in registers for every value head
+  f32x4 acc[4];
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb) acc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    const uint16_t* p = q + (cp.t0 + rowc) * qs + (int64_t)L.hk * D + 32 * s + 4 * g4;
-    const u16x4 lo = *reinterpret_cast<const u16x4*>(p), hi = *reinterpret_cast<const u16x4*>(p + 16);
-    const u16x8 x = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-    L.qr[s] = row < cp.len ? x : zero;
+    const bf16x8 ak = frag(sm.K, LDK, 16 * w, 32 * s, lane);
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb)
+      if (cb <= w) acc[cb] = mma(ak, frag(sm.K, LDK, 16 * cb, 32 * s, lane), acc[cb]);
   }
-}
-template <typename BetaT>
-__device__ __forceinline__ void head_loads(HeadLoads& H, const ChunkPos& cp, int h, const uint16_t* __restrict__ v,
-                                           int64_t vs, const float* __restrict__ g, const BetaT* __restrict__ beta,
-                                           int Hv) {
-  using namespace pf;
-  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
-  load_rows4(H.vreg, v + (int64_t)h * D, vs, cp.t0, cp.len, t >> 4, 8 * (t & 15));
-  // padding tokens: g = 0, beta = 0 (their loads read the chunk's last token)
-  const int tok = lane < cp.len ? lane : cp.len - 1;
-  const float gr = g[(cp.t0 + tok) * Hv + h];
-  const float br = Elem<BetaT>::load(beta + (cp.t0 + tok) * Hv + h);
-  H.graw = w == 0 && lane < cp.len ? gr : 0.f;
-  H.braw = w == 0 && lane < cp.len ? br : 0.f;
+  for (int j = 0; j < r; ++j) {
+    const int h = h0 + j;
+    if (w == 0) {  // cumulative decay within the chunk
+      if (j > 0) {
+        const float gr = g[(cp.t0 + tok) * Hv + h];
+        const float br = Elem<BetaT>::load(beta + (cp.t0 + tok) * Hv + h);
+        graw = lane < cp.len ? gr : 0.f;
+        braw = lane < cp.len ? br : 0.f;
+      }
+      float G = graw;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const float up = __shfl_up(G, o, kWave);
+        if (lane >= o) G += up;
+      }
+      sm.G[lane] = G;
+      sm.EG[lane] = expf(G);
+      sm.B[lane] = braw;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {  // X[i][jj], i = 16 w + 4 g + rr, jj = 16 cb + c
+        const int i = 16 * w + 4 * g4 + rr, jj = 16 * cb + c16;
+        float x = 0.f;
+        if (cb <= w && i > jj) x = -sm.B[i] * acc[cb][rr] * __expf(sm.G[i] - sm.G[jj]);
+        sm.X[i * LDF + jj] = x;
+      }
+    __syncthreads();
+    unit_lower_inv64(sm.X, sm.T, w, lane);
+    // token tile w: fragments (w, s), s <= w / 2: lane (c, g) element e = T[16 w + c][32 s + 8 g + e] x ...
+    uint8_t* dst = tfrag + ((int64_t)slot * Hv + h) * tf::BYTES + lane * 16;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      if (2 * s > w) continue;
+      const float* trow = &sm.T[(16 * w + c16) * LDF + 32 * s + 8 * g4];
+      float a[8], b[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int col = 32 * s + 8 * g4 + e;
+        a[e] = trow[e] * sm.B[col];
+        b[e] = a[e] * sm.EG[col];
+      }
+      *reinterpret_cast<bf16x8*>(dst + tf::fid(w, s) * ws::FRAG) = pack8(b);
+      *reinterpret_cast<bf16x8*>(dst + (tf::FRAGS + tf::fid(w, s)) * ws::FRAG) = pack8(a);
+    }
+    if (j + 1 < r) __syncthreads();  // the next head rewrites G, X and T
+  }
 }
 
-// The key head's part of an item: l2norm of K (row-major LDS copy, largest |K| -> kappa) and of Q
-// (k-slot ordered fragments qf, kept in registers), and the key-head fragments QG and kappa K^T,
-// written into the record of the key head's first value head (rec).  Returns kappa's exponent.
-__device__ __forceinline__ int local_key(LocalSmem& sm, const KeyLoads& L, int use_l2, bf16x8 (&qf)[4],
-                                         uint8_t* __restrict__ rec) {
+// ============================================================================================
+// Chunked prefill, segment-parallel and fused (the path gdn_chunk_prefill runs).
+// ============================================================================================
+// A sequence's chunks are cut into segments of L consecutive chunks (the host picks L so that
+// about one segment per compute unit and value head exists).  One workgroup per (segment, value
+// head) walks its segment's chunks; per chunk its 8 waves build the operand fragments described
+// above in LDS (l2norm, decay, Q K^T, W and U from the inverse kernel's fragments, kappa K^T), then
+// every wave advances its 16 columns of the fp32 state and writes their outputs.  Only the
+// inverse kernel's 12 KiB per (chunk, value head) passes through memory.
+// A segment other than the first of its sequence needs its true initial state: the state after
+// segment j is S_{j+1} = A_j S_j + B_j, with A_j the segment's linear map (the chain run from the
+// identity with U = 0) and B_j its affine part (run from zero).  A summary pass computes A_j and
+// B_j for every segment with a successor, seg_combine_kernel applies them in order per sequence
+// (fp32 MFMA), and the output pass runs every segment from its true state.
+// With unit keys (in-kernel l2norm) and 0 <= beta <= 1 each token's map gamma (I - beta k k^T) has
+// spectral norm <= gamma, so ||A_j|| <= exp(sum of g over segment j).  When that bound is below
+// 2^-64, A_j S_j lies far below the fp32 rounding of S_{j+1} and A_j is not formed (flag 0).
+namespace sg {
+constexpr int NT = 512;                      // 8 waves
+constexpr int kMinSeg = 4;                   // shortest segment the host cuts (chunks)
+constexpr int kTargetItems = 256;            // segments x value heads the host aims for
+constexpr float kNegligibleLog = -44.3614f;  // ln(2^-64)
+constexpr int kTrans = 2 * pf::D * pf::D;    // floats per (slot, head): A, then B
+}  // namespace sg
+
+// The segments of a batch: packed sequences (seg0[s] = segments of the sequences before s, built by
+// seg_table_kernel) or nseq uniform sequences of seq_len tokens.  Segment j of sequence s covers
+// chunks L (j - first_seg(s)) .. + L - 1 (fewer in its last segment); an empty sequence has one
+// segment without chunks.  Every segment but the last of its sequence owns a transition slot
+// (A, B), numbered first_slot(s) = first_seg(s) - s onwards.
+struct SegTable {
+  const int32_t* cu;
+  const int32_t* chunk0;
+  const int32_t* seg0;
+  int nseq, seq_len, L;
+  __device__ __forceinline__ int nch(int s) const {
+    return cu ? chunk0[s + 1] - chunk0[s] : (seq_len + pf::CH - 1) / pf::CH;
+  }
+  __device__ __forceinline__ int nseg_of(int n) const { return n <= L ? 1 : (n + L - 1) / L; }
+  __device__ __forceinline__ int first_seg(int s) const { return cu ? seg0[s] : s * nseg_of(nch(0)); }
+  __device__ __forceinline__ int first_slot(int s) const { return first_seg(s) - s; }
+  // Dense index of sequence s's first chunk (the inverse kernel's fragment slot).
+  __device__ __forceinline__ int first_chunk(int s) const { return cu ? chunk0[s] : s * nch(0); }
+  __device__ __forceinline__ int64_t start(int s) const { return cu ? (int64_t)cu[s] : (int64_t)s * seq_len; }
+  __device__ __forceinline__ int len(int s) const { return cu ? cu[s + 1] - cu[s] : seq_len; }
+  // The sequence of segment j (the last s with first_seg(s) <= j).
+  __device__ int seq_of_seg(int j) const {
+    if (!cu) return j / nseg_of(nch(0));
+    int lo = 0, hi = nseq - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (seg0[mid] <= j) lo = mid;
+      else hi = mid - 1;
+    }
+    return lo;
+  }
+  // The sequence of transition slot t (the last s with first_slot(s) <= t).
+  __device__ int seq_of_slot(int t) const {
+    if (!cu) return t / (nseg_of(nch(0)) - 1);
+    int lo = 0, hi = nseq - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (seg0[mid] - mid <= t) lo = mid;
+      else hi = mid - 1;
+    }
+    return lo;
+  }
+};
+
+// seg0 (nseq + 1 entries) from the chunk prefix sums: one workgroup, a block-wise scan.
+__global__ __launch_bounds__(256) void seg_table_kernel(const int32_t* __restrict__ chunk0, int nseq, int L,
+                                                       int32_t* __restrict__ seg0) {
+  __shared__ int part[256];
+  const int t = threadIdx.x;
+  int base = 0;
+  for (int s0 = 0; s0 < nseq; s0 += 256) {
+    const int s = s0 + t;
+    int n = 0;
+    if (s < nseq) {
+      const int c = chunk0[s + 1] - chunk0[s];
+      n = c <= L ? 1 : (c + L - 1) / L;
+    }
+    part[t] = n;
+    __syncthreads();
+    for (int o = 1; o < 256; o <<= 1) {  // inclusive scan
+      const int x = t >= o ? part[t - o] : 0;
+      __syncthreads();
+      part[t] += x;
+      __syncthreads();
+    }
+    if (s < nseq) seg0[s] = base + part[t] - n;
+    base += part[255];
+    __syncthreads();
+  }
+  if (t == 0) seg0[nseq] = base;
+}
+
+// Per-chunk operands, double-buffered: the local waves fill one buffer while the chain waves read
+// the other.  Fragment layouts as described at the top of this section (k-slot order).
+struct alignas(16) SegBuf {
+  uint16_t K[pf::CH * pf::LDK];   // K rows (l2-normalised), token-major
+  uint16_t V[pf::CH * pf::LDK];   // V rows
+  uint8_t wn[16 * ws::FRAG];      // -W fragments [tb 4][j 4]
+  uint8_t qg[16 * ws::FRAG];      // q fragments [tb 4][j 4]
+  uint8_t qk[8 * ws::FRAG];       // QK fragments [tb 4][j 2] (the two all-zero ones unused)
+  float dec[pf::CH];              // e^{G_last - G_t}
+  float egs[pf::CH];              // scale e^{G_t}
+  float gl;                       // e^{G_last}
+};
+struct SegSmem {
+  SegBuf buf[2];
+  float red[8];
+};
+
+enum SegMode { kSegOut = 0, kSegB = 1, kSegA = 2 };
+
+// A local wave's inputs for one chunk, loaded a chunk ahead.  Local wave w (threads t < 256) holds K
+// and V rows 4 tq + i x features 8 fb .. (t = 16 tq + fb: rows 16 w .. 16 w + 15), q of token tile w
+// in k-slot order, the T diag(beta e^G) fragments of token tile w and the g of token `lane`.  Rows
+// past the chunk's end hold its last row (every load is in bounds) and are zeroed where they are
+// used: a select right after a load would make the wave wait for the load there.
+struct LocIn {
+  u16x8 kr[4], vr[4], qr[4];
+  bf16x8 tbe[2];
+  float graw;
+  int len;
+};
+template <bool kNeedQ>
+__device__ __forceinline__ void loc_load(LocIn& L, int64_t t0, int len, int kh, int h,
+                                         const uint16_t* __restrict__ q, int64_t qs, const uint16_t* __restrict__ k,
+                                         int64_t ks, const uint16_t* __restrict__ v, int64_t vs,
+                                         const float* __restrict__ g, int Hv, const uint8_t* __restrict__ tfr) {
   using namespace pf;
-  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
   const int tq = t >> 4, fb = t & 15;
-  u16x8 kx[4], qr[4];
+  L.len = len;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    kx[i] = L.kx[i];
-    qr[i] = L.qr[i];
+    const int row = 4 * tq + i, rc = row < len ? row : len - 1;
+    L.kr[i] = *reinterpret_cast<const u16x8*>(k + (t0 + rc) * ks + (int64_t)kh * D + 8 * fb);
+    L.vr[i] = *reinterpret_cast<const u16x8*>(v + (t0 + rc) * vs + (int64_t)h * D + 8 * fb);
   }
-  // K: l2norm, row-major LDS copy, largest |K|
-  {
-    if (use_l2) l2norm_rows4(kx);
-    // largest |K|: bf16 bit patterns with the sign cleared order like their magnitudes (NaN aside)
-    typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
-    u16x2 mx = {0, 0};
+  if (kNeedQ) {
+    const int row = 16 * w + c16, rowc = row < len ? row : len - 1;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      *reinterpret_cast<u16x8*>(&sm.K[(4 * tq + i) * LDK + 8 * fb]) = kx[i];
-      const u32x4v wv = __builtin_bit_cast(u32x4v, kx[i]);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const u16x2 a = __builtin_bit_cast(u16x2, wv[e] & 0x7fff7fffu);
-        mx = __builtin_elementwise_max(mx, a);
-      }
+    for (int s = 0; s < 4; ++s) {
+      const uint16_t* p = q + (t0 + rowc) * qs + (int64_t)kh * D + 32 * s + 4 * g4;
+      const u16x4 lo = *reinterpret_cast<const u16x4*>(p), hi = *reinterpret_cast<const u16x4*>(p + 16);
+      L.qr[s] = u16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
-    float m = fmaxf(bf2f(mx[0]), bf2f(mx[1]));
-    m = wave_max(m);
-    if (lane == 0) sm.KMX[w] = m;
   }
-  // Q: l2norm in registers (a row is spread over lanes l%16 + 16g' and the 4 blocks)
-  {
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+    if (2 * s <= w) L.tbe[s] = *reinterpret_cast<const bf16x8*>(tfr + tf::fid(w, s) * ws::FRAG + lane * 16);
+  const int tok = lane < len ? lane : len - 1;
+  L.graw = g[(t0 + tok) * Hv + h];
+}
+
+// Local phase 1 (wave w < 4): K rows (l2norm) and V rows into the buffer, q (l2norm) as fragments
+// (kept in qf for phase 2), the decay scan (every local wave holds G of token `lane`; wave 0 writes
+// the factors the chain reads).
+template <bool kNeedQ>
+__device__ __forceinline__ void loc_phase1(SegBuf& B, const LocIn& in, int use_l2,
+                                           bf16x8 (&qf)[4], float& G) {
+  using namespace pf;
+  int t;  // opaque per call: the LDS addresses derived from it are not hoisted out of the chunk loop
+  asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"((int)threadIdx.x));
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
+  const int tq = t >> 4, fb = t & 15, len = in.len;
+  const u16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+  u16x8 kx[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) kx[i] = 4 * tq + i < len ? in.kr[i] : zero;
+  if (use_l2) l2norm_rows4(kx);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) *reinterpret_cast<u16x8*>(&B.K[(4 * tq + i) * LDK + 8 * fb]) = kx[i];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    *reinterpret_cast<u16x8*>(&B.V[(4 * tq + i) * LDK + 8 * fb]) = 4 * tq + i < len ? in.vr[i] : zero;
+  if (kNeedQ) {
+    u16x8 qr[4];
+    const bool live = 16 * w + (lane & 15) < len;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qr[s] = live ? in.qr[s] : zero;
     if (use_l2) {
       float ss = 0.f;
 #pragma unroll
@@ -475,892 +704,457 @@ __device__ __forceinline__ int local_key(LocalSmem& sm, const KeyLoads& L, int u
       for (int s = 0; s < 4; ++s) qr[s] = scale_bf16(qr[s], inv);
     }
 #pragma unroll
-    for (int s = 0; s < 4; ++s) qf[s] = __builtin_bit_cast(bf16x8, qr[s]);
+    for (int s = 0; s < 4; ++s) {
+      qf[s] = __builtin_bit_cast(bf16x8, qr[s]);
+      *reinterpret_cast<bf16x8*>(B.qg + (w * 4 + s) * ws::FRAG + lane * 16) = qf[s];
+    }
   }
-  __syncthreads();
-  // QG fragments (this wave's token tile, straight from the k-slot ordered Q fragments) and the
-  // kappa-scaled fp16 K^T fragments
+  G = lane < len ? in.graw : 0.f;  // cumulative decay within the chunk (g = 0 past its end)
 #pragma unroll
-  for (int s = 0; s < 4; ++s)
-    *reinterpret_cast<bf16x8*>(rec + ws::QG + (w * 4 + s) * ws::FRAG + lane * 16) = qf[s];
-  const float kmax = fmaxf(fmaxf(sm.KMX[0], sm.KMX[1]), fmaxf(sm.KMX[2], sm.KMX[3]));
-  const int ke = fp16_fit_exp(kmax);
-  const float kappa = ldexpf(1.0f, ke);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int idx = t + NT * i;  // fragment idx / 64 = (rb, j), lane idx % 64
-    const int f_ = idx >> 6, rb = f_ >> 1, j = f_ & 1;  // idx % 64 == lane (idx = t + 256 i)
-    const u16x8 kt = frag_tr_kperm(sm.K, LDK, 32 * j, 16 * rb, lane);
-    f16x8 o;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = (_Float16)(bf2f(kt[e]) * kappa);
-    *reinterpret_cast<f16x8*>(rec + ws::KT + idx * 16) = o;
+  for (int o = 1; o < 64; o <<= 1) {
+    const float up = __shfl_up(G, o, kWave);
+    if (lane >= o) G += up;
   }
-  return ke;
+  if (w == 0) {
+    const float gl = __shfl(G, 63, kWave);
+    B.dec[lane] = expf(gl - G);
+    B.egs[lane] = kScale * expf(G);
+    if (lane == 0) B.gl = expf(gl);
+  }
 }
 
-// A = K K^T -> X in LDS, and (Q K^T)^T = K Q^T, whose accumulator layout is exactly the k-slot
-// ordered QK fragment layout -> workspace.  Both are lower triangles of 16x16 blocks; wave W takes
-// the A blocks of row tile 3 - W and the QK blocks of its own row tile W (whose q it holds), so
-// every wave computes 5 blocks.  X carries -beta_i and the decay e^{G_i - G_j}, QK the scale and
-// the decay; sm.G and sm.B hold the value head's cumulative decay and beta.
-template <int W>
-__device__ __forceinline__ void aqk_blocks(LocalSmem& sm, const bf16x8 (&qf)[4], uint8_t* __restrict__ rec,
-                                           int lane) {
+// Local phase 2 (wave W < 4, after the K rows are in): the QK fragments and the -W fragments of
+// token tile W.  (Q K^T)^T = K Q^T and W^T = K^T (T diag(beta e^G))^T: both accumulator layouts are
+// the k-slot ordered fragment layouts.
+template <int W, bool kNeedQ>
+__device__ __forceinline__ void loc_phase2(SegBuf& B, const bf16x8 (&qf)[4], float G, const bf16x8 (&tbe)[2]) {
   using namespace pf;
-  constexpr int TA = 3 - W;  // A row tile
-  const int c16 = lane & 15, g4 = lane >> 4;
-  f32x4 accA[TA + 1], accQ[W + 1];
-#pragma unroll
-  for (int cb = 0; cb <= TA; ++cb) accA[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int cb = 0; cb <= W; ++cb) accQ[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    const bf16x8 ak = frag(sm.K, LDK, 16 * TA, 32 * s, lane);
-#pragma unroll
-    for (int cb = 0; cb <= TA; ++cb) accA[cb] = mma(ak, frag(sm.K, LDK, 16 * cb, 32 * s, lane), accA[cb]);
-#pragma unroll
-    for (int cb = 0; cb <= W; ++cb) accQ[cb] = mma(frag_kperm(sm.K, LDK, 16 * cb, 32 * s, lane), qf[s], accQ[cb]);
-  }
-#pragma unroll
-  for (int cb = 0; cb < 4; ++cb)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {  // X[i][jj], i = 16 TA + 4g + r, jj = 16cb + c
-      const int i = 16 * TA + 4 * g4 + r, jj = 16 * cb + c16;
-      float x = 0.f;
-      if (cb <= TA && i > jj) x = -sm.B[i] * accA[cb <= TA ? cb : 0][r] * __expf(sm.G[i] - sm.G[jj]);
-      sm.X[i * LDF + jj] = x;
-    }
-  f32x4 qk[4];
-#pragma unroll
-  for (int cb = 0; cb < 4; ++cb)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {  // QK[i][jj], i = 16W + c, jj = 16cb + 4g + r
-      const int i = 16 * W + c16, jj = 16 * cb + 4 * g4 + r;
-      qk[cb][r] = (cb <= W && i >= jj) ? kScale * accQ[cb <= W ? cb : 0][r] * __expf(sm.G[i] - sm.G[jj]) : 0.f;
-    }
-#pragma unroll
-  for (int j = 0; j < 2; ++j)
-    if (2 * j <= W)  // fragment (W, j) is non-zero only when its first column block 2j <= W
-      *reinterpret_cast<bf16x8*>(rec + ws::QK + (W * 2 + j) * ws::FRAG + lane * 16) =
-          pack_acc_bf16(qk[2 * j], qk[2 * j + 1]);
-}
-
-// One value head's part: cumulative decay, X = -(beta K K^T o decay) and the QK fragments, the
-// inverse, W and U -- everything state-independent about (chunk, value head), into its record.
-// sm.K holds the key head's normalised K; the caller has synchronised since the last value head.
-__device__ __forceinline__ void local_head(LocalSmem& sm, const HeadLoads& H, const bf16x8 (&qf)[4], int ke,
-                                           uint8_t* __restrict__ rec) {
-  using namespace pf;
-  // the thread index through an opaque move: the caller loops over value heads, and addresses
-  // derived from it would otherwise be hoisted out of that loop and held in registers
   int t;
   asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"((int)threadIdx.x));
-  const int w = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
-  const int tq = t >> 4, fb = t & 15;
-  u16x8 vreg[4];
+  const int lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
+  if (kNeedQ) {
+    f32x4 accQ[W + 1];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) vreg[i] = H.vreg[i];
-  const float graw = H.graw, braw = H.braw;
-  if (t == 0) {
-    reinterpret_cast<float*>(rec + ws::KSC)[0] = ldexpf(1.0f, -ke);
-    reinterpret_cast<float*>(rec + ws::KAP)[0] = ldexpf(1.0f, ke);
-  }
-  if (w == 0) {  // cumulative decay within the chunk
-    float G = graw;
+    for (int cb = 0; cb <= W; ++cb) accQ[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const float up = __shfl_up(G, o, kWave);
-      if (lane >= o) G += up;
-    }
-    const float gl = __shfl(G, 63, kWave);
-    const float eg = expf(G), dec = expf(gl - G);
-    sm.G[lane] = G;
-    sm.EG[lane] = eg;
-    sm.B[lane] = braw;
-    reinterpret_cast<float*>(rec + ws::DEC)[lane] = dec;
-    reinterpret_cast<float*>(rec + ws::EGS)[lane] = kScale * eg;
-    if (lane == 0) reinterpret_cast<float*>(rec + ws::GL)[0] = expf(gl);
-  }
-  __syncthreads();
-
-  // A = K K^T -> X in LDS and the QK fragments -> workspace (aqk_blocks), with the wave index as a
-  // compile-time constant so every block bound is static
-  switch (w) {
-    case 0: aqk_blocks<0>(sm, qf, rec, lane); break;
-    case 1: aqk_blocks<1>(sm, qf, rec, lane); break;
-    case 2: aqk_blocks<2>(sm, qf, rec, lane); break;
-    default: aqk_blocks<3>(sm, qf, rec, lane); break;
-  }
-  __syncthreads();
-
-  unit_lower_inv64(sm.X, sm.T, w, lane);
-
-  // W^T = K^T (T diag(beta e^G))^T: its accumulator layout is the k-slot ordered W fragment layout.
-  // U = T diag(beta) V in accumulator layout (the scan kernel's initial vn tiles).
-  {
-    bf16x8 tbe[2], tb[2];
+    for (int s = 0; s < 4; ++s)
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const float* trow = &sm.T[(16 * w + c16) * LDF + 32 * s + 8 * g4];
-      float a[8], b[8];
+      for (int cb = 0; cb <= W; ++cb) accQ[cb] = mma(frag_kperm(B.K, LDK, 16 * cb, 32 * s, lane), qf[s], accQ[cb]);
+    const float gi = __shfl(G, 16 * W + c16, kWave);
+    f32x4 qk[4];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int col = 32 * s + 8 * g4 + e;
-        a[e] = trow[e] * sm.B[col];
-        b[e] = a[e] * sm.EG[col];
+    for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {  // QK[i][jj], i = 16W + c, jj = 16cb + 4g + r
+        const int jj = 16 * cb + 4 * g4 + r;
+        const float gj = __shfl(G, jj, kWave);
+        qk[cb][r] = (cb <= W && 16 * W + c16 >= jj) ? kScale * accQ[cb <= W ? cb : 0][r] * __expf(gi - gj) : 0.f;
       }
-      tb[s] = pack8(a);
-      tbe[s] = pack8(b);
-    }
-    {
-      f32x4 accW[8];
-#pragma unroll
-      for (int cb = 0; cb < 8; ++cb) {
-        accW[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < 2; ++s)
-          accW[cb] = mma(__builtin_bit_cast(bf16x8, frag_tr(sm.K, LDK, 32 * s, 16 * cb, lane)), tbe[s], accW[cb]);
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        *reinterpret_cast<bf16x8*>(rec + ws::WN + (w * 4 + j) * ws::FRAG + lane * 16) =
-            pack_acc_bf16(-accW[2 * j], -accW[2 * j + 1]);
-    }
-    // V row-major into the X buffer (dead after the inverse; its scratch blocks were read by the
-    // inverse's last step -- hence the barrier)
-    uint16_t* sV = reinterpret_cast<uint16_t*>(sm.X);
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<u16x8*>(&sV[(4 * tq + i) * LDK + 8 * fb]) = vreg[i];
-    __syncthreads();
-    f32x4 u[8];
-    float m = 0.f;
-#pragma unroll
-    for (int cb = 0; cb < 8; ++cb) {
-      u[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < 2; ++s)
-        u[cb] = mma(tb[s], __builtin_bit_cast(bf16x8, frag_tr(sV, LDK, 32 * s, 16 * cb, lane)), u[cb]);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) m = fmaxf(m, fabsf(u[cb][r]));
-    }
-    const int ue = fp16_fit_exp(wave_max(m));
-    const float us = ldexpf(1.0f, ue);
-    if (lane == 0) reinterpret_cast<float*>(rec + ws::USC)[w] = ldexpf(1.0f, -ue);
-    typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-#pragma unroll
-    for (int cb = 0; cb < 8; ++cb) {
-      const f16x4 hv = {(_Float16)(u[cb][0] * us), (_Float16)(u[cb][1] * us), (_Float16)(u[cb][2] * us),
-                        (_Float16)(u[cb][3] * us)};
-      *reinterpret_cast<f16x4*>(rec + ws::U + ((cb * 64 + lane) * 4 + w) * 8) = hv;
-    }
-  }
-}
-
-// Grid (key heads, chunks): one workgroup per (chunk, key head) does the key head's shared work
-// once and then each of its Hv / Hqk value heads in turn (the next head's inputs load while the
-// current one is computed).
-template <typename BetaT>
-__global__ __launch_bounds__(pf::NT, 3) void chunk_local_kernel(
-    const uint16_t* __restrict__ q, int64_t qs, const uint16_t* __restrict__ k, int64_t ks,
-    const uint16_t* __restrict__ v, int64_t vs,
-    const float* __restrict__ g, const BetaT* __restrict__ beta, const int32_t* __restrict__ cu,
-    const int32_t* __restrict__ seq_chunk0, int nseq, int seq_len, int Hqk, int Hv, int use_l2,
-    uint8_t* __restrict__ work) {
-  __shared__ LocalSmem sm;
-  const int r = Hv / Hqk;
-  KeyLoads KL;
-  key_loads(KL, (int64_t)blockIdx.y * gridDim.x + blockIdx.x, q, qs, k, ks, cu, seq_chunk0, nseq, seq_len, Hqk);
-  const int h0 = KL.hk * r;
-  HeadLoads H;
-  head_loads<BetaT>(H, KL.cp, h0, v, vs, g, beta, Hv);
-  uint8_t* rec0 = work + ((int64_t)KL.slot * Hv + h0) * ws::BYTES;
-  bf16x8 qf[4];
-  const int ke = local_key(sm, KL, use_l2, qf, rec0);
-  for (int j = 0; j < r; ++j) {
-    if (j > 0) {
-      head_loads<BetaT>(H, KL.cp, h0 + j, v, vs, g, beta, Hv);
-      __syncthreads();  // this head rewrites the decay arrays and X
-    }
-    local_head(sm, H, qf, ke, rec0 + (int64_t)j * ws::BYTES);
-  }
-}
-
-// ============================================================================================
-// Chunked prefill, part 2: the inter-chunk state recurrence (the scan).
-// ============================================================================================
-// One workgroup per (sequence, value head, 16-column slice of the state): 8 workgroups per head,
-// so a single long sequence still spreads over nseq * Hv * 8 workgroups.  The 6 waves specialise:
-//   waves 0-1 (chain): vn = U - W S  and  S' = GL S + K^T (DEC vn) with the fp32 state slice
-//                    S [128, 16] split by rows: wave 0 holds S rows 0-63, wave 1 rows 64-127, each in
-//                    4 accumulator tiles for the whole sequence.  Each wave forms its half of the
-//                    k-sum W S (8 MFMAs; wave 0 starts from U), the two partial sums are swapped
-//                    through LDS with a per-wave step flag, and each wave then updates its own rows
-//                    (8 MFMAs).  Both products take their B operand straight from accumulator
-//                    registers (k-slot order)
-//   waves 2-3 (output): o = Qg S + QK vn one chunk behind the chain (two token tiles each), from
-//                    the S and vn the chain published in LDS and Qg / QK fragments they load
-//                    themselves two chunks ahead
-//   waves 4-5:       copy each chunk's WN and KT fragments, this slice's U tiles and the header
-//                    (34.5 KiB) from L2 into a 3-slot LDS ring, two steps ahead
-//   wave 6:          touches the records of the chunk kPrefetchAhead steps ahead, so they are in
-//                    L2 (fetched from HBM once for the head's 8 slices) before they are copied
-// One barrier per chunk.  During step c the chain computes chunk c from registers it read out of
-// ring slot c%3 during step c-1, reads chunk c+1 from slot (c+1)%3 into registers, and writes
-// vn(c) and S(c+1) into exchange slots c%3 and (c+1)%3; the output waves read exchange slot (c-1)%3;
-// the loaders fill ring slot c%3 with chunk c+3.  So no LDS read latency sits on the chain's
-// critical path beyond the partial-sum swap.
-// The state update runs on fp16 MFMA.  Usually DEC vn and K^T fit fp16 as they are (see the fast
-// path); otherwise DEC vn is scaled per column by a power of two sigma into [2^14, 2^15) and K^T
-// by kappa, and the product is folded in as S' = (GL S sigma kappa + P) / (sigma kappa), so the fp32
-// state only ever sees exact power-of-two rescaling besides the MFMA sum.
-namespace rg {  // one ring slot
-constexpr int WN = 0, KT = 16 * ws::FRAG, U = 32 * ws::FRAG, HDR = U + 2048, BYTES = HDR + 512;
-}  // namespace rg
-constexpr int kScanThreads = 448;  // 2 chain waves, 2 output waves, 2 loader waves, 1 prefetch wave
-constexpr int kPrefetchAhead = 6;  // chunks between the L2 prefetch and the chain step
-__device__ __forceinline__ bf16x8 lds_frag(const uint8_t* base, int f, int lane) {
-  return *reinterpret_cast<const bf16x8*>(base + f * ws::FRAG + lane * 16);
-}
-__device__ __forceinline__ f16x8 lds_frag_h(const uint8_t* base, int f, int lane) {
-  return *reinterpret_cast<const f16x8*>(base + f * ws::FRAG + lane * 16);
-}
-struct ScanSmem {
-  uint8_t ring[3][rg::BYTES];
-  uint8_t xch[3][6 * ws::FRAG];  // S (4 k-slot ordered bf16 B fragments) and vn (2)
-  f32x4 part[2][4][64];          // the chain waves' partial sums of vn, [wave][token tile][lane]
-  float init_buf[2][pf::D * 16]; // the next sequences' initial state slices [row][16 columns]
-  uint32_t pf_sink[64];          // landing place of the prefetch wave's copies (never read)
-  int flag[2];                   // step counter of each chain wave's published partial sum
-};
-
-// The sequences a scan workgroup walks: packed (cu / seq_chunk0) or uniform (seq_len tokens and
-// nch_u chunks each), and their state rows.  Indices are wave-uniform, so these are scalar loads.
-struct SeqTable {
-  const int32_t* cu;
-  const int32_t* chunk0;
-  const int32_t* rows;
-  int n_rows, seq_len, nch_u;
-  __device__ __forceinline__ int64_t start(int s) const { return cu ? (int64_t)cu[s] : (int64_t)s * seq_len; }
-  __device__ __forceinline__ int len(int s) const { return cu ? cu[s + 1] - cu[s] : seq_len; }
-  __device__ __forceinline__ int first_chunk(int s) const { return cu ? chunk0[s] : s * nch_u; }
-};
-// First sequence of group g when `groups` groups share the chunk stream: the first sequence whose
-// first chunk lies at or past g * total / groups (so groups hold whole sequences and differ by
-// at most one sequence's chunks).
-__device__ __forceinline__ int group_start(const SeqTable& t, int nseq, int64_t total, int groups, int g) {
-  if (g <= 0) return 0;
-  if (g >= groups) return nseq;
-  const int64_t q = total * g / groups;
-  int lo = 0, hi = nseq;  // first_chunk(nseq) == total >= q
-  while (lo < hi) {
-    const int mid = (lo + hi) >> 1;
-    if (t.first_chunk(mid) >= q) hi = mid;
-    else lo = mid + 1;
-  }
-  return lo;
-}
-// A position in a group's chunk stream: chunk c of the nch chunks of sequence s (which starts at
-// packed token t0, holds L tokens and keeps its states in slot row `row`, -1: none), k = the
-// ordinal of s among the group's non-empty sequences.
-struct Walk {
-  int s, c, nch, k, L, row;
-  int64_t t0;
-};
-__device__ __forceinline__ int next_nonempty(const SeqTable& t, int s, int s_hi) {
-  while (s < s_hi && t.len(s) == 0) ++s;
-  return s;
-}
-__device__ __forceinline__ void walk_open(Walk& w, const SeqTable& t, int s, int s_hi) {
-  w.s = s;
-  w.c = 0;
-  w.L = s < s_hi ? t.len(s) : 0;
-  w.nch = (w.L + pf::CH - 1) / pf::CH;
-  w.t0 = s < s_hi ? t.start(s) : 0;
-  w.row = s < s_hi ? state_row(t.rows, t.n_rows, s) : -1;
-}
-__device__ __forceinline__ void walk_begin(Walk& w, const SeqTable& t, int s_lo, int s_hi) {
-  walk_open(w, t, next_nonempty(t, s_lo, s_hi), s_hi);
-  w.k = 0;
-}
-__device__ __forceinline__ bool walk_last(const Walk& w) { return w.c == w.nch - 1; }
-__device__ __forceinline__ void walk_next(Walk& w, const SeqTable& t, int s_hi) {
-  if (++w.c < w.nch) return;
-  walk_open(w, t, next_nonempty(t, w.s + 1, s_hi), s_hi);
-  ++w.k;
-}
-
-// One chunk's operands for one chain wave (half = 0: S rows 0-63, 1: rows 64-127).
-// The KT fragments live outside: they are double-buffered, so that the next chunk's are read while
-// this chunk's update MFMAs still use theirs.
-struct ChainIn {
-  bf16x8 fw[8];  // WN fragments (tb, k-block 2 half + j) at [tb * 2 + j]
-  f16x8 u[2];    // this lane's U values (tiles 0,1 | 2,3); wave 0 only
-  f32x4 uf[4];   // the same, scaled to fp32 (chain_u_convert); wave 0 only
-  f32x4 dv[4];   // DEC of this lane's tokens
-  f32x4 usc;     // wave 0 only
-  float gl, ksc, kap;
-};
-typedef f16x8 KFrags[8];  // KT fragments of row tiles 4 half .. 4 half + 3 (2 k-blocks each)
-template <int HALF>
-__device__ __forceinline__ void chain_read_w(ChainIn& in, const uint8_t* ring, int lane) {
-  const int g4 = lane >> 4;
-#pragma unroll
-  for (int tb = 0; tb < 4; ++tb)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) in.fw[tb * 2 + j] = lds_frag(ring + rg::WN, tb * 4 + 2 * HALF + j, lane);
-  const float* hdr = reinterpret_cast<const float*>(ring + rg::HDR);
-  if (HALF == 0) {
-    in.usc = *reinterpret_cast<const f32x4*>(hdr + (ws::USC - ws::HDR) / 4);
-    in.u[0] = *reinterpret_cast<const f16x8*>(ring + rg::U + lane * 32);
-    in.u[1] = *reinterpret_cast<const f16x8*>(ring + rg::U + lane * 32 + 16);
-  }
-  in.gl = hdr[(ws::GL - ws::HDR) / 4];
-  in.ksc = hdr[(ws::KSC - ws::HDR) / 4];
-  in.kap = hdr[(ws::KAP - ws::HDR) / 4];
-#pragma unroll
-  for (int tb = 0; tb < 4; ++tb) in.dv[tb] = *reinterpret_cast<const f32x4*>(hdr + 16 * tb + 4 * g4);
-}
-// U -> fp32 with its tile scales (1 unless |U| left [2^-4, 2^14); same value in every lane), done
-// once the reads have landed, off the next step's critical path.
-__device__ __forceinline__ void chain_u_convert(ChainIn& in) {
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    in.uf[0][r] = (float)in.u[0][r];
-    in.uf[1][r] = (float)in.u[0][4 + r];
-    in.uf[2][r] = (float)in.u[1][r];
-    in.uf[3][r] = (float)in.u[1][4 + r];
-  }
-  const bool unit = in.usc[0] == 1.0f && in.usc[1] == 1.0f && in.usc[2] == 1.0f && in.usc[3] == 1.0f;
-  if (!__builtin_amdgcn_readfirstlane((int)unit)) {
-#pragma unroll
-    for (int tb = 0; tb < 4; ++tb) in.uf[tb] *= in.usc[tb];
-  }
-}
-template <int HALF>
-__device__ __forceinline__ void chain_read_k(KFrags& fk, const uint8_t* ring, int lane) {
-#pragma unroll
-  for (int f = 0; f < 8; ++f) fk[f] = lds_frag_h(ring + rg::KT, 8 * HALF + f, lane);
-}
-// Bounded waits: `limit` polls, then the wait gives up and raises the device status word (read
-// back by gdn_device_status), so a broken invariant neither hangs the GPU nor passes silently.
-struct WaitCtl {
-  int limit;
-  int* status;
-};
-// Wait until the other chain wave has published step `target` (it always publishes before it waits
-// itself, so the wait ends; the bound only keeps a broken invariant from hanging the GPU).  Program
-// order suffices after it for the same reason as in set_flag.
-__device__ __forceinline__ void wait_flag(int* flag, int target, const WaitCtl& wc, int lane) {
-  int i = 0;
-  for (; i < wc.limit; ++i) {
-    const int v = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    if (__builtin_amdgcn_readfirstlane(v) == target) break;
-  }
-  if (i == wc.limit && lane == 0) __hip_atomic_fetch_or(wc.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  asm volatile("" ::: "memory");  // the partial-sum reads stay behind the flag read
-}
-// Publish step `value` after this wave's earlier LDS writes.  LDS performs a CU's operations in one
-// global order, one wave's in program order, so a reader that sees the flag and then reads the
-// partial sums sees them written: no fence (and no wait for the writes) is needed, only program
-// order, which the compiler barriers keep.
-__device__ __forceinline__ void set_flag(int* flag, int value, int lane) {
-  asm volatile("" ::: "memory");
-  if (lane == 0) __hip_atomic_store(flag, value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-// The loader waves move a chunk's ring operands straight from L2 into LDS with global_load_lds
-// (16 bytes per lane: one wave instruction fills one 1 KiB fragment, lane l at byte 16 l), so the
-// data never passes through registers and the loaders issue no LDS stores.  Fragments of one
-// chunk: WN 0..15 and KT 0..15 (KT from the key head's record rec_kq), U fragments 2n, 2n+1 of
-// slice n, and the 512-byte header (lanes < 32).  Loader wave 0 issues WN 0-7, KT 0-7, U 0 and
-// the header (kDmaOps0 instructions), wave 1 WN 8-15, KT 8-15 and U 1 (kDmaOps1).
-constexpr int kDmaOps0 = 18, kDmaOps1 = 17;
-__device__ __forceinline__ void dma_frag(uint8_t* lds, const uint8_t* src, int lane) {
-  __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(src + lane * 16),
-                                   reinterpret_cast<uint32_t*>(lds), 16, 0, 0);
-}
-// The 128 x 16 fp32 initial-state slice at src (row pitch D floats) into an init_buf (row-major,
-// 64 bytes a row): 8 instructions, loader wave wl issues 4 (kInitOps).
-constexpr int kInitOps = 4;
-__device__ __forceinline__ void init_dma(float* dst, const float* src, int wl, int lane) {
-#pragma unroll
-  for (int i = kInitOps * wl; i < kInitOps * wl + kInitOps; ++i) {
-    const int p = 64 * i + lane;  // 16-byte piece: row p / 4, columns 4 (p % 4) ..
-    __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(src + (p >> 2) * pf::D + 4 * (p & 3)),
-                                     reinterpret_cast<uint32_t*>(dst + 256 * i), 16, 0, 0);
-  }
-}
-// L2 prefetch of the lines slice n of a head reads from one chunk's records: its eighth of WN, KT
-// (key head's record) and QG (key head's record), its U tiles, an eighth of QK, the header and
-// the row factors -- 78 lines of 128 bytes, 2 instructions.  Each lane copies one dword of its
-// line into pf_sink (4-byte global_load_lds), so nothing lands in registers; the lines stay in the
-// XCD's L2 for the other slices, which run on the same XCD.
-__device__ __forceinline__ void scan_prefetch(uint32_t* sink, const uint8_t* rec, const uint8_t* rec_kq, int n,
-                                              int lane) {
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int x = 64 * i + lane;
-    const uint8_t* p = nullptr;
-    if (x < 16) p = rec + ws::WN + (16 * n + x) * 128;
-    else if (x < 32) p = rec_kq + ws::KT + (16 * n + x - 16) * 128;
-    else if (x < 48) p = rec + ws::U + n * 2048 + (x - 32) * 128;
-    else if (x < 64) p = rec_kq + ws::QG + (16 * n + x - 48) * 128;
-    else if (x < 72) p = rec + ws::QK + (8 * n + x - 64) * 128;
-    else if (x < 76) p = rec + ws::HDR + (x - 72) * 128;
-    else if (x < 78) p = rec + ws::EGS + (x - 76) * 128;
-    if (p) __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t*>(p), sink, 4, 0, 0);
-  }
-}
-__device__ __forceinline__ void scan_dma(uint8_t* dst, const uint8_t* rec, const uint8_t* rec_kq, int n, int wl,
-                                         int lane) {
-#pragma unroll
-  for (int i = 0; i < 8; ++i) dma_frag(dst + rg::WN + (8 * wl + i) * ws::FRAG, rec + ws::WN + (8 * wl + i) * ws::FRAG, lane);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) dma_frag(dst + rg::KT + (8 * wl + i) * ws::FRAG, rec_kq + ws::KT + (8 * wl + i) * ws::FRAG, lane);
-  dma_frag(dst + rg::U + wl * ws::FRAG, rec + ws::U + n * 2048 + wl * ws::FRAG, lane);
-  if (wl == 0 && lane < 32) dma_frag(dst + rg::HDR, rec + ws::HDR, lane);
-}
-// Wait until every chunk but the most recently issued one has landed in LDS (keep: the newest
-// chunk's copies may stay in flight) -- per-wave instruction counts, the loaders issue nothing else.
-__device__ __forceinline__ void dma_wait(int wl, bool keep) {
-  if (!keep) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  else if (wl == 0) asm volatile("s_waitcnt vmcnt(18)" ::: "memory");
-  else asm volatile("s_waitcnt vmcnt(17)" ::: "memory");
-}
-static_assert(kDmaOps0 == 18 && kDmaOps1 == 17, "dma_wait's counts follow scan_dma");
-// The loaders' workgroup barrier.  __syncthreads() would also wait for every copy in flight (its
-// release fence covers the LDS the copies write); the loaders order their copies themselves with
-// dma_wait, so they meet the other waves at the bare barrier.  The LDS reads of a slot by the
-// other waves complete before those waves reach the barrier (their __syncthreads waits for them),
-// so a copy issued after the barrier cannot overtake them.
-__device__ __forceinline__ void loader_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-// The chain and output waves' workgroup barrier: it waits for their own LDS accesses (lgkmcnt 0),
-// which is all the other waves depend on; their global loads and stores (the output waves' next
-// operands, the rows of o and of final states) stay in flight across it.
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
-// An output wave's per-chunk operands.  Output wave P handles token tiles A = P and B = 3 - P (one
-// and two non-zero QK fragments: tile tb has QK fragments (tb, j) for j <= tb / 2), so the two
-// output waves do equal work: its QG fragments (8, from the key head's record), its 3 QK fragments
-// and the row factors scale e^{G_t} of this lane's token in each of its tiles.
-struct OutFrags {
-  bf16x8 qg[8], qk[3];
-  float egs[2];
-};
-template <int P>
-__device__ __forceinline__ void out_load(OutFrags& f, const uint8_t* rec, const uint8_t* rec_kq, int lane) {
-  constexpr int A = P, B = 3 - P;
-  const float* eg = reinterpret_cast<const float*>(rec + ws::EGS) + (lane & 15);
-  f.egs[0] = eg[16 * A];
-  f.egs[1] = eg[16 * B];
-  const uint8_t* qg = rec_kq + ws::QG + lane * 16;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    f.qg[j] = *reinterpret_cast<const bf16x8*>(qg + (A * 4 + j) * ws::FRAG);
-    f.qg[4 + j] = *reinterpret_cast<const bf16x8*>(qg + (B * 4 + j) * ws::FRAG);
-  }
-  const uint8_t* qk = rec + ws::QK + lane * 16;
-  f.qk[0] = *reinterpret_cast<const bf16x8*>(qk + (A * 2) * ws::FRAG);
-  f.qk[1] = *reinterpret_cast<const bf16x8*>(qk + (B * 2) * ws::FRAG);
-  f.qk[2] = *reinterpret_cast<const bf16x8*>(qk + (B * 2 + 1) * ws::FRAG);
-}
-// o^T = S^T Qg^T + vn^T QK^T, tile by tile.  The k-slot ordered B fragments of S and vn are A
-// fragments of S^T and vn^T, and the QG / QK A fragments are B fragments of their transposes, so
-// the transposed products need no data movement -- and their accumulator layout gives each lane 4
-// consecutive output columns of one token: lane (c, g) holds o[16 tb + c][16 n + 4g .. 4g + 3].
-template <int P, typename OutT>
-__device__ __forceinline__ void out_step(const OutFrags& f, const uint8_t* xch, OutT* out, int64_t t0, int len,
-                                         int Hv, int h, int col0, int lane) {
-  using namespace pf;
-  constexpr int A = P, B = 3 - P;
-  bf16x8 sb[4], vb[2];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) sb[j] = lds_frag(xch, j, lane);
-#pragma unroll
-  for (int j = 0; j < 2; ++j) vb[j] = lds_frag(xch, 4 + j, lane);
-  f32x4 O[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    O[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) O[i] = mma(sb[j], f.qg[i * 4 + j], O[i]);
-    O[i] *= f.egs[i];
-  }
-  O[0] = mma(vb[0], f.qk[0], O[0]);
-  O[1] = mma(vb[0], f.qk[1], O[1]);
-  O[1] = mma(vb[1], f.qk[2], O[1]);
-  const int c16 = lane & 15, g4 = lane >> 4;
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int row = 16 * (i == 0 ? A : B) + c16;
-    if (row < len) {
-      OutT* o = out + ((t0 + row) * Hv + h) * D + col0 + 4 * g4;
-      if constexpr (sizeof(OutT) == 2) {
-        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-        const u32x2 pk = {f2bf2(O[i][0], O[i][1]), f2bf2(O[i][2], O[i][3])};
-        *reinterpret_cast<u32x2*>(o) = pk;
-      } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) Elem<OutT>::store(o + r, O[i][r]);
-      }
-    }
-  }
-}
-// An output wave: step c computes chunk c-1 of the stream (F0 / F1: even / odd chunks, loaded two
-// chunks ahead; the walk follows chunk c-1 for its sequence position).
-template <int P, typename OutT>
-__device__ __forceinline__ void output_wave(const ScanSmem& sm, const uint8_t* rec0, int64_t rstride,
-                                            int64_t kq_off, OutT* out, const SeqTable& tab, int s_lo, int s_hi,
-                                            int nch, int Hv, int h, int col0, int lane) {
-  using namespace pf;
-  Walk w;
-  walk_begin(w, tab, s_lo, s_hi);
-  OutFrags F0, F1;
-  if (nch > 0) out_load<P>(F0, rec0, rec0 + kq_off, lane);
-  lds_barrier();  // prologue
-  if (nch > 1) out_load<P>(F1, rec0 + rstride, rec0 + rstride + kq_off, lane);
-  lds_barrier();  // step 0
-  int xp = 0;        // (c - 1) % 3
-  for (int c = 1; c <= nch; c += 2) {
-    {
-      const int len = w.L - w.c * CH < CH ? w.L - w.c * CH : CH;
-      out_step<P, OutT>(F0, sm.xch[xp], out, w.t0 + (int64_t)w.c * CH, len, Hv, h, col0, lane);
-      walk_next(w, tab, s_hi);
-      if (c + 1 < nch) out_load<P>(F0, rec0 + (int64_t)(c + 1) * rstride, rec0 + (int64_t)(c + 1) * rstride + kq_off, lane);
-      xp = xp == 2 ? 0 : xp + 1;
-      lds_barrier();  // end of step c
-    }
-    if (c + 1 <= nch) {
-      const int len = w.L - w.c * CH < CH ? w.L - w.c * CH : CH;
-      out_step<P, OutT>(F1, sm.xch[xp], out, w.t0 + (int64_t)w.c * CH, len, Hv, h, col0, lane);
-      walk_next(w, tab, s_hi);
-      if (c + 2 < nch) out_load<P>(F1, rec0 + (int64_t)(c + 2) * rstride, rec0 + (int64_t)(c + 2) * rstride + kq_off, lane);
-      xp = xp == 2 ? 0 : xp + 1;
-      lds_barrier();  // end of step c+1
-    }
-  }
-}
-
-// What a chain step does after its update when its chunk ends a sequence: store this lane's final
-// state column (fin; nullptr: not kept) and continue from the next sequence's initial state (nxt:
-// this lane's column of an init_buf; nullptr: zeros).
-struct Swap {
-  bool last;
-  float* fin;
-  const float* nxt;
-};
-template <int HALF>
-__device__ __forceinline__ void chain_step(ScanSmem& sm, f32x4 (&S)[4], bf16x8 (&Sb)[2], ChainIn& in, KFrags& fk,
-                                           KFrags& fk_next, int c, int nch, int& x0, const Swap& sw,
-                                           const WaitCtl& wc, int lane) {
-  uint8_t* xch = sm.xch[x0];
-  const int x1 = x0 == 2 ? 0 : x0 + 1;
-  const uint8_t* nxt = sm.ring[x1];  // chunk c+1 sits in ring slot (c+1) % 3
-  // this wave's half of the k-sum: U (wave 0) + sum over S rows 64 HALF.. of WN S
-  f32x4 acc[4];
-  if (HALF == 0) {
-#pragma unroll
-    for (int tb = 0; tb < 4; ++tb) acc[tb] = in.uf[tb];
-  } else {
-#pragma unroll
-    for (int tb = 0; tb < 4; ++tb) acc[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-#pragma unroll
-  for (int j = 0; j < 2; ++j)
-#pragma unroll
-    for (int tb = 0; tb < 4; ++tb) acc[tb] = mma(in.fw[tb * 2 + j], Sb[j], acc[tb]);
-  // publish the partial sum, then the step flag (one wave's LDS writes complete in order)
-#pragma unroll
-  for (int tb = 0; tb < 4; ++tb) sm.part[HALF][tb][lane] = acc[tb];
-  set_flag(&sm.flag[HALF], c + 1, lane);
-  f32x4 dv[4];
-#pragma unroll
-  for (int tb = 0; tb < 4; ++tb) dv[tb] = in.dv[tb];
-  const float gl = in.gl, ksc = in.ksc, kap = in.kap;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    S[i] *= gl;
-    asm volatile("" : "+v"(S[i]));  // done while the other wave finishes its half
-  }
-  wait_flag(&sm.flag[1 - HALF], c + 1, wc, lane);
-  // vn = U - W S: both waves add the same two partial sums (a + b == b + a exactly)
-  f32x4 vn[4];
-#pragma unroll
-  for (int tb = 0; tb < 4; ++tb) vn[tb] = acc[tb] + sm.part[1 - HALF][tb][lane];
-#pragma unroll
-  for (int tb = 0; tb < 4; ++tb) asm volatile("" : "+v"(vn[tb]));  // complete before the reads below
-  // chunk c+1's operands: issued behind the partial-sum reads (whose completion the chain waits
-  // for; LDS returns in order and the wait counter saturates at 15), so they arrive while this
-  // chunk's update runs
-  __builtin_amdgcn_sched_barrier(0);
-  if (c + 1 < nch) {
-    chain_read_w<HALF>(in, nxt, lane);
-    chain_read_k<HALF>(fk_next, nxt, lane);
-  }
-  // DEC vn -> fp16; wave 1 publishes vn (bf16) for the output waves
-  float m = 0.f;
-#pragma unroll
-  for (int tb = 0; tb < 4; ++tb)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      dv[tb][r] *= vn[tb][r];
-      m = fmaxf(m, fabsf(dv[tb][r]));
-    }
-  if (HALF == 1) {
 #pragma unroll
     for (int j = 0; j < 2; ++j)
-      *reinterpret_cast<bf16x8*>(&xch[(4 + j) * ws::FRAG + lane * 16]) = pack_acc_bf16(vn[2 * j], vn[2 * j + 1]);
+      if (2 * j <= W)
+        *reinterpret_cast<bf16x8*>(B.qk + (W * 2 + j) * ws::FRAG + lane * 16) = pack_acc_bf16(qk[2 * j], qk[2 * j + 1]);
   }
-  // Fast path (the usual case): kappa = 1 and every |DEC vn| below 2^14 with the largest at
-  // least 2^-4, so DEC vn goes to fp16 unscaled.  Otherwise: per-column power-of-two scaling.
-  // Both waves hold the same DEC vn, so they take the same path.
-  const bool fast = kap == 1.0f && __builtin_amdgcn_ballot_w64(m >= 16384.0f) == 0 &&
-                    __builtin_amdgcn_ballot_w64(m >= 0.0625f) != 0;
-  if (__builtin_amdgcn_readfirstlane((int)fast)) {
-    f16x8 vh[2];
+  f32x4 accW[8];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) vh[j] = pack_acc_f16(dv[2 * j], dv[2 * j + 1], 1.0f);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      S[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fk[i * 2], vh[0], S[i], 0, 0, 0);
-      S[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fk[i * 2 + 1], vh[1], S[i], 0, 0, 0);
-    }
-  } else {
-    m = fmaxf(m, __shfl_xor(m, 16, kWave));
-    m = fmaxf(m, __shfl_xor(m, 32, kWave));
-    const int se = fp16_scale_exp(m);
-    f16x8 vh[2];
-    const float sigma = ldexpf(1.0f, se);
-#pragma unroll
-    for (int j = 0; j < 2; ++j) vh[j] = pack_acc_f16(dv[2 * j], dv[2 * j + 1], sigma);
-    const float pre = sigma * kap;        // exact powers of two
-    const float post = ldexpf(ksc, -se);  // 1 / (sigma * kappa)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      S[i] *= pre;
-      S[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fk[i * 2], vh[0], S[i], 0, 0, 0);
-      S[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fk[i * 2 + 1], vh[1], S[i], 0, 0, 0);
-      S[i] *= post;
-    }
+  for (int cb = 0; cb < 8; ++cb) {
+    accW[cb] = mma(__builtin_bit_cast(bf16x8, frag_tr(B.K, LDK, 0, 16 * cb, lane)), tbe[0], f32x4{0.f, 0.f, 0.f, 0.f});
+    if (W >= 2) accW[cb] = mma(__builtin_bit_cast(bf16x8, frag_tr(B.K, LDK, 32, 16 * cb, lane)), tbe[1], accW[cb]);
   }
-  // next chunk's U to fp32 while the update's MFMAs run
-  if (HALF == 0) chain_u_convert(in);
-  if (sw.last) {
-    const int g4 = lane >> 4;
-    if (sw.fin) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) sw.fin[(64 * HALF + 16 * i + 4 * g4 + r) * pf::D] = S[i][r];
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) S[i][r] = sw.nxt ? sw.nxt[(64 * HALF + 16 * i + 4 * g4 + r) * 16] : 0.f;
-  }
-  uint8_t* xn = sm.xch[x1];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    Sb[j] = pack_acc_bf16(S[2 * j], S[2 * j + 1]);
-    *reinterpret_cast<bf16x8*>(&xn[(2 * HALF + j) * ws::FRAG + lane * 16]) = Sb[j];
-  }
-  x0 = x1;
-  lds_barrier();  // end of step c
+  for (int j = 0; j < 4; ++j)
+    *reinterpret_cast<bf16x8*>(B.wn + (W * 4 + j) * ws::FRAG + lane * 16) = pack_acc_bf16(-accW[2 * j], -accW[2 * j + 1]);
 }
 
-// The chain wave holding S rows 64 HALF .. 64 HALF + 63 (4 accumulator tiles) of one 16-column
-// slice (this lane: column col) through every chunk of its group's sequences: at a sequence's last
-// chunk the step stores the final state and continues from the next sequence's initial state,
-// which the loader waves have staged in init_buf[(k + 1) & 1].  The walk runs one chunk ahead
-// (wn), so its table reads are in flight a whole step before they are needed.  The chain's
-// barriers wait only for its LDS accesses: its final-state stores need no ordering with the
-// other waves.
-template <int HALF>
-__device__ __forceinline__ void chain_wave(ScanSmem& sm, const float* __restrict__ init,
-                                           float* __restrict__ final_state, int Hv, int h, int col,
-                                           const SeqTable& tab, int s_lo, int s_hi, int nch, const WaitCtl& wc,
-                                           int lane) {
-  using namespace pf;
-  const int g4 = lane >> 4;
-  auto state_col = [&](const float* base, int row) -> const float* {  // this lane's column of a state
-    return (base && row >= 0) ? base + ((int64_t)row * Hv + h) * D * D + col : nullptr;
-  };
-  Walk w, wn;  // chunk c, chunk c+1
-  walk_begin(w, tab, s_lo, s_hi);
-  wn = w;
-  walk_next(wn, tab, s_hi);
-  f32x4 S[4];
-  const float* s0 = state_col(init, w.row);
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) S[i][r] = s0 ? s0[(64 * HALF + 16 * i + 4 * g4 + r) * D] : 0.f;
-  bf16x8 Sb[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    Sb[j] = pack_acc_bf16(S[2 * j], S[2 * j + 1]);
-    *reinterpret_cast<bf16x8*>(&sm.xch[0][(2 * HALF + j) * ws::FRAG + lane * 16]) = Sb[j];
-  }
-  if (lane == 0) sm.flag[HALF] = 0;
-  lds_barrier();  // prologue
-  ChainIn in;
-  KFrags fk0, fk1;  // chunks c even / odd
-  if (nch > 0) {
-    chain_read_w<HALF>(in, sm.ring[0], lane);
-    if (HALF == 0) chain_u_convert(in);
-    chain_read_k<HALF>(fk0, sm.ring[0], lane);
-  }
-  auto swap_of = [&]() {
-    Swap sw{false, nullptr, nullptr};
-    if (walk_last(w)) {  // then wn is the first chunk of the next non-empty sequence (if any)
-      sw.last = true;
-      sw.fin = const_cast<float*>(state_col(final_state, w.row));
-      if (state_col(init, wn.row)) sw.nxt = sm.init_buf[(w.k + 1) & 1] + (lane & 15);
-    }
-    return sw;
-  };
-  int x0 = 0;  // c % 3
-  for (int c = 0; c < nch; c += 2) {
-    chain_step<HALF>(sm, S, Sb, in, fk0, fk1, c, nch, x0, swap_of(), wc, lane);
-    w = wn;
-    walk_next(wn, tab, s_hi);
-    if (c + 1 < nch) {
-      chain_step<HALF>(sm, S, Sb, in, fk1, fk0, c + 1, nch, x0, swap_of(), wc, lane);
-      w = wn;
-      walk_next(wn, tab, s_hi);
-    }
-  }
-  lds_barrier();  // step nch (the output waves' last chunk)
+// x = hi + lo with hi = bf16(x), lo = bf16(x - hi): 8 accumulator values (two tiles) as two k-slot
+// ordered bf16 fragments; hi + lo carries about 16 significant bits.
+__device__ __forceinline__ void split_bf16(f32x4 a, f32x4 b, bf16x8& hi, bf16x8& lo) {
+  hi = pack_acc_bf16(a, b);
+  const u32x4v h = __builtin_bit_cast(u32x4v, hi);
+  f32x4 ra, rb;
+  ra[0] = a[0] - __uint_as_float(h[0] << 16);
+  ra[1] = a[1] - __uint_as_float(h[0] & 0xffff0000u);
+  ra[2] = a[2] - __uint_as_float(h[1] << 16);
+  ra[3] = a[3] - __uint_as_float(h[1] & 0xffff0000u);
+  rb[0] = b[0] - __uint_as_float(h[2] << 16);
+  rb[1] = b[1] - __uint_as_float(h[2] & 0xffff0000u);
+  rb[2] = b[2] - __uint_as_float(h[3] << 16);
+  rb[3] = b[3] - __uint_as_float(h[3] & 0xffff0000u);
+  lo = pack_acc_bf16(ra, rb);
 }
 
-// The scan: one workgroup per (sequence group, value head, 16-column slice).  A group is a run of
-// whole sequences; its chunk records are consecutive workspace slots, so the workgroup streams
-// them in order and carries the state across sequence boundaries (groups == nseq: one sequence per
-// workgroup).
-template <typename OutT>
-__global__ __launch_bounds__(kScanThreads, 1) void chunk_scan_kernel(
-    const float* __restrict__ init, float* __restrict__ final_state, OutT* __restrict__ out,
-    const int32_t* __restrict__ cu, const int32_t* __restrict__ seq_chunk0, const int32_t* __restrict__ rows,
-    int n_rows, int nseq, int seq_len, int Hqk, int Hv, int groups, int64_t total_chunks,
-    const uint8_t* __restrict__ work, WaitCtl wc) {
+// A chain wave's state: columns 32 w' .. 32 w' + 31 of the value head's [128, 128] fp32 state as two
+// 16-column slices (n = 2 w' + sl), S[sl][i][r] = S[16 i + 4 g + r][16 n + c].
+struct ChainRegs {
+  f32x4 S[2][8];
+  bf16x8 hi[2][2], lo[2][2];  // DEC vn, split, carried from part 1 to part 2
+};
+// Chain part 1 for one chunk: U (fp32, from the inverse kernel's T diag(beta) fragments and the V
+// rows), vn = U - W S, the outputs o = diag(scale e^G) Q S + QK vn, and DEC vn split for part 2.
+template <bool kUseU>
+__device__ __forceinline__ void chain_part1(const SegBuf& B, ChainRegs& R, const bf16x8 (&tbv)[tf::FRAGS], bool out_on,
+                                            uint16_t* __restrict__ out, int64_t t0, int len, int Hv, int h, int wc,
+                                            int lane_in) {
   using namespace pf;
-  __shared__ ScanSmem sm;
-  // block -> (group-head pair, slice); the 8 slices of a pair share blockIdx % 8 and therefore an
-  // XCD (workgroups are dispatched round-robin over the 8 XCDs), so they share one L2.
-  const int b = blockIdx.x;
-  const int pair = (b >> 6) * 8 + (b & 7), n = (b >> 3) & 7;
-  if (pair >= groups * Hv) return;
-  const int h = pair % Hv, grp = pair / Hv;
-  const SeqTable tab{cu, seq_chunk0, rows, n_rows, seq_len, (seq_len + CH - 1) / CH};
-  int s_lo, s_hi;
-  if (groups == nseq) {
-    s_lo = grp;
-    s_hi = grp + 1;
-  } else {
-    s_lo = group_start(tab, nseq, total_chunks, groups, grp);
-    s_hi = group_start(tab, nseq, total_chunks, groups, grp + 1);
-  }
-  if (s_lo >= s_hi) return;
-  const int slot0 = tab.first_chunk(s_lo);
-  const int nch = tab.first_chunk(s_hi) - slot0;  // chunks of the group's stream
-  const int t = threadIdx.x, lane = t & 63, c16 = lane & 15;
-  const int role = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int64_t rstride = (int64_t)Hv * ws::BYTES;
-  const uint8_t* rec0 = work + (int64_t)slot0 * rstride + (int64_t)h * ws::BYTES;
-  const int64_t kq_off = -(int64_t)(h % (Hv / Hqk)) * ws::BYTES;  // record of the key head's owner
-  const int col = 16 * n + c16;
-
-  if (role < 2) {
-    // ---------------- chain waves ----------------
-    if (role == 0) chain_wave<0>(sm, init, final_state, Hv, h, col, tab, s_lo, s_hi, nch, wc, lane);
-    else chain_wave<1>(sm, init, final_state, Hv, h, col, tab, s_lo, s_hi, nch, wc, lane);
-  } else if (role < 4) {
-    // ---------------- output waves: step c computes chunk c-1 ----------------
-    if (role == 2) output_wave<0, OutT>(sm, rec0, rstride, kq_off, out, tab, s_lo, s_hi, nch, Hv, h, 16 * n, lane);
-    else output_wave<1, OutT>(sm, rec0, rstride, kq_off, out, tab, s_lo, s_hi, nch, Hv, h, 16 * n, lane);
-  } else if (role == 6) {
-    // ---------------- prefetch wave: chunk c + kPrefetchAhead at step c ----------------
-    // Its copies are never waited for until the end (their own wave's counter), so a slow HBM
-    // fetch delays nothing; at most a few dozen are in flight.
-    auto touch = [&](int c) {
-      const uint8_t* rec = rec0 + (int64_t)c * rstride;
-      scan_prefetch(sm.pf_sink, rec, rec + kq_off, n, lane);
-    };
-    for (int c = 3; c < kPrefetchAhead && c < nch; ++c) touch(c);
-    loader_barrier();  // prologue
-    for (int c = 0; c < nch; ++c) {
-      if (c + kPrefetchAhead < nch) touch(c + kPrefetchAhead);
-      loader_barrier();  // end of step c
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no copy may land after the workgroup ends
-    loader_barrier();  // step nch
-  } else {
-    // ---------------- loader waves ----------------
-    const int wl = role - 4, lt = t - 256;
-    // Empty sequences have no chunks: their final state is their initial state (zeros without
-    // one).  Loader lane lt copies row lt of the slice.
-    if (final_state) {
-      for (int s = s_lo; s < s_hi; ++s) {
-        if (tab.len(s) != 0) continue;
-        const int r = state_row(rows, n_rows, s);
-        if (r < 0) continue;
-        const int64_t off = ((int64_t)r * Hv + h) * D * D + (int64_t)lt * D + 16 * n;
+  int lane;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(lane) : "v"(lane_in));
+  const int c16 = lane & 15, g4 = lane >> 4;
+  bf16x8 Sb[2][4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const f32x4 x = init ? *reinterpret_cast<const f32x4*>(init + off + 4 * q) : f32x4{0.f, 0.f, 0.f, 0.f};
-          *reinterpret_cast<f32x4*>(final_state + off + 4 * q) = x;
+  for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) Sb[sl][j] = pack_acc_bf16(R.S[sl][2 * j], R.S[sl][2 * j + 1]);
+  f32x4 acc[2][4];
+#pragma unroll
+  for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) acc[sl][tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (kUseU) {  // U = T diag(beta) V, token tile tb, k-blocks kb <= tb / 2
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl) {
+      const int n = 2 * wc + sl;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const bf16x8 vf = __builtin_bit_cast(bf16x8, frag_tr(B.V, LDK, 32 * kb, 16 * n, lane));
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb)
+          if (2 * kb <= tb) acc[sl][tb] = mma(tbv[tf::fid(tb, kb)], vf, acc[sl][tb]);
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+      const bf16x8 a = lds_frag(B.wn, tb * 4 + j, lane);
+      acc[0][tb] = mma(a, Sb[0][j], acc[0][tb]);
+      acc[1][tb] = mma(a, Sb[1][j], acc[1][tb]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (out_on) {  // o^T tile by tile: lane (c, g) holds o[16 tb + c][16 n + 4 g .. 4 g + 3]
+    bf16x8 vb[2][2];
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl) {
+      vb[sl][0] = pack_acc_bf16(acc[sl][0], acc[sl][1]);
+      vb[sl][1] = pack_acc_bf16(acc[sl][2], acc[sl][3]);
+    }
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+      f32x4 O[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bf16x8 qf = lds_frag(B.qg, tb * 4 + j, lane);
+        O[0] = mma(Sb[0][j], qf, O[0]);
+        O[1] = mma(Sb[1][j], qf, O[1]);
+      }
+      const float e = B.egs[16 * tb + c16];
+      const bf16x8 k0 = lds_frag(B.qk, tb * 2, lane);
+#pragma unroll
+      for (int sl = 0; sl < 2; ++sl) {
+        O[sl] *= e;
+        O[sl] = mma(vb[sl][0], k0, O[sl]);
+      }
+      if (tb >= 2) {
+        const bf16x8 k1 = lds_frag(B.qk, tb * 2 + 1, lane);
+#pragma unroll
+        for (int sl = 0; sl < 2; ++sl) O[sl] = mma(vb[sl][1], k1, O[sl]);
+      }
+      const int row = 16 * tb + c16;
+      if (row < len) {
+#pragma unroll
+        for (int sl = 0; sl < 2; ++sl) {
+          typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+          const u32x2 pk = {f2bf2(O[sl][0], O[sl][1]), f2bf2(O[sl][2], O[sl][3])};
+          *reinterpret_cast<u32x2*>(out + ((t0 + row) * Hv + h) * D + 16 * (2 * wc + sl) + 4 * g4) = pk;
         }
       }
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the copies below count their own loads
+      __builtin_amdgcn_sched_barrier(0);
     }
-    // Chunk j sits in ring slot j % 3.  The chain reads chunk j's operands during step j-1 (chunk 0:
-    // after the prologue barrier), so from step j on that slot is free: step j (>= 1) starts the
-    // copy of chunk j+3 into it, and the copy has steps j and j+1 to land (chunk 3, started at
-    // step 1, has one step).  Before the barrier that ends step j, chunk j+2 must be complete.
-    // When chunk j+1 ends the k-th sequence, step j (the prologue for j+1 = 0) also copies the
-    // next sequence's initial state slice into init_buf[(k + 1) & 1], issued before the chunk
-    // copy, so it is complete at the same barrier; the chain reads it at the end of step j+1.
-    // The other buffer may still be read during that step, and a buffer is reused two sequences
-    // later, after the step that read it ended.
-    auto dma_chunk = [&](int c) {
-      const uint8_t* rec = rec0 + (int64_t)c * rstride;
-      scan_dma(sm.ring[c % 3], rec, rec + kq_off, n, wl, lane);
-    };
-    Walk w;  // follows chunk j+1
-    walk_begin(w, tab, s_lo, s_hi);
-    auto dma_next_init = [&]() {
-      if (!init || !walk_last(w)) return;
-      Walk w2 = w;  // the next non-empty sequence's first chunk
-      walk_next(w2, tab, s_hi);
-      if (w2.row >= 0) init_dma(sm.init_buf[(w.k + 1) & 1], init + ((int64_t)w2.row * Hv + h) * D * D + 16 * n, wl, lane);
-    };
-    if (nch > 0) dma_next_init();
-    if (nch > 0) dma_chunk(0);
-    if (nch > 1) dma_chunk(1);
-    if (nch > 2) dma_chunk(2);
-    dma_wait(wl, nch > 2);  // chunks 0 and 1 (and the initial state after chunk 0)
-    loader_barrier();       // prologue
-    for (int c = 0; c < nch; ++c) {
-      walk_next(w, tab, s_hi);
-      if (c + 1 < nch) dma_next_init();
-      if (c == 1 && 3 < nch) dma_chunk(3);
-      const bool issued = c >= 1 && c + 3 < nch;
-      if (issued) dma_chunk(c + 3);
-      dma_wait(wl, issued);  // chunk c+2 (and the initial state after chunk c+1)
-      loader_barrier();      // end of step c
+  }
+  // DEC vn -> hi + lo bf16 (k-slot ordered B fragments of the update)
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) {
+    const f32x4 dec = *reinterpret_cast<const f32x4*>(&B.dec[16 * tb + 4 * g4]);
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl) acc[sl][tb] *= dec;
+  }
+#pragma unroll
+  for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) split_bf16(acc[sl][2 * j], acc[sl][2 * j + 1], R.hi[sl][j], R.lo[sl][j]);
+}
+// Chain part 2: S' = e^{G_last} S + K^T (DEC vn), K^T straight from the K rows (exact in bf16).
+__device__ __forceinline__ void chain_part2(const SegBuf& B, ChainRegs& R, int lane_in) {
+  using namespace pf;
+  int lane;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(lane) : "v"(lane_in));
+  const float gl = B.gl;
+#pragma unroll
+  for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) R.S[sl][i] *= gl;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const bf16x8 kt = __builtin_bit_cast(bf16x8, frag_tr_kperm(B.K, LDK, 32 * j, 16 * i, lane));
+#pragma unroll
+      for (int sl = 0; sl < 2; ++sl) {
+        R.S[sl][i] = mma(kt, R.hi[sl][j], R.S[sl][i]);
+        R.S[sl][i] = mma(kt, R.lo[sl][j], R.S[sl][i]);
+      }
     }
-    dma_wait(wl, false);
-    loader_barrier();  // step nch
+    if (i & 1) __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// Segment kernel.  pass 0 (output): one workgroup per (segment, value head) from the segment's
+// initial state (the sequence's initial state row, zero, or the combined state of the previous
+// segment in its transition slot), writing o and, at a sequence's last segment, the final state.
+// pass 1 (summary): two workgroups per (transition slot, value head): B (from zero, with U) and A
+// (from the identity, without U), written into the slot; A is skipped when negligible.
+// Waves 0-3 (local) prepare chunk c+1's operands in one buffer while waves 4-7 (chain) run chunk c
+// from the other: two LDS barriers a chunk, met by both roles.
+template <typename BetaT, typename OutT, int kPass>
+__global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
+    const uint16_t* __restrict__ q, int64_t qs, const uint16_t* __restrict__ k, int64_t ks,
+    const uint16_t* __restrict__ v, int64_t vs, const float* __restrict__ g, const BetaT* __restrict__ beta,
+    OutT* __restrict__ out, SegTable tab, int Hqk, int Hv, int use_l2, const float* __restrict__ init,
+    const int32_t* __restrict__ rows, int n_rows, float* __restrict__ final_state, float* __restrict__ trans,
+    int* __restrict__ tflags, const uint8_t* __restrict__ tfrag) {
+  using namespace pf;
+  __shared__ SegSmem sm;
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
+  int mode, h, s, idx, slot = -1;
+  if (kPass == 0) {
+    const int item = blockIdx.x, j = item / Hv;
+    h = item % Hv;
+    if (j >= tab.first_seg(tab.nseq)) return;
+    s = tab.seq_of_seg(j);
+    idx = j - tab.first_seg(s);
+    if (idx > 0) slot = tab.first_slot(s) + idx - 1;  // the previous segment's slot holds this one's state
+    mode = kSegOut;
+  } else {
+    const int item = blockIdx.x, rest = item >> 1;
+    const int ts = rest / Hv;
+    h = rest % Hv;
+    if (ts >= tab.first_slot(tab.nseq)) return;
+    s = tab.seq_of_slot(ts);
+    idx = ts - tab.first_slot(s);
+    slot = ts;
+    mode = (item & 1) ? kSegA : kSegB;
+  }
+  const int kh = h / (Hv / Hqk);
+  const int nch_s = tab.nch(s), c_begin = idx * tab.L;
+  const int n = nch_s - c_begin < tab.L ? nch_s - c_begin : tab.L;
+  const int64_t t_seq = tab.start(s);
+  const int Ls = tab.len(s);
+  float* tslot = slot >= 0 ? trans + ((int64_t)slot * Hv + h) * sg::kTrans : nullptr;
+  if (mode == kSegA) {  // is A negligible?  (exp of the summed log decay, unit keys, beta in [0, 1])
+    int compute = 1;
+    if (use_l2) {
+      const int64_t tb0 = t_seq + (int64_t)c_begin * CH;
+      const int ntok = (Ls - c_begin * CH) < n * CH ? Ls - c_begin * CH : n * CH;
+      float sum = 0.f;
+      int ok = 1;
+      for (int i = t; i < ntok; i += sg::NT) {
+        sum += g[(tb0 + i) * Hv + h];
+        const float b = Elem<BetaT>::load(beta + (tb0 + i) * Hv + h);
+        ok &= (b >= 0.f && b <= 1.f) ? 1 : 0;
+      }
+      sum = wave_sum_fast(sum);
+      ok = __builtin_amdgcn_ballot_w64(ok == 0) == 0 ? 1 : 0;
+      if (lane == 0) sm.red[w] = ok ? sum : __builtin_huge_valf();
+      __syncthreads();
+      float tot = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) tot += sm.red[i];
+      compute = tot < sg::kNegligibleLog ? 0 : 1;  // NaN or a beta outside [0, 1]: computed
+    }
+    if (t == 0) tflags[(int64_t)slot * Hv + h] = compute;
+    if (!compute) return;
+  }
+  constexpr bool need_q = kPass == 0;
+  const int chunk_slot0 = tab.first_chunk(s) + c_begin;
+  auto tfr = [&](int c) { return tfrag + ((int64_t)(chunk_slot0 + c) * Hv + h) * tf::BYTES; };
+  auto chunk_t0 = [&](int c) { return t_seq + (int64_t)(c_begin + c) * CH; };
+  auto chunk_len = [&](int c) { return Ls - (c_begin + c) * CH < CH ? Ls - (c_begin + c) * CH : CH; };
+  if (w < 4) {
+    // ------------------------------------------------------------ local waves
+    LocIn in;
+    bf16x8 qf[4], tbe[2];
+    float G = 0.f;
+    auto load = [&](int c) {
+      loc_load<need_q>(in, chunk_t0(c), chunk_len(c), kh, h, q, qs, k, ks, v, vs, g, Hv, tfr(c));
+    };
+    auto phase2 = [&](SegBuf& B) {
+      switch (w) {
+        case 0: loc_phase2<0, need_q>(B, qf, G, tbe); break;
+        case 1: loc_phase2<1, need_q>(B, qf, G, tbe); break;
+        case 2: loc_phase2<2, need_q>(B, qf, G, tbe); break;
+        default: loc_phase2<3, need_q>(B, qf, G, tbe); break;
+      }
+    };
+    if (n > 0) {
+      load(0);
+      loc_phase1<need_q>(sm.buf[0], in, use_l2, qf, G);
+      tbe[0] = in.tbe[0];
+      tbe[1] = in.tbe[1];
+      if (n > 1) load(1);
+    }
+    lds_barrier();
+    if (n > 0) phase2(sm.buf[0]);
+    lds_barrier();
+    for (int c = 0; c < n; ++c) {
+      const bool more = c + 1 < n;
+      if (more) {
+        loc_phase1<need_q>(sm.buf[(c + 1) & 1], in, use_l2, qf, G);
+        tbe[0] = in.tbe[0];
+        tbe[1] = in.tbe[1];
+        if (c + 2 < n) load(c + 2);
+      }
+      lds_barrier();
+      if (more) phase2(sm.buf[(c + 1) & 1]);
+      lds_barrier();
+    }
+  } else {
+    // ------------------------------------------------------------ chain waves
+    const int wc = w - 4;
+    ChainRegs R;
+    {  // initial state
+      const float* src = nullptr;
+      if (mode == kSegOut) {
+        if (slot >= 0) src = tslot + D * D;
+        else if (init) {
+          const int r0 = state_row(rows, n_rows, s);
+          if (r0 >= 0) src = init + ((int64_t)r0 * Hv + h) * D * D;
+        }
+      }
+      if (src) {
+#pragma unroll
+        for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) R.S[sl][i][r] = src[(16 * i + 4 * g4 + r) * D + 32 * wc + 16 * sl + c16];
+      } else {
+#pragma unroll
+        for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              R.S[sl][i][r] = (mode == kSegA && 16 * i + 4 * g4 + r == 32 * wc + 16 * sl + c16) ? 1.f : 0.f;
+      }
+    }
+    bf16x8 tb[tf::FRAGS], tbn[tf::FRAGS];
+    auto tload = [&](bf16x8 (&dst)[tf::FRAGS], int c) {
+      const uint8_t* p = tfr(c) + tf::FRAGS * ws::FRAG + lane * 16;
+#pragma unroll
+      for (int f = 0; f < tf::FRAGS; ++f) dst[f] = *reinterpret_cast<const bf16x8*>(p + f * ws::FRAG);
+    };
+    if (mode != kSegA && n > 0) tload(tb, 0);
+    lds_barrier();
+    lds_barrier();
+    for (int c = 0; c < n; ++c) {
+      const SegBuf& B = sm.buf[c & 1];
+      if (mode != kSegA && c + 1 < n) tload(tbn, c + 1);
+      if (kPass == 0) chain_part1<true>(B, R, tb, true, out, chunk_t0(c), chunk_len(c), Hv, h, wc, lane);
+      else if (mode == kSegB) chain_part1<true>(B, R, tb, false, out, 0, 0, Hv, h, wc, lane);
+      else chain_part1<false>(B, R, tb, false, out, 0, 0, Hv, h, wc, lane);
+      lds_barrier();
+      chain_part2(B, R, lane);
+#pragma unroll
+      for (int f = 0; f < tf::FRAGS; ++f) tb[f] = tbn[f];
+      lds_barrier();
+    }
+    // the state after the segment
+    float* dst = nullptr;
+    if (mode == kSegOut) {
+      if (final_state && idx == tab.nseg_of(nch_s) - 1) {
+        const int r0 = state_row(rows, n_rows, s);
+        if (r0 >= 0) dst = final_state + ((int64_t)r0 * Hv + h) * D * D;
+      }
+    } else {
+      dst = tslot + (mode == kSegA ? 0 : D * D);
+    }
+    if (dst) {
+#pragma unroll
+      for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) dst[(16 * i + 4 * g4 + r) * D + 32 * wc + 16 * sl + c16] = R.S[sl][i][r];
+    }
+  }
+}
+
+// S_{j+1} = A_j S_j + B_j along each sequence's segments, in fp32 (v_mfma_f32_16x16x4_f32); the result
+// overwrites B_j, which the output pass reads as segment j+1's initial state.  One workgroup per
+// (sequence with transition slots, value head, 16-column slice), started at the sequence's first
+// slot; the 8 slices of a (slot, head) share blockIdx % 8, hence an XCD and its L2.  A_j flagged
+// negligible is skipped: S_{j+1} = B_j as written.
+struct CombineSmem {
+  float A[pf::D * (pf::D + 4)];
+  float S[pf::D * 16];
+};
+__global__ __launch_bounds__(256) void seg_combine_kernel(SegTable tab, int Hv, const float* __restrict__ init,
+                                                         const int32_t* __restrict__ rows, int n_rows,
+                                                         float* __restrict__ trans, const int* __restrict__ tflags) {
+  using namespace pf;
+  __shared__ CombineSmem sm;
+  const int b = blockIdx.x;
+  const int item = (b >> 6) * 8 + (b & 7), n = (b >> 3) & 7;
+  const int ts = item / Hv, h = item % Hv;
+  if (ts >= tab.first_slot(tab.nseq)) return;
+  const int s = tab.seq_of_slot(ts);
+  if (ts != tab.first_slot(s)) return;
+  const int nsl = tab.first_slot(s + 1) - ts;
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  const int LDA = D + 4;
+  const float* s0 = nullptr;
+  if (init) {
+    const int r0 = state_row(rows, n_rows, s);
+    if (r0 >= 0) s0 = init + ((int64_t)r0 * Hv + h) * D * D;
+  }
+  // S slice: row p / 16 ... thread t holds rows t / 16 + 16 m, column t % 16
+  for (int i = t; i < D * 16; i += 256) sm.S[i] = s0 ? s0[(i >> 4) * D + 16 * n + (i & 15)] : 0.f;
+  __syncthreads();
+  for (int kk = 0; kk < nsl; ++kk) {
+    float* base = trans + ((int64_t)(ts + kk) * Hv + h) * sg::kTrans;
+    float* Bm = base + D * D;
+    if (tflags[(int64_t)(ts + kk) * Hv + h]) {
+      for (int i = t; i < D * D / 4; i += 256) {
+        const f32x4 a = *reinterpret_cast<const f32x4*>(base + 4 * i);
+        *reinterpret_cast<f32x4*>(&sm.A[(i >> 5) * LDA + 4 * (i & 31)]) = a;
+      }
+      __syncthreads();
+      f32x4 acc[2];
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const int rt = 2 * w + m;  // row tile
+        acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+        for (int k0 = 0; k0 < D; k0 += 16) acc[m] = mm16_f32(&sm.A[16 * rt * LDA + k0], LDA, &sm.S[k0 * 16], 16, acc[m], lane);
+      }
+      __syncthreads();  // every wave has read S
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const int rt = 2 * w + m;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = 16 * rt + 4 * (lane >> 4) + r, c = lane & 15;
+          const float x = acc[m][r] + Bm[row * D + 16 * n + c];
+          sm.S[row * 16 + c] = x;
+          Bm[row * D + 16 * n + c] = x;
+        }
+      }
+      __syncthreads();
+    } else {
+      for (int i = t; i < D * 16; i += 256) sm.S[i] = Bm[(i >> 4) * D + 16 * n + (i & 15)];
+      __syncthreads();
+    }
   }
 }
 
@@ -1512,9 +1306,6 @@ __global__ void gating_kernel(const uint16_t* __restrict__ a, const uint16_t* __
   g[i] = -expf(A_log[h]) * softplus_f(bf2f(a[r * ab_stride + h]) + dt_bias[h]);
 }
 
-// Status word of the bounded waits (bit 0: a wait gave up), one per device.
-__device__ int g_wait_status;
-
 // Workspace of gdn_chunk_prefill_noalloc: one static array per device (host code reaches it only
 // through the address hipGetSymbolAddress returns on that device).
 static __device__ __align__(256) uint8_t scratch[GDN_NOALLOC_SCRATCH_BYTES];
@@ -1522,23 +1313,6 @@ static __device__ __align__(256) uint8_t scratch[GDN_NOALLOC_SCRATCH_BYTES];
 }  // namespace gdn
 
 using namespace gdn;
-
-namespace {
-constexpr int kDefaultWaitLimit = 1 << 18;
-int g_wait_limit = kDefaultWaitLimit;
-// Device address of g_wait_status on the current device (looked up once per device); null on failure.
-int* wait_status_ptr() {
-  static int* cached[64] = {nullptr};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-  if (!cached[dev]) {
-    void* p = nullptr;
-    if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_wait_status)) != hipSuccess) return nullptr;
-    cached[dev] = (int*)p;
-  }
-  return cached[dev];
-}
-}  // namespace
 
 // Device address of `scratch` on the current device, looked up once per device (null on failure).
 static uint8_t* scratch_ptr() {
@@ -1551,29 +1325,6 @@ static uint8_t* scratch_ptr() {
     cached[dev] = (uint8_t*)p;
   }
   return cached[dev];
-}
-
-extern "C" int gdn_device_status(int clear) {
-  clear_error();
-  int* p = wait_status_ptr();
-  if (!p) return set_error(GDN_ELAUNCH, "gdn_device_status: no device status word on the current device");
-  int v = 0;
-  if (hipMemcpy(&v, p, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess)
-    return set_error(GDN_ELAUNCH, "gdn_device_status: reading the status word failed");
-  if (clear) {
-    const int zero = 0;
-    if (hipMemcpy(p, &zero, sizeof(int), hipMemcpyHostToDevice) != hipSuccess)
-      return set_error(GDN_ELAUNCH, "gdn_device_status: clearing the status word failed");
-  }
-  if (v) return set_error(GDN_EWAIT, "a bounded inter-wave wait of the chunked prefill gave up: the outputs and "
-                                     "final states of the calls since the last status check are wrong");
-  return GDN_OK;
-}
-
-extern "C" int gdn_set_wait_limit(int64_t polls) {
-  clear_error();
-  g_wait_limit = polls < 0 ? kDefaultWaitLimit : (polls > (1ll << 30) ? (1 << 30) : (int)polls);
-  return GDN_OK;
 }
 
 extern "C" int gdn_unit_lower_inv(const float* X, float* T, int64_t batch, int n, void* stream) {
@@ -1599,16 +1350,35 @@ int device_cus() {
   }
   return cached[dev];
 }
-int scan_groups(int nseq, int Hv) {
-  const int per_group = 8 * Hv, cus = device_cus();
-  if (nseq <= 1 || per_group > cus) return nseq;
-  const int g = cus / per_group;
-  return g < nseq ? g : nseq;
+// Segment length (chunks) for a call: about sg::kTargetItems (segment, value head) items, at least
+// sg::kMinSeg chunks per segment.
+int64_t seg_len(int64_t total_chunks, int Hv) {
+  const int64_t work = total_chunks * (int64_t)Hv;
+  const int64_t L = (work + sg::kTargetItems - 1) / sg::kTargetItems;
+  return L < sg::kMinSeg ? sg::kMinSeg : L;
+}
+// Workspace layout: the segment table (nseq + 1 int32), the transition flags, the transition
+// slots (A, B fp32 per (slot, value head)) and the inverse kernel's fragments (12 KiB per (chunk,
+// value head)), each part 256-byte aligned.
+struct SegLayout {
+  int64_t L, nslots, off_flags, off_trans, off_tfrag, bytes;
+};
+SegLayout seg_layout(int64_t total_chunks, int nseq, int Hv) {
+  auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
+  SegLayout l;
+  l.L = seg_len(total_chunks, Hv);
+  l.nslots = total_chunks / l.L;
+  l.off_flags = up(((int64_t)nseq + 1) * 4);
+  l.off_trans = l.off_flags + up(l.nslots * Hv * 4);
+  l.off_tfrag = l.off_trans + l.nslots * Hv * (int64_t)sg::kTrans * 4;
+  l.bytes = l.off_tfrag + total_chunks * Hv * (int64_t)tf::BYTES;
+  return l;
 }
 }  // namespace
 
-extern "C" int64_t gdn_chunk_prefill_workspace_bytes(int64_t total_chunks, int Hv) {
-  return total_chunks * (int64_t)Hv * ws::BYTES;
+extern "C" int64_t gdn_chunk_prefill_workspace_bytes(int64_t total_chunks, int nseq, int Hv) {
+  if (total_chunks < 0 || nseq < 0 || Hv <= 0) return -1;
+  return seg_layout(total_chunks, nseq, Hv).bytes;
 }
 
 extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const void* k, int64_t k_stride,
@@ -1637,42 +1407,60 @@ extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const voi
   GDN_REQUIRE(aligned(out, 8), "gdn_chunk_prefill: out must be 8-byte aligned");
   GDN_REQUIRE((!initial_state || aligned(initial_state, 16)) && (!final_state || aligned(final_state, 16)),
               "gdn_chunk_prefill: initial/final state must be 16-byte aligned");
-  GDN_REQUIRE(total_chunks == 0 || (workspace && aligned(workspace, 256) &&
-                                    workspace_bytes >= gdn_chunk_prefill_workspace_bytes(total_chunks, Hv)),
+  GDN_REQUIRE(workspace && aligned(workspace, 256) &&
+                  workspace_bytes >= gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hv),
               "gdn_chunk_prefill: workspace missing, misaligned or smaller than %lld bytes",
-              (long long)gdn_chunk_prefill_workspace_bytes(total_chunks, Hv));
-  GDN_REQUIRE(total_chunks < (1ll << 31) && ((int64_t)nseq * Hv + 7) / 8 * 64 < (1ll << 31),
-              "gdn_chunk_prefill: grid too large");
+              (long long)gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hv));
+  GDN_REQUIRE(total_chunks < (1ll << 31), "gdn_chunk_prefill: too many chunks");
   if (nseq == 0) return GDN_OK;
-  hipStream_t s = (hipStream_t)stream;
+  hipStream_t st = (hipStream_t)stream;
+  const SegLayout lay = seg_layout(total_chunks, nseq, Hv);
   uint8_t* work = (uint8_t*)workspace;
-  if (total_chunks > 0) {
-    dim3 g1((unsigned)Hqk, (unsigned)total_chunks);
-    if (beta_dtype == GDN_BF16)
-      chunk_local_kernel<uint16_t><<<g1, pf::NT, 0, s>>>((const uint16_t*)q, q_stride, (const uint16_t*)k, k_stride,
-                                                         (const uint16_t*)v, v_stride,
-                                                         g, (const uint16_t*)beta, cu_seqlens, seq_chunk0, nseq,
-                                                         seq_len, Hqk, Hv, use_qk_l2norm, work);
-    else
-      chunk_local_kernel<float><<<g1, pf::NT, 0, s>>>((const uint16_t*)q, q_stride, (const uint16_t*)k, k_stride,
-                                                      (const uint16_t*)v, v_stride,
-                                                      g, (const float*)beta, cu_seqlens, seq_chunk0, nseq, seq_len,
-                                                      Hqk, Hv, use_qk_l2norm, work);
-    int rc = check_launch("gdn_chunk_prefill(local)");
+  int32_t* seg0 = (int32_t*)work;
+  int* tflags = (int*)(work + lay.off_flags);
+  float* trans = (float*)(work + lay.off_trans);
+  uint8_t* tfrag = work + lay.off_tfrag;
+  const int64_t nseg_max = (int64_t)nseq + total_chunks / lay.L;  // each sequence: <= nch / L + 1 segments
+  GDN_REQUIRE(nseg_max * Hv < (1ll << 31) && lay.nslots * Hv * 64 < (1ll << 31), "gdn_chunk_prefill: grid too large");
+  if (cu_seqlens) {
+    seg_table_kernel<<<1, 256, 0, st>>>(seq_chunk0, nseq, (int)lay.L, seg0);
+    int rc = check_launch("gdn_chunk_prefill(table)");
     if (rc) return rc;
   }
-  // Sequence groups: when the Hv x 8 workgroups of one group leave CUs free, split the sequences
-  // into as many groups (balanced by chunks) as fill the CUs once; each workgroup then streams its
-  // group's sequences back to back.  Otherwise one sequence per workgroup.
-  const WaitCtl wc{g_wait_limit, wait_status_ptr()};
-  if (!wc.status) return set_error(GDN_ELAUNCH, "gdn_chunk_prefill: no device status word on the current device");
-  const int groups = scan_groups(nseq, Hv);
-  const int64_t pairs = (int64_t)groups * Hv;
-  const int64_t scan_blocks = (pairs + 7) / 8 * 64;
-  chunk_scan_kernel<uint16_t><<<(unsigned)scan_blocks, kScanThreads, 0, s>>>(
-      initial_state, final_state, (uint16_t*)out, cu_seqlens, seq_chunk0, state_rows, n_rows, nseq, seq_len, Hqk,
-      Hv, groups, total_chunks, work, wc);
-  return check_launch("gdn_chunk_prefill(state)");
+  if (total_chunks > 0) {  // the intra-chunk inverses, all chunks in parallel
+    const dim3 gi((unsigned)Hqk, (unsigned)total_chunks);
+    if (beta_dtype == GDN_BF16)
+      inv_kernel<uint16_t><<<gi, pf::NT, 0, st>>>((const uint16_t*)k, k_stride, g, (const uint16_t*)beta, cu_seqlens,
+                                                  seq_chunk0, nseq, seq_len, Hqk, Hv, use_qk_l2norm, tfrag);
+    else
+      inv_kernel<float><<<gi, pf::NT, 0, st>>>((const uint16_t*)k, k_stride, g, (const float*)beta, cu_seqlens,
+                                               seq_chunk0, nseq, seq_len, Hqk, Hv, use_qk_l2norm, tfrag);
+    int rc = check_launch("gdn_chunk_prefill(inverse)");
+    if (rc) return rc;
+  }
+  const SegTable tab{cu_seqlens, seq_chunk0, cu_seqlens ? seg0 : nullptr, nseq, seq_len, (int)lay.L};
+  auto launch = [&](int pass, int64_t blocks) {
+#define GDN_SEG_LAUNCH(BT)                                                                                     \
+  (pass == 0 ? seg_kernel<BT, uint16_t, 0> : seg_kernel<BT, uint16_t, 1>)<<<(unsigned)blocks, sg::NT, 0, st>>>( \
+      (const uint16_t*)q, q_stride, (const uint16_t*)k, k_stride, (const uint16_t*)v, v_stride, g,             \
+      (const BT*)beta, (uint16_t*)out, tab, Hqk, Hv, use_qk_l2norm, initial_state, state_rows, n_rows,           \
+      final_state, trans, tflags, tfrag)
+    if (beta_dtype == GDN_BF16) GDN_SEG_LAUNCH(uint16_t);
+    else GDN_SEG_LAUNCH(float);
+#undef GDN_SEG_LAUNCH
+  };
+  if (lay.nslots > 0) {  // segment summaries, then their combination along each sequence
+    launch(1, lay.nslots * Hv * 2);
+    int rc = check_launch("gdn_chunk_prefill(summary)");
+    if (rc) return rc;
+    const int64_t items = lay.nslots * Hv;
+    seg_combine_kernel<<<(unsigned)((items + 7) / 8 * 64), 256, 0, st>>>(tab, Hv, initial_state, state_rows, n_rows,
+                                                                       trans, tflags);
+    rc = check_launch("gdn_chunk_prefill(combine)");
+    if (rc) return rc;
+  }
+  launch(0, nseg_max * Hv);
+  return check_launch("gdn_chunk_prefill(output)");
 }
 
 extern "C" int gdn_chunk_prefill(const void* q, int64_t q_stride, const void* k, int64_t k_stride,
@@ -1696,11 +1484,12 @@ extern "C" int gdn_chunk_prefill_noalloc(const void* q, int64_t q_stride, const 
                                          int use_qk_l2norm, void* stream) {
   clear_error();
   GDN_REQUIRE(total_chunks >= 0 && Hv > 0, "gdn_chunk_prefill_noalloc: bad sizes");
-  const int64_t need = gdn_chunk_prefill_workspace_bytes(total_chunks, Hv);
+  GDN_REQUIRE(nseq >= 0, "gdn_chunk_prefill_noalloc: bad sizes");
+  const int64_t need = gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hv);
   GDN_REQUIRE(need <= GDN_NOALLOC_SCRATCH_BYTES,
               "gdn_chunk_prefill_noalloc: the call needs %lld bytes of workspace, the static scratch holds %lld "
-              "(%lld chunks x %d value heads is too many; use gdn_chunk_prefill_rows with a workspace)",
-              (long long)need, (long long)GDN_NOALLOC_SCRATCH_BYTES, (long long)total_chunks, Hv);
+              "(%lld chunks, %d sequences, %d value heads; use gdn_chunk_prefill_rows with a workspace)",
+              (long long)need, (long long)GDN_NOALLOC_SCRATCH_BYTES, (long long)total_chunks, nseq, Hv);
   uint8_t* ws_ptr = scratch_ptr();
   if (!ws_ptr) return set_error(GDN_ELAUNCH, "gdn_chunk_prefill_noalloc: no static scratch on the current device");
   return gdn_chunk_prefill_rows(q, q_stride, k, k_stride, v, v_stride, g, beta, beta_dtype, initial_state,

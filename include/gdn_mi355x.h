@@ -29,8 +29,7 @@ enum {
   GDN_OK = 0,
   GDN_EINVAL = 1,   /* bad shape, dtype, stride, alignment or null pointer */
   GDN_EUNSUP = 2,   /* valid but not supported by this build (e.g. head_dim != 128) */
-  GDN_ELAUNCH = 3,  /* the HIP launch failed; the message carries hipGetErrorString */
-  GDN_EWAIT = 4     /* a kernel's bounded wait gave up (gdn_device_status): results are wrong */
+  GDN_ELAUNCH = 3   /* the HIP launch failed; the message carries hipGetErrorString */
 };
 
 /* Library version (major*10000 + minor*100 + patch). */
@@ -42,22 +41,6 @@ const char* gdn_last_error(void);
 /* Limits of this build: writes head_dim (128), max value heads per key head, max conv kernel. */
 int gdn_limits(int* head_dim, int* max_group_ratio, int* max_conv_kernel);
 
-/*
- * Device status of the current device: GDN_OK, or GDN_EWAIT when a kernel's bounded inter-wave
- * wait (the chunked prefill's two-wave state chain) gave up since the last clearing check -- the
- * outputs and final states of the calls launched since then are wrong.  clear != 0 resets the
- * status.  Waits for the device (a synchronous copy of one word): call it where a check is wanted,
- * not inside stream capture.  No reference counterpart: the reference's device ops have no bounded
- * waits (fail-loud contract of src/cb_engine.py:327).
- */
-int gdn_device_status(int clear);
-
-/*
- * Poll bound of the kernels' bounded waits for launches that follow (default 262144 polls;
- * polls < 0 restores the default).  A small bound makes a wait give up while every kernel still
- * runs to its end: it exists to test the status plumbing.
- */
-int gdn_set_wait_limit(int64_t polls);
 
 /*
  * Single-token recurrent gated delta rule (decode), fp32 state.
@@ -128,8 +111,14 @@ int gdn_decode_fused(const void* mixed, int64_t mixed_stride, const void* z, int
  */
 int gdn_unit_lower_inv(const float* X, float* T, int64_t batch, int n, void* stream);
 
-/* Bytes of device workspace gdn_chunk_prefill needs for `total_chunks` 64-token chunks. */
-int64_t gdn_chunk_prefill_workspace_bytes(int64_t total_chunks, int Hv);
+/*
+ * Bytes of device workspace gdn_chunk_prefill needs for `total_chunks` 64-token chunks of `nseq`
+ * sequences and Hv value heads (-1 for negative sizes): the segment table (4 bytes a sequence), the
+ * fp32 transition maps of the segments that have a successor (at most about 32 MiB: sequences are
+ * cut into segments so that about 256 (segment, value head) items exist) and the intra-chunk
+ * inverse fragments (12 KiB per (chunk, value head)).
+ */
+int64_t gdn_chunk_prefill_workspace_bytes(int64_t total_chunks, int nseq, int Hv);
 
 /*
  * Chunked gated delta rule prefill (chunk 64, fp32 state), optionally over packed sequences.
@@ -145,7 +134,7 @@ int64_t gdn_chunk_prefill_workspace_bytes(int64_t total_chunks, int Hv);
  *   cu_seqlens: device int32 [nseq+1] (packed varlen) with seq_chunk0: device int32 [nseq+1],
  *     seq_chunk0[s] = sum over earlier sequences of ceil(len/64); or both NULL for nseq
  *     sequences of seq_len tokens.  total_chunks = sum of ceil(len/64) over sequences.
- *   workspace: device memory of gdn_chunk_prefill_workspace_bytes(total_chunks, Hv) bytes,
+ *   workspace: device memory of gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hv) bytes,
  *     256-byte aligned (caller-owned; contents are scratch).
  */
 int gdn_chunk_prefill(const void* q, int64_t q_stride, const void* k, int64_t k_stride,
@@ -219,17 +208,18 @@ int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const void* k, int64
 
 /*
  * gdn_chunk_prefill_rows without a workspace argument and without any allocation: the kernels'
- * workspace is a static device array of GDN_NOALLOC_SCRATCH_BYTES (64 MiB) that the library holds on
+ * workspace is a static device array of GDN_NOALLOC_SCRATCH_BYTES (128 MiB) that the library holds on
  * every GPU it runs on until the process ends.  A call whose
- * gdn_chunk_prefill_workspace_bytes(total_chunks, Hv) exceeds it is rejected with GDN_EINVAL before
- * any launch (64 MiB holds 900 (chunk, value head) records, e.g. 1792 tokens at Hv = 32).  Every
+ * gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hv) exceeds it is rejected with GDN_EINVAL
+ * before any launch (the workspace is about 32 MiB plus 12 KiB per (chunk, value head) plus 4 bytes
+ * a sequence: 128 MiB holds e.g. 8192 tokens at Hv = 32).  Every
  * call on one GPU shares that GPU's array: calls that overlap on one GPU (other streams, other host
  * threads) race and give wrong results -- order them on one stream.  The array needs no clearing
  * (every record a call reads, the same call writes first).
  * No counterpart in the reference: for callers that cannot allocate (code under HIP graph capture,
  * serving loops, harnesses that forbid hipMalloc).
  */
-#define GDN_NOALLOC_SCRATCH_BYTES (64ll << 20)
+#define GDN_NOALLOC_SCRATCH_BYTES (128ll << 20)
 int gdn_chunk_prefill_noalloc(const void* q, int64_t q_stride, const void* k, int64_t k_stride,
                               const void* v, int64_t v_stride, const float* g, const void* beta,
                               int beta_dtype, const float* initial_state, float* final_state,

@@ -235,32 +235,3 @@ def test_gating(gdn, oracle, dev):
     assert torch.equal(beta.cpu(), beta_ref)
     assert rel_l2(g, g_ref) <= 1e-6
 
-
-@pytest.mark.gpu
-def test_scan_wait_give_up_is_reported(gdn, oracle, dev):
-    """A bounded inter-wave wait of the state chain that gives up raises the device status word
-    (GDN_EWAIT through check_device_status) while every kernel still runs to its end; with the
-    default bound the same call is clean and matches the oracle.  The give-up is forced from the
-    host with a zero poll bound."""
-    from importlib import import_module
-    L = import_module(gdn.__name__ + "._lib")
-    L.check_device_status()
-    q, k, v, g, beta, s0 = _gdn_inputs(300, 2, 4, seed=70)
-    args = [x.to(dev) for x in (q, k, v, g, beta)]
-    try:
-        L.set_wait_limit(0)
-        gdn.fast_chunk_gated_delta_rule_v2(*args, initial_state=s0.to(dev), output_final_state=True,
-                                           use_qk_l2norm_in_kernel=True)
-        torch.cuda.synchronize()
-        with pytest.raises(L.GDNError, match="code 4"):
-            L.check_device_status()
-    finally:
-        L.set_wait_limit(-1)
-    L.check_device_status()                      # the raising check cleared it
-    o, s = gdn.fast_chunk_gated_delta_rule_v2(*args, initial_state=s0.to(dev), output_final_state=True,
-                                              use_qk_l2norm_in_kernel=True)
-    torch.cuda.synchronize()
-    L.check_device_status()
-    o_ref, s_ref = oracle.chunk_gated_delta_rule_v2(q.repeat_interleave(2, 2), k.repeat_interleave(2, 2), v, g,
-                                                    beta, 64, s0, True, True)
-    assert rel_l2(o, o_ref) <= OUT_TOL and rel_l2(s, s_ref) <= STATE_TOL
