@@ -612,9 +612,10 @@ __global__ __launch_bounds__(256) void seg_table_kernel(const int32_t* __restric
 struct alignas(16) SegBuf {
   uint16_t K[pf::CH * pf::LDK];   // K rows (l2-normalised), token-major
   uint16_t V[pf::CH * pf::LDK];   // V rows
-  uint8_t wn[16 * ws::FRAG];      // -W fragments [tb 4][j 4]
-  uint8_t qg[16 * ws::FRAG];      // q fragments [tb 4][j 4]
-  uint8_t qk[8 * ws::FRAG];       // QK fragments [tb 4][j 2] (the two all-zero ones unused)
+  uint8_t wn[16 * ws::FRAG];          // -W fragments [tb 4][j 4]
+  uint8_t qg[16 * ws::FRAG];          // q fragments [tb 4][j 4]
+  uint8_t qk[tf::FRAGS * ws::FRAG];   // QK fragments of the lower blocks, index tf::fid(tb, j)
+  uint8_t tb[tf::FRAGS * ws::FRAG];   // T diag(beta) fragments (the inverse kernel's), index tf::fid(tb, k)
   float dec[pf::CH];              // e^{G_last - G_t}
   float egs[pf::CH];              // scale e^{G_t}
   float gl;                       // e^{G_last}
@@ -633,7 +634,7 @@ enum SegMode { kSegOut = 0, kSegB = 1, kSegA = 2 };
 // used: a select right after a load would make the wave wait for the load there.
 struct LocIn {
   u16x8 kr[4], vr[4], qr[4];
-  bf16x8 tbe[2];
+  bf16x8 tbe[2], tbu[2];
   float graw;
   int len;
 };
@@ -663,7 +664,10 @@ __device__ __forceinline__ void loc_load(LocIn& L, int64_t t0, int len, int kh, 
   }
 #pragma unroll
   for (int s = 0; s < 2; ++s)
-    if (2 * s <= w) L.tbe[s] = *reinterpret_cast<const bf16x8*>(tfr + tf::fid(w, s) * ws::FRAG + lane * 16);
+    if (2 * s <= w) {
+      L.tbe[s] = *reinterpret_cast<const bf16x8*>(tfr + tf::fid(w, s) * ws::FRAG + lane * 16);
+      L.tbu[s] = *reinterpret_cast<const bf16x8*>(tfr + (tf::FRAGS + tf::fid(w, s)) * ws::FRAG + lane * 16);
+    }
   const int tok = lane < len ? lane : len - 1;
   L.graw = g[(t0 + tok) * Hv + h];
 }
@@ -672,7 +676,7 @@ __device__ __forceinline__ void loc_load(LocIn& L, int64_t t0, int len, int kh, 
 // (kept in qf for phase 2), the decay scan (every local wave holds G of token `lane`; wave 0 writes
 // the factors the chain reads).
 template <bool kNeedQ>
-__device__ __forceinline__ void loc_phase1(SegBuf& B, const LocIn& in, int use_l2,
+__device__ __forceinline__ void loc_phase1(SegBuf& B, const LocIn& in, int use_l2, bool q_on,
                                            bf16x8 (&qf)[4], float& G) {
   using namespace pf;
   int t;  // opaque per call: the LDS addresses derived from it are not hoisted out of the chunk loop
@@ -689,7 +693,10 @@ __device__ __forceinline__ void loc_phase1(SegBuf& B, const LocIn& in, int use_l
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     *reinterpret_cast<u16x8*>(&B.V[(4 * tq + i) * LDK + 8 * fb]) = 4 * tq + i < len ? in.vr[i] : zero;
-  if (kNeedQ) {
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+    if (2 * s <= w) *reinterpret_cast<bf16x8*>(B.tb + tf::fid(w, s) * ws::FRAG + lane * 16) = in.tbu[s];
+  if (kNeedQ && q_on) {
     u16x8 qr[4];
     const bool live = 16 * w + (lane & 15) < len;
 #pragma unroll
@@ -727,12 +734,13 @@ __device__ __forceinline__ void loc_phase1(SegBuf& B, const LocIn& in, int use_l
 // token tile W.  (Q K^T)^T = K Q^T and W^T = K^T (T diag(beta e^G))^T: both accumulator layouts are
 // the k-slot ordered fragment layouts.
 template <int W, bool kNeedQ>
-__device__ __forceinline__ void loc_phase2(SegBuf& B, const bf16x8 (&qf)[4], float G, const bf16x8 (&tbe)[2]) {
+__device__ __forceinline__ void loc_phase2(SegBuf& B, const bf16x8 (&qf)[4], float G, const bf16x8 (&tbe)[2],
+                                           bool q_on) {
   using namespace pf;
   int t;
   asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"((int)threadIdx.x));
   const int lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
-  if (kNeedQ) {
+  if (kNeedQ && q_on) {
     f32x4 accQ[W + 1];
 #pragma unroll
     for (int cb = 0; cb <= W; ++cb) accQ[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -753,7 +761,7 @@ __device__ __forceinline__ void loc_phase2(SegBuf& B, const bf16x8 (&qf)[4], flo
 #pragma unroll
     for (int j = 0; j < 2; ++j)
       if (2 * j <= W)
-        *reinterpret_cast<bf16x8*>(B.qk + (W * 2 + j) * ws::FRAG + lane * 16) = pack_acc_bf16(qk[2 * j], qk[2 * j + 1]);
+        *reinterpret_cast<bf16x8*>(B.qk + tf::fid(W, j) * ws::FRAG + lane * 16) = pack_acc_bf16(qk[2 * j], qk[2 * j + 1]);
   }
   f32x4 accW[8];
 #pragma unroll
@@ -792,7 +800,7 @@ struct ChainRegs {
 // Chain part 1 for one chunk: U (fp32, from the inverse kernel's T diag(beta) fragments and the V
 // rows), vn = U - W S, the outputs o = diag(scale e^G) Q S + QK vn, and DEC vn split for part 2.
 template <bool kUseU>
-__device__ __forceinline__ void chain_part1(const SegBuf& B, ChainRegs& R, const bf16x8 (&tbv)[tf::FRAGS], bool out_on,
+__device__ __forceinline__ void chain_part1(const SegBuf& B, ChainRegs& R, bool out_on,
                                             uint16_t* __restrict__ out, int64_t t0, int len, int Hv, int h, int wc,
                                             int lane_in) {
   using namespace pf;
@@ -818,7 +826,7 @@ __device__ __forceinline__ void chain_part1(const SegBuf& B, ChainRegs& R, const
         const bf16x8 vf = __builtin_bit_cast(bf16x8, frag_tr(B.V, LDK, 32 * kb, 16 * n, lane));
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb)
-          if (2 * kb <= tb) acc[sl][tb] = mma(tbv[tf::fid(tb, kb)], vf, acc[sl][tb]);
+          if (2 * kb <= tb) acc[sl][tb] = mma(lds_frag(B.tb, tf::fid(tb, kb), lane), vf, acc[sl][tb]);
       }
     }
   }
@@ -849,14 +857,14 @@ __device__ __forceinline__ void chain_part1(const SegBuf& B, ChainRegs& R, const
         O[1] = mma(Sb[1][j], qf, O[1]);
       }
       const float e = B.egs[16 * tb + c16];
-      const bf16x8 k0 = lds_frag(B.qk, tb * 2, lane);
+      const bf16x8 k0 = lds_frag(B.qk, tf::fid(tb, 0), lane);
 #pragma unroll
       for (int sl = 0; sl < 2; ++sl) {
         O[sl] *= e;
         O[sl] = mma(vb[sl][0], k0, O[sl]);
       }
       if (tb >= 2) {
-        const bf16x8 k1 = lds_frag(B.qk, tb * 2 + 1, lane);
+        const bf16x8 k1 = lds_frag(B.qk, tf::fid(tb, 1), lane);
 #pragma unroll
         for (int sl = 0; sl < 2; ++sl) O[sl] = mma(vb[sl][1], k1, O[sl]);
       }
@@ -922,7 +930,8 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     const uint16_t* __restrict__ v, int64_t vs, const float* __restrict__ g, const BetaT* __restrict__ beta,
     OutT* __restrict__ out, SegTable tab, int Hqk, int Hv, int use_l2, const float* __restrict__ init,
     const int32_t* __restrict__ rows, int n_rows, float* __restrict__ final_state, float* __restrict__ trans,
-    int* __restrict__ tflags, const uint8_t* __restrict__ tfrag) {
+    int* __restrict__ tflags, const uint8_t* __restrict__ tfrag, const int* __restrict__ warm,
+    const int* __restrict__ seq_ok) {
   using namespace pf;
   __shared__ SegSmem sm;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
@@ -944,7 +953,9 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     idx = ts - tab.first_slot(s);
     slot = ts;
     mode = (item & 1) ? kSegA : kSegB;
+    if (seq_ok[(int64_t)s * Hv + h]) return;  // the output pass warms up instead
   }
+  const bool warm_path = kPass == 0 && slot >= 0 && seq_ok[(int64_t)s * Hv + h] != 0;
   const int kh = h / (Hv / Hqk);
   const int nch_s = tab.nch(s), c_begin = idx * tab.L;
   const int n = nch_s - c_begin < tab.L ? nch_s - c_begin : tab.L;
@@ -976,10 +987,13 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     if (!compute) return;
   }
   constexpr bool need_q = kPass == 0;
-  const int chunk_slot0 = tab.first_chunk(s) + c_begin;
+  // pass 0 after a warm-up: the chain starts from zero w0 chunks before the segment, without outputs
+  const int w0 = (kPass == 0 && warm_path) ? warm[(int64_t)slot * Hv + h] : 0;
+  const int cb0 = c_begin - w0, ntot = n + w0;
+  const int chunk_slot0 = tab.first_chunk(s) + cb0;
   auto tfr = [&](int c) { return tfrag + ((int64_t)(chunk_slot0 + c) * Hv + h) * tf::BYTES; };
-  auto chunk_t0 = [&](int c) { return t_seq + (int64_t)(c_begin + c) * CH; };
-  auto chunk_len = [&](int c) { return Ls - (c_begin + c) * CH < CH ? Ls - (c_begin + c) * CH : CH; };
+  auto chunk_t0 = [&](int c) { return t_seq + (int64_t)(cb0 + c) * CH; };
+  auto chunk_len = [&](int c) { return Ls - (cb0 + c) * CH < CH ? Ls - (cb0 + c) * CH : CH; };
   if (w < 4) {
     // ------------------------------------------------------------ local waves
     LocIn in;
@@ -988,34 +1002,34 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     auto load = [&](int c) {
       loc_load<need_q>(in, chunk_t0(c), chunk_len(c), kh, h, q, qs, k, ks, v, vs, g, Hv, tfr(c));
     };
-    auto phase2 = [&](SegBuf& B) {
+    auto phase2 = [&](SegBuf& B, bool q_on) {
       switch (w) {
-        case 0: loc_phase2<0, need_q>(B, qf, G, tbe); break;
-        case 1: loc_phase2<1, need_q>(B, qf, G, tbe); break;
-        case 2: loc_phase2<2, need_q>(B, qf, G, tbe); break;
-        default: loc_phase2<3, need_q>(B, qf, G, tbe); break;
+        case 0: loc_phase2<0, need_q>(B, qf, G, tbe, q_on); break;
+        case 1: loc_phase2<1, need_q>(B, qf, G, tbe, q_on); break;
+        case 2: loc_phase2<2, need_q>(B, qf, G, tbe, q_on); break;
+        default: loc_phase2<3, need_q>(B, qf, G, tbe, q_on); break;
       }
     };
-    if (n > 0) {
+    if (ntot > 0) {
       load(0);
-      loc_phase1<need_q>(sm.buf[0], in, use_l2, qf, G);
+      loc_phase1<need_q>(sm.buf[0], in, use_l2, w0 == 0, qf, G);
       tbe[0] = in.tbe[0];
       tbe[1] = in.tbe[1];
-      if (n > 1) load(1);
+      if (ntot > 1) load(1);
     }
     lds_barrier();
-    if (n > 0) phase2(sm.buf[0]);
+    if (ntot > 0) phase2(sm.buf[0], w0 == 0);
     lds_barrier();
-    for (int c = 0; c < n; ++c) {
-      const bool more = c + 1 < n;
+    for (int c = 0; c < ntot; ++c) {
+      const bool more = c + 1 < ntot;
       if (more) {
-        loc_phase1<need_q>(sm.buf[(c + 1) & 1], in, use_l2, qf, G);
+        loc_phase1<need_q>(sm.buf[(c + 1) & 1], in, use_l2, c + 1 >= w0, qf, G);
         tbe[0] = in.tbe[0];
         tbe[1] = in.tbe[1];
-        if (c + 2 < n) load(c + 2);
+        if (c + 2 < ntot) load(c + 2);
       }
       lds_barrier();
-      if (more) phase2(sm.buf[(c + 1) & 1]);
+      if (more) phase2(sm.buf[(c + 1) & 1], c + 1 >= w0);
       lds_barrier();
     }
   } else {
@@ -1025,7 +1039,7 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     {  // initial state
       const float* src = nullptr;
       if (mode == kSegOut) {
-        if (slot >= 0) src = tslot + D * D;
+        if (slot >= 0) src = warm_path ? nullptr : tslot + D * D;
         else if (init) {
           const int r0 = state_row(rows, n_rows, s);
           if (r0 >= 0) src = init + ((int64_t)r0 * Hv + h) * D * D;
@@ -1048,25 +1062,15 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
               R.S[sl][i][r] = (mode == kSegA && 16 * i + 4 * g4 + r == 32 * wc + 16 * sl + c16) ? 1.f : 0.f;
       }
     }
-    bf16x8 tb[tf::FRAGS], tbn[tf::FRAGS];
-    auto tload = [&](bf16x8 (&dst)[tf::FRAGS], int c) {
-      const uint8_t* p = tfr(c) + tf::FRAGS * ws::FRAG + lane * 16;
-#pragma unroll
-      for (int f = 0; f < tf::FRAGS; ++f) dst[f] = *reinterpret_cast<const bf16x8*>(p + f * ws::FRAG);
-    };
-    if (mode != kSegA && n > 0) tload(tb, 0);
     lds_barrier();
     lds_barrier();
-    for (int c = 0; c < n; ++c) {
+    for (int c = 0; c < ntot; ++c) {
       const SegBuf& B = sm.buf[c & 1];
-      if (mode != kSegA && c + 1 < n) tload(tbn, c + 1);
-      if (kPass == 0) chain_part1<true>(B, R, tb, true, out, chunk_t0(c), chunk_len(c), Hv, h, wc, lane);
-      else if (mode == kSegB) chain_part1<true>(B, R, tb, false, out, 0, 0, Hv, h, wc, lane);
-      else chain_part1<false>(B, R, tb, false, out, 0, 0, Hv, h, wc, lane);
+      if (kPass == 0) chain_part1<true>(B, R, c >= w0, out, chunk_t0(c), chunk_len(c), Hv, h, wc, lane);
+      else if (mode == kSegB) chain_part1<true>(B, R, false, out, 0, 0, Hv, h, wc, lane);
+      else chain_part1<false>(B, R, false, out, 0, 0, Hv, h, wc, lane);
       lds_barrier();
       chain_part2(B, R, lane);
-#pragma unroll
-      for (int f = 0; f < tf::FRAGS; ++f) tb[f] = tbn[f];
       lds_barrier();
     }
     // the state after the segment
@@ -1090,6 +1094,63 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
   }
 }
 
+// Warm-up lengths.  The state entering segment j + 1 differs from the chain run from zero over the
+// last w chunks of segment j by the map of those w chunks applied to the state before them; with
+// unit keys and beta in [0, 1] that map's norm is at most exp(sum of g over the w chunks).  For each
+// transition slot (the state after segment j) warm[] holds the least w whose bound is below 2^-64
+// (0: none within the segment, or keys not normalised in the kernel, or a beta outside [0, 1] on the
+// way), and seq_ok[] flags the (sequence, value head) pairs whose every slot has one: those run no
+// summaries and no combination, and each later segment starts with its warm-up.  One workgroup per
+// (sequence, value head); the windows are scanned back from the segment's end 4 chunks at a time.
+template <typename BetaT>
+__global__ __launch_bounds__(256) void seg_warm_kernel(SegTable tab, const float* __restrict__ g,
+                                                      const BetaT* __restrict__ beta, int Hv, int use_l2,
+                                                      int* __restrict__ warm, int* __restrict__ seq_ok) {
+  using namespace pf;
+  __shared__ float part[4];
+  const int s = blockIdx.x / Hv, h = blockIdx.x % Hv;
+  const int t = threadIdx.x, wv = t >> 6, lane = t & 63;
+  const int nseg = tab.nseg_of(tab.nch(s)), slot0 = tab.first_slot(s), L = tab.L;
+  int all_ok = use_l2 ? 1 : 0;
+  for (int j = 0; j + 1 < nseg; ++j) {
+    int wsel = 0;
+    if (use_l2) {
+      const int64_t seg_t0 = tab.start(s) + (int64_t)j * L * CH;  // segment j: L full chunks
+      float acc = 0.f;
+      bool done = false;
+      for (int base = 0; base < L && !done; base += 4) {
+        const int ci = base + wv;  // chunk counted back from the segment's end
+        float sum = 0.f;
+        int ok = 1;
+        if (ci < L) {
+          const int64_t tok = seg_t0 + (int64_t)(L - 1 - ci) * CH + lane;
+          sum = g[tok * Hv + h];
+          const float b = Elem<BetaT>::load(beta + tok * Hv + h);
+          ok = (b >= 0.f && b <= 1.f) ? 1 : 0;
+        }
+        sum = wave_sum_fast(sum);
+        ok = __builtin_amdgcn_ballot_w64(ok == 0) == 0 ? 1 : 0;
+        if (lane == 0) part[wv] = ok ? sum : __builtin_nanf("");
+        __syncthreads();
+        for (int i = 0; i < 4 && !done; ++i) {
+          if (base + i >= L) break;
+          acc += part[i];
+          if (acc < sg::kNegligibleLog) {
+            wsel = base + i + 1;
+            done = true;
+          } else if (!(acc == acc)) {
+            done = true;  // NaN, or a beta outside [0, 1]: no warm-up reaches past it
+          }
+        }
+        __syncthreads();
+      }
+    }
+    if (t == 0) warm[(int64_t)(slot0 + j) * Hv + h] = wsel;
+    all_ok &= wsel > 0 ? 1 : 0;
+  }
+  if (t == 0) seq_ok[(int64_t)s * Hv + h] = all_ok;
+}
+
 // S_{j+1} = A_j S_j + B_j along each sequence's segments, in fp32 (v_mfma_f32_16x16x4_f32); the result
 // overwrites B_j, which the output pass reads as segment j+1's initial state.  One workgroup per
 // (sequence with transition slots, value head, 16-column slice), started at the sequence's first
@@ -1101,7 +1162,8 @@ struct CombineSmem {
 };
 __global__ __launch_bounds__(256) void seg_combine_kernel(SegTable tab, int Hv, const float* __restrict__ init,
                                                          const int32_t* __restrict__ rows, int n_rows,
-                                                         float* __restrict__ trans, const int* __restrict__ tflags) {
+                                                         float* __restrict__ trans, const int* __restrict__ tflags,
+                                                         const int* __restrict__ seq_ok) {
   using namespace pf;
   __shared__ CombineSmem sm;
   const int b = blockIdx.x;
@@ -1109,7 +1171,7 @@ __global__ __launch_bounds__(256) void seg_combine_kernel(SegTable tab, int Hv, 
   const int ts = item / Hv, h = item % Hv;
   if (ts >= tab.first_slot(tab.nseq)) return;
   const int s = tab.seq_of_slot(ts);
-  if (ts != tab.first_slot(s)) return;
+  if (ts != tab.first_slot(s) || seq_ok[(int64_t)s * Hv + h]) return;
   const int nsl = tab.first_slot(s + 1) - ts;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const int LDA = D + 4;
@@ -1357,11 +1419,12 @@ int64_t seg_len(int64_t total_chunks, int Hv) {
   const int64_t L = (work + sg::kTargetItems - 1) / sg::kTargetItems;
   return L < sg::kMinSeg ? sg::kMinSeg : L;
 }
-// Workspace layout: the segment table (nseq + 1 int32), the transition flags, the transition
-// slots (A, B fp32 per (slot, value head)) and the inverse kernel's fragments (12 KiB per (chunk,
-// value head)), each part 256-byte aligned.
+// Workspace layout: the segment table (nseq + 1 int32), the transition flags and warm-up lengths
+// (int32 per (slot, value head)), the warm-up flags (int32 per (sequence, value head)), the
+// transition slots (A, B fp32 per (slot, value head)) and the inverse kernel's fragments (12 KiB
+// per (chunk, value head)), each part 256-byte aligned.
 struct SegLayout {
-  int64_t L, nslots, off_flags, off_trans, off_tfrag, bytes;
+  int64_t L, nslots, off_flags, off_warm, off_seqok, off_trans, off_tfrag, bytes;
 };
 SegLayout seg_layout(int64_t total_chunks, int nseq, int Hv) {
   auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
@@ -1369,7 +1432,9 @@ SegLayout seg_layout(int64_t total_chunks, int nseq, int Hv) {
   l.L = seg_len(total_chunks, Hv);
   l.nslots = total_chunks / l.L;
   l.off_flags = up(((int64_t)nseq + 1) * 4);
-  l.off_trans = l.off_flags + up(l.nslots * Hv * 4);
+  l.off_warm = l.off_flags + up(l.nslots * Hv * 4);
+  l.off_seqok = l.off_warm + up(l.nslots * Hv * 4);
+  l.off_trans = l.off_seqok + up((int64_t)nseq * Hv * 4);
   l.off_tfrag = l.off_trans + l.nslots * Hv * (int64_t)sg::kTrans * 4;
   l.bytes = l.off_tfrag + total_chunks * Hv * (int64_t)tf::BYTES;
   return l;
@@ -1418,10 +1483,13 @@ extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const voi
   uint8_t* work = (uint8_t*)workspace;
   int32_t* seg0 = (int32_t*)work;
   int* tflags = (int*)(work + lay.off_flags);
+  int* warm = (int*)(work + lay.off_warm);
+  int* seq_ok = (int*)(work + lay.off_seqok);
   float* trans = (float*)(work + lay.off_trans);
   uint8_t* tfrag = work + lay.off_tfrag;
   const int64_t nseg_max = (int64_t)nseq + total_chunks / lay.L;  // each sequence: <= nch / L + 1 segments
-  GDN_REQUIRE(nseg_max * Hv < (1ll << 31) && lay.nslots * Hv * 64 < (1ll << 31), "gdn_chunk_prefill: grid too large");
+  GDN_REQUIRE(nseg_max * Hv < (1ll << 31) && lay.nslots * Hv * 64 < (1ll << 31) && (int64_t)nseq * Hv < (1ll << 31),
+              "gdn_chunk_prefill: grid too large");
   if (cu_seqlens) {
     seg_table_kernel<<<1, 256, 0, st>>>(seq_chunk0, nseq, (int)lay.L, seg0);
     int rc = check_launch("gdn_chunk_prefill(table)");
@@ -1444,18 +1512,26 @@ extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const voi
   (pass == 0 ? seg_kernel<BT, uint16_t, 0> : seg_kernel<BT, uint16_t, 1>)<<<(unsigned)blocks, sg::NT, 0, st>>>( \
       (const uint16_t*)q, q_stride, (const uint16_t*)k, k_stride, (const uint16_t*)v, v_stride, g,             \
       (const BT*)beta, (uint16_t*)out, tab, Hqk, Hv, use_qk_l2norm, initial_state, state_rows, n_rows,           \
-      final_state, trans, tflags, tfrag)
+      final_state, trans, tflags, tfrag, warm, seq_ok)
     if (beta_dtype == GDN_BF16) GDN_SEG_LAUNCH(uint16_t);
     else GDN_SEG_LAUNCH(float);
 #undef GDN_SEG_LAUNCH
   };
-  if (lay.nslots > 0) {  // segment summaries, then their combination along each sequence
+  if (lay.nslots > 0) {  // warm-up lengths; segment summaries and their combination where none fits
+    if (beta_dtype == GDN_BF16)
+      seg_warm_kernel<uint16_t><<<(unsigned)(nseq * Hv), 256, 0, st>>>(tab, g, (const uint16_t*)beta, Hv,
+                                                                       use_qk_l2norm, warm, seq_ok);
+    else
+      seg_warm_kernel<float><<<(unsigned)(nseq * Hv), 256, 0, st>>>(tab, g, (const float*)beta, Hv, use_qk_l2norm,
+                                                                    warm, seq_ok);
+    int rc = check_launch("gdn_chunk_prefill(warm-up)");
+    if (rc) return rc;
     launch(1, lay.nslots * Hv * 2);
-    int rc = check_launch("gdn_chunk_prefill(summary)");
+    rc = check_launch("gdn_chunk_prefill(summary)");
     if (rc) return rc;
     const int64_t items = lay.nslots * Hv;
     seg_combine_kernel<<<(unsigned)((items + 7) / 8 * 64), 256, 0, st>>>(tab, Hv, initial_state, state_rows, n_rows,
-                                                                       trans, tflags);
+                                                                       trans, tflags, seq_ok);
     rc = check_launch("gdn_chunk_prefill(combine)");
     if (rc) return rc;
   }

@@ -161,6 +161,32 @@ def test_chunk_prefill_slow_decay_state_accuracy(gdn, oracle, dev):
     assert rel_l2(o, o_ref) <= OUT_TOL and rel_l2(s, s_ref) <= STATE_TOL
 
 
+def test_chunk_prefill_warm_up_and_exact_paths_per_head(gdn, oracle, dev):
+    """Two packed sequences (2500 and 1596 tokens, 4-chunk segments at this size), one value head per
+    path the kernel can take for a later segment's initial state: strong decay (a one-chunk warm-up
+    bounds the dropped state by 2^-64); moderate and slow decay (no window within a segment reaches
+    the bound: the exact summaries and combine, A formed); strong decay with one beta above 1 in the
+    last chunk of a segment (the bound does not hold there: the exact path).  Every head against the
+    oracle."""
+    lens = [2500, 1596]
+    cu = torch.tensor([0, 2500, 4096], dtype=torch.int32)
+    q, k, v, g, beta, _ = _gdn_inputs(4096, 2, 4, seed=21, state=False)
+    g[..., 0] *= 10.0
+    g[..., 1] *= 0.5
+    g[..., 2] *= 0.05
+    g[..., 3] *= 10.0
+    beta[0, 1000, 3] = 1.5
+    s0 = 0.02 * torch.randn(2, 4, 128, 128, generator=torch.Generator().manual_seed(22))
+    o_ref, s_ref = oracle.chunk_gated_delta_rule_varlen(_rep(q, 2), _rep(k, 2), v, g, beta, cu, 64, s0, True, True)
+    o, s = gdn.fast_chunk_gated_delta_rule_v2(q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta.to(dev),
+                                              initial_state=s0.to(dev), output_final_state=True,
+                                              use_qk_l2norm_in_kernel=True, cu_seqlens=cu.to(dev))
+    for h in range(4):
+        assert rel_l2(o[:, :, h], o_ref[:, :, h]) <= OUT_TOL, f"value head {h}"
+        for i in range(len(lens)):
+            assert rel_l2(s[i, h], s_ref[i, h]) <= STATE_TOL, f"sequence {i} value head {h}"
+
+
 @pytest.mark.parametrize("with_history", [False, True])
 def test_conv_prefill(gdn, oracle, dev, with_history):
     C, K = 512, 4
