@@ -420,11 +420,13 @@ struct InvSmem {
   float G[pf::CH], EG[pf::CH], B[pf::CH];
 };
 template <typename BetaT>
-__global__ __launch_bounds__(pf::NT, 3) void inv_kernel(const uint16_t* __restrict__ k, int64_t ks,
+__global__ __launch_bounds__(pf::NT, 3) void inv_kernel(const uint16_t* __restrict__ q, int64_t qs,
+                                                       const uint16_t* __restrict__ k, int64_t ks,
                                                        const float* __restrict__ g, const BetaT* __restrict__ beta,
                                                        const int32_t* __restrict__ cu,
                                                        const int32_t* __restrict__ seq_chunk0, int nseq, int seq_len,
-                                                       int Hqk, int Hv, int use_l2, uint8_t* __restrict__ tfrag) {
+                                                       int Hqk, int Hv, int use_l2, uint8_t* __restrict__ tfrag,
+                                                       uint16_t* __restrict__ qkn) {
   using namespace pf;
   __shared__ InvSmem sm;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
@@ -439,15 +441,30 @@ __global__ __launch_bounds__(pf::NT, 3) void inv_kernel(const uint16_t* __restri
     graw = lane < cp.len ? gr : 0.f;
     braw = lane < cp.len ? br : 0.f;
   }
+  // q and k of the chunk (l2-normalised when asked, zero past the chunk's end) for the segment kernel:
+  // the q fragments of token tile w in k-slot order, then the K rows, 16 KiB each per (chunk, key head)
+  uint16_t* qk_out = qkn + ((int64_t)slot * Hqk + hk) * (2 * CH * D);
+  uint16_t* sQ = reinterpret_cast<uint16_t*>(sm.X);  // staged in X's space, which is written later
   {
-    u16x8 kx[4];
+    u16x8 kx[4], qx[4];
     const int tq = t >> 4, fb = t & 15;
     load_rows4(kx, k + (int64_t)hk * D, ks, cp.t0, cp.len, tq, 8 * fb);
-    if (use_l2) l2norm_rows4(kx);
+    load_rows4(qx, q + (int64_t)hk * D, qs, cp.t0, cp.len, tq, 8 * fb);
+    if (use_l2) {
+      l2norm_rows4(kx);
+      l2norm_rows4(qx);
+    }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<u16x8*>(&sm.K[(4 * tq + i) * LDK + 8 * fb]) = kx[i];
+    for (int i = 0; i < 4; ++i) {
+      *reinterpret_cast<u16x8*>(&sm.K[(4 * tq + i) * LDK + 8 * fb]) = kx[i];
+      *reinterpret_cast<u16x8*>(&sQ[(4 * tq + i) * LDK + 8 * fb]) = qx[i];
+      *reinterpret_cast<u16x8*>(qk_out + CH * D + (4 * tq + i) * D + 8 * fb) = kx[i];
+    }
   }
   __syncthreads();
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+    *reinterpret_cast<bf16x8*>(qk_out + (w * 4 + s) * (ws::FRAG / 2) + lane * 8) = frag_kperm(sQ, LDK, 16 * w, 32 * s, lane);
   // K K^T, row tile w (blocks cb <= w), kept in registers for every value head
   f32x4 acc[4];
 #pragma unroll
@@ -616,6 +633,7 @@ struct alignas(16) SegBuf {
   uint8_t qg[16 * ws::FRAG];          // q fragments [tb 4][j 4]
   uint8_t qk[tf::FRAGS * ws::FRAG];   // QK fragments of the lower blocks, index tf::fid(tb, j)
   uint8_t tb[tf::FRAGS * ws::FRAG];   // T diag(beta) fragments (the inverse kernel's), index tf::fid(tb, k)
+  float gs[pf::CH];               // G_t, the cumulative log decay within the chunk
   float dec[pf::CH];              // e^{G_last - G_t}
   float egs[pf::CH];              // scale e^{G_t}
   float gl;                       // e^{G_last}
@@ -628,114 +646,103 @@ struct SegSmem {
 enum SegMode { kSegOut = 0, kSegB = 1, kSegA = 2 };
 
 // A local wave's inputs for one chunk, loaded a chunk ahead.  Local wave w (threads t < 256) holds K
-// and V rows 4 tq + i x features 8 fb .. (t = 16 tq + fb: rows 16 w .. 16 w + 15), q of token tile w
-// in k-slot order, the T diag(beta e^G) fragments of token tile w and the g of token `lane`.  Rows
-// past the chunk's end hold its last row (every load is in bounds) and are zeroed where they are
-// used: a select right after a load would make the wave wait for the load there.
+// and V rows 4 tq + i x features 8 fb .. (t = 16 tq + fb: rows 16 w .. 16 w + 15), the q fragments of
+// token tile w, the T diag(beta e^G) and T diag(beta) fragments of token tile w and the g of token
+// `lane`.  q and K come from the inverse kernel's record (normalised, zero past the chunk's end).
+// V rows past the chunk's end repeat its last row: T diag(beta) has zero columns there (beta is 0
+// past the end), so they add nothing to U.  Every address is a wave-uniform base plus a 32-bit
+// lane offset.
 struct LocIn {
-  u16x8 kr[4], vr[4], qr[4];
-  bf16x8 tbe[2], tbu[2];
+  u16x8 kr[4], vr[4];
+  bf16x8 qr[4], tbe[2], tbu[2];
   float graw;
-  int len;
 };
 template <bool kNeedQ>
-__device__ __forceinline__ void loc_load(LocIn& L, int64_t t0, int len, int kh, int h,
-                                         const uint16_t* __restrict__ q, int64_t qs, const uint16_t* __restrict__ k,
-                                         int64_t ks, const uint16_t* __restrict__ v, int64_t vs,
-                                         const float* __restrict__ g, int Hv, const uint8_t* __restrict__ tfr) {
+__device__ __forceinline__ void loc_load(LocIn& L, int64_t t0, int len, int h, const uint16_t* __restrict__ qkc,
+                                         const uint16_t* __restrict__ v, uint32_t vs, const float* __restrict__ g,
+                                         int Hv, const uint8_t* __restrict__ tfr) {
   using namespace pf;
-  const int t = threadIdx.x, w = t >> 6, lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
-  const int tq = t >> 4, fb = t & 15;
-  L.len = len;
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  const uint32_t tq = t >> 4, fb = t & 15;
+  const uint16_t* kb = qkc + CH * D;
+  const uint16_t* vb = v + t0 * vs + (int64_t)h * D;
+  const float* gb = g + t0 * Hv + h;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int row = 4 * tq + i, rc = row < len ? row : len - 1;
-    L.kr[i] = *reinterpret_cast<const u16x8*>(k + (t0 + rc) * ks + (int64_t)kh * D + 8 * fb);
-    L.vr[i] = *reinterpret_cast<const u16x8*>(v + (t0 + rc) * vs + (int64_t)h * D + 8 * fb);
+    const uint32_t row = 4 * tq + i, rc = row < (uint32_t)len ? row : (uint32_t)len - 1;
+    L.kr[i] = *reinterpret_cast<const u16x8*>(kb + (row * D + 8 * fb));
+    L.vr[i] = *reinterpret_cast<const u16x8*>(vb + (rc * vs + 8 * fb));
   }
   if (kNeedQ) {
-    const int row = 16 * w + c16, rowc = row < len ? row : len - 1;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const uint16_t* p = q + (t0 + rowc) * qs + (int64_t)kh * D + 32 * s + 4 * g4;
-      const u16x4 lo = *reinterpret_cast<const u16x4*>(p), hi = *reinterpret_cast<const u16x4*>(p + 16);
-      L.qr[s] = u16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-    }
+    for (int s = 0; s < 4; ++s)
+      L.qr[s] = *reinterpret_cast<const bf16x8*>(qkc + (uint32_t)((w * 4 + s) * (ws::FRAG / 2) + lane * 8));
   }
+  // every wave issues the same loads (tiles 0 and 1 read their one fragment twice): the wait
+  // counts before the uses then stay exact along every path through the chunk loop
 #pragma unroll
-  for (int s = 0; s < 2; ++s)
-    if (2 * s <= w) {
-      L.tbe[s] = *reinterpret_cast<const bf16x8*>(tfr + tf::fid(w, s) * ws::FRAG + lane * 16);
-      L.tbu[s] = *reinterpret_cast<const bf16x8*>(tfr + (tf::FRAGS + tf::fid(w, s)) * ws::FRAG + lane * 16);
-    }
-  const int tok = lane < len ? lane : len - 1;
-  L.graw = g[(t0 + tok) * Hv + h];
+  for (int s = 0; s < 2; ++s) {
+    L.tbe[s] = *reinterpret_cast<const bf16x8*>(tfr + (uint32_t)(tf::fid(w, s) * ws::FRAG + lane * 16));
+    L.tbu[s] = *reinterpret_cast<const bf16x8*>(tfr + (uint32_t)((tf::FRAGS + tf::fid(w, s)) * ws::FRAG + lane * 16));
+  }
+  const uint32_t tok = lane < len ? lane : len - 1;
+  L.graw = gb[tok * (uint32_t)Hv];
 }
 
-// Local phase 1 (wave w < 4): K rows (l2norm) and V rows into the buffer, q (l2norm) as fragments
-// (kept in qf for phase 2), the decay scan (every local wave holds G of token `lane`; wave 0 writes
-// the factors the chain reads).
+// Inclusive prefix sum over the 64 lanes (DPP: shifts within rows of 16, then the row totals
+// broadcast into the later rows).
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ float dpp_or_zero(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, kRowMask, 0xf, false));
+}
+__device__ __forceinline__ float wave_incl_scan(float x) {
+  x += dpp_or_zero<0x111, 0xf>(x);  // row_shr:1
+  x += dpp_or_zero<0x112, 0xf>(x);  // row_shr:2
+  x += dpp_or_zero<0x114, 0xf>(x);  // row_shr:4
+  x += dpp_or_zero<0x118, 0xf>(x);  // row_shr:8
+  x += dpp_or_zero<0x142, 0xa>(x);  // row_bcast:15 into rows 1 and 3
+  x += dpp_or_zero<0x143, 0xc>(x);  // row_bcast:31 into rows 2 and 3
+  return x;
+}
+
+// Local phase 1 (wave w < 4): K and V rows into the buffer, the q fragments (kept in qf for phase
+// 2); wave 0 also forms the decay factors (G, e^{G_last - G}, scale e^G, e^{G_last}).
 template <bool kNeedQ>
-__device__ __forceinline__ void loc_phase1(SegBuf& B, const LocIn& in, int use_l2, bool q_on,
-                                           bf16x8 (&qf)[4], float& G) {
+__device__ __forceinline__ void loc_phase1(SegBuf& B, const LocIn& in, int len, bool q_on, bf16x8 (&qf)[4]) {
   using namespace pf;
   int t;  // opaque per call: the LDS addresses derived from it are not hoisted out of the chunk loop
   asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"((int)threadIdx.x));
   const int w = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
-  const int tq = t >> 4, fb = t & 15, len = in.len;
-  const u16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
-  u16x8 kx[4];
+  const int tq = t >> 4, fb = t & 15;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) kx[i] = 4 * tq + i < len ? in.kr[i] : zero;
-  if (use_l2) l2norm_rows4(kx);
+  for (int i = 0; i < 4; ++i) *reinterpret_cast<u16x8*>(&B.K[(4 * tq + i) * LDK + 8 * fb]) = in.kr[i];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) *reinterpret_cast<u16x8*>(&B.K[(4 * tq + i) * LDK + 8 * fb]) = kx[i];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    *reinterpret_cast<u16x8*>(&B.V[(4 * tq + i) * LDK + 8 * fb]) = 4 * tq + i < len ? in.vr[i] : zero;
+  for (int i = 0; i < 4; ++i) *reinterpret_cast<u16x8*>(&B.V[(4 * tq + i) * LDK + 8 * fb]) = in.vr[i];
 #pragma unroll
   for (int s = 0; s < 2; ++s)
     if (2 * s <= w) *reinterpret_cast<bf16x8*>(B.tb + tf::fid(w, s) * ws::FRAG + lane * 16) = in.tbu[s];
   if (kNeedQ && q_on) {
-    u16x8 qr[4];
-    const bool live = 16 * w + (lane & 15) < len;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) qr[s] = live ? in.qr[s] : zero;
-    if (use_l2) {
-      float ss = 0.f;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) ss = sumsq_bf16(qr[s], ss);
-      ss = xor32_sum(xor16_sum(ss));
-      const float inv = l2norm_inv(ss);
-#pragma unroll
-      for (int s = 0; s < 4; ++s) qr[s] = scale_bf16(qr[s], inv);
-    }
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      qf[s] = __builtin_bit_cast(bf16x8, qr[s]);
+      qf[s] = in.qr[s];
       *reinterpret_cast<bf16x8*>(B.qg + (w * 4 + s) * ws::FRAG + lane * 16) = qf[s];
     }
   }
-  G = lane < len ? in.graw : 0.f;  // cumulative decay within the chunk (g = 0 past its end)
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const float up = __shfl_up(G, o, kWave);
-    if (lane >= o) G += up;
-  }
   if (w == 0) {
+    const float G = wave_incl_scan(lane < len ? in.graw : 0.f);  // g = 0 past the chunk's end
     const float gl = __shfl(G, 63, kWave);
+    B.gs[lane] = G;
     B.dec[lane] = expf(gl - G);
     B.egs[lane] = kScale * expf(G);
     if (lane == 0) B.gl = expf(gl);
   }
 }
 
-// Local phase 2 (wave W < 4, after the K rows are in): the QK fragments and the -W fragments of
-// token tile W.  (Q K^T)^T = K Q^T and W^T = K^T (T diag(beta e^G))^T: both accumulator layouts are
-// the k-slot ordered fragment layouts.
+// Local phase 2 (wave W < 4, after the K rows and the decay are in): the QK fragments and the -W
+// fragments of token tile W.  (Q K^T)^T = K Q^T and W^T = K^T (T diag(beta e^G))^T: both accumulator
+// layouts are the k-slot ordered fragment layouts.
 template <int W, bool kNeedQ>
-__device__ __forceinline__ void loc_phase2(SegBuf& B, const bf16x8 (&qf)[4], float G, const bf16x8 (&tbe)[2],
-                                           bool q_on) {
+__device__ __forceinline__ void loc_phase2(SegBuf& B, const bf16x8 (&qf)[4], const bf16x8 (&tbe)[2], bool q_on) {
   using namespace pf;
   int t;
   asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"((int)threadIdx.x));
@@ -748,16 +755,17 @@ __device__ __forceinline__ void loc_phase2(SegBuf& B, const bf16x8 (&qf)[4], flo
     for (int s = 0; s < 4; ++s)
 #pragma unroll
       for (int cb = 0; cb <= W; ++cb) accQ[cb] = mma(frag_kperm(B.K, LDK, 16 * cb, 32 * s, lane), qf[s], accQ[cb]);
-    const float gi = __shfl(G, 16 * W + c16, kWave);
+    const float gi = B.gs[16 * W + c16];
     f32x4 qk[4];
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb)
+    for (int cb = 0; cb < 4; ++cb) {
+      const f32x4 gj = *reinterpret_cast<const f32x4*>(&B.gs[16 * cb + 4 * g4]);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {  // QK[i][jj], i = 16W + c, jj = 16cb + 4g + r
         const int jj = 16 * cb + 4 * g4 + r;
-        const float gj = __shfl(G, jj, kWave);
-        qk[cb][r] = (cb <= W && 16 * W + c16 >= jj) ? kScale * accQ[cb <= W ? cb : 0][r] * __expf(gi - gj) : 0.f;
+        qk[cb][r] = (cb <= W && 16 * W + c16 >= jj) ? kScale * accQ[cb <= W ? cb : 0][r] * __expf(gi - gj[r]) : 0.f;
       }
+    }
 #pragma unroll
     for (int j = 0; j < 2; ++j)
       if (2 * j <= W)
@@ -798,15 +806,26 @@ struct ChainRegs {
   bf16x8 hi[2][2], lo[2][2];  // DEC vn, split, carried from part 1 to part 2
 };
 // Chain part 1 for one chunk: U (fp32, from the inverse kernel's T diag(beta) fragments and the V
-// rows), vn = U - W S, the outputs o = diag(scale e^G) Q S + QK vn, and DEC vn split for part 2.
-template <bool kUseU>
-__device__ __forceinline__ void chain_part1(const SegBuf& B, ChainRegs& R, bool out_on,
-                                            uint16_t* __restrict__ out, int64_t t0, int len, int Hv, int h, int wc,
-                                            int lane_in) {
+// rows), vn = U - W S, the outputs o = diag(scale e^G) Q S + QK vn (kOut), and DEC vn split for part
+// 2.  W S and Q S share the loop over the state's k-blocks j (16 independent accumulators); the LDS
+// fragments of block j + 1 are requested before the products of block j, so their latency hides
+// behind those products.
+template <bool kUseU, bool kOut>
+__device__ __forceinline__ void chain_part1(const SegBuf& B, ChainRegs& R, uint16_t* __restrict__ out, int64_t t0,
+                                            int len, int Hv, int h, int wc, int lane_in) {
   using namespace pf;
   int lane;
   asm volatile("v_mov_b32 %0, %1" : "=v"(lane) : "v"(lane_in));
   const int c16 = lane & 15, g4 = lane >> 4;
+  bf16x8 fw[4], fq[4];  // block j's -W and q fragments (token tiles 0..3)
+  auto fetch = [&](int j, bf16x8 (&w_)[4], bf16x8 (&q_)[4]) {
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+      w_[tb] = lds_frag(B.wn, tb * 4 + j, lane);
+      if (kOut) q_[tb] = lds_frag(B.qg, tb * 4 + j, lane);
+    }
+  };
+  fetch(0, fw, fq);
   bf16x8 Sb[2][4];
 #pragma unroll
   for (int sl = 0; sl < 2; ++sl)
@@ -818,29 +837,55 @@ __device__ __forceinline__ void chain_part1(const SegBuf& B, ChainRegs& R, bool 
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb) acc[sl][tb] = f32x4{0.f, 0.f, 0.f, 0.f};
   if (kUseU) {  // U = T diag(beta) V, token tile tb, k-blocks kb <= tb / 2
+    bf16x8 vf[2][2], ft[tf::FRAGS];
 #pragma unroll
-    for (int sl = 0; sl < 2; ++sl) {
-      const int n = 2 * wc + sl;
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const bf16x8 vf = __builtin_bit_cast(bf16x8, frag_tr(B.V, LDK, 32 * kb, 16 * n, lane));
+      for (int sl = 0; sl < 2; ++sl)
+        vf[kb][sl] = __builtin_bit_cast(bf16x8, frag_tr(B.V, LDK, 32 * kb, 16 * (2 * wc + sl), lane));
 #pragma unroll
-        for (int tb = 0; tb < 4; ++tb)
-          if (2 * kb <= tb) acc[sl][tb] = mma(lds_frag(B.tb, tf::fid(tb, kb), lane), vf, acc[sl][tb]);
+    for (int f = 0; f < tf::FRAGS; ++f) ft[f] = lds_frag(B.tb, f, lane);
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb)
+        if (2 * kb <= tb) {
+          acc[0][tb] = mma(ft[tf::fid(tb, kb)], vf[kb][0], acc[0][tb]);
+          acc[1][tb] = mma(ft[tf::fid(tb, kb)], vf[kb][1], acc[1][tb]);
+        }
+  }
+  // o^T tile by tile: lane (c, g) of O[tb][sl] holds o[16 tb + c][16 n + 4 g .. 4 g + 3]
+  f32x4 O[4][2];
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) O[tb][0] = O[tb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    bf16x8 nw[4], nq[4];
+    if (j < 3) fetch(j + 1, nw, nq);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+      acc[0][tb] = mma(fw[tb], Sb[0][j], acc[0][tb]);
+      acc[1][tb] = mma(fw[tb], Sb[1][j], acc[1][tb]);
+      if (kOut) {
+        O[tb][0] = mma(Sb[0][j], fq[tb], O[tb][0]);
+        O[tb][1] = mma(Sb[1][j], fq[tb], O[tb][1]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (j < 3) {
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        fw[tb] = nw[tb];
+        if (kOut) fq[tb] = nq[tb];
       }
     }
   }
+  if (kOut) {
+    bf16x8 kq[tf::FRAGS];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-#pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
-      const bf16x8 a = lds_frag(B.wn, tb * 4 + j, lane);
-      acc[0][tb] = mma(a, Sb[0][j], acc[0][tb]);
-      acc[1][tb] = mma(a, Sb[1][j], acc[1][tb]);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  if (out_on) {  // o^T tile by tile: lane (c, g) holds o[16 tb + c][16 n + 4 g .. 4 g + 3]
+    for (int f = 0; f < tf::FRAGS; ++f) kq[f] = lds_frag(B.qk, f, lane);
+    const float e0 = B.egs[c16], e1 = B.egs[16 + c16], e2 = B.egs[32 + c16], e3 = B.egs[48 + c16];
     bf16x8 vb[2][2];
 #pragma unroll
     for (int sl = 0; sl < 2; ++sl) {
@@ -848,37 +893,31 @@ __device__ __forceinline__ void chain_part1(const SegBuf& B, ChainRegs& R, bool 
       vb[sl][1] = pack_acc_bf16(acc[sl][2], acc[sl][3]);
     }
 #pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
-      f32x4 O[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    for (int sl = 0; sl < 2; ++sl) {
+      O[0][sl] *= e0;
+      O[1][sl] *= e1;
+      O[2][sl] *= e2;
+      O[3][sl] *= e3;
+    }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const bf16x8 qf = lds_frag(B.qg, tb * 4 + j, lane);
-        O[0] = mma(Sb[0][j], qf, O[0]);
-        O[1] = mma(Sb[1][j], qf, O[1]);
-      }
-      const float e = B.egs[16 * tb + c16];
-      const bf16x8 k0 = lds_frag(B.qk, tf::fid(tb, 0), lane);
+    for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
-      for (int sl = 0; sl < 2; ++sl) {
-        O[sl] *= e;
-        O[sl] = mma(vb[sl][0], k0, O[sl]);
+      for (int tb = 2 * jj; tb < 4; ++tb) {
+        O[tb][0] = mma(vb[0][jj], kq[tf::fid(tb, jj)], O[tb][0]);
+        O[tb][1] = mma(vb[1][jj], kq[tf::fid(tb, jj)], O[tb][1]);
       }
-      if (tb >= 2) {
-        const bf16x8 k1 = lds_frag(B.qk, tf::fid(tb, 1), lane);
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    uint16_t* orow = out + ((t0 + c16) * Hv + h) * D + 32 * wc + 4 * g4;
+    const int64_t tile = (int64_t)16 * Hv * D;
 #pragma unroll
-        for (int sl = 0; sl < 2; ++sl) O[sl] = mma(vb[sl][1], k1, O[sl]);
-      }
-      const int row = 16 * tb + c16;
-      if (row < len) {
+    for (int tb = 0; tb < 4; ++tb)
+      if (16 * tb + c16 < len) {
 #pragma unroll
         for (int sl = 0; sl < 2; ++sl) {
-          typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-          const u32x2 pk = {f2bf2(O[sl][0], O[sl][1]), f2bf2(O[sl][2], O[sl][3])};
-          *reinterpret_cast<u32x2*>(out + ((t0 + row) * Hv + h) * D + 16 * (2 * wc + sl) + 4 * g4) = pk;
+          const u32x2 pk = {f2bf2(O[tb][sl][0], O[tb][sl][1]), f2bf2(O[tb][sl][2], O[tb][sl][3])};
+          *reinterpret_cast<u32x2*>(orow + tb * tile + 16 * sl) = pk;
         }
       }
-      __builtin_amdgcn_sched_barrier(0);
-    }
   }
   // DEC vn -> hi + lo bf16 (k-slot ordered B fragments of the update)
 #pragma unroll
@@ -892,28 +931,36 @@ __device__ __forceinline__ void chain_part1(const SegBuf& B, ChainRegs& R, bool 
 #pragma unroll
     for (int j = 0; j < 2; ++j) split_bf16(acc[sl][2 * j], acc[sl][2 * j + 1], R.hi[sl][j], R.lo[sl][j]);
 }
-// Chain part 2: S' = e^{G_last} S + K^T (DEC vn), K^T straight from the K rows (exact in bf16).
+// Chain part 2: S' = e^{G_last} S + K^T (DEC vn), K^T straight from the K rows (exact in bf16).  For
+// each token half j the hi terms of all 16 accumulators go first, then the lo terms; the K^T
+// fragments of half 1 are requested before the products of half 0.
 __device__ __forceinline__ void chain_part2(const SegBuf& B, ChainRegs& R, int lane_in) {
   using namespace pf;
   int lane;
   asm volatile("v_mov_b32 %0, %1" : "=v"(lane) : "v"(lane_in));
+  bf16x8 kt[2][8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) kt[0][i] = __builtin_bit_cast(bf16x8, frag_tr_kperm(B.K, LDK, 0, 16 * i, lane));
   const float gl = B.gl;
 #pragma unroll
   for (int sl = 0; sl < 2; ++sl)
 #pragma unroll
     for (int i = 0; i < 8; ++i) R.S[sl][i] *= gl;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < 8; ++i) kt[1][i] = __builtin_bit_cast(bf16x8, frag_tr_kperm(B.K, LDK, 32, 16 * i, lane));
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const bf16x8 kt = __builtin_bit_cast(bf16x8, frag_tr_kperm(B.K, LDK, 32 * j, 16 * i, lane));
+  for (int j = 0; j < 2; ++j) {
 #pragma unroll
-      for (int sl = 0; sl < 2; ++sl) {
-        R.S[sl][i] = mma(kt, R.hi[sl][j], R.S[sl][i]);
-        R.S[sl][i] = mma(kt, R.lo[sl][j], R.S[sl][i]);
-      }
+    for (int i = 0; i < 8; ++i) {
+      R.S[0][i] = mma(kt[j][i], R.hi[0][j], R.S[0][i]);
+      R.S[1][i] = mma(kt[j][i], R.hi[1][j], R.S[1][i]);
     }
-    if (i & 1) __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      R.S[0][i] = mma(kt[j][i], R.lo[0][j], R.S[0][i]);
+      R.S[1][i] = mma(kt[j][i], R.lo[1][j], R.S[1][i]);
+    }
   }
 }
 
@@ -926,9 +973,9 @@ __device__ __forceinline__ void chain_part2(const SegBuf& B, ChainRegs& R, int l
 // from the other: two LDS barriers a chunk, met by both roles.
 template <typename BetaT, typename OutT, int kPass>
 __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
-    const uint16_t* __restrict__ q, int64_t qs, const uint16_t* __restrict__ k, int64_t ks,
-    const uint16_t* __restrict__ v, int64_t vs, const float* __restrict__ g, const BetaT* __restrict__ beta,
-    OutT* __restrict__ out, SegTable tab, int Hqk, int Hv, int use_l2, const float* __restrict__ init,
+    const uint16_t* __restrict__ qkn, const uint16_t* __restrict__ v, int64_t vs, const float* __restrict__ g,
+    const BetaT* __restrict__ beta, OutT* __restrict__ out, SegTable tab, int Hqk, int Hv, int use_l2,
+    const float* __restrict__ init,
     const int32_t* __restrict__ rows, int n_rows, float* __restrict__ final_state, float* __restrict__ trans,
     int* __restrict__ tflags, const uint8_t* __restrict__ tfrag, const int* __restrict__ warm,
     const int* __restrict__ seq_ok) {
@@ -996,40 +1043,51 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
   auto chunk_len = [&](int c) { return Ls - (cb0 + c) * CH < CH ? Ls - (cb0 + c) * CH : CH; };
   if (w < 4) {
     // ------------------------------------------------------------ local waves
-    LocIn in;
+    // Chunk j's inputs are loaded into register set j & 1 a full step before they are used: step c
+    // requests chunk c + 2 into one set and prepares chunk c + 1 from the other.  The chunk loop is
+    // unrolled by two so that each set keeps its registers; every load in it is unconditional (past
+    // the end the last chunk is requested again, unused), which keeps the wait counts exact.
+    LocIn ia, ib;
     bf16x8 qf[4], tbe[2];
-    float G = 0.f;
-    auto load = [&](int c) {
-      loc_load<need_q>(in, chunk_t0(c), chunk_len(c), kh, h, q, qs, k, ks, v, vs, g, Hv, tfr(c));
+    auto load = [&](LocIn& L, int c) __attribute__((always_inline)) {
+      const uint16_t* qkc = qkn + ((int64_t)(chunk_slot0 + c) * Hqk + kh) * (2 * CH * D);
+      loc_load<need_q>(L, chunk_t0(c), chunk_len(c), h, qkc, v, (uint32_t)vs, g, Hv, tfr(c));
     };
-    auto phase2 = [&](SegBuf& B, bool q_on) {
+    auto phase2 = [&](SegBuf& B, bool q_on) __attribute__((always_inline)) {
       switch (w) {
-        case 0: loc_phase2<0, need_q>(B, qf, G, tbe, q_on); break;
-        case 1: loc_phase2<1, need_q>(B, qf, G, tbe, q_on); break;
-        case 2: loc_phase2<2, need_q>(B, qf, G, tbe, q_on); break;
-        default: loc_phase2<3, need_q>(B, qf, G, tbe, q_on); break;
+        case 0: loc_phase2<0, need_q>(B, qf, tbe, q_on); break;
+        case 1: loc_phase2<1, need_q>(B, qf, tbe, q_on); break;
+        case 2: loc_phase2<2, need_q>(B, qf, tbe, q_on); break;
+        default: loc_phase2<3, need_q>(B, qf, tbe, q_on); break;
       }
     };
+    auto step = [&](int c, LocIn& nxt, const LocIn& cur) __attribute__((always_inline)) {  // prepare chunk c + 1 from cur
+      load(nxt, c + 2 < ntot ? c + 2 : ntot - 1);
+      loc_phase1<need_q>(sm.buf[(c + 1) & 1], cur, chunk_len(c + 1), c + 1 >= w0, qf);
+      tbe[0] = cur.tbe[0];
+      tbe[1] = cur.tbe[1];
+      lds_barrier();
+      phase2(sm.buf[(c + 1) & 1], c + 1 >= w0);
+      lds_barrier();
+    };
     if (ntot > 0) {
-      load(0);
-      loc_phase1<need_q>(sm.buf[0], in, use_l2, w0 == 0, qf, G);
-      tbe[0] = in.tbe[0];
-      tbe[1] = in.tbe[1];
-      if (ntot > 1) load(1);
+      load(ia, 0);
+      load(ib, ntot > 1 ? 1 : 0);
+      loc_phase1<need_q>(sm.buf[0], ia, chunk_len(0), w0 == 0, qf);
+      tbe[0] = ia.tbe[0];
+      tbe[1] = ia.tbe[1];
     }
     lds_barrier();
     if (ntot > 0) phase2(sm.buf[0], w0 == 0);
     lds_barrier();
-    for (int c = 0; c < ntot; ++c) {
-      const bool more = c + 1 < ntot;
-      if (more) {
-        loc_phase1<need_q>(sm.buf[(c + 1) & 1], in, use_l2, c + 1 >= w0, qf, G);
-        tbe[0] = in.tbe[0];
-        tbe[1] = in.tbe[1];
-        if (c + 2 < ntot) load(c + 2);
-      }
+    int c = 0;
+    for (; c + 2 < ntot; c += 2) {
+      step(c, ia, ib);
+      step(c + 1, ib, ia);
+    }
+    if (c + 1 < ntot) step(c, ia, ib);
+    if (ntot > 0) {  // the chain's last step: nothing left to prepare
       lds_barrier();
-      if (more) phase2(sm.buf[(c + 1) & 1], c + 1 >= w0);
       lds_barrier();
     }
   } else {
@@ -1066,9 +1124,9 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     lds_barrier();
     for (int c = 0; c < ntot; ++c) {
       const SegBuf& B = sm.buf[c & 1];
-      if (kPass == 0) chain_part1<true>(B, R, c >= w0, out, chunk_t0(c), chunk_len(c), Hv, h, wc, lane);
-      else if (mode == kSegB) chain_part1<true>(B, R, false, out, 0, 0, Hv, h, wc, lane);
-      else chain_part1<false>(B, R, false, out, 0, 0, Hv, h, wc, lane);
+      if (kPass == 0 && c >= w0) chain_part1<true, true>(B, R, out, chunk_t0(c), chunk_len(c), Hv, h, wc, lane);
+      else if (mode != kSegA) chain_part1<true, false>(B, R, out, 0, 0, Hv, h, wc, lane);
+      else chain_part1<false, false>(B, R, out, 0, 0, Hv, h, wc, lane);
       lds_barrier();
       chain_part2(B, R, lane);
       lds_barrier();
@@ -1421,12 +1479,13 @@ int64_t seg_len(int64_t total_chunks, int Hv) {
 }
 // Workspace layout: the segment table (nseq + 1 int32), the transition flags and warm-up lengths
 // (int32 per (slot, value head)), the warm-up flags (int32 per (sequence, value head)), the
-// transition slots (A, B fp32 per (slot, value head)) and the inverse kernel's fragments (12 KiB
-// per (chunk, value head)), each part 256-byte aligned.
+// transition slots (A, B fp32 per (slot, value head)), the inverse kernel's fragments (12 KiB per
+// (chunk, value head)) and its q|k records (32 KiB per (chunk, key head)), each part 256-byte
+// aligned.
 struct SegLayout {
-  int64_t L, nslots, off_flags, off_warm, off_seqok, off_trans, off_tfrag, bytes;
+  int64_t L, nslots, off_flags, off_warm, off_seqok, off_trans, off_tfrag, off_qkn, bytes;
 };
-SegLayout seg_layout(int64_t total_chunks, int nseq, int Hv) {
+SegLayout seg_layout(int64_t total_chunks, int nseq, int Hqk, int Hv) {
   auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
   SegLayout l;
   l.L = seg_len(total_chunks, Hv);
@@ -1436,14 +1495,15 @@ SegLayout seg_layout(int64_t total_chunks, int nseq, int Hv) {
   l.off_seqok = l.off_warm + up(l.nslots * Hv * 4);
   l.off_trans = l.off_seqok + up((int64_t)nseq * Hv * 4);
   l.off_tfrag = l.off_trans + l.nslots * Hv * (int64_t)sg::kTrans * 4;
-  l.bytes = l.off_tfrag + total_chunks * Hv * (int64_t)tf::BYTES;
+  l.off_qkn = l.off_tfrag + total_chunks * Hv * (int64_t)tf::BYTES;
+  l.bytes = l.off_qkn + total_chunks * Hqk * (int64_t)(2 * pf::CH * pf::D * 2);
   return l;
 }
 }  // namespace
 
-extern "C" int64_t gdn_chunk_prefill_workspace_bytes(int64_t total_chunks, int nseq, int Hv) {
-  if (total_chunks < 0 || nseq < 0 || Hv <= 0) return -1;
-  return seg_layout(total_chunks, nseq, Hv).bytes;
+extern "C" int64_t gdn_chunk_prefill_workspace_bytes(int64_t total_chunks, int nseq, int Hqk, int Hv) {
+  if (total_chunks < 0 || nseq < 0 || Hqk <= 0 || Hv <= 0) return -1;
+  return seg_layout(total_chunks, nseq, Hqk, Hv).bytes;
 }
 
 extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const void* k, int64_t k_stride,
@@ -1470,16 +1530,17 @@ extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const voi
                   v_stride % 8 == 0,
               "gdn_chunk_prefill: q/k/v rows must be 16-byte aligned");
   GDN_REQUIRE(aligned(out, 8), "gdn_chunk_prefill: out must be 8-byte aligned");
+  GDN_REQUIRE(v_stride > 0 && v_stride < (1ll << 26), "gdn_chunk_prefill: v_stride %lld out of range", (long long)v_stride);
   GDN_REQUIRE((!initial_state || aligned(initial_state, 16)) && (!final_state || aligned(final_state, 16)),
               "gdn_chunk_prefill: initial/final state must be 16-byte aligned");
   GDN_REQUIRE(workspace && aligned(workspace, 256) &&
-                  workspace_bytes >= gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hv),
+                  workspace_bytes >= gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hqk, Hv),
               "gdn_chunk_prefill: workspace missing, misaligned or smaller than %lld bytes",
-              (long long)gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hv));
+              (long long)gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hqk, Hv));
   GDN_REQUIRE(total_chunks < (1ll << 31), "gdn_chunk_prefill: too many chunks");
   if (nseq == 0) return GDN_OK;
   hipStream_t st = (hipStream_t)stream;
-  const SegLayout lay = seg_layout(total_chunks, nseq, Hv);
+  const SegLayout lay = seg_layout(total_chunks, nseq, Hqk, Hv);
   uint8_t* work = (uint8_t*)workspace;
   int32_t* seg0 = (int32_t*)work;
   int* tflags = (int*)(work + lay.off_flags);
@@ -1487,6 +1548,7 @@ extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const voi
   int* seq_ok = (int*)(work + lay.off_seqok);
   float* trans = (float*)(work + lay.off_trans);
   uint8_t* tfrag = work + lay.off_tfrag;
+  uint16_t* qkn = (uint16_t*)(work + lay.off_qkn);
   const int64_t nseg_max = (int64_t)nseq + total_chunks / lay.L;  // each sequence: <= nch / L + 1 segments
   GDN_REQUIRE(nseg_max * Hv < (1ll << 31) && lay.nslots * Hv * 64 < (1ll << 31) && (int64_t)nseq * Hv < (1ll << 31),
               "gdn_chunk_prefill: grid too large");
@@ -1498,11 +1560,13 @@ extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const voi
   if (total_chunks > 0) {  // the intra-chunk inverses, all chunks in parallel
     const dim3 gi((unsigned)Hqk, (unsigned)total_chunks);
     if (beta_dtype == GDN_BF16)
-      inv_kernel<uint16_t><<<gi, pf::NT, 0, st>>>((const uint16_t*)k, k_stride, g, (const uint16_t*)beta, cu_seqlens,
-                                                  seq_chunk0, nseq, seq_len, Hqk, Hv, use_qk_l2norm, tfrag);
+      inv_kernel<uint16_t><<<gi, pf::NT, 0, st>>>((const uint16_t*)q, q_stride, (const uint16_t*)k, k_stride, g,
+                                                  (const uint16_t*)beta, cu_seqlens, seq_chunk0, nseq, seq_len, Hqk,
+                                                  Hv, use_qk_l2norm, tfrag, qkn);
     else
-      inv_kernel<float><<<gi, pf::NT, 0, st>>>((const uint16_t*)k, k_stride, g, (const float*)beta, cu_seqlens,
-                                               seq_chunk0, nseq, seq_len, Hqk, Hv, use_qk_l2norm, tfrag);
+      inv_kernel<float><<<gi, pf::NT, 0, st>>>((const uint16_t*)q, q_stride, (const uint16_t*)k, k_stride, g,
+                                               (const float*)beta, cu_seqlens, seq_chunk0, nseq, seq_len, Hqk, Hv,
+                                               use_qk_l2norm, tfrag, qkn);
     int rc = check_launch("gdn_chunk_prefill(inverse)");
     if (rc) return rc;
   }
@@ -1510,8 +1574,8 @@ extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const voi
   auto launch = [&](int pass, int64_t blocks) {
 #define GDN_SEG_LAUNCH(BT)                                                                                     \
   (pass == 0 ? seg_kernel<BT, uint16_t, 0> : seg_kernel<BT, uint16_t, 1>)<<<(unsigned)blocks, sg::NT, 0, st>>>( \
-      (const uint16_t*)q, q_stride, (const uint16_t*)k, k_stride, (const uint16_t*)v, v_stride, g,             \
-      (const BT*)beta, (uint16_t*)out, tab, Hqk, Hv, use_qk_l2norm, initial_state, state_rows, n_rows,           \
+      qkn, (const uint16_t*)v, v_stride, g, (const BT*)beta,                                                    \
+      (uint16_t*)out, tab, Hqk, Hv, use_qk_l2norm, initial_state, state_rows, n_rows,           \
       final_state, trans, tflags, tfrag, warm, seq_ok)
     if (beta_dtype == GDN_BF16) GDN_SEG_LAUNCH(uint16_t);
     else GDN_SEG_LAUNCH(float);
@@ -1559,9 +1623,9 @@ extern "C" int gdn_chunk_prefill_noalloc(const void* q, int64_t q_stride, const 
                                          int nseq, int seq_len, int Hqk, int Hv, int D, int in_dtype,
                                          int use_qk_l2norm, void* stream) {
   clear_error();
-  GDN_REQUIRE(total_chunks >= 0 && Hv > 0, "gdn_chunk_prefill_noalloc: bad sizes");
+  GDN_REQUIRE(total_chunks >= 0 && Hqk > 0 && Hv > 0, "gdn_chunk_prefill_noalloc: bad sizes");
   GDN_REQUIRE(nseq >= 0, "gdn_chunk_prefill_noalloc: bad sizes");
-  const int64_t need = gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hv);
+  const int64_t need = gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hqk, Hv);
   GDN_REQUIRE(need <= GDN_NOALLOC_SCRATCH_BYTES,
               "gdn_chunk_prefill_noalloc: the call needs %lld bytes of workspace, the static scratch holds %lld "
               "(%lld chunks, %d sequences, %d value heads; use gdn_chunk_prefill_rows with a workspace)",
