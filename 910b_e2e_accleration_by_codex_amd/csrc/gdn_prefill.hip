@@ -399,6 +399,22 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// Inclusive prefix sum over the 64 lanes (DPP: shifts within rows of 16, then the row totals
+// broadcast into the later rows).
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ float dpp_or_zero(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, kRowMask, 0xf, false));
+}
+__device__ __forceinline__ float wave_incl_scan(float x) {
+  x += dpp_or_zero<0x111, 0xf>(x);  // row_shr:1
+  x += dpp_or_zero<0x112, 0xf>(x);  // row_shr:2
+  x += dpp_or_zero<0x114, 0xf>(x);  // row_shr:4
+  x += dpp_or_zero<0x118, 0xf>(x);  // row_shr:8
+  x += dpp_or_zero<0x142, 0xa>(x);  // row_bcast:15 into rows 1 and 3
+  x += dpp_or_zero<0x143, 0xc>(x);  // row_bcast:31 into rows 2 and 3
+  return x;
+}
+
 // ============================================================================================
 // Chunked prefill, part 1: the intra-chunk inverse, parallel over every (chunk, key head).
 // ============================================================================================
@@ -419,52 +435,75 @@ struct InvSmem {
   float T[pf::CH * pf::LDF];
   float G[pf::CH], EG[pf::CH], B[pf::CH];
 };
+// Raw inputs of one (chunk, key head) item, requested one item ahead: 4 token rows x 8 features of
+// q and k (rows past the chunk's end zero), and wave 0's g and beta of the first value head.
+struct InvIn {
+  u16x8 kx[4];  // rows past the chunk's end repeat its last row until masked at the use
+  float graw, braw;
+};
 template <typename BetaT>
-__global__ __launch_bounds__(pf::NT, 3) void inv_kernel(const uint16_t* __restrict__ q, int64_t qs,
-                                                       const uint16_t* __restrict__ k, int64_t ks,
+__device__ __forceinline__ void inv_load(InvIn& in, const ChunkPos& cp, int hk, int h0, const uint16_t* __restrict__ k,
+                                         int64_t ks,
+                                         const float* __restrict__ g, const BetaT* __restrict__ beta, int Hv) {
+  using namespace pf;
+  const int t = threadIdx.x, lane = t & 63, tq = t >> 4, fb = t & 15;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 4 * tq + i, rc = row < cp.len ? row : cp.len - 1;
+    in.kx[i] = *reinterpret_cast<const u16x8*>(k + (cp.t0 + rc) * ks + (int64_t)hk * D + 8 * fb);
+  }
+  const int tok = lane < cp.len ? lane : cp.len - 1;
+  in.graw = g[(cp.t0 + tok) * Hv + h0];
+  in.braw = Elem<BetaT>::load(beta + (cp.t0 + tok) * Hv + h0);
+}
+// Persistent: workgroup b takes items b, b + gridDim.x, ... (item = chunk slot * Hqk + key head) and
+// requests the next item's inputs as soon as the current ones are in LDS, so their latency hides
+// behind the current item's inverses.
+template <typename BetaT>
+__global__ __launch_bounds__(pf::NT, 3) void inv_kernel(const uint16_t* __restrict__ k, int64_t ks,
                                                        const float* __restrict__ g, const BetaT* __restrict__ beta,
                                                        const int32_t* __restrict__ cu,
                                                        const int32_t* __restrict__ seq_chunk0, int nseq, int seq_len,
-                                                       int Hqk, int Hv, int use_l2, uint8_t* __restrict__ tfrag,
-                                                       uint16_t* __restrict__ qkn) {
+                                                       int64_t items, int Hqk, int Hv, int use_l2,
+                                                       uint8_t* __restrict__ tfrag, uint16_t* __restrict__ kn) {
   using namespace pf;
   __shared__ InvSmem sm;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
-  const int hk = blockIdx.x, slot = blockIdx.y;
-  const ChunkPos cp = chunk_pos(slot, cu, seq_chunk0, nseq, seq_len);
-  const int r = Hv / Hqk, h0 = hk * r;
-  const int tok = lane < cp.len ? lane : cp.len - 1;
-  float graw = 0.f, braw = 0.f;
-  if (w == 0) {  // the first value head's g and beta (zero past the chunk's end)
-    const float gr = g[(cp.t0 + tok) * Hv + h0];
-    const float br = Elem<BetaT>::load(beta + (cp.t0 + tok) * Hv + h0);
-    graw = lane < cp.len ? gr : 0.f;
-    braw = lane < cp.len ? br : 0.f;
-  }
-  // q and k of the chunk (l2-normalised when asked, zero past the chunk's end) for the segment kernel:
-  // the q fragments of token tile w in k-slot order, then the K rows, 16 KiB each per (chunk, key head)
-  uint16_t* qk_out = qkn + ((int64_t)slot * Hqk + hk) * (2 * CH * D);
-  uint16_t* sQ = reinterpret_cast<uint16_t*>(sm.X);  // staged in X's space, which is written later
+  const int r = Hv / Hqk;
+  int64_t item = blockIdx.x;
+  if (item >= items) return;
+  InvIn in;
   {
-    u16x8 kx[4], qx[4];
+    const ChunkPos cp0 = chunk_pos((int)(item / Hqk), cu, seq_chunk0, nseq, seq_len);
+    inv_load<BetaT>(in, cp0, (int)(item % Hqk), (int)(item % Hqk) * r, k, ks, g, beta, Hv);
+  }
+  for (; item < items; item += gridDim.x) {
+  const int hk = (int)(item % Hqk), slot = (int)(item / Hqk);
+  const ChunkPos cp = chunk_pos(slot, cu, seq_chunk0, nseq, seq_len);
+  const int h0 = hk * r;
+  const int tok = lane < cp.len ? lane : cp.len - 1;
+  float graw = lane < cp.len ? in.graw : 0.f, braw = lane < cp.len ? in.braw : 0.f;
+  // the K rows of the chunk (l2-normalised when asked, zero past the chunk's end) for the segment
+  // kernel, 16 KiB per (chunk, key head)
+  uint16_t* k_out = kn + ((int64_t)slot * Hqk + hk) * (CH * D);
+  {
     const int tq = t >> 4, fb = t & 15;
-    load_rows4(kx, k + (int64_t)hk * D, ks, cp.t0, cp.len, tq, 8 * fb);
-    load_rows4(qx, q + (int64_t)hk * D, qs, cp.t0, cp.len, tq, 8 * fb);
-    if (use_l2) {
-      l2norm_rows4(kx);
-      l2norm_rows4(qx);
-    }
+    const u16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) in.kx[i] = 4 * tq + i < cp.len ? in.kx[i] : zero;
+    if (use_l2) l2norm_rows4(in.kx);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      *reinterpret_cast<u16x8*>(&sm.K[(4 * tq + i) * LDK + 8 * fb]) = kx[i];
-      *reinterpret_cast<u16x8*>(&sQ[(4 * tq + i) * LDK + 8 * fb]) = qx[i];
-      *reinterpret_cast<u16x8*>(qk_out + CH * D + (4 * tq + i) * D + 8 * fb) = kx[i];
+      *reinterpret_cast<u16x8*>(&sm.K[(4 * tq + i) * LDK + 8 * fb]) = in.kx[i];
+      *reinterpret_cast<u16x8*>(k_out + (4 * tq + i) * D + 8 * fb) = in.kx[i];
     }
   }
+  if (item + gridDim.x < items) {  // the next item's inputs
+    const int64_t nx = item + gridDim.x;
+    const ChunkPos cpn = chunk_pos((int)(nx / Hqk), cu, seq_chunk0, nseq, seq_len);
+    inv_load<BetaT>(in, cpn, (int)(nx % Hqk), (int)(nx % Hqk) * r, k, ks, g, beta, Hv);
+  }
   __syncthreads();
-#pragma unroll
-  for (int s = 0; s < 4; ++s)
-    *reinterpret_cast<bf16x8*>(qk_out + (w * 4 + s) * (ws::FRAG / 2) + lane * 8) = frag_kperm(sQ, LDK, 16 * w, 32 * s, lane);
   // K K^T, row tile w (blocks cb <= w), kept in registers for every value head
   f32x4 acc[4];
 #pragma unroll
@@ -478,33 +517,34 @@ __global__ __launch_bounds__(pf::NT, 3) void inv_kernel(const uint16_t* __restri
   }
   for (int j = 0; j < r; ++j) {
     const int h = h0 + j;
-    if (w == 0) {  // cumulative decay within the chunk
-      if (j > 0) {
-        const float gr = g[(cp.t0 + tok) * Hv + h];
-        const float br = Elem<BetaT>::load(beta + (cp.t0 + tok) * Hv + h);
-        graw = lane < cp.len ? gr : 0.f;
-        braw = lane < cp.len ? br : 0.f;
-      }
-      float G = graw;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const float up = __shfl_up(G, o, kWave);
-        if (lane >= o) G += up;
-      }
+    if (w == 0) {  // cumulative decay within the chunk (DPP scan); the next head's g and beta requested
+      const float G = wave_incl_scan(graw);
       sm.G[lane] = G;
       sm.EG[lane] = expf(G);
       sm.B[lane] = braw;
+      if (j + 1 < r) {
+        const float gr = g[(cp.t0 + tok) * Hv + h + 1];
+        const float br = Elem<BetaT>::load(beta + (cp.t0 + tok) * Hv + h + 1);
+        graw = lane < cp.len ? gr : 0.f;
+        braw = lane < cp.len ? br : 0.f;
+      }
     }
     __syncthreads();
+    {  // X[i][jj] = -beta_i (K K^T)_{i jj} e^{G_i - G_jj}, i = 16 w + 4 g + rr > jj = 16 cb + c
+      const f32x4 Gi = *reinterpret_cast<const f32x4*>(&sm.G[16 * w + 4 * g4]);
+      const f32x4 Bi = *reinterpret_cast<const f32x4*>(&sm.B[16 * w + 4 * g4]);
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb)
+      for (int cb = 0; cb < 4; ++cb) {
+        const float Gj = sm.G[16 * cb + c16];
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {  // X[i][jj], i = 16 w + 4 g + rr, jj = 16 cb + c
-        const int i = 16 * w + 4 * g4 + rr, jj = 16 * cb + c16;
-        float x = 0.f;
-        if (cb <= w && i > jj) x = -sm.B[i] * acc[cb][rr] * __expf(sm.G[i] - sm.G[jj]);
-        sm.X[i * LDF + jj] = x;
+        for (int rr = 0; rr < 4; ++rr) {
+          const int i = 16 * w + 4 * g4 + rr, jj = 16 * cb + c16;
+          float x = 0.f;
+          if (cb <= w && i > jj) x = -Bi[rr] * acc[cb][rr] * __expf(Gi[rr] - Gj);
+          sm.X[i * LDF + jj] = x;
+        }
       }
+    }
     __syncthreads();
     unit_lower_inv64(sm.X, sm.T, w, lane);
     // token tile w: fragments (w, s), s <= w / 2: lane (c, g) element e = T[16 w + c][32 s + 8 g + e] x ...
@@ -523,7 +563,8 @@ __global__ __launch_bounds__(pf::NT, 3) void inv_kernel(const uint16_t* __restri
       *reinterpret_cast<bf16x8*>(dst + tf::fid(w, s) * ws::FRAG) = pack8(b);
       *reinterpret_cast<bf16x8*>(dst + (tf::FRAGS + tf::fid(w, s)) * ws::FRAG) = pack8(a);
     }
-    if (j + 1 < r) __syncthreads();  // the next head rewrites G, X and T
+    __syncthreads();  // the next head (or item) rewrites K, G, X and T
+  }
   }
 }
 
@@ -624,6 +665,15 @@ __global__ __launch_bounds__(256) void seg_table_kernel(const int32_t* __restric
   if (t == 0) seg0[nseq] = base;
 }
 
+// Work item of workgroup b of n: workgroups are dealt to the 8 XCDs round-robin (b % 8), so items
+// 2p and 2p + 1 (the two value heads that read one key head's q and K, the two summaries of a slot)
+// go to workgroups b and b + 8, which share an XCD and its L2; otherwise the order is kept.  A
+// bijection on [0, n) (the last n % 16 workgroups keep their own number).
+__device__ __forceinline__ int xcd_item(int b, int n) {
+  if (b >= (n & ~15)) return b;
+  return 2 * (8 * (b >> 4) + (b & 7)) + ((b >> 3) & 1);
+}
+
 // Per-chunk operands, double-buffered: the local waves fill one buffer while the chain waves read
 // the other.  Fragment layouts as described at the top of this section (k-slot order).
 struct alignas(16) SegBuf {
@@ -648,35 +698,43 @@ enum SegMode { kSegOut = 0, kSegB = 1, kSegA = 2 };
 // A local wave's inputs for one chunk, loaded a chunk ahead.  Local wave w (threads t < 256) holds K
 // and V rows 4 tq + i x features 8 fb .. (t = 16 tq + fb: rows 16 w .. 16 w + 15), the q fragments of
 // token tile w, the T diag(beta e^G) and T diag(beta) fragments of token tile w and the g of token
-// `lane`.  q and K come from the inverse kernel's record (normalised, zero past the chunk's end).
-// V rows past the chunk's end repeat its last row: T diag(beta) has zero columns there (beta is 0
-// past the end), so they add nothing to U.  Every address is a wave-uniform base plus a 32-bit
-// lane offset.
+// `lane`.  K comes from the inverse kernel's record (normalised, zero past the chunk's end); q is
+// raw, in k-slot order (lane (c, g) of fragment s: q[16 w + c][32 s + 4 g .. + 3] and [.. + 16 ..]),
+// masked and normalised at its use.  V rows past the chunk's end repeat its last row: T diag(beta)
+// has zero columns there (beta is 0 past the end), so they add nothing to U.  Every address is a
+// wave-uniform base plus a 32-bit lane offset.
 struct LocIn {
-  u16x8 kr[4], vr[4];
-  bf16x8 qr[4], tbe[2], tbu[2];
+  u16x8 kr[4], vr[4], qr[4];
+  bf16x8 tbe[2], tbu[2];
   float graw;
 };
 template <bool kNeedQ>
-__device__ __forceinline__ void loc_load(LocIn& L, int64_t t0, int len, int h, const uint16_t* __restrict__ qkc,
-                                         const uint16_t* __restrict__ v, uint32_t vs, const float* __restrict__ g,
-                                         int Hv, const uint8_t* __restrict__ tfr) {
+__device__ __forceinline__ void loc_load(LocIn& L, int64_t t0, int len, int kh, int h,
+                                         const uint16_t* __restrict__ kc, const uint16_t* __restrict__ q,
+                                         uint32_t qs, const uint16_t* __restrict__ v, uint32_t vs,
+                                         const float* __restrict__ g, int Hv, const uint8_t* __restrict__ tfr) {
   using namespace pf;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const uint32_t tq = t >> 4, fb = t & 15;
-  const uint16_t* kb = qkc + CH * D;
-  const uint16_t* vb = v + t0 * vs + (int64_t)h * D;
+  // byte offsets as 32-bit values: the loads address a uniform base plus a VGPR offset
+  const char* kb = reinterpret_cast<const char*>(kc);
+  const char* vb = reinterpret_cast<const char*>(v + t0 * vs + (int64_t)h * D);
   const float* gb = g + t0 * Hv + h;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t row = 4 * tq + i, rc = row < (uint32_t)len ? row : (uint32_t)len - 1;
-    L.kr[i] = *reinterpret_cast<const u16x8*>(kb + (row * D + 8 * fb));
-    L.vr[i] = *reinterpret_cast<const u16x8*>(vb + (rc * vs + 8 * fb));
+    L.kr[i] = *reinterpret_cast<const u16x8*>(kb + ((row * D + 8 * fb) * 2u));
+    L.vr[i] = *reinterpret_cast<const u16x8*>(vb + ((rc * vs + 8 * fb) * 2u));
   }
   if (kNeedQ) {
+    const uint32_t row = 16 * w + (lane & 15), rc = row < (uint32_t)len ? row : (uint32_t)len - 1;
+    const char* qb = reinterpret_cast<const char*>(q + t0 * qs + (int64_t)kh * D);
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
-      L.qr[s] = *reinterpret_cast<const bf16x8*>(qkc + (uint32_t)((w * 4 + s) * (ws::FRAG / 2) + lane * 8));
+    for (int s = 0; s < 4; ++s) {
+      const uint32_t off = (rc * qs + 32 * s + 4 * (lane >> 4)) * 2u;
+      const u16x4 lo = *reinterpret_cast<const u16x4*>(qb + off), hi = *reinterpret_cast<const u16x4*>(qb + off + 32u);
+      L.qr[s] = u16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
   }
   // every wave issues the same loads (tiles 0 and 1 read their one fragment twice): the wait
   // counts before the uses then stay exact along every path through the chunk loop
@@ -686,29 +744,15 @@ __device__ __forceinline__ void loc_load(LocIn& L, int64_t t0, int len, int h, c
     L.tbu[s] = *reinterpret_cast<const bf16x8*>(tfr + (uint32_t)((tf::FRAGS + tf::fid(w, s)) * ws::FRAG + lane * 16));
   }
   const uint32_t tok = lane < len ? lane : len - 1;
-  L.graw = gb[tok * (uint32_t)Hv];
+  L.graw = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(gb) + tok * (uint32_t)Hv * 4u);
 }
 
-// Inclusive prefix sum over the 64 lanes (DPP: shifts within rows of 16, then the row totals
-// broadcast into the later rows).
-template <int kCtrl, int kRowMask>
-__device__ __forceinline__ float dpp_or_zero(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, kRowMask, 0xf, false));
-}
-__device__ __forceinline__ float wave_incl_scan(float x) {
-  x += dpp_or_zero<0x111, 0xf>(x);  // row_shr:1
-  x += dpp_or_zero<0x112, 0xf>(x);  // row_shr:2
-  x += dpp_or_zero<0x114, 0xf>(x);  // row_shr:4
-  x += dpp_or_zero<0x118, 0xf>(x);  // row_shr:8
-  x += dpp_or_zero<0x142, 0xa>(x);  // row_bcast:15 into rows 1 and 3
-  x += dpp_or_zero<0x143, 0xc>(x);  // row_bcast:31 into rows 2 and 3
-  return x;
-}
-
-// Local phase 1 (wave w < 4): K and V rows into the buffer, the q fragments (kept in qf for phase
-// 2); wave 0 also forms the decay factors (G, e^{G_last - G}, scale e^G, e^{G_last}).
+// Local phase 1 (wave w < 4): K and V rows into the buffer, the q fragments (masked, l2-normalised
+// when asked; kept in qf for phase 2); wave 0 also forms the decay factors (G, e^{G_last - G},
+// scale e^G, e^{G_last}).
 template <bool kNeedQ>
-__device__ __forceinline__ void loc_phase1(SegBuf& B, const LocIn& in, int len, bool q_on, bf16x8 (&qf)[4]) {
+__device__ __forceinline__ void loc_phase1(SegBuf& B, const LocIn& in, int len, int use_l2, bool q_on,
+                                           bf16x8 (&qf)[4]) {
   using namespace pf;
   int t;  // opaque per call: the LDS addresses derived from it are not hoisted out of the chunk loop
   asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"((int)threadIdx.x));
@@ -722,9 +766,23 @@ __device__ __forceinline__ void loc_phase1(SegBuf& B, const LocIn& in, int len, 
   for (int s = 0; s < 2; ++s)
     if (2 * s <= w) *reinterpret_cast<bf16x8*>(B.tb + tf::fid(w, s) * ws::FRAG + lane * 16) = in.tbu[s];
   if (kNeedQ && q_on) {
+    const u16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+    const bool live = 16 * w + (lane & 15) < len;
+    u16x8 qr[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qr[s] = live ? in.qr[s] : zero;
+    if (use_l2) {  // the row's 128 values sit in the 4 lanes c, c + 16, c + 32, c + 48
+      float ss = 0.f;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) ss = sumsq_bf16(qr[s], ss);
+      ss = xor32_sum(xor16_sum(ss));
+      const float inv = l2norm_inv(ss);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) qr[s] = scale_bf16(qr[s], inv);
+    }
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      qf[s] = in.qr[s];
+      qf[s] = __builtin_bit_cast(bf16x8, qr[s]);
       *reinterpret_cast<bf16x8*>(B.qg + (w * 4 + s) * ws::FRAG + lane * 16) = qf[s];
     }
   }
@@ -825,7 +883,20 @@ __device__ __forceinline__ void chain_part1(const SegBuf& B, ChainRegs& R, uint1
       if (kOut) q_[tb] = lds_frag(B.qg, tb * 4 + j, lane);
     }
   };
+  // the U operands and block 0's fragments are requested first; the bf16 copy of the state is
+  // formed while they arrive
+  bf16x8 vf[2][2], ft[tf::FRAGS];
+  if (kUseU) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int sl = 0; sl < 2; ++sl)
+        vf[kb][sl] = __builtin_bit_cast(bf16x8, frag_tr(B.V, LDK, 32 * kb, 16 * (2 * wc + sl), lane));
+#pragma unroll
+    for (int f = 0; f < tf::FRAGS; ++f) ft[f] = lds_frag(B.tb, f, lane);
+  }
   fetch(0, fw, fq);
+  __builtin_amdgcn_sched_barrier(0);
   bf16x8 Sb[2][4];
 #pragma unroll
   for (int sl = 0; sl < 2; ++sl)
@@ -837,14 +908,6 @@ __device__ __forceinline__ void chain_part1(const SegBuf& B, ChainRegs& R, uint1
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb) acc[sl][tb] = f32x4{0.f, 0.f, 0.f, 0.f};
   if (kUseU) {  // U = T diag(beta) V, token tile tb, k-blocks kb <= tb / 2
-    bf16x8 vf[2][2], ft[tf::FRAGS];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int sl = 0; sl < 2; ++sl)
-        vf[kb][sl] = __builtin_bit_cast(bf16x8, frag_tr(B.V, LDK, 32 * kb, 16 * (2 * wc + sl), lane));
-#pragma unroll
-    for (int f = 0; f < tf::FRAGS; ++f) ft[f] = lds_frag(B.tb, f, lane);
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -939,20 +1002,20 @@ __device__ __forceinline__ void chain_part2(const SegBuf& B, ChainRegs& R, int l
   int lane;
   asm volatile("v_mov_b32 %0, %1" : "=v"(lane) : "v"(lane_in));
   bf16x8 kt[2][8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) kt[0][i] = __builtin_bit_cast(bf16x8, frag_tr_kperm(B.K, LDK, 0, 16 * i, lane));
   const float gl = B.gl;
 #pragma unroll
-  for (int sl = 0; sl < 2; ++sl)
+  for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) R.S[sl][i] *= gl;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) kt[1][i] = __builtin_bit_cast(bf16x8, frag_tr_kperm(B.K, LDK, 32, 16 * i, lane));
+    for (int i = 0; i < 8; ++i) kt[j][i] = __builtin_bit_cast(bf16x8, frag_tr_kperm(B.K, LDK, 32 * j, 16 * i, lane));
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
+      if (j == 0) {  // the decay of the state, each tile just before its first product
+        R.S[0][i] *= gl;
+        R.S[1][i] *= gl;
+      }
       R.S[0][i] = mma(kt[j][i], R.hi[0][j], R.S[0][i]);
       R.S[1][i] = mma(kt[j][i], R.hi[1][j], R.S[1][i]);
     }
@@ -973,7 +1036,8 @@ __device__ __forceinline__ void chain_part2(const SegBuf& B, ChainRegs& R, int l
 // from the other: two LDS barriers a chunk, met by both roles.
 template <typename BetaT, typename OutT, int kPass>
 __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
-    const uint16_t* __restrict__ qkn, const uint16_t* __restrict__ v, int64_t vs, const float* __restrict__ g,
+    const uint16_t* __restrict__ q, int64_t qs, const uint16_t* __restrict__ kn, const uint16_t* __restrict__ v,
+    int64_t vs, const float* __restrict__ g,
     const BetaT* __restrict__ beta, OutT* __restrict__ out, SegTable tab, int Hqk, int Hv, int use_l2,
     const float* __restrict__ init,
     const int32_t* __restrict__ rows, int n_rows, float* __restrict__ final_state, float* __restrict__ trans,
@@ -984,7 +1048,7 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
   const int t = threadIdx.x, w = t >> 6, lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
   int mode, h, s, idx, slot = -1;
   if (kPass == 0) {
-    const int item = blockIdx.x, j = item / Hv;
+    const int item = xcd_item(blockIdx.x, gridDim.x), j = item / Hv;
     h = item % Hv;
     if (j >= tab.first_seg(tab.nseq)) return;
     s = tab.seq_of_seg(j);
@@ -992,7 +1056,7 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     if (idx > 0) slot = tab.first_slot(s) + idx - 1;  // the previous segment's slot holds this one's state
     mode = kSegOut;
   } else {
-    const int item = blockIdx.x, rest = item >> 1;
+    const int item = xcd_item(blockIdx.x, gridDim.x), rest = item >> 1;
     const int ts = rest / Hv;
     h = rest % Hv;
     if (ts >= tab.first_slot(tab.nseq)) return;
@@ -1050,8 +1114,8 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     LocIn ia, ib;
     bf16x8 qf[4], tbe[2];
     auto load = [&](LocIn& L, int c) __attribute__((always_inline)) {
-      const uint16_t* qkc = qkn + ((int64_t)(chunk_slot0 + c) * Hqk + kh) * (2 * CH * D);
-      loc_load<need_q>(L, chunk_t0(c), chunk_len(c), h, qkc, v, (uint32_t)vs, g, Hv, tfr(c));
+      const uint16_t* kc = kn + ((int64_t)(chunk_slot0 + c) * Hqk + kh) * (CH * D);
+      loc_load<need_q>(L, chunk_t0(c), chunk_len(c), kh, h, kc, q, (uint32_t)qs, v, (uint32_t)vs, g, Hv, tfr(c));
     };
     auto phase2 = [&](SegBuf& B, bool q_on) __attribute__((always_inline)) {
       switch (w) {
@@ -1063,7 +1127,7 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     };
     auto step = [&](int c, LocIn& nxt, const LocIn& cur) __attribute__((always_inline)) {  // prepare chunk c + 1 from cur
       load(nxt, c + 2 < ntot ? c + 2 : ntot - 1);
-      loc_phase1<need_q>(sm.buf[(c + 1) & 1], cur, chunk_len(c + 1), c + 1 >= w0, qf);
+      loc_phase1<need_q>(sm.buf[(c + 1) & 1], cur, chunk_len(c + 1), use_l2, c + 1 >= w0, qf);
       tbe[0] = cur.tbe[0];
       tbe[1] = cur.tbe[1];
       lds_barrier();
@@ -1073,7 +1137,7 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     if (ntot > 0) {
       load(ia, 0);
       load(ib, ntot > 1 ? 1 : 0);
-      loc_phase1<need_q>(sm.buf[0], ia, chunk_len(0), w0 == 0, qf);
+      loc_phase1<need_q>(sm.buf[0], ia, chunk_len(0), use_l2, w0 == 0, qf);
       tbe[0] = ia.tbe[0];
       tbe[1] = ia.tbe[1];
     }
@@ -1480,7 +1544,7 @@ int64_t seg_len(int64_t total_chunks, int Hv) {
 // Workspace layout: the segment table (nseq + 1 int32), the transition flags and warm-up lengths
 // (int32 per (slot, value head)), the warm-up flags (int32 per (sequence, value head)), the
 // transition slots (A, B fp32 per (slot, value head)), the inverse kernel's fragments (12 KiB per
-// (chunk, value head)) and its q|k records (32 KiB per (chunk, key head)), each part 256-byte
+// (chunk, value head)) and its normalised K rows (16 KiB per (chunk, key head)), each part 256-byte
 // aligned.
 struct SegLayout {
   int64_t L, nslots, off_flags, off_warm, off_seqok, off_trans, off_tfrag, off_qkn, bytes;
@@ -1496,7 +1560,7 @@ SegLayout seg_layout(int64_t total_chunks, int nseq, int Hqk, int Hv) {
   l.off_trans = l.off_seqok + up((int64_t)nseq * Hv * 4);
   l.off_tfrag = l.off_trans + l.nslots * Hv * (int64_t)sg::kTrans * 4;
   l.off_qkn = l.off_tfrag + total_chunks * Hv * (int64_t)tf::BYTES;
-  l.bytes = l.off_qkn + total_chunks * Hqk * (int64_t)(2 * pf::CH * pf::D * 2);
+  l.bytes = l.off_qkn + total_chunks * Hqk * (int64_t)(pf::CH * pf::D * 2);
   return l;
 }
 }  // namespace
@@ -1530,9 +1594,10 @@ extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const voi
                   v_stride % 8 == 0,
               "gdn_chunk_prefill: q/k/v rows must be 16-byte aligned");
   GDN_REQUIRE(aligned(out, 8), "gdn_chunk_prefill: out must be 8-byte aligned");
-  GDN_REQUIRE(v_stride > 0 && v_stride < (1ll << 26), "gdn_chunk_prefill: v_stride %lld out of range", (long long)v_stride);
   GDN_REQUIRE((!initial_state || aligned(initial_state, 16)) && (!final_state || aligned(final_state, 16)),
               "gdn_chunk_prefill: initial/final state must be 16-byte aligned");
+  GDN_REQUIRE(v_stride > 0 && v_stride < (1ll << 26) && q_stride > 0 && q_stride < (1ll << 26),
+              "gdn_chunk_prefill: q/v token strides out of range");
   GDN_REQUIRE(workspace && aligned(workspace, 256) &&
                   workspace_bytes >= gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hqk, Hv),
               "gdn_chunk_prefill: workspace missing, misaligned or smaller than %lld bytes",
@@ -1548,7 +1613,7 @@ extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const voi
   int* seq_ok = (int*)(work + lay.off_seqok);
   float* trans = (float*)(work + lay.off_trans);
   uint8_t* tfrag = work + lay.off_tfrag;
-  uint16_t* qkn = (uint16_t*)(work + lay.off_qkn);
+  uint16_t* kn = (uint16_t*)(work + lay.off_qkn);
   const int64_t nseg_max = (int64_t)nseq + total_chunks / lay.L;  // each sequence: <= nch / L + 1 segments
   GDN_REQUIRE(nseg_max * Hv < (1ll << 31) && lay.nslots * Hv * 64 < (1ll << 31) && (int64_t)nseq * Hv < (1ll << 31),
               "gdn_chunk_prefill: grid too large");
@@ -1558,15 +1623,16 @@ extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const voi
     if (rc) return rc;
   }
   if (total_chunks > 0) {  // the intra-chunk inverses, all chunks in parallel
-    const dim3 gi((unsigned)Hqk, (unsigned)total_chunks);
+    const int64_t items = total_chunks * Hqk;
+    const unsigned gi = (unsigned)(items < 3ll * device_cus() ? items : 3ll * device_cus());
     if (beta_dtype == GDN_BF16)
-      inv_kernel<uint16_t><<<gi, pf::NT, 0, st>>>((const uint16_t*)q, q_stride, (const uint16_t*)k, k_stride, g,
-                                                  (const uint16_t*)beta, cu_seqlens, seq_chunk0, nseq, seq_len, Hqk,
-                                                  Hv, use_qk_l2norm, tfrag, qkn);
+      inv_kernel<uint16_t><<<gi, pf::NT, 0, st>>>((const uint16_t*)k, k_stride, g,
+                                                  (const uint16_t*)beta, cu_seqlens, seq_chunk0, nseq, seq_len, items,
+                                                  Hqk, Hv, use_qk_l2norm, tfrag, kn);
     else
-      inv_kernel<float><<<gi, pf::NT, 0, st>>>((const uint16_t*)q, q_stride, (const uint16_t*)k, k_stride, g,
-                                               (const float*)beta, cu_seqlens, seq_chunk0, nseq, seq_len, Hqk, Hv,
-                                               use_qk_l2norm, tfrag, qkn);
+      inv_kernel<float><<<gi, pf::NT, 0, st>>>((const uint16_t*)k, k_stride, g,
+                                               (const float*)beta, cu_seqlens, seq_chunk0, nseq, seq_len, items, Hqk,
+                                               Hv, use_qk_l2norm, tfrag, kn);
     int rc = check_launch("gdn_chunk_prefill(inverse)");
     if (rc) return rc;
   }
@@ -1574,7 +1640,7 @@ extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const voi
   auto launch = [&](int pass, int64_t blocks) {
 #define GDN_SEG_LAUNCH(BT)                                                                                     \
   (pass == 0 ? seg_kernel<BT, uint16_t, 0> : seg_kernel<BT, uint16_t, 1>)<<<(unsigned)blocks, sg::NT, 0, st>>>( \
-      qkn, (const uint16_t*)v, v_stride, g, (const BT*)beta,                                                    \
+      (const uint16_t*)q, q_stride, kn, (const uint16_t*)v, v_stride, g, (const BT*)beta,                                                    \
       (uint16_t*)out, tab, Hqk, Hv, use_qk_l2norm, initial_state, state_rows, n_rows,           \
       final_state, trans, tflags, tfrag, warm, seq_ok)
     if (beta_dtype == GDN_BF16) GDN_SEG_LAUNCH(uint16_t);

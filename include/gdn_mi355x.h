@@ -117,7 +117,7 @@ int gdn_unit_lower_inv(const float* X, float* T, int64_t batch, int n, void* str
  * bytes per sequence and per segment), the fp32 transition maps of the segments that have a
  * successor (at most about 32 MiB: sequences are cut into segments so that about 256 (segment,
  * value head) items exist), the intra-chunk inverse fragments (12 KiB per (chunk, value head)) and
- * the normalised q|k records (32 KiB per (chunk, key head)).
+ * the normalised K rows (16 KiB per (chunk, key head)).
  */
 int64_t gdn_chunk_prefill_workspace_bytes(int64_t total_chunks, int nseq, int Hqk, int Hv);
 
@@ -213,7 +213,7 @@ int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const void* k, int64
  * every GPU it runs on until the process ends.  A call whose
  * gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hqk, Hv) exceeds it is rejected with
  * GDN_EINVAL before any launch (the workspace is at most about 32 MiB plus 12 KiB per (chunk, value
- * head) plus 32 KiB per (chunk, key head): 256 MiB holds e.g. 8192 tokens at Hqk = 16, Hv = 32).  Every
+ * head) plus 16 KiB per (chunk, key head): 256 MiB holds e.g. 8192 tokens at Hqk = 16, Hv = 32).  Every
  * call on one GPU shares that GPU's array: calls that overlap on one GPU (other streams, other host
  * threads) race and give wrong results -- order them on one stream.  The array needs no clearing
  * (every record a call reads, the same call writes first).
