@@ -415,6 +415,87 @@ __device__ __forceinline__ float wave_incl_scan(float x) {
   return x;
 }
 
+// Segment bookkeeping of the chunked prefill (shared by its kernels).
+namespace sg {
+constexpr int NT = 512;                      // 8 waves
+constexpr int kMinSeg = 4;                   // shortest segment the host cuts (chunks)
+constexpr int kTargetItems = 256;            // segments x value heads the host aims for
+constexpr float kNegligibleLog = -44.3614f;  // ln(2^-64)
+constexpr int kTrans = 2 * pf::D * pf::D;    // floats per (slot, head): A, then B
+}  // namespace sg
+
+// The segments of a batch: packed sequences (seg0[s] = segments of the sequences before s, built by
+// seg_table_kernel) or nseq uniform sequences of seq_len tokens.  Segment j of sequence s covers
+// chunks L (j - first_seg(s)) .. + L - 1 (fewer in its last segment); an empty sequence has one
+// segment without chunks.  Every segment but the last of its sequence owns a transition slot
+// (A, B), numbered first_slot(s) = first_seg(s) - s onwards.
+struct SegTable {
+  const int32_t* cu;
+  const int32_t* chunk0;
+  const int32_t* seg0;
+  int nseq, seq_len, L;
+  __device__ __forceinline__ int nch(int s) const {
+    return cu ? chunk0[s + 1] - chunk0[s] : (seq_len + pf::CH - 1) / pf::CH;
+  }
+  __device__ __forceinline__ int nseg_of(int n) const { return n <= L ? 1 : (n + L - 1) / L; }
+  __device__ __forceinline__ int first_seg(int s) const { return cu ? seg0[s] : s * nseg_of(nch(0)); }
+  __device__ __forceinline__ int first_slot(int s) const { return first_seg(s) - s; }
+  // Dense index of sequence s's first chunk (the inverse kernel's fragment slot).
+  __device__ __forceinline__ int first_chunk(int s) const { return cu ? chunk0[s] : s * nch(0); }
+  __device__ __forceinline__ int64_t start(int s) const { return cu ? (int64_t)cu[s] : (int64_t)s * seq_len; }
+  __device__ __forceinline__ int len(int s) const { return cu ? cu[s + 1] - cu[s] : seq_len; }
+  // The sequence of segment j (the last s with first_seg(s) <= j).
+  __device__ int seq_of_seg(int j) const {
+    if (!cu) return j / nseg_of(nch(0));
+    int lo = 0, hi = nseq - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (seg0[mid] <= j) lo = mid;
+      else hi = mid - 1;
+    }
+    return lo;
+  }
+  // The sequence of transition slot t (the last s with first_slot(s) <= t).
+  __device__ int seq_of_slot(int t) const {
+    if (!cu) return t / (nseg_of(nch(0)) - 1);
+    int lo = 0, hi = nseq - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (seg0[mid] - mid <= t) lo = mid;
+      else hi = mid - 1;
+    }
+    return lo;
+  }
+};
+
+// seg0 (nseq + 1 entries) from the chunk prefix sums: one workgroup, a block-wise scan.
+__global__ __launch_bounds__(256) void seg_table_kernel(const int32_t* __restrict__ chunk0, int nseq, int L,
+                                                       int32_t* __restrict__ seg0) {
+  __shared__ int part[256];
+  const int t = threadIdx.x;
+  int base = 0;
+  for (int s0 = 0; s0 < nseq; s0 += 256) {
+    const int s = s0 + t;
+    int n = 0;
+    if (s < nseq) {
+      const int c = chunk0[s + 1] - chunk0[s];
+      n = c <= L ? 1 : (c + L - 1) / L;
+    }
+    part[t] = n;
+    __syncthreads();
+    for (int o = 1; o < 256; o <<= 1) {  // inclusive scan
+      const int x = t >= o ? part[t - o] : 0;
+      __syncthreads();
+      part[t] += x;
+      __syncthreads();
+    }
+    if (s < nseq) seg0[s] = base + part[t] - n;
+    base += part[255];
+    __syncthreads();
+  }
+  if (t == 0) seg0[nseq] = base;
+}
+
 // ============================================================================================
 // Chunked prefill, part 1: the intra-chunk inverse, parallel over every (chunk, key head).
 // ============================================================================================
@@ -435,6 +516,39 @@ struct InvSmem {
   float T[pf::CH * pf::LDF];
   float G[pf::CH], EG[pf::CH], B[pf::CH];
 };
+// Warm-up length for the transition after the segment ending with the chunk at token t_last (one
+// wave): the least w such that the summed log decay of the segment's last w chunks is below
+// ln 2^-64 -- the norm bound of the dropped map with unit keys and beta in [0, 1] -- or 0 when there
+// is none within the segment's L chunks or a beta outside [0, 1] (or a NaN) comes first.  Chunks
+// are taken back from the segment's end, four at a time (lane = token).
+template <typename BetaT>
+__device__ int chunk_warm(const float* __restrict__ g, const BetaT* __restrict__ beta, int Hv, int h, int64_t t_last,
+                          int L) {
+  const int lane = threadIdx.x & 63;
+  float acc = 0.f;
+  for (int c0 = 0; c0 < L; c0 += 4) {
+    float x[4];
+    int ok[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t tok = t_last - (int64_t)(c0 + u) * pf::CH + lane;
+      const bool in = c0 + u < L;
+      const float gv = in ? g[tok * Hv + h] : 0.f;
+      const float bv = in ? Elem<BetaT>::load(beta + tok * Hv + h) : 0.f;
+      x[u] = gv;
+      ok[u] = (bv >= 0.f && bv <= 1.f && gv == gv) ? 1 : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (c0 + u >= L) return 0;
+      if (__builtin_amdgcn_ballot_w64(ok[u] == 0) != 0) return 0;
+      acc += wave_sum_fast(x[u]);
+      if (acc < sg::kNegligibleLog) return c0 + u + 1;
+    }
+  }
+  return 0;
+}
+
 // Raw inputs of one (chunk, key head) item, requested one item ahead: 4 token rows x 8 features of
 // q and k (rows past the chunk's end zero), and wave 0's g and beta of the first value head.
 struct InvIn {
@@ -465,7 +579,8 @@ __global__ __launch_bounds__(pf::NT, 3) void inv_kernel(const uint16_t* __restri
                                                        const int32_t* __restrict__ cu,
                                                        const int32_t* __restrict__ seq_chunk0, int nseq, int seq_len,
                                                        int64_t items, int Hqk, int Hv, int use_l2,
-                                                       uint8_t* __restrict__ tfrag, uint16_t* __restrict__ kn) {
+                                                       uint8_t* __restrict__ tfrag, uint16_t* __restrict__ kn,
+                                                       SegTable tab, int* __restrict__ warm) {
   using namespace pf;
   __shared__ InvSmem sm;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
@@ -565,6 +680,16 @@ __global__ __launch_bounds__(pf::NT, 3) void inv_kernel(const uint16_t* __restri
     }
     __syncthreads();  // the next head (or item) rewrites K, G, X and T
   }
+  // the last chunk of a segment with a successor: that transition slot's warm-up length per value
+  // head (wave j takes head h0 + j)
+  const int nch = tab.nch(cp.seq);
+  if ((cp.c + 1) % tab.L == 0 && cp.c + 1 < nch) {
+    const int ts = tab.first_slot(cp.seq) + (cp.c + 1) / tab.L - 1;
+    for (int j = w; j < r; j += 4) {
+      const int w_ = use_l2 ? chunk_warm(g, beta, Hv, h0 + j, cp.t0, tab.L) : 0;
+      if (lane == 0) warm[(int64_t)ts * Hv + h0 + j] = w_;
+    }
+  }
   }
 }
 
@@ -585,84 +710,21 @@ __global__ __launch_bounds__(pf::NT, 3) void inv_kernel(const uint16_t* __restri
 // With unit keys (in-kernel l2norm) and 0 <= beta <= 1 each token's map gamma (I - beta k k^T) has
 // spectral norm <= gamma, so ||A_j|| <= exp(sum of g over segment j).  When that bound is below
 // 2^-64, A_j S_j lies far below the fp32 rounding of S_{j+1} and A_j is not formed (flag 0).
-namespace sg {
-constexpr int NT = 512;                      // 8 waves
-constexpr int kMinSeg = 4;                   // shortest segment the host cuts (chunks)
-constexpr int kTargetItems = 256;            // segments x value heads the host aims for
-constexpr float kNegligibleLog = -44.3614f;  // ln(2^-64)
-constexpr int kTrans = 2 * pf::D * pf::D;    // floats per (slot, head): A, then B
-}  // namespace sg
 
-// The segments of a batch: packed sequences (seg0[s] = segments of the sequences before s, built by
-// seg_table_kernel) or nseq uniform sequences of seq_len tokens.  Segment j of sequence s covers
-// chunks L (j - first_seg(s)) .. + L - 1 (fewer in its last segment); an empty sequence has one
-// segment without chunks.  Every segment but the last of its sequence owns a transition slot
-// (A, B), numbered first_slot(s) = first_seg(s) - s onwards.
-struct SegTable {
-  const int32_t* cu;
-  const int32_t* chunk0;
-  const int32_t* seg0;
-  int nseq, seq_len, L;
-  __device__ __forceinline__ int nch(int s) const {
-    return cu ? chunk0[s + 1] - chunk0[s] : (seq_len + pf::CH - 1) / pf::CH;
+// Warm-up lengths.  The state entering segment j + 1 differs from the chain run from zero over the
+// last w chunks of segment j by the map of those w chunks applied to the state before them; with
+// unit keys and beta in [0, 1] that map's norm is at most exp(sum of g over the w chunks).  The
+// inverse kernel writes each transition slot's least w whose bound is below 2^-64 (0: none).  A
+// (sequence, value head) pair whose every slot has one runs no summaries and no combination, and
+// its later segments start from their warm-ups.  One wave reads the pair's slots, 64 at a time.
+__device__ bool seq_warm_ok(const SegTable& tab, const int* __restrict__ warm, int Hv, int h, int s) {
+  const int lane = threadIdx.x & 63;
+  const int ts0 = tab.first_slot(s), nslot = tab.first_slot(s + 1) - ts0;
+  for (int j0 = 0; j0 < nslot; j0 += 64) {
+    const int wv = j0 + lane < nslot ? warm[(int64_t)(ts0 + j0 + lane) * Hv + h] : 1;
+    if (__builtin_amdgcn_ballot_w64(wv == 0) != 0) return false;
   }
-  __device__ __forceinline__ int nseg_of(int n) const { return n <= L ? 1 : (n + L - 1) / L; }
-  __device__ __forceinline__ int first_seg(int s) const { return cu ? seg0[s] : s * nseg_of(nch(0)); }
-  __device__ __forceinline__ int first_slot(int s) const { return first_seg(s) - s; }
-  // Dense index of sequence s's first chunk (the inverse kernel's fragment slot).
-  __device__ __forceinline__ int first_chunk(int s) const { return cu ? chunk0[s] : s * nch(0); }
-  __device__ __forceinline__ int64_t start(int s) const { return cu ? (int64_t)cu[s] : (int64_t)s * seq_len; }
-  __device__ __forceinline__ int len(int s) const { return cu ? cu[s + 1] - cu[s] : seq_len; }
-  // The sequence of segment j (the last s with first_seg(s) <= j).
-  __device__ int seq_of_seg(int j) const {
-    if (!cu) return j / nseg_of(nch(0));
-    int lo = 0, hi = nseq - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (seg0[mid] <= j) lo = mid;
-      else hi = mid - 1;
-    }
-    return lo;
-  }
-  // The sequence of transition slot t (the last s with first_slot(s) <= t).
-  __device__ int seq_of_slot(int t) const {
-    if (!cu) return t / (nseg_of(nch(0)) - 1);
-    int lo = 0, hi = nseq - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (seg0[mid] - mid <= t) lo = mid;
-      else hi = mid - 1;
-    }
-    return lo;
-  }
-};
-
-// seg0 (nseq + 1 entries) from the chunk prefix sums: one workgroup, a block-wise scan.
-__global__ __launch_bounds__(256) void seg_table_kernel(const int32_t* __restrict__ chunk0, int nseq, int L,
-                                                       int32_t* __restrict__ seg0) {
-  __shared__ int part[256];
-  const int t = threadIdx.x;
-  int base = 0;
-  for (int s0 = 0; s0 < nseq; s0 += 256) {
-    const int s = s0 + t;
-    int n = 0;
-    if (s < nseq) {
-      const int c = chunk0[s + 1] - chunk0[s];
-      n = c <= L ? 1 : (c + L - 1) / L;
-    }
-    part[t] = n;
-    __syncthreads();
-    for (int o = 1; o < 256; o <<= 1) {  // inclusive scan
-      const int x = t >= o ? part[t - o] : 0;
-      __syncthreads();
-      part[t] += x;
-      __syncthreads();
-    }
-    if (s < nseq) seg0[s] = base + part[t] - n;
-    base += part[255];
-    __syncthreads();
-  }
-  if (t == 0) seg0[nseq] = base;
+  return true;
 }
 
 // Work item of workgroup b of n: workgroups are dealt to the 8 XCDs round-robin (b % 8), so items
@@ -1041,8 +1103,7 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     const BetaT* __restrict__ beta, OutT* __restrict__ out, SegTable tab, int Hqk, int Hv, int use_l2,
     const float* __restrict__ init,
     const int32_t* __restrict__ rows, int n_rows, float* __restrict__ final_state, float* __restrict__ trans,
-    int* __restrict__ tflags, const uint8_t* __restrict__ tfrag, const int* __restrict__ warm,
-    const int* __restrict__ seq_ok) {
+    int* __restrict__ tflags, const uint8_t* __restrict__ tfrag, const int* __restrict__ warm) {
   using namespace pf;
   __shared__ SegSmem sm;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
@@ -1064,9 +1125,9 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     idx = ts - tab.first_slot(s);
     slot = ts;
     mode = (item & 1) ? kSegA : kSegB;
-    if (seq_ok[(int64_t)s * Hv + h]) return;  // the output pass warms up instead
+    if (seq_warm_ok(tab, warm, Hv, h, s)) return;  // the output pass warms up instead
   }
-  const bool warm_path = kPass == 0 && slot >= 0 && seq_ok[(int64_t)s * Hv + h] != 0;
+  const bool warm_path = kPass == 0 && slot >= 0 && seq_warm_ok(tab, warm, Hv, h, s);
   const int kh = h / (Hv / Hqk);
   const int nch_s = tab.nch(s), c_begin = idx * tab.L;
   const int n = nch_s - c_begin < tab.L ? nch_s - c_begin : tab.L;
@@ -1216,68 +1277,11 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
   }
 }
 
-// Warm-up lengths.  The state entering segment j + 1 differs from the chain run from zero over the
-// last w chunks of segment j by the map of those w chunks applied to the state before them; with
-// unit keys and beta in [0, 1] that map's norm is at most exp(sum of g over the w chunks).  For each
-// transition slot (the state after segment j) warm[] holds the least w whose bound is below 2^-64
-// (0: none within the segment, or keys not normalised in the kernel, or a beta outside [0, 1] on the
-// way), and seq_ok[] flags the (sequence, value head) pairs whose every slot has one: those run no
-// summaries and no combination, and each later segment starts with its warm-up.  One workgroup per
-// (sequence, value head); the windows are scanned back from the segment's end 4 chunks at a time.
-template <typename BetaT>
-__global__ __launch_bounds__(256) void seg_warm_kernel(SegTable tab, const float* __restrict__ g,
-                                                      const BetaT* __restrict__ beta, int Hv, int use_l2,
-                                                      int* __restrict__ warm, int* __restrict__ seq_ok) {
-  using namespace pf;
-  __shared__ float part[4];
-  const int s = blockIdx.x / Hv, h = blockIdx.x % Hv;
-  const int t = threadIdx.x, wv = t >> 6, lane = t & 63;
-  const int nseg = tab.nseg_of(tab.nch(s)), slot0 = tab.first_slot(s), L = tab.L;
-  int all_ok = use_l2 ? 1 : 0;
-  for (int j = 0; j + 1 < nseg; ++j) {
-    int wsel = 0;
-    if (use_l2) {
-      const int64_t seg_t0 = tab.start(s) + (int64_t)j * L * CH;  // segment j: L full chunks
-      float acc = 0.f;
-      bool done = false;
-      for (int base = 0; base < L && !done; base += 4) {
-        const int ci = base + wv;  // chunk counted back from the segment's end
-        float sum = 0.f;
-        int ok = 1;
-        if (ci < L) {
-          const int64_t tok = seg_t0 + (int64_t)(L - 1 - ci) * CH + lane;
-          sum = g[tok * Hv + h];
-          const float b = Elem<BetaT>::load(beta + tok * Hv + h);
-          ok = (b >= 0.f && b <= 1.f) ? 1 : 0;
-        }
-        sum = wave_sum_fast(sum);
-        ok = __builtin_amdgcn_ballot_w64(ok == 0) == 0 ? 1 : 0;
-        if (lane == 0) part[wv] = ok ? sum : __builtin_nanf("");
-        __syncthreads();
-        for (int i = 0; i < 4 && !done; ++i) {
-          if (base + i >= L) break;
-          acc += part[i];
-          if (acc < sg::kNegligibleLog) {
-            wsel = base + i + 1;
-            done = true;
-          } else if (!(acc == acc)) {
-            done = true;  // NaN, or a beta outside [0, 1]: no warm-up reaches past it
-          }
-        }
-        __syncthreads();
-      }
-    }
-    if (t == 0) warm[(int64_t)(slot0 + j) * Hv + h] = wsel;
-    all_ok &= wsel > 0 ? 1 : 0;
-  }
-  if (t == 0) seq_ok[(int64_t)s * Hv + h] = all_ok;
-}
-
 // S_{j+1} = A_j S_j + B_j along each sequence's segments, in fp32 (v_mfma_f32_16x16x4_f32); the result
 // overwrites B_j, which the output pass reads as segment j+1's initial state.  One workgroup per
-// (sequence with transition slots, value head, 16-column slice), started at the sequence's first
-// slot; the 8 slices of a (slot, head) share blockIdx % 8, hence an XCD and its L2.  A_j flagged
-// negligible is skipped: S_{j+1} = B_j as written.
+// (sequence, value head, 16-column slice); the 8 slices of a (sequence, head) share blockIdx % 8,
+// hence an XCD and its L2.  Pairs without transition slots, or whose later segments warm up, exit
+// at once.  A_j flagged negligible is skipped: S_{j+1} = B_j as written.
 struct CombineSmem {
   float A[pf::D * (pf::D + 4)];
   float S[pf::D * 16];
@@ -1285,16 +1289,15 @@ struct CombineSmem {
 __global__ __launch_bounds__(256) void seg_combine_kernel(SegTable tab, int Hv, const float* __restrict__ init,
                                                          const int32_t* __restrict__ rows, int n_rows,
                                                          float* __restrict__ trans, const int* __restrict__ tflags,
-                                                         const int* __restrict__ seq_ok) {
+                                                         const int* __restrict__ warm) {
   using namespace pf;
   __shared__ CombineSmem sm;
   const int b = blockIdx.x;
-  const int item = (b >> 6) * 8 + (b & 7), n = (b >> 3) & 7;
-  const int ts = item / Hv, h = item % Hv;
-  if (ts >= tab.first_slot(tab.nseq)) return;
-  const int s = tab.seq_of_slot(ts);
-  if (ts != tab.first_slot(s) || seq_ok[(int64_t)s * Hv + h]) return;
-  const int nsl = tab.first_slot(s + 1) - ts;
+  const int item = (b >> 6) * 8 + (b & 7), n = (b >> 3) & 7;  // item = (sequence, value head)
+  const int s = item / Hv, h = item % Hv;
+  if (s >= tab.nseq) return;
+  const int ts = tab.first_slot(s), nsl = tab.first_slot(s + 1) - ts;
+  if (nsl == 0 || seq_warm_ok(tab, warm, Hv, h, s)) return;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const int LDA = D + 4;
   const float* s0 = nullptr;
@@ -1541,13 +1544,13 @@ int64_t seg_len(int64_t total_chunks, int Hv) {
   const int64_t L = (work + sg::kTargetItems - 1) / sg::kTargetItems;
   return L < sg::kMinSeg ? sg::kMinSeg : L;
 }
-// Workspace layout: the segment table (nseq + 1 int32), the transition flags and warm-up lengths
-// (int32 per (slot, value head)), the warm-up flags (int32 per (sequence, value head)), the
+// Workspace layout: the segment table (nseq + 1 int32), the transition flags (int32 per (slot,
+// value head)), the warm-up lengths (int32 per (slot, value head)), the
 // transition slots (A, B fp32 per (slot, value head)), the inverse kernel's fragments (12 KiB per
 // (chunk, value head)) and its normalised K rows (16 KiB per (chunk, key head)), each part 256-byte
 // aligned.
 struct SegLayout {
-  int64_t L, nslots, off_flags, off_warm, off_seqok, off_trans, off_tfrag, off_qkn, bytes;
+  int64_t L, nslots, off_flags, off_warm, off_trans, off_tfrag, off_qkn, bytes;
 };
 SegLayout seg_layout(int64_t total_chunks, int nseq, int Hqk, int Hv) {
   auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
@@ -1556,8 +1559,7 @@ SegLayout seg_layout(int64_t total_chunks, int nseq, int Hqk, int Hv) {
   l.nslots = total_chunks / l.L;
   l.off_flags = up(((int64_t)nseq + 1) * 4);
   l.off_warm = l.off_flags + up(l.nslots * Hv * 4);
-  l.off_seqok = l.off_warm + up(l.nslots * Hv * 4);
-  l.off_trans = l.off_seqok + up((int64_t)nseq * Hv * 4);
+  l.off_trans = l.off_warm + up(l.nslots * Hv * 4);
   l.off_tfrag = l.off_trans + l.nslots * Hv * (int64_t)sg::kTrans * 4;
   l.off_qkn = l.off_tfrag + total_chunks * Hv * (int64_t)tf::BYTES;
   l.bytes = l.off_qkn + total_chunks * Hqk * (int64_t)(pf::CH * pf::D * 2);
@@ -1610,58 +1612,49 @@ extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const voi
   int32_t* seg0 = (int32_t*)work;
   int* tflags = (int*)(work + lay.off_flags);
   int* warm = (int*)(work + lay.off_warm);
-  int* seq_ok = (int*)(work + lay.off_seqok);
   float* trans = (float*)(work + lay.off_trans);
   uint8_t* tfrag = work + lay.off_tfrag;
   uint16_t* kn = (uint16_t*)(work + lay.off_qkn);
   const int64_t nseg_max = (int64_t)nseq + total_chunks / lay.L;  // each sequence: <= nch / L + 1 segments
-  GDN_REQUIRE(nseg_max * Hv < (1ll << 31) && lay.nslots * Hv * 64 < (1ll << 31) && (int64_t)nseq * Hv < (1ll << 31),
+  GDN_REQUIRE(nseg_max * Hv < (1ll << 31) && lay.nslots * Hv * 2 < (1ll << 31) && (int64_t)nseq * Hv * 64 < (1ll << 31),
               "gdn_chunk_prefill: grid too large");
   if (cu_seqlens) {
     seg_table_kernel<<<1, 256, 0, st>>>(seq_chunk0, nseq, (int)lay.L, seg0);
     int rc = check_launch("gdn_chunk_prefill(table)");
     if (rc) return rc;
   }
+  const SegTable tab{cu_seqlens, seq_chunk0, cu_seqlens ? seg0 : nullptr, nseq, seq_len, (int)lay.L};
   if (total_chunks > 0) {  // the intra-chunk inverses, all chunks in parallel
     const int64_t items = total_chunks * Hqk;
     const unsigned gi = (unsigned)(items < 3ll * device_cus() ? items : 3ll * device_cus());
     if (beta_dtype == GDN_BF16)
       inv_kernel<uint16_t><<<gi, pf::NT, 0, st>>>((const uint16_t*)k, k_stride, g,
                                                   (const uint16_t*)beta, cu_seqlens, seq_chunk0, nseq, seq_len, items,
-                                                  Hqk, Hv, use_qk_l2norm, tfrag, kn);
+                                                  Hqk, Hv, use_qk_l2norm, tfrag, kn, tab, warm);
     else
       inv_kernel<float><<<gi, pf::NT, 0, st>>>((const uint16_t*)k, k_stride, g,
                                                (const float*)beta, cu_seqlens, seq_chunk0, nseq, seq_len, items, Hqk,
-                                               Hv, use_qk_l2norm, tfrag, kn);
+                                               Hv, use_qk_l2norm, tfrag, kn, tab, warm);
     int rc = check_launch("gdn_chunk_prefill(inverse)");
     if (rc) return rc;
   }
-  const SegTable tab{cu_seqlens, seq_chunk0, cu_seqlens ? seg0 : nullptr, nseq, seq_len, (int)lay.L};
   auto launch = [&](int pass, int64_t blocks) {
 #define GDN_SEG_LAUNCH(BT)                                                                                     \
   (pass == 0 ? seg_kernel<BT, uint16_t, 0> : seg_kernel<BT, uint16_t, 1>)<<<(unsigned)blocks, sg::NT, 0, st>>>( \
       (const uint16_t*)q, q_stride, kn, (const uint16_t*)v, v_stride, g, (const BT*)beta,                                                    \
       (uint16_t*)out, tab, Hqk, Hv, use_qk_l2norm, initial_state, state_rows, n_rows,           \
-      final_state, trans, tflags, tfrag, warm, seq_ok)
+      final_state, trans, tflags, tfrag, warm)
     if (beta_dtype == GDN_BF16) GDN_SEG_LAUNCH(uint16_t);
     else GDN_SEG_LAUNCH(float);
 #undef GDN_SEG_LAUNCH
   };
-  if (lay.nslots > 0) {  // warm-up lengths; segment summaries and their combination where none fits
-    if (beta_dtype == GDN_BF16)
-      seg_warm_kernel<uint16_t><<<(unsigned)(nseq * Hv), 256, 0, st>>>(tab, g, (const uint16_t*)beta, Hv,
-                                                                       use_qk_l2norm, warm, seq_ok);
-    else
-      seg_warm_kernel<float><<<(unsigned)(nseq * Hv), 256, 0, st>>>(tab, g, (const float*)beta, Hv, use_qk_l2norm,
-                                                                    warm, seq_ok);
-    int rc = check_launch("gdn_chunk_prefill(warm-up)");
-    if (rc) return rc;
+  if (lay.nslots > 0) {  // segment summaries and their combination where no warm-up fits
     launch(1, lay.nslots * Hv * 2);
-    rc = check_launch("gdn_chunk_prefill(summary)");
+    int rc = check_launch("gdn_chunk_prefill(summary)");
     if (rc) return rc;
-    const int64_t items = lay.nslots * Hv;
+    const int64_t items = (int64_t)nseq * Hv;
     seg_combine_kernel<<<(unsigned)((items + 7) / 8 * 64), 256, 0, st>>>(tab, Hv, initial_state, state_rows, n_rows,
-                                                                       trans, tflags, seq_ok);
+                                                                       trans, tflags, warm);
     rc = check_launch("gdn_chunk_prefill(combine)");
     if (rc) return rc;
   }
