@@ -345,8 +345,11 @@ __global__ __launch_bounds__(kHeadThreads * R) void decode_fused_kernel(
     const float* __restrict__ dt_bias, const void* norm_w, float eps, float* rec_state,
     uint16_t* __restrict__ out, const uint8_t* __restrict__ active, int Hk, int K) {
   constexpr int kGroups = R + 2;  // conv channel blocks of 128: q, k, v_0..v_{R-1}
+  constexpr int kWaves = 4 * R;                   // waves of the workgroup
+  constexpr int kRG = kHeadThreads * R / 32;      // row groups of 32 threads (a row's 32 float4)
+  constexpr int kRows = (kD + kRG - 1) / kRG;     // rows of each head's state per thread
   __shared__ float s_q[kD], s_k[kD], s_v[R][kD];
-  __shared__ float s_red[R][2][4][kD];
+  __shared__ float s_red[R][2][kWaves][kD];
   __shared__ float s_gamma[R], s_beta[R];
   const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
   const int j = t / kHeadThreads, tl = t % kHeadThreads, wl = tl >> 6;  // head in group, local ids
@@ -358,7 +361,6 @@ __global__ __launch_bounds__(kHeadThreads * R) void decode_fused_kernel(
   }
   const int h = hk * R + j;
   const int C = (2 * Hk + Hv) * kD;
-  const int64_t sidx = ((int64_t)n * Hv + h) * kD * kD;
   const uint16_t* xr = mixed + n * mixed_stride;
   const bool k4 = K == 4;
   const bool bias_on = conv_b != nullptr;
@@ -410,8 +412,19 @@ __global__ __launch_bounds__(kHeadThreads * R) void decode_fused_kernel(
       nwr[0] = ww.x; nwr[1] = ww.y; nwr[2] = ww.z; nwr[3] = ww.w;
     }
   }
-  StateRegs S;
-  state_load(S, rec_state + sidx, tl);
+  // every thread holds columns 4 cg..+3 of rows rg + kRG m of each of the R heads' states; head 0's
+  // loads go out first, so its column sums and stores proceed while later heads are still arriving
+  const int cg = t & 31, rg = t >> 5;
+  f32x4 S[R][kRows];
+#pragma unroll
+  for (int jj = 0; jj < R; ++jj) {
+    const f32x4* p = reinterpret_cast<const f32x4*>(rec_state + ((int64_t)n * Hv + hk * R + jj) * kD * kD);
+#pragma unroll
+    for (int m = 0; m < kRows; ++m) {
+      if (kRG * kRows == kD || rg + kRG * m < kD) S[jj][m] = __builtin_nontemporal_load(p + (rg + kRG * m) * 32 + cg);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
   // nothing derived from the small loads may be computed before this point
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
@@ -451,61 +464,85 @@ __global__ __launch_bounds__(kHeadThreads * R) void decode_fused_kernel(
     s_beta[lane] = rbf(sigmoid_f(bf2f((uint16_t)g_b)));
     s_gamma[lane] = expf(-expf(g_al) * softplus_f(bf2f((uint16_t)g_a) + g_dt));
   }
-  __syncthreads();
+  lds_barrier();  // q, k, v, gamma, beta in LDS; the state loads stay in flight
 
-  // ---- phase B: column sums S^T k and S^T q (two row groups per wave by register swap, four
-  //      waves through LDS); k.q on the readout waves ----------------------------------------------
+  // ---- per head, in load order: column sums S^T k and S^T q (two row groups per wave by register
+  //      swap, the waves through LDS), delta for this thread's 4 columns, the rows streamed back, and
+  //      the head's readout o = gamma S^T q + (k.q) delta with its gated RMSNorm -----------------------
   float kq = 0.f;
   if (read_wave) kq = wave_sum_fast(s_k[lane] * s_q[lane] + s_k[lane + 64] * s_q[lane + 64]);
-  float kr[kRowsPerThread], qr[kRowsPerThread];
-  row_values(s_k, tl, kr);
-  row_values(s_q, tl, qr);
-  state_partial(S, kr, tl, s_red[j][0]);
-  state_partial(S, qr, tl, s_red[j][1]);
-  __syncthreads();
-
-  // ---- phase C: every thread derives delta for its own 4 columns and streams its rows back; then
-  //      the conv windows go back and the readout waves form o (bf16, as the reference's recurrent
-  //      output) and the gated RMSNorm of the head's 128 outputs --------------------------------
-  const float gamma = s_gamma[j], bt = s_beta[j];
-  // (measured: 16-byte reads of the partials and k kept in registers for the stores are both slower)
-  f32x4 d;
-  const int cg = tl & 31;
+  float kr[kRows], qr[kRows];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) d[e] = (s_v[j][4 * cg + e] - gamma * red_sum(s_red[j], 0, 4 * cg + e)) * bt;
-  {
-    f32x4* p = reinterpret_cast<f32x4*>(rec_state + sidx) + state_f4(tl);
+  for (int m = 0; m < kRows; ++m) {
+    const int row = rg + kRG * m < kD ? rg + kRG * m : 0;
+    kr[m] = s_k[row];
+    qr[m] = s_q[row];
+  }
 #pragma unroll
-    for (int m = 0; m < kRowsPerThread; ++m)
-      __builtin_nontemporal_store(S.s[m] * gamma + d * s_k[(tl >> 5) + 8 * m], p + m * 8 * 32);
+  for (int jj = 0; jj < R; ++jj) {
+    {
+      f32x4 pk = f32x4{0.f, 0.f, 0.f, 0.f}, pq = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int m = 0; m < kRows; ++m)
+        if (kRG * kRows == kD || rg + kRG * m < kD) {
+          pk += S[jj][m] * kr[m];
+          pq += S[jj][m] * qr[m];
+        }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        pk[e] = xor32_sum(pk[e]);
+        pq[e] = xor32_sum(pq[e]);
+      }
+      if (lane < 32) {
+        *reinterpret_cast<f32x4*>(&s_red[jj][0][wv][4 * lane]) = pk;
+        *reinterpret_cast<f32x4*>(&s_red[jj][1][wv][4 * lane]) = pq;
+      }
+    }
+    lds_barrier();
+    const float gamma = s_gamma[jj], bt = s_beta[jj];
+    f32x4 ck = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w2 = 0; w2 < kWaves; ++w2) ck += *reinterpret_cast<const f32x4*>(&s_red[jj][0][w2][4 * cg]);
+    const f32x4 vv = *reinterpret_cast<const f32x4*>(&s_v[jj][4 * cg]);
+    const f32x4 d = (vv - gamma * ck) * bt;
+    {
+      f32x4* p = reinterpret_cast<f32x4*>(rec_state + ((int64_t)n * Hv + hk * R + jj) * kD * kD);
+#pragma unroll
+      for (int m = 0; m < kRows; ++m)
+        if (kRG * kRows == kD || rg + kRG * m < kD)
+          __builtin_nontemporal_store(S[jj][m] * gamma + d * kr[m], p + (rg + kRG * m) * 32 + cg);
+    }
+    if (read_wave && j == jj) {  // lanes l and l + 32 hold the same columns (t & 31 == l & 31)
+      f32x4 cq = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int w2 = 0; w2 < kWaves; ++w2) cq += *reinterpret_cast<const f32x4*>(&s_red[jj][1][w2][oc]);
+      float o[4], ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        o[e] = rbf(gamma * cq[e] + kq * d[e]);
+        ss += o[e] * o[e];
+      }
+      ss = half_sum(ss);
+      const float inv = rsqrt_f(ss / (float)kD + eps);
+      uint16_t ov[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float xn = rbf(o[e] * inv);
+        const float wt = kWBf16 ? bf2f((uint16_t)(nwr[e >> 1] >> (16 * (e & 1)))) : __uint_as_float(nwr[e]);
+        const float y = kWBf16 ? rbf(wt * xn) : wt * xn;
+        ov[e] = f2bf(y * silu_f(bf2f((uint16_t)(zr[e >> 1] >> (16 * (e & 1))))));
+      }
+      if (lane < 32) {
+        const uint64_t pk = (uint64_t)ov[0] | ((uint64_t)ov[1] << 16) | ((uint64_t)ov[2] << 32) | ((uint64_t)ov[3] << 48);
+        __builtin_nontemporal_store(pk, reinterpret_cast<uint64_t*>(out + ((int64_t)n * Hv + h) * kD + oc));
+      }
+    }
   }
   if (conv_wave && k4) {
 #pragma unroll
     for (int u = 0; u < 2; ++u)
       __builtin_nontemporal_store(((uint64_t)cnew[u].y << 32) | cnew[u].x,
                                   reinterpret_cast<uint64_t*>(conv_state + ((int64_t)n * C + ch0 + lane + 64 * u) * 4));
-  }
-  if (read_wave) {  // lanes l and l + 32 hold the same columns (tl & 31 == l & 31)
-    float o[4], ss = 0.f;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      o[e] = rbf(gamma * red_sum(s_red[j], 1, oc + e) + kq * d[e]);
-      ss += o[e] * o[e];
-    }
-    ss = half_sum(ss);
-    const float inv = rsqrt_f(ss / (float)kD + eps);
-    uint16_t ov[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float xn = rbf(o[e] * inv);
-      const float wt = kWBf16 ? bf2f((uint16_t)(nwr[e >> 1] >> (16 * (e & 1)))) : __uint_as_float(nwr[e]);
-      const float y = kWBf16 ? rbf(wt * xn) : wt * xn;
-      ov[e] = f2bf(y * silu_f(bf2f((uint16_t)(zr[e >> 1] >> (16 * (e & 1))))));
-    }
-    if (lane < 32) {
-      const uint64_t pk = (uint64_t)ov[0] | ((uint64_t)ov[1] << 16) | ((uint64_t)ov[2] << 32) | ((uint64_t)ov[3] << 48);
-      __builtin_nontemporal_store(pk, reinterpret_cast<uint64_t*>(out + ((int64_t)n * Hv + h) * kD + oc));
-    }
   }
 }
 

@@ -104,6 +104,16 @@ __device__ __forceinline__ float xor32_sum(float v) {
 // Sum over the whole wave.
 __device__ __forceinline__ float wave_sum_fast(float v) { return xor32_sum(half_sum(v)); }
 
+// Workgroup barrier over LDS only: it waits for this wave's LDS accesses (lgkmcnt 0), which is all
+// the other waves depend on, and leaves global loads and stores in flight (__syncthreads would
+// drain them: its release fence waits for every outstanding memory access, the next chunk's
+// prefetched inputs included).
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // Treat v as produced at this point: no use of a loaded value can be hoisted above it, so a load
 // issued earlier is not waited for before the loads issued between the two.
 __device__ __forceinline__ void pin(uint32_t& v) { asm volatile("" : "+v"(v)); }

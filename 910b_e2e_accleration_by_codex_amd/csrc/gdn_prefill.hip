@@ -389,15 +389,6 @@ __device__ __forceinline__ bf16x8 lds_frag(const uint8_t* base, int f, int lane)
 __device__ __forceinline__ f16x8 lds_frag_h(const uint8_t* base, int f, int lane) {
   return *reinterpret_cast<const f16x8*>(base + f * ws::FRAG + lane * 16);
 }
-// Workgroup barrier over LDS only: it waits for this wave's LDS accesses (lgkmcnt 0), which is all
-// the other waves depend on, and leaves global loads and stores in flight (__syncthreads would
-// drain them: its release fence waits for every outstanding memory access, the next chunk's
-// prefetched inputs included).
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
 
 // Inclusive prefix sum over the 64 lanes (DPP: shifts within rows of 16, then the row totals
 // broadcast into the later rows).
