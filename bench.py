@@ -213,22 +213,48 @@ def bench_prefill_long(gdn, dev, T=32768, seed=3, check=True):
     return res
 
 
-def cpu_baseline_prefill(T=8192, seed=0):
-    """The oracle's chunked rule (torch CPU restatement of src/gdn_chunk_fast2.py) at T=8192."""
+def cpu_model():
+    """The host CPU's model name (first /proc/cpuinfo entry), for the baseline record."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median_time(fn, reps):
+    """One untimed warm-up pass, then the median wall time of `reps` passes."""
+    fn()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2]
+
+
+def cpu_baseline_prefill(T=8192, seed=0, reps=5):
+    """The oracle's chunked rule (torch CPU restatement of src/gdn_chunk_fast2.py) at T=8192: one
+    warm-up pass, then the median of `reps` passes."""
     oracle = importlib.import_module("oracle.gdn_oracle")
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
     q, k, v, g, beta, s0 = _gdn_inputs(T, seed, "cpu")
     r = HV // HK
     q, k = q.repeat_interleave(r, 2), k.repeat_interleave(r, 2)
-    t0 = time.perf_counter()
-    oracle.chunk_gated_delta_rule_v2(q, k, v, g, beta, 64, s0, True, True)
-    dt = time.perf_counter() - t0
+    dt = _median_time(lambda: oracle.chunk_gated_delta_rule_v2(q, k, v, g, beta, 64, s0, True, True), reps)
+    model = cpu_model()
     return dict(value=round(T / dt), unit="tokens/s/layer", us_per_layer=round(dt * 1e6), cores=threads,
-                kind="port", sample=f"oracle chunk_gated_delta_rule_v2, B=1 T={T} H_v={HV} d={D}, one timed pass")
+                kind="port", cpu_model=model,
+                sample=f"oracle chunk_gated_delta_rule_v2, B=1 T={T} H_v={HV} d={D}, warm-up then median of "
+                       f"{reps} passes, torch {torch.__version__} CPU, {threads} threads on {model}")
 
 
-def cpu_baseline_decode(layers_cpu=LAYERS, reps=3):
+def cpu_baseline_decode(layers_cpu=LAYERS, reps=5):
     """The oracle (torch CPU restatement of the reference decode path) on this host's cores."""
     oracle = importlib.import_module("oracle.gdn_oracle")
     threads = len(os.sched_getaffinity(0))
@@ -251,18 +277,12 @@ def cpu_baseline_decode(layers_cpu=LAYERS, reps=3):
         for p in ls:
             oracle.gdn_decode_core(p["mixed"], p["z"], p["a"], p["b"], p["conv_state"], p["conv_weight"],
                                    p["A_log"], p["dt_bias"], p["norm_weight"], p["rec_state"], HK, HV, D)
-    one()  # warm-up
-    times = []
-    for _ in range(reps):
-        t0 = time.perf_counter()
-        one()
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    us = times[len(times) // 2] * 1e6 / layers_cpu
-    return dict(value=us, unit="us/layer", cores=threads, kind="port",
-                sample=f"oracle gdn_decode_core, {layers_cpu} distinct layers x {reps} timed passes "
-                       f"(median), same shapes as the GPU workload, torch {torch.__version__} CPU, "
-                       f"{threads} threads")
+    us = _median_time(one, reps) * 1e6 / layers_cpu
+    model = cpu_model()
+    return dict(value=us, unit="us/layer", cores=threads, kind="port", cpu_model=model,
+                sample=f"oracle gdn_decode_core, {layers_cpu} distinct layers per pass, warm-up then median "
+                       f"of {reps} passes, same shapes as the GPU workload, torch {torch.__version__} CPU, "
+                       f"{threads} threads on {model}")
 
 
 def bench_attention(gdn, dev, reps=3, seed=4):
