@@ -411,7 +411,10 @@ namespace sg {
 constexpr int NT = 512;                      // 8 waves
 constexpr int kMinSeg = 4;                   // shortest segment the host cuts (chunks)
 constexpr int kTargetItems = 256;            // segments x value heads the host aims for
-constexpr float kNegligibleLog = -44.3614f;  // ln(2^-64)
+constexpr float kNegligibleLog = -44.3614f;  // ln(2^-64): a segment map A_j this small is not formed
+// A warm-up drops a map bounded by 2^-40 relative to the state before it: 2^16 below fp32's
+// rounding of the state it feeds, unless the state shrank by more than that over the warm-up.
+constexpr float kWarmLog = -27.7259f;        // ln(2^-40)
 constexpr int kTrans = 2 * pf::D * pf::D;    // floats per (slot, head): A, then B
 }  // namespace sg
 
@@ -509,7 +512,7 @@ struct InvSmem {
 };
 // Warm-up length for the transition after the segment ending with the chunk at token t_last (one
 // wave): the least w such that the summed log decay of the segment's last w chunks is below
-// ln 2^-64 -- the norm bound of the dropped map with unit keys and beta in [0, 1] -- or 0 when there
+// ln 2^-40 -- the norm bound of the dropped map with unit keys and beta in [0, 1] -- or 0 when there
 // is none within the segment's L chunks or a beta outside [0, 1] (or a NaN) comes first.  Chunks
 // are taken back from the segment's end, four at a time (lane = token).
 template <typename BetaT>
@@ -534,7 +537,7 @@ __device__ int chunk_warm(const float* __restrict__ g, const BetaT* __restrict__
       if (c0 + u >= L) return 0;
       if (__builtin_amdgcn_ballot_w64(ok[u] == 0) != 0) return 0;
       acc += wave_sum_fast(x[u]);
-      if (acc < sg::kNegligibleLog) return c0 + u + 1;
+      if (acc < sg::kWarmLog) return c0 + u + 1;
     }
   }
   return 0;
@@ -705,7 +708,7 @@ __global__ __launch_bounds__(pf::NT, 3) void inv_kernel(const uint16_t* __restri
 // Warm-up lengths.  The state entering segment j + 1 differs from the chain run from zero over the
 // last w chunks of segment j by the map of those w chunks applied to the state before them; with
 // unit keys and beta in [0, 1] that map's norm is at most exp(sum of g over the w chunks).  The
-// inverse kernel writes each transition slot's least w whose bound is below 2^-64 (0: none).  A
+// inverse kernel writes each transition slot's least w whose bound is below 2^-40 (0: none).  A
 // (sequence, value head) pair whose every slot has one runs no summaries and no combination, and
 // its later segments start from their warm-ups.  One wave reads the pair's slots, 64 at a time.
 __device__ bool seq_warm_ok(const SegTable& tab, const int* __restrict__ warm, int Hv, int h, int s) {
