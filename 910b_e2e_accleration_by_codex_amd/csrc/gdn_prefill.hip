@@ -160,18 +160,19 @@ __device__ __forceinline__ void inv64_merge2b(float* sX, float* sT, int w, int l
   if (ib == 3) acc = mm16_f32(sT + 48 * LDF + 48, LDF, Yb, LDF, acc, lane);
   st16_f32(sT + 16 * ib * LDF + 16 * jb, LDF, acc, lane);
 }
-// All 4 waves of a 256-thread workgroup: the phases with a barrier after each.
+// All 4 waves of a 256-thread workgroup: the phases with an LDS barrier after each (global memory
+// requests of the caller stay in flight).
 __device__ void unit_lower_inv64(float* sX, float* sT, int w, int lane) {
   inv64_diag(sX, sT, w, lane);
-  __syncthreads();
+  lds_barrier();
   inv64_merge1a(sX, sT, w, lane);
-  __syncthreads();
+  lds_barrier();
   inv64_merge1b(sX, sT, w, lane);
-  __syncthreads();
+  lds_barrier();
   inv64_merge2a(sX, sT, w, lane);
-  __syncthreads();
+  lds_barrier();
   inv64_merge2b(sX, sT, w, lane);
-  __syncthreads();
+  lds_barrier();
 }
 
 __global__ __launch_bounds__(pf::NT) void unit_lower_inv_kernel(const float* __restrict__ X, float* __restrict__ T) {
@@ -612,7 +613,7 @@ __global__ __launch_bounds__(pf::NT, 3) void inv_kernel(const uint16_t* __restri
     const ChunkPos cpn = chunk_pos((int)(nx / Hqk), cu, seq_chunk0, nseq, seq_len);
     inv_load<BetaT>(in, cpn, (int)(nx % Hqk), (int)(nx % Hqk) * r, k, ks, g, beta, Hv);
   }
-  __syncthreads();
+  lds_barrier();
   // K K^T, row tile w (blocks cb <= w), kept in registers for every value head
   f32x4 acc[4];
 #pragma unroll
@@ -638,7 +639,7 @@ __global__ __launch_bounds__(pf::NT, 3) void inv_kernel(const uint16_t* __restri
         braw = lane < cp.len ? br : 0.f;
       }
     }
-    __syncthreads();
+    lds_barrier();
     {  // X[i][jj] = -beta_i (K K^T)_{i jj} e^{G_i - G_jj}, i = 16 w + 4 g + rr > jj = 16 cb + c
       const f32x4 Gi = *reinterpret_cast<const f32x4*>(&sm.G[16 * w + 4 * g4]);
       const f32x4 Bi = *reinterpret_cast<const f32x4*>(&sm.B[16 * w + 4 * g4]);
@@ -654,7 +655,7 @@ __global__ __launch_bounds__(pf::NT, 3) void inv_kernel(const uint16_t* __restri
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
     unit_lower_inv64(sm.X, sm.T, w, lane);
     // token tile w: fragments (w, s), s <= w / 2: lane (c, g) element e = T[16 w + c][32 s + 8 g + e] x ...
     uint8_t* dst = tfrag + ((int64_t)slot * Hv + h) * tf::BYTES + lane * 16;
@@ -672,7 +673,7 @@ __global__ __launch_bounds__(pf::NT, 3) void inv_kernel(const uint16_t* __restri
       *reinterpret_cast<bf16x8*>(dst + tf::fid(w, s) * ws::FRAG) = pack8(b);
       *reinterpret_cast<bf16x8*>(dst + (tf::FRAGS + tf::fid(w, s)) * ws::FRAG) = pack8(a);
     }
-    __syncthreads();  // the next head (or item) rewrites K, G, X and T
+    lds_barrier();  // the next head (or item) rewrites K, G, X and T
   }
   // the last chunk of a segment with a successor: that transition slot's warm-up length per value
   // head (wave j takes head h0 + j)
