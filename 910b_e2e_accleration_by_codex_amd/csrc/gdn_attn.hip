@@ -14,8 +14,11 @@
 //      lane, row groups of tokens), reduced across the row groups in LDS.
 //   3. attn_combine_kernel: per (slot, query head): the splits merged with their max (flash
 //      decoding), o rounded to bf16 and multiplied by bf16(sigmoid(gate)).
-// Rounding: scores, softmax and P V accumulate in fp32 (the eager path rounds the scores and the
-// probabilities to bf16); the test holds the result to an fp32 reference.
+// Rounding: scores and the softmax's max and exponentials are fp32 (the eager path rounds the scores
+// to bf16 too).  The probabilities are rounded to bf16, as the eager path rounds its normalised
+// ones, and P V multiplies those bf16 values against bf16 V (v_dot2_f32_bf16) with fp32
+// accumulation; the split's exp-sum adds the same rounded values.  The test holds the result to an
+// fp32 reference.
 #include "gdn_device.h"
 #include "gdn_internal.h"
 

@@ -318,15 +318,15 @@ __global__ __launch_bounds__(256) void gated_rmsnorm_kernel(const uint16_t* __re
 // ============================================================================================
 // Fused decode layer core: one workgroup per (slot, key head) owning its R value heads, so every
 // conv channel it reads is also written by it alone (the in-place conv state needs no grid sync).
-// 256 threads stream each value head's state: load, column sums, delta, store.  R + 2 waves (spread
-// over the heads) also convolve the group's q, k and R v channel blocks (conv update + SiLU,
-// l2norm), one more computes the gating, and the last wave of each head forms the readout
+// All R * 256 threads stream every one of the R value heads' states: each thread holds 4 columns of
+// 128 / (8 R) rows of each head, the heads' loads go out in head order, and per head the workgroup
+// forms the column sums, delta and the stores while the later heads are still arriving.  R + 2
+// waves (spread over the workgroup) also convolve the group's q, k and R v channel blocks (conv
+// update + SiLU, l2norm), one more computes the gating, and one wave per head forms the readout
 // o = gamma S^T q + (k.q) delta with its gated RMSNorm.  Their small loads (conv window / weight /
 // input, gating inputs, the readout's gate and norm weight) are issued first and kept as raw bits
-// until the wave's 64 KiB state loads are out, so the prologue runs while the state is in flight;
-// the readout and the K = 4 conv window write-back come after the state stores, so no write sits
-// in the read phase and nothing but delta sits between a wave's last state load and its first
-// store.  Everything read or written once per step (state, conv windows, input, gate, output)
+// until the wave's state loads are out, so the prologue runs while the state is in flight; the
+// K = 4 conv window write-back comes after the state stores, so no write sits in the read phase.  Everything read or written once per step (state, conv windows, input, gate, output)
 // carries the non-temporal hint: measured 0.5 us/layer faster than cached accesses for the small
 // tensors at 16 slots x 32 heads.
 // (A separate control wave doing all of the prologue and readout was measured 18% slower: one

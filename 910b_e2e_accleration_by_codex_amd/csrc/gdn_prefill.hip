@@ -8,13 +8,15 @@
 //   vn  = U - W S,   o = diag(scale e^G) Q S + QK vn,   S' = e^{G_last} S + K^T diag(e^{G_last - G}) vn
 // which is src/gdn_chunk_fast2.py:31-59 (and HF torch_chunk_gated_delta_rule) written per chunk.
 //
-// Two kernels: chunk_local_kernel does every state-independent part of a chunk in parallel over all
-// (chunk, value head) pairs and writes ready-made MFMA operand fragments to a workspace;
-// chunk_scan_kernel walks the chunks of each sequence in order with the fp32 state held in MFMA
-// accumulators (one workgroup per 16-column slice of a head's state).  Products run on
-// v_mfma_f32_16x16x32_bf16 / _f16 with fp32 accumulation; the 64x64 inverse is fp32 throughout
-// (v_mfma_f32_16x16x4_f32).  The state update uses fp16 operands (DEC vn and K^T) with power-of-two
-// range scaling, so the running state never sees a bf16 rounding of its increment.
+// Two kernels: inv_kernel forms every chunk's 64x64 inverse (fp32, v_mfma_f32_16x16x4_f32) in
+// parallel over all (chunk, key head) pairs and writes it as bf16 MFMA fragments, with the
+// normalised K rows; seg_kernel cuts each sequence into segments of consecutive chunks and walks
+// one segment per workgroup with the fp32 state in MFMA accumulators, building every other operand
+// of a chunk in LDS (local waves) while the chain waves run the previous chunk.  A segment's true
+// initial state comes from a warm-up over the end of the segment before it, or from a summary
+// pass plus an fp32 combination.  Products run on v_mfma_f32_16x16x32_bf16 with fp32
+// accumulation; the state update feeds DEC vn as a bf16 hi + lo pair, so the running state never
+// sees a bf16 rounding of its increment.
 #include "gdn_device.h"
 #include "gdn_internal.h"
 
@@ -24,7 +26,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 namespace pf {
 constexpr int D = 128;          // head dim
@@ -42,12 +43,6 @@ constexpr float kScale = 0.08838834764831845f;  // (float)(1 / sqrt(128))
 __device__ __forceinline__ bf16x8 frag(const uint16_t* base, int ld, int row0, int k0, int lane) {
   const uint16_t* p = base + (row0 + (lane & 15)) * ld + k0 + 8 * (lane >> 4);
   return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(p));
-}
-__device__ __forceinline__ bf16x8 frag_neg(const uint16_t* base, int ld, int row0, int k0, int lane) {
-  const uint16_t* p = base + (row0 + (lane & 15)) * ld + k0 + 8 * (lane >> 4);
-  u16x8 v = *reinterpret_cast<const u16x8*>(p);
-  v ^= (uint16_t)0x8000;
-  return __builtin_bit_cast(bf16x8, v);
 }
 __device__ __forceinline__ f32x4 mma(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -201,46 +196,15 @@ __global__ __launch_bounds__(pf::NT) void unit_lower_inv_kernel(const float* __r
 // fragment below is permuted the same way along k:  A-frag element e of lane (c, g) for tile
 // (m, j) = M[16 m + c][32 j + kpos(8 g + e)].
 //
-//   WN  16 frags [tb 4][j 4]  bf16  M = -W,  W = T diag(beta e^G) K     (tokens x features)
-//   KT  16 frags [rb 8][j 2]  fp16  M = kappa K^T                       (features x tokens)
-//   QG  16 frags [tb 4][j 4]  bf16  M = q (l2-normalised)               (tokens x features)
-//   QK   8 frags [tb 4][j 2]  bf16  M = scale q_i.k_j e^{G_i - G_j}, i >= j, else 0 (the two
-//                                   all-zero fragments (tb, j) = (0, 1), (1, 1) are not written)
-//   U   fp16 [slice 8][lane 64][tb 4][r 4] = U[16 tb + 4 g + r][16 slice + c] / USC[tb],
-//       U = T diag(beta) V (accumulator layout of each 16-column slice)
-//   DEC [64] fp32 = e^{G_last - G_t};  USC [4] fp32;  GL = e^{G_last};  KSC = 1 / kappa;  KAP = kappa;
-//   EGS [64] fp32 = scale e^{G_t} (the output rows' factor for q S)
-// kappa (per chunk, for |K|) and 1 / USC (per token tile, for |U|) are powers of two chosen by
-// fp16_fit_exp: 1 when the largest magnitude already sits in [2^-4, 2^14), else the power that
-// moves it into [2^14, 2^15) -- inside fp16's range with full relative precision either way.
+//   wn  16 frags [tb 4][j 4]  bf16  M = -W,  W = T diag(beta e^G) K     (tokens x features)
+//   qg  16 frags [tb 4][j 4]  bf16  M = q (l2-normalised)               (tokens x features)
+//   qk   6 frags tf::fid(tb, j)  bf16  M = scale q_i.k_j e^{G_i - G_j}, i >= j, else 0 (the
+//                                   all-zero upper fragments are not formed)
+//   tb   6 frags tf::fid(tb, k)  bf16  T diag(beta), the inverse kernel's (U = T diag(beta) V)
+// K^T and V enter the products straight from the row-major K and V tiles (ds_read_b64_tr_b16).
 namespace ws {
 constexpr int FRAG = 1024;                       // bytes per fragment
-constexpr int WN = 0;                            // byte offsets inside one record
-constexpr int KT = WN + 16 * FRAG;               // 16384
-constexpr int QG = KT + 16 * FRAG;               // 32768
-constexpr int QK = QG + 16 * FRAG;               // 49152
-constexpr int U = QK + 8 * FRAG;                 // 57344
-constexpr int DEC = U + pf::CH * pf::D * 2;      // 73728
-constexpr int USC = DEC + pf::CH * 4;            // 73984 (16-byte aligned: read as one float4)
-constexpr int GL = USC + 16;                     // 74000
-constexpr int KSC = GL + 4;                      // 74004
-constexpr int KAP = KSC + 4;                     // 74008
-constexpr int HDR = DEC;                         // DEC, USC, GL, KSC, KAP: the 512 bytes the scan stages
-constexpr int EGS = HDR + 512;                   // 74240
-constexpr int BYTES = EGS + pf::CH * 4;          // 74496 (multiple of 256)
 }  // namespace ws
-
-// Exponent se such that 2^se max|x| lies in [2^14, 2^15) (0 for 0 / non-finite; clamped to +-60).
-__device__ __forceinline__ int fp16_scale_exp(float amax) {
-  const int e = (int)((__float_as_uint(amax) >> 23) & 0xff) - 127;
-  if (!(amax > 0.f) || e == 128) return 0;
-  const int se = 14 - e;
-  return se < -60 ? -60 : (se > 60 ? 60 : se);
-}
-// As fp16_scale_exp, but 0 whenever max|x| already lies in [2^-4, 2^14).
-__device__ __forceinline__ int fp16_fit_exp(float amax) {
-  return (amax >= 0.0625f && amax < 16384.0f) ? 0 : fp16_scale_exp(amax);
-}
 
 // Slot row of sequence s for state I/O: rows[s] (or s without rows); -1 if outside [0, n_rows).
 __device__ __forceinline__ int state_row(const int32_t* rows, int n_rows, int s) {
@@ -281,21 +245,6 @@ __device__ __forceinline__ ChunkPos chunk_pos(int slot, const int32_t* cu, const
   return p;
 }
 
-// Load 4 token rows x 8 features (rows 4*tq.., features f0..f0+7) of a [tokens, heads*D] bf16
-// tensor, zero beyond `len`, and l2-normalise each row (a row is spread over 16 consecutive lanes)
-// with the rounding of torch bf16 ops.
-// Rows past the chunk's end (len >= 1) read its last row and are zeroed afterwards: every load is
-// issued unconditionally, so the group goes out back to back with no branch around it.
-__device__ __forceinline__ void load_rows4(u16x8* x, const uint16_t* base, int64_t stride, int64_t t0, int len,
-                                           int tq, int f0) {
-  const u16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = 4 * tq + i;
-    const u16x8 r = *reinterpret_cast<const u16x8*>(base + (t0 + (row < len ? row : len - 1)) * stride + f0);
-    x[i] = row < len ? r : zero;
-  }
-}
 // The pieces of torch's bf16 l2norm x * rsqrt(sum(x^2) + eps) (each op rounded to bf16), two
 // values at a time: the squares are exact in fp32, rounded to bf16 as a pair (v_cvt_pk_bf16_f32)
 // and added with one v_dot2 against (1, 1).
@@ -337,7 +286,7 @@ __device__ __forceinline__ void l2norm_rows4(u16x8* x) {
   for (int i = 0; i < 4; ++i) x[i] = scale_bf16(x[i], l2norm_inv(ss[i]));
 }
 
-// A-fragment of a bf16 [rows, ld] tile in k-slot order (two 8-byte reads; see the workspace notes).
+// A-fragment of a bf16 [rows, ld] tile in k-slot order (two 8-byte reads).
 __device__ __forceinline__ bf16x8 frag_kperm(const uint16_t* base, int ld, int row0, int k0, int lane) {
   const uint16_t* p = base + (row0 + (lane & 15)) * ld + k0 + 4 * (lane >> 4);
   const u16x4 lo = *reinterpret_cast<const u16x4*>(p), hi = *reinterpret_cast<const u16x4*>(p + 16);
@@ -373,22 +322,8 @@ __device__ __forceinline__ bf16x8 pack_acc_bf16(f32x4 a, f32x4 b) {
   const u32x4 u = {w0, w1, w2, w3};
   return __builtin_bit_cast(bf16x8, u);
 }
-__device__ __forceinline__ f16x8 pack_acc_f16(f32x4 a, f32x4 b, float sa) {
-  f16x8 h;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    h[r] = (_Float16)(a[r] * sa);
-    h[4 + r] = (_Float16)(b[r] * sa);
-  }
-  return h;
-}
-__device__ __forceinline__ float wave_max(float v) { return wave_max_fast(v); }
-
 __device__ __forceinline__ bf16x8 lds_frag(const uint8_t* base, int f, int lane) {
   return *reinterpret_cast<const bf16x8*>(base + f * ws::FRAG + lane * 16);
-}
-__device__ __forceinline__ f16x8 lds_frag_h(const uint8_t* base, int f, int lane) {
-  return *reinterpret_cast<const f16x8*>(base + f * ws::FRAG + lane * 16);
 }
 
 // Inclusive prefix sum over the 64 lanes (DPP: shifts within rows of 16, then the row totals
@@ -692,11 +627,12 @@ __global__ __launch_bounds__(pf::NT, 3) void inv_kernel(const uint16_t* __restri
 // Chunked prefill, segment-parallel and fused (the path gdn_chunk_prefill runs).
 // ============================================================================================
 // A sequence's chunks are cut into segments of L consecutive chunks (the host picks L so that
-// about one segment per compute unit and value head exists).  One workgroup per (segment, value
-// head) walks its segment's chunks; per chunk its 8 waves build the operand fragments described
-// above in LDS (l2norm, decay, Q K^T, W and U from the inverse kernel's fragments, kappa K^T), then
-// every wave advances its 16 columns of the fp32 state and writes their outputs.  Only the
-// inverse kernel's 12 KiB per (chunk, value head) passes through memory.
+// about one (segment, value head) pair per compute unit exists).  One workgroup per (segment, value
+// head) walks its segment's chunks.  Per chunk, its 4 local waves build the operand fragments
+// described above in LDS (q masked and l2-normalised, the decay, Q K^T, -W from the K rows and the
+// inverse kernel's T diag(beta e^G)), and its 4 chain waves advance 32 columns of the fp32 state
+// each and write their outputs.  Only the inverse kernel's records (12 KiB of T fragments per
+// (chunk, value head), 16 KiB of K rows per (chunk, key head)) pass through memory.
 // A segment other than the first of its sequence needs its true initial state: the state after
 // segment j is S_{j+1} = A_j S_j + B_j, with A_j the segment's linear map (the chain run from the
 // identity with U = 0) and B_j its affine part (run from zero).  A summary pass computes A_j and

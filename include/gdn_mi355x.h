@@ -315,7 +315,8 @@ int gdn_swiglu_partial(const float* part, int splits, void* out, int M, int64_t 
  *   k_cache_t [N, kv, hd, T] bf16 (K transposed), v_cache [N, kv, T, hd] bf16; T % 4 == 0.
  *   out [N, out_stride] bf16: the gated attention output, nh * hd columns (o_proj's input).
  *   work: gdn_attn_decode_workspace_bytes(N, nh, hd, T) bytes, 256-byte aligned.
- * hd in {64, 128, 256}; nh / kv in {1, 2, 4, 6, 8}.  Scores, softmax and P V run in fp32.
+ * hd in {64, 128, 256}; nh / kv in {1, 2, 4, 6, 8}.  Scores and the softmax run in fp32; P V
+ * multiplies bf16-rounded probabilities with bf16 V and accumulates in fp32.
  */
 int64_t gdn_attn_decode_workspace_bytes(int N, int nh, int hd, int T);
 int gdn_attn_decode(const void* proj, int64_t proj_stride, const int64_t* pos, const void* q_norm_w,
