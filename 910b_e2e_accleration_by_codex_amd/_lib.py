@@ -32,7 +32,7 @@ _SIGNATURES = {
     "gdn_unit_lower_inv": ([_P, _P, _L, _I, _P], _I),
     "gdn_chunk_prefill": ([_P, _L, _P, _L, _P, _L, _P, _P, _I, _P, _P, _P, _L, _P, _P, _L, _I, _I, _I, _I,
                            _I, _I, _I, _P, _L, _P], _I),
-    "gdn_chunk_prefill_workspace_bytes": ([_L, _I, _I, _I], _L),
+    "gdn_chunk_prefill_workspace_bytes": ([_L, _I, _I], _L),
     "gdn_decode_linear_workspace_bytes": ([_I, _L, _L], _L),
     "gdn_decode_linear": ([_P, _L, _P, _L, _P, _L, _I, _L, _L, _P, _L, _P], _I),
     "gdn_decode_linear_packed_elems": ([_L, _L], _L),

@@ -9,8 +9,9 @@
 // which is src/gdn_chunk_fast2.py:31-59 (and HF torch_chunk_gated_delta_rule) written per chunk.
 //
 // Two kernels: inv_kernel forms every chunk's 64x64 inverse (fp32, v_mfma_f32_16x16x4_f32) in
-// parallel over all (chunk, key head) pairs and writes it as bf16 MFMA fragments, with the
-// normalised K rows; seg_kernel cuts each sequence into segments of consecutive chunks and walks
+// parallel over all (chunk, value head) pairs, one wave each with everything in registers, and
+// writes T diag(beta) as bf16 MFMA fragments; seg_kernel cuts each sequence into segments of
+// consecutive chunks and walks
 // one segment per workgroup with the fp32 state in MFMA accumulators, building every other operand
 // of a chunk in LDS (local waves) while the chain waves run the previous chunk.  A segment's true
 // initial state comes from a warm-up over the end of the segment before it, or from a summary
@@ -46,12 +47,6 @@ __device__ __forceinline__ bf16x8 frag(const uint16_t* base, int ld, int row0, i
 }
 __device__ __forceinline__ f32x4 mma(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-__device__ __forceinline__ bf16x8 pack8(const float* v) {
-  u16x8 u;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) u[e] = f2bf(v[e]);
-  return __builtin_bit_cast(bf16x8, u);
 }
 
 // fp32 16x16x16 product on v_mfma_f32_16x16x4_f32 (lane: A[l%16][kk*4 + l/16], B[kk*4 + l/16][l%16]).
@@ -300,15 +295,9 @@ __device__ __forceinline__ u16x4 lds_tr16(const uint16_t* p) {
   const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p);
   return __builtin_bit_cast(u16x4, v);
 }
-// Fragment with k along the rows of a row-major [k][m] bf16 tile: lane (c, g) = (l % 16, l / 16)
-// gets M[k0 + 8g + e][m0 + c], e < 8 -- the A operand of M^T or the B operand of M.
-__device__ __forceinline__ u16x8 frag_tr(const uint16_t* base, int ld, int k0, int m0, int lane) {
-  const int j = lane & 15, g = lane >> 4;
-  const uint16_t* p = base + (k0 + 8 * g + (j >> 2)) * ld + m0 + 4 * (j & 3);
-  const u16x4 lo = lds_tr16(p), hi = lds_tr16(p + 4 * ld);
-  return u16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-}
-// The same in k-slot order: element e of lane (c, g) is M[k0 + kpos(8g + e)][m0 + c].
+// Fragment with k along the rows of a row-major [k][m] bf16 tile, in k-slot order: element e of lane
+// (c, g) = (l % 16, l / 16) is M[k0 + kpos(8g + e)][m0 + c] -- the A operand of M^T or the B operand
+// of M.
 __device__ __forceinline__ u16x8 frag_tr_kperm(const uint16_t* base, int ld, int k0, int m0, int lane) {
   const int j = lane & 15, g = lane >> 4;
   const uint16_t* p = base + (k0 + 4 * g + (j >> 2)) * ld + m0 + 4 * (j & 3);
@@ -427,25 +416,96 @@ __global__ __launch_bounds__(256) void seg_table_kernel(const int32_t* __restric
 }
 
 // ============================================================================================
-// Chunked prefill, part 1: the intra-chunk inverse, parallel over every (chunk, key head).
+// Chunked prefill, part 1: the intra-chunk inverse, parallel over every (chunk, value head).
 // ============================================================================================
-// For each value head of the key head: X = -(beta_i k_i.k_j e^{G_i - G_j})_{i>j} and
-// T = (I - X)^{-1} (unit_lower_inv64, fp32), written as the bf16 MFMA fragments the segment kernel
-// multiplies K and V with: T diag(beta e^G) (W = T diag(beta e^G) K) and T diag(beta)
-// (U = T diag(beta) V), lower-triangular fragments only (token tile w, k-block s <= w / 2).  It is
-// latency-bound work (dependent fp32 products, barriers), so it runs in its own kernel at 3
-// workgroups per compute unit.  K K^T is formed once per key head.
+// X = -(beta_i k_i.k_j e^{G_i - G_j})_{i>j} and T = (I - X)^{-1} in fp32, written as the bf16 MFMA
+// fragments of T diag(beta), lower-triangular fragments only (token tile w, k-block s <= w / 2), in
+// k-slot order.  The segment kernel multiplies V with them (U = T diag(beta) V) and, with their
+// columns scaled by e^G, K (W = T diag(beta e^G) K).  One wave owns one (chunk, value head) and
+// keeps everything in registers: no LDS round trips of intermediate products and no barriers.
 namespace tf {
-constexpr int FRAGS = 6;                      // per matrix
-constexpr int BYTES = 2 * FRAGS * ws::FRAG;   // T diag(beta e^G), then T diag(beta): 12 KiB
+constexpr int FRAGS = 6;                      // lower fragments of T diag(beta)
+constexpr int BYTES = FRAGS * ws::FRAG;       // 6 KiB
 __device__ __forceinline__ int fid(int w, int s) { return w < 2 ? w : 2 * w - 2 + s; }
 }  // namespace tf
-struct InvSmem {
-  uint16_t K[pf::CH * pf::LDK];
-  float X[pf::CH * pf::LDF];
-  float T[pf::CH * pf::LDF];
-  float G[pf::CH], EG[pf::CH], B[pf::CH];
-};
+
+// A 16x16 fp32 block in "D layout" is the MFMA accumulator layout: lane (c, g) = (l % 16, l / 16)
+// holds M[4g + r][c], r < 4.  v_mfma_f32_16x16x4_f32 takes, per lane, A[l % 16][slot l / 16] and
+// B[slot l / 16][l % 16]; with slot g of instruction kk standing for k = 4g + kk, the A operand of
+// A B is the D layout of A^T and the B operand the D layout of B.  So
+//   rmm(Dl(A^T), Dl(B), Dl(C)) = Dl(A B + C)   and   Dl((A B)^T) = rmm(Dl(B), Dl(A^T), 0):
+// a product and its transpose come from the same two registers.
+__device__ __forceinline__ f32x4 rmm(f32x4 aT, f32x4 b, f32x4 acc) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(aT[0], b[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(aT[1], b[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(aT[2], b[2], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(aT[3], b[3], acc, 0, 0, 0);
+  return acc;
+}
+__device__ __forceinline__ f32x4 plus_eye(f32x4 m, int lane) {
+  const int c = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    if (4 * g + r == c) m[r] += 1.f;
+  return m;
+}
+// Index of the lower block (a, b), b <= a, of a 4x4 block grid.
+__device__ __forceinline__ constexpr int tri(int a, int b) { return a * (a + 1) / 2 + b; }
+
+// (I - X)^{-1} for a strictly lower 64x64 X, one wave, registers only.  In: XT[tri(a, b)] =
+// Dl(X_ab^T) for every lower block, Xd[a] = Dl(X_aa).  Out: TT[tri(a, b)] = Dl(T_ab^T).
+// Same blocking as src/gdn_chunk_fast.py:33-62: the diagonal blocks first, then the blocks below
+// them, T_ij = T_ii sum_{k=j}^{i-1} X_ik T_kj.  A diagonal block is (I+X)(I+X^2)(I+X^4)(I+X^8)
+// (exact for nilpotent X, X^16 = 0; |X_ij| <= 1 keeps the powers far from overflow), applied from
+// the right for T and, as (I+X^T)(I+X^2T)(I+X^4T)(I+X^8T), for T^T: both chains multiply from the
+// left by powers whose transposes are already at hand.
+__device__ __forceinline__ void reg_inv64(const f32x4 (&XT)[10], const f32x4 (&Xd)[4], f32x4 (&TT)[10], int lane) {
+  const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+  f32x4 TD[6];  // Dl(T_ab) for the blocks of rows 0..2 (tri index < 6)
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const f32x4 X = Xd[a], Xt = XT[tri(a, a)];
+    const f32x4 P2 = rmm(Xt, X, z), P2T = rmm(X, Xt, z);
+    const f32x4 P4 = rmm(P2T, P2, z), P4T = rmm(P2, P2T, z);
+    const f32x4 P8T = rmm(P4, P4T, z);
+    if (a < 3) {  // T_aa, used as a right factor below
+      f32x4 R = plus_eye(X, lane);
+      R = rmm(P2T, R, R);
+      R = rmm(P4T, R, R);
+      R = rmm(P8T, R, R);
+      TD[tri(a, a)] = R;
+    }
+    f32x4 Q = plus_eye(P8T, lane);
+    Q = rmm(P4, Q, Q);
+    Q = rmm(P2, Q, Q);
+    Q = rmm(X, Q, Q);
+    TT[tri(a, a)] = Q;
+  }
+  f32x4 Y;
+  // first subdiagonal
+  Y = rmm(XT[tri(1, 0)], TD[tri(0, 0)], z);
+  TD[tri(1, 0)] = rmm(TT[tri(1, 1)], Y, z);
+  TT[tri(1, 0)] = rmm(Y, TT[tri(1, 1)], z);
+  Y = rmm(XT[tri(2, 1)], TD[tri(1, 1)], z);
+  TD[tri(2, 1)] = rmm(TT[tri(2, 2)], Y, z);
+  TT[tri(2, 1)] = rmm(Y, TT[tri(2, 2)], z);
+  Y = rmm(XT[tri(3, 2)], TD[tri(2, 2)], z);
+  TT[tri(3, 2)] = rmm(Y, TT[tri(3, 3)], z);
+  // second
+  Y = rmm(XT[tri(2, 0)], TD[tri(0, 0)], z);
+  Y = rmm(XT[tri(2, 1)], TD[tri(1, 0)], Y);
+  TD[tri(2, 0)] = rmm(TT[tri(2, 2)], Y, z);
+  TT[tri(2, 0)] = rmm(Y, TT[tri(2, 2)], z);
+  Y = rmm(XT[tri(3, 1)], TD[tri(1, 1)], z);
+  Y = rmm(XT[tri(3, 2)], TD[tri(2, 1)], Y);
+  TT[tri(3, 1)] = rmm(Y, TT[tri(3, 3)], z);
+  // third
+  Y = rmm(XT[tri(3, 0)], TD[tri(0, 0)], z);
+  Y = rmm(XT[tri(3, 1)], TD[tri(1, 0)], Y);
+  Y = rmm(XT[tri(3, 2)], TD[tri(2, 0)], Y);
+  TT[tri(3, 0)] = rmm(Y, TT[tri(3, 3)], z);
+}
+
 // Warm-up length for the transition after the segment ending with the chunk at token t_last (one
 // wave): the least w such that the summed log decay of the segment's last w chunks is below
 // ln 2^-40 -- the norm bound of the dropped map with unit keys and beta in [0, 1] -- or 0 when there
@@ -479,147 +539,124 @@ __device__ int chunk_warm(const float* __restrict__ g, const BetaT* __restrict__
   return 0;
 }
 
-// Raw inputs of one (chunk, key head) item, requested one item ahead: 4 token rows x 8 features of
-// q and k (rows past the chunk's end zero), and wave 0's g and beta of the first value head.
-struct InvIn {
-  u16x8 kx[4];  // rows past the chunk's end repeat its last row until masked at the use
-  float graw, braw;
-};
+// One wave per (chunk, value head) item (item = chunk slot * Hv + value head; a workgroup's 4 waves
+// are independent, so a wave past the end simply exits).  Lane (i, g) holds K[16 t + i][32 s + 8 g
+// .. + 7] for token tiles t and k-blocks s < 4: the A fragment of tile t and, as K^T, the B
+// fragment of tile t, so K K^T needs nothing but these registers.
 template <typename BetaT>
-__device__ __forceinline__ void inv_load(InvIn& in, const ChunkPos& cp, int hk, int h0, const uint16_t* __restrict__ k,
-                                         int64_t ks,
-                                         const float* __restrict__ g, const BetaT* __restrict__ beta, int Hv) {
-  using namespace pf;
-  const int t = threadIdx.x, lane = t & 63, tq = t >> 4, fb = t & 15;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = 4 * tq + i, rc = row < cp.len ? row : cp.len - 1;
-    in.kx[i] = *reinterpret_cast<const u16x8*>(k + (cp.t0 + rc) * ks + (int64_t)hk * D + 8 * fb);
-  }
-  const int tok = lane < cp.len ? lane : cp.len - 1;
-  in.graw = g[(cp.t0 + tok) * Hv + h0];
-  in.braw = Elem<BetaT>::load(beta + (cp.t0 + tok) * Hv + h0);
-}
-// Persistent: workgroup b takes items b, b + gridDim.x, ... (item = chunk slot * Hqk + key head) and
-// requests the next item's inputs as soon as the current ones are in LDS, so their latency hides
-// behind the current item's inverses.
-template <typename BetaT>
-__global__ __launch_bounds__(pf::NT, 3) void inv_kernel(const uint16_t* __restrict__ k, int64_t ks,
+__global__ __launch_bounds__(pf::NT, 2) void inv_kernel(const uint16_t* __restrict__ k, int64_t ks,
                                                        const float* __restrict__ g, const BetaT* __restrict__ beta,
                                                        const int32_t* __restrict__ cu,
                                                        const int32_t* __restrict__ seq_chunk0, int nseq, int seq_len,
                                                        int64_t items, int Hqk, int Hv, int use_l2,
-                                                       uint8_t* __restrict__ tfrag, uint16_t* __restrict__ kn,
+                                                       uint8_t* __restrict__ tfrag, float* __restrict__ knorm,
                                                        SegTable tab, int* __restrict__ warm) {
   using namespace pf;
-  __shared__ InvSmem sm;
+  __shared__ float sdec[4][2][CH];  // per wave: G and beta by token
   const int t = threadIdx.x, w = t >> 6, lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
-  const int r = Hv / Hqk;
-  int64_t item = blockIdx.x;
+  const int64_t item = (int64_t)blockIdx.x * 4 + w;
   if (item >= items) return;
-  InvIn in;
-  {
-    const ChunkPos cp0 = chunk_pos((int)(item / Hqk), cu, seq_chunk0, nseq, seq_len);
-    inv_load<BetaT>(in, cp0, (int)(item % Hqk), (int)(item % Hqk) * r, k, ks, g, beta, Hv);
-  }
-  for (; item < items; item += gridDim.x) {
-  const int hk = (int)(item % Hqk), slot = (int)(item / Hqk);
+  const int slot = (int)(item / Hv), h = (int)(item % Hv);
+  const int r = Hv / Hqk, hk = h / r;
   const ChunkPos cp = chunk_pos(slot, cu, seq_chunk0, nseq, seq_len);
-  const int h0 = hk * r;
-  const int tok = lane < cp.len ? lane : cp.len - 1;
-  float graw = lane < cp.len ? in.graw : 0.f, braw = lane < cp.len ? in.braw : 0.f;
-  // the K rows of the chunk (l2-normalised when asked, zero past the chunk's end) for the segment
-  // kernel, 16 KiB per (chunk, key head)
-  uint16_t* k_out = kn + ((int64_t)slot * Hqk + hk) * (CH * D);
+  u16x8 kf[4][4];
   {
-    const int tq = t >> 4, fb = t & 15;
+    const uint16_t* kb = k + cp.t0 * ks + (int64_t)hk * D + 8 * g4;
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      const int row = 16 * tt + c16, rc = row < cp.len ? row : cp.len - 1;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) kf[tt][s] = *reinterpret_cast<const u16x8*>(kb + rc * ks + 32 * s);
+    }
+  }
+  const int tok = lane < cp.len ? lane : cp.len - 1;
+  const float graw = g[(cp.t0 + tok) * Hv + h];
+  const float braw = Elem<BetaT>::load(beta + (cp.t0 + tok) * Hv + h);
+  {  // rows past the chunk's end are zero; l2norm with torch's bf16 op rounding (a row sits in the
+     // lanes c, c + 16, c + 32, c + 48).  Each row's factor bf16(rsqrt(...)) is also written for the
+     // segment kernel, which scales the same raw rows by it: bit-identical normalised rows.
     const u16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) in.kx[i] = 4 * tq + i < cp.len ? in.kx[i] : zero;
-    if (use_l2) l2norm_rows4(in.kx);
+    for (int tt = 0; tt < 4; ++tt) {
+      const bool live = 16 * tt + c16 < cp.len;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      *reinterpret_cast<u16x8*>(&sm.K[(4 * tq + i) * LDK + 8 * fb]) = in.kx[i];
-      *reinterpret_cast<u16x8*>(k_out + (4 * tq + i) * D + 8 * fb) = in.kx[i];
-    }
-  }
-  if (item + gridDim.x < items) {  // the next item's inputs
-    const int64_t nx = item + gridDim.x;
-    const ChunkPos cpn = chunk_pos((int)(nx / Hqk), cu, seq_chunk0, nseq, seq_len);
-    inv_load<BetaT>(in, cpn, (int)(nx % Hqk), (int)(nx % Hqk) * r, k, ks, g, beta, Hv);
-  }
-  lds_barrier();
-  // K K^T, row tile w (blocks cb <= w), kept in registers for every value head
-  f32x4 acc[4];
+      for (int s = 0; s < 4; ++s) kf[tt][s] = live ? kf[tt][s] : zero;
+      if (use_l2) {
+        float ss = 0.f;
 #pragma unroll
-  for (int cb = 0; cb < 4; ++cb) acc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int s = 0; s < 4; ++s) ss = sumsq_bf16(kf[tt][s], ss);
+        const float inv = l2norm_inv(xor32_sum(xor16_sum(ss)));
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    const bf16x8 ak = frag(sm.K, LDK, 16 * w, 32 * s, lane);
-#pragma unroll
-    for (int cb = 0; cb < 4; ++cb)
-      if (cb <= w) acc[cb] = mma(ak, frag(sm.K, LDK, 16 * cb, 32 * s, lane), acc[cb]);
-  }
-  for (int j = 0; j < r; ++j) {
-    const int h = h0 + j;
-    if (w == 0) {  // cumulative decay within the chunk (DPP scan); the next head's g and beta requested
-      const float G = wave_incl_scan(graw);
-      sm.G[lane] = G;
-      sm.EG[lane] = expf(G);
-      sm.B[lane] = braw;
-      if (j + 1 < r) {
-        const float gr = g[(cp.t0 + tok) * Hv + h + 1];
-        const float br = Elem<BetaT>::load(beta + (cp.t0 + tok) * Hv + h + 1);
-        graw = lane < cp.len ? gr : 0.f;
-        braw = lane < cp.len ? br : 0.f;
+        for (int s = 0; s < 4; ++s) kf[tt][s] = scale_bf16(kf[tt][s], inv);
+        if (g4 == 0) knorm[((int64_t)slot * Hv + h) * CH + 16 * tt + c16] = inv;
       }
     }
-    lds_barrier();
-    {  // X[i][jj] = -beta_i (K K^T)_{i jj} e^{G_i - G_jj}, i = 16 w + 4 g + rr > jj = 16 cb + c
-      const f32x4 Gi = *reinterpret_cast<const f32x4*>(&sm.G[16 * w + 4 * g4]);
-      const f32x4 Bi = *reinterpret_cast<const f32x4*>(&sm.B[16 * w + 4 * g4]);
+  }
+  // K K^T: kk[tri(a, b)] = Dl of block (b, a) -- lane (c, g) r: (K K^T)[16 b + 4 g + r][16 a + c]
+  f32x4 kk[10];
 #pragma unroll
-      for (int cb = 0; cb < 4; ++cb) {
-        const float Gj = sm.G[16 * cb + c16];
+  for (int a = 0; a < 4; ++a)
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int i = 16 * w + 4 * g4 + rr, jj = 16 * cb + c16;
-          float x = 0.f;
-          if (cb <= w && i > jj) x = -Bi[rr] * acc[cb][rr] * __expf(Gi[rr] - Gj);
-          sm.X[i * LDF + jj] = x;
-        }
-      }
+    for (int b = 0; b <= a; ++b) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) acc = mma(__builtin_bit_cast(bf16x8, kf[b][s]), __builtin_bit_cast(bf16x8, kf[a][s]), acc);
+      kk[tri(a, b)] = acc;
     }
-    lds_barrier();
-    unit_lower_inv64(sm.X, sm.T, w, lane);
-    // token tile w: fragments (w, s), s <= w / 2: lane (c, g) element e = T[16 w + c][32 s + 8 g + e] x ...
-    uint8_t* dst = tfrag + ((int64_t)slot * Hv + h) * tf::BYTES + lane * 16;
+  {  // decay within the chunk (g = 0 and beta = 0 past its end)
+    const float G = wave_incl_scan(lane < cp.len ? graw : 0.f);
+    sdec[w][0][lane] = G;
+    sdec[w][1][lane] = lane < cp.len ? braw : 0.f;
+  }
+  __builtin_amdgcn_wave_barrier();  // this wave's own LDS writes, read back in order
+  float Gc[4], Bc[4];   // at token 16 a + c
+  f32x4 Gr[4], Br[4];   // at tokens 16 b + 4 g + r
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    Gc[a] = sdec[w][0][16 * a + c16];
+    Bc[a] = sdec[w][1][16 * a + c16];
+    Gr[a] = *reinterpret_cast<const f32x4*>(&sdec[w][0][16 * a + 4 * g4]);
+    Br[a] = *reinterpret_cast<const f32x4*>(&sdec[w][1][16 * a + 4 * g4]);
+  }
+  // X^T blocks from the symmetric K K^T: Dl(X_ab^T) at lane (c, g) r is X[i = 16a + c][j = 16b + 4g + r]
+  // = -beta_i (K K^T)[j][i] e^{G_i - G_j}; the diagonal blocks also as Dl(X_aa)
+  f32x4 XT[10], Xd[4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b <= a; ++b)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int i = 16 * a + c16, j = 16 * b + 4 * g4 + rr;
+        XT[tri(a, b)][rr] = i > j ? -Bc[a] * kk[tri(a, b)][rr] * __expf(Gc[a] - Gr[b][rr]) : 0.f;
+      }
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int i = 16 * a + 4 * g4 + rr, j = 16 * a + c16;
+      Xd[a][rr] = i > j ? -Br[a][rr] * kk[tri(a, a)][rr] * __expf(Gr[a][rr] - Gc[a]) : 0.f;
+    }
+  f32x4 TT[10];
+  reg_inv64(XT, Xd, TT, lane);
+  // fragments (w', s), s <= w' / 2: element e of lane (i, g) = T[16 w' + i][j] beta_j with
+  // j = 32 s + kpos(8 g + e), kpos(8 g + e) = 16 (e >> 2) + 4 g + (e & 3): blocks 2s (e < 4) and 2s + 1
+  uint8_t* dst = tfrag + ((int64_t)slot * Hv + h) * tf::BYTES + lane * 16;
+  const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int wt = 0; wt < 4; ++wt)
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      if (2 * s > w) continue;
-      const float* trow = &sm.T[(16 * w + c16) * LDF + 32 * s + 8 * g4];
-      float a[8], b[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int col = 32 * s + 8 * g4 + e;
-        a[e] = trow[e] * sm.B[col];
-        b[e] = a[e] * sm.EG[col];
-      }
-      *reinterpret_cast<bf16x8*>(dst + tf::fid(w, s) * ws::FRAG) = pack8(b);
-      *reinterpret_cast<bf16x8*>(dst + (tf::FRAGS + tf::fid(w, s)) * ws::FRAG) = pack8(a);
+      if (2 * s > wt) continue;
+      const f32x4 t0 = TT[tri(wt, 2 * s)], t1 = 2 * s + 1 <= wt ? TT[tri(wt, 2 * s + 1 <= wt ? 2 * s + 1 : 0)] : z;
+      *reinterpret_cast<bf16x8*>(dst + tf::fid(wt, s) * ws::FRAG) = pack_acc_bf16(t0 * Br[2 * s], t1 * Br[2 * s + 1]);
     }
-    lds_barrier();  // the next head (or item) rewrites K, G, X and T
-  }
-  // the last chunk of a segment with a successor: that transition slot's warm-up length per value
-  // head (wave j takes head h0 + j)
+  // the last chunk of a segment with a successor: that transition slot's warm-up length
   const int nch = tab.nch(cp.seq);
   if ((cp.c + 1) % tab.L == 0 && cp.c + 1 < nch) {
     const int ts = tab.first_slot(cp.seq) + (cp.c + 1) / tab.L - 1;
-    for (int j = w; j < r; j += 4) {
-      const int w_ = use_l2 ? chunk_warm(g, beta, Hv, h0 + j, cp.t0, tab.L) : 0;
-      if (lane == 0) warm[(int64_t)ts * Hv + h0 + j] = w_;
-    }
-  }
+    const int wv = use_l2 ? chunk_warm(g, beta, Hv, h, cp.t0, tab.L) : 0;
+    if (lane == 0) warm[(int64_t)ts * Hv + h] = wv;
   }
 }
 
@@ -629,10 +666,10 @@ __global__ __launch_bounds__(pf::NT, 3) void inv_kernel(const uint16_t* __restri
 // A sequence's chunks are cut into segments of L consecutive chunks (the host picks L so that
 // about one (segment, value head) pair per compute unit exists).  One workgroup per (segment, value
 // head) walks its segment's chunks.  Per chunk, its 4 local waves build the operand fragments
-// described above in LDS (q masked and l2-normalised, the decay, Q K^T, -W from the K rows and the
-// inverse kernel's T diag(beta e^G)), and its 4 chain waves advance 32 columns of the fp32 state
-// each and write their outputs.  Only the inverse kernel's records (12 KiB of T fragments per
-// (chunk, value head), 16 KiB of K rows per (chunk, key head)) pass through memory.
+// described above in LDS (K and q masked and l2-normalised, the decay, Q K^T, -W from the K rows and
+// the inverse kernel's T diag(beta) scaled by e^G), and its 4 chain waves advance 32 columns of the
+// fp32 state each and write their outputs.  Only the inverse kernel's records (6 KiB of T
+// fragments per (chunk, value head)) pass through memory besides the inputs and outputs.
 // A segment other than the first of its sequence needs its true initial state: the state after
 // segment j is S_{j+1} = A_j S_j + B_j, with A_j the segment's linear map (the chain run from the
 // identity with U = 0) and B_j its affine part (run from zero).  A summary pass computes A_j and
@@ -678,6 +715,7 @@ struct alignas(16) SegBuf {
   uint8_t tb[tf::FRAGS * ws::FRAG];   // T diag(beta) fragments (the inverse kernel's), index tf::fid(tb, k)
   float gs[pf::CH];               // G_t, the cumulative log decay within the chunk
   float dec[pf::CH];              // e^{G_last - G_t}
+  float eg[pf::CH];               // e^{G_t}
   float egs[pf::CH];              // scale e^{G_t}
   float gl;                       // e^{G_last}
 };
@@ -690,33 +728,35 @@ enum SegMode { kSegOut = 0, kSegB = 1, kSegA = 2 };
 
 // A local wave's inputs for one chunk, loaded a chunk ahead.  Local wave w (threads t < 256) holds K
 // and V rows 4 tq + i x features 8 fb .. (t = 16 tq + fb: rows 16 w .. 16 w + 15), the q fragments of
-// token tile w, the T diag(beta e^G) and T diag(beta) fragments of token tile w and the g of token
-// `lane`.  K comes from the inverse kernel's record (normalised, zero past the chunk's end); q is
-// raw, in k-slot order (lane (c, g) of fragment s: q[16 w + c][32 s + 4 g .. + 3] and [.. + 16 ..]),
-// masked and normalised at its use.  V rows past the chunk's end repeat its last row: T diag(beta)
-// has zero columns there (beta is 0 past the end), so they add nothing to U.  Every address is a
-// wave-uniform base plus a 32-bit lane offset.
+// token tile w, the T diag(beta) fragments of token tile w, its rows' K l2norm factors and the g of
+// token `lane`.  K, q and V are raw; rows past the chunk's end repeat its last row.  K and q are
+// masked and normalised at their use (q in k-slot order: lane (c, g) of fragment s holds
+// q[16 w + c][32 s + 4 g .. + 3] and [.. + 16 ..]); V needs no mask, as T diag(beta) has zero columns
+// past the end (beta is 0 there), so those rows add nothing to U.  Every address is a wave-uniform
+// base plus a 32-bit lane offset.
 struct LocIn {
   u16x8 kr[4], vr[4], qr[4];
-  bf16x8 tbe[2], tbu[2];
+  bf16x8 tb[2];
+  f32x4 kn;  // the inverse kernel's l2norm factors of K rows 4 tq .. 4 tq + 3
   float graw;
 };
 template <bool kNeedQ>
 __device__ __forceinline__ void loc_load(LocIn& L, int64_t t0, int len, int kh, int h,
-                                         const uint16_t* __restrict__ kc, const uint16_t* __restrict__ q,
+                                         const uint16_t* __restrict__ k, uint32_t ks, const uint16_t* __restrict__ q,
                                          uint32_t qs, const uint16_t* __restrict__ v, uint32_t vs,
-                                         const float* __restrict__ g, int Hv, const uint8_t* __restrict__ tfr) {
+                                         const float* __restrict__ g, int Hv, const uint8_t* __restrict__ tfr,
+                                         const float* __restrict__ knc) {
   using namespace pf;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const uint32_t tq = t >> 4, fb = t & 15;
   // byte offsets as 32-bit values: the loads address a uniform base plus a VGPR offset
-  const char* kb = reinterpret_cast<const char*>(kc);
+  const char* kb = reinterpret_cast<const char*>(k + t0 * ks + (int64_t)kh * D);
   const char* vb = reinterpret_cast<const char*>(v + t0 * vs + (int64_t)h * D);
   const float* gb = g + t0 * Hv + h;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t row = 4 * tq + i, rc = row < (uint32_t)len ? row : (uint32_t)len - 1;
-    L.kr[i] = *reinterpret_cast<const u16x8*>(kb + ((row * D + 8 * fb) * 2u));
+    L.kr[i] = *reinterpret_cast<const u16x8*>(kb + ((rc * ks + 8 * fb) * 2u));
     L.vr[i] = *reinterpret_cast<const u16x8*>(vb + ((rc * vs + 8 * fb) * 2u));
   }
   if (kNeedQ) {
@@ -732,17 +772,16 @@ __device__ __forceinline__ void loc_load(LocIn& L, int64_t t0, int len, int kh, 
   // every wave issues the same loads (tiles 0 and 1 read their one fragment twice): the wait
   // counts before the uses then stay exact along every path through the chunk loop
 #pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    L.tbe[s] = *reinterpret_cast<const bf16x8*>(tfr + (uint32_t)(tf::fid(w, s) * ws::FRAG + lane * 16));
-    L.tbu[s] = *reinterpret_cast<const bf16x8*>(tfr + (uint32_t)((tf::FRAGS + tf::fid(w, s)) * ws::FRAG + lane * 16));
-  }
+  for (int s = 0; s < 2; ++s)
+    L.tb[s] = *reinterpret_cast<const bf16x8*>(tfr + (uint32_t)(tf::fid(w, s) * ws::FRAG + lane * 16));
+  L.kn = *reinterpret_cast<const f32x4*>(reinterpret_cast<const char*>(knc) + tq * 16u);
   const uint32_t tok = lane < len ? lane : len - 1;
   L.graw = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(gb) + tok * (uint32_t)Hv * 4u);
 }
 
-// Local phase 1 (wave w < 4): K and V rows into the buffer, the q fragments (masked, l2-normalised
-// when asked; kept in qf for phase 2); wave 0 also forms the decay factors (G, e^{G_last - G},
-// scale e^G, e^{G_last}).
+// Local phase 1 (wave w < 4): K rows (masked, l2-normalised when asked), V rows and the T diag(beta)
+// fragments into the buffer, the q fragments (masked, l2-normalised when asked; kept in qf for
+// phase 2); wave 0 also forms the decay factors (G, e^{G_last - G}, e^G, scale e^G, e^{G_last}).
 template <bool kNeedQ>
 __device__ __forceinline__ void loc_phase1(SegBuf& B, const LocIn& in, int len, int use_l2, bool q_on,
                                            bf16x8 (&qf)[4]) {
@@ -751,13 +790,19 @@ __device__ __forceinline__ void loc_phase1(SegBuf& B, const LocIn& in, int len, 
   asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"((int)threadIdx.x));
   const int w = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
   const int tq = t >> 4, fb = t & 15;
+  {  // K rows: zero past the chunk's end, scaled by the inverse kernel's l2norm factors
+    const u16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-  for (int i = 0; i < 4; ++i) *reinterpret_cast<u16x8*>(&B.K[(4 * tq + i) * LDK + 8 * fb]) = in.kr[i];
+    for (int i = 0; i < 4; ++i) {
+      const u16x8 kr = use_l2 ? scale_bf16(in.kr[i], in.kn[i]) : in.kr[i];
+      *reinterpret_cast<u16x8*>(&B.K[(4 * tq + i) * LDK + 8 * fb]) = 4 * tq + i < len ? kr : zero;
+    }
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) *reinterpret_cast<u16x8*>(&B.V[(4 * tq + i) * LDK + 8 * fb]) = in.vr[i];
 #pragma unroll
   for (int s = 0; s < 2; ++s)
-    if (2 * s <= w) *reinterpret_cast<bf16x8*>(B.tb + tf::fid(w, s) * ws::FRAG + lane * 16) = in.tbu[s];
+    if (2 * s <= w) *reinterpret_cast<bf16x8*>(B.tb + tf::fid(w, s) * ws::FRAG + lane * 16) = in.tb[s];
   if (kNeedQ && q_on) {
     const u16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
     const bool live = 16 * w + (lane & 15) < len;
@@ -782,22 +827,44 @@ __device__ __forceinline__ void loc_phase1(SegBuf& B, const LocIn& in, int len, 
   if (w == 0) {
     const float G = wave_incl_scan(lane < len ? in.graw : 0.f);  // g = 0 past the chunk's end
     const float gl = __shfl(G, 63, kWave);
+    const float eg = expf(G);
     B.gs[lane] = G;
     B.dec[lane] = expf(gl - G);
-    B.egs[lane] = kScale * expf(G);
+    B.eg[lane] = eg;
+    B.egs[lane] = kScale * eg;
     if (lane == 0) B.gl = expf(gl);
   }
 }
 
 // Local phase 2 (wave W < 4, after the K rows and the decay are in): the QK fragments and the -W
 // fragments of token tile W.  (Q K^T)^T = K Q^T and W^T = K^T (T diag(beta e^G))^T: both accumulator
-// layouts are the k-slot ordered fragment layouts.
+// layouts are the k-slot ordered fragment layouts.  T diag(beta e^G) is the inverse kernel's
+// T diag(beta) with column j scaled by e^{G_j} (element e of lane (c, g) in k-block s is column
+// 32 s + 16 (e >> 2) + 4 g + (e & 3)).
 template <int W, bool kNeedQ>
-__device__ __forceinline__ void loc_phase2(SegBuf& B, const bf16x8 (&qf)[4], const bf16x8 (&tbe)[2], bool q_on) {
+__device__ __forceinline__ void loc_phase2(SegBuf& B, const bf16x8 (&qf)[4], const bf16x8 (&tbu)[2], bool q_on) {
   using namespace pf;
   int t;
   asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"((int)threadIdx.x));
   const int lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
+  bf16x8 tbe[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    if (2 * s > W) continue;
+    const f32x4 e0 = *reinterpret_cast<const f32x4*>(&B.eg[32 * s + 4 * g4]);
+    const f32x4 e1 = *reinterpret_cast<const f32x4*>(&B.eg[32 * s + 16 + 4 * g4]);
+    const u32x4v u = __builtin_bit_cast(u32x4v, tbu[s]);
+    f32x4 a, b;
+    a[0] = __uint_as_float(u[0] << 16) * e0[0];
+    a[1] = __uint_as_float(u[0] & 0xffff0000u) * e0[1];
+    a[2] = __uint_as_float(u[1] << 16) * e0[2];
+    a[3] = __uint_as_float(u[1] & 0xffff0000u) * e0[3];
+    b[0] = __uint_as_float(u[2] << 16) * e1[0];
+    b[1] = __uint_as_float(u[2] & 0xffff0000u) * e1[1];
+    b[2] = __uint_as_float(u[3] << 16) * e1[2];
+    b[3] = __uint_as_float(u[3] & 0xffff0000u) * e1[3];
+    tbe[s] = pack_acc_bf16(a, b);
+  }
   if (kNeedQ && q_on) {
     f32x4 accQ[W + 1];
 #pragma unroll
@@ -825,8 +892,8 @@ __device__ __forceinline__ void loc_phase2(SegBuf& B, const bf16x8 (&qf)[4], con
   f32x4 accW[8];
 #pragma unroll
   for (int cb = 0; cb < 8; ++cb) {
-    accW[cb] = mma(__builtin_bit_cast(bf16x8, frag_tr(B.K, LDK, 0, 16 * cb, lane)), tbe[0], f32x4{0.f, 0.f, 0.f, 0.f});
-    if (W >= 2) accW[cb] = mma(__builtin_bit_cast(bf16x8, frag_tr(B.K, LDK, 32, 16 * cb, lane)), tbe[1], accW[cb]);
+    accW[cb] = mma(__builtin_bit_cast(bf16x8, frag_tr_kperm(B.K, LDK, 0, 16 * cb, lane)), tbe[0], f32x4{0.f, 0.f, 0.f, 0.f});
+    if (W >= 2) accW[cb] = mma(__builtin_bit_cast(bf16x8, frag_tr_kperm(B.K, LDK, 32, 16 * cb, lane)), tbe[1], accW[cb]);
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j)
@@ -884,7 +951,7 @@ __device__ __forceinline__ void chain_part1(const SegBuf& B, ChainRegs& R, uint1
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int sl = 0; sl < 2; ++sl)
-        vf[kb][sl] = __builtin_bit_cast(bf16x8, frag_tr(B.V, LDK, 32 * kb, 16 * (2 * wc + sl), lane));
+        vf[kb][sl] = __builtin_bit_cast(bf16x8, frag_tr_kperm(B.V, LDK, 32 * kb, 16 * (2 * wc + sl), lane));
 #pragma unroll
     for (int f = 0; f < tf::FRAGS; ++f) ft[f] = lds_frag(B.tb, f, lane);
   }
@@ -1029,12 +1096,13 @@ __device__ __forceinline__ void chain_part2(const SegBuf& B, ChainRegs& R, int l
 // from the other: two LDS barriers a chunk, met by both roles.
 template <typename BetaT, typename OutT, int kPass>
 __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
-    const uint16_t* __restrict__ q, int64_t qs, const uint16_t* __restrict__ kn, const uint16_t* __restrict__ v,
+    const uint16_t* __restrict__ q, int64_t qs, const uint16_t* __restrict__ k, int64_t ks, const uint16_t* __restrict__ v,
     int64_t vs, const float* __restrict__ g,
     const BetaT* __restrict__ beta, OutT* __restrict__ out, SegTable tab, int Hqk, int Hv, int use_l2,
     const float* __restrict__ init,
     const int32_t* __restrict__ rows, int n_rows, float* __restrict__ final_state, float* __restrict__ trans,
-    int* __restrict__ tflags, const uint8_t* __restrict__ tfrag, const int* __restrict__ warm) {
+    int* __restrict__ tflags, const uint8_t* __restrict__ tfrag, const float* __restrict__ knorm,
+    const int* __restrict__ warm) {
   using namespace pf;
   __shared__ SegSmem sm;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
@@ -1104,24 +1172,24 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     // unrolled by two so that each set keeps its registers; every load in it is unconditional (past
     // the end the last chunk is requested again, unused), which keeps the wait counts exact.
     LocIn ia, ib;
-    bf16x8 qf[4], tbe[2];
+    bf16x8 qf[4], tbu[2];
     auto load = [&](LocIn& L, int c) __attribute__((always_inline)) {
-      const uint16_t* kc = kn + ((int64_t)(chunk_slot0 + c) * Hqk + kh) * (CH * D);
-      loc_load<need_q>(L, chunk_t0(c), chunk_len(c), kh, h, kc, q, (uint32_t)qs, v, (uint32_t)vs, g, Hv, tfr(c));
+      loc_load<need_q>(L, chunk_t0(c), chunk_len(c), kh, h, k, (uint32_t)ks, q, (uint32_t)qs, v, (uint32_t)vs, g, Hv,
+                       tfr(c), knorm + ((int64_t)(chunk_slot0 + c) * Hv + h) * CH);
     };
     auto phase2 = [&](SegBuf& B, bool q_on) __attribute__((always_inline)) {
       switch (w) {
-        case 0: loc_phase2<0, need_q>(B, qf, tbe, q_on); break;
-        case 1: loc_phase2<1, need_q>(B, qf, tbe, q_on); break;
-        case 2: loc_phase2<2, need_q>(B, qf, tbe, q_on); break;
-        default: loc_phase2<3, need_q>(B, qf, tbe, q_on); break;
+        case 0: loc_phase2<0, need_q>(B, qf, tbu, q_on); break;
+        case 1: loc_phase2<1, need_q>(B, qf, tbu, q_on); break;
+        case 2: loc_phase2<2, need_q>(B, qf, tbu, q_on); break;
+        default: loc_phase2<3, need_q>(B, qf, tbu, q_on); break;
       }
     };
     auto step = [&](int c, LocIn& nxt, const LocIn& cur) __attribute__((always_inline)) {  // prepare chunk c + 1 from cur
       load(nxt, c + 2 < ntot ? c + 2 : ntot - 1);
       loc_phase1<need_q>(sm.buf[(c + 1) & 1], cur, chunk_len(c + 1), use_l2, c + 1 >= w0, qf);
-      tbe[0] = cur.tbe[0];
-      tbe[1] = cur.tbe[1];
+      tbu[0] = cur.tb[0];
+      tbu[1] = cur.tb[1];
       lds_barrier();
       phase2(sm.buf[(c + 1) & 1], c + 1 >= w0);
       lds_barrier();
@@ -1130,8 +1198,8 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
       load(ia, 0);
       load(ib, ntot > 1 ? 1 : 0);
       loc_phase1<need_q>(sm.buf[0], ia, chunk_len(0), use_l2, w0 == 0, qf);
-      tbe[0] = ia.tbe[0];
-      tbe[1] = ia.tbe[1];
+      tbu[0] = ia.tb[0];
+      tbu[1] = ia.tb[1];
     }
     lds_barrier();
     if (ntot > 0) phase2(sm.buf[0], w0 == 0);
@@ -1476,14 +1544,13 @@ int64_t seg_len(int64_t total_chunks, int Hv) {
   return L < sg::kMinSeg ? sg::kMinSeg : L;
 }
 // Workspace layout: the segment table (nseq + 1 int32), the transition flags (int32 per (slot,
-// value head)), the warm-up lengths (int32 per (slot, value head)), the
-// transition slots (A, B fp32 per (slot, value head)), the inverse kernel's fragments (12 KiB per
-// (chunk, value head)) and its normalised K rows (16 KiB per (chunk, key head)), each part 256-byte
-// aligned.
+// value head)), the warm-up lengths (int32 per (slot, value head)), the transition slots (A, B fp32
+// per (slot, value head)), the inverse kernel's fragments (6 KiB per (chunk, value head)) and its K
+// l2norm factors (64 fp32 per (chunk, value head)), each part 256-byte aligned.
 struct SegLayout {
-  int64_t L, nslots, off_flags, off_warm, off_trans, off_tfrag, off_qkn, bytes;
+  int64_t L, nslots, off_flags, off_warm, off_trans, off_tfrag, off_knorm, bytes;
 };
-SegLayout seg_layout(int64_t total_chunks, int nseq, int Hqk, int Hv) {
+SegLayout seg_layout(int64_t total_chunks, int nseq, int Hv) {
   auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
   SegLayout l;
   l.L = seg_len(total_chunks, Hv);
@@ -1492,15 +1559,15 @@ SegLayout seg_layout(int64_t total_chunks, int nseq, int Hqk, int Hv) {
   l.off_warm = l.off_flags + up(l.nslots * Hv * 4);
   l.off_trans = l.off_warm + up(l.nslots * Hv * 4);
   l.off_tfrag = l.off_trans + l.nslots * Hv * (int64_t)sg::kTrans * 4;
-  l.off_qkn = l.off_tfrag + total_chunks * Hv * (int64_t)tf::BYTES;
-  l.bytes = l.off_qkn + total_chunks * Hqk * (int64_t)(pf::CH * pf::D * 2);
+  l.off_knorm = l.off_tfrag + total_chunks * Hv * (int64_t)tf::BYTES;
+  l.bytes = l.off_knorm + total_chunks * Hv * (int64_t)(pf::CH * 4);
   return l;
 }
 }  // namespace
 
-extern "C" int64_t gdn_chunk_prefill_workspace_bytes(int64_t total_chunks, int nseq, int Hqk, int Hv) {
-  if (total_chunks < 0 || nseq < 0 || Hqk <= 0 || Hv <= 0) return -1;
-  return seg_layout(total_chunks, nseq, Hqk, Hv).bytes;
+extern "C" int64_t gdn_chunk_prefill_workspace_bytes(int64_t total_chunks, int nseq, int Hv) {
+  if (total_chunks < 0 || nseq < 0 || Hv <= 0) return -1;
+  return seg_layout(total_chunks, nseq, Hv).bytes;
 }
 
 extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const void* k, int64_t k_stride,
@@ -1529,25 +1596,29 @@ extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const voi
   GDN_REQUIRE(aligned(out, 8), "gdn_chunk_prefill: out must be 8-byte aligned");
   GDN_REQUIRE((!initial_state || aligned(initial_state, 16)) && (!final_state || aligned(final_state, 16)),
               "gdn_chunk_prefill: initial/final state must be 16-byte aligned");
-  GDN_REQUIRE(v_stride > 0 && v_stride < (1ll << 26) && q_stride > 0 && q_stride < (1ll << 26),
-              "gdn_chunk_prefill: q/v token strides out of range");
+  // the segment kernel addresses a chunk's q, k and v rows with 32-bit byte offsets: 63 strides plus a
+  // row must stay below 2^32 bytes
+  GDN_REQUIRE(q_stride > 0 && q_stride < (1ll << 25) && k_stride > 0 && k_stride < (1ll << 25) && v_stride > 0 &&
+                  v_stride < (1ll << 25),
+              "gdn_chunk_prefill: q/k/v token strides out of range");
   GDN_REQUIRE(workspace && aligned(workspace, 256) &&
-                  workspace_bytes >= gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hqk, Hv),
+                  workspace_bytes >= gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hv),
               "gdn_chunk_prefill: workspace missing, misaligned or smaller than %lld bytes",
-              (long long)gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hqk, Hv));
+              (long long)gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hv));
   GDN_REQUIRE(total_chunks < (1ll << 31), "gdn_chunk_prefill: too many chunks");
   if (nseq == 0) return GDN_OK;
   hipStream_t st = (hipStream_t)stream;
-  const SegLayout lay = seg_layout(total_chunks, nseq, Hqk, Hv);
+  const SegLayout lay = seg_layout(total_chunks, nseq, Hv);
   uint8_t* work = (uint8_t*)workspace;
   int32_t* seg0 = (int32_t*)work;
   int* tflags = (int*)(work + lay.off_flags);
   int* warm = (int*)(work + lay.off_warm);
   float* trans = (float*)(work + lay.off_trans);
   uint8_t* tfrag = work + lay.off_tfrag;
-  uint16_t* kn = (uint16_t*)(work + lay.off_qkn);
+  float* knorm = (float*)(work + lay.off_knorm);
   const int64_t nseg_max = (int64_t)nseq + total_chunks / lay.L;  // each sequence: <= nch / L + 1 segments
-  GDN_REQUIRE(nseg_max * Hv < (1ll << 31) && lay.nslots * Hv * 2 < (1ll << 31) && (int64_t)nseq * Hv * 64 < (1ll << 31),
+  GDN_REQUIRE(nseg_max * Hv < (1ll << 31) && lay.nslots * Hv * 2 < (1ll << 31) && (int64_t)nseq * Hv * 64 < (1ll << 31) &&
+                  total_chunks * Hv < (1ll << 33),
               "gdn_chunk_prefill: grid too large");
   if (cu_seqlens) {
     seg_table_kernel<<<1, 256, 0, st>>>(seq_chunk0, nseq, (int)lay.L, seg0);
@@ -1555,26 +1626,26 @@ extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const voi
     if (rc) return rc;
   }
   const SegTable tab{cu_seqlens, seq_chunk0, cu_seqlens ? seg0 : nullptr, nseq, seq_len, (int)lay.L};
-  if (total_chunks > 0) {  // the intra-chunk inverses, all chunks in parallel
-    const int64_t items = total_chunks * Hqk;
-    const unsigned gi = (unsigned)(items < 3ll * device_cus() ? items : 3ll * device_cus());
+  if (total_chunks > 0) {  // the intra-chunk inverses, one wave per (chunk, value head)
+    const int64_t items = total_chunks * Hv;
+    const unsigned gi = (unsigned)((items + 3) / 4);
     if (beta_dtype == GDN_BF16)
       inv_kernel<uint16_t><<<gi, pf::NT, 0, st>>>((const uint16_t*)k, k_stride, g,
                                                   (const uint16_t*)beta, cu_seqlens, seq_chunk0, nseq, seq_len, items,
-                                                  Hqk, Hv, use_qk_l2norm, tfrag, kn, tab, warm);
+                                                  Hqk, Hv, use_qk_l2norm, tfrag, knorm, tab, warm);
     else
       inv_kernel<float><<<gi, pf::NT, 0, st>>>((const uint16_t*)k, k_stride, g,
                                                (const float*)beta, cu_seqlens, seq_chunk0, nseq, seq_len, items, Hqk,
-                                               Hv, use_qk_l2norm, tfrag, kn, tab, warm);
+                                               Hv, use_qk_l2norm, tfrag, knorm, tab, warm);
     int rc = check_launch("gdn_chunk_prefill(inverse)");
     if (rc) return rc;
   }
   auto launch = [&](int pass, int64_t blocks) {
 #define GDN_SEG_LAUNCH(BT)                                                                                     \
   (pass == 0 ? seg_kernel<BT, uint16_t, 0> : seg_kernel<BT, uint16_t, 1>)<<<(unsigned)blocks, sg::NT, 0, st>>>( \
-      (const uint16_t*)q, q_stride, kn, (const uint16_t*)v, v_stride, g, (const BT*)beta,                                                    \
+      (const uint16_t*)q, q_stride, (const uint16_t*)k, k_stride, (const uint16_t*)v, v_stride, g, (const BT*)beta,                                                    \
       (uint16_t*)out, tab, Hqk, Hv, use_qk_l2norm, initial_state, state_rows, n_rows,           \
-      final_state, trans, tflags, tfrag, warm)
+      final_state, trans, tflags, tfrag, knorm, warm)
     if (beta_dtype == GDN_BF16) GDN_SEG_LAUNCH(uint16_t);
     else GDN_SEG_LAUNCH(float);
 #undef GDN_SEG_LAUNCH
@@ -1615,7 +1686,7 @@ extern "C" int gdn_chunk_prefill_noalloc(const void* q, int64_t q_stride, const 
   clear_error();
   GDN_REQUIRE(total_chunks >= 0 && Hqk > 0 && Hv > 0, "gdn_chunk_prefill_noalloc: bad sizes");
   GDN_REQUIRE(nseq >= 0, "gdn_chunk_prefill_noalloc: bad sizes");
-  const int64_t need = gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hqk, Hv);
+  const int64_t need = gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hv);
   GDN_REQUIRE(need <= GDN_NOALLOC_SCRATCH_BYTES,
               "gdn_chunk_prefill_noalloc: the call needs %lld bytes of workspace, the static scratch holds %lld "
               "(%lld chunks, %d sequences, %d value heads; use gdn_chunk_prefill_rows with a workspace)",

@@ -183,7 +183,7 @@ def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size=64, initial_st
             init = initial_state.to(torch.float32).contiguous()
         final = torch.empty(nseq, Hv, D, D, dtype=torch.float32, device=dev) if output_final_state else None
     out = torch.empty(B, T, Hv, D, dtype=query.dtype, device=dev)
-    wbytes = int(_lib.lib().gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hqk, Hv))
+    wbytes = int(_lib.lib().gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hv))
     work = torch.empty(max(wbytes, 1), dtype=torch.uint8, device=dev)
     _lib.call("gdn_chunk_prefill_rows", _lib.ptr(q), qs, _lib.ptr(k), ks, _lib.ptr(v), vs, _lib.ptr(g32),
               _lib.ptr(beta), _lib.dtype_code(beta), _lib.ptr(init), _lib.ptr(final), _lib.ptr(rows), n_rows,

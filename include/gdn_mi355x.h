@@ -113,13 +113,12 @@ int gdn_unit_lower_inv(const float* X, float* T, int64_t batch, int n, void* str
 
 /*
  * Bytes of device workspace gdn_chunk_prefill needs for `total_chunks` 64-token chunks of `nseq`
- * sequences, Hqk key heads and Hv value heads (-1 for bad sizes): the segment table and flags (a few
- * bytes per sequence and per segment), the fp32 transition maps of the segments that have a
- * successor (at most about 32 MiB: sequences are cut into segments so that about 256 (segment,
- * value head) items exist), the intra-chunk inverse fragments (12 KiB per (chunk, value head)) and
- * the normalised K rows (16 KiB per (chunk, key head)).
+ * sequences and Hv value heads (-1 for bad sizes): the segment table and flags (a few bytes per
+ * sequence and per segment), the fp32 transition maps of the segments that have a successor (at
+ * most 32 MiB: sequences are cut into segments so that at most about 256 (segment, value head)
+ * items exist) and the intra-chunk inverse's output (6.25 KiB per (chunk, value head)).
  */
-int64_t gdn_chunk_prefill_workspace_bytes(int64_t total_chunks, int nseq, int Hqk, int Hv);
+int64_t gdn_chunk_prefill_workspace_bytes(int64_t total_chunks, int nseq, int Hv);
 
 /*
  * Chunked gated delta rule prefill (chunk 64, fp32 state), optionally over packed sequences.
@@ -135,7 +134,7 @@ int64_t gdn_chunk_prefill_workspace_bytes(int64_t total_chunks, int nseq, int Hq
  *   cu_seqlens: device int32 [nseq+1] (packed varlen) with seq_chunk0: device int32 [nseq+1],
  *     seq_chunk0[s] = sum over earlier sequences of ceil(len/64); or both NULL for nseq
  *     sequences of seq_len tokens.  total_chunks = sum of ceil(len/64) over sequences.
- *   workspace: device memory of gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hqk, Hv) bytes,
+ *   workspace: device memory of gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hv) bytes,
  *     256-byte aligned (caller-owned; contents are scratch).
  */
 int gdn_chunk_prefill(const void* q, int64_t q_stride, const void* k, int64_t k_stride,
@@ -211,9 +210,9 @@ int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const void* k, int64
  * gdn_chunk_prefill_rows without a workspace argument and without any allocation: the kernels'
  * workspace is a static device array of GDN_NOALLOC_SCRATCH_BYTES (256 MiB) that the library holds on
  * every GPU it runs on until the process ends.  A call whose
- * gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hqk, Hv) exceeds it is rejected with
- * GDN_EINVAL before any launch (the workspace is at most about 32 MiB plus 12 KiB per (chunk, value
- * head) plus 16 KiB per (chunk, key head): 256 MiB holds e.g. 8192 tokens at Hqk = 16, Hv = 32).  Every
+ * gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hv) exceeds it is rejected with GDN_EINVAL
+ * before any launch (the workspace is at most about 32 MiB plus 6.25 KiB per (chunk, value head): 256 MiB
+ * holds e.g. 65,536 tokens at Hv = 32).  Every
  * call on one GPU shares that GPU's array: calls that overlap on one GPU (other streams, other host
  * threads) race and give wrong results -- order them on one stream.  The array needs no clearing
  * (every record a call reads, the same call writes first).

@@ -86,7 +86,7 @@ def test_version_limits_and_error_path(lib):
     assert h.gdn_decode_linear_packed_elems(98, 100) == 0
     rc = h.gdn_add_rmsnorm(p, p, p, None, p, 4, 256, ctypes.c_float(1e-6), None)
     assert rc == 1 and b"null" in h.gdn_last_error()
-    need = h.gdn_chunk_prefill_workspace_bytes(10, 1, 16, 32)
+    need = h.gdn_chunk_prefill_workspace_bytes(10, 1, 32)
     assert need > 0 and need % 256 == 0
     with pytest.raises(lib.GDNError):
         lib.call("gdn_gated_rmsnorm", None, 0, None, 0, None, 1, None, 1, 128, ctypes.c_float(1e-6), None)

@@ -50,14 +50,14 @@ def test_noalloc_prefill_matches_workspace_entry_point(gdn, dev):
         c0_h = torch.tensor([0] + list(torch.cumsum(torch.tensor(nch), 0)), dtype=torch.int32)
         total = int(c0_h[-1])
         cu, c0 = cu_h.to(dev), c0_h.to(dev)
-        wbytes = int(L.lib().gdn_chunk_prefill_workspace_bytes(total, len(lens), Hk, Hv))
+        wbytes = int(L.lib().gdn_chunk_prefill_workspace_bytes(total, len(lens), Hv))
         assert wbytes <= 256 << 20
         work = torch.empty(wbytes, dtype=torch.uint8, device=dev)
         o_ref, f_ref = _call(L, "gdn_chunk_prefill_rows", q, k, v, g, beta, s0, cu, c0, total, Hk, Hv, work=work)
         o, f = _call(L, "gdn_chunk_prefill_noalloc", q, k, v, g, beta, s0, cu, c0, total, Hk, Hv)
         torch.cuda.synchronize()
         assert torch.equal(o, o_ref) and torch.equal(f, f_ref), f"lens {lens}"
-    # beyond the scratch (12 KiB of inverse fragments per (chunk, value head) and 16 KiB of K rows
-    # per (chunk, key head)): refused on the host before any launch
+    # beyond the scratch (6.25 KiB of inverse output per (chunk, value head)): refused on the host
+    # before any launch
     with pytest.raises(L.GDNError, match="static scratch holds"):
         _call(L, "gdn_chunk_prefill_noalloc", q, k, v, g, beta, s0, cu, c0, 20_000, Hk, Hv)
