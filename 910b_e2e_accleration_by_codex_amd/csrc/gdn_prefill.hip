@@ -452,50 +452,59 @@ __device__ __forceinline__ f32x4 plus_eye(f32x4 m, int lane) {
 // Index of the lower block (a, b), b <= a, of a 4x4 block grid.
 __device__ __forceinline__ constexpr int tri(int a, int b) { return a * (a + 1) / 2 + b; }
 
-// (I - X)^{-1} for a strictly lower 64x64 X, one wave, registers only.  In: XT[tri(a, b)] =
-// Dl(X_ab^T) for every lower block, Xd[a] = Dl(X_aa).  Out: TT[tri(a, b)] = Dl(T_ab^T).
-// Same blocking as src/gdn_chunk_fast.py:33-62: the diagonal blocks first, then the blocks below
-// them, T_ij = T_ii sum_{k=j}^{i-1} X_ik T_kj.  A diagonal block is (I+X)(I+X^2)(I+X^4)(I+X^8)
-// (exact for nilpotent X, X^16 = 0; |X_ij| <= 1 keeps the powers far from overflow), applied from
-// the right for T and, as (I+X^T)(I+X^2T)(I+X^4T)(I+X^8T), for T^T: both chains multiply from the
-// left by powers whose transposes are already at hand.
-__device__ __forceinline__ void reg_inv64(const f32x4 (&XT)[10], const f32x4 (&Xd)[4], f32x4 (&TT)[10], int lane) {
+// Dl(M^T) from Dl(M) through a wave-private 16 x 20 fp32 LDS tile: the wave writes M row-major and
+// reads its transpose back 16 bytes per lane.  A wave's LDS accesses complete in issue order, and
+// the compiler keeps a tile's store -> load -> next store order (they may alias), so no barrier is
+// needed.
+constexpr int kTrPitch = 20;
+__device__ __forceinline__ f32x4 ltr(float* tile, f32x4 m, int lane) {
+  const int c = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) tile[(4 * g + r) * kTrPitch + c] = m[r];
+  return *reinterpret_cast<const f32x4*>(&tile[c * kTrPitch + 4 * g]);
+}
+
+// (I - X)^{-1} for a strictly lower 64x64 X, one wave.  In: XT[tri(a, b)] = Dl(X_ab^T) for every
+// lower block, Xd[a] = Dl(X_aa).  Out: TT[tri(a, b)] = Dl(T_ab^T).  tiles: 4 wave-private transpose
+// tiles.  Same blocking as src/gdn_chunk_fast.py:33-62: the diagonal blocks first, then the blocks
+// below them, T_ij = T_ii sum_{k=j}^{i-1} X_ik T_kj.  A diagonal block's T^T is
+// (I+X^8T)(I+X^4T)(I+X^2T)(I+X^T) (exact for nilpotent X, X^16 = 0; |X_ij| <= 1 keeps the powers far
+// from overflow), applied from the right with the powers X^2, X^4 as left factors; the transposes a
+// product needs as an operand are taken through LDS.
+__device__ __forceinline__ void reg_inv64(const f32x4 (&XT)[10], const f32x4 (&Xd)[4], f32x4 (&TT)[10], float* tiles,
+                                          int lane) {
   const f32x4 z = {0.f, 0.f, 0.f, 0.f};
   f32x4 TD[6];  // Dl(T_ab) for the blocks of rows 0..2 (tri index < 6)
 #pragma unroll
   for (int a = 0; a < 4; ++a) {
+    float* tile = tiles + a * 16 * kTrPitch;
     const f32x4 X = Xd[a], Xt = XT[tri(a, a)];
-    const f32x4 P2 = rmm(Xt, X, z), P2T = rmm(X, Xt, z);
-    const f32x4 P4 = rmm(P2T, P2, z), P4T = rmm(P2, P2T, z);
-    const f32x4 P8T = rmm(P4, P4T, z);
-    if (a < 3) {  // T_aa, used as a right factor below
-      f32x4 R = plus_eye(X, lane);
-      R = rmm(P2T, R, R);
-      R = rmm(P4T, R, R);
-      R = rmm(P8T, R, R);
-      TD[tri(a, a)] = R;
-    }
-    f32x4 Q = plus_eye(P8T, lane);
+    const f32x4 P2 = rmm(Xt, X, z);
+    const f32x4 P2T = ltr(tile, P2, lane);
+    const f32x4 P4 = rmm(P2T, P2, z);
+    const f32x4 P4T = ltr(tile, P4, lane);
+    f32x4 Q = plus_eye(rmm(P4, P4T, z), lane);  // I + (X^8)^T
     Q = rmm(P4, Q, Q);
     Q = rmm(P2, Q, Q);
     Q = rmm(X, Q, Q);
     TT[tri(a, a)] = Q;
+    if (a < 3) TD[tri(a, a)] = ltr(tile, Q, lane);
   }
   f32x4 Y;
   // first subdiagonal
   Y = rmm(XT[tri(1, 0)], TD[tri(0, 0)], z);
   TD[tri(1, 0)] = rmm(TT[tri(1, 1)], Y, z);
-  TT[tri(1, 0)] = rmm(Y, TT[tri(1, 1)], z);
+  TT[tri(1, 0)] = ltr(tiles, TD[tri(1, 0)], lane);
   Y = rmm(XT[tri(2, 1)], TD[tri(1, 1)], z);
   TD[tri(2, 1)] = rmm(TT[tri(2, 2)], Y, z);
-  TT[tri(2, 1)] = rmm(Y, TT[tri(2, 2)], z);
+  TT[tri(2, 1)] = ltr(tiles + 16 * kTrPitch, TD[tri(2, 1)], lane);
   Y = rmm(XT[tri(3, 2)], TD[tri(2, 2)], z);
   TT[tri(3, 2)] = rmm(Y, TT[tri(3, 3)], z);
   // second
   Y = rmm(XT[tri(2, 0)], TD[tri(0, 0)], z);
   Y = rmm(XT[tri(2, 1)], TD[tri(1, 0)], Y);
   TD[tri(2, 0)] = rmm(TT[tri(2, 2)], Y, z);
-  TT[tri(2, 0)] = rmm(Y, TT[tri(2, 2)], z);
+  TT[tri(2, 0)] = ltr(tiles + 2 * 16 * kTrPitch, TD[tri(2, 0)], lane);
   Y = rmm(XT[tri(3, 1)], TD[tri(1, 1)], z);
   Y = rmm(XT[tri(3, 2)], TD[tri(2, 1)], Y);
   TT[tri(3, 1)] = rmm(Y, TT[tri(3, 3)], z);
@@ -542,7 +551,9 @@ __device__ int chunk_warm(const float* __restrict__ g, const BetaT* __restrict__
 // One wave per (chunk, value head) item (item = chunk slot * Hv + value head; a workgroup's 4 waves
 // are independent, so a wave past the end simply exits).  Lane (i, g) holds K[16 t + i][32 s + 8 g
 // .. + 7] for token tiles t and k-blocks s < 4: the A fragment of tile t and, as K^T, the B
-// fragment of tile t, so K K^T needs nothing but these registers.
+// fragment of tile t, so K K^T needs nothing but these registers.  (Waves that each take several
+// items and prefetch the next one's inputs need more registers, halve the resident waves and were
+// measured slower.)
 template <typename BetaT>
 __global__ __launch_bounds__(pf::NT, 2) void inv_kernel(const uint16_t* __restrict__ k, int64_t ks,
                                                        const float* __restrict__ g, const BetaT* __restrict__ beta,
@@ -552,7 +563,8 @@ __global__ __launch_bounds__(pf::NT, 2) void inv_kernel(const uint16_t* __restri
                                                        uint8_t* __restrict__ tfrag, float* __restrict__ knorm,
                                                        SegTable tab, int* __restrict__ warm) {
   using namespace pf;
-  __shared__ float sdec[4][2][CH];  // per wave: G and beta by token
+  __shared__ float sdec[4][2][CH];                // per wave: G and beta by token
+  __shared__ float strp[4][4 * 16 * kTrPitch];    // per wave: 4 transpose tiles
   const int t = threadIdx.x, w = t >> 6, lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
   const int64_t item = (int64_t)blockIdx.x * 4 + w;
   if (item >= items) return;
@@ -638,7 +650,7 @@ __global__ __launch_bounds__(pf::NT, 2) void inv_kernel(const uint16_t* __restri
       Xd[a][rr] = i > j ? -Br[a][rr] * kk[tri(a, a)][rr] * __expf(Gr[a][rr] - Gc[a]) : 0.f;
     }
   f32x4 TT[10];
-  reg_inv64(XT, Xd, TT, lane);
+  reg_inv64(XT, Xd, TT, strp[w], lane);
   // fragments (w', s), s <= w' / 2: element e of lane (i, g) = T[16 w' + i][j] beta_j with
   // j = 32 s + kpos(8 g + e), kpos(8 g + e) = 16 (e >> 2) + 4 g + (e & 3): blocks 2s (e < 4) and 2s + 1
   uint8_t* dst = tfrag + ((int64_t)slot * Hv + h) * tf::BYTES + lane * 16;
