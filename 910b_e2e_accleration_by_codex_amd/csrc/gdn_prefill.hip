@@ -445,8 +445,7 @@ __device__ __forceinline__ f32x4 rmm(f32x4 aT, f32x4 b, f32x4 acc) {
 __device__ __forceinline__ f32x4 plus_eye(f32x4 m, int lane) {
   const int c = lane & 15, g = lane >> 4;
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
-    if (4 * g + r == c) m[r] += 1.f;
+  for (int r = 0; r < 4; ++r) m[r] += 4 * g + r == c ? 1.f : 0.f;
   return m;
 }
 // Index of the lower block (a, b), b <= a, of a 4x4 block grid.
@@ -565,7 +564,8 @@ __global__ __launch_bounds__(pf::NT, 2) void inv_kernel(const uint16_t* __restri
   using namespace pf;
   __shared__ float sdec[4][2][CH];                // per wave: G and beta by token
   __shared__ float strp[4][4 * 16 * kTrPitch];    // per wave: 4 transpose tiles
-  const int t = threadIdx.x, w = t >> 6, lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
+  const int t = threadIdx.x, lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);  // the item is wave-uniform: scalar control flow
   const int64_t item = (int64_t)blockIdx.x * 4 + w;
   if (item >= items) return;
   const int slot = (int)(item / Hv), h = (int)(item % Hv);
@@ -588,6 +588,7 @@ __global__ __launch_bounds__(pf::NT, 2) void inv_kernel(const uint16_t* __restri
      // lanes c, c + 16, c + 32, c + 48).  Each row's factor bf16(rsqrt(...)) is also written for the
      // segment kernel, which scales the same raw rows by it: bit-identical normalised rows.
     const u16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+    float mine = 0.f;  // lane (c, g) stores the factor of row 16 g + c
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
       const bool live = 16 * tt + c16 < cp.len;
@@ -600,9 +601,10 @@ __global__ __launch_bounds__(pf::NT, 2) void inv_kernel(const uint16_t* __restri
         const float inv = l2norm_inv(xor32_sum(xor16_sum(ss)));
 #pragma unroll
         for (int s = 0; s < 4; ++s) kf[tt][s] = scale_bf16(kf[tt][s], inv);
-        if (g4 == 0) knorm[((int64_t)slot * Hv + h) * CH + 16 * tt + c16] = inv;
+        mine = g4 == tt ? inv : mine;
       }
     }
+    if (use_l2) knorm[((int64_t)slot * Hv + h) * CH + lane] = mine;
   }
   // K K^T: kk[tri(a, b)] = Dl of block (b, a) -- lane (c, g) r: (K K^T)[16 b + 4 g + r][16 a + c]
   f32x4 kk[10];
@@ -638,16 +640,18 @@ __global__ __launch_bounds__(pf::NT, 2) void inv_kernel(const uint16_t* __restri
 #pragma unroll
     for (int b = 0; b <= a; ++b)
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
+      for (int rr = 0; rr < 4; ++rr) {  // straight-line: the exponent is clamped to <= 0, the mask multiplies
         const int i = 16 * a + c16, j = 16 * b + 4 * g4 + rr;
-        XT[tri(a, b)][rr] = i > j ? -Bc[a] * kk[tri(a, b)][rr] * __expf(Gc[a] - Gr[b][rr]) : 0.f;
+        const float x = -Bc[a] * kk[tri(a, b)][rr] * __expf(fminf(Gc[a] - Gr[b][rr], 0.f));
+        XT[tri(a, b)][rr] = x * (i > j ? 1.f : 0.f);
       }
 #pragma unroll
   for (int a = 0; a < 4; ++a)
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       const int i = 16 * a + 4 * g4 + rr, j = 16 * a + c16;
-      Xd[a][rr] = i > j ? -Br[a][rr] * kk[tri(a, a)][rr] * __expf(Gr[a][rr] - Gc[a]) : 0.f;
+      const float x = -Br[a][rr] * kk[tri(a, a)][rr] * __expf(fminf(Gr[a][rr] - Gc[a], 0.f));
+      Xd[a][rr] = x * (i > j ? 1.f : 0.f);
     }
   f32x4 TT[10];
   reg_inv64(XT, Xd, TT, strp[w], lane);
