@@ -352,6 +352,7 @@ struct SegTable {
   const int32_t* cu;
   const int32_t* chunk0;
   const int32_t* seg0;
+  const int32_t* order;  // output pass: segments longest first (nullptr: in index order)
   int nseq, seq_len, L;
   __device__ __forceinline__ int nch(int s) const {
     return cu ? chunk0[s + 1] - chunk0[s] : (seq_len + pf::CH - 1) / pf::CH;
@@ -387,10 +388,25 @@ struct SegTable {
   }
 };
 
-// seg0 (nseq + 1 entries) from the chunk prefix sums: one workgroup, a block-wise scan.
+// Inclusive scan of part[0..255] in place (all 256 threads; barriers inside).
+__device__ __forceinline__ void block_scan256(int* part, int t) {
+  for (int o = 1; o < 256; o <<= 1) {
+    const int x = t >= o ? part[t - o] : 0;
+    __syncthreads();
+    part[t] += x;
+    __syncthreads();
+  }
+}
+// The output pass deals (segment, value head) items to compute units in launch order, so segments
+// are listed longest first (a greedy longest-processing-time schedule): a counting sort by chunk
+// count, for segment lengths up to kLptMaxLen (else the order is the identity).
+constexpr int kLptMaxLen = 2048;
+// seg0 (nseq + 1 entries) from the chunk prefix sums, and order[] (segments by decreasing chunk
+// count; ties in any order): one workgroup.
 __global__ __launch_bounds__(256) void seg_table_kernel(const int32_t* __restrict__ chunk0, int nseq, int L,
-                                                       int32_t* __restrict__ seg0) {
+                                                       int32_t* __restrict__ seg0, int32_t* __restrict__ order) {
   __shared__ int part[256];
+  __shared__ int hist[kLptMaxLen + 1];
   const int t = threadIdx.x;
   int base = 0;
   for (int s0 = 0; s0 < nseq; s0 += 256) {
@@ -402,17 +418,43 @@ __global__ __launch_bounds__(256) void seg_table_kernel(const int32_t* __restric
     }
     part[t] = n;
     __syncthreads();
-    for (int o = 1; o < 256; o <<= 1) {  // inclusive scan
-      const int x = t >= o ? part[t - o] : 0;
-      __syncthreads();
-      part[t] += x;
-      __syncthreads();
-    }
+    block_scan256(part, t);
     if (s < nseq) seg0[s] = base + part[t] - n;
     base += part[255];
     __syncthreads();
   }
   if (t == 0) seg0[nseq] = base;
+  if (L > kLptMaxLen) {
+    for (int j = t; j < base; j += 256) order[j] = j;
+    return;
+  }
+  for (int i = t; i <= L; i += 256) hist[i] = 0;
+  __syncthreads();
+  // segment idx of sequence s covers min(L, n - idx L) chunks (an empty sequence: one of 0)
+  for (int s = t; s < nseq; s += 256) {
+    const int n = chunk0[s + 1] - chunk0[s], ns = n <= L ? 1 : (n + L - 1) / L;
+    for (int idx = 0; idx < ns; ++idx) atomicAdd(&hist[n - idx * L < L ? n - idx * L : L], 1);
+  }
+  __syncthreads();
+  // hist[len] := number of segments longer than len (exclusive scan from len = L down to 0): thread t
+  // takes positions p = len' order L - p in [t * per, (t + 1) * per)
+  const int per = (L + 1 + 255) / 256, p0 = t * per, p1 = p0 + per < L + 1 ? p0 + per : L + 1;
+  int sum = 0;
+  for (int p = p0; p < p1; ++p) sum += hist[L - p];
+  part[t] = sum;
+  __syncthreads();
+  block_scan256(part, t);
+  int acc = part[t] - sum;
+  for (int p = p0; p < p1; ++p) {
+    const int c = hist[L - p];
+    hist[L - p] = acc;
+    acc += c;
+  }
+  __syncthreads();
+  for (int s = t; s < nseq; s += 256) {
+    const int n = chunk0[s + 1] - chunk0[s], ns = n <= L ? 1 : (n + L - 1) / L, j0 = seg0[s];
+    for (int idx = 0; idx < ns; ++idx) order[atomicAdd(&hist[n - idx * L < L ? n - idx * L : L], 1)] = j0 + idx;
+  }
 }
 
 // ============================================================================================
@@ -1124,9 +1166,10 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
   const int t = threadIdx.x, w = t >> 6, lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
   int mode, h, s, idx, slot = -1;
   if (kPass == 0) {
-    const int item = xcd_item(blockIdx.x, gridDim.x), j = item / Hv;
+    const int item = xcd_item(blockIdx.x, gridDim.x), jo = item / Hv;
     h = item % Hv;
-    if (j >= tab.first_seg(tab.nseq)) return;
+    if (jo >= tab.first_seg(tab.nseq)) return;
+    const int j = tab.order ? tab.order[jo] : jo;
     s = tab.seq_of_seg(j);
     idx = j - tab.first_seg(s);
     if (idx > 0) slot = tab.first_slot(s) + idx - 1;  // the previous segment's slot holds this one's state
@@ -1559,19 +1602,21 @@ int64_t seg_len(int64_t total_chunks, int Hv) {
   const int64_t L = (work + sg::kTargetItems - 1) / sg::kTargetItems;
   return L < sg::kMinSeg ? sg::kMinSeg : L;
 }
-// Workspace layout: the segment table (nseq + 1 int32), the transition flags (int32 per (slot,
+// Workspace layout: the segment table (nseq + 1 int32), the longest-first segment order (int32 per
+// segment), the transition flags (int32 per (slot,
 // value head)), the warm-up lengths (int32 per (slot, value head)), the transition slots (A, B fp32
 // per (slot, value head)), the inverse kernel's fragments (6 KiB per (chunk, value head)) and its K
 // l2norm factors (64 fp32 per (chunk, value head)), each part 256-byte aligned.
 struct SegLayout {
-  int64_t L, nslots, off_flags, off_warm, off_trans, off_tfrag, off_knorm, bytes;
+  int64_t L, nslots, off_order, off_flags, off_warm, off_trans, off_tfrag, off_knorm, bytes;
 };
 SegLayout seg_layout(int64_t total_chunks, int nseq, int Hv) {
   auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
   SegLayout l;
   l.L = seg_len(total_chunks, Hv);
   l.nslots = total_chunks / l.L;
-  l.off_flags = up(((int64_t)nseq + 1) * 4);
+  l.off_order = up(((int64_t)nseq + 1) * 4);
+  l.off_flags = l.off_order + up(((int64_t)nseq + total_chunks / l.L) * 4);  // segments: <= nseq + chunks / L
   l.off_warm = l.off_flags + up(l.nslots * Hv * 4);
   l.off_trans = l.off_warm + up(l.nslots * Hv * 4);
   l.off_tfrag = l.off_trans + l.nslots * Hv * (int64_t)sg::kTrans * 4;
@@ -1627,6 +1672,7 @@ extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const voi
   const SegLayout lay = seg_layout(total_chunks, nseq, Hv);
   uint8_t* work = (uint8_t*)workspace;
   int32_t* seg0 = (int32_t*)work;
+  int32_t* order = (int32_t*)(work + lay.off_order);
   int* tflags = (int*)(work + lay.off_flags);
   int* warm = (int*)(work + lay.off_warm);
   float* trans = (float*)(work + lay.off_trans);
@@ -1637,11 +1683,12 @@ extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const voi
                   total_chunks * Hv < (1ll << 33),
               "gdn_chunk_prefill: grid too large");
   if (cu_seqlens) {
-    seg_table_kernel<<<1, 256, 0, st>>>(seq_chunk0, nseq, (int)lay.L, seg0);
+    seg_table_kernel<<<1, 256, 0, st>>>(seq_chunk0, nseq, (int)lay.L, seg0, order);
     int rc = check_launch("gdn_chunk_prefill(table)");
     if (rc) return rc;
   }
-  const SegTable tab{cu_seqlens, seq_chunk0, cu_seqlens ? seg0 : nullptr, nseq, seq_len, (int)lay.L};
+  const SegTable tab{cu_seqlens, seq_chunk0, cu_seqlens ? seg0 : nullptr, cu_seqlens ? order : nullptr, nseq, seq_len,
+                     (int)lay.L};
   if (total_chunks > 0) {  // the intra-chunk inverses, one wave per (chunk, value head)
     const int64_t items = total_chunks * Hv;
     const unsigned gi = (unsigned)((items + 3) / 4);
