@@ -816,7 +816,7 @@ __device__ __forceinline__ void loc_load(LocIn& L, int64_t t0, int len, int kh, 
                                          const uint16_t* __restrict__ k, uint32_t ks, const uint16_t* __restrict__ q,
                                          uint32_t qs, const uint16_t* __restrict__ v, uint32_t vs,
                                          const float* __restrict__ g, int Hv, const uint8_t* __restrict__ tfr,
-                                         const float* __restrict__ knc) {
+                                         const float* __restrict__ knc, bool q_on) {
   using namespace pf;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const uint32_t tq = t >> 4, fb = t & 15;
@@ -830,8 +830,8 @@ __device__ __forceinline__ void loc_load(LocIn& L, int64_t t0, int len, int kh, 
     L.kr[i] = *reinterpret_cast<const u16x8*>(kb + ((rc * ks + 8 * fb) * 2u));
     L.vr[i] = *reinterpret_cast<const u16x8*>(vb + ((rc * vs + 8 * fb) * 2u));
   }
-  if (kNeedQ) {
-    const uint32_t row = 16 * w + (lane & 15), rc = row < (uint32_t)len ? row : (uint32_t)len - 1;
+  if (kNeedQ) {  // a warm-up chunk (no outputs) reads one row for all lanes: the loads stay, the bytes go
+    const uint32_t row = 16 * w + (lane & 15), rc = !q_on ? 0u : (row < (uint32_t)len ? row : (uint32_t)len - 1);
     const char* qb = reinterpret_cast<const char*>(q + t0 * qs + (int64_t)kh * D);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
@@ -1247,7 +1247,7 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     bf16x8 qf[4], tbu[2];
     auto load = [&](LocIn& L, int c) __attribute__((always_inline)) {
       loc_load<need_q>(L, chunk_t0(c), chunk_len(c), kh, h, k, (uint32_t)ks, q, (uint32_t)qs, v, (uint32_t)vs, g, Hv,
-                       tfr(c), knorm + ((int64_t)(chunk_slot0 + c) * Hv + h) * CH);
+                       tfr(c), knorm + ((int64_t)(chunk_slot0 + c) * Hv + h) * CH, c >= w0);
     };
     auto phase2 = [&](SegBuf& B, bool q_on) __attribute__((always_inline)) {
       switch (w) {
