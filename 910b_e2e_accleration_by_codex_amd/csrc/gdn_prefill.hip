@@ -1659,7 +1659,7 @@ extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const voi
   GDN_SUPPORT(in_dtype == GDN_BF16, "gdn_chunk_prefill: q/k/v must be bfloat16 (MFMA operands)");
   GDN_REQUIRE(beta_dtype == GDN_F32 || beta_dtype == GDN_BF16, "gdn_chunk_prefill: bad beta dtype");
   GDN_REQUIRE(Hqk > 0 && Hv > 0 && Hv % Hqk == 0, "gdn_chunk_prefill: bad heads Hqk=%d Hv=%d", Hqk, Hv);
-  GDN_REQUIRE(nseq >= 0 && total_tokens >= 0 && total_chunks >= 0, "gdn_chunk_prefill: negative sizes");
+  GDN_REQUIRE(nseq >= 0 && total_tokens >= 0 && total_chunks >= 0 && seq_len >= 0, "gdn_chunk_prefill: negative sizes");
   GDN_REQUIRE(cu_seqlens ? seq_chunk0 != nullptr : (int64_t)nseq * seq_len == total_tokens,
               "gdn_chunk_prefill: cu_seqlens needs seq_chunk0; without it nseq*seq_len must be total_tokens");
   GDN_REQUIRE(cu_seqlens || total_chunks == (int64_t)nseq * ((seq_len + pf::CH - 1) / pf::CH),
@@ -1726,7 +1726,10 @@ extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const voi
     else GDN_SEG_LAUNCH(float);
 #undef GDN_SEG_LAUNCH
   };
-  if (lay.nslots > 0) {  // segment summaries and their combination where no warm-up fits
+  // A sequence spans several segments only beyond L chunks: seq_len is the uniform length, or for
+  // packed sequences an upper bound of the longest one (0: unknown)
+  const int64_t max_seq_chunks = seq_len > 0 ? ((int64_t)seq_len + pf::CH - 1) / pf::CH : total_chunks;
+  if (lay.nslots > 0 && max_seq_chunks > lay.L) {  // segment summaries and their combination where no warm-up fits
     launch(1, lay.nslots * Hv * 2);
     int rc = check_launch("gdn_chunk_prefill(summary)");
     if (rc) return rc;

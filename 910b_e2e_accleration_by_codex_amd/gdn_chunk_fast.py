@@ -62,6 +62,7 @@ class Varlen:
         s0 = torch.zeros(host.numel(), dtype=torch.int64)
         s0[1:] = torch.cumsum(nch, 0)
         self.total_chunks = int(s0[-1])
+        self.max_len = int((host[1:] - host[:-1]).max()) if self.nseq else 0  # the kernels' seq_len bound
         self.cu = _to_device_int32(host, device)
         self.seq_chunk0 = _to_device_int32(s0, device)
 
@@ -89,7 +90,7 @@ def _chunk_table(B, T, cu_seqlens, device):
     if cu_seqlens is None:
         return None, None, B, T, B * ((T + CHUNK - 1) // CHUNK)
     vl = _varlen(cu_seqlens, B, T, device)
-    return vl.cu, vl.seq_chunk0, vl.nseq, 0, vl.total_chunks
+    return vl.cu, vl.seq_chunk0, vl.nseq, vl.max_len, vl.total_chunks
 
 
 class Rows:

@@ -187,6 +187,44 @@ def test_chunk_prefill_warm_up_and_exact_paths_per_head(gdn, oracle, dev):
             assert rel_l2(s[i, h], s_ref[i, h]) <= STATE_TOL, f"sequence {i} value head {h}"
 
 
+@pytest.mark.parametrize("lens", [[200, 1, 256, 130, 0, 64], [2500, 300, 1596]])
+def test_chunk_prefill_seq_len_bound_matches_unknown(gdn, oracle, dev, lens):
+    """Packed sequences through the C ABI with seq_len = 0 (no bound: the segment summaries are
+    launched) and with seq_len = the longest sequence: bit-identical outputs and states, and against
+    the oracle.  At 4 value heads these sizes cut segments of 4 chunks: in the first case no sequence
+    spans two segments (the summaries are skipped), in the second two sequences do (kept)."""
+    import importlib
+    from conftest import PKG_NAME
+    L = importlib.import_module(PKG_NAME + "._lib")
+    Hk, Hv, D = 2, 4, 128
+    T = sum(lens)
+    q, k, v, g, beta, _ = _gdn_inputs(T, Hk, Hv, seed=31, state=False, decay=1.0)
+    s0 = 0.02 * torch.randn(len(lens), Hv, D, D, generator=torch.Generator().manual_seed(32))
+    cu_h = torch.tensor([0] + torch.cumsum(torch.tensor(lens), 0).tolist(), dtype=torch.int32)
+    nch = [(n + 63) // 64 for n in lens]
+    c0_h = torch.tensor([0] + torch.cumsum(torch.tensor(nch), 0).tolist(), dtype=torch.int32)
+    total = int(c0_h[-1])
+    qd, kd, vd, gd, bd = (x[0].contiguous().to(dev) for x in (q, k, v, g, beta))
+    s0d, cu, c0 = s0.to(dev), cu_h.to(dev), c0_h.to(dev)
+    work = torch.empty(int(L.lib().gdn_chunk_prefill_workspace_bytes(total, len(lens), Hv)), dtype=torch.uint8,
+                       device=dev)
+    res = []
+    for bound in (0, max(lens)):
+        out = torch.empty(T, Hv, D, dtype=torch.bfloat16, device=dev)
+        fin = torch.empty_like(s0d)
+        L.call("gdn_chunk_prefill", L.ptr(qd), qd.stride(0), L.ptr(kd), kd.stride(0), L.ptr(vd), vd.stride(0),
+               L.ptr(gd), L.ptr(bd), L.BF16, L.ptr(s0d), L.ptr(fin), L.ptr(out), T, L.ptr(cu), L.ptr(c0), total,
+               len(lens), bound, Hk, Hv, D, L.BF16, 1, L.ptr(work), work.numel(), L.stream_of(qd))
+        torch.cuda.synchronize()
+        res.append((out.clone(), fin.clone()))
+    assert torch.equal(res[0][0], res[1][0]) and torch.equal(res[0][1], res[1][1])
+    o_ref, s_ref = oracle.chunk_gated_delta_rule_varlen(_rep(q, 2), _rep(k, 2), v, g, beta, cu_h, 64, s0, True, True)
+    assert rel_l2(res[1][0].cpu().unsqueeze(0), o_ref) <= OUT_TOL
+    for i, n in enumerate(lens):
+        if n:
+            assert rel_l2(res[1][1][i].cpu(), s_ref[i]) <= STATE_TOL, f"sequence {i}"
+
+
 @pytest.mark.parametrize("with_history", [False, True])
 def test_conv_prefill(gdn, oracle, dev, with_history):
     C, K = 512, 4
