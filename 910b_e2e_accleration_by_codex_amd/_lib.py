@@ -53,6 +53,8 @@ _SIGNATURES = {
                                  _I, _I, _I, _I, _P], _I),
     "gdn_chunk_prefill_rows": ([_P, _L, _P, _L, _P, _L, _P, _P, _I, _P, _P, _P, _I, _P, _L, _P, _P, _L, _I,
                                 _I, _I, _I, _I, _I, _I, _P, _L, _P], _I),
+    "gdn_chunk_prefill_rows_gated": ([_P, _L, _P, _L, _P, _L, _P, _P, _I, _P, _P, _P, _I, _P, _L, _P, _P, _L,
+                                      _I, _I, _I, _I, _I, _I, _I, _P, _L, _P, _I, _F, _P, _L, _P], _I),
     "gdn_chunk_prefill_noalloc": ([_P, _L, _P, _L, _P, _L, _P, _P, _I, _P, _P, _P, _I, _P, _L, _P, _P, _L, _I,
                                    _I, _I, _I, _I, _I, _I, _P], _I),
     "gdn_conv_prefill_rows": ([_P, _L, _P, _P, _P, _P, _P, _P, _I, _L, _P, _I, _I, _I, _I, _P], _I),

@@ -242,6 +242,9 @@ __global__ __launch_bounds__(256) void conv_update_kernel(const uint16_t* __rest
 // ============================================================================================
 // Gated RMSNorm (HF Qwen3_5RMSNormGated): one wave per row, D % 64 == 0, D <= 512.
 // ============================================================================================
+// Every gated norm here (and the one fused into the prefill output kernel, which repeats
+// gated_rmsnorm128_kernel's arithmetic) takes the row factor from the hardware reciprocal square
+// root and SiLU from the hardware exp and reciprocal: outputs within one bf16 ulp of torch's.
 // x, gate and weight hold this lane's D/64 values (element j*64 + lane; x bf16-rounded), all
 // loaded beforehand so a caller can fetch them long before the row is ready.
 __device__ __forceinline__ void gated_norm_row(const float* x, const float* gate, const float* weight, bool w_bf16,
@@ -250,11 +253,11 @@ __device__ __forceinline__ void gated_norm_row(const float* x, const float* gate
   const int nper = D / 64;
   for (int j = 0; j < nper; ++j) ss += x[j] * x[j];
   ss = wave_sum(ss);
-  const float inv = rsqrt_f(ss / (float)D + eps);
+  const float inv = rsq_fast(ss / (float)D + eps);
   for (int j = 0; j < nper; ++j) {
     const float xn = rbf(x[j] * inv);
     const float y = w_bf16 ? rbf(weight[j] * xn) : weight[j] * xn;
-    out[j * 64 + lane] = f2bf(y * silu_f(gate[j]));
+    out[j * 64 + lane] = f2bf(y * silu_fast(gate[j]));
   }
 }
 
@@ -283,7 +286,7 @@ __global__ __launch_bounds__(256) void gated_rmsnorm128_kernel(const uint16_t* _
   }
 #pragma unroll
   for (int o = 1; o < 16; o <<= 1) ss += __shfl_xor(ss, o, kWave);
-  const float inv = rsqrt_f(ss / 128.0f + eps);
+  const float inv = rsq_fast(ss / 128.0f + eps);
   u16x8 ov;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -291,7 +294,7 @@ __global__ __launch_bounds__(256) void gated_rmsnorm128_kernel(const uint16_t* _
     const float xn = rbf(xf[e] * inv);
     const float y = kWBf16 ? rbf(bf2f(reinterpret_cast<const uint16_t*>(weight)[c]) * xn)
                            : reinterpret_cast<const float*>(weight)[c] * xn;
-    ov[e] = f2bf(y * silu_f(bf2f(zv[e])));
+    ov[e] = f2bf(y * silu_fast(bf2f(zv[e])));
   }
   if (ok) *reinterpret_cast<u16x8*>(out + row * 128 + 8 * sub) = ov;
 }
@@ -523,14 +526,14 @@ __global__ __launch_bounds__(kHeadThreads * R) void decode_fused_kernel(
         ss += o[e] * o[e];
       }
       ss = half_sum(ss);
-      const float inv = rsqrt_f(ss / (float)kD + eps);
+      const float inv = rsq_fast(ss / (float)kD + eps);
       uint16_t ov[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float xn = rbf(o[e] * inv);
         const float wt = kWBf16 ? bf2f((uint16_t)(nwr[e >> 1] >> (16 * (e & 1)))) : __uint_as_float(nwr[e]);
         const float y = kWBf16 ? rbf(wt * xn) : wt * xn;
-        ov[e] = f2bf(y * silu_f(bf2f((uint16_t)(zr[e >> 1] >> (16 * (e & 1))))));
+        ov[e] = f2bf(y * silu_fast(bf2f((uint16_t)(zr[e >> 1] >> (16 * (e & 1))))));
       }
       if (lane < 32) {
         const uint64_t pk = (uint64_t)ov[0] | ((uint64_t)ov[1] << 16) | ((uint64_t)ov[2] << 32) | ((uint64_t)ov[3] << 48);

@@ -994,12 +994,86 @@ struct ChainRegs {
   f32x4 S[2][8];
   bf16x8 hi[2][2], lo[2][2];  // DEC vn, split, carried from part 1 to part 2
 };
+// The gated RMSNorm of the fused prefill layer (HF Qwen3_5RMSNormGated, modeling_qwen3_5.py, over
+// each (token, value head) row of D = 128), applied to a chunk's outputs before they are stored:
+// out = bf16(w bf16(x rsqrt(mean(x^2) + eps)) silu(z)) with x = bf16(o).  The chain waves leave
+// bf16(o) in the chunk's V tile (each wave in its own 32 columns, which only it reads); during the
+// next step, local wave w reads rows 16 w .. 16 w + 15 of it just before it writes the next V rows
+// there, and normalises, gates and stores them.  Lane mapping, sum order (8 columns in a lane, then
+// the butterfly over 16 lanes) and roundings are gated_rmsnorm128_kernel's: the result is the same,
+// bit for bit, as that kernel applied to the stored outputs.
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+struct GateArgs {
+  const uint16_t* z;  // [tokens, Hv * D] bf16 gate rows, token stride zs
+  int64_t zs;
+  const void* w;      // [D] norm weight, bf16 (kNorm 1) or fp32 (kNorm 2)
+  float eps;
+};
+struct NormIn {
+  u16x8 o[4], z[4];  // rows 4 tq + i, columns 8 fb .. 8 fb + 7 (t = 16 tq + fb)
+};
+// Requests one chunk's z rows (token base zb = z + t0 zs + h D; rows past len repeat the last).
+__device__ __forceinline__ void norm_fetch_z(NormIn& N, const uint16_t* __restrict__ zb, uint32_t zs, int len) {
+  int t;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"((int)threadIdx.x));
+  const uint32_t tq = t >> 4, fb = t & 15;
+  const char* zc = reinterpret_cast<const char*>(zb);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t row = 4 * tq + i, rc = row < (uint32_t)len ? row : (uint32_t)len - 1;
+    N.z[i] = *reinterpret_cast<const u16x8*>(zc + ((rc * zs + 8 * fb) * 2u));
+  }
+}
+// Reads a chunk's bf16 outputs from the V tile of B.
+__device__ __forceinline__ void norm_fetch_o(NormIn& N, const SegBuf& B) {
+  using namespace pf;
+  int t;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"((int)threadIdx.x));
+  const uint32_t tq = t >> 4, fb = t & 15;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) N.o[i] = *reinterpret_cast<const u16x8*>(&B.V[(4 * tq + i) * LDK + 8 * fb]);
+}
+// Normalises, gates and stores the rows of N below len (ob = out + (t0 Hv + h) D); wt = the weight
+// of columns 8 fb .. 8 fb + 7.
+template <int kNorm>
+__device__ __forceinline__ void norm_store(const NormIn& N, const float (&wt)[8], float eps, uint16_t* __restrict__ ob,
+                                           int Hv, int len) {
+  using namespace pf;
+  int t;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"((int)threadIdx.x));
+  const int tq = t >> 4, fb = t & 15;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 4 * tq + i;
+    float xf[8], ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      xf[e] = bf2f(N.o[i][e]);
+      ss += xf[e] * xf[e];
+    }
+    ss = row16_sum(ss);
+    const float inv = rsq_fast(ss / 128.0f + eps);
+    u32x4v ov;
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {  // pairs: one conversion rounds two values
+      const uint32_t xn = f2bf2(xf[e] * inv, xf[e + 1] * inv);
+      float y0 = wt[e] * __uint_as_float(xn << 16), y1 = wt[e + 1] * __uint_as_float(xn & 0xffff0000u);
+      if (kNorm == 1) {
+        const uint32_t yr = f2bf2(y0, y1);
+        y0 = __uint_as_float(yr << 16);
+        y1 = __uint_as_float(yr & 0xffff0000u);
+      }
+      ov[e >> 1] = f2bf2(y0 * silu_fast(bf2f(N.z[i][e])), y1 * silu_fast(bf2f(N.z[i][e + 1])));
+    }
+    if (row < len) *reinterpret_cast<u32x4v*>(ob + ((int64_t)row * Hv * D + 8 * fb)) = ov;
+  }
+}
 // Chain part 1 for one chunk: U (fp32, from the inverse kernel's T diag(beta) fragments and the V
 // rows), vn = U - W S, the outputs o = diag(scale e^G) Q S + QK vn (kOut), and DEC vn split for part
 // 2.  W S and Q S share the loop over the state's k-blocks j (16 independent accumulators); the LDS
 // fragments of block j + 1 are requested before the products of block j, so their latency hides
 // behind those products.
-template <bool kUseU, bool kOut>
+template <bool kUseU, bool kOut, bool kNorm = false>
 __device__ __forceinline__ void chain_part1(const SegBuf& B, ChainRegs& R, uint16_t* __restrict__ out, int64_t t0,
                                             int len, int Hv, int h, int wc, int lane_in) {
   using namespace pf;
@@ -1100,18 +1174,29 @@ __device__ __forceinline__ void chain_part1(const SegBuf& B, ChainRegs& R, uint1
         O[tb][0] = mma(vb[0][jj], kq[tf::fid(tb, jj)], O[tb][0]);
         O[tb][1] = mma(vb[1][jj], kq[tf::fid(tb, jj)], O[tb][1]);
       }
-    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-    uint16_t* orow = out + ((t0 + c16) * Hv + h) * D + 32 * wc + 4 * g4;
-    const int64_t tile = (int64_t)16 * Hv * D;
+    if (kNorm) {  // bf16(o) into this wave's 32 columns of the V tile (read by no other wave):
+                  // the local waves normalise, gate and store the rows one step later
+      uint16_t* vrow = const_cast<uint16_t*>(B.V) + c16 * LDK + 32 * wc + 4 * g4;
 #pragma unroll
-    for (int tb = 0; tb < 4; ++tb)
-      if (16 * tb + c16 < len) {
+      for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
         for (int sl = 0; sl < 2; ++sl) {
-          const u32x2 pk = {f2bf2(O[tb][sl][0], O[tb][sl][1]), f2bf2(O[tb][sl][2], O[tb][sl][3])};
-          *reinterpret_cast<u32x2*>(orow + tb * tile + 16 * sl) = pk;
+          const u32x2v pk = {f2bf2(O[tb][sl][0], O[tb][sl][1]), f2bf2(O[tb][sl][2], O[tb][sl][3])};
+          *reinterpret_cast<u32x2v*>(vrow + 16 * tb * LDK + 16 * sl) = pk;
         }
-      }
+    } else {
+      uint16_t* orow = out + ((t0 + c16) * Hv + h) * D + 32 * wc + 4 * g4;
+      const int64_t tile = (int64_t)16 * Hv * D;
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb)
+        if (16 * tb + c16 < len) {
+#pragma unroll
+          for (int sl = 0; sl < 2; ++sl) {
+            const u32x2v pk = {f2bf2(O[tb][sl][0], O[tb][sl][1]), f2bf2(O[tb][sl][2], O[tb][sl][3])};
+            *reinterpret_cast<u32x2v*>(orow + tb * tile + 16 * sl) = pk;
+          }
+        }
+    }
   }
   // DEC vn -> hi + lo bf16 (k-slot ordered B fragments of the update)
 #pragma unroll
@@ -1165,7 +1250,7 @@ __device__ __forceinline__ void chain_part2(const SegBuf& B, ChainRegs& R, int l
 // (from the identity, without U), written into the slot; A is skipped when negligible.
 // Waves 0-3 (local) prepare chunk c+1's operands in one buffer while waves 4-7 (chain) run chunk c
 // from the other: two LDS barriers a chunk, met by both roles.
-template <typename BetaT, typename OutT, int kPass>
+template <typename BetaT, typename OutT, int kPass, int kNorm = 0>
 __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     const uint16_t* __restrict__ q, int64_t qs, const uint16_t* __restrict__ k, int64_t ks, const uint16_t* __restrict__ v,
     int64_t vs, const float* __restrict__ g,
@@ -1173,7 +1258,7 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     const float* __restrict__ init,
     const int32_t* __restrict__ rows, int n_rows, float* __restrict__ final_state, float* __restrict__ trans,
     int* __restrict__ tflags, const uint8_t* __restrict__ tfrag, const float* __restrict__ knorm,
-    const int* __restrict__ warm) {
+    const int* __restrict__ warm, GateArgs gate) {
   using namespace pf;
   __shared__ SegSmem sm;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
@@ -1257,16 +1342,41 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
         default: loc_phase2<3, need_q>(B, qf, tbu, q_on); break;
       }
     };
+    // gated norm (kNorm): the weight of columns 8 fb .. 8 fb + 7, and chunk j's outputs (j >= w0)
+    float wt[8];
+    if (kNorm) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int col = 8 * (t & 15) + e;
+        wt[e] = kNorm == 1 ? bf2f(reinterpret_cast<const uint16_t*>(gate.w)[col]) : reinterpret_cast<const float*>(gate.w)[col];
+      }
+    }
+    NormIn nin;
+    auto norm_req_z = [&](int j) __attribute__((always_inline)) {  // a step ahead of its use
+      const int jz = j >= w0 ? j : w0;  // a chunk without outputs requests a valid chunk's rows, unused
+      norm_fetch_z(nin, gate.z + chunk_t0(jz) * gate.zs + (int64_t)h * D, (uint32_t)gate.zs, chunk_len(jz));
+    };
+    auto norm_out = [&](int j) __attribute__((always_inline)) {
+      norm_store<kNorm>(nin, wt, gate.eps, out + (chunk_t0(j >= w0 ? j : w0) * Hv + h) * D, Hv,
+                        j >= w0 ? chunk_len(j) : 0);
+    };
     auto step = [&](int c, LocIn& nxt, const LocIn& cur) __attribute__((always_inline)) {  // prepare chunk c + 1 from cur
+      if (kNorm) norm_fetch_o(nin, sm.buf[(c + 1) & 1]);  // the chain's outputs of step c - 1, before
+                                                          // chunk c + 1's V rows replace them
       load(nxt, c + 2 < ntot ? c + 2 : ntot - 1);
       loc_phase1<need_q>(sm.buf[(c + 1) & 1], cur, chunk_len(c + 1), use_l2, c + 1 >= w0, qf);
       tbu[0] = cur.tb[0];
       tbu[1] = cur.tb[1];
+      if (kNorm) {
+        norm_out(c - 1);
+        norm_req_z(c);
+      }
       lds_barrier();
       phase2(sm.buf[(c + 1) & 1], c + 1 >= w0);
       lds_barrier();
     };
     if (ntot > 0) {
+      if (kNorm) norm_req_z(-1);  // unused: every step then finds one z request in flight
       load(ia, 0);
       load(ib, ntot > 1 ? 1 : 0);
       loc_phase1<need_q>(sm.buf[0], ia, chunk_len(0), use_l2, w0 == 0, qf);
@@ -1282,9 +1392,18 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
       step(c + 1, ib, ia);
     }
     if (c + 1 < ntot) step(c, ia, ib);
-    if (ntot > 0) {  // the chain's last step: nothing left to prepare
+    if (ntot > 0) {  // the chain's last step: nothing left to prepare (the outputs of the last two chunks)
+      if (kNorm && ntot > 1) {
+        norm_fetch_o(nin, sm.buf[ntot & 1]);
+        norm_out(ntot - 2);
+      }
+      if (kNorm) norm_req_z(ntot - 1);
       lds_barrier();
       lds_barrier();
+      if (kNorm) {
+        norm_fetch_o(nin, sm.buf[(ntot - 1) & 1]);
+        norm_out(ntot - 1);
+      }
     }
   } else {
     // ------------------------------------------------------------ chain waves
@@ -1320,7 +1439,8 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     lds_barrier();
     for (int c = 0; c < ntot; ++c) {
       const SegBuf& B = sm.buf[c & 1];
-      if (kPass == 0 && c >= w0) chain_part1<true, true>(B, R, out, chunk_t0(c), chunk_len(c), Hv, h, wc, lane);
+      if (kPass == 0 && c >= w0)
+        chain_part1<true, true, kNorm != 0>(B, R, out, chunk_t0(c), chunk_len(c), Hv, h, wc, lane);
       else if (mode != kSegA) chain_part1<true, false>(B, R, out, 0, 0, Hv, h, wc, lane);
       else chain_part1<false, false>(B, R, out, 0, 0, Hv, h, wc, lane);
       lds_barrier();
@@ -1428,9 +1548,6 @@ __global__ __launch_bounds__(256) void seg_combine_kernel(SegTable tab, int Hv, 
 // sequence leaves (its last K inputs) is written afterwards by conv_state_capture_kernel, so the
 // history may be the same slot rows the state goes to.
 constexpr int kConvRun = 8;
-// SiLU with the hardware exp and reciprocal (each within about 1 ulp in fp32, so the bf16 result
-// is within one bf16 ulp of the exactly rounded x / (1 + e^-x)).
-__device__ __forceinline__ float silu_fast(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 __device__ __forceinline__ int find_seq(const int32_t* cu, int nseq, int64_t p) {
   int lo = 0, hi = nseq - 1;  // last sequence whose start <= p (skips empty ones)
   while (lo < hi) {
@@ -1644,14 +1761,14 @@ extern "C" int64_t gdn_chunk_prefill_workspace_bytes(int64_t total_chunks, int n
   return seg_layout(total_chunks, nseq, Hv).bytes;
 }
 
-extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const void* k, int64_t k_stride,
-                                      const void* v, int64_t v_stride, const float* g, const void* beta,
-                                      int beta_dtype, const float* initial_state, float* final_state,
-                                      const int32_t* state_rows, int n_rows, void* out, int64_t total_tokens,
-                                      const int32_t* cu_seqlens, const int32_t* seq_chunk0, int64_t total_chunks,
-                                      int nseq, int seq_len, int Hqk, int Hv, int D, int in_dtype,
-                                      int use_qk_l2norm, void* workspace, int64_t workspace_bytes, void* stream) {
-  clear_error();
+namespace {
+// gdn_chunk_prefill_rows, and with norm_mode 1 / 2 (bf16 / fp32 norm weight) the fused gated norm.
+int chunk_prefill_impl(const void* q, int64_t q_stride, const void* k, int64_t k_stride, const void* v,
+                       int64_t v_stride, const float* g, const void* beta, int beta_dtype, const float* initial_state,
+                       float* final_state, const int32_t* state_rows, int n_rows, void* out, int64_t total_tokens,
+                       const int32_t* cu_seqlens, const int32_t* seq_chunk0, int64_t total_chunks, int nseq,
+                       int seq_len, int Hqk, int Hv, int D, int in_dtype, int use_qk_l2norm, void* workspace,
+                       int64_t workspace_bytes, void* stream, const GateArgs& gate, int norm_mode) {
   GDN_REQUIRE(state_rows ? n_rows >= 0 : n_rows == nseq,
               "gdn_chunk_prefill: without state_rows, n_rows must equal nseq");
   GDN_REQUIRE(q && k && v && g && beta && out, "gdn_chunk_prefill: null input/output pointer");
@@ -1717,11 +1834,14 @@ extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const voi
     if (rc) return rc;
   }
   auto launch = [&](int pass, int64_t blocks) {
-#define GDN_SEG_LAUNCH(BT)                                                                                     \
-  (pass == 0 ? seg_kernel<BT, uint16_t, 0> : seg_kernel<BT, uint16_t, 1>)<<<(unsigned)blocks, sg::NT, 0, st>>>( \
-      (const uint16_t*)q, q_stride, (const uint16_t*)k, k_stride, (const uint16_t*)v, v_stride, g, (const BT*)beta,                                                    \
-      (uint16_t*)out, tab, Hqk, Hv, use_qk_l2norm, initial_state, state_rows, n_rows,           \
-      final_state, trans, tflags, tfrag, knorm, warm)
+#define GDN_SEG_LAUNCH(BT)                                                                                           \
+  (pass == 1 ? seg_kernel<BT, uint16_t, 1>                                                                          \
+             : norm_mode == 1 ? seg_kernel<BT, uint16_t, 0, 1>                                                      \
+                              : norm_mode == 2 ? seg_kernel<BT, uint16_t, 0, 2> : seg_kernel<BT, uint16_t, 0>)      \
+      <<<(unsigned)blocks, sg::NT, 0, st>>>((const uint16_t*)q, q_stride, (const uint16_t*)k, k_stride,              \
+                                            (const uint16_t*)v, v_stride, g, (const BT*)beta, (uint16_t*)out, tab, Hqk, \
+                                            Hv, use_qk_l2norm, initial_state, state_rows, n_rows, final_state, trans,  \
+                                            tflags, tfrag, knorm, warm, gate)
     if (beta_dtype == GDN_BF16) GDN_SEG_LAUNCH(uint16_t);
     else GDN_SEG_LAUNCH(float);
 #undef GDN_SEG_LAUNCH
@@ -1741,6 +1861,41 @@ extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const voi
   }
   launch(0, nseg_max * Hv);
   return check_launch("gdn_chunk_prefill(output)");
+}
+}  // namespace
+
+extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const void* k, int64_t k_stride,
+                                      const void* v, int64_t v_stride, const float* g, const void* beta,
+                                      int beta_dtype, const float* initial_state, float* final_state,
+                                      const int32_t* state_rows, int n_rows, void* out, int64_t total_tokens,
+                                      const int32_t* cu_seqlens, const int32_t* seq_chunk0, int64_t total_chunks,
+                                      int nseq, int seq_len, int Hqk, int Hv, int D, int in_dtype,
+                                      int use_qk_l2norm, void* workspace, int64_t workspace_bytes, void* stream) {
+  clear_error();
+  return chunk_prefill_impl(q, q_stride, k, k_stride, v, v_stride, g, beta, beta_dtype, initial_state, final_state,
+                            state_rows, n_rows, out, total_tokens, cu_seqlens, seq_chunk0, total_chunks, nseq, seq_len,
+                            Hqk, Hv, D, in_dtype, use_qk_l2norm, workspace, workspace_bytes, stream, GateArgs{}, 0);
+}
+
+extern "C" int gdn_chunk_prefill_rows_gated(const void* q, int64_t q_stride, const void* k, int64_t k_stride,
+                                            const void* v, int64_t v_stride, const float* g, const void* beta,
+                                            int beta_dtype, const float* initial_state, float* final_state,
+                                            const int32_t* state_rows, int n_rows, void* out, int64_t total_tokens,
+                                            const int32_t* cu_seqlens, const int32_t* seq_chunk0,
+                                            int64_t total_chunks, int nseq, int seq_len, int Hqk, int Hv, int D,
+                                            int in_dtype, int use_qk_l2norm, const void* z, int64_t z_stride,
+                                            const void* norm_weight, int norm_w_dtype, float eps, void* workspace,
+                                            int64_t workspace_bytes, void* stream) {
+  clear_error();
+  GDN_REQUIRE(z && norm_weight, "gdn_chunk_prefill_rows_gated: null gate or norm weight");
+  GDN_REQUIRE(norm_w_dtype == GDN_BF16 || norm_w_dtype == GDN_F32, "gdn_chunk_prefill_rows_gated: bad norm weight dtype");
+  GDN_REQUIRE(aligned(z, 16) && z_stride % 8 == 0 && z_stride >= (int64_t)Hv * D,
+              "gdn_chunk_prefill_rows_gated: gate rows must be 16-byte aligned and hold Hv * D values");
+  const GateArgs gate{(const uint16_t*)z, z_stride, norm_weight, eps};
+  return chunk_prefill_impl(q, q_stride, k, k_stride, v, v_stride, g, beta, beta_dtype, initial_state, final_state,
+                            state_rows, n_rows, out, total_tokens, cu_seqlens, seq_chunk0, total_chunks, nseq, seq_len,
+                            Hqk, Hv, D, in_dtype, use_qk_l2norm, workspace, workspace_bytes, stream, gate,
+                            norm_w_dtype == GDN_BF16 ? 1 : 2);
 }
 
 extern "C" int gdn_chunk_prefill(const void* q, int64_t q_stride, const void* k, int64_t k_stride,

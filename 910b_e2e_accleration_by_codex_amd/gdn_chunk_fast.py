@@ -138,7 +138,7 @@ def check_chunk_args(query, key, value, chunk_size):
 
 def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size=64, initial_state=None,
                            output_final_state=False, use_qk_l2norm_in_kernel=False, cu_seqlens=None,
-                           state_rows=None, final_state_out=None, **kwargs):
+                           state_rows=None, final_state_out=None, norm_gate=None, **kwargs):
     """query/key [B,T,Hqk,d] (Hqk = Hv after repeat_interleave, or Hv/r key heads read by value
     head h as h // r), value [B,T,Hv,d] bf16, g [B,T,Hv] (log decay, read in fp32), beta
     [B,T,Hv], initial_state [B or n_seq, Hv, d, d] | None.
@@ -146,7 +146,11 @@ def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size=64, initial_st
     Slot rows (added for a continuous-batching engine): with ``state_rows`` (int [n_seq]) the states
     live in slot buffers -- ``initial_state`` (or None = zero) and ``final_state_out`` are fp32
     [n_rows, Hv, d, d], sequence s uses row state_rows[s], and the two may be the same tensor; the
-    final state is then written there and returned."""
+    final state is then written there and returned.
+    Fused output norm (the GDN layer's Qwen3_5RMSNormGated, src/cb_tp.py:171-176): with
+    ``norm_gate`` = (z, norm_weight, eps), z bf16 [B*T, >= Hv*d] rows with unit inner stride (head h
+    of token t at z[t, h*d:(h+1)*d]) and norm_weight [d] bf16 or fp32, the returned rows are
+    gated_rmsnorm(out, z, norm_weight, eps) -- computed by the output kernel before the store."""
     check_chunk_args(query, key, value, chunk_size)
     _lib.require_cuda(query, key, value, g, beta, initial_state)
     B, T, Hqk, D = query.shape
@@ -187,11 +191,25 @@ def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size=64, initial_st
     out = torch.empty(B, T, Hv, D, dtype=query.dtype, device=dev)
     wbytes = int(_lib.lib().gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hv))
     work = torch.empty(max(wbytes, 1), dtype=torch.uint8, device=dev)
-    _lib.call("gdn_chunk_prefill_rows", _lib.ptr(q), qs, _lib.ptr(k), ks, _lib.ptr(v), vs, _lib.ptr(g32),
-              _lib.ptr(beta), _lib.dtype_code(beta), _lib.ptr(init), _lib.ptr(final), _lib.ptr(rows), n_rows,
-              _lib.ptr(out), B * T, _lib.ptr(cu), _lib.ptr(seq_chunk0), total_chunks, nseq, seq_len, Hqk, Hv,
-              D, _lib.dtype_code(query), int(bool(use_qk_l2norm_in_kernel)), _lib.ptr(work), wbytes,
-              _lib.stream_of(query))
+    args = (_lib.ptr(q), qs, _lib.ptr(k), ks, _lib.ptr(v), vs, _lib.ptr(g32), _lib.ptr(beta),
+            _lib.dtype_code(beta), _lib.ptr(init), _lib.ptr(final), _lib.ptr(rows), n_rows, _lib.ptr(out), B * T,
+            _lib.ptr(cu), _lib.ptr(seq_chunk0), total_chunks, nseq, seq_len, Hqk, Hv, D, _lib.dtype_code(query),
+            int(bool(use_qk_l2norm_in_kernel)))
+    if norm_gate is None:
+        _lib.call("gdn_chunk_prefill_rows", *args, _lib.ptr(work), wbytes, _lib.stream_of(query))
+        return out, final
+    z, norm_weight, eps = norm_gate
+    _lib.require_cuda(z, norm_weight)
+    z = z.reshape(B * T, -1)
+    if z.dtype != torch.bfloat16 or z.shape[1] < Hv * D or z.device != dev:
+        raise ValueError(f"chunk_gated_delta_rule: norm gate must be bf16 [{B * T}, >= {Hv * D}] on {dev}")
+    if z.stride(1) != 1 or z.stride(0) % 8 or z.data_ptr() % 16:
+        z = z.contiguous()
+    if tuple(norm_weight.shape) != (D,) or norm_weight.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"chunk_gated_delta_rule: norm weight must be bf16 or fp32 [{D}]")
+    w = norm_weight.contiguous()
+    _lib.call("gdn_chunk_prefill_rows_gated", *args, _lib.ptr(z), z.stride(0), _lib.ptr(w), _lib.dtype_code(w),
+              float(eps), _lib.ptr(work), wbytes, _lib.stream_of(query))
     return out, final
 
 
@@ -288,8 +306,8 @@ def gdn_prefill_core(mixed_qkv, z, a, b, conv_weight, A_log, dt_bias, norm_weigh
     """GDN prefill layer between in_proj_* and out_proj for one or more packed prompts
     (src/cb_tp.py:153-181 fresh, :230-263 continued): conv prefill + SiLU, split q|k|v, gating,
     chunked rule with l2norm (value head h reads key head h // r, no repeat_interleave copy),
-    gated RMSNorm.  mixed_qkv [T, C] bf16 (pre-conv), z [T, Hv*d], a, b [T, Hv];
-    cu_seqlens int [n_seq+1] (host or device) | Varlen | None -- host lengths, as the scheduler
+    gated RMSNorm (fused into the rule's output kernel).  mixed_qkv [T, C] bf16 (pre-conv),
+    z [T, Hv*d], a, b [T, Hv]; cu_seqlens int [n_seq+1] (host or device) | Varlen | None -- host lengths, as the scheduler
     holds them, keep the call free of GPU waits; conv_history [n_seq, C, K] | None;
     initial_state [n_seq, Hv, d, d] | None.
     Returns (core [T, Hv*d] bf16, conv_state [n_seq, C, K] bf16, rec_state [n_seq, Hv, d, d] fp32).
@@ -324,13 +342,12 @@ def gdn_prefill_core(mixed_qkv, z, a, b, conv_weight, A_log, dt_bias, norm_weigh
     k = qkv[:, kd:2 * kd].reshape(1, T, Hk, D)
     v = qkv[:, 2 * kd:].reshape(1, T, Hv, D)
     beta, g = gdn_gating(a.reshape(1, T, Hv), b.reshape(1, T, Hv), A_log, dt_bias)
+    gate = (z.reshape(T, -1), norm_weight, eps)
     if slots is not None:
         core, rec = chunk_gated_delta_rule(q, k, v, g, beta, chunk_size, rec_slots if continuation else None,
                                            True, True, cu_seqlens=cu_seqlens, state_rows=slots,
-                                           final_state_out=rec_slots)
+                                           final_state_out=rec_slots, norm_gate=gate)
     else:
         core, rec = chunk_gated_delta_rule(q, k, v, g, beta, chunk_size, initial_state, True, True,
-                                           cu_seqlens=cu_seqlens)
-    from .cb_engine import gated_rmsnorm
-    core = gated_rmsnorm(core.reshape(T * Hv, D), z.reshape(T * Hv, D), norm_weight, eps)
+                                           cu_seqlens=cu_seqlens, norm_gate=gate)
     return core.reshape(T, Hv * D), conv_state, rec

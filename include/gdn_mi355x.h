@@ -210,6 +210,26 @@ int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const void* k, int64
                            int use_qk_l2norm, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * gdn_chunk_prefill_rows whose output rows pass through the layer's gated RMSNorm before they are
+ * stored: out[t, h] = gdn_gated_rmsnorm(o[t, h], z[t, h], norm_weight, eps), with o the rule's
+ * output rounded to bf16 first -- bit for bit what the two calls in a row give.  Replaces the
+ * rule's output write and the Qwen3_5RMSNormGated call that follows it in the GDN prefill layer
+ * (src/cb_tp.py:171-176; HF:175-184), saving the output's round trip through HBM.
+ *   z: gate rows [total_tokens, >= Hv * D] bf16, row stride z_stride elements (a multiple of 8),
+ *      16-byte aligned; head h of token t at z + t * z_stride + h * D;
+ *   norm_weight [D] (norm_w_dtype: GDN_BF16 or GDN_F32);  in_dtype must be GDN_BF16, D = 128.
+ */
+int gdn_chunk_prefill_rows_gated(const void* q, int64_t q_stride, const void* k, int64_t k_stride,
+                                 const void* v, int64_t v_stride, const float* g, const void* beta,
+                                 int beta_dtype, const float* initial_state, float* final_state,
+                                 const int32_t* state_rows, int n_rows, void* out, int64_t total_tokens,
+                                 const int32_t* cu_seqlens, const int32_t* seq_chunk0, int64_t total_chunks,
+                                 int nseq, int seq_len, int Hqk, int Hv, int D, int in_dtype,
+                                 int use_qk_l2norm, const void* z, int64_t z_stride, const void* norm_weight,
+                                 int norm_w_dtype, float eps, void* workspace, int64_t workspace_bytes,
+                                 void* stream);
+
+/*
  * gdn_chunk_prefill_rows without a workspace argument and without any allocation: the kernels'
  * workspace is a static device array of GDN_NOALLOC_SCRATCH_BYTES (256 MiB) that the library holds on
  * every GPU it runs on until the process ends.  A call whose

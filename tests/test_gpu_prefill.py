@@ -225,6 +225,39 @@ def test_chunk_prefill_seq_len_bound_matches_unknown(gdn, oracle, dev, lens):
             assert rel_l2(res[1][1][i].cpu(), s_ref[i]) <= STATE_TOL, f"sequence {i}"
 
 
+@pytest.mark.parametrize("w_dtype", [torch.bfloat16, torch.float32])
+def test_chunk_prefill_fused_gated_norm_matches_two_calls(gdn, oracle, dev, w_dtype):
+    """The rule with its output rows passed through the gated RMSNorm in the output kernel against
+    the rule followed by gdn_gated_rmsnorm: equal final states and bit-identical outputs (same sum
+    order and roundings), and against the oracle.  Packed sequences of 1300, 5 and 900 tokens (at
+    4 value heads, segments of 4 chunks: later segments start from a warm-up or the exact path; a
+    one-chunk sequence), gate rows from a wider tensor (row stride > Hv * d)."""
+    import importlib
+    from conftest import PKG_NAME
+    engine = importlib.import_module(PKG_NAME + ".cb_engine")
+    Hk, Hv, D = 2, 4, 128
+    lens = [1300, 5, 900]
+    T = sum(lens)
+    cu = torch.tensor([0, 1300, 1305, 2205], dtype=torch.int32)
+    q, k, v, g, beta, _ = _gdn_inputs(T, Hk, Hv, seed=41, state=False)
+    s0 = 0.02 * torch.randn(3, Hv, D, D, generator=torch.Generator().manual_seed(42))
+    g_ = torch.Generator().manual_seed(43)
+    zw = torch.randn(T, Hv * D + 256, generator=g_).to(torch.bfloat16).to(dev)
+    z = zw[:, 128:128 + Hv * D]
+    nw = (1 + 0.1 * torch.randn(D, generator=g_)).to(w_dtype).to(dev)
+    args = (q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta.to(dev))
+    kw = dict(initial_state=s0.to(dev), output_final_state=True, use_qk_l2norm_in_kernel=True,
+              cu_seqlens=cu.to(dev))
+    o, s = gdn.chunk_gated_delta_rule(*args, **kw)
+    o2 = engine.gated_rmsnorm(o.reshape(T * Hv, D), z.reshape(T, Hv, D).reshape(T * Hv, D), nw, 1e-6)
+    of, sf = gdn.chunk_gated_delta_rule(*args, **kw, norm_gate=(z, nw, 1e-6))
+    assert torch.equal(s, sf)
+    assert torch.equal(o2.reshape(T, Hv, D), of.reshape(T, Hv, D))
+    o_ref, _ = oracle.chunk_gated_delta_rule_varlen(_rep(q, 2), _rep(k, 2), v, g, beta, cu, 64, s0, True, True)
+    ref = oracle.gated_rmsnorm(o_ref.to(torch.bfloat16).reshape(T * Hv, D), z.cpu().reshape(T * Hv, D), nw.cpu())
+    assert rel_l2(of.reshape(T * Hv, D), ref) <= OUT_TOL
+
+
 @pytest.mark.parametrize("with_history", [False, True])
 def test_conv_prefill(gdn, oracle, dev, with_history):
     C, K = 512, 4
