@@ -20,6 +20,7 @@
 // sees a bf16 rounding of its increment.
 #include "gdn_device.h"
 #include "gdn_internal.h"
+#include <type_traits>
 
 namespace gdn {
 
@@ -811,7 +812,11 @@ struct LocIn {
   f32x4 kn;  // the inverse kernel's l2norm factors of K rows 4 tq .. 4 tq + 3
   float graw;
 };
-template <bool kNeedQ>
+// Parts of a chunk's loads, and of phase 1 (kPart < 0: all): 0 the K rows and their l2norm factors,
+// 1 the V rows and the T diag(beta) fragments, 2 the q rows, 3 the g values.  The chunk loop
+// interleaves the next chunk's load parts with this chunk's phase-1 parts, so a wave's vector
+// memory instructions do not queue up in one block after the barrier.
+template <bool kNeedQ, int kPart = -1>
 __device__ __forceinline__ void loc_load(LocIn& L, int64_t t0, int len, int kh, int h,
                                          const uint16_t* __restrict__ k, uint32_t ks, const uint16_t* __restrict__ q,
                                          uint32_t qs, const uint16_t* __restrict__ v, uint32_t vs,
@@ -821,16 +826,30 @@ __device__ __forceinline__ void loc_load(LocIn& L, int64_t t0, int len, int kh, 
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const uint32_t tq = t >> 4, fb = t & 15;
   // byte offsets as 32-bit values: the loads address a uniform base plus a VGPR offset
-  const char* kb = reinterpret_cast<const char*>(k + t0 * ks + (int64_t)kh * D);
-  const char* vb = reinterpret_cast<const char*>(v + t0 * vs + (int64_t)h * D);
-  const float* gb = g + t0 * Hv + h;
+  if (kPart < 0 || kPart == 0) {
+    const char* kb = reinterpret_cast<const char*>(k + t0 * ks + (int64_t)kh * D);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t row = 4 * tq + i, rc = row < (uint32_t)len ? row : (uint32_t)len - 1;
-    L.kr[i] = *reinterpret_cast<const u16x8*>(kb + ((rc * ks + 8 * fb) * 2u));
-    L.vr[i] = *reinterpret_cast<const u16x8*>(vb + ((rc * vs + 8 * fb) * 2u));
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t row = 4 * tq + i, rc = row < (uint32_t)len ? row : (uint32_t)len - 1;
+      L.kr[i] = *reinterpret_cast<const u16x8*>(kb + ((rc * ks + 8 * fb) * 2u));
+    }
+    L.kn = *reinterpret_cast<const f32x4*>(reinterpret_cast<const char*>(knc) + tq * 16u);
   }
-  if (kNeedQ) {  // a warm-up chunk (no outputs) reads one row for all lanes: the loads stay, the bytes go
+  if (kPart < 0 || kPart == 1) {
+    const char* vb = reinterpret_cast<const char*>(v + t0 * vs + (int64_t)h * D);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t row = 4 * tq + i, rc = row < (uint32_t)len ? row : (uint32_t)len - 1;
+      L.vr[i] = *reinterpret_cast<const u16x8*>(vb + ((rc * vs + 8 * fb) * 2u));
+    }
+    // every wave issues the same loads (tiles 0 and 1 read their one fragment twice): the wait
+    // counts before the uses then stay exact along every path through the chunk loop
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+      L.tb[s] = *reinterpret_cast<const bf16x8*>(tfr + (uint32_t)(tf::fid(w, s) * ws::FRAG + lane * 16));
+  }
+  if (kNeedQ && (kPart < 0 || kPart == 2)) {  // a warm-up chunk (no outputs) reads one row for all lanes:
+                                               // the loads stay, the bytes go
     const uint32_t row = 16 * w + (lane & 15), rc = !q_on ? 0u : (row < (uint32_t)len ? row : (uint32_t)len - 1);
     const char* qb = reinterpret_cast<const char*>(q + t0 * qs + (int64_t)kh * D);
 #pragma unroll
@@ -840,20 +859,18 @@ __device__ __forceinline__ void loc_load(LocIn& L, int64_t t0, int len, int kh, 
       L.qr[s] = u16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
   }
-  // every wave issues the same loads (tiles 0 and 1 read their one fragment twice): the wait
-  // counts before the uses then stay exact along every path through the chunk loop
-#pragma unroll
-  for (int s = 0; s < 2; ++s)
-    L.tb[s] = *reinterpret_cast<const bf16x8*>(tfr + (uint32_t)(tf::fid(w, s) * ws::FRAG + lane * 16));
-  L.kn = *reinterpret_cast<const f32x4*>(reinterpret_cast<const char*>(knc) + tq * 16u);
-  const uint32_t tok = lane < len ? lane : len - 1;
-  L.graw = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(gb) + tok * (uint32_t)Hv * 4u);
+  if (kPart < 0 || kPart == 3) {
+    const float* gb = g + t0 * Hv + h;
+    const uint32_t tok = lane < len ? lane : len - 1;
+    L.graw = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(gb) + tok * (uint32_t)Hv * 4u);
+  }
 }
 
 // Local phase 1 (wave w < 4): K rows (masked, l2-normalised when asked), V rows and the T diag(beta)
 // fragments into the buffer, the q fragments (masked, l2-normalised when asked; kept in qf for
 // phase 2); wave 0 also forms the decay factors (G, e^{G_last - G}, e^G, scale e^G, e^{G_last}).
-template <bool kNeedQ>
+// kPart as for loc_load: part p uses only the inputs of load part p.
+template <bool kNeedQ, int kPart = -1>
 __device__ __forceinline__ void loc_phase1(SegBuf& B, const LocIn& in, int len, int use_l2, bool q_on,
                                            bf16x8 (&qf)[4]) {
   using namespace pf;
@@ -861,7 +878,7 @@ __device__ __forceinline__ void loc_phase1(SegBuf& B, const LocIn& in, int len, 
   asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"((int)threadIdx.x));
   const int w = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
   const int tq = t >> 4, fb = t & 15;
-  {  // K rows: zero past the chunk's end, scaled by the inverse kernel's l2norm factors
+  if (kPart < 0 || kPart == 0) {  // K rows: zero past the chunk's end, scaled by the inverse kernel's l2norm factors
     const u16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -869,12 +886,14 @@ __device__ __forceinline__ void loc_phase1(SegBuf& B, const LocIn& in, int len, 
       *reinterpret_cast<u16x8*>(&B.K[(4 * tq + i) * LDK + 8 * fb]) = 4 * tq + i < len ? kr : zero;
     }
   }
+  if (kPart < 0 || kPart == 1) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) *reinterpret_cast<u16x8*>(&B.V[(4 * tq + i) * LDK + 8 * fb]) = in.vr[i];
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<u16x8*>(&B.V[(4 * tq + i) * LDK + 8 * fb]) = in.vr[i];
 #pragma unroll
-  for (int s = 0; s < 2; ++s)
-    if (2 * s <= w) *reinterpret_cast<bf16x8*>(B.tb + tf::fid(w, s) * ws::FRAG + lane * 16) = in.tb[s];
-  if (kNeedQ && q_on) {
+    for (int s = 0; s < 2; ++s)
+      if (2 * s <= w) *reinterpret_cast<bf16x8*>(B.tb + tf::fid(w, s) * ws::FRAG + lane * 16) = in.tb[s];
+  }
+  if (kNeedQ && (kPart < 0 || kPart == 2) && q_on) {
     const u16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
     const bool live = 16 * w + (lane & 15) < len;
     u16x8 qr[4];
@@ -895,7 +914,7 @@ __device__ __forceinline__ void loc_phase1(SegBuf& B, const LocIn& in, int len, 
       *reinterpret_cast<bf16x8*>(B.qg + (w * 4 + s) * ws::FRAG + lane * 16) = qf[s];
     }
   }
-  if (w == 0) {
+  if ((kPart < 0 || kPart == 3) && w == 0) {
     const float G = wave_incl_scan(lane < len ? in.graw : 0.f);  // g = 0 past the chunk's end
     const float gl = __shfl(G, 63, kWave);
     const float eg = expf(G);
@@ -1330,9 +1349,10 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     // the end the last chunk is requested again, unused), which keeps the wait counts exact.
     LocIn ia, ib;
     bf16x8 qf[4], tbu[2];
-    auto load = [&](LocIn& L, int c) __attribute__((always_inline)) {
-      loc_load<need_q>(L, chunk_t0(c), chunk_len(c), kh, h, k, (uint32_t)ks, q, (uint32_t)qs, v, (uint32_t)vs, g, Hv,
-                       tfr(c), knorm + ((int64_t)(chunk_slot0 + c) * Hv + h) * CH, c >= w0);
+    auto load = [&](LocIn& L, int c, auto part) __attribute__((always_inline)) {
+      loc_load<need_q, decltype(part)::value>(L, chunk_t0(c), chunk_len(c), kh, h, k, (uint32_t)ks, q, (uint32_t)qs, v,
+                                              (uint32_t)vs, g, Hv, tfr(c),
+                                              knorm + ((int64_t)(chunk_slot0 + c) * Hv + h) * CH, c >= w0);
     };
     auto phase2 = [&](SegBuf& B, bool q_on) __attribute__((always_inline)) {
       switch (w) {
@@ -1363,8 +1383,26 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     auto step = [&](int c, LocIn& nxt, const LocIn& cur) __attribute__((always_inline)) {  // prepare chunk c + 1 from cur
       if (kNorm) norm_fetch_o(nin, sm.buf[(c + 1) & 1]);  // the chain's outputs of step c - 1, before
                                                           // chunk c + 1's V rows replace them
-      load(nxt, c + 2 < ntot ? c + 2 : ntot - 1);
-      loc_phase1<need_q>(sm.buf[(c + 1) & 1], cur, chunk_len(c + 1), use_l2, c + 1 >= w0, qf);
+      {  // chunk c + 2's load parts interleaved with chunk c + 1's phase-1 parts
+        const int cn = c + 2 < ntot ? c + 2 : ntot - 1;
+        SegBuf& B1 = sm.buf[(c + 1) & 1];
+        const int len1 = chunk_len(c + 1);
+        load(nxt, cn, std::integral_constant<int, 0>{});
+        __builtin_amdgcn_sched_barrier(0);
+        loc_phase1<need_q, 0>(B1, cur, len1, use_l2, c + 1 >= w0, qf);
+        __builtin_amdgcn_sched_barrier(0);
+        load(nxt, cn, std::integral_constant<int, 1>{});
+        __builtin_amdgcn_sched_barrier(0);
+        loc_phase1<need_q, 1>(B1, cur, len1, use_l2, c + 1 >= w0, qf);
+        __builtin_amdgcn_sched_barrier(0);
+        load(nxt, cn, std::integral_constant<int, 2>{});
+        __builtin_amdgcn_sched_barrier(0);
+        loc_phase1<need_q, 2>(B1, cur, len1, use_l2, c + 1 >= w0, qf);
+        __builtin_amdgcn_sched_barrier(0);
+        load(nxt, cn, std::integral_constant<int, 3>{});
+        __builtin_amdgcn_sched_barrier(0);
+        loc_phase1<need_q, 3>(B1, cur, len1, use_l2, c + 1 >= w0, qf);
+      }
       tbu[0] = cur.tb[0];
       tbu[1] = cur.tb[1];
       if (kNorm) {
@@ -1377,8 +1415,8 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     };
     if (ntot > 0) {
       if (kNorm) norm_req_z(-1);  // unused: every step then finds one z request in flight
-      load(ia, 0);
-      load(ib, ntot > 1 ? 1 : 0);
+      load(ia, 0, std::integral_constant<int, -1>{});
+      load(ib, ntot > 1 ? 1 : 0, std::integral_constant<int, -1>{});
       loc_phase1<need_q>(sm.buf[0], ia, chunk_len(0), use_l2, w0 == 0, qf);
       tbu[0] = ia.tb[0];
       tbu[1] = ia.tb[1];
