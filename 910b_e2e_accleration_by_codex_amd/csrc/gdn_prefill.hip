@@ -485,12 +485,6 @@ __device__ __forceinline__ f32x4 rmm(f32x4 aT, f32x4 b, f32x4 acc) {
   acc = __builtin_amdgcn_mfma_f32_16x16x4f32(aT[3], b[3], acc, 0, 0, 0);
   return acc;
 }
-__device__ __forceinline__ f32x4 plus_eye(f32x4 m, int lane) {
-  const int c = lane & 15, g = lane >> 4;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) m[r] += 4 * g + r == c ? 1.f : 0.f;
-  return m;
-}
 // Index of the lower block (a, b), b <= a, of a 4x4 block grid.
 __device__ __forceinline__ constexpr int tri(int a, int b) { return a * (a + 1) / 2 + b; }
 
@@ -506,31 +500,63 @@ __device__ __forceinline__ f32x4 ltr(float* tile, f32x4 m, int lane) {
   return *reinterpret_cast<const f32x4*>(&tile[c * kTrPitch + 4 * g]);
 }
 
+// Lane l's value v from lane n of its row of 16 lanes (DPP row_newbcast).
+template <int N>
+__device__ __forceinline__ float row_bcast(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x150 + N, 0xf, 0xf, true));
+}
+// t[i] += sum_{m < i} row_bcast<m>(x[i]) t[m] for i = 1 .. 15, in order of m.
+template <int I, int M>
+__device__ __forceinline__ void fwd_sub(const float (&x)[16], float (&t)[16]) {
+  if constexpr (I < 16) {
+    if constexpr (M < I) {
+      t[I] = __builtin_fmaf(row_bcast<M>(x[I]), t[M], t[I]);
+      fwd_sub<I, M + 1>(x, t);
+    } else {
+      fwd_sub<I + 1, 0>(x, t);
+    }
+  }
+}
+
 // (I - X)^{-1} for a strictly lower 64x64 X, one wave.  In: XT[tri(a, b)] = Dl(X_ab^T) for every
-// lower block, Xd[a] = Dl(X_aa).  Out: TT[tri(a, b)] = Dl(T_ab^T).  tiles: 4 wave-private transpose
-// tiles.  Same blocking as src/gdn_chunk_fast.py:33-62: the diagonal blocks first, then the blocks
-// below them, T_ij = T_ii sum_{k=j}^{i-1} X_ik T_kj.  A diagonal block's T^T is
-// (I+X^8T)(I+X^4T)(I+X^2T)(I+X^T) (exact for nilpotent X, X^16 = 0; |X_ij| <= 1 keeps the powers far
-// from overflow), applied from the right with the powers X^2, X^4 as left factors; the transposes a
-// product needs as an operand are taken through LDS.
+// lower block, Xd[a] = Dl(X_aa).  Out: TT[tri(a, b)] = Dl(T_ab^T).  tiles: 4 wave-private 16 x 20
+// fp32 LDS tiles.  Same blocking as src/gdn_chunk_fast.py:33-62: the diagonal blocks first, then the
+// blocks below them, T_ij = T_ii sum_{k=j}^{i-1} X_ik T_kj.  The four diagonal blocks are solved at
+// once by forward substitution on the VALU: lane (a, j) = (l / 16, l % 16) holds column j of X_aa
+// and forms column j of T_aa, t_i = [i = j] + sum_{m < i} X_aa[i][m] t_m, with X_aa[i][m] taken
+// from lane m of its row (120 FMAs, in place of 24 products of 16x16 blocks on the fp32 MFMA).
+// Columns go in and out through the tiles (stored transposed: tile a row j = column j of the block).
 __device__ __forceinline__ void reg_inv64(const f32x4 (&XT)[10], const f32x4 (&Xd)[4], f32x4 (&TT)[10], float* tiles,
                                           int lane) {
   const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+  const int c = lane & 15, g = lane >> 4;
   f32x4 TD[6];  // Dl(T_ab) for the blocks of rows 0..2 (tri index < 6)
+  {
 #pragma unroll
-  for (int a = 0; a < 4; ++a) {
-    float* tile = tiles + a * 16 * kTrPitch;
-    const f32x4 X = Xd[a], Xt = XT[tri(a, a)];
-    const f32x4 P2 = rmm(Xt, X, z);
-    const f32x4 P2T = ltr(tile, P2, lane);
-    const f32x4 P4 = rmm(P2T, P2, z);
-    const f32x4 P4T = ltr(tile, P4, lane);
-    f32x4 Q = plus_eye(rmm(P4, P4T, z), lane);  // I + (X^8)^T
-    Q = rmm(P4, Q, Q);
-    Q = rmm(P2, Q, Q);
-    Q = rmm(X, Q, Q);
-    TT[tri(a, a)] = Q;
-    if (a < 3) TD[tri(a, a)] = ltr(tile, Q, lane);
+    for (int a = 0; a < 4; ++a)  // lane (c, g) holds X_aa[4g + r][c]: tile a, row c, columns 4g ..
+      *reinterpret_cast<f32x4*>(&tiles[(16 * a + c) * kTrPitch + 4 * g]) = Xd[a];
+    float x[16], t[16];
+    float* col = &tiles[(16 * g + c) * kTrPitch];  // this lane's column: block g, column c
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(&col[4 * m]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x[4 * m + r] = v[r];
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) t[i] = i == c ? 1.f : 0.f;
+    fwd_sub<1, 0>(x, t);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) *reinterpret_cast<f32x4*>(&col[4 * m]) = f32x4{t[4 * m], t[4 * m + 1], t[4 * m + 2], t[4 * m + 3]};
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {  // Dl(T_aa): T_aa[4g + r][c] = tile a [c][4g + r]; Dl(T_aa^T): tile a [4g + r][c]
+      const float* tile = &tiles[16 * a * kTrPitch];
+      f32x4 tt;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) tt[r] = tile[(4 * g + r) * kTrPitch + c];
+      TT[tri(a, a)] = tt;
+      if (a < 3) TD[tri(a, a)] = *reinterpret_cast<const f32x4*>(&tile[c * kTrPitch + 4 * g]);
+    }
   }
   f32x4 Y;
   // first subdiagonal
