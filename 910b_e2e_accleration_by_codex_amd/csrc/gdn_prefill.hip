@@ -926,10 +926,16 @@ __device__ __forceinline__ void loc_phase1(SegBuf& B, const LocIn& in, int len, 
 #pragma unroll
     for (int s = 0; s < 4; ++s) qr[s] = live ? in.qr[s] : zero;
     if (use_l2) {  // the row's 128 values sit in the 4 lanes c, c + 16, c + 32, c + 48
-      float ss = 0.f;
+      // sum of squares = diagonal of Q Q^T over the tile's 16 rows (4 MFMAs on the fragments in
+      // hand: as a B operand, lane (c, g)'s A fragment is Q^T's).  The products are exact and summed
+      // in fp32, where torch rounds each square to bf16 first: the factor can differ from torch's by
+      // one bf16 ulp on some rows, which only moves outputs (q does not enter the state).
+      f32x4 qq = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < 4; ++s) ss = sumsq_bf16(qr[s], ss);
-      ss = xor32_sum(xor16_sum(ss));
+      for (int s = 0; s < 4; ++s) qq = mma(__builtin_bit_cast(bf16x8, qr[s]), __builtin_bit_cast(bf16x8, qr[s]), qq);
+      const int c16 = lane & 15, g4 = lane >> 4;  // (Q Q^T)[c][c] sits in lane (c, c / 4), element c % 4
+      const float dg = (c16 & 3) == 0 ? qq[0] : (c16 & 3) == 1 ? qq[1] : (c16 & 3) == 2 ? qq[2] : qq[3];
+      const float ss = xor32_sum(xor16_sum(g4 == (c16 >> 2) ? dg : 0.f));
       const float inv = l2norm_inv(ss);
 #pragma unroll
       for (int s = 0; s < 4; ++s) qr[s] = scale_bf16(qr[s], inv);
@@ -943,12 +949,12 @@ __device__ __forceinline__ void loc_phase1(SegBuf& B, const LocIn& in, int len, 
   if ((kPart < 0 || kPart == 3) && w == 0) {
     const float G = wave_incl_scan(lane < len ? in.graw : 0.f);  // g = 0 past the chunk's end
     const float gl = __shfl(G, 63, kWave);
-    const float eg = expf(G);
+    const float eg = __expf(G);  // the hardware exp: within a few fp32 ulp, far below the bf16 roundings
     B.gs[lane] = G;
-    B.dec[lane] = expf(gl - G);
+    B.dec[lane] = __expf(gl - G);
     B.eg[lane] = eg;
     B.egs[lane] = kScale * eg;
-    if (lane == 0) B.gl = expf(gl);
+    if (lane == 0) B.gl = __expf(gl);
   }
 }
 
