@@ -33,7 +33,7 @@ BF16_PEAK = 2.5e15         # flop/s, dense bf16 MFMA
 N_SLOTS, HK, HV, D, KC, LAYERS = 16, 16, 32, 128, 4, 48
 # HBM bytes per decode_fused_kernel launch at this workload, measured with two rocprofv3 --pmc runs
 # (FETCH_SIZE, WRITE_SIZE) scaled by what the counters read for a 256 MiB device copy
-DECODE_TRAFFIC = 70_010_817
+DECODE_TRAFFIC = 69_993_300
 C = (2 * HK + HV) * D
 
 
