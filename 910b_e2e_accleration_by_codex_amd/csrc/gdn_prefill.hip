@@ -1043,8 +1043,22 @@ __device__ __forceinline__ void split_bf16(f32x4 a, f32x4 b, bf16x8& hi, bf16x8&
 // 16-column slices (n = 2 w' + sl), S[sl][i][r] = S[16 i + 4 g + r][16 n + c].
 struct ChainRegs {
   f32x4 S[2][8];
-  bf16x8 hi[2][2], lo[2][2];  // DEC vn, split, carried from part 1 to part 2
+  bf16x8 hi[2][2], lo[2][2];  // DEC vn, split (by part 1, or by part 2 from vn)
+  f32x4 vn[2][4];             // vn carried from part 1 to part 2 when part 2 splits it
 };
+// DEC vn -> hi + lo bf16 (the k-slot ordered B fragments of the update).
+__device__ __forceinline__ void dec_split(const SegBuf& B, f32x4 (&vn)[2][4], ChainRegs& R, int g4) {
+#pragma unroll
+  for (int tb = 0; tb < 4; ++tb) {
+    const f32x4 dec = *reinterpret_cast<const f32x4*>(&B.dec[16 * tb + 4 * g4]);
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl) vn[sl][tb] *= dec;
+  }
+#pragma unroll
+  for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) split_bf16(vn[sl][2 * j], vn[sl][2 * j + 1], R.hi[sl][j], R.lo[sl][j]);
+}
 // The gated RMSNorm of the fused prefill layer (HF Qwen3_5RMSNormGated, modeling_qwen3_5.py, over
 // each (token, value head) row of D = 128), applied to a chunk's outputs before they are stored:
 // out = bf16(w bf16(x rsqrt(mean(x^2) + eps)) silu(z)) with x = bf16(o).  The chain waves leave
@@ -1121,10 +1135,10 @@ __device__ __forceinline__ void norm_store(const NormIn& N, const float (&wt)[8]
 }
 // Chain part 1 for one chunk: U (fp32, from the inverse kernel's T diag(beta) fragments and the V
 // rows), vn = U - W S, the outputs o = diag(scale e^G) Q S + QK vn (kOut), and DEC vn split for part
-// 2.  W S and Q S share the loop over the state's k-blocks j (16 independent accumulators); the LDS
-// fragments of block j + 1 are requested before the products of block j, so their latency hides
-// behind those products.
-template <bool kUseU, bool kOut, bool kNorm = false>
+// 2 (kSplitLate: vn itself, split by part 2).  W S and Q S share the loop over the state's k-blocks j
+// (16 independent accumulators); the LDS fragments of block j + 1 are requested before the products
+// of block j, so their latency hides behind those products.
+template <bool kUseU, bool kOut, bool kNorm, bool kSplitLate>
 __device__ __forceinline__ void chain_part1(const SegBuf& B, ChainRegs& R, uint16_t* __restrict__ out, int64_t t0,
                                             int len, int Hv, int h, int wc, int lane_in) {
   using namespace pf;
@@ -1249,21 +1263,22 @@ __device__ __forceinline__ void chain_part1(const SegBuf& B, ChainRegs& R, uint1
         }
     }
   }
-  // DEC vn -> hi + lo bf16 (k-slot ordered B fragments of the update)
+  if (kSplitLate) {
 #pragma unroll
-  for (int tb = 0; tb < 4; ++tb) {
-    const f32x4 dec = *reinterpret_cast<const f32x4*>(&B.dec[16 * tb + 4 * g4]);
+    for (int sl = 0; sl < 2; ++sl)
 #pragma unroll
-    for (int sl = 0; sl < 2; ++sl) acc[sl][tb] *= dec;
+      for (int tb = 0; tb < 4; ++tb) R.vn[sl][tb] = acc[sl][tb];
+  } else {
+    dec_split(B, acc, R, g4);
   }
-#pragma unroll
-  for (int sl = 0; sl < 2; ++sl)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) split_bf16(acc[sl][2 * j], acc[sl][2 * j + 1], R.hi[sl][j], R.lo[sl][j]);
 }
 // Chain part 2: S' = e^{G_last} S + K^T (DEC vn), K^T straight from the K rows (exact in bf16).  For
 // each token half j the hi terms of all 16 accumulators go first, then the lo terms; the K^T
-// fragments of half 1 are requested before the products of half 0.
+// fragments of half 1 are requested before the products of half 0.  kSplitLate: DEC vn is formed and
+// split here, while the K^T fragments arrive (the step's first half then holds less of the chain's
+// work: the choice for the output pass without the fused norm, whose local waves finish the first
+// half earlier than the chain).
+template <bool kSplitLate>
 __device__ __forceinline__ void chain_part2(const SegBuf& B, ChainRegs& R, int lane_in) {
   using namespace pf;
   int lane;
@@ -1274,6 +1289,7 @@ __device__ __forceinline__ void chain_part2(const SegBuf& B, ChainRegs& R, int l
   for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int i = 0; i < 8; ++i) kt[j][i] = __builtin_bit_cast(bf16x8, frag_tr_kperm(B.K, LDK, 32 * j, 16 * i, lane));
+  if (kSplitLate) dec_split(B, R.vn, R, lane >> 4);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -1509,12 +1525,13 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     lds_barrier();
     for (int c = 0; c < ntot; ++c) {
       const SegBuf& B = sm.buf[c & 1];
+      constexpr bool late = kNorm == 0;
       if (kPass == 0 && c >= w0)
-        chain_part1<true, true, kNorm != 0>(B, R, out, chunk_t0(c), chunk_len(c), Hv, h, wc, lane);
-      else if (mode != kSegA) chain_part1<true, false>(B, R, out, 0, 0, Hv, h, wc, lane);
-      else chain_part1<false, false>(B, R, out, 0, 0, Hv, h, wc, lane);
+        chain_part1<true, true, kNorm != 0, late>(B, R, out, chunk_t0(c), chunk_len(c), Hv, h, wc, lane);
+      else if (mode != kSegA) chain_part1<true, false, false, late>(B, R, out, 0, 0, Hv, h, wc, lane);
+      else chain_part1<false, false, false, late>(B, R, out, 0, 0, Hv, h, wc, lane);
       lds_barrier();
-      chain_part2(B, R, lane);
+      chain_part2<late>(B, R, lane);
       lds_barrier();
     }
     // the state after the segment
