@@ -1059,12 +1059,12 @@ __device__ __forceinline__ void dec_split(const SegBuf& B, f32x4 (&vn)[2][4], Ch
 #pragma unroll
     for (int j = 0; j < 2; ++j) split_bf16(vn[sl][2 * j], vn[sl][2 * j + 1], R.hi[sl][j], R.lo[sl][j]);
 }
-// The gated RMSNorm of the fused prefill layer (HF Qwen3_5RMSNormGated, modeling_qwen3_5.py, over
-// each (token, value head) row of D = 128), applied to a chunk's outputs before they are stored:
-// out = bf16(w bf16(x rsqrt(mean(x^2) + eps)) silu(z)) with x = bf16(o).  The chain waves leave
-// bf16(o) in the chunk's V tile (each wave in its own 32 columns, which only it reads); during the
-// next step, local wave w reads rows 16 w .. 16 w + 15 of it just before it writes the next V rows
-// there, and normalises, gates and stores them.  Lane mapping, sum order (8 columns in a lane, then
+// The output pass's stores.  The chain waves leave bf16(o) in the chunk's V tile (each wave in its
+// own 32 columns, which only it reads); during the next step, local wave w reads rows 16 w .. 16 w +
+// 15 of it just before it writes the next V rows there, and stores them, 16 bytes per lane -- as
+// they are (kNorm 0), or through the gated RMSNorm of the fused prefill layer (HF
+// Qwen3_5RMSNormGated, modeling_qwen3_5.py, over each (token, value head) row of D = 128):
+// out = bf16(w bf16(x rsqrt(mean(x^2) + eps)) silu(z)) with x = bf16(o).  Lane mapping, sum order (8 columns in a lane, then
 // the butterfly over 16 lanes) and roundings are gated_rmsnorm128_kernel's: the result is the same,
 // bit for bit, as that kernel applied to the stored outputs.
 typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
@@ -1110,6 +1110,10 @@ __device__ __forceinline__ void norm_store(const NormIn& N, const float (&wt)[8]
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = 4 * tq + i;
+    if (kNorm == 0) {  // no norm: the outputs as they are
+      if (row < len) *reinterpret_cast<u16x8*>(ob + ((int64_t)row * Hv * D + 8 * fb)) = N.o[i];
+      continue;
+    }
     float xf[8], ss = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -1134,13 +1138,12 @@ __device__ __forceinline__ void norm_store(const NormIn& N, const float (&wt)[8]
   }
 }
 // Chain part 1 for one chunk: U (fp32, from the inverse kernel's T diag(beta) fragments and the V
-// rows), vn = U - W S, the outputs o = diag(scale e^G) Q S + QK vn (kOut), and DEC vn split for part
-// 2 (kSplitLate: vn itself, split by part 2).  W S and Q S share the loop over the state's k-blocks j
+// rows), vn = U - W S, the outputs o = diag(scale e^G) Q S + QK vn (kOut: left in bf16 in the V tile
+// for the local waves to store), and DEC vn split for part 2 (kSplitLate: vn itself, split by part 2).  W S and Q S share the loop over the state's k-blocks j
 // (16 independent accumulators); the LDS fragments of block j + 1 are requested before the products
 // of block j, so their latency hides behind those products.
-template <bool kUseU, bool kOut, bool kNorm, bool kSplitLate>
-__device__ __forceinline__ void chain_part1(const SegBuf& B, ChainRegs& R, uint16_t* __restrict__ out, int64_t t0,
-                                            int len, int Hv, int h, int wc, int lane_in) {
+template <bool kUseU, bool kOut, bool kSplitLate>
+__device__ __forceinline__ void chain_part1(const SegBuf& B, ChainRegs& R, int wc, int lane_in) {
   using namespace pf;
   int lane;
   asm volatile("v_mov_b32 %0, %1" : "=v"(lane) : "v"(lane_in));
@@ -1239,29 +1242,16 @@ __device__ __forceinline__ void chain_part1(const SegBuf& B, ChainRegs& R, uint1
         O[tb][0] = mma(vb[0][jj], kq[tf::fid(tb, jj)], O[tb][0]);
         O[tb][1] = mma(vb[1][jj], kq[tf::fid(tb, jj)], O[tb][1]);
       }
-    if (kNorm) {  // bf16(o) into this wave's 32 columns of the V tile (read by no other wave):
-                  // the local waves normalise, gate and store the rows one step later
-      uint16_t* vrow = const_cast<uint16_t*>(B.V) + c16 * LDK + 32 * wc + 4 * g4;
+    // bf16(o) into this wave's 32 columns of the V tile (read by no other wave): the local waves
+    // store the rows one step later (through the gated norm when asked), off the chain's path
+    uint16_t* vrow = const_cast<uint16_t*>(B.V) + c16 * LDK + 32 * wc + 4 * g4;
 #pragma unroll
-      for (int tb = 0; tb < 4; ++tb)
+    for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
-        for (int sl = 0; sl < 2; ++sl) {
-          const u32x2v pk = {f2bf2(O[tb][sl][0], O[tb][sl][1]), f2bf2(O[tb][sl][2], O[tb][sl][3])};
-          *reinterpret_cast<u32x2v*>(vrow + 16 * tb * LDK + 16 * sl) = pk;
-        }
-    } else {
-      uint16_t* orow = out + ((t0 + c16) * Hv + h) * D + 32 * wc + 4 * g4;
-      const int64_t tile = (int64_t)16 * Hv * D;
-#pragma unroll
-      for (int tb = 0; tb < 4; ++tb)
-        if (16 * tb + c16 < len) {
-#pragma unroll
-          for (int sl = 0; sl < 2; ++sl) {
-            const u32x2v pk = {f2bf2(O[tb][sl][0], O[tb][sl][1]), f2bf2(O[tb][sl][2], O[tb][sl][3])};
-            *reinterpret_cast<u32x2v*>(orow + tb * tile + 16 * sl) = pk;
-          }
-        }
-    }
+      for (int sl = 0; sl < 2; ++sl) {
+        const u32x2v pk = {f2bf2(O[tb][sl][0], O[tb][sl][1]), f2bf2(O[tb][sl][2], O[tb][sl][3])};
+        *reinterpret_cast<u32x2v*>(vrow + 16 * tb * LDK + 16 * sl) = pk;
+      }
   }
   if (kSplitLate) {
 #pragma unroll
@@ -1410,7 +1400,7 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
         default: loc_phase2<3, need_q>(B, qf, tbu, q_on); break;
       }
     };
-    // gated norm (kNorm): the weight of columns 8 fb .. 8 fb + 7, and chunk j's outputs (j >= w0)
+    // the stores of chunk j's outputs (j >= w0); the gated norm's weight of columns 8 fb .. 8 fb + 7
     float wt[8];
     if (kNorm) {
 #pragma unroll
@@ -1429,7 +1419,7 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
                         j >= w0 ? chunk_len(j) : 0);
     };
     auto step = [&](int c, LocIn& nxt, const LocIn& cur) __attribute__((always_inline)) {  // prepare chunk c + 1 from cur
-      if (kNorm) norm_fetch_o(nin, sm.buf[(c + 1) & 1]);  // the chain's outputs of step c - 1, before
+      if (kPass == 0) norm_fetch_o(nin, sm.buf[(c + 1) & 1]);  // the chain's outputs of step c - 1, before
                                                           // chunk c + 1's V rows replace them
       {  // chunk c + 2's load parts interleaved with chunk c + 1's phase-1 parts
         const int cn = c + 2 < ntot ? c + 2 : ntot - 1;
@@ -1453,10 +1443,8 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
       }
       tbu[0] = cur.tb[0];
       tbu[1] = cur.tb[1];
-      if (kNorm) {
-        norm_out(c - 1);
-        norm_req_z(c);
-      }
+      if (kPass == 0) norm_out(c - 1);
+      if (kNorm) norm_req_z(c);
       lds_barrier();
       phase2(sm.buf[(c + 1) & 1], c + 1 >= w0);
       lds_barrier();
@@ -1479,14 +1467,14 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     }
     if (c + 1 < ntot) step(c, ia, ib);
     if (ntot > 0) {  // the chain's last step: nothing left to prepare (the outputs of the last two chunks)
-      if (kNorm && ntot > 1) {
+      if (kPass == 0 && ntot > 1) {
         norm_fetch_o(nin, sm.buf[ntot & 1]);
         norm_out(ntot - 2);
       }
       if (kNorm) norm_req_z(ntot - 1);
       lds_barrier();
       lds_barrier();
-      if (kNorm) {
+      if (kPass == 0) {
         norm_fetch_o(nin, sm.buf[(ntot - 1) & 1]);
         norm_out(ntot - 1);
       }
@@ -1527,9 +1515,9 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
       const SegBuf& B = sm.buf[c & 1];
       constexpr bool late = kNorm == 0;
       if (kPass == 0 && c >= w0)
-        chain_part1<true, true, kNorm != 0, late>(B, R, out, chunk_t0(c), chunk_len(c), Hv, h, wc, lane);
-      else if (mode != kSegA) chain_part1<true, false, false, late>(B, R, out, 0, 0, Hv, h, wc, lane);
-      else chain_part1<false, false, false, late>(B, R, out, 0, 0, Hv, h, wc, lane);
+        chain_part1<true, true, late>(B, R, wc, lane);
+      else if (mode != kSegA) chain_part1<true, false, late>(B, R, wc, lane);
+      else chain_part1<false, false, late>(B, R, wc, lane);
       lds_barrier();
       chain_part2<late>(B, R, lane);
       lds_barrier();
@@ -1800,18 +1788,6 @@ extern "C" int gdn_unit_lower_inv(const float* X, float* T, int64_t batch, int n
 }
 
 namespace {
-// Compute units of the current device (cached per device).
-int device_cus() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cached[dev]) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
-}
 // Segment length (chunks) for a call: about sg::kTargetItems (segment, value head) items, at least
 // sg::kMinSeg chunks per segment.
 int64_t seg_len(int64_t total_chunks, int Hv) {
