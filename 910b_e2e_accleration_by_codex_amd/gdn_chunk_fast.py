@@ -307,8 +307,8 @@ def gdn_prefill_core(mixed_qkv, z, a, b, conv_weight, A_log, dt_bias, norm_weigh
     (src/cb_tp.py:153-181 fresh, :230-263 continued): conv prefill + SiLU, split q|k|v, gating,
     chunked rule with l2norm (value head h reads key head h // r, no repeat_interleave copy),
     gated RMSNorm (fused into the rule's output kernel).  mixed_qkv [T, C] bf16 (pre-conv),
-    z [T, Hv*d], a, b [T, Hv]; cu_seqlens int [n_seq+1] (host or device) | Varlen | None -- host lengths, as the scheduler
-    holds them, keep the call free of GPU waits; conv_history [n_seq, C, K] | None;
+    z [T, Hv*d], a, b [T, Hv]; cu_seqlens int [n_seq+1] (host or device) | Varlen | None -- host
+    lengths, as the scheduler holds them, keep the call free of GPU waits; conv_history [n_seq, C, K] | None;
     initial_state [n_seq, Hv, d, d] | None.
     Returns (core [T, Hv*d] bf16, conv_state [n_seq, C, K] bf16, rec_state [n_seq, Hv, d, d] fp32).
     Slot rows (the engine's state buffers, src/cb_engine.py:198-205, src/cb_tp.py:178-179, :256-262):
