@@ -1623,6 +1623,11 @@ __global__ __launch_bounds__(256) void seg_combine_kernel(SegTable tab, int Hv, 
 // sequence leaves (its last K inputs) is written afterwards by conv_state_capture_kernel, so the
 // history may be the same slot rows the state goes to.
 constexpr int kConvRun = 8;
+// A bijection on [0, n): b -> (b % 8) * (n / 8) + b / 8 below 8 (n / 8), the identity above.
+__device__ __forceinline__ int64_t xcd_range_item(int64_t b, int64_t n) {
+  const int64_t per = n / 8;
+  return b >= 8 * per ? b : (b % 8) * per + b / 8;
+}
 __device__ __forceinline__ int find_seq(const int32_t* cu, int nseq, int64_t p) {
   int lo = 0, hi = nseq - 1;  // last sequence whose start <= p (skips empty ones)
   while (lo < hi) {
@@ -1641,9 +1646,13 @@ __global__ __launch_bounds__(256) void conv_prefill_kernel(const uint16_t* __res
                                                            const int32_t* __restrict__ rows, int n_rows,
                                                            uint16_t* __restrict__ out, int64_t total_tokens,
                                                            const int32_t* __restrict__ cu, int nseq, int seq_len,
-                                                           int C) {
-  const int cg = blockIdx.x * blockDim.x + threadIdx.x;  // 8-channel group
-  const int64_t p0 = (int64_t)blockIdx.y * kConvRun;
+                                                           int C, int nblk) {
+  // Workgroup b covers item xcd_range_item(b): token run item / nblk, channel block item % nblk.  The
+  // 8 XCDs take workgroups b % 8 in turn; the remap gives each XCD a contiguous range of items, so
+  // the K - 1 input rows a run shares with the previous run are read again from that XCD's L2.
+  const int64_t item = xcd_range_item(blockIdx.x, gridDim.x);
+  const int cg = (int)(item % nblk) * blockDim.x + threadIdx.x;  // 8-channel group
+  const int64_t p0 = item / nblk * kConvRun;
   if (8 * cg >= C) return;
   const int c0 = 8 * cg;
   const int nrun = total_tokens - p0 < kConvRun ? (int)(total_tokens - p0) : kConvRun;
@@ -2014,13 +2023,16 @@ extern "C" int gdn_conv_prefill_rows(const void* x, int64_t x_stride, const void
                 "gdn_conv_prefill: C and the row stride must be multiples of 8 with 16-byte aligned rows");
     GDN_REQUIRE(total_tokens < (1ll << 31), "gdn_conv_prefill: too many tokens");
     GDN_REQUIRE(aligned(weight, 16), "gdn_conv_prefill: weight must be 16-byte aligned");
-    dim3 grid((unsigned)((C / 8 + 255) / 256), (unsigned)((total_tokens + kConvRun - 1) / kConvRun));
+    const int nblk = (C / 8 + 255) / 256;
+    const int64_t nwg = (int64_t)nblk * ((total_tokens + kConvRun - 1) / kConvRun);
+    GDN_REQUIRE(nwg < (1ll << 31), "gdn_conv_prefill: grid too large");
+    const unsigned grid = (unsigned)nwg;
 #define GDN_CONV_PREFILL(KK)                                                                                    \
   case KK:                                                                                                     \
     conv_prefill_kernel<KK><<<grid, 256, 0, s>>>((const uint16_t*)x, x_stride, (const uint16_t*)weight,          \
                                                  (const uint16_t*)bias, (const uint16_t*)history, state_rows,      \
                                                  n_rows, (uint16_t*)out, total_tokens, cu_seqlens, nseq, seq_len, \
-                                                 C);                                                           \
+                                                 C, nblk);                                                     \
     break;
     switch (K) {
       GDN_CONV_PREFILL(1)
