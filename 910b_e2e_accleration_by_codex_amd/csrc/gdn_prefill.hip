@@ -765,9 +765,10 @@ __global__ __launch_bounds__(pf::NT, 2) void inv_kernel(const uint16_t* __restri
 // about one (segment, value head) pair per compute unit exists).  One workgroup per (segment, value
 // head) walks its segment's chunks.  Per chunk, its 4 local waves build the operand fragments
 // described above in LDS (K and q masked and l2-normalised, the decay, Q K^T, -W from the K rows and
-// the inverse kernel's T diag(beta) scaled by e^G), and its 4 chain waves advance 32 columns of the
-// fp32 state each and write their outputs.  Only the inverse kernel's records (6 KiB of T
-// fragments per (chunk, value head)) pass through memory besides the inputs and outputs.
+// the inverse kernel's T diag(beta) scaled by e^G) and store the previous chunk's outputs, and its 4
+// chain waves advance 32 columns of the fp32 state each and leave their outputs in LDS.  Only the
+// inverse kernel's records (6 KiB of T fragments and 256 B of K row factors per (chunk, value head))
+// pass through memory besides the inputs and outputs.
 // A segment other than the first of its sequence needs its true initial state: the state after
 // segment j is S_{j+1} = A_j S_j + B_j, with A_j the segment's linear map (the chain run from the
 // identity with U = 0) and B_j its affine part (run from zero).  A summary pass computes A_j and
@@ -1305,8 +1306,8 @@ __device__ __forceinline__ void chain_part2(const SegBuf& B, ChainRegs& R, int l
 // segment in its transition slot), writing o and, at a sequence's last segment, the final state.
 // pass 1 (summary): two workgroups per (transition slot, value head): B (from zero, with U) and A
 // (from the identity, without U), written into the slot; A is skipped when negligible.
-// Waves 0-3 (local) prepare chunk c+1's operands in one buffer while waves 4-7 (chain) run chunk c
-// from the other: two LDS barriers a chunk, met by both roles.
+// Waves 0-3 (local) prepare chunk c+1's operands in one buffer (and store chunk c-1's outputs) while
+// waves 4-7 (chain) run chunk c from the other: two LDS barriers a chunk, met by both roles.
 template <typename BetaT, typename OutT, int kPass, int kNorm = 0>
 __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     const uint16_t* __restrict__ q, int64_t qs, const uint16_t* __restrict__ k, int64_t ks, const uint16_t* __restrict__ v,
