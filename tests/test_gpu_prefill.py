@@ -225,13 +225,14 @@ def test_chunk_prefill_seq_len_bound_matches_unknown(gdn, oracle, dev, lens):
             assert rel_l2(res[1][1][i].cpu(), s_ref[i]) <= STATE_TOL, f"sequence {i}"
 
 
-@pytest.mark.parametrize("w_dtype", [torch.bfloat16, torch.float32])
-def test_chunk_prefill_fused_gated_norm_matches_two_calls(gdn, oracle, dev, w_dtype):
+@pytest.mark.parametrize("w_dtype,decay", [(torch.bfloat16, 0.1), (torch.float32, 0.1), (torch.bfloat16, 0.005)])
+def test_chunk_prefill_fused_gated_norm_matches_two_calls(gdn, oracle, dev, w_dtype, decay):
     """The rule with its output rows passed through the gated RMSNorm in the output kernel against
     the rule followed by gdn_gated_rmsnorm: equal final states and bit-identical outputs (same sum
     order and roundings), and against the oracle.  Packed sequences of 1300, 5 and 900 tokens (at
-    4 value heads, segments of 4 chunks: later segments start from a warm-up or the exact path; a
-    one-chunk sequence), gate rows from a wider tensor (row stride > Hv * d)."""
+    4 value heads, segments of 4 chunks; at decay 0.1 later segments start from a warm-up, at 0.005
+    from the exact summaries and combine; a one-chunk sequence), gate rows from a wider tensor (row
+    stride > Hv * d)."""
     import importlib
     from conftest import PKG_NAME
     engine = importlib.import_module(PKG_NAME + ".cb_engine")
@@ -239,7 +240,7 @@ def test_chunk_prefill_fused_gated_norm_matches_two_calls(gdn, oracle, dev, w_dt
     lens = [1300, 5, 900]
     T = sum(lens)
     cu = torch.tensor([0, 1300, 1305, 2205], dtype=torch.int32)
-    q, k, v, g, beta, _ = _gdn_inputs(T, Hk, Hv, seed=41, state=False)
+    q, k, v, g, beta, _ = _gdn_inputs(T, Hk, Hv, seed=41, state=False, decay=decay)
     s0 = 0.02 * torch.randn(3, Hv, D, D, generator=torch.Generator().manual_seed(42))
     g_ = torch.Generator().manual_seed(43)
     zw = torch.randn(T, Hv * D + 256, generator=g_).to(torch.bfloat16).to(dev)
