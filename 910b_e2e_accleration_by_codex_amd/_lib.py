@@ -33,6 +33,7 @@ _SIGNATURES = {
     "gdn_chunk_prefill": ([_P, _L, _P, _L, _P, _L, _P, _P, _I, _P, _P, _P, _L, _P, _P, _L, _I, _I, _I, _I,
                            _I, _I, _I, _P, _L, _P], _I),
     "gdn_chunk_prefill_workspace_bytes": ([_L, _I, _I], _L),
+    "gdn_prefill_layer_workspace_bytes": ([_L, _L, _I, _I, _I, _I], _L),
     "gdn_decode_linear_workspace_bytes": ([_I, _L, _L], _L),
     "gdn_decode_linear": ([_P, _L, _P, _L, _P, _L, _I, _L, _L, _P, _L, _P], _I),
     "gdn_decode_linear_packed_elems": ([_L, _L], _L),
@@ -55,6 +56,8 @@ _SIGNATURES = {
                                 _I, _I, _I, _I, _I, _I, _P, _L, _P], _I),
     "gdn_chunk_prefill_rows_gated": ([_P, _L, _P, _L, _P, _L, _P, _P, _I, _P, _P, _P, _I, _P, _L, _P, _P, _L,
                                       _I, _I, _I, _I, _I, _I, _I, _P, _L, _P, _I, _F, _P, _L, _P], _I),
+    "gdn_prefill_layer_rows": ([_P, _L, _P, _L, _P, _P, _L, _P, _P, _P, _P, _P, _I, _F, _P, _P, _P, _P, _P, _I,
+                                _P, _L, _P, _P, _L, _I, _I, _I, _I, _I, _I, _P, _L, _P], _I),
     "gdn_chunk_prefill_noalloc": ([_P, _L, _P, _L, _P, _L, _P, _P, _I, _P, _P, _P, _I, _P, _L, _P, _P, _L, _I,
                                    _I, _I, _I, _I, _I, _I, _P], _I),
     "gdn_conv_prefill_rows": ([_P, _L, _P, _P, _P, _P, _P, _P, _I, _L, _P, _I, _I, _I, _I, _P], _I),

@@ -404,8 +404,8 @@ __device__ __forceinline__ void block_scan256(int* part, int t) {
 constexpr int kLptMaxLen = 2048;
 // seg0 (nseq + 1 entries) from the chunk prefix sums, and order[] (segments by decreasing chunk
 // count; ties in any order): one workgroup.
-__global__ __launch_bounds__(256) void seg_table_kernel(const int32_t* __restrict__ chunk0, int nseq, int L,
-                                                       int32_t* __restrict__ seg0, int32_t* __restrict__ order) {
+__device__ void seg_table_wg(const int32_t* __restrict__ chunk0, int nseq, int L, int32_t* __restrict__ seg0,
+                             int32_t* __restrict__ order) {
   __shared__ int part[256];
   __shared__ int hist[kLptMaxLen + 1];
   const int t = threadIdx.x;
@@ -456,6 +456,10 @@ __global__ __launch_bounds__(256) void seg_table_kernel(const int32_t* __restric
     const int n = chunk0[s + 1] - chunk0[s], ns = n <= L ? 1 : (n + L - 1) / L, j0 = seg0[s];
     for (int idx = 0; idx < ns; ++idx) order[atomicAdd(&hist[n - idx * L < L ? n - idx * L : L], 1)] = j0 + idx;
   }
+}
+__global__ __launch_bounds__(256) void seg_table_kernel(const int32_t* __restrict__ chunk0, int nseq, int L,
+                                                       int32_t* __restrict__ seg0, int32_t* __restrict__ order) {
+  seg_table_wg(chunk0, nseq, L, seg0, order);
 }
 
 // ============================================================================================
@@ -1639,19 +1643,13 @@ __device__ __forceinline__ int find_seq(const int32_t* cu, int nseq, int64_t p) 
   return lo;
 }
 
+// The work of one conv workgroup: token run item / nblk, channel block item % nblk.
 template <int K>
-__global__ __launch_bounds__(256) void conv_prefill_kernel(const uint16_t* __restrict__ x, int64_t x_stride,
-                                                           const uint16_t* __restrict__ weight,
-                                                           const uint16_t* __restrict__ bias,
-                                                           const uint16_t* __restrict__ history,
-                                                           const int32_t* __restrict__ rows, int n_rows,
-                                                           uint16_t* __restrict__ out, int64_t total_tokens,
-                                                           const int32_t* __restrict__ cu, int nseq, int seq_len,
-                                                           int C, int nblk) {
-  // Workgroup b covers item xcd_range_item(b): token run item / nblk, channel block item % nblk.  The
-  // 8 XCDs take workgroups b % 8 in turn; the remap gives each XCD a contiguous range of items, so
-  // the K - 1 input rows a run shares with the previous run are read again from that XCD's L2.
-  const int64_t item = xcd_range_item(blockIdx.x, gridDim.x);
+__device__ __forceinline__ void conv_run(int64_t item, int nblk, const uint16_t* __restrict__ x, int64_t x_stride,
+                                         const uint16_t* __restrict__ weight, const uint16_t* __restrict__ bias,
+                                         const uint16_t* __restrict__ history, const int32_t* __restrict__ rows,
+                                         int n_rows, uint16_t* __restrict__ out, int64_t total_tokens,
+                                         const int32_t* __restrict__ cu, int nseq, int seq_len, int C) {
   const int cg = (int)(item % nblk) * blockDim.x + threadIdx.x;  // 8-channel group
   const int64_t p0 = item / nblk * kConvRun;
   if (8 * cg >= C) return;
@@ -1726,16 +1724,30 @@ __global__ __launch_bounds__(256) void conv_prefill_kernel(const uint16_t* __res
     *reinterpret_cast<u16x8*>(out + p * (int64_t)C + c0) = o;
   }
 }
+// Workgroup b covers item xcd_range_item(b).  The 8 XCDs take workgroups b % 8 in turn; the remap
+// gives each XCD a contiguous range of items, so the K - 1 input rows a run shares with the
+// previous run are read again from that XCD's L2.
+template <int K>
+__global__ __launch_bounds__(256) void conv_prefill_kernel(const uint16_t* __restrict__ x, int64_t x_stride,
+                                                           const uint16_t* __restrict__ weight,
+                                                           const uint16_t* __restrict__ bias,
+                                                           const uint16_t* __restrict__ history,
+                                                           const int32_t* __restrict__ rows, int n_rows,
+                                                           uint16_t* __restrict__ out, int64_t total_tokens,
+                                                           const int32_t* __restrict__ cu, int nseq, int seq_len,
+                                                           int C, int nblk) {
+  conv_run<K>(xcd_range_item(blockIdx.x, gridDim.x), nblk, x, x_stride, weight, bias, history, rows, n_rows, out,
+              total_tokens, cu, nseq, seq_len, C);
+}
 
 // The decode conv state each sequence leaves: its last K inputs, the front filled from its history
 // row (or zeros) when the sequence is shorter than K -- an empty sequence keeps its history.  One
 // thread per (sequence, channel) reads its old row entries before writing them, so `history` and
 // `state` may be the same slot rows.
-__global__ void conv_state_capture_kernel(const uint16_t* __restrict__ x, int64_t x_stride,
-                                          const uint16_t* history, const int32_t* __restrict__ hist_rows,
-                                          uint16_t* state, const int32_t* __restrict__ state_rows, int n_rows,
-                                          const int32_t* __restrict__ cu, int nseq, int seq_len, int C, int K) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void capture_one(int64_t i, const uint16_t* __restrict__ x, int64_t x_stride,
+                                            const uint16_t* history, const int32_t* __restrict__ hist_rows,
+                                            uint16_t* state, const int32_t* __restrict__ state_rows, int n_rows,
+                                            const int32_t* __restrict__ cu, int nseq, int seq_len, int C, int K) {
   if (i >= (int64_t)nseq * C) return;
   const int s = (int)(i / C), c = (int)(i % C);
   const int orow = state_row(state_rows, n_rows, s);
@@ -1751,19 +1763,89 @@ __global__ void conv_state_capture_kernel(const uint16_t* __restrict__ x, int64_
   }
   for (int j = 0; j < K; ++j) state[((int64_t)orow * C + c) * K + j] = win[j];
 }
+__global__ void conv_state_capture_kernel(const uint16_t* __restrict__ x, int64_t x_stride,
+                                          const uint16_t* history, const int32_t* __restrict__ hist_rows,
+                                          uint16_t* state, const int32_t* __restrict__ state_rows, int n_rows,
+                                          const int32_t* __restrict__ cu, int nseq, int seq_len, int C, int K) {
+  capture_one((int64_t)blockIdx.x * blockDim.x + threadIdx.x, x, x_stride, history, hist_rows, state, state_rows,
+              n_rows, cu, nseq, seq_len, C, K);
+}
 
 // ============================================================================================
 // Gating: beta = sigmoid(b) in bf16, g = -exp(A_log) * softplus(a + dt_bias) in fp32.
 // ============================================================================================
-__global__ void gating_kernel(const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, int64_t ab_stride,
-                              const float* __restrict__ A_log, const float* __restrict__ dt_bias,
-                              uint16_t* __restrict__ beta, float* __restrict__ g, int64_t rows, int Hv) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void gating_one(int64_t i, const uint16_t* __restrict__ a, const uint16_t* __restrict__ b,
+                                           int64_t ab_stride, const float* __restrict__ A_log,
+                                           const float* __restrict__ dt_bias, uint16_t* __restrict__ beta,
+                                           float* __restrict__ g, int64_t rows, int Hv) {
   if (i >= rows * Hv) return;
   const int64_t r = i / Hv;
   const int h = (int)(i % Hv);
   beta[i] = f2bf(sigmoid_f(bf2f(b[r * ab_stride + h])));
   g[i] = -expf(A_log[h]) * softplus_f(bf2f(a[r * ab_stride + h]) + dt_bias[h]);
+}
+__global__ void gating_kernel(const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, int64_t ab_stride,
+                              const float* __restrict__ A_log, const float* __restrict__ dt_bias,
+                              uint16_t* __restrict__ beta, float* __restrict__ g, int64_t rows, int Hv) {
+  gating_one((int64_t)blockIdx.x * blockDim.x + threadIdx.x, a, b, ab_stride, A_log, dt_bias, beta, g, rows, Hv);
+}
+
+// ============================================================================================
+// The GDN prefill layer's first launch: the conv of every token run and, as further workgroups of
+// the same grid, the decode conv state capture (when the history rows are not the state rows), the
+// gating and the chunked rule's segment table.  None reads what another writes, so one launch does
+// the work of four (each of which costs a few microseconds of launch however little it computes).
+// ============================================================================================
+struct PrologueArgs {
+  const uint16_t* x;  // conv: [tokens, C] input rows
+  int64_t x_stride;
+  const uint16_t* weight;
+  const uint16_t* bias;
+  const uint16_t* history;
+  const int32_t* rows;
+  int n_rows;
+  uint16_t* conv_out;  // [tokens, C]
+  int64_t total_tokens;
+  const int32_t* cu;
+  int nseq, seq_len, C, nblk;
+  int64_t n_conv;      // conv workgroups (first in the grid)
+  uint16_t* state;     // capture: [n_rows, C, K] state rows
+  int64_t n_cap;       // capture workgroups (0: captured by a launch of its own)
+  const uint16_t* a;   // gating
+  const uint16_t* b;
+  int64_t ab_stride;
+  const float* A_log;
+  const float* dt_bias;
+  uint16_t* beta;
+  float* g;
+  int Hv;
+  int64_t n_gate;
+  const int32_t* chunk0;  // segment table (one workgroup, last in the grid)
+  int L;
+  int32_t* seg0;
+  int32_t* order;
+  int table;
+};
+template <int K>
+__global__ __launch_bounds__(256) void layer_prologue_kernel(PrologueArgs P) {
+  int64_t b = blockIdx.x;
+  if (b < P.n_conv) {  // the conv workgroups' remap keeps their XCD (workgroup b runs on XCD b % 8)
+    conv_run<K>(xcd_range_item(b, P.n_conv), P.nblk, P.x, P.x_stride, P.weight, P.bias, P.history, P.rows, P.n_rows,
+                P.conv_out, P.total_tokens, P.cu, P.nseq, P.seq_len, P.C);
+    return;
+  }
+  b -= P.n_conv;
+  if (b < P.n_cap) {
+    capture_one(b * 256 + threadIdx.x, P.x, P.x_stride, P.history, P.rows, P.state, P.rows, P.n_rows, P.cu, P.nseq,
+                P.seq_len, P.C, K);
+    return;
+  }
+  b -= P.n_cap;
+  if (b < P.n_gate) {
+    gating_one(b * 256 + threadIdx.x, P.a, P.b, P.ab_stride, P.A_log, P.dt_bias, P.beta, P.g, P.total_tokens, P.Hv);
+    return;
+  }
+  if (P.table) seg_table_wg(P.chunk0, P.nseq, P.L, P.seg0, P.order);
 }
 
 // Workspace of gdn_chunk_prefill_noalloc: one static array per device (host code reaches it only
@@ -1841,7 +1923,8 @@ int chunk_prefill_impl(const void* q, int64_t q_stride, const void* k, int64_t k
                        float* final_state, const int32_t* state_rows, int n_rows, void* out, int64_t total_tokens,
                        const int32_t* cu_seqlens, const int32_t* seq_chunk0, int64_t total_chunks, int nseq,
                        int seq_len, int Hqk, int Hv, int D, int in_dtype, int use_qk_l2norm, void* workspace,
-                       int64_t workspace_bytes, void* stream, const GateArgs& gate, int norm_mode) {
+                       int64_t workspace_bytes, void* stream, const GateArgs& gate, int norm_mode,
+                       bool table_built = false) {
   GDN_REQUIRE(state_rows ? n_rows >= 0 : n_rows == nseq,
               "gdn_chunk_prefill: without state_rows, n_rows must equal nseq");
   GDN_REQUIRE(q && k && v && g && beta && out, "gdn_chunk_prefill: null input/output pointer");
@@ -1885,7 +1968,7 @@ int chunk_prefill_impl(const void* q, int64_t q_stride, const void* k, int64_t k
   GDN_REQUIRE(nseg_max * Hv < (1ll << 31) && lay.nslots * Hv * 2 < (1ll << 31) && (int64_t)nseq * Hv * 64 < (1ll << 31) &&
                   total_chunks * Hv < (1ll << 33),
               "gdn_chunk_prefill: grid too large");
-  if (cu_seqlens) {
+  if (cu_seqlens && !table_built) {
     seg_table_kernel<<<1, 256, 0, st>>>(seq_chunk0, nseq, (int)lay.L, seg0, order);
     int rc = check_launch("gdn_chunk_prefill(table)");
     if (rc) return rc;
@@ -2076,4 +2159,138 @@ extern "C" int gdn_gating(const void* a, const void* b, int64_t ab_stride, const
   gating_kernel<<<(unsigned)((n + 255) / 256), 256, 0, (hipStream_t)stream>>>(
       (const uint16_t*)a, (const uint16_t*)b, ab_stride, A_log, dt_bias, (uint16_t*)beta_out, g_out, rows, Hv);
   return check_launch("gdn_gating");
+}
+
+namespace {
+// Byte offsets of the layer workspace: the conv output [tokens, C] bf16, beta [tokens, Hv] bf16,
+// g [tokens, Hv] fp32, then the chunked rule's workspace.
+struct LayerLayout {
+  int64_t off_beta, off_g, off_chunk, bytes;
+};
+LayerLayout layer_layout(int64_t total_tokens, int64_t total_chunks, int nseq, int Hk, int Hv, int D) {
+  auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
+  const int64_t C = (int64_t)(2 * Hk + Hv) * D;
+  LayerLayout l;
+  l.off_beta = up(total_tokens * C * 2);
+  l.off_g = l.off_beta + up(total_tokens * Hv * 2);
+  l.off_chunk = l.off_g + up(total_tokens * Hv * 4);
+  l.bytes = l.off_chunk + gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hv);
+  return l;
+}
+}  // namespace
+
+extern "C" int64_t gdn_prefill_layer_workspace_bytes(int64_t total_tokens, int64_t total_chunks, int nseq, int Hk,
+                                                     int Hv, int D) {
+  if (total_tokens < 0 || total_chunks < 0 || nseq < 0 || Hk <= 0 || Hv <= 0 || D <= 0) return -1;
+  return layer_layout(total_tokens, total_chunks, nseq, Hk, Hv, D).bytes;
+}
+
+extern "C" int gdn_prefill_layer_rows(const void* mixed, int64_t mixed_stride, const void* z, int64_t z_stride,
+                                      const void* a, const void* b, int64_t ab_stride, const void* conv_w,
+                                      const void* conv_b, const float* A_log, const float* dt_bias,
+                                      const void* norm_w, int norm_w_dtype, float eps, const void* conv_history,
+                                      void* conv_state, const float* initial_state, float* final_state,
+                                      const int32_t* state_rows, int n_rows, void* out, int64_t total_tokens,
+                                      const int32_t* cu_seqlens, const int32_t* seq_chunk0, int64_t total_chunks,
+                                      int nseq, int seq_len, int Hk, int Hv, int D, int K, void* workspace,
+                                      int64_t workspace_bytes, void* stream) {
+  clear_error();
+  GDN_REQUIRE(mixed && z && a && b && conv_w && A_log && dt_bias && norm_w && conv_state && out,
+              "gdn_prefill_layer: null pointer");
+  GDN_REQUIRE(Hk > 0 && Hv > 0 && Hv % Hk == 0 && nseq >= 0 && total_tokens >= 0 && total_chunks >= 0,
+              "gdn_prefill_layer: bad sizes");
+  GDN_SUPPORT(D == pf::D, "gdn_prefill_layer: head dim %d unsupported (needs %d)", D, pf::D);
+  GDN_SUPPORT(K >= 1 && K <= 8, "gdn_prefill_layer: conv kernel size %d unsupported", K);
+  GDN_REQUIRE(norm_w_dtype == GDN_BF16 || norm_w_dtype == GDN_F32, "gdn_prefill_layer: bad norm weight dtype");
+  GDN_REQUIRE(state_rows ? n_rows >= 0 : n_rows == nseq,
+              "gdn_prefill_layer: without state_rows, n_rows must equal nseq");
+  GDN_REQUIRE(cu_seqlens || (int64_t)nseq * seq_len == total_tokens,
+              "gdn_prefill_layer: nseq*seq_len != total_tokens without cu_seqlens");
+  const int C = (2 * Hk + Hv) * D;
+  GDN_REQUIRE(mixed_stride >= C && mixed_stride % 8 == 0 && aligned(mixed, 16) && aligned(conv_w, 16),
+              "gdn_prefill_layer: mixed rows and the conv weight must be 16-byte aligned");
+  GDN_REQUIRE(aligned(z, 16) && z_stride % 8 == 0 && z_stride >= (int64_t)Hv * D,
+              "gdn_prefill_layer: gate rows must be 16-byte aligned and hold Hv * D values");
+  GDN_REQUIRE(total_tokens < (1ll << 31), "gdn_prefill_layer: too many tokens");
+  const LayerLayout lay = layer_layout(total_tokens, total_chunks, nseq, Hk, Hv, D);
+  GDN_REQUIRE(workspace && aligned(workspace, 256) && workspace_bytes >= lay.bytes,
+              "gdn_prefill_layer: workspace missing, misaligned or smaller than %lld bytes", (long long)lay.bytes);
+  if (nseq == 0) return GDN_OK;
+  hipStream_t st = (hipStream_t)stream;
+  uint8_t* work = (uint8_t*)workspace;
+  uint16_t* conv_out = (uint16_t*)work;
+  uint16_t* beta = (uint16_t*)(work + lay.off_beta);
+  float* g = (float*)(work + lay.off_g);
+  uint8_t* chunk_ws = work + lay.off_chunk;
+  // one launch for the conv, the gating, the segment table and (when the history rows are not the
+  // state rows) the conv state capture
+  const bool cap_fused = !conv_history || conv_history != conv_state;
+  const SegLayout seg = seg_layout(total_chunks, nseq, Hv);
+  PrologueArgs P{};
+  P.x = (const uint16_t*)mixed;
+  P.x_stride = mixed_stride;
+  P.weight = (const uint16_t*)conv_w;
+  P.bias = (const uint16_t*)conv_b;
+  P.history = (const uint16_t*)conv_history;
+  P.rows = state_rows;
+  P.n_rows = n_rows;
+  P.conv_out = conv_out;
+  P.total_tokens = total_tokens;
+  P.cu = cu_seqlens;
+  P.nseq = nseq;
+  P.seq_len = seq_len;
+  P.C = C;
+  P.nblk = (C / 8 + 255) / 256;
+  P.n_conv = (int64_t)P.nblk * ((total_tokens + kConvRun - 1) / kConvRun);
+  P.state = (uint16_t*)conv_state;
+  P.n_cap = cap_fused ? ((int64_t)nseq * C + 255) / 256 : 0;
+  P.a = (const uint16_t*)a;
+  P.b = (const uint16_t*)b;
+  P.ab_stride = ab_stride;
+  P.A_log = A_log;
+  P.dt_bias = dt_bias;
+  P.beta = beta;
+  P.g = g;
+  P.Hv = Hv;
+  P.n_gate = (total_tokens * Hv + 255) / 256;
+  P.chunk0 = seq_chunk0;
+  P.L = (int)seg.L;
+  P.seg0 = (int32_t*)chunk_ws;
+  P.order = (int32_t*)(chunk_ws + seg.off_order);
+  P.table = cu_seqlens ? 1 : 0;
+  const int64_t grid = P.n_conv + P.n_cap + P.n_gate + P.table;
+  GDN_REQUIRE(grid < (1ll << 31), "gdn_prefill_layer: grid too large");
+  if (grid > 0) {
+#define GDN_PROLOGUE(KK) \
+  case KK:               \
+    layer_prologue_kernel<KK><<<(unsigned)grid, 256, 0, st>>>(P); \
+    break;
+    switch (K) {
+      GDN_PROLOGUE(1)
+      GDN_PROLOGUE(2)
+      GDN_PROLOGUE(3)
+      GDN_PROLOGUE(4)
+      GDN_PROLOGUE(5)
+      GDN_PROLOGUE(6)
+      GDN_PROLOGUE(7)
+      GDN_PROLOGUE(8)
+    }
+#undef GDN_PROLOGUE
+    int rc = check_launch("gdn_prefill_layer(prologue)");
+    if (rc) return rc;
+  }
+  if (!cap_fused) {  // the history rows are the state rows: the capture reads them after the conv has
+    const int64_t n = (int64_t)nseq * C;
+    conv_state_capture_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(
+        (const uint16_t*)mixed, mixed_stride, (const uint16_t*)conv_history, state_rows, (uint16_t*)conv_state,
+        state_rows, n_rows, cu_seqlens, nseq, seq_len, C, K);
+    int rc = check_launch("gdn_prefill_layer(state)");
+    if (rc) return rc;
+  }
+  const GateArgs gate{(const uint16_t*)z, z_stride, norm_w, eps};
+  const int64_t kd = (int64_t)Hk * D;
+  return chunk_prefill_impl(conv_out, C, conv_out + kd, C, conv_out + 2 * kd, C, g, beta, GDN_BF16, initial_state,
+                            final_state, state_rows, n_rows, out, total_tokens, cu_seqlens, seq_chunk0, total_chunks,
+                            nseq, seq_len, Hk, Hv, D, GDN_BF16, 1, chunk_ws, workspace_bytes - lay.off_chunk, stream,
+                            gate, norm_w_dtype == GDN_BF16 ? 1 : 2, cu_seqlens != nullptr);
 }

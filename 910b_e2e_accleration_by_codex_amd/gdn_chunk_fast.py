@@ -306,7 +306,8 @@ def gdn_prefill_core(mixed_qkv, z, a, b, conv_weight, A_log, dt_bias, norm_weigh
     """GDN prefill layer between in_proj_* and out_proj for one or more packed prompts
     (src/cb_tp.py:153-181 fresh, :230-263 continued): conv prefill + SiLU, split q|k|v, gating,
     chunked rule with l2norm (value head h reads key head h // r, no repeat_interleave copy),
-    gated RMSNorm (fused into the rule's output kernel).  mixed_qkv [T, C] bf16 (pre-conv),
+    gated RMSNorm (fused into the rule's output kernel) -- one call of gdn_prefill_layer_rows, whose
+    first launch does the conv, the conv state, the gating and the segment table.  mixed_qkv [T, C] bf16 (pre-conv),
     z [T, Hv*d], a, b [T, Hv]; cu_seqlens int [n_seq+1] (host or device) | Varlen | None -- host
     lengths, as the scheduler holds them, keep the call free of GPU waits; conv_history [n_seq, C, K] | None;
     initial_state [n_seq, Hv, d, d] | None.
@@ -316,38 +317,75 @@ def gdn_prefill_core(mixed_qkv, z, a, b, conv_weight, A_log, dt_bias, norm_weigh
     [N, C, K] bf16 and ``rec_slots`` [N, Hv, d, d] fp32, and with ``continuation`` each sequence
     first reads its conv history and initial state from those rows (a later chunk of a prompt);
     then (core, conv_slots, rec_slots) is returned and conv_history / initial_state are not used."""
+    _lib.require_cuda(mixed_qkv, z, a, b, conv_weight, A_log, dt_bias, norm_weight, conv_history, initial_state)
     T, C = mixed_qkv.shape
     Hk, Hv, D = num_k_heads, num_v_heads, head_dim
     if C != (2 * Hk + Hv) * D:
         raise ValueError(f"gdn_prefill_core: C={C} != (2*{Hk}+{Hv})*{D}")
-    w = conv_weight.reshape(C, -1)
-    if cu_seqlens is not None:  # checked and uploaded once for both kernels
-        cu_seqlens = _varlen(cu_seqlens, 1, T, mixed_qkv.device)
+    if chunk_size != CHUNK or D != 128:
+        raise ValueError(f"gdn_prefill_core: supports {SUPPORTED}")
+    if mixed_qkv.dtype != torch.bfloat16 or conv_weight.dtype != torch.bfloat16:
+        raise TypeError("gdn_prefill_core: mixed_qkv and conv_weight must be bfloat16")
+    dev = mixed_qkv.device
+    w = conv_weight.reshape(C, -1).contiguous()
+    K = w.shape[1]
+    if cu_seqlens is not None:  # checked and uploaded once (a Varlen is used as it is)
+        vl = _varlen(cu_seqlens, 1, T, dev)
+        cu, chunk0, nseq, seq_len, total_chunks = vl.cu, vl.seq_chunk0, vl.nseq, vl.max_len, vl.total_chunks
+    else:
+        cu, chunk0, nseq, seq_len, total_chunks = None, None, 1, T, (T + CHUNK - 1) // CHUNK
+    x = mixed_qkv
+    if x.stride(1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
+        x = x.contiguous()
+    z2 = z.reshape(T, -1)
+    if z2.dtype != torch.bfloat16 or z2.shape[1] < Hv * D:
+        raise ValueError(f"gdn_prefill_core: z must be bf16 [{T}, >= {Hv * D}]")
+    if z2.stride(1) != 1 or z2.stride(0) % 8 or z2.data_ptr() % 16:
+        z2 = z2.contiguous()
+    a2, b2 = a.reshape(T, Hv), b.reshape(T, Hv)
+    if a2.stride() != b2.stride() or a2.stride(-1) != 1:
+        a2, b2 = a2.contiguous(), b2.contiguous()
+    bias = conv_bias.to(torch.bfloat16).contiguous() if conv_bias is not None else None
+    A32, dt32 = A_log.to(torch.float32).contiguous(), dt_bias.to(torch.float32).contiguous()
+    nw = norm_weight.contiguous()
+    if tuple(nw.shape) != (D,) or nw.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"gdn_prefill_core: norm weight must be bf16 or fp32 [{D}]")
     if slots is not None:
         if conv_slots is None or rec_slots is None:
             raise ValueError("gdn_prefill_core: slots needs conv_slots and rec_slots")
-        if conv_slots.shape[0] != rec_slots.shape[0]:
+        n_rows = conv_slots.shape[0]
+        if rec_slots.shape[0] != n_rows:
             raise ValueError("gdn_prefill_core: conv_slots and rec_slots must hold the same slot count")
-        nseq = cu_seqlens.nseq if cu_seqlens is not None else 1
-        slots = slots if isinstance(slots, Rows) else Rows(slots, nseq, conv_slots.shape[0], mixed_qkv.device)
-        conv_out, conv_state = causal_conv1d_prefill(mixed_qkv.t().unsqueeze(0), w, conv_bias,
-                                                     conv_slots if continuation else None, cu_seqlens,
-                                                     state_rows=slots, state_out=conv_slots)
+        if (tuple(conv_slots.shape) != (n_rows, C, K) or conv_slots.dtype != torch.bfloat16
+                or not conv_slots.is_contiguous() or conv_slots.device != dev):
+            raise ValueError(f"gdn_prefill_core: conv_slots must be a contiguous bf16 [{n_rows},{C},{K}] slot buffer")
+        if (tuple(rec_slots.shape) != (n_rows, Hv, D, D) or rec_slots.dtype != torch.float32
+                or not rec_slots.is_contiguous() or rec_slots.device != dev):
+            raise ValueError(f"gdn_prefill_core: rec_slots must be a contiguous fp32 [{n_rows},{Hv},{D},{D}] "
+                             "slot buffer")
+        rows = _check_rows(slots, nseq, n_rows, dev)
+        hist, conv_state = (conv_slots if continuation else None), conv_slots
+        init, rec = (rec_slots if continuation else None), rec_slots
     else:
-        conv_out, conv_state = causal_conv1d_prefill(mixed_qkv.t().unsqueeze(0), w, conv_bias,
-                                                     conv_history, cu_seqlens)
-    qkv = conv_out[0].t()                                     # [T, C] view, dense rows
-    kd = Hk * D
-    q = qkv[:, :kd].reshape(1, T, Hk, D)
-    k = qkv[:, kd:2 * kd].reshape(1, T, Hk, D)
-    v = qkv[:, 2 * kd:].reshape(1, T, Hv, D)
-    beta, g = gdn_gating(a.reshape(1, T, Hv), b.reshape(1, T, Hv), A_log, dt_bias)
-    gate = (z.reshape(T, -1), norm_weight, eps)
-    if slots is not None:
-        core, rec = chunk_gated_delta_rule(q, k, v, g, beta, chunk_size, rec_slots if continuation else None,
-                                           True, True, cu_seqlens=cu_seqlens, state_rows=slots,
-                                           final_state_out=rec_slots, norm_gate=gate)
-    else:
-        core, rec = chunk_gated_delta_rule(q, k, v, g, beta, chunk_size, initial_state, True, True,
-                                           cu_seqlens=cu_seqlens, norm_gate=gate)
-    return core.reshape(T, Hv * D), conv_state, rec
+        n_rows, rows = nseq, None
+        hist = None
+        if conv_history is not None:
+            if tuple(conv_history.shape) != (nseq, C, K):
+                raise ValueError(f"gdn_prefill_core: conv_history must be [{nseq},{C},{K}]")
+            hist = conv_history.to(torch.bfloat16).contiguous()
+        conv_state = torch.empty(nseq, C, K, dtype=torch.bfloat16, device=dev)
+        init = None
+        if initial_state is not None:
+            if tuple(initial_state.shape) != (nseq, Hv, D, D):
+                raise ValueError(f"gdn_prefill_core: initial_state must be [{nseq},{Hv},{D},{D}]")
+            init = initial_state.to(torch.float32).contiguous()
+        rec = torch.empty(nseq, Hv, D, D, dtype=torch.float32, device=dev)
+    core = torch.empty(T, Hv * D, dtype=torch.bfloat16, device=dev)
+    wbytes = int(_lib.lib().gdn_prefill_layer_workspace_bytes(T, total_chunks, nseq, Hk, Hv, D))
+    work = torch.empty(max(wbytes, 1), dtype=torch.uint8, device=dev)
+    _lib.call("gdn_prefill_layer_rows", _lib.ptr(x), x.stride(0), _lib.ptr(z2), z2.stride(0), _lib.ptr(a2),
+              _lib.ptr(b2), a2.stride(0), _lib.ptr(w), _lib.ptr(bias), _lib.ptr(A32), _lib.ptr(dt32), _lib.ptr(nw),
+              _lib.dtype_code(nw), float(eps), _lib.ptr(hist), _lib.ptr(conv_state), _lib.ptr(init), _lib.ptr(rec),
+              _lib.ptr(rows), n_rows, _lib.ptr(core), T, _lib.ptr(cu), _lib.ptr(chunk0), total_chunks, nseq,
+              seq_len, Hk, Hv, D, K, _lib.ptr(work), wbytes, _lib.stream_of(mixed_qkv))
+    return core, conv_state, rec

@@ -264,6 +264,38 @@ int gdn_conv_prefill_rows(const void* x, int64_t x_stride, const void* weight, c
                           int seq_len, int C, int K, void* stream);
 
 /*
+ * The whole GDN prefill layer between the input projections and out_proj, for one or more packed
+ * prompts (src/cb_tp.py:153-181 fresh, :230-263 continued): conv prefill + SiLU and the decode conv
+ * state (gdn_conv_prefill_rows), split q | k | v, gating (gdn_gating), the chunked rule with l2norm,
+ * value head h reading key head h / (Hv / Hk), and the gated RMSNorm
+ * (gdn_chunk_prefill_rows_gated) -- the same results as those calls in a row, bit for bit, in
+ * fewer launches: the conv, the state capture, the gating and the segment table share one launch.
+ *   mixed [total_tokens, (2 Hk + Hv) D] bf16 (pre-conv in_proj_qkv rows), row stride mixed_stride
+ *     (a multiple of 8, 16-byte aligned);  z [total_tokens, >= Hv D] bf16, row stride z_stride (a
+ *     multiple of 8, 16-byte aligned);  a, b [total_tokens, Hv] bf16, row stride ab_stride;
+ *   conv_w [(2 Hk + Hv) D, K] bf16 (16-byte aligned), conv_b [(2 Hk + Hv) D] bf16 or NULL;
+ *   A_log, dt_bias [Hv] fp32;  norm_w [D] (norm_w_dtype GDN_BF16 or GDN_F32), eps;
+ *   conv_history / conv_state: [n_rows, C, K] bf16 with state_rows (slot rows, as
+ *     gdn_conv_prefill_rows; may be the same buffer), else [nseq, C, K]; conv_history NULL = zero;
+ *   initial_state / final_state: [n_rows or nseq, Hv, D, D] fp32 as gdn_chunk_prefill_rows;
+ *   out [total_tokens, Hv D] bf16 (the normed core);  cu_seqlens, seq_chunk0, total_chunks, nseq,
+ *     seq_len as gdn_chunk_prefill;  D = 128, K <= 8;
+ *   workspace: gdn_prefill_layer_workspace_bytes(total_tokens, total_chunks, nseq, Hk, Hv, D) bytes,
+ *     256-byte aligned (the conv output, beta and g, then the chunked rule's workspace).
+ */
+int64_t gdn_prefill_layer_workspace_bytes(int64_t total_tokens, int64_t total_chunks, int nseq, int Hk,
+                                          int Hv, int D);
+int gdn_prefill_layer_rows(const void* mixed, int64_t mixed_stride, const void* z, int64_t z_stride,
+                           const void* a, const void* b, int64_t ab_stride, const void* conv_w,
+                           const void* conv_b, const float* A_log, const float* dt_bias,
+                           const void* norm_w, int norm_w_dtype, float eps, const void* conv_history,
+                           void* conv_state, const float* initial_state, float* final_state,
+                           const int32_t* state_rows, int n_rows, void* out, int64_t total_tokens,
+                           const int32_t* cu_seqlens, const int32_t* seq_chunk0, int64_t total_chunks,
+                           int nseq, int seq_len, int Hk, int Hv, int D, int K, void* workspace,
+                           int64_t workspace_bytes, void* stream);
+
+/*
  * Decode-step projections: out[M, N] = x[M, K] W[N, K]^T, M <= 16 rows (one token per slot), bf16 x,
  * W (nn.Linear weight layout [out_features, in_features]) and out, fp32 accumulation.  Replaces the
  * GDN layer's in_proj_qkv / in_proj_z / in_proj_b / in_proj_a and out_proj calls of the decode step

@@ -130,3 +130,67 @@ def test_decode_masked_slots(gdn, oracle, dev):
                                  Hk, Hv, D)
     assert rel_l2(o[act], o_o) <= OUT_TOL
     assert torch.equal(cs[act].cpu(), c_o) and rel_l2(rs[act], r_o) <= STATE_TOL
+
+
+def _composed_layer(gdn, mixed, z, a, b, cw, A_log, dt, nw, cu, hist=None, init=None, rows=None, conv_slots=None,
+                    rec_slots=None, cont=False):
+    """The prefill layer as separate calls: conv prefill, gating, the chunked rule with the fused norm."""
+    T = mixed.shape[0]
+    if rows is not None:
+        conv_out, conv_state = gdn.causal_conv1d_prefill(mixed.t().unsqueeze(0), cw, None,
+                                                         conv_slots if cont else None, cu, state_rows=rows,
+                                                         state_out=conv_slots)
+    else:
+        conv_out, conv_state = gdn.causal_conv1d_prefill(mixed.t().unsqueeze(0), cw, None, hist, cu)
+    qkv = conv_out[0].t()
+    kd = Hk * D
+    q, k, v = (qkv[:, :kd].reshape(1, T, Hk, D), qkv[:, kd:2 * kd].reshape(1, T, Hk, D),
+               qkv[:, 2 * kd:].reshape(1, T, Hv, D))
+    beta, g = gdn.gdn_gating(a.reshape(1, T, Hv), b.reshape(1, T, Hv), A_log, dt)
+    if rows is not None:
+        core, rec = gdn.chunk_gated_delta_rule(q, k, v, g, beta, 64, rec_slots if cont else None, True, True,
+                                               cu_seqlens=cu, state_rows=rows, final_state_out=rec_slots,
+                                               norm_gate=(z, nw, 1e-6))
+    else:
+        core, rec = gdn.chunk_gated_delta_rule(q, k, v, g, beta, 64, init, True, True, cu_seqlens=cu,
+                                               norm_gate=(z, nw, 1e-6))
+    return core.reshape(T, Hv * D), conv_state, rec
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["fresh", "history", "slots_continued"])
+def test_prefill_layer_entry_matches_separate_calls(gdn, dev, mode):
+    """gdn_prefill_core (one gdn_prefill_layer_rows call: conv, conv state, gating and segment table
+    in one launch) against the same layer as separate calls, bit for bit: outputs, conv states and
+    recurrent states.  Packed prompts of 300, 1, 0 and 777 tokens; fresh (zero history), with an
+    explicit conv history and initial states, and through slot rows continuing a previous chunk
+    (history rows = state rows: the conv state is captured by a launch of its own)."""
+    lens = [300, 1, 0, 777]
+    cu = torch.tensor([0, 300, 301, 301, 1078], dtype=torch.int32)
+    T = 1078
+    mixed, z, a, b = (t.to(dev) for t in _layer_inputs(T, 61))
+    cw, A_log, dt, nw = (t.to(dev) for t in _params(62))
+    g_ = torch.Generator().manual_seed(63)
+    if mode == "slots_continued":
+        N = 6
+        slots = torch.tensor([4, 0, 2, 5], dtype=torch.int32)
+        cs0 = torch.randn(N, C, K, generator=g_).to(torch.bfloat16).to(dev)
+        rs0 = (0.02 * torch.randn(N, Hv, D, D, generator=g_)).to(dev)
+        cs1, rs1 = cs0.clone(), rs0.clone()
+        o1, c1, r1 = gdn.gdn_prefill_core(mixed, z, a, b, cw, A_log, dt, nw, Hk, Hv, D, cu_seqlens=cu, slots=slots,
+                                          conv_slots=cs1, rec_slots=rs1, continuation=True)
+        cs2, rs2 = cs0.clone(), rs0.clone()
+        o2, c2, r2 = _composed_layer(gdn, mixed, z, a, b, cw, A_log, dt, nw, cu.to(dev), rows=slots,
+                                     conv_slots=cs2, rec_slots=rs2, cont=True)
+    else:
+        hist = init = None
+        if mode == "history":
+            hist = torch.randn(len(lens), C, K, generator=g_).to(torch.bfloat16).to(dev)
+            init = (0.02 * torch.randn(len(lens), Hv, D, D, generator=g_)).to(dev)
+        o1, c1, r1 = gdn.gdn_prefill_core(mixed, z, a, b, cw, A_log, dt, nw, Hk, Hv, D, cu_seqlens=cu,
+                                          conv_history=hist, initial_state=init)
+        o2, c2, r2 = _composed_layer(gdn, mixed, z, a, b, cw, A_log, dt, nw, cu.to(dev), hist=hist, init=init)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
+    assert torch.equal(c1, c2)
+    assert torch.equal(r1, r2)
