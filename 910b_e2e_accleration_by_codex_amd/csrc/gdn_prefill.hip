@@ -1792,8 +1792,8 @@ __global__ void gating_kernel(const uint16_t* __restrict__ a, const uint16_t* __
 
 // ============================================================================================
 // The GDN prefill layer's first launch: the conv of every token run and, as further workgroups of
-// the same grid, the decode conv state capture (when the history rows are not the state rows), the
-// gating and the chunked rule's segment table.  None reads what another writes, so one launch does
+// the same grid, the chunked rule's segment table, the decode conv state capture (when the history
+// rows are not the state rows) and the gating.  None reads what another writes, so one launch does
 // the work of four (each of which costs a few microseconds of launch however little it computes).
 // ============================================================================================
 struct PrologueArgs {
@@ -1826,26 +1826,34 @@ struct PrologueArgs {
   int32_t* order;
   int table;
 };
+// Grid order: the segment table, the capture and the gating first (so they run beside the conv
+// instead of after it), padded to a multiple of 8 workgroups, then the conv.
+__host__ __device__ __forceinline__ int64_t prologue_pre(const PrologueArgs& P) {
+  return (P.table + P.n_cap + P.n_gate + 7) / 8 * 8;
+}
 template <int K>
 __global__ __launch_bounds__(256) void layer_prologue_kernel(PrologueArgs P) {
   int64_t b = blockIdx.x;
-  if (b < P.n_conv) {  // the conv workgroups' remap keeps their XCD (workgroup b runs on XCD b % 8)
+  const int64_t pre = prologue_pre(P);
+  if (b >= pre) {  // the conv workgroups' remap keeps their XCD (workgroup b runs on XCD b % 8, and pre % 8 == 0)
+    b -= pre;
     conv_run<K>(xcd_range_item(b, P.n_conv), P.nblk, P.x, P.x_stride, P.weight, P.bias, P.history, P.rows, P.n_rows,
                 P.conv_out, P.total_tokens, P.cu, P.nseq, P.seq_len, P.C);
     return;
   }
-  b -= P.n_conv;
+  if (b < P.table) {
+    seg_table_wg(P.chunk0, P.nseq, P.L, P.seg0, P.order);
+    return;
+  }
+  b -= P.table;
   if (b < P.n_cap) {
     capture_one(b * 256 + threadIdx.x, P.x, P.x_stride, P.history, P.rows, P.state, P.rows, P.n_rows, P.cu, P.nseq,
                 P.seq_len, P.C, K);
     return;
   }
   b -= P.n_cap;
-  if (b < P.n_gate) {
+  if (b < P.n_gate)
     gating_one(b * 256 + threadIdx.x, P.a, P.b, P.ab_stride, P.A_log, P.dt_bias, P.beta, P.g, P.total_tokens, P.Hv);
-    return;
-  }
-  if (P.table) seg_table_wg(P.chunk0, P.nseq, P.L, P.seg0, P.order);
 }
 
 // Workspace of gdn_chunk_prefill_noalloc: one static array per device (host code reaches it only
@@ -2258,7 +2266,7 @@ extern "C" int gdn_prefill_layer_rows(const void* mixed, int64_t mixed_stride, c
   P.seg0 = (int32_t*)chunk_ws;
   P.order = (int32_t*)(chunk_ws + seg.off_order);
   P.table = cu_seqlens ? 1 : 0;
-  const int64_t grid = P.n_conv + P.n_cap + P.n_gate + P.table;
+  const int64_t grid = prologue_pre(P) + P.n_conv;
   GDN_REQUIRE(grid < (1ll << 31), "gdn_prefill_layer: grid too large");
   if (grid > 0) {
 #define GDN_PROLOGUE(KK) \
