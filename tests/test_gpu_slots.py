@@ -133,15 +133,15 @@ def test_decode_masked_slots(gdn, oracle, dev):
 
 
 def _composed_layer(gdn, mixed, z, a, b, cw, A_log, dt, nw, cu, hist=None, init=None, rows=None, conv_slots=None,
-                    rec_slots=None, cont=False):
+                    rec_slots=None, cont=False, bias=None):
     """The prefill layer as separate calls: conv prefill, gating, the chunked rule with the fused norm."""
     T = mixed.shape[0]
     if rows is not None:
-        conv_out, conv_state = gdn.causal_conv1d_prefill(mixed.t().unsqueeze(0), cw, None,
+        conv_out, conv_state = gdn.causal_conv1d_prefill(mixed.t().unsqueeze(0), cw, bias,
                                                          conv_slots if cont else None, cu, state_rows=rows,
                                                          state_out=conv_slots)
     else:
-        conv_out, conv_state = gdn.causal_conv1d_prefill(mixed.t().unsqueeze(0), cw, None, hist, cu)
+        conv_out, conv_state = gdn.causal_conv1d_prefill(mixed.t().unsqueeze(0), cw, bias, hist, cu)
     qkv = conv_out[0].t()
     kd = Hk * D
     q, k, v = (qkv[:, :kd].reshape(1, T, Hk, D), qkv[:, kd:2 * kd].reshape(1, T, Hk, D),
@@ -158,19 +158,24 @@ def _composed_layer(gdn, mixed, z, a, b, cw, A_log, dt, nw, cu, hist=None, init=
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("mode", ["fresh", "history", "slots_continued"])
+@pytest.mark.parametrize("mode", ["fresh", "history", "history_f32_norm_bias", "slots_continued"])
 def test_prefill_layer_entry_matches_separate_calls(gdn, dev, mode):
     """gdn_prefill_core (one gdn_prefill_layer_rows call: conv, conv state, gating and segment table
     in one launch) against the same layer as separate calls, bit for bit: outputs, conv states and
     recurrent states.  Packed prompts of 300, 1, 0 and 777 tokens; fresh (zero history), with an
-    explicit conv history and initial states, and through slot rows continuing a previous chunk
-    (history rows = state rows: the conv state is captured by a launch of its own)."""
+    explicit conv history and initial states (also with an fp32 norm weight and a conv bias), and
+    through slot rows continuing a previous chunk (history rows = state rows: the conv state is
+    captured by a launch of its own)."""
     lens = [300, 1, 0, 777]
     cu = torch.tensor([0, 300, 301, 301, 1078], dtype=torch.int32)
     T = 1078
     mixed, z, a, b = (t.to(dev) for t in _layer_inputs(T, 61))
     cw, A_log, dt, nw = (t.to(dev) for t in _params(62))
     g_ = torch.Generator().manual_seed(63)
+    bias = None
+    if mode == "history_f32_norm_bias":
+        nw = nw.float() + 0.01
+        bias = (0.1 * torch.randn(C, generator=g_)).to(torch.bfloat16).to(dev)
     if mode == "slots_continued":
         N = 6
         slots = torch.tensor([4, 0, 2, 5], dtype=torch.int32)
@@ -184,12 +189,13 @@ def test_prefill_layer_entry_matches_separate_calls(gdn, dev, mode):
                                      conv_slots=cs2, rec_slots=rs2, cont=True)
     else:
         hist = init = None
-        if mode == "history":
+        if mode != "fresh":
             hist = torch.randn(len(lens), C, K, generator=g_).to(torch.bfloat16).to(dev)
             init = (0.02 * torch.randn(len(lens), Hv, D, D, generator=g_)).to(dev)
         o1, c1, r1 = gdn.gdn_prefill_core(mixed, z, a, b, cw, A_log, dt, nw, Hk, Hv, D, cu_seqlens=cu,
-                                          conv_history=hist, initial_state=init)
-        o2, c2, r2 = _composed_layer(gdn, mixed, z, a, b, cw, A_log, dt, nw, cu.to(dev), hist=hist, init=init)
+                                          conv_history=hist, initial_state=init, conv_bias=bias)
+        o2, c2, r2 = _composed_layer(gdn, mixed, z, a, b, cw, A_log, dt, nw, cu.to(dev), hist=hist, init=init,
+                                     bias=bias)
     torch.cuda.synchronize()
     assert torch.equal(o1, o2)
     assert torch.equal(c1, c2)
