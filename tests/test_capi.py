@@ -28,7 +28,8 @@ def test_header_declares_entry_points():
                  "gdn_chunk_prefill", "gdn_conv_prefill", "gdn_gating", "gdn_unit_lower_inv",
                  "gdn_decode_fused_masked", "gdn_chunk_prefill_rows", "gdn_conv_prefill_rows",
                  "gdn_decode_linear", "gdn_decode_linear_workspace_bytes", "gdn_decode_linear_pack",
-                 "gdn_decode_linear_packed", "gdn_add_rmsnorm"):
+                 "gdn_decode_linear_packed", "gdn_add_rmsnorm", "gdn_chunk_prefill_rows_gated",
+                 "gdn_prefill_layer_rows", "gdn_prefill_layer_workspace_bytes", "gdn_chunk_prefill_noalloc"):
         assert name in syms
 
 
@@ -91,3 +92,28 @@ def test_version_limits_and_error_path(lib):
     with pytest.raises(lib.GDNError):
         lib.call("gdn_gated_rmsnorm", None, 0, None, 0, None, 1, None, 1, 128, ctypes.c_float(1e-6), None)
 
+
+
+def test_prefill_layer_entry_host_checks(lib):
+    """gdn_prefill_layer_rows validates on the host before any HIP call: its workspace holds the conv
+    output, beta and g besides the chunked rule's workspace; null pointers, an unsupported head dim,
+    misaligned gate rows and a short workspace are refused with their codes."""
+    h = lib.lib()
+    T, nch, nseq, Hk, Hv, D, K = 1000, 20, 2, 16, 32, 128, 4
+    C = (2 * Hk + Hv) * D
+    need = h.gdn_prefill_layer_workspace_bytes(T, nch, nseq, Hk, Hv, D)
+    assert need % 256 == 0
+    assert need >= T * C * 2 + T * Hv * 2 + T * Hv * 4 + h.gdn_chunk_prefill_workspace_bytes(nch, nseq, Hv)
+    p = ctypes.c_void_p(256)
+    eps = ctypes.c_float(1e-6)
+
+    def call(mixed=p, z=p, D_=D, ws=need, z_stride=Hv * D, n_rows=nseq):
+        return h.gdn_prefill_layer_rows(mixed, C, z, z_stride, p, p, Hv, p, None, p, p, p, 1, eps, None, p, None, p,
+                                        None, n_rows, p, T, p, p, nch, nseq, 0, Hk, Hv, D_, K, p, ws, None)
+
+    assert call(mixed=None) == 1 and b"null" in h.gdn_last_error()
+    assert call(D_=64) == 2 and b"head dim" in h.gdn_last_error()
+    assert call(z=ctypes.c_void_p(256 + 2)) == 1 and b"gate rows" in h.gdn_last_error()
+    assert call(z_stride=Hv * D - 8) == 1 and b"gate rows" in h.gdn_last_error()
+    assert call(n_rows=nseq + 1) == 1 and b"n_rows" in h.gdn_last_error()
+    assert call(ws=need - 256) == 1 and b"workspace" in h.gdn_last_error()
