@@ -470,10 +470,18 @@ __global__ __launch_bounds__(256) void seg_table_kernel(const int32_t* __restric
 // k-slot order.  The segment kernel multiplies V with them (U = T diag(beta) V) and, with their
 // columns scaled by e^G, K (W = T diag(beta e^G) K).  One wave owns one (chunk, value head) and
 // keeps everything in registers: no LDS round trips of intermediate products and no barriers.
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
 namespace tf {
 constexpr int FRAGS = 6;                      // lower fragments of T diag(beta)
-constexpr int BYTES = FRAGS * ws::FRAG;       // 6 KiB
 __device__ __forceinline__ int fid(int w, int s) { return w < 2 ? w : 2 * w - 2 + s; }
+// In memory a record is 5 KiB: fragments 0 = (0, 0) and 3 = (2, 1) straddle the diagonal, their
+// second 16-column block is zero, and they keep only the first 8 bytes of each lane (512 B); the
+// other four keep 16 bytes a lane.  Byte offsets 0, 512, 1536, 2560, 3072, 4096.
+constexpr int BYTES = 5 * ws::FRAG;
+__host__ __device__ __forceinline__ constexpr bool half(int f) { return f == 0 || f == 3; }
+__host__ __device__ __forceinline__ constexpr int offset(int f) {
+  return f * ws::FRAG - (f >= 1 ? ws::FRAG / 2 : 0) - (f >= 4 ? ws::FRAG / 2 : 0);
+}
 }  // namespace tf
 
 // A 16x16 fp32 block in "D layout" is the MFMA accumulator layout: lane (c, g) = (l % 16, l / 16)
@@ -620,6 +628,14 @@ __device__ int chunk_warm(const float* __restrict__ g, const BetaT* __restrict__
   return 0;
 }
 
+// Workgroup order -> item order.  The 8 XCDs take workgroups b % 8 in turn; this bijection on [0, n),
+// b -> (b % 8) * (n / 8) + b / 8 below 8 (n / 8) and the identity above, gives each XCD a contiguous
+// range of items.
+__device__ __forceinline__ int64_t xcd_range_item(int64_t b, int64_t n) {
+  const int64_t per = n / 8;
+  return b >= 8 * per ? b : (b % 8) * per + b / 8;
+}
+
 // One wave per (chunk, value head) item (item = chunk slot * Hv + value head; a workgroup's 4 waves
 // are independent, so a wave past the end simply exits).  Lane (i, g) holds K[16 t + i][32 s + 8 g
 // .. + 7] for token tiles t and k-blocks s < 4: the A fragment of tile t and, as K^T, the B
@@ -639,7 +655,9 @@ __global__ __launch_bounds__(pf::NT, 2) void inv_kernel(const uint16_t* __restri
   __shared__ float strp[4][4 * 16 * kTrPitch];    // per wave: 4 transpose tiles
   const int t = threadIdx.x, lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);  // the item is wave-uniform: scalar control flow
-  const int64_t item = (int64_t)blockIdx.x * 4 + w;
+  // the 8 workgroups of one chunk's 32 value heads share an XCD, so the chunk's g and beta lines
+  // (one token's heads per line) come from HBM once per chunk, not once per XCD
+  const int64_t item = xcd_range_item(blockIdx.x, gridDim.x) * 4 + w;
   if (item >= items) return;
   const int slot = (int)(item / Hv), h = (int)(item % Hv);
   const int r = Hv / Hqk, hk = h / r;
@@ -679,7 +697,9 @@ __global__ __launch_bounds__(pf::NT, 2) void inv_kernel(const uint16_t* __restri
         mine = g4 == tt ? invc[tt] : mine;
       }
     }
-    if (use_l2) knorm[((int64_t)slot * Hv + h) * CH + lane] = mine;
+    float* rec = knorm + ((int64_t)slot * Hv + h) * (2 * CH);
+    if (use_l2) rec[lane] = mine;
+    rec[CH + lane] = graw;  // the chunk's g of this head, contiguous for the segment kernel
     sdec[w][2][lane] = mine;
   }
   // K K^T: kk[tri(a, b)] = Dl of block (b, a) -- lane (c, g) r: (K K^T)[16 b + 4 g + r][16 a + c]
@@ -743,7 +763,7 @@ __global__ __launch_bounds__(pf::NT, 2) void inv_kernel(const uint16_t* __restri
   reg_inv64(XT, Xd, TT, strp[w], lane);
   // fragments (w', s), s <= w' / 2: element e of lane (i, g) = T[16 w' + i][j] beta_j with
   // j = 32 s + kpos(8 g + e), kpos(8 g + e) = 16 (e >> 2) + 4 g + (e & 3): blocks 2s (e < 4) and 2s + 1
-  uint8_t* dst = tfrag + ((int64_t)slot * Hv + h) * tf::BYTES + lane * 16;
+  uint8_t* dst = tfrag + ((int64_t)slot * Hv + h) * tf::BYTES;
   const f32x4 z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int wt = 0; wt < 4; ++wt)
@@ -751,7 +771,13 @@ __global__ __launch_bounds__(pf::NT, 2) void inv_kernel(const uint16_t* __restri
     for (int s = 0; s < 2; ++s) {
       if (2 * s > wt) continue;
       const f32x4 t0 = TT[tri(wt, 2 * s)], t1 = 2 * s + 1 <= wt ? TT[tri(wt, 2 * s + 1 <= wt ? 2 * s + 1 : 0)] : z;
-      *reinterpret_cast<bf16x8*>(dst + tf::fid(wt, s) * ws::FRAG) = pack_acc_bf16(t0 * Br[2 * s], t1 * Br[2 * s + 1]);
+      const int f = tf::fid(wt, s);
+      typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+      const u32x4 pk = __builtin_bit_cast(u32x4, pack_acc_bf16(t0 * Br[2 * s], t1 * Br[2 * s + 1]));
+      if (tf::half(f))  // the second block (e >= 4) is zero: 8 bytes a lane
+        *reinterpret_cast<u32x2v*>(dst + tf::offset(f) + lane * 8) = u32x2v{pk[0], pk[1]};
+      else
+        *reinterpret_cast<u32x4*>(dst + tf::offset(f) + lane * 16) = pk;
     }
   // the last chunk of a segment with a successor: that transition slot's warm-up length
   const int nch = tab.nch(cp.seq);
@@ -771,8 +797,8 @@ __global__ __launch_bounds__(pf::NT, 2) void inv_kernel(const uint16_t* __restri
 // described above in LDS (K and q masked and l2-normalised, the decay, Q K^T, -W from the K rows and
 // the inverse kernel's T diag(beta) scaled by e^G) and store the previous chunk's outputs, and its 4
 // chain waves advance 32 columns of the fp32 state each and leave their outputs in LDS.  Only the
-// inverse kernel's records (6 KiB of T fragments and 256 B of K row factors per (chunk, value head))
-// pass through memory besides the inputs and outputs.
+// inverse kernel's records (6 KiB of T fragments and 512 B of K row factors and g per (chunk, value
+// head)) pass through memory besides the inputs and outputs.
 // A segment other than the first of its sequence needs its true initial state: the state after
 // segment j is S_{j+1} = A_j S_j + B_j, with A_j the segment's linear map (the chain run from the
 // identity with U = 0) and B_j its affine part (run from zero).  A summary pass computes A_j and
@@ -851,8 +877,7 @@ template <bool kNeedQ, int kPart = -1>
 __device__ __forceinline__ void loc_load(LocIn& L, int64_t t0, int len, int kh, int h,
                                          const uint16_t* __restrict__ k, uint32_t ks, const uint16_t* __restrict__ q,
                                          uint32_t qs, const uint16_t* __restrict__ v, uint32_t vs,
-                                         const float* __restrict__ g, int Hv, const uint8_t* __restrict__ tfr,
-                                         const float* __restrict__ knc, bool q_on) {
+                                         const uint8_t* __restrict__ tfr, const float* __restrict__ knc, bool q_on) {
   using namespace pf;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const uint32_t tq = t >> 4, fb = t & 15;
@@ -874,10 +899,18 @@ __device__ __forceinline__ void loc_load(LocIn& L, int64_t t0, int len, int kh, 
       L.vr[i] = *reinterpret_cast<const u16x8*>(vb + ((rc * vs + 8 * fb) * 2u));
     }
     // every wave issues the same loads (tiles 0 and 1 read their one fragment twice): the wait
-    // counts before the uses then stay exact along every path through the chunk loop
+    // counts before the uses then stay exact along every path through the chunk loop.  A half
+    // fragment is read 16 bytes a lane from its 8-byte slots (the upper 8 bytes, the next lane's or
+    // the next fragment's, are dropped: the second block is zero)
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
-      L.tb[s] = *reinterpret_cast<const bf16x8*>(tfr + (uint32_t)(tf::fid(w, s) * ws::FRAG + lane * 16));
+    for (int s = 0; s < 2; ++s) {
+      typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+      const int f = tf::fid(w, s);
+      const bool hf = tf::half(f);
+      u32x4 x = *reinterpret_cast<const u32x4*>(tfr + (uint32_t)(tf::offset(f) + lane * (hf ? 8 : 16)));
+      if (hf) x[2] = x[3] = 0u;
+      L.tb[s] = __builtin_bit_cast(bf16x8, x);
+    }
   }
   if (kNeedQ && (kPart < 0 || kPart == 2)) {  // a warm-up chunk (no outputs) reads one row for all lanes:
                                                // the loads stay, the bytes go
@@ -890,11 +923,8 @@ __device__ __forceinline__ void loc_load(LocIn& L, int64_t t0, int len, int kh, 
       L.qr[s] = u16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
   }
-  if (kPart < 0 || kPart == 3) {
-    const float* gb = g + t0 * Hv + h;
-    const uint32_t tok = lane < len ? lane : len - 1;
-    L.graw = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(gb) + tok * (uint32_t)Hv * 4u);
-  }
+  if (kPart < 0 || kPart == 3)  // g of token `lane` (the last token's past the end), from the inverse kernel's record
+    L.graw = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(knc) + (pf::CH + lane) * 4u);
 }
 
 // Local phase 1 (wave w < 4): K rows (masked, l2-normalised when asked), V rows and the T diag(beta)
@@ -1072,7 +1102,6 @@ __device__ __forceinline__ void dec_split(const SegBuf& B, f32x4 (&vn)[2][4], Ch
 // out = bf16(w bf16(x rsqrt(mean(x^2) + eps)) silu(z)) with x = bf16(o).  Lane mapping, sum order (8 columns in a lane, then
 // the butterfly over 16 lanes) and roundings are gated_rmsnorm128_kernel's: the result is the same,
 // bit for bit, as that kernel applied to the stored outputs.
-typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
 struct GateArgs {
   const uint16_t* z;  // [tokens, Hv * D] bf16 gate rows, token stride zs
   int64_t zs;
@@ -1394,8 +1423,8 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     bf16x8 qf[4], tbu[2];
     auto load = [&](LocIn& L, int c, auto part) __attribute__((always_inline)) {
       loc_load<need_q, decltype(part)::value>(L, chunk_t0(c), chunk_len(c), kh, h, k, (uint32_t)ks, q, (uint32_t)qs, v,
-                                              (uint32_t)vs, g, Hv, tfr(c),
-                                              knorm + ((int64_t)(chunk_slot0 + c) * Hv + h) * CH, c >= w0);
+                                              (uint32_t)vs, tfr(c),
+                                              knorm + ((int64_t)(chunk_slot0 + c) * Hv + h) * (2 * CH), c >= w0);
     };
     auto phase2 = [&](SegBuf& B, bool q_on) __attribute__((always_inline)) {
       switch (w) {
@@ -1628,11 +1657,6 @@ __global__ __launch_bounds__(256) void seg_combine_kernel(SegTable tab, int Hv, 
 // sequence leaves (its last K inputs) is written afterwards by conv_state_capture_kernel, so the
 // history may be the same slot rows the state goes to.
 constexpr int kConvRun = 8;
-// A bijection on [0, n): b -> (b % 8) * (n / 8) + b / 8 below 8 (n / 8), the identity above.
-__device__ __forceinline__ int64_t xcd_range_item(int64_t b, int64_t n) {
-  const int64_t per = n / 8;
-  return b >= 8 * per ? b : (b % 8) * per + b / 8;
-}
 __device__ __forceinline__ int find_seq(const int32_t* cu, int nseq, int64_t p) {
   int lo = 0, hi = nseq - 1;  // last sequence whose start <= p (skips empty ones)
   while (lo < hi) {
@@ -1898,8 +1922,9 @@ int64_t seg_len(int64_t total_chunks, int Hv) {
 // Workspace layout: the segment table (nseq + 1 int32), the longest-first segment order (int32 per
 // segment), the transition flags (int32 per (slot,
 // value head)), the warm-up lengths (int32 per (slot, value head)), the transition slots (A, B fp32
-// per (slot, value head)), the inverse kernel's fragments (6 KiB per (chunk, value head)) and its K
-// l2norm factors (64 fp32 per (chunk, value head)), each part 256-byte aligned.
+// per (slot, value head)), the inverse kernel's fragments (6 KiB per (chunk, value head)) and its
+// records of 64 K l2norm factors then the chunk's 64 g values (fp32, 512 B per (chunk, value head)),
+// each part 256-byte aligned.
 struct SegLayout {
   int64_t L, nslots, off_order, off_flags, off_warm, off_trans, off_tfrag, off_knorm, bytes;
 };
@@ -1914,7 +1939,7 @@ SegLayout seg_layout(int64_t total_chunks, int nseq, int Hv) {
   l.off_trans = l.off_warm + up(l.nslots * Hv * 4);
   l.off_tfrag = l.off_trans + l.nslots * Hv * (int64_t)sg::kTrans * 4;
   l.off_knorm = l.off_tfrag + total_chunks * Hv * (int64_t)tf::BYTES;
-  l.bytes = l.off_knorm + total_chunks * Hv * (int64_t)(pf::CH * 4);
+  l.bytes = l.off_knorm + total_chunks * Hv * (int64_t)(2 * pf::CH * 4);
   return l;
 }
 }  // namespace
