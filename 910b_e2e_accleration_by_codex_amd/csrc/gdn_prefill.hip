@@ -797,7 +797,7 @@ __global__ __launch_bounds__(pf::NT, 2) void inv_kernel(const uint16_t* __restri
 // described above in LDS (K and q masked and l2-normalised, the decay, Q K^T, -W from the K rows and
 // the inverse kernel's T diag(beta) scaled by e^G) and store the previous chunk's outputs, and its 4
 // chain waves advance 32 columns of the fp32 state each and leave their outputs in LDS.  Only the
-// inverse kernel's records (6 KiB of T fragments and 512 B of K row factors and g per (chunk, value
+// inverse kernel's records (5 KiB of T fragments and 512 B of K row factors and g per (chunk, value
 // head)) pass through memory besides the inputs and outputs.
 // A segment other than the first of its sequence needs its true initial state: the state after
 // segment j is S_{j+1} = A_j S_j + B_j, with A_j the segment's linear map (the chain run from the
@@ -1922,7 +1922,7 @@ int64_t seg_len(int64_t total_chunks, int Hv) {
 // Workspace layout: the segment table (nseq + 1 int32), the longest-first segment order (int32 per
 // segment), the transition flags (int32 per (slot,
 // value head)), the warm-up lengths (int32 per (slot, value head)), the transition slots (A, B fp32
-// per (slot, value head)), the inverse kernel's fragments (6 KiB per (chunk, value head)) and its
+// per (slot, value head)), the inverse kernel's fragments (5 KiB per (chunk, value head)) and its
 // records of 64 K l2norm factors then the chunk's 64 g values (fp32, 512 B per (chunk, value head)),
 // each part 256-byte aligned.
 struct SegLayout {
