@@ -12,7 +12,7 @@ no CPU fallback.
 from ._lib import GDNError, LIB_PATH
 from .recurrent_single_step import recurrent_single_step
 from .cb_engine import (ELEM_CONV, GDNDecodeGraph, GDNSlots, causal_conv1d_update, elem_conv_update,
-                        fused_gated_rmsnorm, gated_rmsnorm, gdn_decode_core, gdn_decode_layer,
+                        fused_gated_rmsnorm, fused_rmsnorm, gated_rmsnorm, gdn_decode_core, gdn_decode_layer,
                         patch_model)
 from .gdn_chunk_fast import (Rows, Varlen, _unit_lower_inv, causal_conv1d_prefill, chunk_gated_delta_rule,
                              fast_chunk_gated_delta_rule, gdn_gating, gdn_prefill_core)
@@ -20,7 +20,7 @@ from .gdn_chunk_fast2 import fast_chunk_gated_delta_rule_v2
 
 __all__ = [
     "GDNError", "LIB_PATH", "recurrent_single_step", "ELEM_CONV", "GDNDecodeGraph", "GDNSlots",
-    "causal_conv1d_update", "elem_conv_update", "fused_gated_rmsnorm", "gated_rmsnorm",
+    "causal_conv1d_update", "elem_conv_update", "fused_gated_rmsnorm", "fused_rmsnorm", "gated_rmsnorm",
     "gdn_decode_core", "gdn_decode_layer", "patch_model", "_unit_lower_inv",
     "causal_conv1d_prefill", "chunk_gated_delta_rule", "fast_chunk_gated_delta_rule", "gdn_gating",
     "gdn_prefill_core", "Varlen", "Rows",

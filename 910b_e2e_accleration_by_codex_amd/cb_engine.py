@@ -87,6 +87,19 @@ def fused_gated_rmsnorm(self, hidden_states, gate=None):
     return gated_rmsnorm(hidden_states, gate, self.weight, self.variance_epsilon)
 
 
+def fused_rmsnorm(self, x):
+    """Bound onto bf16 Qwen3_5RMSNorm modules by patch_model (src/cb_engine.py:62-63): HF's
+    Qwen3_5RMSNorm.forward -- x * rsqrt(mean(x^2) + eps) in fp32, times (1 + w) in fp32, one bf16
+    rounding -- as one gdn_add_rmsnorm launch per call over the rows of x [..., H] bf16 (a
+    non-contiguous x, such as q_norm's half of the fused q|gate projection, is copied first)."""
+    H = x.shape[-1]
+    x2 = x.reshape(-1, H)
+    if not x2.is_contiguous():
+        x2 = x2.contiguous()
+    _, y = add_rms_norm(x2, None, self.weight, self.eps)
+    return y.view(x.shape)
+
+
 def gdn_decode_core(mixed, z, a, b, conv_state, conv_weight, A_log, dt_bias, norm_weight, rec_state,
                     num_k_heads, num_v_heads, head_dim, eps=1e-6, conv_bias=None, out=None, active=None):
     """One fused kernel for the GDN decode layer between in_proj_* and out_proj
@@ -150,9 +163,11 @@ def patch_model(model, fast_gdn=False, gdn_v2=False):
     """Install the HIP hot-path functions on a transformers Qwen3.5 model (src/cb_engine.py:54-77):
     every Qwen3_5GatedDeltaNet gets ``recurrent_gated_delta_rule`` and, with ``fast_gdn``,
     ``chunk_gated_delta_rule`` (v2 with ``gdn_v2``; v2 is only installed together with fast_gdn,
-    as in the reference); every Qwen3_5RMSNormGated gets the fused gated norm.  transformers >= 5.6
-    calls the module-level functions from GatedDeltaNet.forward, so those names are rebound in the
-    modeling module as well.  Qwen3_5RMSNorm is left to transformers."""
+    as in the reference); every Qwen3_5RMSNormGated gets the fused gated norm and every bf16
+    Qwen3_5RMSNorm the fused norm (HF's numerics; the reference's npu_rms_norm rounds 1 + w to the
+    input dtype first, a closed rounding not followed here; norms of other dtypes are left to
+    transformers).  transformers >= 5.6 calls the module-level functions from
+    GatedDeltaNet.forward, so those names are rebound in the modeling module as well."""
     from transformers.models.qwen3_5 import modeling_qwen3_5 as M
     from .gdn_chunk_fast import fast_chunk_gated_delta_rule as v1
     from .gdn_chunk_fast2 import fast_chunk_gated_delta_rule_v2 as v2
@@ -160,6 +175,8 @@ def patch_model(model, fast_gdn=False, gdn_v2=False):
     for m in model.modules():
         if isinstance(m, M.Qwen3_5RMSNormGated):
             m.forward = fused_gated_rmsnorm.__get__(m, M.Qwen3_5RMSNormGated)
+        elif isinstance(m, M.Qwen3_5RMSNorm) and m.weight.dtype == torch.bfloat16:
+            m.forward = fused_rmsnorm.__get__(m, M.Qwen3_5RMSNorm)
         elif isinstance(m, M.Qwen3_5GatedDeltaNet):
             m.recurrent_gated_delta_rule = recurrent_single_step
             if chunk_fn is not None:

@@ -105,3 +105,33 @@ def test_gdn_decode_layer_matches_layer_forward(gdn, dev, restore_transformers):
         assert rel_l2(outs[s], ref[s]) <= 1e-2
     assert torch.equal(conv, cache.layers[0].conv_states[0])
     assert rel_l2(rec, cache.layers[0].recurrent_states[0]) <= 1e-3
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("H", [64, 256, 1000, 5120])
+def test_patched_rmsnorm_matches_hf(gdn, dev, H):
+    """patch_model's fused Qwen3_5RMSNorm (src/cb_engine.py:62-63) against transformers' own forward
+    on the GPU: within one bf16 ulp everywhere (the sum of squares is taken in another order) and
+    mostly exact; 3-D rows, and a non-contiguous input like q_norm's half of the fused q|gate
+    projection.  H = 1000 takes the element-loop kernel, the others the 16-byte one."""
+    import copy
+    g_ = torch.Generator().manual_seed(H)
+    ref = M.Qwen3_5RMSNorm(H, eps=1e-6)
+    with torch.no_grad():
+        ref.weight.copy_(0.1 * torch.randn(H, generator=g_))
+    ref = ref.to(dev, torch.bfloat16)
+    pat = copy.deepcopy(ref)
+    gdn.patch_model(torch.nn.ModuleList([pat]))
+    assert pat.forward.__func__ is gdn.fused_rmsnorm
+    x = (3 * torch.randn(2, 37, H, generator=g_)).to(torch.bfloat16).to(dev)
+    qg = (3 * torch.randn(3, 5, 2, 2 * H, generator=g_)).to(torch.bfloat16).to(dev)
+    xs = torch.chunk(qg, 2, dim=-1)[0]          # [3, 5, 2, H], rows strided by 2H
+    for inp in (x, xs):
+        with torch.no_grad():
+            y_ref, y = ref(inp), pat(inp)
+        torch.cuda.synchronize()
+        assert y.shape == inp.shape and y.dtype == torch.bfloat16
+        diff = (y.float() - y_ref.float()).abs()
+        ulp = y_ref.float().abs().clamp_min(2 ** -126) * 2 ** -7
+        assert (diff <= ulp).all(), "fused RMSNorm off by more than one bf16 ulp"
+        assert (diff == 0).float().mean() >= 0.98

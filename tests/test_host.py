@@ -46,12 +46,17 @@ def test_patch_model_installs_functions(gdn):
                                 layer_types=["linear_attention"], intermediate_size=64, num_attention_heads=2,
                                 num_key_value_heads=1, head_dim=64, vocab_size=32)
         layer = M.Qwen3_5GatedDeltaNet(cfg, 0)
-        holder = torch.nn.ModuleList([layer])
+        norm16 = M.Qwen3_5RMSNorm(64).to(torch.bfloat16)
+        norm32 = M.Qwen3_5RMSNorm(64)
+        holder = torch.nn.ModuleList([layer, norm16, norm32])
         gdn.patch_model(holder, fast_gdn=True, gdn_v2=True)
         assert layer.chunk_gated_delta_rule is gdn.fast_chunk_gated_delta_rule_v2
         assert layer.recurrent_gated_delta_rule is gdn.recurrent_single_step
         assert M.torch_chunk_gated_delta_rule is gdn.fast_chunk_gated_delta_rule_v2
         assert layer.norm.forward.__func__ is gdn.fused_gated_rmsnorm
+        # bf16 Qwen3_5RMSNorm modules get the fused norm (src/cb_engine.py:62-63,70-71); others stay HF's
+        assert norm16.forward.__func__ is gdn.fused_rmsnorm
+        assert not hasattr(norm32.forward, "__func__") or norm32.forward.__func__ is not gdn.fused_rmsnorm
     finally:
         M.torch_chunk_gated_delta_rule, M.torch_recurrent_gated_delta_rule, M.causal_conv1d_update = saved
 
