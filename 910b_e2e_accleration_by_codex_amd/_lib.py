@@ -103,8 +103,14 @@ def call(name, *args):
         raise GDNError(f"{name} failed (code {rc}): {msg}")
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(t):
-    """Raw hipStream_t of torch's current stream on t's device."""
+    """Raw hipStream_t of torch's current stream on t's device (torch's raw-handle query when it has
+    one: no Stream object per call)."""
+    if _raw_stream is not None:
+        return ctypes.c_void_p(_raw_stream(t.get_device()))
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 

@@ -112,39 +112,49 @@ def gdn_decode_core(mixed, z, a, b, conv_state, conv_weight, A_log, dt_bias, nor
     output rows -- the held slots of src/cb_tp.py:274-285 without the save / restore copies.
     Returns the normed core [N, H_v*d] bf16."""
     _lib.require_cuda(mixed, z, a, b, conv_state, conv_weight, rec_state)
+    # (the per-call host work is kept to what the arguments need: this runs once per layer and step)
     N, C = mixed.shape
     Hk, Hv, D = num_k_heads, num_v_heads, head_dim
     K = conv_weight.shape[-1]
     if C != (2 * Hk + Hv) * D:
         raise ValueError(f"gdn_decode_core: C={C} != (2*{Hk}+{Hv})*{D}")
-    if tuple(conv_state.shape) != (N, C, K) or not conv_state.is_contiguous():
+    if conv_state.shape != (N, C, K) or not conv_state.is_contiguous():
         raise ValueError("gdn_decode_core: conv_state must be a contiguous [N, C, K] tensor")
-    if tuple(rec_state.shape) != (N, Hv, D, D) or rec_state.dtype != torch.float32 \
-            or not rec_state.is_contiguous():
+    if rec_state.shape != (N, Hv, D, D) or rec_state.dtype != torch.float32 or not rec_state.is_contiguous():
         raise ValueError("gdn_decode_core: rec_state must be a contiguous fp32 [N, H_v, d, d] tensor")
-    for name, t in (("mixed", mixed), ("z", z), ("a", a), ("b", b), ("conv_state", conv_state),
-                    ("conv_weight", conv_weight)):
-        if t.dtype != torch.bfloat16:
-            raise TypeError(f"gdn_decode_core: {name} must be bfloat16")
+    bf16 = torch.bfloat16
+    if mixed.dtype != bf16 or z.dtype != bf16 or a.dtype != bf16 or b.dtype != bf16 or conv_state.dtype != bf16 \
+            or conv_weight.dtype != bf16:
+        for name, t in (("mixed", mixed), ("z", z), ("a", a), ("b", b), ("conv_state", conv_state),
+                        ("conv_weight", conv_weight)):
+            if t.dtype != bf16:
+                raise TypeError(f"gdn_decode_core: {name} must be bfloat16")
     mixed, ms = _row_view(mixed)
-    z, zs = _row_view(z.reshape(N, Hv * D))
+    if z.dim() != 2:
+        z = z.reshape(N, Hv * D)
+    z, zs = _row_view(z)
     if zs % 4 or z.data_ptr() % 8:          # the kernel reads 4 gate values per 8-byte load
         z, zs = z.contiguous(), Hv * D
-    a = a.reshape(N, Hv)
-    b = b.reshape(N, Hv)
+    if a.dim() != 2:
+        a = a.reshape(N, Hv)
+    if b.dim() != 2:
+        b = b.reshape(N, Hv)
     if a.stride() != b.stride() or a.stride(-1) != 1:
         a, b = a.contiguous(), b.contiguous()
-    conv_weight = conv_weight.reshape(C, K).contiguous()
+    if not conv_weight.is_contiguous():      # [C, K] or [C, 1, K]: the same memory when contiguous
+        conv_weight = conv_weight.contiguous()
+    if conv_weight.numel() != C * K:
+        raise ValueError(f"gdn_decode_core: conv_weight must hold [C={C}, K={K}]")
     if conv_bias is not None:
-        conv_bias = conv_bias.to(torch.bfloat16).contiguous()
-    A32 = A_log.to(torch.float32).contiguous()
-    dt32 = dt_bias.to(torch.float32).contiguous()
-    nw = norm_weight if norm_weight.dtype in (torch.float32, torch.bfloat16) else norm_weight.float()
-    nw = nw.contiguous()
-    if nw.data_ptr() % 16:
-        nw = nw.clone()
+        conv_bias = conv_bias.to(bf16).contiguous()
+    A32 = A_log if A_log.dtype == torch.float32 and A_log.is_contiguous() else A_log.to(torch.float32).contiguous()
+    dt32 = dt_bias if dt_bias.dtype == torch.float32 and dt_bias.is_contiguous() \
+        else dt_bias.to(torch.float32).contiguous()
+    nw = norm_weight if norm_weight.dtype in (torch.float32, bf16) else norm_weight.float()
+    if not nw.is_contiguous() or nw.data_ptr() % 16:
+        nw = nw.contiguous().clone()
     if out is None:
-        out = torch.empty(N, Hv * D, dtype=torch.bfloat16, device=mixed.device)
+        out = torch.empty(N, Hv * D, dtype=bf16, device=mixed.device)
     elif not out.is_contiguous() or out.data_ptr() % 8:
         raise ValueError("gdn_decode_core: out must be a contiguous, 8-byte aligned bf16 [N, H_v*d] tensor")
     if active is not None:
@@ -152,10 +162,11 @@ def gdn_decode_core(mixed, z, a, b, conv_state, conv_weight, A_log, dt_bias, nor
         if active.numel() != N:
             raise ValueError(f"gdn_decode_core: active must have N={N} entries")
         active = active.reshape(N).to(torch.uint8).contiguous()
-    _lib.call("gdn_decode_fused_masked", _lib.ptr(mixed), ms, _lib.ptr(z), zs, _lib.ptr(a), _lib.ptr(b),
-              a.stride(0), _lib.ptr(conv_state), _lib.ptr(conv_weight), _lib.ptr(conv_bias),
-              _lib.ptr(A32), _lib.ptr(dt32), _lib.ptr(nw), _lib.dtype_code(nw), float(eps),
-              _lib.ptr(rec_state), _lib.ptr(out), _lib.ptr(active), N, Hk, Hv, D, K, _lib.stream_of(mixed))
+    _lib.call("gdn_decode_fused_masked", mixed.data_ptr(), ms, z.data_ptr(), zs, a.data_ptr(), b.data_ptr(),
+              a.stride(0), conv_state.data_ptr(), conv_weight.data_ptr(),
+              None if conv_bias is None else conv_bias.data_ptr(), A32.data_ptr(), dt32.data_ptr(), nw.data_ptr(),
+              _lib.dtype_code(nw), float(eps), rec_state.data_ptr(), out.data_ptr(),
+              None if active is None else active.data_ptr(), N, Hk, Hv, D, K, _lib.stream_of(mixed))
     return out
 
 
