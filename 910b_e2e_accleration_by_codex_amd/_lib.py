@@ -118,6 +118,11 @@ def ptr(t):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
+def ptr_int(t):
+    """Device address as a plain int (None for None): what a c_void_p argument takes directly."""
+    return None if t is None else t.data_ptr()
+
+
 def dtype_code(t):
     if t.dtype == torch.float32:
         return F32

@@ -53,19 +53,22 @@ class Varlen:
     def __init__(self, cu_seqlens, T, device):
         if isinstance(cu_seqlens, Varlen):
             raise TypeError("already a Varlen")
-        host = torch.as_tensor(cu_seqlens).detach().to("cpu", torch.int64).reshape(-1)
-        if host.numel() < 2 or int(host[0]) != 0 or int(host[-1]) != T or bool((host[1:] < host[:-1]).any()):
-            raise ValueError(f"cu_seqlens must be non-decreasing from 0 to {T}, got {host.tolist()[:8]}...")
+        if isinstance(cu_seqlens, (list, tuple)):
+            cu = [int(x) for x in cu_seqlens]
+        else:
+            cu = torch.as_tensor(cu_seqlens).detach().to("cpu", torch.int64).reshape(-1).tolist()
+        if len(cu) < 2 or cu[0] != 0 or cu[-1] != T or any(y < x for x, y in zip(cu, cu[1:])):
+            raise ValueError(f"cu_seqlens must be non-decreasing from 0 to {T}, got {cu[:8]}...")
         self.T = T
-        self.host = host
-        self.nseq = host.numel() - 1
-        nch = (host[1:] - host[:-1] + CHUNK - 1) // CHUNK
-        s0 = torch.zeros(host.numel(), dtype=torch.int64)
-        s0[1:] = torch.cumsum(nch, 0)
-        self.total_chunks = int(s0[-1])
-        self.max_len = int((host[1:] - host[:-1]).max()) if self.nseq else 0  # the kernels' seq_len bound
-        self.cu = _to_device_int32(host, device)
-        self.seq_chunk0 = _to_device_int32(s0, device)
+        self.nseq = len(cu) - 1
+        s0 = [0]
+        for x, y in zip(cu, cu[1:]):
+            s0.append(s0[-1] + (y - x + CHUNK - 1) // CHUNK)
+        self.total_chunks = s0[-1]
+        self.max_len = max(y - x for x, y in zip(cu, cu[1:])) if self.nseq else 0  # the kernels' seq_len bound
+        # both tables go up in one pinned copy (the host overhead of a layer call with a fresh table)
+        both = _to_device_int32(torch.tensor(cu + s0, dtype=torch.int64), device)
+        self.cu, self.seq_chunk0 = both[:len(cu)], both[len(cu):]
 
 
 def _varlen(cu_seqlens, B, T, device):
@@ -99,13 +102,16 @@ class Rows:
     [0, n_rows).  Host input (CPU tensor / list) costs no GPU wait; a device tensor is read back once."""
 
     def __init__(self, state_rows, nseq, n_rows, device):
-        host = torch.as_tensor(state_rows).detach().to("cpu", torch.int64).reshape(-1)
-        if host.numel() != nseq:
+        if isinstance(state_rows, (list, tuple)):
+            rows = [int(x) for x in state_rows]
+        else:
+            rows = torch.as_tensor(state_rows).detach().to("cpu", torch.int64).reshape(-1).tolist()
+        if len(rows) != nseq:
             raise ValueError(f"state_rows must hold one row per sequence ({nseq})")
-        if nseq and (int(host.min()) < 0 or int(host.max()) >= n_rows):
+        if nseq and (min(rows) < 0 or max(rows) >= n_rows):
             raise ValueError(f"state_rows must lie in [0, {n_rows})")
         self.nseq, self.n_rows = nseq, n_rows
-        self.dev = _to_device_int32(host, device)
+        self.dev = _to_device_int32(torch.tensor(rows, dtype=torch.int64), device)
 
 
 def _check_rows(state_rows, nseq, n_rows, device):
@@ -327,8 +333,10 @@ def gdn_prefill_core(mixed_qkv, z, a, b, conv_weight, A_log, dt_bias, norm_weigh
     if mixed_qkv.dtype != torch.bfloat16 or conv_weight.dtype != torch.bfloat16:
         raise TypeError("gdn_prefill_core: mixed_qkv and conv_weight must be bfloat16")
     dev = mixed_qkv.device
-    w = conv_weight.reshape(C, -1).contiguous()
-    K = w.shape[1]
+    w = conv_weight if conv_weight.is_contiguous() else conv_weight.contiguous()  # [C, K] or [C, 1, K]
+    K = w.numel() // C
+    if w.numel() != C * K:
+        raise ValueError(f"gdn_prefill_core: conv_weight must hold [C={C}, K]")
     if cu_seqlens is not None:  # checked and uploaded once (a Varlen is used as it is)
         vl = _varlen(cu_seqlens, 1, T, dev)
         cu, chunk0, nseq, seq_len, total_chunks = vl.cu, vl.seq_chunk0, vl.nseq, vl.max_len, vl.total_chunks
@@ -337,18 +345,21 @@ def gdn_prefill_core(mixed_qkv, z, a, b, conv_weight, A_log, dt_bias, norm_weigh
     x = mixed_qkv
     if x.stride(1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
         x = x.contiguous()
-    z2 = z.reshape(T, -1)
-    if z2.dtype != torch.bfloat16 or z2.shape[1] < Hv * D:
+    z2 = z if z.dim() == 2 else z.reshape(T, -1)
+    if z2.dtype != torch.bfloat16 or z2.shape[0] != T or z2.shape[1] < Hv * D:
         raise ValueError(f"gdn_prefill_core: z must be bf16 [{T}, >= {Hv * D}]")
     if z2.stride(1) != 1 or z2.stride(0) % 8 or z2.data_ptr() % 16:
         z2 = z2.contiguous()
-    a2, b2 = a.reshape(T, Hv), b.reshape(T, Hv)
+    a2 = a if a.dim() == 2 else a.reshape(T, Hv)
+    b2 = b if b.dim() == 2 else b.reshape(T, Hv)
     if a2.stride() != b2.stride() or a2.stride(-1) != 1:
         a2, b2 = a2.contiguous(), b2.contiguous()
     bias = conv_bias.to(torch.bfloat16).contiguous() if conv_bias is not None else None
-    A32, dt32 = A_log.to(torch.float32).contiguous(), dt_bias.to(torch.float32).contiguous()
-    nw = norm_weight.contiguous()
-    if tuple(nw.shape) != (D,) or nw.dtype not in (torch.bfloat16, torch.float32):
+    A32 = A_log if A_log.dtype == torch.float32 and A_log.is_contiguous() else A_log.to(torch.float32).contiguous()
+    dt32 = dt_bias if dt_bias.dtype == torch.float32 and dt_bias.is_contiguous() \
+        else dt_bias.to(torch.float32).contiguous()
+    nw = norm_weight if norm_weight.is_contiguous() else norm_weight.contiguous()
+    if nw.shape != (D,) or nw.dtype not in (torch.bfloat16, torch.float32):
         raise ValueError(f"gdn_prefill_core: norm weight must be bf16 or fp32 [{D}]")
     if slots is not None:
         if conv_slots is None or rec_slots is None:
@@ -383,9 +394,10 @@ def gdn_prefill_core(mixed_qkv, z, a, b, conv_weight, A_log, dt_bias, norm_weigh
     core = torch.empty(T, Hv * D, dtype=torch.bfloat16, device=dev)
     wbytes = int(_lib.lib().gdn_prefill_layer_workspace_bytes(T, total_chunks, nseq, Hk, Hv, D))
     work = torch.empty(max(wbytes, 1), dtype=torch.uint8, device=dev)
-    _lib.call("gdn_prefill_layer_rows", _lib.ptr(x), x.stride(0), _lib.ptr(z2), z2.stride(0), _lib.ptr(a2),
-              _lib.ptr(b2), a2.stride(0), _lib.ptr(w), _lib.ptr(bias), _lib.ptr(A32), _lib.ptr(dt32), _lib.ptr(nw),
-              _lib.dtype_code(nw), float(eps), _lib.ptr(hist), _lib.ptr(conv_state), _lib.ptr(init), _lib.ptr(rec),
-              _lib.ptr(rows), n_rows, _lib.ptr(core), T, _lib.ptr(cu), _lib.ptr(chunk0), total_chunks, nseq,
-              seq_len, Hk, Hv, D, K, _lib.ptr(work), wbytes, _lib.stream_of(mixed_qkv))
+    p = _lib.ptr_int
+    _lib.call("gdn_prefill_layer_rows", x.data_ptr(), x.stride(0), z2.data_ptr(), z2.stride(0), a2.data_ptr(),
+              b2.data_ptr(), a2.stride(0), w.data_ptr(), p(bias), A32.data_ptr(), dt32.data_ptr(), nw.data_ptr(),
+              _lib.dtype_code(nw), float(eps), p(hist), conv_state.data_ptr(), p(init), rec.data_ptr(),
+              p(rows), n_rows, core.data_ptr(), T, p(cu), p(chunk0), total_chunks, nseq,
+              seq_len, Hk, Hv, D, K, work.data_ptr(), wbytes, _lib.stream_of(mixed_qkv))
     return core, conv_state, rec
