@@ -34,6 +34,21 @@ def test_cu_seqlens_validation(gdn):
             cf._chunk_table(1, 200, torch.tensor(bad), "cpu")
     with pytest.raises(ValueError):
         cf._chunk_table(2, 100, torch.tensor([0, 100]), "cpu")
+    # host lists, tuples and tensors give the same tables (lists skip the tensor round trip)
+    for form in ([0, 64, 64, 130, 200], (0, 64, 64, 130, 200), torch.tensor([0, 64, 64, 130, 200], dtype=torch.int32)):
+        vl = cf.Varlen(form, 200, "cpu")
+        assert vl.cu.tolist() == [0, 64, 64, 130, 200] and vl.seq_chunk0.tolist() == [0, 1, 1, 3, 5]
+        assert vl.cu.dtype == vl.seq_chunk0.dtype == torch.int32
+        assert (vl.nseq, vl.total_chunks, vl.max_len) == (4, 5, 70)
+    for bad in ([0, 50, 40, 200], (1, 200), [0, 100]):
+        with pytest.raises(ValueError):
+            cf.Varlen(bad, 200, "cpu")
+    # slot rows: one per sequence, inside [0, n_rows)
+    assert cf.Rows([3, 0, 2], 3, 4, "cpu").dev.tolist() == [3, 0, 2]
+    assert cf.Rows(torch.tensor([3, 0, 2]), 3, 4, "cpu").dev.tolist() == [3, 0, 2]
+    for rows in ([3, 0], [3, 0, 4], [-1, 0, 2]):
+        with pytest.raises(ValueError):
+            cf.Rows(rows, 3, 4, "cpu")
 
 
 def test_patch_model_installs_functions(gdn):
