@@ -15,7 +15,7 @@ from .cb_engine import (ELEM_CONV, GDNDecodeGraph, GDNSlots, causal_conv1d_updat
                         fused_gated_rmsnorm, fused_rmsnorm, gated_rmsnorm, gdn_decode_core, gdn_decode_layer,
                         patch_model)
 from .gdn_chunk_fast import (Rows, Varlen, _unit_lower_inv, causal_conv1d_prefill, chunk_gated_delta_rule,
-                             fast_chunk_gated_delta_rule, gdn_gating, gdn_prefill_core)
+                             chunk_inverse_records, fast_chunk_gated_delta_rule, gdn_gating, gdn_prefill_core)
 from .gdn_chunk_fast2 import fast_chunk_gated_delta_rule_v2
 
 __all__ = [
@@ -23,6 +23,6 @@ __all__ = [
     "causal_conv1d_update", "elem_conv_update", "fused_gated_rmsnorm", "fused_rmsnorm", "gated_rmsnorm",
     "gdn_decode_core", "gdn_decode_layer", "patch_model", "_unit_lower_inv",
     "causal_conv1d_prefill", "chunk_gated_delta_rule", "fast_chunk_gated_delta_rule", "gdn_gating",
-    "gdn_prefill_core", "Varlen", "Rows",
+    "gdn_prefill_core", "Varlen", "Rows", "chunk_inverse_records",
     "fast_chunk_gated_delta_rule_v2",
 ]

@@ -13,7 +13,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libgdn_mi355x.so")
 
-F32, BF16 = 0, 1
+F32, BF16, F16 = 0, 1, 2
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -61,6 +61,10 @@ _SIGNATURES = {
     "gdn_chunk_prefill_noalloc": ([_P, _L, _P, _L, _P, _L, _P, _P, _I, _P, _P, _P, _I, _P, _L, _P, _P, _L, _I,
                                    _I, _I, _I, _I, _I, _I, _P], _I),
     "gdn_conv_prefill_rows": ([_P, _L, _P, _P, _P, _P, _P, _P, _I, _L, _P, _I, _I, _I, _I, _P], _I),
+    "gdn_chunk_prefill_inverse": ([_P, _L, _P, _P, _I, _L, _P, _P, _L, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P,
+                                   _L, _P], _I),
+    "gdn_chunk_prefill_generic": ([_P, _L, _P, _L, _P, _L, _P, _P, _I, _P, _P, _P, _I, _P, _L, _P, _I, _I, _I,
+                                   _I, _I, _I, _I, _I, _P], _I),
 }
 
 _lib = None
@@ -128,7 +132,9 @@ def dtype_code(t):
         return F32
     if t.dtype == torch.bfloat16:
         return BF16
-    raise TypeError(f"unsupported dtype {t.dtype} (float32 or bfloat16)")
+    if t.dtype == torch.float16:
+        return F16
+    raise TypeError(f"unsupported dtype {t.dtype} (float32, bfloat16 or float16)")
 
 
 def require_cuda(*ts):

@@ -13,7 +13,8 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB_NAME = "libgdn_mi355x.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
-SOURCES = ["gdn_capi.hip", "gdn_decode.hip", "gdn_prefill.hip", "gdn_gemv.hip", "gdn_attn.hip"]
+SOURCES = ["gdn_capi.hip", "gdn_decode.hip", "gdn_prefill.hip", "gdn_prefill_generic.hip", "gdn_gemv.hip",
+           "gdn_attn.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",

@@ -37,6 +37,12 @@ template <> struct Elem<uint16_t> {
   __device__ static __forceinline__ float round(float v) { return rbf(v); }
 };
 
+// Slot row of sequence s for state I/O: rows[s] (or s without rows); -1 if outside [0, n_rows).
+__device__ __forceinline__ int state_row(const int32_t* rows, int n_rows, int s) {
+  const int r = rows ? rows[s] : s;
+  return (r >= 0 && r < n_rows) ? r : -1;
+}
+
 // ---- scalar math with torch's CPU formulas ------------------------------------------------
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
 // SiLU with the hardware exp and reciprocal (each within about 1 ulp in fp32, so a bf16 result is

@@ -20,6 +20,8 @@
 // sees a bf16 rounding of its increment.
 #include "gdn_device.h"
 #include "gdn_internal.h"
+#include "gdn_inverse.h"
+#include <atomic>
 #include <type_traits>
 
 namespace gdn {
@@ -62,120 +64,37 @@ __device__ __forceinline__ f32x4 mm16_f32(const float* A, int lda, const float* 
   }
   return acc;
 }
-// Store a 16x16 fp32 accumulator (D layout) at M[0..15][0..15] (pitch ld).
-__device__ __forceinline__ void st16_f32(float* M, int ld, f32x4 acc, int lane) {
+// (I - X)^{-1} for a batch of strictly lower 64x64 fp32 X, by reg_inv64: the routine the chunked
+// prefill's inverse kernel runs (16x16 diagonal blocks by forward substitution, then the blocks
+// below them on the fp32 MFMA, the blocking of src/gdn_chunk_fast.py:33-62).  One wave per matrix,
+// four independent waves per workgroup.  Only the strictly lower part of X is read; T is written
+// whole (upper blocks zero).
+__global__ __launch_bounds__(256) void unit_lower_inv_kernel(const float* __restrict__ X, float* __restrict__ T,
+                                                             int64_t batch) {
+  __shared__ float tiles[4][4 * 16 * kTrPitch];  // per wave: reg_inv64's transpose tiles
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, c = lane & 15, g = lane >> 4;
+  const int64_t m = (int64_t)blockIdx.x * 4 + w;
+  if (m >= batch) return;
+  const float* Xm = X + m * 4096;
+  const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+  f32x4 XT[10], Xd[4], TT[10];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) M[(4 * (lane >> 4) + r) * ld + (lane & 15)] = acc[r];
-}
-
-// ---- (I - X)^{-1} for a strictly lower 64x64 fp32 X (only its strictly lower part is read) ----
-// Same blocking as src/gdn_chunk_fast.py:33-62 -- the four 16x16 diagonal blocks first, then the
-// merges [[A,0],[B X21 A, B]] for 32x32 and 64x64 -- all on fp32 MFMA.  A diagonal block is
-// inverted as (I+X)(I+X^2)(I+X^4)(I+X^8) (exact for nilpotent X, X^16 = 0) instead of the
-// reference's 16-step row recurrence: six dependent products instead of sixteen dependent steps;
-// with |X_ij| <= 1 (l2-normalised k, beta <= 1, decay <= 1) the powers of a 16x16 block stay far
-// from fp32 overflow (the reference avoids powers of the whole 64x64 block, which can overflow).
-// All 4 waves must call it (it holds barriers).  Its four 16x16 scratch blocks live in the upper
-// blocks (0,1) (0,2) (0,3) (1,2) of sX, which the inverse never reads.  Writes all of sT (upper
-// blocks zero).
-__device__ __forceinline__ float* inv_scratch(float* sX, int k) {
-  return sX + (k == 3 ? 16 * pf::LDF + 32 : 16 * (k + 1));
-}
-// The inverse in five barrier-free phases for waves 0-3 (the caller puts a workgroup barrier
-// between consecutive phases): the diagonal blocks, then the two merge levels in two steps each.
-// Phase 0: diagonal block w: T = (I+X)(I+X^2)(I+X^4)(I+X^8) (X^16 = 0), six fp32 MFMA products.
-__device__ __forceinline__ void inv64_diag(float* sX, float* sT, int w, int lane) {
-  using namespace pf;
-  const int c = lane & 15, g = lane >> 4;
-  const float* Xb = sX + 16 * w * LDF + 16 * w;
-  float* Tb = sT + 16 * w * LDF + 16 * w;
-  float* P = inv_scratch(sX, w);  // wave-private 16x16 scratch
+  for (int a = 0; a < 4; ++a) {
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int i = 4 * g + r;
-    Tb[i * LDF + c] = Xb[i * LDF + c] + (i == c ? 1.0f : 0.0f);
+    for (int b = 0; b < a; ++b)  // Dl(X_ab^T): lane (c, g) r = X[16a + c][16b + 4g + r] (all strictly lower)
+      XT[tri(a, b)] = *reinterpret_cast<const f32x4*>(&Xm[(16 * a + c) * 64 + 16 * b + 4 * g]);
+    XT[tri(a, a)] = z;  // not read
+#pragma unroll
+    for (int r = 0; r < 4; ++r)  // Dl(X_aa): lane (c, g) r = X[16a + 4g + r][16a + c], strictly lower part
+      Xd[a][r] = 4 * g + r > c ? Xm[(16 * a + 4 * g + r) * 64 + 16 * a + c] : 0.f;
   }
-  const float* Pin = Xb;
-  const int ldp = LDF;
+  reg_inv64(XT, Xd, TT, tiles[w], lane);
+  float* Tm = T + m * 4096;
 #pragma unroll
-  for (int step = 0; step < 3; ++step) {
-    f32x4 p2 = mm16_f32(Pin, ldp, Pin, ldp, f32x4{0.f, 0.f, 0.f, 0.f}, lane);  // X^(2^(step+1))
-    st16_f32(P, LDF, p2, lane);
-    __builtin_amdgcn_wave_barrier();
-    f32x4 tp = mm16_f32(Tb, LDF, P, LDF, f32x4{0.f, 0.f, 0.f, 0.f}, lane);    // T X^(2^(step+1))
+  for (int a = 0; a < 4; ++a)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) Tb[(4 * g + r) * LDF + c] += tp[r];
-    __builtin_amdgcn_wave_barrier();
-    Pin = P;
-  }
-  float* Trow = sT + 16 * w * LDF;
-  for (int col = 16 * (w + 1) + c; col < CH; col += 16)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) Trow[(4 * g + r) * LDF + col] = 0.f;
-}
-// Phase 1: Y = X10 T00 (wave 0), X32 T22 (wave 1).
-__device__ __forceinline__ void inv64_merge1a(float* sX, float* sT, int w, int lane) {
-  using namespace pf;
-  if (w >= 2) return;
-  const int b0 = 32 * w;  // block row/col offsets: rows b0+16.., cols b0..
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  acc = mm16_f32(sX + (b0 + 16) * LDF + b0, LDF, sT + b0 * LDF + b0, LDF, acc, lane);
-  st16_f32(inv_scratch(sX, w), LDF, acc, lane);
-}
-// Phase 2: T10 = T11 Y (wave 0), T32 = T33 Y (wave 1).
-__device__ __forceinline__ void inv64_merge1b(float* sX, float* sT, int w, int lane) {
-  using namespace pf;
-  if (w >= 2) return;
-  const int b0 = 32 * w;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  acc = mm16_f32(sT + (b0 + 16) * LDF + b0 + 16, LDF, inv_scratch(sX, w), LDF, acc, lane);
-  st16_f32(sT + (b0 + 16) * LDF + b0, LDF, acc, lane);
-}
-// Phase 3: Y20 = X20 T00 + X21 T10, Y30 = X30 T00 + X31 T10, Y21 = X21 T11, Y31 = X31 T11.
-__device__ __forceinline__ void inv64_merge2a(float* sX, float* sT, int w, int lane) {
-  using namespace pf;
-  const int ib = 2 + (w & 1), jb = w >> 1;  // wave 0: Y20, 1: Y30, 2: Y21, 3: Y31
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  if (jb == 0) acc = mm16_f32(sX + 16 * ib * LDF + 0, LDF, sT + 0 * LDF + 0, LDF, acc, lane);
-  acc = mm16_f32(sX + 16 * ib * LDF + 16, LDF, sT + 16 * LDF + 16 * jb, LDF, acc, lane);
-  st16_f32(inv_scratch(sX, w), LDF, acc, lane);
-}
-// Phase 4: T20 = T22 Y20, T30 = T32 Y20 + T33 Y30, T21 = T22 Y21, T31 = T32 Y21 + T33 Y31.
-__device__ __forceinline__ void inv64_merge2b(float* sX, float* sT, int w, int lane) {
-  using namespace pf;
-  const int ib = 2 + (w & 1), jb = w >> 1;
-  const float* Ya = inv_scratch(sX, 2 * jb);      // Y2jb
-  const float* Yb = inv_scratch(sX, 2 * jb + 1);  // Y3jb
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  acc = mm16_f32(sT + 16 * ib * LDF + 32, LDF, Ya, LDF, acc, lane);
-  if (ib == 3) acc = mm16_f32(sT + 48 * LDF + 48, LDF, Yb, LDF, acc, lane);
-  st16_f32(sT + 16 * ib * LDF + 16 * jb, LDF, acc, lane);
-}
-// All 4 waves of a 256-thread workgroup: the phases with an LDS barrier after each (global memory
-// requests of the caller stay in flight).
-__device__ void unit_lower_inv64(float* sX, float* sT, int w, int lane) {
-  inv64_diag(sX, sT, w, lane);
-  lds_barrier();
-  inv64_merge1a(sX, sT, w, lane);
-  lds_barrier();
-  inv64_merge1b(sX, sT, w, lane);
-  lds_barrier();
-  inv64_merge2a(sX, sT, w, lane);
-  lds_barrier();
-  inv64_merge2b(sX, sT, w, lane);
-  lds_barrier();
-}
-
-__global__ __launch_bounds__(pf::NT) void unit_lower_inv_kernel(const float* __restrict__ X, float* __restrict__ T) {
-  using namespace pf;
-  __shared__ float sX[CH * LDF], sT[CH * LDF];
-  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
-  const float* Xm = X + (int64_t)blockIdx.x * CH * CH;
-  for (int i = t; i < CH * CH; i += NT) sX[(i / CH) * LDF + (i % CH)] = (i / CH) > (i % CH) ? Xm[i] : 0.f;
-  __syncthreads();
-  unit_lower_inv64(sX, sT, w, lane);
-  float* Tm = T + (int64_t)blockIdx.x * CH * CH;
-  for (int i = t; i < CH * CH; i += NT) Tm[i] = sT[(i / CH) * LDF + (i % CH)];
+    for (int b = 0; b < 4; ++b)  // Dl(T_ab^T): lane (c, g) r = T[16a + c][16b + 4g + r]
+      *reinterpret_cast<f32x4*>(&Tm[(16 * a + c) * 64 + 16 * b + 4 * g]) = b <= a ? TT[tri(a, b <= a ? b : 0)] : z;
 }
 
 // ============================================================================================
@@ -202,11 +121,6 @@ namespace ws {
 constexpr int FRAG = 1024;                       // bytes per fragment
 }  // namespace ws
 
-// Slot row of sequence s for state I/O: rows[s] (or s without rows); -1 if outside [0, n_rows).
-__device__ __forceinline__ int state_row(const int32_t* rows, int n_rows, int s) {
-  const int r = rows ? rows[s] : s;
-  return (r >= 0 && r < n_rows) ? r : -1;
-}
 
 struct ChunkPos {
   int64_t t0;  // first packed token of the chunk
@@ -316,21 +230,6 @@ __device__ __forceinline__ bf16x8 lds_frag(const uint8_t* base, int f, int lane)
   return *reinterpret_cast<const bf16x8*>(base + f * ws::FRAG + lane * 16);
 }
 
-// Inclusive prefix sum over the 64 lanes (DPP: shifts within rows of 16, then the row totals
-// broadcast into the later rows).
-template <int kCtrl, int kRowMask>
-__device__ __forceinline__ float dpp_or_zero(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, kRowMask, 0xf, false));
-}
-__device__ __forceinline__ float wave_incl_scan(float x) {
-  x += dpp_or_zero<0x111, 0xf>(x);  // row_shr:1
-  x += dpp_or_zero<0x112, 0xf>(x);  // row_shr:2
-  x += dpp_or_zero<0x114, 0xf>(x);  // row_shr:4
-  x += dpp_or_zero<0x118, 0xf>(x);  // row_shr:8
-  x += dpp_or_zero<0x142, 0xa>(x);  // row_bcast:15 into rows 1 and 3
-  x += dpp_or_zero<0x143, 0xc>(x);  // row_bcast:31 into rows 2 and 3
-  return x;
-}
 
 // Segment bookkeeping of the chunked prefill (shared by its kernels).
 namespace sg {
@@ -484,117 +383,6 @@ __host__ __device__ __forceinline__ constexpr int offset(int f) {
 }
 }  // namespace tf
 
-// A 16x16 fp32 block in "D layout" is the MFMA accumulator layout: lane (c, g) = (l % 16, l / 16)
-// holds M[4g + r][c], r < 4.  v_mfma_f32_16x16x4_f32 takes, per lane, A[l % 16][slot l / 16] and
-// B[slot l / 16][l % 16]; with slot g of instruction kk standing for k = 4g + kk, the A operand of
-// A B is the D layout of A^T and the B operand the D layout of B.  So
-//   rmm(Dl(A^T), Dl(B), Dl(C)) = Dl(A B + C)   and   Dl((A B)^T) = rmm(Dl(B), Dl(A^T), 0):
-// a product and its transpose come from the same two registers.
-__device__ __forceinline__ f32x4 rmm(f32x4 aT, f32x4 b, f32x4 acc) {
-  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(aT[0], b[0], acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(aT[1], b[1], acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(aT[2], b[2], acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(aT[3], b[3], acc, 0, 0, 0);
-  return acc;
-}
-// Index of the lower block (a, b), b <= a, of a 4x4 block grid.
-__device__ __forceinline__ constexpr int tri(int a, int b) { return a * (a + 1) / 2 + b; }
-
-// Dl(M^T) from Dl(M) through a wave-private 16 x 20 fp32 LDS tile: the wave writes M row-major and
-// reads its transpose back 16 bytes per lane.  A wave's LDS accesses complete in issue order, and
-// the compiler keeps a tile's store -> load -> next store order (they may alias), so no barrier is
-// needed.
-constexpr int kTrPitch = 20;
-__device__ __forceinline__ f32x4 ltr(float* tile, f32x4 m, int lane) {
-  const int c = lane & 15, g = lane >> 4;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) tile[(4 * g + r) * kTrPitch + c] = m[r];
-  return *reinterpret_cast<const f32x4*>(&tile[c * kTrPitch + 4 * g]);
-}
-
-// Lane l's value v from lane n of its row of 16 lanes (DPP row_newbcast).
-template <int N>
-__device__ __forceinline__ float row_bcast(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x150 + N, 0xf, 0xf, true));
-}
-// t[i] += sum_{m < i} row_bcast<m>(x[i]) t[m] for i = 1 .. 15, in order of m.
-template <int I, int M>
-__device__ __forceinline__ void fwd_sub(const float (&x)[16], float (&t)[16]) {
-  if constexpr (I < 16) {
-    if constexpr (M < I) {
-      t[I] = __builtin_fmaf(row_bcast<M>(x[I]), t[M], t[I]);
-      fwd_sub<I, M + 1>(x, t);
-    } else {
-      fwd_sub<I + 1, 0>(x, t);
-    }
-  }
-}
-
-// (I - X)^{-1} for a strictly lower 64x64 X, one wave.  In: XT[tri(a, b)] = Dl(X_ab^T) for every
-// lower block, Xd[a] = Dl(X_aa).  Out: TT[tri(a, b)] = Dl(T_ab^T).  tiles: 4 wave-private 16 x 20
-// fp32 LDS tiles.  Same blocking as src/gdn_chunk_fast.py:33-62: the diagonal blocks first, then the
-// blocks below them, T_ij = T_ii sum_{k=j}^{i-1} X_ik T_kj.  The four diagonal blocks are solved at
-// once by forward substitution on the VALU: lane (a, j) = (l / 16, l % 16) holds column j of X_aa
-// and forms column j of T_aa, t_i = [i = j] + sum_{m < i} X_aa[i][m] t_m, with X_aa[i][m] taken
-// from lane m of its row (120 FMAs, in place of 24 products of 16x16 blocks on the fp32 MFMA).
-// Columns go in and out through the tiles (stored transposed: tile a row j = column j of the block).
-__device__ __forceinline__ void reg_inv64(const f32x4 (&XT)[10], const f32x4 (&Xd)[4], f32x4 (&TT)[10], float* tiles,
-                                          int lane) {
-  const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-  const int c = lane & 15, g = lane >> 4;
-  f32x4 TD[6];  // Dl(T_ab) for the blocks of rows 0..2 (tri index < 6)
-  {
-#pragma unroll
-    for (int a = 0; a < 4; ++a)  // lane (c, g) holds X_aa[4g + r][c]: tile a, row c, columns 4g ..
-      *reinterpret_cast<f32x4*>(&tiles[(16 * a + c) * kTrPitch + 4 * g]) = Xd[a];
-    float x[16], t[16];
-    float* col = &tiles[(16 * g + c) * kTrPitch];  // this lane's column: block g, column c
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(&col[4 * m]);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) x[4 * m + r] = v[r];
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) t[i] = i == c ? 1.f : 0.f;
-    fwd_sub<1, 0>(x, t);
-#pragma unroll
-    for (int m = 0; m < 4; ++m) *reinterpret_cast<f32x4*>(&col[4 * m]) = f32x4{t[4 * m], t[4 * m + 1], t[4 * m + 2], t[4 * m + 3]};
-#pragma unroll
-    for (int a = 0; a < 4; ++a) {  // Dl(T_aa): T_aa[4g + r][c] = tile a [c][4g + r]; Dl(T_aa^T): tile a [4g + r][c]
-      const float* tile = &tiles[16 * a * kTrPitch];
-      f32x4 tt;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) tt[r] = tile[(4 * g + r) * kTrPitch + c];
-      TT[tri(a, a)] = tt;
-      if (a < 3) TD[tri(a, a)] = *reinterpret_cast<const f32x4*>(&tile[c * kTrPitch + 4 * g]);
-    }
-  }
-  f32x4 Y;
-  // first subdiagonal
-  Y = rmm(XT[tri(1, 0)], TD[tri(0, 0)], z);
-  TD[tri(1, 0)] = rmm(TT[tri(1, 1)], Y, z);
-  TT[tri(1, 0)] = ltr(tiles, TD[tri(1, 0)], lane);
-  Y = rmm(XT[tri(2, 1)], TD[tri(1, 1)], z);
-  TD[tri(2, 1)] = rmm(TT[tri(2, 2)], Y, z);
-  TT[tri(2, 1)] = ltr(tiles + 16 * kTrPitch, TD[tri(2, 1)], lane);
-  Y = rmm(XT[tri(3, 2)], TD[tri(2, 2)], z);
-  TT[tri(3, 2)] = rmm(Y, TT[tri(3, 3)], z);
-  // second
-  Y = rmm(XT[tri(2, 0)], TD[tri(0, 0)], z);
-  Y = rmm(XT[tri(2, 1)], TD[tri(1, 0)], Y);
-  TD[tri(2, 0)] = rmm(TT[tri(2, 2)], Y, z);
-  TT[tri(2, 0)] = ltr(tiles + 2 * 16 * kTrPitch, TD[tri(2, 0)], lane);
-  Y = rmm(XT[tri(3, 1)], TD[tri(1, 1)], z);
-  Y = rmm(XT[tri(3, 2)], TD[tri(2, 1)], Y);
-  TT[tri(3, 1)] = rmm(Y, TT[tri(3, 3)], z);
-  // third
-  Y = rmm(XT[tri(3, 0)], TD[tri(0, 0)], z);
-  Y = rmm(XT[tri(3, 1)], TD[tri(1, 0)], Y);
-  Y = rmm(XT[tri(3, 2)], TD[tri(2, 0)], Y);
-  TT[tri(3, 0)] = rmm(Y, TT[tri(3, 3)], z);
-}
-
 // Warm-up length for the transition after the segment ending with the chunk at token t_last (one
 // wave): the least w such that the summed log decay of the segment's last w chunks is below
 // ln 2^-40 -- the norm bound of the dropped map with unit keys and beta in [0, 1] -- or 0 when there
@@ -746,9 +534,10 @@ __global__ __launch_bounds__(pf::NT, 2) void inv_kernel(const uint16_t* __restri
 #pragma unroll
     for (int b = 0; b <= a; ++b)
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {  // straight-line: the exponent is clamped to <= 0, the mask multiplies
+      for (int rr = 0; rr < 4; ++rr) {  // straight-line: the exponent is 0 off the strict lower part, the
+                                         // mask multiplies (any sign of g: e^{G_i - G_j} as the reference)
         const int i = 16 * a + c16, j = 16 * b + 4 * g4 + rr;
-        const float x = -Bc[a] * kk[tri(a, b)][rr] * __expf(fminf(Gc[a] - Gr[b][rr], 0.f));
+        const float x = -Bc[a] * kk[tri(a, b)][rr] * __expf(i > j ? Gc[a] - Gr[b][rr] : 0.f);
         XT[tri(a, b)][rr] = x * (i > j ? 1.f : 0.f);
       }
 #pragma unroll
@@ -756,7 +545,7 @@ __global__ __launch_bounds__(pf::NT, 2) void inv_kernel(const uint16_t* __restri
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       const int i = 16 * a + 4 * g4 + rr, j = 16 * a + c16;
-      const float x = -Br[a][rr] * kk[tri(a, a)][rr] * __expf(fminf(Gr[a][rr] - Gc[a], 0.f));
+      const float x = -Br[a][rr] * kk[tri(a, a)][rr] * __expf(i > j ? Gr[a][rr] - Gc[a] : 0.f);
       Xd[a][rr] = x * (i > j ? 1.f : 0.f);
     }
   f32x4 TT[10];
@@ -1888,17 +1677,34 @@ static __device__ __align__(256) uint8_t scratch[GDN_NOALLOC_SCRATCH_BYTES];
 
 using namespace gdn;
 
-// Device address of `scratch` on the current device, looked up once per device (null on failure).
-static uint8_t* scratch_ptr() {
-  static uint8_t* cached[64] = {nullptr};
+// Device address of `scratch` for a call on `stream`: the stream must belong to the current device
+// (the null stream does), and the address is looked up once per device, with that device current,
+// by hipGetSymbolAddress (each GPU holds its own copy of the array).  0 and *out set, or an error code.
+static int scratch_ptr(hipStream_t stream, uint8_t** out) {
+  static std::atomic<uintptr_t> cached[64];
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-  if (!cached[dev]) {
-    void* p = nullptr;
-    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
-    cached[dev] = (uint8_t*)p;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+    return set_error(GDN_ELAUNCH, "gdn_chunk_prefill_noalloc: no current HIP device");
+  if (stream) {
+    hipDevice_t sd = dev;
+    if (hipStreamGetDevice(stream, &sd) != hipSuccess)
+      return set_error(GDN_EINVAL, "gdn_chunk_prefill_noalloc: cannot query the stream's device");
+    if (sd != dev)
+      return set_error(GDN_EINVAL,
+                       "gdn_chunk_prefill_noalloc: the stream belongs to device %d but device %d is current "
+                       "(the static scratch is per device: make the stream's device current)",
+                       (int)sd, dev);
   }
-  return cached[dev];
+  uintptr_t p = cached[dev].load(std::memory_order_acquire);
+  if (!p) {
+    void* a = nullptr;
+    if (hipGetSymbolAddress(&a, HIP_SYMBOL(scratch)) != hipSuccess || !a)
+      return set_error(GDN_ELAUNCH, "gdn_chunk_prefill_noalloc: no static scratch on device %d", dev);
+    p = (uintptr_t)a;
+    cached[dev].store(p, std::memory_order_release);
+  }
+  *out = (uint8_t*)p;
+  return GDN_OK;
 }
 
 extern "C" int gdn_unit_lower_inv(const float* X, float* T, int64_t batch, int n, void* stream) {
@@ -1907,7 +1713,8 @@ extern "C" int gdn_unit_lower_inv(const float* X, float* T, int64_t batch, int n
   GDN_SUPPORT(n == 64, "gdn_unit_lower_inv: only 64x64 blocks are supported (got %d)", n);
   GDN_REQUIRE(batch >= 0 && batch < (1ll << 31), "gdn_unit_lower_inv: bad batch %lld", (long long)batch);
   if (batch == 0) return GDN_OK;
-  unit_lower_inv_kernel<<<(unsigned)batch, pf::NT, 0, (hipStream_t)stream>>>(X, T);
+  GDN_REQUIRE(aligned(X, 16) && aligned(T, 16), "gdn_unit_lower_inv: X and T must be 16-byte aligned");
+  unit_lower_inv_kernel<<<(unsigned)((batch + 3) / 4), 256, 0, (hipStream_t)stream>>>(X, T, batch);
   return check_launch("gdn_unit_lower_inv");
 }
 
@@ -1957,7 +1764,7 @@ int chunk_prefill_impl(const void* q, int64_t q_stride, const void* k, int64_t k
                        const int32_t* cu_seqlens, const int32_t* seq_chunk0, int64_t total_chunks, int nseq,
                        int seq_len, int Hqk, int Hv, int D, int in_dtype, int use_qk_l2norm, void* workspace,
                        int64_t workspace_bytes, void* stream, const GateArgs& gate, int norm_mode,
-                       bool table_built = false) {
+                       bool table_built = false, bool check_only = false) {
   GDN_REQUIRE(state_rows ? n_rows >= 0 : n_rows == nseq,
               "gdn_chunk_prefill: without state_rows, n_rows must equal nseq");
   GDN_REQUIRE(q && k && v && g && beta && out, "gdn_chunk_prefill: null input/output pointer");
@@ -1986,9 +1793,15 @@ int chunk_prefill_impl(const void* q, int64_t q_stride, const void* k, int64_t k
               "gdn_chunk_prefill: workspace missing, misaligned or smaller than %lld bytes",
               (long long)gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hv));
   GDN_REQUIRE(total_chunks < (1ll << 31), "gdn_chunk_prefill: too many chunks");
-  if (nseq == 0) return GDN_OK;
-  hipStream_t st = (hipStream_t)stream;
   const SegLayout lay = seg_layout(total_chunks, nseq, Hv);
+  {
+    const int64_t nseg_max = (int64_t)nseq + total_chunks / lay.L;  // each sequence: <= nch / L + 1 segments
+    GDN_REQUIRE(nseg_max * Hv < (1ll << 31) && lay.nslots * Hv * 2 < (1ll << 31) &&
+                    (int64_t)nseq * Hv * 64 < (1ll << 31) && total_chunks * Hv < (1ll << 33),
+                "gdn_chunk_prefill: grid too large");
+  }
+  if (check_only || nseq == 0) return GDN_OK;
+  hipStream_t st = (hipStream_t)stream;
   uint8_t* work = (uint8_t*)workspace;
   int32_t* seg0 = (int32_t*)work;
   int32_t* order = (int32_t*)(work + lay.off_order);
@@ -1997,10 +1810,7 @@ int chunk_prefill_impl(const void* q, int64_t q_stride, const void* k, int64_t k
   float* trans = (float*)(work + lay.off_trans);
   uint8_t* tfrag = work + lay.off_tfrag;
   float* knorm = (float*)(work + lay.off_knorm);
-  const int64_t nseg_max = (int64_t)nseq + total_chunks / lay.L;  // each sequence: <= nch / L + 1 segments
-  GDN_REQUIRE(nseg_max * Hv < (1ll << 31) && lay.nslots * Hv * 2 < (1ll << 31) && (int64_t)nseq * Hv * 64 < (1ll << 31) &&
-                  total_chunks * Hv < (1ll << 33),
-              "gdn_chunk_prefill: grid too large");
+  const int64_t nseg_max = (int64_t)nseq + total_chunks / lay.L;
   if (cu_seqlens && !table_built) {
     seg_table_kernel<<<1, 256, 0, st>>>(seq_chunk0, nseq, (int)lay.L, seg0, order);
     int rc = check_launch("gdn_chunk_prefill(table)");
@@ -2053,6 +1863,34 @@ int chunk_prefill_impl(const void* q, int64_t q_stride, const void* k, int64_t k
 }
 }  // namespace
 
+// The inverse kernel's records of (chunk, value head) `item`, dense: T diag(beta) as the output pass
+// reads it, [64, 64] fp32 (row = token of the chunk; the bf16 values of the fragments, zeros where
+// no fragment holds a value), and the K rows' l2norm factors [64].  Fragment f = tf::fid(w', s),
+// element e of lane (i, g): row 16 w' + i, column 32 s + 16 (e >> 2) + 4 g + (e & 3); the two half
+// fragments keep e < 4 only.  Lane l writes row l.  One wave per item.
+__global__ __launch_bounds__(256) void inv_records_expand_kernel(const uint8_t* __restrict__ tfrag,
+                                                                 const float* __restrict__ knorm, int64_t items,
+                                                                 float* __restrict__ t_out,
+                                                                 float* __restrict__ factor_out) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t item = (int64_t)blockIdx.x * 4 + w;
+  if (item >= items) return;
+  const uint8_t* rec = tfrag + item * tf::BYTES;
+  const int wt = lane >> 4, i = lane & 15;
+  float* row = t_out + item * 4096 + lane * 64;
+  for (int j = 0; j < 64; ++j) {
+    const int s = j >> 5, jj = j & 31, e = 4 * (jj >> 4) + (jj & 3), gg = (jj & 15) >> 2;
+    float x = 0.f;
+    if (2 * s <= wt) {
+      const int f = tf::fid(wt, s), l = i + 16 * gg;
+      if (!tf::half(f)) x = bf2f(reinterpret_cast<const uint16_t*>(rec + tf::offset(f) + l * 16)[e]);
+      else if (e < 4) x = bf2f(reinterpret_cast<const uint16_t*>(rec + tf::offset(f) + l * 8)[e]);
+    }
+    row[j] = x;
+  }
+  if (factor_out) factor_out[item * 64 + lane] = knorm[item * 2 * pf::CH + lane];
+}
+
 extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const void* k, int64_t k_stride,
                                       const void* v, int64_t v_stride, const float* g, const void* beta,
                                       int beta_dtype, const float* initial_state, float* final_state,
@@ -2061,6 +1899,10 @@ extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const voi
                                       int nseq, int seq_len, int Hqk, int Hv, int D, int in_dtype,
                                       int use_qk_l2norm, void* workspace, int64_t workspace_bytes, void* stream) {
   clear_error();
+  if (D != pf::D || in_dtype != GDN_BF16)  // other head dims and dtypes: the generic fp32 kernel
+    return gdn_chunk_prefill_generic(q, q_stride, k, k_stride, v, v_stride, g, beta, beta_dtype, initial_state,
+                                     final_state, state_rows, n_rows, out, total_tokens, cu_seqlens, nseq, seq_len,
+                                     Hqk, Hv, D, D, in_dtype, use_qk_l2norm, stream);
   return chunk_prefill_impl(q, q_stride, k, k_stride, v, v_stride, g, beta, beta_dtype, initial_state, final_state,
                             state_rows, n_rows, out, total_tokens, cu_seqlens, seq_chunk0, total_chunks, nseq, seq_len,
                             Hqk, Hv, D, in_dtype, use_qk_l2norm, workspace, workspace_bytes, stream, GateArgs{}, 0);
@@ -2114,12 +1956,68 @@ extern "C" int gdn_chunk_prefill_noalloc(const void* q, int64_t q_stride, const 
               "gdn_chunk_prefill_noalloc: the call needs %lld bytes of workspace, the static scratch holds %lld "
               "(%lld chunks, %d sequences, %d value heads; use gdn_chunk_prefill_rows with a workspace)",
               (long long)need, (long long)GDN_NOALLOC_SCRATCH_BYTES, (long long)total_chunks, nseq, Hv);
-  uint8_t* ws_ptr = scratch_ptr();
-  if (!ws_ptr) return set_error(GDN_ELAUNCH, "gdn_chunk_prefill_noalloc: no static scratch on the current device");
+  uint8_t* ws_ptr = nullptr;
+  {
+    const int rc = scratch_ptr((hipStream_t)stream, &ws_ptr);
+    if (rc) return rc;
+  }
   return gdn_chunk_prefill_rows(q, q_stride, k, k_stride, v, v_stride, g, beta, beta_dtype, initial_state,
                                 final_state, state_rows, n_rows, out, total_tokens, cu_seqlens, seq_chunk0,
                                 total_chunks, nseq, seq_len, Hqk, Hv, D, in_dtype, use_qk_l2norm, ws_ptr,
                                 GDN_NOALLOC_SCRATCH_BYTES, stream);
+}
+
+extern "C" int gdn_chunk_prefill_inverse(const void* k, int64_t k_stride, const float* g, const void* beta,
+                                         int beta_dtype, int64_t total_tokens, const int32_t* cu_seqlens,
+                                         const int32_t* seq_chunk0, int64_t total_chunks, int nseq, int seq_len,
+                                         int Hqk, int Hv, int D, int in_dtype, int use_qk_l2norm, float* t_out,
+                                         float* factor_out, void* workspace, int64_t workspace_bytes,
+                                         void* stream) {
+  clear_error();
+  GDN_REQUIRE(k && g && beta && t_out, "gdn_chunk_prefill_inverse: null pointer");
+  GDN_SUPPORT(D == pf::D && in_dtype == GDN_BF16, "gdn_chunk_prefill_inverse: needs bf16 keys with D = %d", pf::D);
+  GDN_REQUIRE(beta_dtype == GDN_F32 || beta_dtype == GDN_BF16, "gdn_chunk_prefill_inverse: bad beta dtype");
+  GDN_REQUIRE(Hqk > 0 && Hv > 0 && Hv % Hqk == 0 && nseq >= 0 && total_tokens >= 0 && total_chunks >= 0 &&
+                  seq_len >= 0,
+              "gdn_chunk_prefill_inverse: bad sizes");
+  GDN_REQUIRE(cu_seqlens ? seq_chunk0 != nullptr : (int64_t)nseq * seq_len == total_tokens,
+              "gdn_chunk_prefill_inverse: cu_seqlens needs seq_chunk0; without it nseq*seq_len must be total_tokens");
+  GDN_REQUIRE(cu_seqlens || total_chunks == (int64_t)nseq * ((seq_len + pf::CH - 1) / pf::CH),
+              "gdn_chunk_prefill_inverse: total_chunks inconsistent with nseq/seq_len");
+  GDN_REQUIRE(aligned(k, 16) && k_stride % 8 == 0 && k_stride > 0 && k_stride < (1ll << 25),
+              "gdn_chunk_prefill_inverse: k rows must be 16-byte aligned");
+  GDN_REQUIRE(workspace && aligned(workspace, 256) &&
+                  workspace_bytes >= gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hv),
+              "gdn_chunk_prefill_inverse: workspace missing, misaligned or too small");
+  GDN_REQUIRE(total_chunks * Hv < (1ll << 33), "gdn_chunk_prefill_inverse: grid too large");
+  if (nseq == 0 || total_chunks == 0) return GDN_OK;
+  hipStream_t st = (hipStream_t)stream;
+  const SegLayout lay = seg_layout(total_chunks, nseq, Hv);
+  uint8_t* work = (uint8_t*)workspace;
+  int32_t* seg0 = (int32_t*)work;
+  if (cu_seqlens) {
+    seg_table_kernel<<<1, 256, 0, st>>>(seq_chunk0, nseq, (int)lay.L, seg0, (int32_t*)(work + lay.off_order));
+    const int rc = check_launch("gdn_chunk_prefill_inverse(table)");
+    if (rc) return rc;
+  }
+  const SegTable tab{cu_seqlens, seq_chunk0, cu_seqlens ? seg0 : nullptr, nullptr, nseq, seq_len, (int)lay.L};
+  uint8_t* tfrag = work + lay.off_tfrag;
+  float* knorm = (float*)(work + lay.off_knorm);
+  int* warm = (int*)(work + lay.off_warm);
+  const int64_t items = total_chunks * Hv;
+  const unsigned gi = (unsigned)((items + 3) / 4);
+  if (beta_dtype == GDN_BF16)
+    inv_kernel<uint16_t><<<gi, pf::NT, 0, st>>>((const uint16_t*)k, k_stride, g, (const uint16_t*)beta, cu_seqlens,
+                                                seq_chunk0, nseq, seq_len, items, Hqk, Hv, use_qk_l2norm, tfrag,
+                                                knorm, tab, warm);
+  else
+    inv_kernel<float><<<gi, pf::NT, 0, st>>>((const uint16_t*)k, k_stride, g, (const float*)beta, cu_seqlens,
+                                             seq_chunk0, nseq, seq_len, items, Hqk, Hv, use_qk_l2norm, tfrag, knorm,
+                                             tab, warm);
+  int rc = check_launch("gdn_chunk_prefill_inverse(inverse)");
+  if (rc) return rc;
+  inv_records_expand_kernel<<<gi, 256, 0, st>>>(tfrag, knorm, items, t_out, use_qk_l2norm ? factor_out : nullptr);
+  return check_launch("gdn_chunk_prefill_inverse(expand)");
 }
 
 extern "C" int gdn_conv_prefill_rows(const void* x, int64_t x_stride, const void* weight, const void* bias,
@@ -2248,10 +2146,25 @@ extern "C" int gdn_prefill_layer_rows(const void* mixed, int64_t mixed_stride, c
   const LayerLayout lay = layer_layout(total_tokens, total_chunks, nseq, Hk, Hv, D);
   GDN_REQUIRE(workspace && aligned(workspace, 256) && workspace_bytes >= lay.bytes,
               "gdn_prefill_layer: workspace missing, misaligned or smaller than %lld bytes", (long long)lay.bytes);
-  if (nseq == 0) return GDN_OK;
-  hipStream_t st = (hipStream_t)stream;
   uint8_t* work = (uint8_t*)workspace;
   uint16_t* conv_out = (uint16_t*)work;
+  const GateArgs gate{(const uint16_t*)z, z_stride, norm_w, eps};
+  const int64_t kd = (int64_t)Hk * D;
+  auto rule = [&](bool check_only) {  // the chunked rule on the prologue's outputs
+    return chunk_prefill_impl(conv_out, C, conv_out + kd, C, conv_out + 2 * kd, C, (float*)(work + lay.off_g),
+                              work + lay.off_beta, GDN_BF16, initial_state, final_state, state_rows, n_rows, out,
+                              total_tokens, cu_seqlens, seq_chunk0, total_chunks, nseq, seq_len, Hk, Hv, D, GDN_BF16,
+                              1, work + lay.off_chunk, workspace_bytes - lay.off_chunk, stream, gate,
+                              norm_w_dtype == GDN_BF16 ? 1 : 2, cu_seqlens != nullptr, check_only);
+  };
+  // every check of the chunked rule runs before the first launch: a refusal leaves the conv state
+  // and the slot rows untouched
+  {
+    const int rc = rule(true);
+    if (rc) return rc;
+  }
+  if (nseq == 0) return GDN_OK;
+  hipStream_t st = (hipStream_t)stream;
   uint16_t* beta = (uint16_t*)(work + lay.off_beta);
   float* g = (float*)(work + lay.off_g);
   uint8_t* chunk_ws = work + lay.off_chunk;
@@ -2320,10 +2233,5 @@ extern "C" int gdn_prefill_layer_rows(const void* mixed, int64_t mixed_stride, c
     int rc = check_launch("gdn_prefill_layer(state)");
     if (rc) return rc;
   }
-  const GateArgs gate{(const uint16_t*)z, z_stride, norm_w, eps};
-  const int64_t kd = (int64_t)Hk * D;
-  return chunk_prefill_impl(conv_out, C, conv_out + kd, C, conv_out + 2 * kd, C, g, beta, GDN_BF16, initial_state,
-                            final_state, state_rows, n_rows, out, total_tokens, cu_seqlens, seq_chunk0, total_chunks,
-                            nseq, seq_len, Hk, Hv, D, GDN_BF16, 1, chunk_ws, workspace_bytes - lay.off_chunk, stream,
-                            gate, norm_w_dtype == GDN_BF16 ? 1 : 2, cu_seqlens != nullptr);
+  return rule(false);
 }

@@ -5,10 +5,11 @@ signature is HF's ``torch_chunk_gated_delta_rule`` (HF modeling_qwen3_5.py:249-2
 (src/gdn_chunk_fast2.py:11) runs the same kernel (gdn_chunk_fast2.py).  Semantics kept: q, k are
 l2-normalised in their own dtype when ``use_qk_l2norm_in_kernel``, q is scaled by d^-1/2, the
 sequence is processed in chunks of 64 with an fp32 running state, the output has query's dtype and
-the final state is fp32.  Supported subset of the reference's arguments: chunk_size 64, bf16
-query/key/value, head dim 128 (the kernels' bf16 MFMA tiles); anything else raises ValueError
-before any GPU work (the reference also takes fp32 inputs, other head dims and chunk sizes --
-every chunk size computes the same recurrence, so a caller passes 64).
+the final state is fp32.  Like the reference it takes any float dtype of q/k/v (fp32, bf16, fp16), head
+dims d_k, d_v in {16, 32, 64, 128} and any chunk_size: bf16 q/k/v with d_k = d_v = 128 (the model's
+shape) run on the segment-parallel bf16 MFMA kernels, everything else on the generic fp32 kernel
+(gdn_chunk_prefill_generic).  Both compute with 64-token chunks: every chunk size gives the same
+recurrence in exact arithmetic (the reference's chunk_size only changes its fp32 rounding order).
 Added beyond the reference: ``cu_seqlens`` (int32 [n_seq+1]) for packed varlen batches
 ([1, sum T, H, d] inputs, [n_seq, H_v, d, d] states), the form HF forwards as ``cu_seq_lens_q``.
 
@@ -124,22 +125,26 @@ def _check_rows(state_rows, nseq, n_rows, device):
     return Rows(state_rows, nseq, n_rows, device).dev
 
 
-SUPPORTED = "chunk_size 64, bfloat16 query/key/value, head dim 128"
+FAST = "bfloat16 query/key/value with head dims 128"
+DIMS = (16, 32, 64, 128)
+FLOATS = (torch.float32, torch.bfloat16, torch.float16)
 
 
 def check_chunk_args(query, key, value, chunk_size):
-    """The supported subset of the reference's arguments (src/gdn_chunk_fast2.py:11-19 accepts any
-    float dtype, head dim and chunk size): the kernels take 64-token chunks of bf16 q/k/v with
-    head dim 128 (bf16 MFMA operands).  Anything else raises ValueError before any GPU work."""
-    if chunk_size != CHUNK:
-        raise ValueError(f"chunk_gated_delta_rule: chunk_size={chunk_size} is not supported ({SUPPORTED}); "
-                         f"every chunk size computes the same recurrence, call it with chunk_size=64")
-    if not (query.dtype == key.dtype == value.dtype == torch.bfloat16):
+    """The reference's argument domain (src/gdn_chunk_fast2.py:11-29): q/k/v of one float dtype
+    (fp32, bf16 or fp16), d_k = q/k's last dim and d_v = v's in {16, 32, 64, 128}, chunk_size a
+    positive integer (computed with 64-token chunks: the same recurrence).  Returns True when the
+    call takes the segment-parallel bf16 kernels (bf16, d_k = d_v = 128), False for the generic
+    fp32 kernel; anything outside the domain raises ValueError before any GPU work."""
+    if not isinstance(chunk_size, int) or isinstance(chunk_size, bool) or chunk_size < 1:
+        raise ValueError(f"chunk_gated_delta_rule: chunk_size must be a positive integer, got {chunk_size!r}")
+    if not (query.dtype == key.dtype == value.dtype) or query.dtype not in FLOATS:
         raise ValueError(f"chunk_gated_delta_rule: query/key/value dtypes {query.dtype}/{key.dtype}/{value.dtype} "
-                         f"are not supported ({SUPPORTED})")
-    if query.dim() != 4 or query.shape[-1] != 128 or value.shape[-1] != 128:
-        raise ValueError(f"chunk_gated_delta_rule: head dim {query.shape[-1]} / {value.shape[-1]} is not supported "
-                         f"({SUPPORTED})")
+                         f"are not supported (one of float32, bfloat16, float16 for all three)")
+    if query.dim() != 4 or query.shape[-1] not in DIMS or value.shape[-1] not in DIMS:
+        raise ValueError(f"chunk_gated_delta_rule: head dims {query.shape[-1]} / {value.shape[-1]} are not supported "
+                         f"(d_k, d_v in {DIMS})")
+    return query.dtype == torch.bfloat16 and query.shape[-1] == 128 and value.shape[-1] == 128
 
 
 def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size=64, initial_state=None,
@@ -157,22 +162,30 @@ def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size=64, initial_st
     ``norm_gate`` = (z, norm_weight, eps), z bf16 [B*T, >= Hv*d] rows with unit inner stride (head h
     of token t at z[t, h*d:(h+1)*d]) and norm_weight [d] bf16 or fp32, the returned rows are
     gated_rmsnorm(out, z, norm_weight, eps) -- computed by the output kernel before the store."""
-    check_chunk_args(query, key, value, chunk_size)
+    fast = check_chunk_args(query, key, value, chunk_size)
     _lib.require_cuda(query, key, value, g, beta, initial_state)
     B, T, Hqk, D = query.shape
-    Hv = value.shape[2]
-    if key.shape != query.shape or tuple(value.shape) != (B, T, Hv, D):
+    Hv, Dv = value.shape[2], value.shape[3]
+    if key.shape != query.shape or tuple(value.shape[:2]) != (B, T):
         raise ValueError(f"chunk_gated_delta_rule: shape mismatch q{tuple(query.shape)} "
                          f"k{tuple(key.shape)} v{tuple(value.shape)}")
+    if Hv % Hqk:
+        raise ValueError(f"chunk_gated_delta_rule: value heads {Hv} not a multiple of query/key heads {Hqk}")
     if tuple(g.shape) != (B, T, Hv) or tuple(beta.shape) != (B, T, Hv):
         raise ValueError("chunk_gated_delta_rule: g and beta must be [B, T, Hv]")
+    if norm_gate is not None and not fast:
+        raise ValueError(f"chunk_gated_delta_rule: the fused output norm needs {FAST}")
     dev = query.device
-    cu, seq_chunk0, nseq, seq_len, total_chunks = _chunk_table(B, T, cu_seqlens, dev)
+    if fast:
+        cu, seq_chunk0, nseq, seq_len, total_chunks = _chunk_table(B, T, cu_seqlens, dev)
+    else:  # the generic kernel walks each sequence itself: no chunk table
+        cu, nseq, seq_len = _seq_args(B, T, cu_seqlens, dev)
+        seq_chunk0, total_chunks = None, 0
     q, qs = _tokens_view(query, "query")
     k, ks = _tokens_view(key, "key")
     v, vs = _tokens_view(value, "value")
     g32 = g.to(torch.float32).contiguous()
-    if beta.dtype not in (torch.float32, torch.bfloat16):
+    if beta.dtype not in ((torch.float32, torch.bfloat16) if fast else FLOATS):
         beta = beta.to(torch.float32)
     beta = beta.contiguous()
     rows, n_rows = None, nseq
@@ -181,20 +194,26 @@ def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size=64, initial_st
             raise ValueError("chunk_gated_delta_rule: state_rows needs final_state_out (the slot buffer)")
         n_rows = final_state_out.shape[0]
         for name, t in (("final_state_out", final_state_out), ("initial_state", initial_state)):
-            if t is not None and (tuple(t.shape) != (n_rows, Hv, D, D) or t.dtype != torch.float32
+            if t is not None and (tuple(t.shape) != (n_rows, Hv, D, Dv) or t.dtype != torch.float32
                                   or not t.is_contiguous() or t.device != dev):
                 raise ValueError(f"chunk_gated_delta_rule: {name} must be a contiguous fp32 "
-                                 f"[{n_rows},{Hv},{D},{D}] slot buffer on {dev}")
+                                 f"[{n_rows},{Hv},{D},{Dv}] slot buffer on {dev}")
         rows = _check_rows(state_rows, nseq, n_rows, dev)
         init, final = initial_state, final_state_out
     else:
         init = None
         if initial_state is not None:
-            if tuple(initial_state.shape) != (nseq, Hv, D, D):
-                raise ValueError(f"chunk_gated_delta_rule: initial_state must be [{nseq},{Hv},{D},{D}]")
+            if tuple(initial_state.shape) != (nseq, Hv, D, Dv):
+                raise ValueError(f"chunk_gated_delta_rule: initial_state must be [{nseq},{Hv},{D},{Dv}]")
             init = initial_state.to(torch.float32).contiguous()
-        final = torch.empty(nseq, Hv, D, D, dtype=torch.float32, device=dev) if output_final_state else None
-    out = torch.empty(B, T, Hv, D, dtype=query.dtype, device=dev)
+        final = torch.empty(nseq, Hv, D, Dv, dtype=torch.float32, device=dev) if output_final_state else None
+    out = torch.empty(B, T, Hv, Dv, dtype=query.dtype, device=dev)
+    if not fast:
+        _lib.call("gdn_chunk_prefill_generic", _lib.ptr(q), qs, _lib.ptr(k), ks, _lib.ptr(v), vs, _lib.ptr(g32),
+                  _lib.ptr(beta), _lib.dtype_code(beta), _lib.ptr(init), _lib.ptr(final), _lib.ptr(rows), n_rows,
+                  _lib.ptr(out), B * T, _lib.ptr(cu), nseq, seq_len, Hqk, Hv, D, Dv, _lib.dtype_code(query),
+                  int(bool(use_qk_l2norm_in_kernel)), _lib.stream_of(query))
+        return out, final
     wbytes = int(_lib.lib().gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hv))
     work = torch.empty(max(wbytes, 1), dtype=torch.uint8, device=dev)
     args = (_lib.ptr(q), qs, _lib.ptr(k), ks, _lib.ptr(v), vs, _lib.ptr(g32), _lib.ptr(beta),
@@ -227,9 +246,9 @@ def fast_chunk_gated_delta_rule(query, key, value, g, beta, chunk_size=64, initi
 
 
 def _unit_lower_inv(X, base=16):
-    """(I - X)^-1 for strictly lower X [..., 64, 64] fp32 on the GPU: the kernel's blocked inverse
-    (16x16 diagonal blocks by forward substitution, fp32 MFMA block merges), the algorithm of
-    src/gdn_chunk_fast.py:33-62."""
+    """(I - X)^-1 for strictly lower X [..., 64, 64] fp32 on the GPU, by the routine the chunked
+    prefill's inverse kernel runs (reg_inv64: 16x16 diagonal blocks by forward substitution, the
+    blocks below them on the fp32 MFMA, in registers), the blocking of src/gdn_chunk_fast.py:33-62."""
     _lib.require_cuda(X)
     if X.shape[-1] != 64 or X.shape[-2] != 64:
         raise ValueError("_unit_lower_inv: the kernel inverts 64x64 blocks")
@@ -238,6 +257,38 @@ def _unit_lower_inv(X, base=16):
     batch = Xf.numel() // (64 * 64)
     _lib.call("gdn_unit_lower_inv", _lib.ptr(Xf), _lib.ptr(out), batch, 64, _lib.stream_of(Xf))
     return out
+
+
+def chunk_inverse_records(key, g, beta, use_qk_l2norm_in_kernel=True, cu_seqlens=None, num_v_heads=None):
+    """What the chunked prefill's first kernel hands to its output pass, dense (for checking it on
+    its own): returns (T [n_chunks, Hv, 64, 64] fp32, factors [n_chunks, Hv, 64] fp32 | None).
+    T[c, h, i, j] = (I - X)^-1[i, j] beta_j of chunk c, head h (X = -(beta_i k_i.k_j
+    e^{G_i - G_j})_{i>j}), the bf16 values the kernel stores; factors = the K rows' l2norm factors
+    bf16(rsqrt(sum k^2 + 1e-6)).  Chunks are numbered sequence by sequence.  key [B, T, Hk, 128]
+    bf16, g [B, T, Hv] (fp32), beta [B, T, Hv] (bf16 or fp32).  src/gdn_chunk_fast2.py:31-43."""
+    _lib.require_cuda(key, g, beta)
+    B, T, Hk, D = key.shape
+    Hv = g.shape[-1] if num_v_heads is None else num_v_heads
+    if key.dtype != torch.bfloat16 or D != 128:
+        raise ValueError("chunk_inverse_records: key must be bf16 with head dim 128")
+    if tuple(g.shape) != (B, T, Hv) or tuple(beta.shape) != (B, T, Hv) or Hv % Hk:
+        raise ValueError("chunk_inverse_records: g, beta must be [B, T, Hv] with Hv a multiple of Hk")
+    dev = key.device
+    cu, seq_chunk0, nseq, seq_len, total_chunks = _chunk_table(B, T, cu_seqlens, dev)
+    k, ks = _tokens_view(key, "key")
+    g32 = g.to(torch.float32).contiguous()
+    if beta.dtype not in (torch.float32, torch.bfloat16):
+        beta = beta.to(torch.float32)
+    beta = beta.contiguous()
+    t_out = torch.empty(total_chunks, Hv, 64, 64, dtype=torch.float32, device=dev)
+    f_out = torch.empty(total_chunks, Hv, 64, dtype=torch.float32, device=dev) if use_qk_l2norm_in_kernel else None
+    wbytes = int(_lib.lib().gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hv))
+    work = torch.empty(max(wbytes, 1), dtype=torch.uint8, device=dev)
+    _lib.call("gdn_chunk_prefill_inverse", _lib.ptr(k), ks, _lib.ptr(g32), _lib.ptr(beta), _lib.dtype_code(beta),
+              B * T, _lib.ptr(cu), _lib.ptr(seq_chunk0), total_chunks, nseq, seq_len, Hk, Hv, D, _lib.BF16,
+              int(bool(use_qk_l2norm_in_kernel)), _lib.ptr(t_out), _lib.ptr(f_out), _lib.ptr(work), wbytes,
+              _lib.stream_of(key))
+    return t_out, f_out
 
 
 def causal_conv1d_prefill(x, weight, bias=None, history=None, cu_seqlens=None, state_rows=None, state_out=None):
@@ -328,8 +379,10 @@ def gdn_prefill_core(mixed_qkv, z, a, b, conv_weight, A_log, dt_bias, norm_weigh
     Hk, Hv, D = num_k_heads, num_v_heads, head_dim
     if C != (2 * Hk + Hv) * D:
         raise ValueError(f"gdn_prefill_core: C={C} != (2*{Hk}+{Hv})*{D}")
-    if chunk_size != CHUNK or D != 128:
-        raise ValueError(f"gdn_prefill_core: supports {SUPPORTED}")
+    if not isinstance(chunk_size, int) or chunk_size < 1:
+        raise ValueError(f"gdn_prefill_core: chunk_size must be a positive integer, got {chunk_size!r}")
+    if D != 128:
+        raise ValueError(f"gdn_prefill_core: the fused layer takes head dim 128 (got {D})")
     if mixed_qkv.dtype != torch.bfloat16 or conv_weight.dtype != torch.bfloat16:
         raise TypeError("gdn_prefill_core: mixed_qkv and conv_weight must be bfloat16")
     dev = mixed_qkv.device
@@ -350,6 +403,15 @@ def gdn_prefill_core(mixed_qkv, z, a, b, conv_weight, A_log, dt_bias, norm_weigh
         raise ValueError(f"gdn_prefill_core: z must be bf16 [{T}, >= {Hv * D}]")
     if z2.stride(1) != 1 or z2.stride(0) % 8 or z2.data_ptr() % 16:
         z2 = z2.contiguous()
+    if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
+        raise TypeError(f"gdn_prefill_core: a and b must be bfloat16 (got {a.dtype}, {b.dtype})")
+    if a.numel() != T * Hv or b.numel() != T * Hv:
+        raise ValueError(f"gdn_prefill_core: a and b must hold [{T}, {Hv}] values")
+    if A_log.numel() != Hv or dt_bias.numel() != Hv:
+        raise ValueError(f"gdn_prefill_core: A_log and dt_bias must hold {Hv} values "
+                         f"(got {A_log.numel()}, {dt_bias.numel()})")
+    if conv_bias is not None and conv_bias.numel() != C:
+        raise ValueError(f"gdn_prefill_core: conv_bias must hold C={C} values (got {conv_bias.numel()})")
     a2 = a if a.dim() == 2 else a.reshape(T, Hv)
     b2 = b if b.dim() == 2 else b.reshape(T, Hv)
     if a2.stride() != b2.stride() or a2.stride(-1) != 1:

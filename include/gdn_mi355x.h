@@ -7,7 +7,8 @@
  * allocates, never synchronises the host, and is therefore safe inside hipGraph stream capture.
  * Tensors are dense row-major unless a stride argument says otherwise; strides are in elements.
  *
- * Dtype codes: GDN_F32 = 0, GDN_BF16 = 1.  bf16 is stored as the upper 16 bits of an IEEE fp32.
+ * Dtype codes: GDN_F32 = 0, GDN_BF16 = 1, GDN_F16 = 2 (IEEE half; taken by gdn_chunk_prefill_generic
+ * only).  bf16 is stored as the upper 16 bits of an IEEE fp32.
  * Return value: 0 on success, otherwise a GDN_E* code; gdn_last_error() then returns a message
  * (thread-local, valid until the next call on the same thread).
  *
@@ -24,7 +25,7 @@
 extern "C" {
 #endif
 
-enum { GDN_F32 = 0, GDN_BF16 = 1 };
+enum { GDN_F32 = 0, GDN_BF16 = 1, GDN_F16 = 2 };
 enum {
   GDN_OK = 0,
   GDN_EINVAL = 1,   /* bad shape, dtype, stride, alignment or null pointer */
@@ -105,11 +106,51 @@ int gdn_decode_fused(const void* mixed, int64_t mixed_stride, const void* z, int
 
 /*
  * (I - X)^{-1} for a batch of strictly lower-triangular 64x64 fp32 matrices (only the strictly
- * lower part of X is read).  The intra-chunk inverse of the chunked rule.
+ * lower part of X is read), by the routine the chunked prefill's inverse kernel runs (reg_inv64:
+ * the four 16x16 diagonal blocks by forward substitution, the blocks below them on the fp32 MFMA,
+ * in registers, one wave per matrix).
  * Replaces _unit_lower_inv / _small_unit_lower_inv (src/gdn_chunk_fast.py:21-62).
- *   X, T [batch, 64, 64] fp32;  n must be 64.
+ *   X, T [batch, 64, 64] fp32, 16-byte aligned;  n must be 64.
  */
 int gdn_unit_lower_inv(const float* X, float* T, int64_t batch, int n, void* stream);
+
+/*
+ * The chunked prefill's first kernel alone (gdn_chunk_prefill's arguments for k, g, beta and the
+ * sequence table; bf16 keys, D = 128): for every (chunk, value head) the T diag(beta) it hands to
+ * the output pass, expanded to dense fp32 (t_out [total_chunks, Hv, 64, 64]: row i, column j =
+ * T[i][j] beta_j of the chunk's X = -(beta_i k_i.k_j e^{G_i - G_j})_{i>j}, T = (I - X)^{-1}, as the
+ * bf16 value stored), and with use_qk_l2norm the K rows' l2norm factors bf16(rsqrt(...))
+ * (factor_out [total_chunks, Hv, 64] or NULL).  Chunks are numbered as seq_chunk0 numbers them.
+ * The state-independent part of src/gdn_chunk_fast2.py:31-43 (attn = _unit_lower_inv(X), times
+ * diag(beta) as v_beta and k_beta carry it); it exposes what the hot path computes so that it can
+ * be checked on its own.  workspace: gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hv).
+ */
+int gdn_chunk_prefill_inverse(const void* k, int64_t k_stride, const float* g, const void* beta,
+                              int beta_dtype, int64_t total_tokens, const int32_t* cu_seqlens,
+                              const int32_t* seq_chunk0, int64_t total_chunks, int nseq, int seq_len,
+                              int Hqk, int Hv, int D, int in_dtype, int use_qk_l2norm, float* t_out,
+                              float* factor_out, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Chunked gated delta rule for any head dims and input dtype, in fp32 throughout (fp32 MFMA):
+ * fast_chunk_gated_delta_rule_v2 (src/gdn_chunk_fast2.py:11-62) takes any float dtype, d_k and
+ * d_v; this is that general form (gdn_chunk_prefill takes it for everything but bf16 q/k/v with
+ * D = 128, which has the segment-parallel kernels).  It walks each sequence's 64-token chunks in
+ * order, one workgroup per (sequence, value head, 64 value columns); no workspace.
+ *   q, k [total_tokens, Hqk, Dk], v [total_tokens, Hv, Dv] in in_dtype (GDN_F32, GDN_BF16 or
+ *   GDN_F16), token strides q_stride / k_stride / v_stride;  Dk, Dv in {16, 32, 64, 128};
+ *   g [total_tokens, Hv] fp32;  beta [total_tokens, Hv] (beta_dtype: GDN_F32, GDN_BF16, GDN_F16);
+ *   initial_state / final_state [n_rows, Hv, Dk, Dv] fp32 or NULL, rows as gdn_chunk_prefill_rows
+ *   (state_rows NULL: row s, n_rows = nseq);  out [total_tokens, Hv, Dv] in in_dtype (dense);
+ *   cu_seqlens device int32 [nseq+1] or NULL (nseq sequences of seq_len tokens).
+ *   use_qk_l2norm: q, k l2-normalised in in_dtype first (each op rounded to in_dtype, as torch).
+ */
+int gdn_chunk_prefill_generic(const void* q, int64_t q_stride, const void* k, int64_t k_stride,
+                              const void* v, int64_t v_stride, const float* g, const void* beta,
+                              int beta_dtype, const float* initial_state, float* final_state,
+                              const int32_t* state_rows, int n_rows, void* out, int64_t total_tokens,
+                              const int32_t* cu_seqlens, int nseq, int seq_len, int Hqk, int Hv, int Dk,
+                              int Dv, int in_dtype, int use_qk_l2norm, void* stream);
 
 /*
  * Bytes of device workspace gdn_chunk_prefill needs for `total_chunks` 64-token chunks of `nseq`
@@ -127,6 +168,8 @@ int64_t gdn_chunk_prefill_workspace_bytes(int64_t total_chunks, int nseq, int Hv
  * torch_chunk_gated_delta_rule (HF:249-260).
  *   q, k [total_tokens, Hqk, D] bf16, token stride q_stride / k_stride (value head h reads key
  *        head h / (Hv / Hqk));  v [total_tokens, Hv, D] bf16, token stride v_stride
+ *        (other dtypes and D in {16, 32, 64}: the call runs gdn_chunk_prefill_generic, and the
+ *        chunk table and workspace arguments are not used)
  *   g [total_tokens, Hv] fp32 (log decay);  beta [total_tokens, Hv] (beta_dtype)
  *   initial_state / final_state [nseq, Hv, D, D] fp32, 16-byte aligned, either may be NULL
  *     (zero / not written)

@@ -29,7 +29,8 @@ def test_header_declares_entry_points():
                  "gdn_decode_fused_masked", "gdn_chunk_prefill_rows", "gdn_conv_prefill_rows",
                  "gdn_decode_linear", "gdn_decode_linear_workspace_bytes", "gdn_decode_linear_pack",
                  "gdn_decode_linear_packed", "gdn_add_rmsnorm", "gdn_chunk_prefill_rows_gated",
-                 "gdn_prefill_layer_rows", "gdn_prefill_layer_workspace_bytes", "gdn_chunk_prefill_noalloc"):
+                 "gdn_prefill_layer_rows", "gdn_prefill_layer_workspace_bytes", "gdn_chunk_prefill_noalloc",
+                 "gdn_chunk_prefill_generic", "gdn_chunk_prefill_inverse"):
         assert name in syms
 
 
@@ -89,6 +90,27 @@ def test_version_limits_and_error_path(lib):
     assert rc == 1 and b"null" in h.gdn_last_error()
     need = h.gdn_chunk_prefill_workspace_bytes(10, 1, 32)
     assert need > 0 and need % 256 == 0
+    # the generic chunked rule: head dims 16 / 32 / 64 / 128 only, a known dtype, consistent sizes
+    rc = h.gdn_chunk_prefill_generic(p, 256, p, 256, p, 256, p, p, 0, None, None, None, 1, p, 64, None, 1, 64, 2,
+                                     2, 96, 64, 0, 1, None)
+    assert rc == 2 and b"d_k 96" in h.gdn_last_error()
+    rc = h.gdn_chunk_prefill_generic(p, 256, p, 256, p, 256, p, p, 0, None, None, None, 1, p, 64, None, 1, 64, 2,
+                                     2, 64, 64, 7, 1, None)
+    assert rc == 1 and b"dtype" in h.gdn_last_error()
+    rc = h.gdn_chunk_prefill_generic(p, 256, p, 256, p, 256, p, p, 0, None, None, None, 1, p, 65, None, 1, 64, 2,
+                                     2, 64, 64, 0, 1, None)
+    assert rc == 1 and b"nseq*seq_len" in h.gdn_last_error()
+    # gdn_chunk_prefill hands other dtypes and head dims to the generic rule (whose checks then run)
+    rc = h.gdn_chunk_prefill(p, 0, p, 0, p, 0, p, p, 1, None, None, p, 64, None, None, 1, 1, 64, 16, 32, 96, 0, 1,
+                             p, 1 << 30, None)
+    assert rc == 2 and b"gdn_chunk_prefill_generic: d_k 96" in h.gdn_last_error()
+    # the inverse kernel alone: bf16 keys at D = 128 only, and a workspace
+    rc = h.gdn_chunk_prefill_inverse(p, 256, p, p, 1, 64, None, None, 1, 1, 64, 2, 2, 64, 1, 1, p, None, p, 1 << 30,
+                                     None)
+    assert rc == 2 and b"D = 128" in h.gdn_last_error()
+    rc = h.gdn_chunk_prefill_inverse(p, 256, p, p, 1, 64, None, None, 1, 1, 64, 2, 2, 128, 1, 1, p, None, p, 16,
+                                     None)
+    assert rc == 1 and b"workspace" in h.gdn_last_error()
     with pytest.raises(lib.GDNError):
         lib.call("gdn_gated_rmsnorm", None, 0, None, 0, None, 1, None, 1, 128, ctypes.c_float(1e-6), None)
 
@@ -107,9 +129,9 @@ def test_prefill_layer_entry_host_checks(lib):
     p = ctypes.c_void_p(256)
     eps = ctypes.c_float(1e-6)
 
-    def call(mixed=p, z=p, D_=D, ws=need, z_stride=Hv * D, n_rows=nseq):
+    def call(mixed=p, z=p, D_=D, ws=need, z_stride=Hv * D, n_rows=nseq, cu=p, chunk0=p, seq_len=0, nch_=nch):
         return h.gdn_prefill_layer_rows(mixed, C, z, z_stride, p, p, Hv, p, None, p, p, p, 1, eps, None, p, None, p,
-                                        None, n_rows, p, T, p, p, nch, nseq, 0, Hk, Hv, D_, K, p, ws, None)
+                                        None, n_rows, p, T, cu, chunk0, nch_, nseq, seq_len, Hk, Hv, D_, K, p, ws, None)
 
     assert call(mixed=None) == 1 and b"null" in h.gdn_last_error()
     assert call(D_=64) == 2 and b"head dim" in h.gdn_last_error()
@@ -117,3 +139,8 @@ def test_prefill_layer_entry_host_checks(lib):
     assert call(z_stride=Hv * D - 8) == 1 and b"gate rows" in h.gdn_last_error()
     assert call(n_rows=nseq + 1) == 1 and b"n_rows" in h.gdn_last_error()
     assert call(ws=need - 256) == 1 and b"workspace" in h.gdn_last_error()
+    # the chunked rule's own checks run before the prologue launch (which would already overwrite the
+    # conv state): packed sequences without their chunk table, a uniform batch whose chunk count does
+    # not match its length -- refused on the host, no launch (a launch would fail here: no GPU)
+    assert call(chunk0=None) == 1 and b"seq_chunk0" in h.gdn_last_error()
+    assert call(cu=None, chunk0=None, seq_len=T // nseq) == 1 and b"total_chunks" in h.gdn_last_error()

@@ -161,6 +161,51 @@ def test_chunk_prefill_slow_decay_state_accuracy(gdn, oracle, dev):
     assert rel_l2(o, o_ref) <= OUT_TOL and rel_l2(s, s_ref) <= STATE_TOL
 
 
+# Heads whose state keeps a long memory (near-zero decay) or grows (g > 0) accumulate the bf16
+# roundings of the W S product (W and the bf16 copy of S, ~2^-9 each) over that memory.  A CPU
+# emulation of the kernel's roundings reproduces the GPU figures (1.46e-3 vs 1.68e-3 at decay 0.001,
+# T=8192; 6.66e-3 vs 6.68e-3 for the growing head) and shows that the W S product sets them: S as
+# bf16 hi + lo alone gives 1.22e-3, W and S in fp32 5.0e-4.  So these regimes are held to the
+# bounds below, above the 1e-3 of the benchmark decays (whose state error is ~1e-4).
+NEAR_ZERO_DECAY_STATE_TOL = 2.5e-3
+GROWING_STATE_TOL = 1e-2
+
+
+def test_chunk_prefill_positive_g_heads(gdn, oracle, dev):
+    """g > 0 (a growing state) on two of four value heads: the reference's decay e^{G_i - G_j} for
+    i > j (src/gdn_chunk_fast2.py:41) has no sign condition.  2048 tokens (several segments: the
+    growing heads take the exact summary path, the others warm up) and a one-chunk call.  Outputs
+    within 1e-2; states within 1e-3 for the decaying heads and GROWING_STATE_TOL for the growing
+    ones (head 1 grows ~e^8 over the 2048 tokens)."""
+    for T, seed in ((2048, 31), (100, 32)):
+        q, k, v, g, beta, s0 = _gdn_inputs(T, 2, 4, seed=seed)
+        g[..., 1] = -g[..., 1] * 0.02        # (0, 0.01] per token: the state grows up to ~e^8
+        g[..., 2] = -g[..., 2] * 0.005
+        o_ref, s_ref = oracle.chunk_gated_delta_rule_v2(_rep(q, 2), _rep(k, 2), v, g, beta, 64, s0, True, True)
+        o, s = gdn.fast_chunk_gated_delta_rule_v2(q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta.to(dev),
+                                                  initial_state=s0.to(dev), output_final_state=True,
+                                                  use_qk_l2norm_in_kernel=True)
+        for h in range(4):
+            tol = GROWING_STATE_TOL if h in (1, 2) else STATE_TOL
+            assert rel_l2(o[:, :, h], o_ref[:, :, h]) <= OUT_TOL, f"T {T} value head {h}"
+            assert rel_l2(s[:, h], s_ref[:, h]) <= tol, (T, h, rel_l2(s[:, h], s_ref[:, h]))
+
+
+@pytest.mark.parametrize("T", [8192, 32768])
+def test_chunk_prefill_near_zero_decay_long(gdn, oracle, dev, T):
+    """Near-zero decay (g ~ -0.002 per token: the state keeps ~500 tokens of memory) over long
+    sequences, two value heads of one key head: outputs within 1e-2, final state within
+    NEAR_ZERO_DECAY_STATE_TOL (measured 1.68e-3 at both lengths)."""
+    q, k, v, g, beta, s0 = _gdn_inputs(T, 1, 2, seed=40 + T % 7, decay=0.001)
+    o_ref, s_ref = oracle.chunk_gated_delta_rule_v2(_rep(q, 2), _rep(k, 2), v, g, beta, 64, s0, True, True)
+    o, s = gdn.fast_chunk_gated_delta_rule_v2(q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta.to(dev),
+                                              initial_state=s0.to(dev), output_final_state=True,
+                                              use_qk_l2norm_in_kernel=True)
+    for h in range(2):
+        assert rel_l2(o[:, :, h], o_ref[:, :, h]) <= OUT_TOL, (h, rel_l2(o[:, :, h], o_ref[:, :, h]))
+        assert rel_l2(s[:, h], s_ref[:, h]) <= NEAR_ZERO_DECAY_STATE_TOL, (h, rel_l2(s[:, h], s_ref[:, h]))
+
+
 def test_chunk_prefill_warm_up_and_exact_paths_per_head(gdn, oracle, dev):
     """Two packed sequences (2500 and 1596 tokens, 4-chunk segments at this size), one value head per
     path the kernel can take for a later segment's initial state: strong decay (a one-chunk warm-up

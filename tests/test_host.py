@@ -93,20 +93,25 @@ def test_decode_step_ops_refuse_cpu_tensors(gdn):
         cb.add_rms_norm(h, h, torch.zeros(256, dtype=bf))
 
 
-def test_chunk_rule_refuses_unsupported_arguments(gdn):
-    """chunk_size != 64, non-bf16 q/k/v and head dims other than 128 raise a ValueError naming the
-    supported subset, before any device work (the reference's v2 accepts them, src/gdn_chunk_fast2.py:11-19)."""
+def test_chunk_rule_argument_domain(gdn):
+    """The reference's v2 takes any float dtype, head dims and chunk size (src/gdn_chunk_fast2.py:11-29):
+    fp32 / bf16 / fp16 q/k/v with d_k, d_v in {16, 32, 64, 128} and any positive chunk_size pass the
+    argument checks and reach the device check (CPU tensors: no CPU fallback); mixed or other dtypes,
+    other head dims and a chunk size below 1 raise a ValueError naming the domain, before any device work."""
     bf = torch.bfloat16
     q = torch.zeros(1, 4, 2, 128, dtype=bf)
     g = torch.zeros(1, 4, 2)
     for fn in (gdn.fast_chunk_gated_delta_rule, gdn.fast_chunk_gated_delta_rule_v2):
-        with pytest.raises(ValueError, match="chunk_size=128 is not supported"):
-            fn(q, q, q, g, g, chunk_size=128)
+        for x, cs in ((q, 128), (q.float(), 64), (q.half(), 16), (torch.zeros(1, 4, 2, 64), 64)):
+            with pytest.raises(ValueError, match="no CPU fallback"):
+                fn(x, x, x, g, g, chunk_size=cs)
+        with pytest.raises(ValueError, match="chunk_size must be a positive integer"):
+            fn(q, q, q, g, g, chunk_size=0)
         qf = q.float()
         with pytest.raises(ValueError, match="dtypes .* are not supported"):
-            fn(qf, qf, qf, g, g)
-        with pytest.raises(ValueError, match="dtypes .* are not supported"):
             fn(q, q, qf, g, g)
-        q64 = torch.zeros(1, 4, 2, 64, dtype=bf)
-        with pytest.raises(ValueError, match="head dim 64"):
-            fn(q64, q64, q64, g, g)
+        with pytest.raises(ValueError, match="dtypes .* are not supported"):
+            fn(q.double(), q.double(), q.double(), g, g)
+        q96 = torch.zeros(1, 4, 2, 96, dtype=bf)
+        with pytest.raises(ValueError, match="head dims 96"):
+            fn(q96, q96, q96, g, g)

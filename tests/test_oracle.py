@@ -61,6 +61,17 @@ def test_config0_chunked_equals_token_recurrence(oracle):
     assert rel_l2(o_c, o_r) < 1e-5 and rel_l2(s_c, s_r) < 1e-5
 
 
+def test_positive_g_head_chunked_equals_token_recurrence(oracle):
+    """The reference's decay exp((G_i - G_j).tril()) (src/gdn_chunk_fast2.py:41) holds for any sign of g;
+    with one head growing (g > 0) the chunked rule still equals the token recurrence."""
+    q, k, v, g, beta = config0(seed=5)
+    g[..., 1] = -g[..., 1] * 0.02          # head 1: g in (0, 0.01], the state grows
+    o_c, s_c = oracle.chunk_gated_delta_rule_v2(q, k, v, g, beta, 64, None, True, False)
+    o_r, s_r = oracle.recurrent_gated_delta_rule(q, k, v, g, beta, None, True, False)
+    assert rel_l2(o_c, o_r) < 1e-5 and rel_l2(s_c, s_r) < 1e-5
+    assert s_r[:, 1].norm() > s_r[:, 0].norm()
+
+
 def test_chunked_matches_hf_chunk_and_recurrent(oracle):
     q, k, v, g, beta = config0(seed=3, T=200)
     s0 = 0.02 * torch.randn(1, 4, 64, 64)
