@@ -237,9 +237,11 @@ constexpr int NT = 512;                      // 8 waves
 constexpr int kMinSeg = 4;                   // shortest segment the host cuts (chunks)
 constexpr int kTargetItems = 256;            // segments x value heads the host aims for
 constexpr float kNegligibleLog = -44.3614f;  // ln(2^-64): a segment map A_j this small is not formed
-// A warm-up drops a map bounded by 2^-40 relative to the state before it: 2^16 below fp32's
-// rounding of the state it feeds, unless the state shrank by more than that over the warm-up.
-constexpr float kWarmLog = -27.7259f;        // ln(2^-40)
+// A warm-up drops a map bounded by 2^-16 relative to the state before it: 2^7 below the bf16
+// rounding (2^-9) of the W S and Q S operands the state passes through every chunk, so the dropped
+// part is lost in the rounding the chain makes anyway (unless the state shrank by more than 2^7 over
+// the warm-up: new tokens contributing under 1/128 of the state they replace).
+constexpr float kWarmLog = -11.0904f;        // ln(2^-16)
 constexpr int kTrans = 2 * pf::D * pf::D;    // floats per (slot, head): A, then B
 }  // namespace sg
 
@@ -385,7 +387,7 @@ __host__ __device__ __forceinline__ constexpr int offset(int f) {
 
 // Warm-up length for the transition after the segment ending with the chunk at token t_last (one
 // wave): the least w such that the summed log decay of the segment's last w chunks is below
-// ln 2^-40 -- the norm bound of the dropped map with unit keys and beta in [0, 1] -- or 0 when there
+// ln 2^-16 -- the norm bound of the dropped map with unit keys and beta in [0, 1] -- or 0 when there
 // is none within the segment's L chunks or a beta outside [0, 1] (or a NaN) comes first.  Chunks
 // are taken back from the segment's end, four at a time (lane = token).
 template <typename BetaT>
@@ -600,7 +602,7 @@ __global__ __launch_bounds__(pf::NT, 2) void inv_kernel(const uint16_t* __restri
 // Warm-up lengths.  The state entering segment j + 1 differs from the chain run from zero over the
 // last w chunks of segment j by the map of those w chunks applied to the state before them; with
 // unit keys and beta in [0, 1] that map's norm is at most exp(sum of g over the w chunks).  The
-// inverse kernel writes each transition slot's least w whose bound is below 2^-40 (0: none).  A
+// inverse kernel writes each transition slot's least w whose bound is below 2^-16 (0: none).  A
 // (sequence, value head) pair whose every slot has one runs no summaries and no combination, and
 // its later segments start from their warm-ups.  One wave reads the pair's slots, 64 at a time.
 __device__ bool seq_warm_ok(const SegTable& tab, const int* __restrict__ warm, int Hv, int h, int s) {
@@ -1719,11 +1721,21 @@ extern "C" int gdn_unit_lower_inv(const float* X, float* T, int64_t batch, int n
 }
 
 namespace {
-// Segment length (chunks) for a call: about sg::kTargetItems (segment, value head) items, at least
-// sg::kMinSeg chunks per segment.
-int64_t seg_len(int64_t total_chunks, int Hv) {
-  const int64_t work = total_chunks * (int64_t)Hv;
-  const int64_t L = (work + sg::kTargetItems - 1) / sg::kTargetItems;
+// Segment length (chunks) for a call: about sg::kTargetItems (segment, value head) items (one
+// workgroup per compute unit), at least sg::kMinSeg chunks per segment.  When the (sequence, value
+// head) pairs fit one round, each sequence gets m = kTargetItems / pairs segments of equal length:
+// the items then fill one round without spilling into a second (at T = 8192 with 48 value heads:
+// 5 segments of 26 chunks, 240 items; the work-based length, 24 chunks, gives 6 segments and 288
+// items, and the 32 past 256 run as a second round).  Beyond one round, the work-based length.
+int64_t seg_len(int64_t total_chunks, int nseq, int Hv) {
+  const int64_t pairs = (int64_t)nseq * Hv;
+  int64_t L;
+  if (pairs > 0 && pairs <= sg::kTargetItems) {
+    const int64_t parts = (int64_t)nseq * (sg::kTargetItems / pairs);
+    L = (total_chunks + parts - 1) / parts;
+  } else {
+    L = (total_chunks * (int64_t)Hv + sg::kTargetItems - 1) / sg::kTargetItems;
+  }
   return L < sg::kMinSeg ? sg::kMinSeg : L;
 }
 // Workspace layout: the segment table (nseq + 1 int32), the longest-first segment order (int32 per
@@ -1738,7 +1750,7 @@ struct SegLayout {
 SegLayout seg_layout(int64_t total_chunks, int nseq, int Hv) {
   auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
   SegLayout l;
-  l.L = seg_len(total_chunks, Hv);
+  l.L = seg_len(total_chunks, nseq, Hv);
   l.nslots = total_chunks / l.L;
   l.off_order = up(((int64_t)nseq + 1) * 4);
   l.off_flags = l.off_order + up(((int64_t)nseq + total_chunks / l.L) * 4);  // segments: <= nseq + chunks / L

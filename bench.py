@@ -8,8 +8,10 @@ a HIP graph and replayed.  A "step" is one replay (48 layers).  ``value`` is mic
 
 Also reported (``secondary``): chunked GDN prefill at T=8192 (B=1, H_k=16, H_v=32, d=128, bf16
 inputs, fp32 state) in tokens/s/layer with its bf16-MFMA and HBM fractions, the fused varlen
-prefill layer, T=32768, and whole decode steps at Qwen3.5-27B shape (the hybrid 64-layer stack,
-and its 48 GDN layers with projections) in tokens/s.
+prefill layer, T=32768, the chunked rule at Qwen3.5-27B's GDN shape (H_k=16, H_v=48) at T=8192 and
+353 tokens, and whole decode steps at Qwen3.5-27B shape (the hybrid 64-layer stack, and its 48 GDN
+layers with projections) in tokens/s.  CPU baselines (the oracle on the host's cores) for the
+decode step, T=8192, the varlen layer and T=32768.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-prefill]
                       [--only decode|prefill|prefill8192|hybrid|attention]
@@ -142,14 +144,14 @@ def _time(fn, reps, dev):
     return e0.elapsed_time(e1) * 1000.0 / reps
 
 
-def _gdn_inputs(T, seed, dev, nseq=1):
+def _gdn_inputs(T, seed, dev, nseq=1, hk=HK, hv=HV):
     g_ = torch.Generator(device="cpu").manual_seed(seed)
-    q = torch.randn(1, T, HK, D, generator=g_).to(torch.bfloat16).to(dev)
-    k = torch.randn(1, T, HK, D, generator=g_).to(torch.bfloat16).to(dev)
-    v = torch.randn(1, T, HV, D, generator=g_).to(torch.bfloat16).to(dev)
-    beta = torch.sigmoid(torch.randn(1, T, HV, generator=g_)).to(torch.bfloat16).to(dev)
-    g = (-torch.nn.functional.softplus(torch.randn(1, T, HV, generator=g_) + 2) * 0.1).to(dev)
-    s0 = (0.02 * torch.randn(nseq, HV, D, D, generator=g_)).to(dev)
+    q = torch.randn(1, T, hk, D, generator=g_).to(torch.bfloat16).to(dev)
+    k = torch.randn(1, T, hk, D, generator=g_).to(torch.bfloat16).to(dev)
+    v = torch.randn(1, T, hv, D, generator=g_).to(torch.bfloat16).to(dev)
+    beta = torch.sigmoid(torch.randn(1, T, hv, generator=g_)).to(torch.bfloat16).to(dev)
+    g = (-torch.nn.functional.softplus(torch.randn(1, T, hv, generator=g_) + 2) * 0.1).to(dev)
+    s0 = (0.02 * torch.randn(nseq, hv, D, D, generator=g_)).to(dev)
     return q, k, v, g, beta, s0
 
 
@@ -159,42 +161,73 @@ def _fractions(name, us, F, B, tokens):
                 flops=F, bytes=B)
 
 
-def bench_prefill(gdn, dev, T=8192, reps=5, seed=0):
-    """Chunked rule alone, B=1, T tokens, H_k=16 key heads read by H_v=32 value heads."""
-    q, k, v, g, beta, s0 = _gdn_inputs(T, seed, dev)
+def bench_prefill(gdn, dev, T=8192, reps=5, seed=0, hk=HK, hv=HV, note=None):
+    """Chunked rule alone, B=1, T tokens, hk key heads read by hv value heads (value head h reads key
+    head h // (hv / hk))."""
+    q, k, v, g, beta, s0 = _gdn_inputs(T, seed, dev, hk=hk, hv=hv)
     us = _time(lambda: gdn.fast_chunk_gated_delta_rule_v2(q, k, v, g, beta, initial_state=s0, output_final_state=True,
                                                           use_qk_l2norm_in_kernel=True), reps, dev)
-    return _fractions(f"chunked rule B=1 T={T} H_k={HK} H_v={HV} d={D} bf16", us, prefill_flops(T), prefill_bytes(T), T)
+    res = _fractions(f"chunked rule B=1 T={T} H_k={hk} H_v={hv} d={D} bf16", us, prefill_flops(T, hv=hv),
+                     prefill_bytes(T, hk=hk, hv=hv), T)
+    if note:
+        res["note"] = note
+    return res
 
 
-def bench_prefill_varlen(gdn, dev, reps=5, seed=2):
-    """Fused prefill layer (conv1d prefill + SiLU, l2norm, gating, chunked rule, gated RMSNorm) over
-    16 packed prompts with lengths uniform in [200, 1500], random initial states, zero conv history."""
+def _varlen_inputs(seed=2):
+    """16 packed prompts with lengths uniform in [200, 1500] (seeded), the layer's weights and states."""
     g_ = torch.Generator(device="cpu").manual_seed(seed)
     lens = torch.randint(200, 1501, (16,), generator=g_)
     cu = torch.zeros(17, dtype=torch.int32)
     cu[1:] = torch.cumsum(lens, 0)
     T = int(cu[-1])
-    mixed = torch.randn(T, C, generator=g_).to(torch.bfloat16).to(dev)
-    z = torch.randn(T, HV * D, generator=g_).to(torch.bfloat16).to(dev)
-    a = torch.randn(T, HV, generator=g_).to(torch.bfloat16).to(dev)
-    b = torch.randn(T, HV, generator=g_).to(torch.bfloat16).to(dev)
-    cw = (0.5 * torch.randn(C, KC, generator=g_)).to(torch.bfloat16).to(dev)
-    A_log = torch.full((HV,), -2.302585092994046, device=dev)
-    dt = torch.full((HV,), 2.0, device=dev)
-    nw = (1 + 0.02 * torch.randn(D, generator=g_)).to(torch.bfloat16).to(dev)
-    s0 = (0.02 * torch.randn(16, HV, D, D, generator=g_)).to(dev)
+    x = dict(mixed=torch.randn(T, C, generator=g_).to(torch.bfloat16),
+             z=torch.randn(T, HV * D, generator=g_).to(torch.bfloat16),
+             a=torch.randn(T, HV, generator=g_).to(torch.bfloat16),
+             b=torch.randn(T, HV, generator=g_).to(torch.bfloat16),
+             cw=(0.5 * torch.randn(C, KC, generator=g_)).to(torch.bfloat16),
+             A_log=torch.full((HV,), -2.302585092994046), dt=torch.full((HV,), 2.0),
+             nw=(1 + 0.02 * torch.randn(D, generator=g_)).to(torch.bfloat16),
+             s0=0.02 * torch.randn(16, HV, D, D, generator=g_))
+    return cu, T, x
+
+
+def bench_prefill_varlen(gdn, dev, reps=5, seed=2, cpu=False):
+    """Fused prefill layer (conv1d prefill + SiLU, l2norm, gating, chunked rule, gated RMSNorm) over
+    16 packed prompts with lengths uniform in [200, 1500], random initial states, zero conv history.
+    With cpu: the oracle's layer (its per-sequence loop, as the reference runs one sequence per call)
+    on the host's cores, one pass, as the CPU baseline."""
+    cu, T, x = _varlen_inputs(seed)
+    d = {n: t.to(dev) for n, t in x.items()}
     # lengths on the host, as a scheduler holds them: the batch's sequence table is checked and uploaded
-    # once per batch step (it is the same for every layer), so the layer never waits on the GPU
+    # once per batch step (it is the same for every layer), outside the timed layer calls
     table = gdn.Varlen(cu, T, dev)
-    us = _time(lambda: gdn.gdn_prefill_core(mixed, z, a, b, cw, A_log, dt, nw, HK, HV, D, cu_seqlens=table,
-                                            initial_state=s0), reps, dev)
-    return _fractions(f"fused prefill layer, 16 packed prompts ({T} tokens), H_k={HK} H_v={HV} d={D}", us,
-                      prefill_flops(T), prefill_layer_bytes(T, 16), T)
+    us = _time(lambda: gdn.gdn_prefill_core(d["mixed"], d["z"], d["a"], d["b"], d["cw"], d["A_log"], d["dt"],
+                                            d["nw"], HK, HV, D, cu_seqlens=table, initial_state=d["s0"]), reps, dev)
+    res = _fractions(f"fused prefill layer, 16 packed prompts ({T} tokens), H_k={HK} H_v={HV} d={D}", us,
+                     prefill_flops(T), prefill_layer_bytes(T, 16), T)
+    res["note"] = ("the batch's Varlen table (host checks + one pinned upload) is built once per batch step "
+                   "outside the timed layer calls")
+    if cpu:
+        oracle = importlib.import_module("oracle.gdn_oracle")
+        threads = len(os.sched_getaffinity(0))
+        torch.set_num_threads(threads)
+        t0 = time.perf_counter()
+        oracle.gdn_prefill_core(x["mixed"], x["z"], x["a"], x["b"], x["cw"], x["A_log"], x["dt"], x["nw"], HK, HV, D,
+                                cu_seqlens=cu, initial_state=x["s0"])
+        dt = time.perf_counter() - t0
+        model = cpu_model()
+        res["cpu_baseline"] = dict(value=round(T / dt), unit="tokens/s/layer", us_per_layer=round(dt * 1e6),
+                                   cores=threads, kind="port", cpu_model=model,
+                                   sample=f"oracle gdn_prefill_core (per-sequence loop) on the same 16 prompts "
+                                          f"({T} tokens), one pass, torch {torch.__version__} CPU, {threads} "
+                                          f"threads on {model}")
+    return res
 
 
 def bench_prefill_long(gdn, dev, T=32768, seed=3, check=True):
-    """B=1, T=32768: per-layer time and the final-state rel-L2 against the CPU oracle."""
+    """B=1, T=32768: per-layer time and the final-state rel-L2 against the CPU oracle, whose one pass
+    is also the CPU baseline."""
     q, k, v, g, beta, s0 = _gdn_inputs(T, seed, dev)
     run = lambda: gdn.fast_chunk_gated_delta_rule_v2(q, k, v, g, beta, initial_state=s0, output_final_state=True,
                                                      use_qk_l2norm_in_kernel=True)
@@ -203,15 +236,24 @@ def bench_prefill_long(gdn, dev, T=32768, seed=3, check=True):
                      prefill_bytes(T), T)
     if check:
         oracle = importlib.import_module("oracle.gdn_oracle")
-        torch.set_num_threads(len(os.sched_getaffinity(0)))
+        threads = len(os.sched_getaffinity(0))
+        torch.set_num_threads(threads)
         o, s = run()
         r = HV // HK
         oc = lambda x: x.cpu().repeat_interleave(r, dim=2)
-        o_ref, s_ref = oracle.chunk_gated_delta_rule_v2(oc(q), oc(k), v.cpu(), g.cpu(), beta.cpu(), 64, s0.cpu(),
-                                                        True, True)
+        args = (oc(q), oc(k), v.cpu(), g.cpu(), beta.cpu(), 64, s0.cpu(), True, True)
+        t0 = time.perf_counter()
+        o_ref, s_ref = oracle.chunk_gated_delta_rule_v2(*args)
+        dt = time.perf_counter() - t0
         rel = lambda x, y: ((x.double().cpu() - y.double()).norm() / y.double().norm()).item()
         res["out_rel_l2_vs_oracle"] = rel(o, o_ref)
         res["state_rel_l2_vs_oracle"] = rel(s, s_ref)
+        model = cpu_model()
+        res["cpu_baseline"] = dict(value=round(T / dt), unit="tokens/s/layer", us_per_layer=round(dt * 1e6),
+                                   cores=threads, kind="port", cpu_model=model,
+                                   sample=f"oracle chunk_gated_delta_rule_v2, B=1 T={T} H_v={HV} d={D}, the pass "
+                                          f"that checks the GPU result, torch {torch.__version__} CPU, {threads} "
+                                          f"threads on {model}")
     return res
 
 
@@ -404,8 +446,13 @@ def main():
     if args.only == "prefill8192":
         res["prefill"] = [bench_prefill(gdn, dev, reps=args.steps)]
     elif args.only in (None, "prefill") and not args.no_prefill:
-        res["prefill"] = [bench_prefill(gdn, dev), bench_prefill_varlen(gdn, dev),
-                          bench_prefill_long(gdn, dev, check=not args.no_cpu)]
+        res["prefill"] = [bench_prefill(gdn, dev), bench_prefill_varlen(gdn, dev, cpu=not args.no_cpu),
+                          bench_prefill_long(gdn, dev, check=not args.no_cpu),
+                          bench_prefill(gdn, dev, T=8192, hv=48),
+                          bench_prefill(gdn, dev, T=353, hv=48, reps=20,
+                                        note="Qwen3.5-27B's GDN shape at the reference's only published prefill "
+                                             "size (its chunk function: 5.64 ms/layer at 353 tokens on its own "
+                                             "accelerator, quoted as context only)")]
         if not args.no_cpu:
             res["prefill"][0]["cpu_baseline"] = cpu_baseline_prefill()
     if args.only in (None, "hybrid"):

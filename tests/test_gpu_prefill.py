@@ -207,12 +207,12 @@ def test_chunk_prefill_near_zero_decay_long(gdn, oracle, dev, T):
 
 
 def test_chunk_prefill_warm_up_and_exact_paths_per_head(gdn, oracle, dev):
-    """Two packed sequences (2500 and 1596 tokens, 4-chunk segments at this size), one value head per
+    """Two packed sequences (2500 and 1596 tokens, 4-chunk segments at this size), value heads on each
     path the kernel can take for a later segment's initial state: strong decay (a one-chunk warm-up
-    bounds the dropped state by 2^-40); moderate and slow decay (no window within a segment reaches
-    the bound: the exact summaries and combine, A formed); strong decay with one beta above 1 in the
-    last chunk of a segment (the bound does not hold there: the exact path).  Every head against the
-    oracle."""
+    bounds the dropped state by 2^-16); moderate decay (a three-chunk warm-up); slow decay (no window
+    within a segment reaches the bound: the exact summaries and combine, A formed); strong decay with
+    one beta above 1 in the last chunk of a segment (the bound does not hold there: the exact path).
+    Every head against the oracle."""
     lens = [2500, 1596]
     cu = torch.tensor([0, 2500, 4096], dtype=torch.int32)
     q, k, v, g, beta, _ = _gdn_inputs(4096, 2, 4, seed=21, state=False)
