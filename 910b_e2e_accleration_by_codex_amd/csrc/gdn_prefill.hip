@@ -242,6 +242,12 @@ constexpr float kNegligibleLog = -44.3614f;  // ln(2^-64): a segment map A_j thi
 // part is lost in the rounding the chain makes anyway (unless the state shrank by more than 2^7 over
 // the warm-up: new tokens contributing under 1/128 of the state they replace).
 constexpr float kWarmLog = -11.0904f;        // ln(2^-16)
+// A chunk whose decay over its tokens is slight (e^{G_last} above e^-2) passes most of the state it
+// receives on: the bf16 rounding of the W S operands then accumulates over many chunks (to 1e-3 of
+// the state over 8192 tokens of decay ~0.002 a token).  Such a chunk forms -W and the state as
+// bf16 hi + lo pairs and takes W S = Wh Sh + Wh Sl + Wl Sh (about 16 significant bits); a chunk with
+// faster decay forgets that rounding within a few chunks and keeps the single bf16 product.
+constexpr float kPreciseGl = 0.135335283f;   // e^-2
 constexpr int kTrans = 2 * pf::D * pf::D;    // floats per (slot, head): A, then B
 }  // namespace sg
 
@@ -629,9 +635,7 @@ __device__ __forceinline__ int xcd_item(int b, int n) {
 struct alignas(16) SegBuf {
   uint16_t K[pf::CH * pf::LDK];   // K rows (l2-normalised), token-major
   uint16_t V[pf::CH * pf::LDK];   // V rows
-  uint8_t wn[16 * ws::FRAG];          // -W fragments [tb 4][j 4]
   uint8_t qg[16 * ws::FRAG];          // q fragments [tb 4][j 4]
-  uint8_t qk[tf::FRAGS * ws::FRAG];   // QK fragments of the lower blocks, index tf::fid(tb, j)
   uint8_t tb[tf::FRAGS * ws::FRAG];   // T diag(beta) fragments (the inverse kernel's), index tf::fid(tb, k)
   float gs[pf::CH];               // G_t, the cumulative log decay within the chunk
   float dec[pf::CH];              // e^{G_last - G_t}
@@ -639,8 +643,17 @@ struct alignas(16) SegBuf {
   float egs[pf::CH];              // scale e^{G_t}
   float gl;                       // e^{G_last}
 };
+// The operands the local waves form after the step's first barrier and the chain reads before the
+// next step's first barrier (-W and QK) are single: the local waves write chunk c + 1's while the
+// chain waves are in part 2 of chunk c, which reads neither.
+struct alignas(16) SegOps {
+  uint8_t wn[16 * ws::FRAG];          // -W fragments [tb 4][j 4] (the bf16 hi part in a precise chunk)
+  uint8_t wl[16 * ws::FRAG];          // the lo part of -W in a precise chunk
+  uint8_t qk[tf::FRAGS * ws::FRAG];   // QK fragments of the lower blocks, index tf::fid(tb, j)
+};
 struct SegSmem {
   SegBuf buf[2];
+  SegOps ops;
   float red[8];
 };
 
@@ -718,6 +731,31 @@ __device__ __forceinline__ void loc_load(LocIn& L, int64_t t0, int len, int kh, 
     L.graw = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(knc) + (pf::CH + lane) * 4u);
 }
 
+// x = hi + lo with hi = bf16(x), lo = bf16(x - hi): 8 accumulator values (two tiles) as two k-slot
+// ordered bf16 fragments; hi + lo carries about 16 significant bits.
+__device__ __forceinline__ bf16x8 lo_bf16(f32x4 a, f32x4 b, bf16x8 hi) {
+  const u32x4v h = __builtin_bit_cast(u32x4v, hi);
+  f32x4 ra, rb;
+  ra[0] = a[0] - __uint_as_float(h[0] << 16);
+  ra[1] = a[1] - __uint_as_float(h[0] & 0xffff0000u);
+  ra[2] = a[2] - __uint_as_float(h[1] << 16);
+  ra[3] = a[3] - __uint_as_float(h[1] & 0xffff0000u);
+  rb[0] = b[0] - __uint_as_float(h[2] << 16);
+  rb[1] = b[1] - __uint_as_float(h[2] & 0xffff0000u);
+  rb[2] = b[2] - __uint_as_float(h[3] << 16);
+  rb[3] = b[3] - __uint_as_float(h[3] & 0xffff0000u);
+  return pack_acc_bf16(ra, rb);
+}
+__device__ __forceinline__ void split_bf16(f32x4 a, f32x4 b, bf16x8& hi, bf16x8& lo) {
+  hi = pack_acc_bf16(a, b);
+  lo = lo_bf16(a, b, hi);
+}
+// Whether a chunk's W S runs in hi + lo (its e^{G_last} above e^-2), read as a wave-uniform value so
+// that the two forms are a scalar branch.  The local and chain waves read the same LDS word.
+__device__ __forceinline__ bool chunk_precise(const SegBuf& B) {
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(B.gl))) > sg::kPreciseGl;
+}
+
 // Local phase 1 (wave w < 4): K rows (masked, l2-normalised when asked), V rows and the T diag(beta)
 // fragments into the buffer, the q fragments (masked, l2-normalised when asked; kept in qf for
 // phase 2); wave 0 also forms the decay factors (G, e^{G_last - G}, e^G, scale e^G, e^{G_last}).
@@ -790,12 +828,14 @@ __device__ __forceinline__ void loc_phase1(SegBuf& B, const LocIn& in, int len, 
 // T diag(beta) with column j scaled by e^{G_j} (element e of lane (c, g) in k-block s is column
 // 32 s + 16 (e >> 2) + 4 g + (e & 3)).
 template <int W, bool kNeedQ>
-__device__ __forceinline__ void loc_phase2(SegBuf& B, const bf16x8 (&qf)[4], const bf16x8 (&tbu)[2], bool q_on) {
+__device__ __forceinline__ void loc_phase2(const SegBuf& B, SegOps& P, const bf16x8 (&qf)[4], const bf16x8 (&tbu)[2],
+                                           bool q_on) {
   using namespace pf;
   int t;
   asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"((int)threadIdx.x));
   const int lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
-  bf16x8 tbe[2];
+  const bool precise = chunk_precise(B);
+  bf16x8 tbe[2], tbl[2];  // T diag(beta e^G), and in a precise chunk the lo part of its fp32 value
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
     if (2 * s > W) continue;
@@ -812,6 +852,7 @@ __device__ __forceinline__ void loc_phase2(SegBuf& B, const bf16x8 (&qf)[4], con
     b[2] = __uint_as_float(u[3] << 16) * e1[2];
     b[3] = __uint_as_float(u[3] & 0xffff0000u) * e1[3];
     tbe[s] = pack_acc_bf16(a, b);
+    if (precise) tbl[s] = lo_bf16(a, b, tbe[s]);
   }
   if (kNeedQ && q_on) {
     f32x4 accQ[W + 1];
@@ -835,9 +876,30 @@ __device__ __forceinline__ void loc_phase2(SegBuf& B, const bf16x8 (&qf)[4], con
 #pragma unroll
     for (int j = 0; j < 2; ++j)
       if (2 * j <= W)
-        *reinterpret_cast<bf16x8*>(B.qk + tf::fid(W, j) * ws::FRAG + lane * 16) = pack_acc_bf16(qk[2 * j], qk[2 * j + 1]);
+        *reinterpret_cast<bf16x8*>(P.qk + tf::fid(W, j) * ws::FRAG + lane * 16) = pack_acc_bf16(qk[2 * j], qk[2 * j + 1]);
   }
   f32x4 accW[8];
+  if (precise) {  // W from hi + lo of T diag(beta e^G), stored as hi + lo
+#pragma unroll
+    for (int cb = 0; cb < 8; ++cb) {
+      const bf16x8 k0 = __builtin_bit_cast(bf16x8, frag_tr_kperm(B.K, LDK, 0, 16 * cb, lane));
+      accW[cb] = mma(k0, tbe[0], f32x4{0.f, 0.f, 0.f, 0.f});
+      accW[cb] = mma(k0, tbl[0], accW[cb]);
+      if (W >= 2) {
+        const bf16x8 k1 = __builtin_bit_cast(bf16x8, frag_tr_kperm(B.K, LDK, 32, 16 * cb, lane));
+        accW[cb] = mma(k1, tbe[1], accW[cb]);
+        accW[cb] = mma(k1, tbl[1], accW[cb]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      bf16x8 hi, lo;
+      split_bf16(-accW[2 * j], -accW[2 * j + 1], hi, lo);
+      *reinterpret_cast<bf16x8*>(P.wn + (W * 4 + j) * ws::FRAG + lane * 16) = hi;
+      *reinterpret_cast<bf16x8*>(P.wl + (W * 4 + j) * ws::FRAG + lane * 16) = lo;
+    }
+    return;
+  }
 #pragma unroll
   for (int cb = 0; cb < 8; ++cb) {
     accW[cb] = mma(__builtin_bit_cast(bf16x8, frag_tr_kperm(B.K, LDK, 0, 16 * cb, lane)), tbe[0], f32x4{0.f, 0.f, 0.f, 0.f});
@@ -845,25 +907,9 @@ __device__ __forceinline__ void loc_phase2(SegBuf& B, const bf16x8 (&qf)[4], con
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j)
-    *reinterpret_cast<bf16x8*>(B.wn + (W * 4 + j) * ws::FRAG + lane * 16) = pack_acc_bf16(-accW[2 * j], -accW[2 * j + 1]);
+    *reinterpret_cast<bf16x8*>(P.wn + (W * 4 + j) * ws::FRAG + lane * 16) = pack_acc_bf16(-accW[2 * j], -accW[2 * j + 1]);
 }
 
-// x = hi + lo with hi = bf16(x), lo = bf16(x - hi): 8 accumulator values (two tiles) as two k-slot
-// ordered bf16 fragments; hi + lo carries about 16 significant bits.
-__device__ __forceinline__ void split_bf16(f32x4 a, f32x4 b, bf16x8& hi, bf16x8& lo) {
-  hi = pack_acc_bf16(a, b);
-  const u32x4v h = __builtin_bit_cast(u32x4v, hi);
-  f32x4 ra, rb;
-  ra[0] = a[0] - __uint_as_float(h[0] << 16);
-  ra[1] = a[1] - __uint_as_float(h[0] & 0xffff0000u);
-  ra[2] = a[2] - __uint_as_float(h[1] << 16);
-  ra[3] = a[3] - __uint_as_float(h[1] & 0xffff0000u);
-  rb[0] = b[0] - __uint_as_float(h[2] << 16);
-  rb[1] = b[1] - __uint_as_float(h[2] & 0xffff0000u);
-  rb[2] = b[2] - __uint_as_float(h[3] << 16);
-  rb[3] = b[3] - __uint_as_float(h[3] & 0xffff0000u);
-  lo = pack_acc_bf16(ra, rb);
-}
 
 // A chain wave's state: columns 32 w' .. 32 w' + 31 of the value head's [128, 128] fp32 state as two
 // 16-column slices (n = 2 w' + sl), S[sl][i][r] = S[16 i + 4 g + r][16 n + c].
@@ -966,9 +1012,12 @@ __device__ __forceinline__ void norm_store(const NormIn& N, const float (&wt)[8]
 // rows), vn = U - W S, the outputs o = diag(scale e^G) Q S + QK vn (kOut: left in bf16 in the V tile
 // for the local waves to store), and DEC vn split for part 2 (kSplitLate: vn itself, split by part 2).  W S and Q S share the loop over the state's k-blocks j
 // (16 independent accumulators); the LDS fragments of block j + 1 are requested before the products
-// of block j, so their latency hides behind those products.
-template <bool kUseU, bool kOut, bool kSplitLate>
-__device__ __forceinline__ void chain_part1(const SegBuf& B, ChainRegs& R, int wc, int lane_in) {
+// of block j, so their latency hides behind those products.  kPrecise: W S = Wh Sh + Wh Sl + Wl Sh
+// from the hi + lo parts of -W and of the state; block j's state parts are formed in its step and
+// its -W lo fragments requested there (behind the hi products), which keeps the registers of the
+// fast form.
+template <bool kUseU, bool kOut, bool kSplitLate, bool kPrecise>
+__device__ __forceinline__ void chain_part1(const SegBuf& B, const SegOps& P, ChainRegs& R, int wc, int lane_in) {
   using namespace pf;
   int lane;
   asm volatile("v_mov_b32 %0, %1" : "=v"(lane) : "v"(lane_in));
@@ -977,7 +1026,7 @@ __device__ __forceinline__ void chain_part1(const SegBuf& B, ChainRegs& R, int w
   auto fetch = [&](int j, bf16x8 (&w_)[4], bf16x8 (&q_)[4]) {
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb) {
-      w_[tb] = lds_frag(B.wn, tb * 4 + j, lane);
+      w_[tb] = lds_frag(P.wn, tb * 4 + j, lane);
       if (kOut) q_[tb] = lds_frag(B.qg, tb * 4 + j, lane);
     }
   };
@@ -996,10 +1045,12 @@ __device__ __forceinline__ void chain_part1(const SegBuf& B, ChainRegs& R, int w
   fetch(0, fw, fq);
   __builtin_amdgcn_sched_barrier(0);
   bf16x8 Sb[2][4];
+  if (!kPrecise) {
 #pragma unroll
-  for (int sl = 0; sl < 2; ++sl)
+    for (int sl = 0; sl < 2; ++sl)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) Sb[sl][j] = pack_acc_bf16(R.S[sl][2 * j], R.S[sl][2 * j + 1]);
+      for (int j = 0; j < 4; ++j) Sb[sl][j] = pack_acc_bf16(R.S[sl][2 * j], R.S[sl][2 * j + 1]);
+  }
   f32x4 acc[2][4];
 #pragma unroll
   for (int sl = 0; sl < 2; ++sl)
@@ -1021,8 +1072,14 @@ __device__ __forceinline__ void chain_part1(const SegBuf& B, ChainRegs& R, int w
   for (int tb = 0; tb < 4; ++tb) O[tb][0] = O[tb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    bf16x8 nw[4], nq[4];
+    bf16x8 nw[4], nq[4], fl[4], Sl[2];
     if (j < 3) fetch(j + 1, nw, nq);
+    if (kPrecise) {
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) fl[tb] = lds_frag(P.wl, tb * 4 + j, lane);
+#pragma unroll
+      for (int sl = 0; sl < 2; ++sl) split_bf16(R.S[sl][2 * j], R.S[sl][2 * j + 1], Sb[sl][j], Sl[sl]);
+    }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb) {
@@ -1031,6 +1088,18 @@ __device__ __forceinline__ void chain_part1(const SegBuf& B, ChainRegs& R, int w
       if (kOut) {
         O[tb][0] = mma(Sb[0][j], fq[tb], O[tb][0]);
         O[tb][1] = mma(Sb[1][j], fq[tb], O[tb][1]);
+      }
+    }
+    if (kPrecise) {
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        acc[0][tb] = mma(fw[tb], Sl[0], acc[0][tb]);
+        acc[1][tb] = mma(fw[tb], Sl[1], acc[1][tb]);
+      }
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        acc[0][tb] = mma(fl[tb], Sb[0][j], acc[0][tb]);
+        acc[1][tb] = mma(fl[tb], Sb[1][j], acc[1][tb]);
       }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -1045,7 +1114,7 @@ __device__ __forceinline__ void chain_part1(const SegBuf& B, ChainRegs& R, int w
   if (kOut) {
     bf16x8 kq[tf::FRAGS];
 #pragma unroll
-    for (int f = 0; f < tf::FRAGS; ++f) kq[f] = lds_frag(B.qk, f, lane);
+    for (int f = 0; f < tf::FRAGS; ++f) kq[f] = lds_frag(P.qk, f, lane);
     const float e0 = B.egs[c16], e1 = B.egs[16 + c16], e2 = B.egs[32 + c16], e3 = B.egs[48 + c16];
     bf16x8 vb[2][2];
 #pragma unroll
@@ -1217,12 +1286,12 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
                                               (uint32_t)vs, tfr(c),
                                               knorm + ((int64_t)(chunk_slot0 + c) * Hv + h) * (2 * CH), c >= w0);
     };
-    auto phase2 = [&](SegBuf& B, bool q_on) __attribute__((always_inline)) {
+    auto phase2 = [&](const SegBuf& B, bool q_on) __attribute__((always_inline)) {
       switch (w) {
-        case 0: loc_phase2<0, need_q>(B, qf, tbu, q_on); break;
-        case 1: loc_phase2<1, need_q>(B, qf, tbu, q_on); break;
-        case 2: loc_phase2<2, need_q>(B, qf, tbu, q_on); break;
-        default: loc_phase2<3, need_q>(B, qf, tbu, q_on); break;
+        case 0: loc_phase2<0, need_q>(B, sm.ops, qf, tbu, q_on); break;
+        case 1: loc_phase2<1, need_q>(B, sm.ops, qf, tbu, q_on); break;
+        case 2: loc_phase2<2, need_q>(B, sm.ops, qf, tbu, q_on); break;
+        default: loc_phase2<3, need_q>(B, sm.ops, qf, tbu, q_on); break;
       }
     };
     // the stores of chunk j's outputs (j >= w0); the gated norm's weight of columns 8 fb .. 8 fb + 7
@@ -1339,10 +1408,17 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     for (int c = 0; c < ntot; ++c) {
       const SegBuf& B = sm.buf[c & 1];
       constexpr bool late = kNorm == 0;
-      if (kPass == 0 && c >= w0)
-        chain_part1<true, true, late>(B, R, wc, lane);
-      else if (mode != kSegA) chain_part1<true, false, late>(B, R, wc, lane);
-      else chain_part1<false, false, late>(B, R, wc, lane);
+      const bool precise = chunk_precise(B);
+      if (kPass == 0 && c >= w0) {
+        if (precise) chain_part1<true, true, late, true>(B, sm.ops, R, wc, lane);
+        else chain_part1<true, true, late, false>(B, sm.ops, R, wc, lane);
+      } else if (mode != kSegA) {
+        if (precise) chain_part1<true, false, late, true>(B, sm.ops, R, wc, lane);
+        else chain_part1<true, false, late, false>(B, sm.ops, R, wc, lane);
+      } else {
+        if (precise) chain_part1<false, false, late, true>(B, sm.ops, R, wc, lane);
+        else chain_part1<false, false, late, false>(B, sm.ops, R, wc, lane);
+      }
       lds_barrier();
       chain_part2<late>(B, R, lane);
       lds_barrier();
@@ -1372,7 +1448,9 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
 // overwrites B_j, which the output pass reads as segment j+1's initial state.  One workgroup per
 // (sequence, value head, 16-column slice); the 8 slices of a (sequence, head) share blockIdx % 8,
 // hence an XCD and its L2.  Pairs without transition slots, or whose later segments warm up, exit
-// at once.  A_j flagged negligible is skipped: S_{j+1} = B_j as written.
+// at once.  A_j flagged negligible is skipped: S_{j+1} = B_j as written.  The walk is sequential in
+// S only: slot j + 1's A rows (16 per thread's 16-byte loads) and its B entries are requested into
+// registers before slot j's product, so each step waits on LDS and the MFMA, not on memory.
 struct CombineSmem {
   float A[pf::D * (pf::D + 4)];
   float S[pf::D * 16];
@@ -1398,41 +1476,58 @@ __global__ __launch_bounds__(256) void seg_combine_kernel(SegTable tab, int Hv, 
   }
   // S slice: row p / 16 ... thread t holds rows t / 16 + 16 m, column t % 16
   for (int i = t; i < D * 16; i += 256) sm.S[i] = s0 ? s0[(i >> 4) * D + 16 * n + (i & 15)] : 0.f;
-  __syncthreads();
+  // slot kk's operands: thread t loads A's 16-byte pieces t + 256 i (the whole slot is allocated, so
+  // a negligible A is read and not used) and the B entries of the 8 outputs it forms: rows
+  // 16 (2 w + m) + 4 (lane / 16) + r, column 16 n + lane % 16
+  f32x4 an[16];
+  float bn[8];
+  int fn = 0;
+  auto fetch = [&](int kk) __attribute__((always_inline)) {
+    const int64_t slot = (int64_t)(ts + kk) * Hv + h;
+    const float* base = trans + slot * sg::kTrans;
+    fn = tflags[slot];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) an[i] = *reinterpret_cast<const f32x4*>(base + 4 * (t + 256 * i));
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) bn[4 * m + r] = base[D * D + (16 * (2 * w + m) + 4 * (lane >> 4) + r) * D + 16 * n + (lane & 15)];
+  };
+  fetch(0);
   for (int kk = 0; kk < nsl; ++kk) {
-    float* base = trans + ((int64_t)(ts + kk) * Hv + h) * sg::kTrans;
-    float* Bm = base + D * D;
-    if (tflags[(int64_t)(ts + kk) * Hv + h]) {
-      for (int i = t; i < D * D / 4; i += 256) {
-        const f32x4 a = *reinterpret_cast<const f32x4*>(base + 4 * i);
-        *reinterpret_cast<f32x4*>(&sm.A[(i >> 5) * LDA + 4 * (i & 31)]) = a;
+    const int fl = fn;
+    float bc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) bc[e] = bn[e];
+    if (fl) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int q4 = t + 256 * i;
+        *reinterpret_cast<f32x4*>(&sm.A[(q4 >> 5) * LDA + 4 * (q4 & 31)]) = an[i];
       }
-      __syncthreads();
-      f32x4 acc[2];
+    }
+    if (kk + 1 < nsl) fetch(kk + 1);
+    __syncthreads();  // A_kk and S_kk in LDS
+    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    if (fl) {
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
         const int rt = 2 * w + m;  // row tile
-        acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll 8
         for (int k0 = 0; k0 < D; k0 += 16) acc[m] = mm16_f32(&sm.A[16 * rt * LDA + k0], LDA, &sm.S[k0 * 16], 16, acc[m], lane);
       }
-      __syncthreads();  // every wave has read S
-#pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        const int rt = 2 * w + m;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = 16 * rt + 4 * (lane >> 4) + r, c = lane & 15;
-          const float x = acc[m][r] + Bm[row * D + 16 * n + c];
-          sm.S[row * 16 + c] = x;
-          Bm[row * D + 16 * n + c] = x;
-        }
-      }
-      __syncthreads();
-    } else {
-      for (int i = t; i < D * 16; i += 256) sm.S[i] = Bm[(i >> 4) * D + 16 * n + (i & 15)];
-      __syncthreads();
     }
+    __syncthreads();  // every wave has read A and S
+    float* Bm = trans + ((int64_t)(ts + kk) * Hv + h) * sg::kTrans + D * D;
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * (2 * w + m) + 4 * (lane >> 4) + r, c = lane & 15;
+        const float x = acc[m][r] + bc[4 * m + r];
+        sm.S[row * 16 + c] = x;
+        if (fl) Bm[row * D + 16 * n + c] = x;
+      }
   }
 }
 

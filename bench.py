@@ -9,7 +9,7 @@ a HIP graph and replayed.  A "step" is one replay (48 layers).  ``value`` is mic
 Also reported (``secondary``): chunked GDN prefill at T=8192 (B=1, H_k=16, H_v=32, d=128, bf16
 inputs, fp32 state) in tokens/s/layer with its bf16-MFMA and HBM fractions, the fused varlen
 prefill layer, T=32768, the chunked rule at Qwen3.5-27B's GDN shape (H_k=16, H_v=48) at T=8192 and
-353 tokens, and whole decode steps at Qwen3.5-27B shape (the hybrid 64-layer stack, and its 48 GDN
+353 tokens, T=8192 at slow decay (g ~ -0.002 a token: the exact segment path), and whole decode steps at Qwen3.5-27B shape (the hybrid 64-layer stack, and its 48 GDN
 layers with projections) in tokens/s.  CPU baselines (the oracle on the host's cores) for the
 decode step, T=8192, the varlen layer and T=32768.
 
@@ -144,13 +144,13 @@ def _time(fn, reps, dev):
     return e0.elapsed_time(e1) * 1000.0 / reps
 
 
-def _gdn_inputs(T, seed, dev, nseq=1, hk=HK, hv=HV):
+def _gdn_inputs(T, seed, dev, nseq=1, hk=HK, hv=HV, decay=0.1):
     g_ = torch.Generator(device="cpu").manual_seed(seed)
     q = torch.randn(1, T, hk, D, generator=g_).to(torch.bfloat16).to(dev)
     k = torch.randn(1, T, hk, D, generator=g_).to(torch.bfloat16).to(dev)
     v = torch.randn(1, T, hv, D, generator=g_).to(torch.bfloat16).to(dev)
     beta = torch.sigmoid(torch.randn(1, T, hv, generator=g_)).to(torch.bfloat16).to(dev)
-    g = (-torch.nn.functional.softplus(torch.randn(1, T, hv, generator=g_) + 2) * 0.1).to(dev)
+    g = (-torch.nn.functional.softplus(torch.randn(1, T, hv, generator=g_) + 2) * decay).to(dev)
     s0 = (0.02 * torch.randn(nseq, hv, D, D, generator=g_)).to(dev)
     return q, k, v, g, beta, s0
 
@@ -161,13 +161,14 @@ def _fractions(name, us, F, B, tokens):
                 flops=F, bytes=B)
 
 
-def bench_prefill(gdn, dev, T=8192, reps=5, seed=0, hk=HK, hv=HV, note=None):
+def bench_prefill(gdn, dev, T=8192, reps=5, seed=0, hk=HK, hv=HV, note=None, decay=0.1):
     """Chunked rule alone, B=1, T tokens, hk key heads read by hv value heads (value head h reads key
-    head h // (hv / hk))."""
-    q, k, v, g, beta, s0 = _gdn_inputs(T, seed, dev, hk=hk, hv=hv)
+    head h // (hv / hk)); g = -softplus(N(0, 1) + 2) * decay per token."""
+    q, k, v, g, beta, s0 = _gdn_inputs(T, seed, dev, hk=hk, hv=hv, decay=decay)
     us = _time(lambda: gdn.fast_chunk_gated_delta_rule_v2(q, k, v, g, beta, initial_state=s0, output_final_state=True,
                                                           use_qk_l2norm_in_kernel=True), reps, dev)
-    res = _fractions(f"chunked rule B=1 T={T} H_k={hk} H_v={hv} d={D} bf16", us, prefill_flops(T, hv=hv),
+    slow = "" if decay == 0.1 else f" g~-{2.1 * decay:g}/token"
+    res = _fractions(f"chunked rule B=1 T={T} H_k={hk} H_v={hv} d={D} bf16{slow}", us, prefill_flops(T, hv=hv),
                      prefill_bytes(T, hk=hk, hv=hv), T)
     if note:
         res["note"] = note
@@ -452,7 +453,12 @@ def main():
                           bench_prefill(gdn, dev, T=353, hv=48, reps=20,
                                         note="Qwen3.5-27B's GDN shape at the reference's only published prefill "
                                              "size (its chunk function: 5.64 ms/layer at 353 tokens on its own "
-                                             "accelerator, quoted as context only)")]
+                                             "accelerator, quoted as context only)"),
+                          bench_prefill(gdn, dev, T=8192, decay=0.001,
+                                        note="slow decay: no segment boundary has a warm-up below 2^-16, so the "
+                                             "exact path runs (both summaries of every segment, their fp32 "
+                                             "combination, then the outputs), and every chunk decays by less "
+                                             "than e^-2 and takes W S in bf16 hi + lo")]
         if not args.no_cpu:
             res["prefill"][0]["cpu_baseline"] = cpu_baseline_prefill()
     if args.only in (None, "hybrid"):

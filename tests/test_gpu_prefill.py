@@ -167,8 +167,7 @@ def test_chunk_prefill_slow_decay_state_accuracy(gdn, oracle, dev):
 # T=8192; 6.66e-3 vs 6.68e-3 for the growing head) and shows that the W S product sets them: S as
 # bf16 hi + lo alone gives 1.22e-3, W and S in fp32 5.0e-4.  So these regimes are held to the
 # bounds below, above the 1e-3 of the benchmark decays (whose state error is ~1e-4).
-NEAR_ZERO_DECAY_STATE_TOL = 2.5e-3
-GROWING_STATE_TOL = 1e-2
+GROWING_STATE_TOL = 2.5e-3
 
 
 def test_chunk_prefill_positive_g_heads(gdn, oracle, dev):
@@ -176,7 +175,8 @@ def test_chunk_prefill_positive_g_heads(gdn, oracle, dev):
     i > j (src/gdn_chunk_fast2.py:41) has no sign condition.  2048 tokens (several segments: the
     growing heads take the exact summary path, the others warm up) and a one-chunk call.  Outputs
     within 1e-2; states within 1e-3 for the decaying heads and GROWING_STATE_TOL for the growing
-    ones (head 1 grows ~e^8 over the 2048 tokens)."""
+    ones (head 1 grows ~e^8 over the 2048 tokens; measured 1.9e-3 there, 1.1e-3 on head 2: their
+    chunks run W S in hi + lo, which took head 1 from 6.7e-3)."""
     for T, seed in ((2048, 31), (100, 32)):
         q, k, v, g, beta, s0 = _gdn_inputs(T, 2, 4, seed=seed)
         g[..., 1] = -g[..., 1] * 0.02        # (0, 0.01] per token: the state grows up to ~e^8
@@ -194,8 +194,9 @@ def test_chunk_prefill_positive_g_heads(gdn, oracle, dev):
 @pytest.mark.parametrize("T", [8192, 32768])
 def test_chunk_prefill_near_zero_decay_long(gdn, oracle, dev, T):
     """Near-zero decay (g ~ -0.002 per token: the state keeps ~500 tokens of memory) over long
-    sequences, two value heads of one key head: outputs within 1e-2, final state within
-    NEAR_ZERO_DECAY_STATE_TOL (measured 1.68e-3 at both lengths)."""
+    sequences, two value heads of one key head: outputs within 1e-2, final state within 1e-3
+    (measured 8.1e-4 to 9.1e-4 at both lengths).  Every chunk here decays by less than e^-2 and runs
+    W S in hi + lo; with the single bf16 product the state was 1.68e-3 off."""
     q, k, v, g, beta, s0 = _gdn_inputs(T, 1, 2, seed=40 + T % 7, decay=0.001)
     o_ref, s_ref = oracle.chunk_gated_delta_rule_v2(_rep(q, 2), _rep(k, 2), v, g, beta, 64, s0, True, True)
     o, s = gdn.fast_chunk_gated_delta_rule_v2(q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta.to(dev),
@@ -203,7 +204,27 @@ def test_chunk_prefill_near_zero_decay_long(gdn, oracle, dev, T):
                                               use_qk_l2norm_in_kernel=True)
     for h in range(2):
         assert rel_l2(o[:, :, h], o_ref[:, :, h]) <= OUT_TOL, (h, rel_l2(o[:, :, h], o_ref[:, :, h]))
-        assert rel_l2(s[:, h], s_ref[:, h]) <= NEAR_ZERO_DECAY_STATE_TOL, (h, rel_l2(s[:, h], s_ref[:, h]))
+        assert rel_l2(s[:, h], s_ref[:, h]) <= STATE_TOL, (h, rel_l2(s[:, h], s_ref[:, h]))
+
+
+def test_chunk_prefill_mixed_chunk_forms(gdn, oracle, dev):
+    """Slow and fast decay alternating in runs of 96 tokens, so that chunks of one sequence switch
+    between the hi + lo form of W S (decay over the chunk above e^-2) and the single bf16 product.
+    Heads 0 and 2 (fast runs of g ~ -0.2) warm up; head 1 (fast runs of g ~ -0.05, about -7 over a
+    4-chunk segment) leaves slots without a warm-up and takes the exact summary path; head 3 decays
+    fast throughout.  Outputs within 1e-2, states within 1e-3."""
+    T = 4096
+    q, k, v, g, beta, s0 = _gdn_inputs(T, 2, 4, seed=55)
+    slow = (torch.arange(T) // 96) % 2 == 0
+    g[0, slow, :3] *= 0.01          # heads 0-2: g ~ -0.002 on the slow runs
+    g[0, :, 1] *= 0.25
+    o_ref, s_ref = oracle.chunk_gated_delta_rule_v2(_rep(q, 2), _rep(k, 2), v, g, beta, 64, s0, True, True)
+    o, s = gdn.fast_chunk_gated_delta_rule_v2(q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta.to(dev),
+                                              initial_state=s0.to(dev), output_final_state=True,
+                                              use_qk_l2norm_in_kernel=True)
+    for h in range(4):
+        assert rel_l2(o[:, :, h], o_ref[:, :, h]) <= OUT_TOL, (h, rel_l2(o[:, :, h], o_ref[:, :, h]))
+        assert rel_l2(s[:, h], s_ref[:, h]) <= STATE_TOL, (h, rel_l2(s[:, h], s_ref[:, h]))
 
 
 def test_chunk_prefill_warm_up_and_exact_paths_per_head(gdn, oracle, dev):
