@@ -14,7 +14,7 @@ layers with projections) in tokens/s.  CPU baselines (the oracle on the host's c
 decode step, T=8192, the varlen layer and T=32768.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-prefill]
-                      [--only decode|prefill|prefill8192|hybrid|attention]
+                      [--only decode|prefill|prefill8192|varlen|hybrid|attention]
 """
 import argparse
 import importlib
@@ -421,8 +421,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill", "prefill8192", "hybrid", "attention"], default=None,
-                    help="run one workload group (prefill8192: the T=8192 chunked rule alone, for profiling)")
+    ap.add_argument("--only", choices=["decode", "prefill", "prefill8192", "varlen", "hybrid", "attention"],
+                    default=None, help="run one workload group (prefill8192: the T=8192 chunked rule alone; varlen: "
+                                       "the 16-prompt prefill layer alone; both for profiling)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first run a 256 MiB device-to-device copy (counter calibration for rocprof)")
     args = ap.parse_args()
@@ -446,6 +447,8 @@ def main():
         res["decode"] = bench_decode(gdn, dev, args.steps, args.warmup)
     if args.only == "prefill8192":
         res["prefill"] = [bench_prefill(gdn, dev, reps=args.steps)]
+    elif args.only == "varlen":
+        res["prefill"] = [bench_prefill_varlen(gdn, dev, reps=args.steps)]
     elif args.only in (None, "prefill") and not args.no_prefill:
         res["prefill"] = [bench_prefill(gdn, dev), bench_prefill_varlen(gdn, dev, cpu=not args.no_cpu),
                           bench_prefill_long(gdn, dev, check=not args.no_cpu),
@@ -465,7 +468,7 @@ def main():
         res["hybrid"] = bench_hybrid(gdn, dev)
     if args.only in (None, "attention"):
         res["hybrid"] = res.get("hybrid", []) + [bench_attention(gdn, dev, reps=args.steps if args.only else 3)]
-    if args.only in ("prefill", "prefill8192", "hybrid", "attention"):
+    if args.only in ("prefill", "prefill8192", "varlen", "hybrid", "attention"):
         print(json.dumps({"secondary": res.get("prefill", []) + res.get("hybrid", [])}))
         return
     dec = res["decode"]
