@@ -447,7 +447,7 @@ __global__ __launch_bounds__(pf::NT, 2) void inv_kernel(const uint16_t* __restri
                                                        uint8_t* __restrict__ tfrag, float* __restrict__ knorm,
                                                        SegTable tab, int* __restrict__ warm) {
   using namespace pf;
-  __shared__ float sdec[4][3][CH];                // per wave: G, beta and the K row factor by token
+  __shared__ float sdec[4][2][CH];                // per wave: G and beta by token
   __shared__ float strp[4][4 * 16 * kTrPitch];    // per wave: 4 transpose tiles
   const int t = threadIdx.x, lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);  // the item is wave-uniform: scalar control flow
@@ -472,10 +472,12 @@ __global__ __launch_bounds__(pf::NT, 2) void inv_kernel(const uint16_t* __restri
   const float graw = g[(cp.t0 + tok) * Hv + h];
   const float braw = Elem<BetaT>::load(beta + (cp.t0 + tok) * Hv + h);
   // rows past the chunk's end are zero; with use_l2, each row's l2norm factor bf16(rsqrt(...)) with
-  // torch's bf16 op rounding (a row sits in the lanes c, c + 16, c + 32, c + 48).  The segment kernel
-  // scales the raw rows by these factors (the normalised rows of the reference, bit for bit); here
-  // the Gram matrix of the raw rows is scaled instead: it differs from the rounded rows' by about
-  // 2e-4 absolute, ten times below the bf16 rounding of the fragments T is stored as.
+  // torch's bf16 op rounding (a row sits in the lanes c, c + 16, c + 32, c + 48), and the rows
+  // scaled by it and rounded to bf16: the reference's normalised rows, bit for bit, as the segment
+  // kernel forms them from the same factors.  The Gram matrix is theirs: formed from the unrounded
+  // products instead (the raw rows' Gram scaled by the factors) it differs by ~2e-4 absolute, a
+  // mismatch between T and the K the state update uses that accumulates in long-memory heads (state
+  // 5.0e-4 -> 8.5e-4 rel-L2 at g ~ -0.002 over 4096 tokens, in emulation).
   float invc[4] = {1.f, 1.f, 1.f, 1.f};  // factor of row 16 t + c
   {
     const u16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -491,12 +493,13 @@ __global__ __launch_bounds__(pf::NT, 2) void inv_kernel(const uint16_t* __restri
         for (int s = 0; s < 4; ++s) ss = sumsq_bf16(kf[tt][s], ss);
         invc[tt] = l2norm_inv(xor32_sum(xor16_sum(ss)));
         mine = g4 == tt ? invc[tt] : mine;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) kf[tt][s] = scale_bf16(kf[tt][s], invc[tt]);
       }
     }
     float* rec = knorm + ((int64_t)slot * Hv + h) * (2 * CH);
     if (use_l2) rec[lane] = mine;
     rec[CH + lane] = graw;  // the chunk's g of this head, contiguous for the segment kernel
-    sdec[w][2][lane] = mine;
   }
   // K K^T: kk[tri(a, b)] = Dl of block (b, a) -- lane (c, g) r: (K K^T)[16 b + 4 g + r][16 a + c]
   f32x4 kk[10];
@@ -509,16 +512,6 @@ __global__ __launch_bounds__(pf::NT, 2) void inv_kernel(const uint16_t* __restri
       for (int s = 0; s < 4; ++s) acc = mma(__builtin_bit_cast(bf16x8, kf[b][s]), __builtin_bit_cast(bf16x8, kf[a][s]), acc);
       kk[tri(a, b)] = acc;
     }
-  __builtin_amdgcn_wave_barrier();  // this wave's own LDS writes, read back in order
-  {  // the Gram matrix of the normalised rows: kk[tri(a, b)] at lane (c, g) r scales by f[16b+4g+r] f[16a+c]
-    f32x4 fr[4];
-#pragma unroll
-    for (int b = 0; b < 4; ++b) fr[b] = *reinterpret_cast<const f32x4*>(&sdec[w][2][16 * b + 4 * g4]);
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-      for (int b = 0; b <= a; ++b) kk[tri(a, b)] = kk[tri(a, b)] * fr[b] * invc[a];
-  }
   {  // decay within the chunk (g = 0 and beta = 0 past its end)
     const float G = wave_incl_scan(lane < cp.len ? graw : 0.f);
     sdec[w][0][lane] = G;
