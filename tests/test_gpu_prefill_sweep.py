@@ -1,0 +1,71 @@
+"""A seeded sweep of the chunked prefill over shapes the fixed cases do not combine: 1-6 packed
+sequences of 0-900 tokens (lengths at and around chunk multiples), key heads 1-8 read by 1-4 value
+heads each, per-head decays from near zero (hi + lo chunks, no warm-up: the exact summary path) to
+fast (warm-ups), beta with exact 0s and 1s, with and without initial states.  Each case against the
+oracle's chunked rule per sequence (src/gdn_chunk_fast2.py:11-62): outputs within 1e-2 rel-L2,
+final states within 1e-3 per sequence, an empty sequence's state unchanged bit for bit.
+"""
+import pytest
+import torch
+
+from conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+OUT_TOL = 1e-2
+STATE_TOL = 1e-3
+D = 128
+DECAYS = (0.0005, 0.003, 0.02, 0.1, 1.0)   # multipliers of -softplus(N(0,1) + 2) per token
+
+
+def _case(i):
+    r = torch.Generator().manual_seed(1000 + i)
+    pick = lambda seq: seq[int(torch.randint(len(seq), (1,), generator=r))]
+    nseq = 1 + int(torch.randint(6, (1,), generator=r))
+    lens = []
+    for _ in range(nseq):
+        base = pick([0, 1, 63, 64, 65, 127, 128, 129, 256, 320, 511, 700, 900])
+        lens.append(base)
+    Hk = pick([1, 2, 4, 8])
+    ratio = pick([1, 2, 3, 4])
+    with_state = bool(torch.randint(2, (1,), generator=r))
+    decay = torch.tensor([pick(DECAYS) for _ in range(Hk * ratio)])
+    return lens, Hk, Hk * ratio, with_state, decay, 2000 + i
+
+
+@pytest.mark.parametrize("i", range(12))
+def test_chunk_prefill_sweep(gdn, oracle, dev, i):
+    lens, Hk, Hv, with_state, decay, seed = _case(i)
+    T = sum(lens)
+    if T == 0:
+        lens[0], T = 65, 65
+    g_ = torch.Generator().manual_seed(seed)
+    q = torch.randn(1, T, Hk, D, generator=g_).to(torch.bfloat16)
+    k = torch.randn(1, T, Hk, D, generator=g_).to(torch.bfloat16)
+    v = torch.randn(1, T, Hv, D, generator=g_).to(torch.bfloat16)
+    beta = torch.sigmoid(torch.randn(1, T, Hv, generator=g_))
+    beta[0, ::11] = 0.0
+    beta[0, 5::13] = 1.0
+    beta = beta.to(torch.bfloat16)
+    g = -torch.nn.functional.softplus(torch.randn(1, T, Hv, generator=g_) + 2) * decay
+    s0 = 0.02 * torch.randn(len(lens), Hv, D, D, generator=g_) if with_state else None
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int32)
+    r = Hv // Hk
+    rep = lambda x: x.repeat_interleave(r, dim=2) if r > 1 else x
+    print(f"case {i}: lens {lens} Hk {Hk} Hv {Hv} state {with_state} decays {decay.tolist()}", flush=True)
+    o_ref, s_ref = oracle.chunk_gated_delta_rule_varlen(rep(q), rep(k), v, g, beta, cu, 64, s0, True, True)
+    o, s = gdn.fast_chunk_gated_delta_rule_v2(q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta.to(dev),
+                                              initial_state=None if s0 is None else s0.to(dev),
+                                              output_final_state=True, use_qk_l2norm_in_kernel=True,
+                                              cu_seqlens=cu.to(dev))
+    torch.cuda.synchronize()
+    for j, L in enumerate(lens):
+        a, b = int(cu[j]), int(cu[j + 1])
+        if L == 0:
+            want = s0[j] if s0 is not None else torch.zeros(Hv, D, D)
+            assert torch.equal(s[j].cpu(), want), f"empty sequence {j}"
+            continue
+        assert rel_l2(o[:, a:b], o_ref[:, a:b]) <= OUT_TOL, (j, L, rel_l2(o[:, a:b], o_ref[:, a:b]))
+        for h in range(Hv):
+            e = rel_l2(s[j, h], s_ref[j, h])
+            assert e <= STATE_TOL, (j, L, h, float(decay[h]), e)
