@@ -6,12 +6,14 @@ for 16 slots x 1 token, H_k=16, H_v=32, d=128, conv channels 8192, kernel 4 -- w
 layer states (3.2 GB working set, so the 256 MB Infinity Cache cannot serve them), captured once as
 a HIP graph and replayed.  A "step" is one replay (48 layers).  ``value`` is microseconds per layer.
 
-Also reported (``secondary``): chunked GDN prefill at T=8192 (B=1, H_k=16, H_v=32, d=128, bf16
-inputs, fp32 state) in tokens/s/layer with its bf16-MFMA and HBM fractions, the fused varlen
-prefill layer, T=32768, the chunked rule at Qwen3.5-27B's GDN shape (H_k=16, H_v=48) at T=8192 and
-353 tokens, T=8192 at slow decay (g ~ -0.002 a token: the exact segment path), and whole decode steps at Qwen3.5-27B shape (the hybrid 64-layer stack, and its 48 GDN
-layers with projections) in tokens/s.  CPU baselines (the oracle on the host's cores) for the
-decode step, T=8192, the varlen layer and T=32768.
+Also reported (``secondary``): the decode layer at one TP=2 rank's share of the heads (H_k=8,
+H_v=16); chunked GDN prefill at T=8192 (B=1, H_k=16, H_v=32, d=128, bf16 inputs, fp32 state) in
+tokens/s/layer with its bf16-MFMA and HBM fractions, the fused varlen prefill layer, T=32768, the
+chunked rule at Qwen3.5-27B's GDN shape (H_k=16, H_v=48) at T=8192 and 353 tokens, T=8192 at slow
+decay (g ~ -0.002 a token: the exact segment path), and whole decode steps at Qwen3.5-27B shape (the
+hybrid 64-layer stack, and its 48 GDN layers with projections) in tokens/s.  CPU baselines (the
+oracle on the host's cores; warm-up, then the median of 5 passes) for the decode step, T=8192, the
+varlen layer and T=32768.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-prefill]
                       [--only decode|prefill|prefill8192|varlen|hybrid|attention]
@@ -39,50 +41,52 @@ DECODE_TRAFFIC = 69_993_300
 C = (2 * HK + HV) * D
 
 
-def decode_bytes_per_layer():
+def decode_bytes_per_layer(hk=HK, hv=HV):
     """Algorithmic HBM bytes of one fused decode layer (each tensor touched once)."""
-    state = 2 * N_SLOTS * HV * D * D * 4            # fp32 state read + write
-    conv = 2 * N_SLOTS * C * KC * 2                 # bf16 conv state read + write
-    conv_w = C * KC * 2
-    mixed = N_SLOTS * C * 2
-    z = N_SLOTS * HV * D * 2
-    out = N_SLOTS * HV * D * 2
-    ab = 2 * N_SLOTS * HV * 2
-    params = HV * 4 * 2 + D * 2                     # A_log, dt_bias fp32; norm weight bf16
+    c = (2 * hk + hv) * D
+    state = 2 * N_SLOTS * hv * D * D * 4            # fp32 state read + write
+    conv = 2 * N_SLOTS * c * KC * 2                 # bf16 conv state read + write
+    conv_w = c * KC * 2
+    mixed = N_SLOTS * c * 2
+    z = N_SLOTS * hv * D * 2
+    out = N_SLOTS * hv * D * 2
+    ab = 2 * N_SLOTS * hv * 2
+    params = hv * 4 * 2 + D * 2                     # A_log, dt_bias fp32; norm weight bf16
     return state + conv + conv_w + mixed + z + out + ab + params
 
 
-def make_decode_layers(dev, seed=0):
+def make_decode_layers(dev, seed=0, hk=HK, hv=HV):
     g_ = torch.Generator(device="cpu").manual_seed(seed)
+    c = (2 * hk + hv) * D
     layers = []
     for _ in range(LAYERS):
         layers.append(dict(
-            mixed=torch.randn(N_SLOTS, C, generator=g_).to(torch.bfloat16).to(dev),
-            z=torch.randn(N_SLOTS, HV * D, generator=g_).to(torch.bfloat16).to(dev),
-            a=torch.randn(N_SLOTS, HV, generator=g_).to(torch.bfloat16).to(dev),
-            b=torch.randn(N_SLOTS, HV, generator=g_).to(torch.bfloat16).to(dev),
-            conv_state=torch.randn(N_SLOTS, C, KC, generator=g_).to(torch.bfloat16).to(dev),
-            conv_weight=(0.5 * torch.randn(C, KC, generator=g_)).to(torch.bfloat16).to(dev),
-            A_log=torch.full((HV,), -2.302585092994046, device=dev),   # log(0.1)
-            dt_bias=torch.full((HV,), 2.0, device=dev),
+            mixed=torch.randn(N_SLOTS, c, generator=g_).to(torch.bfloat16).to(dev),
+            z=torch.randn(N_SLOTS, hv * D, generator=g_).to(torch.bfloat16).to(dev),
+            a=torch.randn(N_SLOTS, hv, generator=g_).to(torch.bfloat16).to(dev),
+            b=torch.randn(N_SLOTS, hv, generator=g_).to(torch.bfloat16).to(dev),
+            conv_state=torch.randn(N_SLOTS, c, KC, generator=g_).to(torch.bfloat16).to(dev),
+            conv_weight=(0.5 * torch.randn(c, KC, generator=g_)).to(torch.bfloat16).to(dev),
+            A_log=torch.full((hv,), -2.302585092994046, device=dev),   # log(0.1)
+            dt_bias=torch.full((hv,), 2.0, device=dev),
             norm_weight=(1 + 0.02 * torch.randn(D, generator=g_)).to(torch.bfloat16).to(dev),
-            rec_state=(0.02 * torch.randn(N_SLOTS, HV, D, D, generator=g_)).to(dev),
+            rec_state=(0.02 * torch.randn(N_SLOTS, hv, D, D, generator=g_)).to(dev),
         ))
     return layers
 
 
-def decode_step(gdn, layers, outs):
+def decode_step(gdn, layers, outs, hk=HK, hv=HV):
     for p, o in zip(layers, outs):
         gdn.gdn_decode_core(p["mixed"], p["z"], p["a"], p["b"], p["conv_state"], p["conv_weight"],
-                            p["A_log"], p["dt_bias"], p["norm_weight"], p["rec_state"], HK, HV, D,
+                            p["A_log"], p["dt_bias"], p["norm_weight"], p["rec_state"], hk, hv, D,
                             out=o)
     return outs
 
 
-def bench_decode(gdn, dev, steps, warmup):
-    layers = make_decode_layers(dev)
-    outs = [torch.empty(N_SLOTS, HV * D, dtype=torch.bfloat16, device=dev) for _ in range(LAYERS)]
-    graph = gdn.GDNDecodeGraph(lambda: decode_step(gdn, layers, outs), device=dev)
+def bench_decode(gdn, dev, steps, warmup, hk=HK, hv=HV):
+    layers = make_decode_layers(dev, hk=hk, hv=hv)
+    outs = [torch.empty(N_SLOTS, hv * D, dtype=torch.bfloat16, device=dev) for _ in range(LAYERS)]
+    graph = gdn.GDNDecodeGraph(lambda: decode_step(gdn, layers, outs, hk, hv), device=dev)
     for _ in range(warmup):
         graph.replay()
     torch.cuda.synchronize()
@@ -102,11 +106,24 @@ def bench_decode(gdn, dev, steps, warmup):
     e2, e3 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e2.record(stream)
     for _ in range(steps):
-        decode_step(gdn, layers, outs)
+        decode_step(gdn, layers, outs, hk, hv)
     e3.record(stream)
     torch.cuda.synchronize()
     us_eager = e2.elapsed_time(e3) * 1000.0 / (steps * LAYERS)
     return dict(ms_per_step=ms, us_per_layer=us_layer, us_per_layer_eager=us_eager, wall_s=wall)
+
+
+def bench_decode_tp_share(gdn, dev, steps, warmup, tp=2):
+    """The decode layer at one tensor-parallel rank's share of the heads (H_k/tp, H_v/tp: the slicing
+    of src/cb_tp.py:69-97); the all-reduce after out_proj that a multi-GPU step adds is not here."""
+    hk, hv = HK // tp, HV // tp
+    r = bench_decode(gdn, dev, steps, warmup, hk=hk, hv=hv)
+    b = decode_bytes_per_layer(hk, hv)
+    return dict(workload=f"decode layer at one TP={tp} rank's share: 16 slots, H_k={hk} H_v={hv} d={D}, conv "
+                         f"{(2 * hk + hv) * D}x{KC}, 48 distinct layers, graph replay (the all-reduce after "
+                         f"out_proj not included)",
+                us_per_layer=round(r["us_per_layer"], 3), hbm_frac=round(b / (r["us_per_layer"] * 1e-6) / HBM_PEAK, 4),
+                bytes=b)
 
 
 def prefill_flops(T, hv=HV, d=D, chunk=64):
@@ -193,11 +210,11 @@ def _varlen_inputs(seed=2):
     return cu, T, x
 
 
-def bench_prefill_varlen(gdn, dev, reps=5, seed=2, cpu=False):
+def bench_prefill_varlen(gdn, dev, reps=5, seed=2, cpu=False, cpu_reps=5):
     """Fused prefill layer (conv1d prefill + SiLU, l2norm, gating, chunked rule, gated RMSNorm) over
     16 packed prompts with lengths uniform in [200, 1500], random initial states, zero conv history.
     With cpu: the oracle's layer (its per-sequence loop, as the reference runs one sequence per call)
-    on the host's cores, one pass, as the CPU baseline."""
+    on the host's cores, warm-up then the median of cpu_reps passes, as the CPU baseline."""
     cu, T, x = _varlen_inputs(seed)
     d = {n: t.to(dev) for n, t in x.items()}
     # lengths on the host, as a scheduler holds them: the batch's sequence table is checked and uploaded
@@ -213,22 +230,21 @@ def bench_prefill_varlen(gdn, dev, reps=5, seed=2, cpu=False):
         oracle = importlib.import_module("oracle.gdn_oracle")
         threads = len(os.sched_getaffinity(0))
         torch.set_num_threads(threads)
-        t0 = time.perf_counter()
-        oracle.gdn_prefill_core(x["mixed"], x["z"], x["a"], x["b"], x["cw"], x["A_log"], x["dt"], x["nw"], HK, HV, D,
-                                cu_seqlens=cu, initial_state=x["s0"])
-        dt = time.perf_counter() - t0
+        dt = _median_time(lambda: oracle.gdn_prefill_core(x["mixed"], x["z"], x["a"], x["b"], x["cw"], x["A_log"],
+                                                          x["dt"], x["nw"], HK, HV, D, cu_seqlens=cu,
+                                                          initial_state=x["s0"]), cpu_reps)
         model = cpu_model()
         res["cpu_baseline"] = dict(value=round(T / dt), unit="tokens/s/layer", us_per_layer=round(dt * 1e6),
                                    cores=threads, kind="port", cpu_model=model,
                                    sample=f"oracle gdn_prefill_core (per-sequence loop) on the same 16 prompts "
-                                          f"({T} tokens), one pass, torch {torch.__version__} CPU, {threads} "
-                                          f"threads on {model}")
+                                          f"({T} tokens), warm-up then median of {cpu_reps} passes, torch "
+                                          f"{torch.__version__} CPU, {threads} threads on {model}")
     return res
 
 
-def bench_prefill_long(gdn, dev, T=32768, seed=3, check=True):
-    """B=1, T=32768: per-layer time and the final-state rel-L2 against the CPU oracle, whose one pass
-    is also the CPU baseline."""
+def bench_prefill_long(gdn, dev, T=32768, seed=3, check=True, cpu_reps=5):
+    """B=1, T=32768: per-layer time and the final-state rel-L2 against the CPU oracle; the oracle's
+    pass, timed, is also the CPU baseline (median of cpu_reps after the checking pass)."""
     q, k, v, g, beta, s0 = _gdn_inputs(T, seed, dev)
     run = lambda: gdn.fast_chunk_gated_delta_rule_v2(q, k, v, g, beta, initial_state=s0, output_final_state=True,
                                                      use_qk_l2norm_in_kernel=True)
@@ -243,18 +259,19 @@ def bench_prefill_long(gdn, dev, T=32768, seed=3, check=True):
         r = HV // HK
         oc = lambda x: x.cpu().repeat_interleave(r, dim=2)
         args = (oc(q), oc(k), v.cpu(), g.cpu(), beta.cpu(), 64, s0.cpu(), True, True)
-        t0 = time.perf_counter()
         o_ref, s_ref = oracle.chunk_gated_delta_rule_v2(*args)
-        dt = time.perf_counter() - t0
         rel = lambda x, y: ((x.double().cpu() - y.double()).norm() / y.double().norm()).item()
         res["out_rel_l2_vs_oracle"] = rel(o, o_ref)
         res["state_rel_l2_vs_oracle"] = rel(s, s_ref)
+        del o_ref, s_ref
+        # the checking pass doubles as the warm-up; then the median of `cpu_reps` timed passes
+        dt = _median_time(lambda: oracle.chunk_gated_delta_rule_v2(*args), cpu_reps, warm=False)
         model = cpu_model()
         res["cpu_baseline"] = dict(value=round(T / dt), unit="tokens/s/layer", us_per_layer=round(dt * 1e6),
                                    cores=threads, kind="port", cpu_model=model,
-                                   sample=f"oracle chunk_gated_delta_rule_v2, B=1 T={T} H_v={HV} d={D}, the pass "
-                                          f"that checks the GPU result, torch {torch.__version__} CPU, {threads} "
-                                          f"threads on {model}")
+                                   sample=f"oracle chunk_gated_delta_rule_v2, B=1 T={T} H_v={HV} d={D}, median of "
+                                          f"{cpu_reps} passes after the one that checks the GPU result, torch "
+                                          f"{torch.__version__} CPU, {threads} threads on {model}")
     return res
 
 
@@ -270,9 +287,11 @@ def cpu_model():
     return "unknown"
 
 
-def _median_time(fn, reps):
-    """One untimed warm-up pass, then the median wall time of `reps` passes."""
-    fn()
+def _median_time(fn, reps, warm=True):
+    """One untimed warm-up pass (unless the caller has just run one), then the median wall time of
+    `reps` passes."""
+    if warm:
+        fn()
     times = []
     for _ in range(reps):
         t0 = time.perf_counter()
@@ -445,6 +464,7 @@ def main():
     res = {}
     if args.only in (None, "decode"):
         res["decode"] = bench_decode(gdn, dev, args.steps, args.warmup)
+        res["decode_share"] = [bench_decode_tp_share(gdn, dev, args.steps, args.warmup)]
     if args.only == "prefill8192":
         res["prefill"] = [bench_prefill(gdn, dev, reps=args.steps)]
     elif args.only == "varlen":
@@ -492,7 +512,7 @@ def main():
                      "us_per_launch_graph": round(dec["us_per_layer"], 3),
                      "us_per_launch_eager": round(dec["us_per_layer_eager"], 3)},
     }
-    line["secondary"] = res.get("prefill", []) + res.get("hybrid", [])
+    line["secondary"] = res.get("decode_share", []) + res.get("prefill", []) + res.get("hybrid", [])
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline_decode()
     print(json.dumps(line))
