@@ -234,7 +234,10 @@ __device__ __forceinline__ bf16x8 lds_frag(const uint8_t* base, int f, int lane)
 // Segment bookkeeping of the chunked prefill (shared by its kernels).
 namespace sg {
 constexpr int NT = 512;                      // 8 waves
-constexpr int kMinSeg = 4;                   // shortest segment the host cuts (chunks)
+// Shortest segment the host cuts (chunks).  2: a short prompt's heads spread over more workgroups
+// (353 tokens at 48 value heads: segments of 2 chunks, 3 chunk steps a workgroup instead of 5);
+// a later segment's warm-up must then fit in the 2 chunks before it.
+constexpr int kMinSeg = 2;
 constexpr int kTargetItems = 256;            // segments x value heads the host aims for
 constexpr float kNegligibleLog = -44.3614f;  // ln(2^-64): a segment map A_j this small is not formed
 // A warm-up drops a map bounded by 2^-16 relative to the state before it: 2^7 below the bf16
