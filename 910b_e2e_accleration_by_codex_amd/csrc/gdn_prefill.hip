@@ -595,8 +595,9 @@ __global__ __launch_bounds__(pf::NT, 2) void inv_kernel(const uint16_t* __restri
 // A segment other than the first of its sequence needs its true initial state: the state after
 // segment j is S_{j+1} = A_j S_j + B_j, with A_j the segment's linear map (the chain run from the
 // identity with U = 0) and B_j its affine part (run from zero).  A summary pass computes A_j and
-// B_j for every segment with a successor, seg_combine_kernel applies them in order per sequence
-// (fp32 MFMA), and the output pass runs every segment from its true state.
+// B_j for every segment with a successor, and the output pass's workgroup of segment j first applies
+// S_{k+1} = A_k S_k + B_k for k < j (bf16 hi + lo products on MFMA, A_k's fragments staged in LDS
+// by the local waves) and then runs the segment from that state.
 // With unit keys (in-kernel l2norm) and 0 <= beta <= 1 each token's map gamma (I - beta k k^T) has
 // spectral norm <= gamma, so ||A_j|| <= exp(sum of g over segment j).  When that bound is below
 // 2^-64, A_j S_j lies far below the fp32 rounding of S_{j+1} and A_j is not formed (flag 0).
@@ -654,6 +655,17 @@ struct SegSmem {
 };
 
 enum SegMode { kSegOut = 0, kSegB = 1, kSegA = 2 };
+
+// A transition slot (sg::kTrans floats per (slot, value head)) as the summary pass writes it and the
+// output pass reads it: A_j as bf16 A fragments, 32 hi parts then 32 lo parts (fragment rt * 4 + kb:
+// rows 16 rt .. 16 rt + 15 of A_j, k-block kb in k-slot order), then B_j in the chain waves' register
+// order (chain wave wc's S[sl][i] at f32x4 index (wc * 2 + sl) * 8 + i of lane block `lane`).
+namespace tr {
+constexpr int A_HI = 0, A_LO = 32 * ws::FRAG, B = 64 * ws::FRAG;  // byte offsets
+static_assert(B + pf::D * pf::D * 4 == sg::kTrans * 4, "a slot holds A's fragments and B");
+__device__ __forceinline__ int b_at(int wc, int sl, int i, int lane) { return (((wc * 2 + sl) * 8 + i) * 64 + lane) * 4; }
+}  // namespace tr
+constexpr int kALd = pf::D + 4;  // row pitch (floats) of A_j's row-major LDS copy in the summary's fragment pass
 
 // A local wave's inputs for one chunk, loaded a chunk ahead.  Local wave w (threads t < 256) holds K
 // and V rows 4 tq + i x features 8 fb .. (t = 16 tq + fb: rows 16 w .. 16 w + 15), the q fragments of
@@ -1208,6 +1220,8 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     const int* __restrict__ warm, GateArgs gate) {
   using namespace pf;
   __shared__ SegSmem sm;
+  static_assert(sizeof(SegSmem) >= (size_t)D * kALd * 4 && sizeof(SegSmem) >= 2 * 64 * ws::FRAG,
+                "the chunk buffers hold A_j's row-major copy and two slots' A fragments");
   const int t = threadIdx.x, w = t >> 6, lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
   int mode, h, s, idx, slot = -1;
   if (kPass == 0) {
@@ -1231,6 +1245,10 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     if (seq_warm_ok(tab, warm, Hv, h, s)) return;  // the output pass warms up instead
   }
   const bool warm_path = kPass == 0 && slot >= 0 && seq_warm_ok(tab, warm, Hv, h, s);
+  // the output pass of a later segment on the exact path forms its initial state from the summaries of
+  // the idx slots before it (ts_first .. ts_first + idx - 1)
+  const int combine_steps = (kPass == 0 && slot >= 0 && !warm_path) ? idx : 0;
+  const int ts_first = tab.first_slot(s);
   const int kh = h / (Hv / Hqk);
   const int nch_s = tab.nch(s), c_begin = idx * tab.L;
   const int n = nch_s - c_begin < tab.L ? nch_s - c_begin : tab.L;
@@ -1339,6 +1357,38 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
       phase2(sm.buf[(c + 1) & 1], c + 1 >= w0);
       lds_barrier();
     };
+    if (combine_steps > 0) {
+      // the combination's A fragments: slot kk's into LDS half kk & 1 while the chain waves use the other
+      // half; each slot's loads are issued a step before its LDS writes (two register sets, the loop
+      // unrolled by two), so their latency hides behind a step of products
+      typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+      u32x4 a0[16], a1[16];
+      auto live = [&](int kk) { return kk < combine_steps && tflags[(int64_t)(ts_first + kk) * Hv + h] != 0; };
+      auto fetch_a = [&](u32x4 (&a)[16], int kk) __attribute__((always_inline)) {
+        const uint8_t* src = reinterpret_cast<const uint8_t*>(trans + ((int64_t)(ts_first + kk) * Hv + h) * sg::kTrans);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) a[u] = *reinterpret_cast<const u32x4*>(src + (t + 256 * u) * 16);
+      };
+      auto put_a = [&](const u32x4 (&a)[16], int kk) __attribute__((always_inline)) {
+        uint8_t* dst = reinterpret_cast<uint8_t*>(&sm) + (kk & 1) * (64 * ws::FRAG);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) *reinterpret_cast<u32x4*>(dst + (t + 256 * u) * 16) = a[u];
+      };
+      if (live(0)) fetch_a(a0, 0);
+      if (live(1)) fetch_a(a1, 1);
+      if (live(0)) put_a(a0, 0);
+      __syncthreads();
+      for (int kk = 0; kk < combine_steps; kk += 2) {  // the chain runs step kk, then step kk + 1
+        if (live(kk + 1)) put_a(a1, kk + 1);  // half 1 was last read in step kk - 1
+        if (live(kk + 2)) fetch_a(a0, kk + 2);
+        __syncthreads();
+        if (kk + 1 < combine_steps) {
+          if (live(kk + 2)) put_a(a0, kk + 2);
+          if (live(kk + 3)) fetch_a(a1, kk + 3);
+          __syncthreads();
+        }
+      }
+    }
     if (ntot > 0) {
       if (kNorm) norm_req_z(-1);  // unused: every step then finds one z request in flight
       load(ia, 0, std::integral_constant<int, -1>{});
@@ -1373,14 +1423,11 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     // ------------------------------------------------------------ chain waves
     const int wc = w - 4;
     ChainRegs R;
-    {  // initial state
+    {  // initial state: the sequence's (then, on the exact path, the combination below), or zero
       const float* src = nullptr;
-      if (mode == kSegOut) {
-        if (slot >= 0) src = warm_path ? nullptr : tslot + D * D;
-        else if (init) {
-          const int r0 = state_row(rows, n_rows, s);
-          if (r0 >= 0) src = init + ((int64_t)r0 * Hv + h) * D * D;
-        }
+      if (mode == kSegOut && (slot < 0 || !warm_path) && init) {
+        const int r0 = state_row(rows, n_rows, s);
+        if (r0 >= 0) src = init + ((int64_t)r0 * Hv + h) * D * D;
       }
       if (src) {
 #pragma unroll
@@ -1397,6 +1444,52 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
 #pragma unroll
             for (int r = 0; r < 4; ++r)
               R.S[sl][i][r] = (mode == kSegA && 16 * i + 4 * g4 + r == 32 * wc + 16 * sl + c16) ? 1.f : 0.f;
+      }
+    }
+    if (combine_steps > 0) {  // S_{k+1} = A_k S_k + B_k over the slots before this segment
+      f32x4 bn[2][8];
+      auto fetch_b = [&](int kk) __attribute__((always_inline)) {
+        const float* src = trans + ((int64_t)(ts_first + kk) * Hv + h) * sg::kTrans + D * D;
+#pragma unroll
+        for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) bn[sl][i] = *reinterpret_cast<const f32x4*>(src + tr::b_at(wc, sl, i, lane));
+      };
+      fetch_b(0);
+      __syncthreads();
+      for (int kk = 0; kk < combine_steps; ++kk) {
+        const bool fl = tflags[(int64_t)(ts_first + kk) * Hv + h] != 0;
+        f32x4 acc[2][8];
+#pragma unroll
+        for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[sl][i] = bn[sl][i];
+        if (kk + 1 < combine_steps) fetch_b(kk + 1);
+        if (fl) {
+          const uint8_t* ah = reinterpret_cast<const uint8_t*>(&sm) + (kk & 1) * (64 * ws::FRAG);
+          const uint8_t* al = ah + 32 * ws::FRAG;
+#pragma unroll
+          for (int kb = 0; kb < 4; ++kb) {
+            bf16x8 sh[2], slo[2];
+#pragma unroll
+            for (int sl = 0; sl < 2; ++sl) split_bf16(R.S[sl][2 * kb], R.S[sl][2 * kb + 1], sh[sl], slo[sl]);
+#pragma unroll
+            for (int rt = 0; rt < 8; ++rt) {
+              const bf16x8 fh = lds_frag(ah, rt * 4 + kb, lane), fo = lds_frag(al, rt * 4 + kb, lane);
+#pragma unroll
+              for (int sl = 0; sl < 2; ++sl) {
+                acc[sl][rt] = mma(fh, sh[sl], acc[sl][rt]);
+                acc[sl][rt] = mma(fh, slo[sl], acc[sl][rt]);
+                acc[sl][rt] = mma(fo, sh[sl], acc[sl][rt]);
+              }
+            }
+          }
+        }
+#pragma unroll
+        for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) R.S[sl][i] = acc[sl][i];
+        __syncthreads();
       }
     }
     lds_barrier();
@@ -1420,110 +1513,54 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
       lds_barrier();
     }
     // the state after the segment
-    float* dst = nullptr;
     if (mode == kSegOut) {
       if (final_state && idx == tab.nseg_of(nch_s) - 1) {
         const int r0 = state_row(rows, n_rows, s);
-        if (r0 >= 0) dst = final_state + ((int64_t)r0 * Hv + h) * D * D;
+        if (r0 >= 0) {
+          float* dst = final_state + ((int64_t)r0 * Hv + h) * D * D;
+#pragma unroll
+          for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) dst[(16 * i + 4 * g4 + r) * D + 32 * wc + 16 * sl + c16] = R.S[sl][i][r];
+        }
       }
-    } else {
-      dst = tslot + (mode == kSegA ? 0 : D * D);
-    }
-    if (dst) {
+    } else if (mode == kSegB) {  // B_j in register order
+      float* dst = tslot + D * D;
+#pragma unroll
+      for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) *reinterpret_cast<f32x4*>(dst + tr::b_at(wc, sl, i, lane)) = R.S[sl][i];
+    } else {  // A_j row-major into LDS, which every wave has finished with, for the fragment pass below
+      __syncthreads();
+      float* At = reinterpret_cast<float*>(&sm);
 #pragma unroll
       for (int sl = 0; sl < 2; ++sl)
 #pragma unroll
         for (int i = 0; i < 8; ++i)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) dst[(16 * i + 4 * g4 + r) * D + 32 * wc + 16 * sl + c16] = R.S[sl][i][r];
+          for (int r = 0; r < 4; ++r) At[(16 * i + 4 * g4 + r) * kALd + 32 * wc + 16 * sl + c16] = R.S[sl][i][r];
+      __syncthreads();
     }
   }
-}
-
-// S_{j+1} = A_j S_j + B_j along each sequence's segments, in fp32 (v_mfma_f32_16x16x4_f32); the result
-// overwrites B_j, which the output pass reads as segment j+1's initial state.  One workgroup per
-// (sequence, value head, 16-column slice); the 8 slices of a (sequence, head) share blockIdx % 8,
-// hence an XCD and its L2.  Pairs without transition slots, or whose later segments warm up, exit
-// at once.  A_j flagged negligible is skipped: S_{j+1} = B_j as written.  The walk is sequential in
-// S only: slot j + 1's A rows (16 per thread's 16-byte loads) and its B entries are requested into
-// registers before slot j's product, so each step waits on LDS and the MFMA, not on memory.
-struct CombineSmem {
-  float A[pf::D * (pf::D + 4)];
-  float S[pf::D * 16];
-};
-__global__ __launch_bounds__(256) void seg_combine_kernel(SegTable tab, int Hv, const float* __restrict__ init,
-                                                         const int32_t* __restrict__ rows, int n_rows,
-                                                         float* __restrict__ trans, const int* __restrict__ tflags,
-                                                         const int* __restrict__ warm) {
-  using namespace pf;
-  __shared__ CombineSmem sm;
-  const int b = blockIdx.x;
-  const int item = (b >> 6) * 8 + (b & 7), n = (b >> 3) & 7;  // item = (sequence, value head)
-  const int s = item / Hv, h = item % Hv;
-  if (s >= tab.nseq) return;
-  const int ts = tab.first_slot(s), nsl = tab.first_slot(s + 1) - ts;
-  if (nsl == 0 || seq_warm_ok(tab, warm, Hv, h, s)) return;
-  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
-  const int LDA = D + 4;
-  const float* s0 = nullptr;
-  if (init) {
-    const int r0 = state_row(rows, n_rows, s);
-    if (r0 >= 0) s0 = init + ((int64_t)r0 * Hv + h) * D * D;
-  }
-  // S slice: row p / 16 ... thread t holds rows t / 16 + 16 m, column t % 16
-  for (int i = t; i < D * 16; i += 256) sm.S[i] = s0 ? s0[(i >> 4) * D + 16 * n + (i & 15)] : 0.f;
-  // slot kk's operands: thread t loads A's 16-byte pieces t + 256 i (the whole slot is allocated, so
-  // a negligible A is read and not used) and the B entries of the 8 outputs it forms: rows
-  // 16 (2 w + m) + 4 (lane / 16) + r, column 16 n + lane % 16
-  f32x4 an[16];
-  float bn[8];
-  int fn = 0;
-  auto fetch = [&](int kk) __attribute__((always_inline)) {
-    const int64_t slot = (int64_t)(ts + kk) * Hv + h;
-    const float* base = trans + slot * sg::kTrans;
-    fn = tflags[slot];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) an[i] = *reinterpret_cast<const f32x4*>(base + 4 * (t + 256 * i));
-#pragma unroll
-    for (int m = 0; m < 2; ++m)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) bn[4 * m + r] = base[D * D + (16 * (2 * w + m) + 4 * (lane >> 4) + r) * D + 16 * n + (lane & 15)];
-  };
-  fetch(0);
-  for (int kk = 0; kk < nsl; ++kk) {
-    const int fl = fn;
-    float bc[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) bc[e] = bn[e];
-    if (fl) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int q4 = t + 256 * i;
-        *reinterpret_cast<f32x4*>(&sm.A[(q4 >> 5) * LDA + 4 * (q4 & 31)]) = an[i];
-      }
+  if (kPass == 1 && mode == kSegA) {  // A_j's bf16 hi + lo A fragments, 4 (fragment, lane) items a thread
+    if (w < 4) {
+      __syncthreads();
+      __syncthreads();
     }
-    if (kk + 1 < nsl) fetch(kk + 1);
-    __syncthreads();  // A_kk and S_kk in LDS
-    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-    if (fl) {
+    const float* At = reinterpret_cast<const float*>(&sm);
+    uint8_t* a8 = reinterpret_cast<uint8_t*>(tslot);
 #pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        const int rt = 2 * w + m;  // row tile
-#pragma unroll 8
-        for (int k0 = 0; k0 < D; k0 += 16) acc[m] = mm16_f32(&sm.A[16 * rt * LDA + k0], LDA, &sm.S[k0 * 16], 16, acc[m], lane);
-      }
+    for (int u = 0; u < 4; ++u) {
+      const int item = t + sg::NT * u, f = item >> 6, ln = item & 63, rt = f >> 2, kb = f & 3;
+      const float* row = At + (16 * rt + (ln & 15)) * kALd + 32 * kb + 4 * (ln >> 4);
+      const f32x4 x0 = *reinterpret_cast<const f32x4*>(row), x1 = *reinterpret_cast<const f32x4*>(row + 16);
+      bf16x8 hi, lo;
+      split_bf16(x0, x1, hi, lo);
+      *reinterpret_cast<bf16x8*>(a8 + tr::A_HI + f * ws::FRAG + ln * 16) = hi;
+      *reinterpret_cast<bf16x8*>(a8 + tr::A_LO + f * ws::FRAG + ln * 16) = lo;
     }
-    __syncthreads();  // every wave has read A and S
-    float* Bm = trans + ((int64_t)(ts + kk) * Hv + h) * sg::kTrans + D * D;
-#pragma unroll
-    for (int m = 0; m < 2; ++m)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = 16 * (2 * w + m) + 4 * (lane >> 4) + r, c = lane & 15;
-        const float x = acc[m][r] + bc[4 * m + r];
-        sm.S[row * 16 + c] = x;
-        if (fl) Bm[row * D + 16 * n + c] = x;
-      }
   }
 }
 
@@ -1954,11 +1991,6 @@ int chunk_prefill_impl(const void* q, int64_t q_stride, const void* k, int64_t k
   if (lay.nslots > 0 && max_seq_chunks > lay.L) {  // segment summaries and their combination where no warm-up fits
     launch(1, lay.nslots * Hv * 2);
     int rc = check_launch("gdn_chunk_prefill(summary)");
-    if (rc) return rc;
-    const int64_t items = (int64_t)nseq * Hv;
-    seg_combine_kernel<<<(unsigned)((items + 7) / 8 * 64), 256, 0, st>>>(tab, Hv, initial_state, state_rows, n_rows,
-                                                                       trans, tflags, warm);
-    rc = check_launch("gdn_chunk_prefill(combine)");
     if (rc) return rc;
   }
   launch(0, nseg_max * Hv);
