@@ -1868,8 +1868,9 @@ int64_t seg_len(int64_t total_chunks, int nseq, int Hv) {
 }
 // Workspace layout: the segment table (nseq + 1 int32), the longest-first segment order (int32 per
 // segment), the transition flags (int32 per (slot,
-// value head)), the warm-up lengths (int32 per (slot, value head)), the transition slots (A, B fp32
-// per (slot, value head)), the inverse kernel's fragments (5 KiB per (chunk, value head)) and its
+// value head)), the warm-up lengths (int32 per (slot, value head)), the transition slots (128 KiB per
+// (slot, value head): A's bf16 hi + lo fragments, then B in fp32; layout in namespace tr), the
+// inverse kernel's fragments (5 KiB per (chunk, value head)) and its
 // records of 64 K l2norm factors then the chunk's 64 g values (fp32, 512 B per (chunk, value head)),
 // each part 256-byte aligned.
 struct SegLayout {

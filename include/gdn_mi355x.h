@@ -178,7 +178,7 @@ int64_t gdn_chunk_prefill_workspace_bytes(int64_t total_chunks, int nseq, int Hv
  *     seq_chunk0[s] = sum over earlier sequences of ceil(len/64); or both NULL for nseq
  *     sequences of seq_len tokens.  total_chunks = sum of ceil(len/64) over sequences.  With
  *     cu_seqlens, seq_len is 0 or an upper bound of every sequence's length: when no sequence can
- *     span more than one segment the call skips the segment summaries (two launches).  A bound
+ *     span more than one segment the call skips the segment summaries (one launch).  A bound
  *     below a sequence's true length gives wrong results for that sequence.
  *   workspace: device memory of gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hv) bytes,
  *     256-byte aligned (caller-owned; contents are scratch).
