@@ -1468,21 +1468,30 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
         if (fl) {
           const uint8_t* ah = reinterpret_cast<const uint8_t*>(&sm) + (kk & 1) * (64 * ws::FRAG);
           const uint8_t* al = ah + 32 * ws::FRAG;
+          // the 32 (k-block, row tile) steps in order, each one's two fragments requested a step ahead
+          bf16x8 nh = lds_frag(ah, 0, lane), no = lds_frag(al, 0, lane);
+          bf16x8 sh[2], slo[2];
 #pragma unroll
-          for (int kb = 0; kb < 4; ++kb) {
-            bf16x8 sh[2], slo[2];
+          for (int it = 0; it < 32; ++it) {
+            const int kb = it >> 3, rt = it & 7;
+            if (rt == 0) {
 #pragma unroll
-            for (int sl = 0; sl < 2; ++sl) split_bf16(R.S[sl][2 * kb], R.S[sl][2 * kb + 1], sh[sl], slo[sl]);
-#pragma unroll
-            for (int rt = 0; rt < 8; ++rt) {
-              const bf16x8 fh = lds_frag(ah, rt * 4 + kb, lane), fo = lds_frag(al, rt * 4 + kb, lane);
-#pragma unroll
-              for (int sl = 0; sl < 2; ++sl) {
-                acc[sl][rt] = mma(fh, sh[sl], acc[sl][rt]);
-                acc[sl][rt] = mma(fh, slo[sl], acc[sl][rt]);
-                acc[sl][rt] = mma(fo, sh[sl], acc[sl][rt]);
-              }
+              for (int sl = 0; sl < 2; ++sl) split_bf16(R.S[sl][2 * kb], R.S[sl][2 * kb + 1], sh[sl], slo[sl]);
             }
+            const bf16x8 fh = nh, fo = no;
+            if (it < 31) {
+              const int f = ((it + 1) & 7) * 4 + ((it + 1) >> 3);
+              nh = lds_frag(ah, f, lane);
+              no = lds_frag(al, f, lane);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int sl = 0; sl < 2; ++sl) {
+              acc[sl][rt] = mma(fh, sh[sl], acc[sl][rt]);
+              acc[sl][rt] = mma(fh, slo[sl], acc[sl][rt]);
+              acc[sl][rt] = mma(fo, sh[sl], acc[sl][rt]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
           }
         }
 #pragma unroll
