@@ -5,7 +5,8 @@
     (gdn_prefill_core) against the oracle's composition (src/cb_tp.py:153-181, :230-263);
   * one long sequence, T = 32768, the chunked rule (src/gdn_chunk_fast2.py:11-62) at full width,
     output and final state of every value head against the oracle;
-  * the chunked rule at Qwen3.5-27B's GDN shape (H_v = 48) at T = 8192, seven value heads;
+  * the chunked rule at Qwen3.5-27B's GDN shape (H_v = 48) at T = 8192, seven value heads, and the
+    fused prefill layer at that shape (conv 10240 x 4) over 4 packed prompts, every head;
   * the Qwen3.5-27B-shaped decode step (48 GDN + 16 attention layers, hidden 5120, H_v = 48, 16
     slots, contexts uniform in [512, 4096]): graph replays equal eager steps over three steps, and
     one GDN layer at that shape (projections, fused core, out_proj) against the oracle's core.
@@ -62,6 +63,43 @@ def test_varlen_prefill_layer_16_prompts(gdn, oracle, dev, history):
         assert rel_l2(rec[s], ref_rec[s]) <= STATE_TOL, f"sequence {s}"
         lo, hi = int(cu[s]), int(cu[s + 1])
         assert rel_l2(core[lo:hi], ref_core[lo:hi]) <= OUT_TOL, f"sequence {s}"
+
+
+@pytest.mark.gpu
+def test_prefill_layer_model_shape_Hv48(gdn, oracle, dev):
+    """The fused prefill layer at Qwen3.5-27B's GDN shape (H_k=16, H_v=48, d=128, conv 10240 x 4; the
+    reference model, src/cb_tp.py:7-10): 4 packed prompts (353 tokens -- the reference's published prefill
+    size --, 1000, 64 and 517) with conv history, initial states, and per-head decays from slow to fast
+    (exp(A_log) from 0.002 to 2), against the oracle's composition: conv states exact, outputs within
+    1e-2 and states within 1e-3 per prompt."""
+    Hk, Hv, K = 16, 48, 4
+    C = (2 * Hk + Hv) * D
+    lens = [353, 1000, 64, 517]
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int32)
+    T = int(cu[-1])
+    g_ = torch.Generator().manual_seed(27)
+    bf = torch.bfloat16
+    x = dict(mixed=torch.randn(T, C, generator=g_).to(bf), z=torch.randn(T, Hv * D, generator=g_).to(bf),
+             a=torch.randn(T, Hv, generator=g_).to(bf), b=torch.randn(T, Hv, generator=g_).to(bf),
+             cw=(0.5 * torch.randn(C, K, generator=g_)).to(bf),
+             A_log=torch.log(torch.logspace(-2.7, 0.3, Hv)), dt=torch.zeros(Hv),
+             nw=(1 + 0.02 * torch.randn(D, generator=g_)).to(bf),
+             s0=0.02 * torch.randn(len(lens), Hv, D, D, generator=g_),
+             hist=torch.randn(len(lens), C, K, generator=g_).to(bf))
+    ref_core, ref_conv, ref_rec = oracle.gdn_prefill_core(x["mixed"], x["z"], x["a"], x["b"], x["cw"], x["A_log"],
+                                                          x["dt"], x["nw"], Hk, Hv, D, cu_seqlens=cu,
+                                                          conv_history=x["hist"], initial_state=x["s0"])
+    d = {k: v.to(dev) for k, v in x.items()}
+    core, conv, rec = gdn.gdn_prefill_core(d["mixed"], d["z"], d["a"], d["b"], d["cw"], d["A_log"], d["dt"], d["nw"],
+                                           Hk, Hv, D, cu_seqlens=cu, conv_history=d["hist"], initial_state=d["s0"])
+    torch.cuda.synchronize()
+    assert torch.equal(conv.cpu(), ref_conv)
+    for s_ in range(len(lens)):
+        lo, hi = int(cu[s_]), int(cu[s_ + 1])
+        assert rel_l2(core[lo:hi], ref_core[lo:hi]) <= OUT_TOL, f"prompt {s_}"
+        for h in range(Hv):
+            e = rel_l2(rec[s_, h], ref_rec[s_, h])
+            assert e <= STATE_TOL, (s_, h, e)
 
 
 @pytest.mark.gpu
