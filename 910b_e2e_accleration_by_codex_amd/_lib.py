@@ -137,6 +137,18 @@ def dtype_code(t):
     raise TypeError(f"unsupported dtype {t.dtype} (float32, bfloat16 or float16)")
 
 
+def dense_rows(t):
+    """A 2-D [rows, cols] tensor as the row kernels read it: unit column stride, row stride a multiple
+    of 8 elements, base 16-byte aligned -- t itself when it qualifies, else a dense copy.  Returns
+    (tensor, row stride).  torch gives a size-1 dimension an arbitrary stride, and one row's stride
+    is never used, so a single row counts its length as its stride."""
+    rs = t.stride(0) if t.shape[0] > 1 else t.shape[1]
+    if (t.stride(1) != 1 and t.shape[1] > 1) or rs % 8 or t.data_ptr() % 16:
+        t = t.clone(memory_format=torch.contiguous_format)
+        rs = t.shape[1]
+    return t, rs
+
+
 def require_cuda(*ts):
     for t in ts:
         if t is not None and not t.is_cuda:

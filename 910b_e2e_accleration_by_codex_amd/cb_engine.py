@@ -228,12 +228,11 @@ def decode_linear(x, weight):
         if K != weight.K or M > 16 or x.dtype != torch.bfloat16:
             raise ValueError(f"decode_linear: x {tuple(x.shape)} {x.dtype} does not fit the packed weight "
                              f"[{weight.N}, {weight.K}] (at most 16 bf16 rows)")
-        if x.stride(1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
-            x = x.contiguous()
+        x, xs = _lib.dense_rows(x)
         out = torch.empty(M, weight.N, dtype=torch.bfloat16, device=x.device)
         wb = int(_lib.lib().gdn_decode_linear_workspace_bytes(M, weight.N, K))
         ws = torch.empty(max(wb // 4, 1), dtype=torch.float32, device=x.device) if wb else None
-        _lib.call("gdn_decode_linear_packed", _lib.ptr(x), x.stride(0), _lib.ptr(weight.data), _lib.ptr(out),
+        _lib.call("gdn_decode_linear_packed", _lib.ptr(x), xs, _lib.ptr(weight.data), _lib.ptr(out),
                   out.stride(0), M, weight.N, K, _lib.ptr(ws), wb, _lib.stream_of(x))
         return out
     _lib.require_cuda(x, weight)
@@ -273,11 +272,10 @@ def decode_linear_partial(x, weight):
     M, K = x.shape
     if not isinstance(weight, PackedWeight) or K != weight.K or M > 16 or x.dtype != torch.bfloat16:
         raise ValueError("decode_linear_partial: bf16 x [M <= 16, K] and a PackedWeight [N, K]")
-    if x.stride(1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
-        x = x.contiguous()
+    x, xs = _lib.dense_rows(x)
     splits = int(_lib.lib().gdn_decode_linear_splits(M, weight.N, K))
     part = torch.empty(splits, M, weight.N, dtype=torch.float32, device=x.device)
-    _lib.call("gdn_decode_linear_packed_partial", _lib.ptr(x), x.stride(0), _lib.ptr(weight.data), _lib.ptr(part),
+    _lib.call("gdn_decode_linear_packed_partial", _lib.ptr(x), xs, _lib.ptr(weight.data), _lib.ptr(part),
               M, weight.N, K, part.numel() * 4, _lib.stream_of(x))
     return Partials(part, splits, M, weight.N)
 

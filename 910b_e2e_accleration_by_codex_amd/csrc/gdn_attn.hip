@@ -307,7 +307,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const int64_t* __rest
   }
   const float a = ns > 0 ? rbf(o / L) : 0.f;  // a negative position attends to nothing: zero output
   const float gate = proj(n, (int64_t)h * 2 * HD + HD + d);
-  out[n * out_stride + (int64_t)h * HD + d] = f2bf(a * rbf(sigmoid_f(gate)));
+  out[n * out_stride + (int64_t)h * HD + d] = f2bf(a * bf2f(sigmoid_bf16(gate)));
 }
 
 template <int HD, int G>

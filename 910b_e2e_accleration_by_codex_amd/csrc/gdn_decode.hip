@@ -169,7 +169,8 @@ __global__ __launch_bounds__(kHeadThreads) void recurrent_step_kernel(
 // ============================================================================================
 // Conv update (elem_conv_update): one thread per (slot, channel).
 // ============================================================================================
-// window = [state[1..K-1], x]; out = silu(bf16(sum_i bf16(window_i * w_i)) (+ bias)); state <- window.
+// window = [state[1..K-1], x]; conv = bf16(sum_i bf16(window_i * w_i)) (+ bias, rounded); state <- window.
+// The callers apply the SiLU (silu_bf16_n).
 __device__ __forceinline__ float conv_channel(uint16_t* st, const uint16_t* wt, float bias, bool has_bias,
                                               uint16_t xv, int K) {
   float acc = 0.f;
@@ -194,7 +195,7 @@ __device__ __forceinline__ float conv_channel(uint16_t* st, const uint16_t* wt, 
   }
   float o = rbf(acc);
   if (has_bias) o = rbf(o + bias);
-  return rbf(silu_f(o));
+  return o;
 }
 
 // K == 4 conv split in two halves so the loads can be issued ahead of the state stream.
@@ -221,7 +222,7 @@ __device__ __forceinline__ float conv4_finish(const Conv4& c, uint2* nw, float b
   *nw = nv;
   float o = rbf(acc);
   if (has_bias) o = rbf(o + bias);
-  return rbf(silu_f(o));
+  return o;
 }
 
 __global__ __launch_bounds__(256) void conv_update_kernel(const uint16_t* __restrict__ x, int64_t x_stride,
@@ -236,7 +237,7 @@ __global__ __launch_bounds__(256) void conv_update_kernel(const uint16_t* __rest
   const float b = bias ? bf2f(bias[c]) : 0.f;
   const float o = conv_channel(state + i * K, weight + (int64_t)c * K, b, bias != nullptr,
                                x[n * x_stride + c], K);
-  out[n * out_stride + c] = f2bf(o);
+  out[n * out_stride + c] = silu_bf16(o);
 }
 
 // ============================================================================================
@@ -452,6 +453,12 @@ __global__ __launch_bounds__(kHeadThreads * R) void decode_fused_kernel(
         x[u] = conv_channel(conv_state + ((int64_t)n * C + ch) * K, conv_w + (int64_t)ch * K, bb, bias_on, xr[ch], K);
       }
     }
+    {
+      uint16_t sx[2];
+      silu_bf16_n<2>(x, sx);
+      x[0] = bf2f(sx[0]);
+      x[1] = bf2f(sx[1]);
+    }
     if (role < 2) {
       l2norm_pair<true>(x[0], x[1]);
       float* dst = role == 0 ? s_q : s_k;
@@ -464,7 +471,7 @@ __global__ __launch_bounds__(kHeadThreads * R) void decode_fused_kernel(
     }
   }
   if (gate_lane) {
-    s_beta[lane] = rbf(sigmoid_f(bf2f((uint16_t)g_b)));
+    s_beta[lane] = bf2f(sigmoid_bf16(bf2f((uint16_t)g_b)));
     s_gamma[lane] = expf(-expf(g_al) * softplus_f(bf2f((uint16_t)g_a) + g_dt));
   }
   lds_barrier();  // q, k, v, gamma, beta in LDS; the state loads stay in flight

@@ -44,13 +44,90 @@ __device__ __forceinline__ int state_row(const int32_t* rows, int n_rows, int s)
 }
 
 // ---- scalar math with torch's CPU formulas ------------------------------------------------
-__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
-// SiLU with the hardware exp and reciprocal (each within about 1 ulp in fp32, so a bf16 result is
-// within one bf16 ulp of the exactly rounded x / (1 + e^-x)); a third of silu_f's instructions.
+// SiLU with the hardware exp and reciprocal, in fp32, for the gated norms' gate factor: within 24
+// ulps of x / (1 + e^-x) (bf16 SiLU outputs go through silu_bf16 below).
 __device__ __forceinline__ float silu_fast(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
-__device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
 // F.softplus(x), beta = 1, threshold = 20.
 __device__ __forceinline__ float softplus_f(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
+// ---- SiLU and sigmoid of a bf16 tensor, bit for bit torch's ---------------------------------
+// torch evaluates F.silu and sigmoid on bf16 in fp32 (x / (1 + e^-x), 1 / (1 + e^-x)) and rounds
+// once to bf16.  Over all 65,280 finite bf16 inputs its results are the exact functions rounded to
+// fp32 and then to bf16, except where its fp32 e^-x overflows (x < -88.72: silu = x / inf = -0,
+// sigmoid = 0); and no exact value lies within 9e-9 (relative) of an fp32 rounding midpoint, so an
+// evaluation in double rounds to the same fp32 value.  A one-ulp slip of the fp32 value flips the
+// bf16 result for a handful of inputs (x = -2^-8 and 2^-7 among them), and a flipped conv output or
+// beta of a sequence's last token moves a fast-decaying head's final state by up to 7e-3.
+__device__ __noinline__ static float silu_exact(float x) {
+  if (x < -88.72283935546875f) return x / __builtin_huge_valf();
+  const double xd = x;
+  return (float)(xd / (1.0 + exp(-xd)));
+}
+__device__ __noinline__ static float sigmoid_exact(float x) {
+  if (x < -88.72283935546875f) return 0.f;  // 1 / (1 + inf)
+  return (float)(1.0 / (1.0 + exp(-(double)x)));
+}
+// e^x for -92 < x < 46: x log2(e) carried in two parts into the hardware exp2, whose own error then
+// dominates (the single-product __expf loses |x| ulps in the rounding of x log2(e)).
+__device__ __forceinline__ float exp_split(float x) {
+  constexpr float kL = 1.44269502162933349609375f;  // log2(e) rounded to fp32
+  constexpr float kLlo = 1.925963033500e-8f;        // log2(e) - kL
+  const float t = x * kL;
+  const float tl = fmaf(x, kLlo, fmaf(x, kL, -t));   // x log2(e) - t
+  return __builtin_amdgcn_exp2f(t) * fmaf(tl, 0.693147180559945f, 1.0f);
+}
+// Two estimates decide the bf16 rounding for all but a few inputs.  silu_fast and sigmoid_fast are
+// within 6 fp32 ulps of the correctly rounded values for every bf16 input with |x| <= 8; the
+// exp_split estimates below, within 2 ulps for every bf16 input in [-32, 64] (both measured over all
+// of them).  An estimate more than its error bound away from a bf16 rounding midpoint rounds to bf16
+// as the exact value does; the fast one fails that (or |x| > 8) for about 1e-4 of N(0, 1) inputs,
+// which then take the exp_split estimate, and the few inputs it leaves (4 bf16 values for each
+// function, x = -2^-8 and 2^-7 among them; x outside [-32, 64]; NaN) take the double evaluation.
+__device__ __forceinline__ float silu_est(float x) { return x * __builtin_amdgcn_rcpf(1.0f + exp_split(-x)); }
+__device__ __forceinline__ float sigmoid_est(float x) { return __builtin_amdgcn_rcpf(1.0f + exp_split(-x)); }
+__device__ __forceinline__ float sigmoid_fast(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
+__device__ __forceinline__ bool bf16_near_mid(float y, uint32_t ulps) {
+  return (__float_as_uint(y) & 0xffffu) - (0x8000u - ulps) <= 2 * ulps;
+}
+__device__ __forceinline__ bool fast_undecided(float y, float x) { return !(fabsf(x) <= 8.f) || bf16_near_mid(y, 7); }
+__device__ __forceinline__ bool est_undecided(float y, float x) {
+  return !(x >= -32.f && x <= 64.f) || bf16_near_mid(y, 3);
+}
+// silu of N values -> bf16 bits.  The N fast estimates are independent (their exp / rcp latencies
+// overlap); one branch, rarely taken, refines the undecided ones.
+template <int N>
+__device__ __forceinline__ void silu_bf16_n(const float (&x)[N], uint16_t (&o)[N]) {
+  float y[N];
+  bool redo = false;
+#pragma unroll
+  for (int e = 0; e < N; ++e) {
+    y[e] = silu_fast(x[e]);
+    redo |= fast_undecided(y[e], x[e]);
+  }
+  if (__builtin_expect(redo, 0)) {
+#pragma unroll
+    for (int e = 0; e < N; ++e)
+      if (fast_undecided(y[e], x[e])) {
+        y[e] = silu_est(x[e]);
+        if (est_undecided(y[e], x[e])) y[e] = silu_exact(x[e]);
+      }
+  }
+#pragma unroll
+  for (int e = 0; e < N; ++e) o[e] = f2bf(y[e]);
+}
+__device__ __forceinline__ uint16_t silu_bf16(float x) {
+  const float a[1] = {x};
+  uint16_t o[1];
+  silu_bf16_n<1>(a, o);
+  return o[0];
+}
+__device__ __forceinline__ uint16_t sigmoid_bf16(float x) {
+  float y = sigmoid_fast(x);
+  if (__builtin_expect(fast_undecided(y, x), 0)) {
+    y = sigmoid_est(x);
+    if (est_undecided(y, x)) y = sigmoid_exact(x);
+  }
+  return f2bf(y);
+}
 // torch.rsqrt = 1 / sqrt(x) with correctly rounded sqrt and divide.
 __device__ __forceinline__ float rsqrt_f(float x) { return 1.0f / sqrtf(x); }
 // The hardware reciprocal square root (within about 1 ulp; x normal), for the gated norms' row

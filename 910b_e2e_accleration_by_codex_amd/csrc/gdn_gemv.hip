@@ -409,12 +409,14 @@ __global__ __launch_bounds__(256) void swiglu_part_kernel(const float* __restric
     u0 += *reinterpret_cast<const f32x4v*>(pp + m);
     u1 += *reinterpret_cast<const f32x4v*>(pp + m + 4);
   }
+  float g[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) g[e] = rbf(e < 4 ? g0[e] : g1[e - 4]);
+  uint16_t sg[8];
+  silu_bf16_n<8>(g, sg);
   u16x8v o;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float g = rbf(e < 4 ? g0[e] : g1[e - 4]), u = rbf(e < 4 ? u0[e] : u1[e - 4]);
-    o[e] = f2bf(rbf(silu_f(g)) * u);
-  }
+  for (int e = 0; e < 8; ++e) o[e] = f2bf(bf2f(sg[e]) * rbf(e < 4 ? u0[e] : u1[e - 4]));
   *reinterpret_cast<u16x8v*>(out + row * m + col) = o;
 }
 

@@ -1595,6 +1595,23 @@ __device__ __forceinline__ int find_seq(const int32_t* cu, int nseq, int64_t p) 
   return lo;
 }
 
+// Eight channels of one token: bf16(bias + sum_r x_r w_r) in fp32 (F.conv1d's order), SiLU, bf16.
+template <int K>
+__device__ __forceinline__ void conv_out8(const float (&f)[K][8], const float (&wf)[K][8], const float (&bv)[8],
+                                          uint16_t* __restrict__ dst) {
+  float cv[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float acc = bv[e];
+#pragma unroll
+    for (int r = 0; r < K; ++r) acc += f[r][e] * wf[r][e];
+    cv[e] = rbf(acc);
+  }
+  uint16_t o[8];
+  silu_bf16_n<8>(cv, o);
+  *reinterpret_cast<u16x8*>(dst) = u16x8{o[0], o[1], o[2], o[3], o[4], o[5], o[6], o[7]};
+}
+
 // The work of one conv workgroup: token run item / nblk, channel block item % nblk.
 template <int K>
 __device__ __forceinline__ void conv_run(int64_t item, int nblk, const uint16_t* __restrict__ x, int64_t x_stride,
@@ -1615,7 +1632,7 @@ __device__ __forceinline__ void conv_run(int64_t item, int nblk, const uint16_t*
     const int64_t tok = p0 - (K - 1) + i;
     xr[i] = (tok >= 0 && i < nrun + K - 1) ? *reinterpret_cast<const u16x8*>(x + tok * x_stride + c0) : zero;
   }
-  u16x8 wt[K];  // weight[c0 + e][r] -> wt[r][e]
+  float wf[K][8];  // weight[c0 + e][r] -> wf[r][e]
   {
     const u16x8* wp = reinterpret_cast<const u16x8*>(weight + (int64_t)c0 * K);  // 8 K contiguous values
     uint16_t w[8 * K];
@@ -1628,7 +1645,7 @@ __device__ __forceinline__ void conv_run(int64_t item, int nblk, const uint16_t*
 #pragma unroll
     for (int e = 0; e < 8; ++e)
 #pragma unroll
-      for (int r = 0; r < K; ++r) wt[r][e] = w[e * K + r];
+      for (int r = 0; r < K; ++r) wf[r][e] = bf2f(w[e * K + r]);
   }
   float bv[8];
 #pragma unroll
@@ -1665,15 +1682,12 @@ __device__ __forceinline__ void conv_run(int64_t item, int nblk, const uint16_t*
         }
       }
     }
-    u16x8 o;
+    float f[K][8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float acc = bv[e];
+    for (int r = 0; r < K; ++r)
 #pragma unroll
-      for (int r = 0; r < K; ++r) acc += bf2f(win[r][e]) * bf2f(wt[r][e]);
-      o[e] = f2bf(silu_fast(rbf(acc)));
-    }
-    *reinterpret_cast<u16x8*>(out + p * (int64_t)C + c0) = o;
+      for (int e = 0; e < 8; ++e) f[r][e] = bf2f(win[r][e]);
+    conv_out8<K>(f, wf, bv, out + p * (int64_t)C + c0);
   }
 }
 // Workgroup b covers item xcd_range_item(b).  The 8 XCDs take workgroups b % 8 in turn; the remap
@@ -1733,7 +1747,7 @@ __device__ __forceinline__ void gating_one(int64_t i, const uint16_t* __restrict
   if (i >= rows * Hv) return;
   const int64_t r = i / Hv;
   const int h = (int)(i % Hv);
-  beta[i] = f2bf(sigmoid_f(bf2f(b[r * ab_stride + h])));
+  beta[i] = sigmoid_bf16(bf2f(b[r * ab_stride + h]));
   g[i] = -expf(A_log[h]) * softplus_f(bf2f(a[r * ab_stride + h]) + dt_bias[h]);
 }
 __global__ void gating_kernel(const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, int64_t ab_stride,

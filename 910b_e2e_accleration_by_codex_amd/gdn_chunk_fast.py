@@ -24,12 +24,15 @@ CHUNK = 64
 
 
 def _tokens_view(x, name):
-    """[B, T, H, d] -> ([B*T, H, d] tensor with dense (H, d), token stride)."""
+    """[B, T, H, d] -> ([B*T, H, d] tensor with dense (H, d), token stride).  torch gives a size-1
+    dimension an arbitrary stride: a single token's stride is never used, a single head's is d."""
     B, T, H, D = x.shape
-    if x.stride(3) != 1 or x.stride(2) != D or (B > 1 and x.stride(0) != T * x.stride(1)):
-        x = x.contiguous()
-    flat = x.as_strided((B * T, H, D), (x.stride(1), D, 1))
-    return flat, x.stride(1)
+    ts = x.stride(1) if T > 1 else (x.stride(0) if B > 1 else H * D)
+    hs = x.stride(2) if H > 1 else D
+    if x.stride(3) != 1 or hs != D or (B > 1 and T > 1 and x.stride(0) != T * ts):
+        x, ts = x.clone(memory_format=torch.contiguous_format), H * D
+    flat = x.as_strided((B * T, H, D), (ts, D, 1))
+    return flat, ts
 
 
 def _to_device_int32(host, device):
@@ -228,12 +231,11 @@ def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size=64, initial_st
     z = z.reshape(B * T, -1)
     if z.dtype != torch.bfloat16 or z.shape[1] < Hv * D or z.device != dev:
         raise ValueError(f"chunk_gated_delta_rule: norm gate must be bf16 [{B * T}, >= {Hv * D}] on {dev}")
-    if z.stride(1) != 1 or z.stride(0) % 8 or z.data_ptr() % 16:
-        z = z.contiguous()
+    z, zs = _lib.dense_rows(z)
     if tuple(norm_weight.shape) != (D,) or norm_weight.dtype not in (torch.bfloat16, torch.float32):
         raise ValueError(f"chunk_gated_delta_rule: norm weight must be bf16 or fp32 [{D}]")
     w = norm_weight.contiguous()
-    _lib.call("gdn_chunk_prefill_rows_gated", *args, _lib.ptr(z), z.stride(0), _lib.ptr(w), _lib.dtype_code(w),
+    _lib.call("gdn_chunk_prefill_rows_gated", *args, _lib.ptr(z), zs, _lib.ptr(w), _lib.dtype_code(w),
               float(eps), _lib.ptr(work), wbytes, _lib.stream_of(query))
     return out, final
 
@@ -307,9 +309,10 @@ def causal_conv1d_prefill(x, weight, bias=None, history=None, cu_seqlens=None, s
     if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
         raise TypeError("causal_conv1d_prefill: x and weight must be bfloat16")
     xt = x.transpose(1, 2)                                   # [B, L, C]
-    if (xt.stride(2) != 1 or (B > 1 and xt.stride(0) != L * xt.stride(1)) or xt.stride(1) % 8
+    xs = xt.stride(1) if L > 1 else (xt.stride(0) if B > 1 else C)  # token row stride (a size-1 dim's
+    if (xt.stride(2) != 1 or (B > 1 and L > 1 and xt.stride(0) != L * xs) or xs % 8  # stride is arbitrary)
             or xt.data_ptr() % 16):
-        xt = xt.contiguous()                                 # the kernel reads 16-byte row pieces
+        xt, xs = xt.clone(memory_format=torch.contiguous_format), C  # the kernel reads 16-byte row pieces
     cu, nseq, seq_len = _seq_args(B, L, cu_seqlens, x.device)
     w = weight.reshape(C, K).contiguous()
     if bias is not None:
@@ -333,7 +336,7 @@ def causal_conv1d_prefill(x, weight, bias=None, history=None, cu_seqlens=None, s
             history = history.to(torch.bfloat16).contiguous()
         state = torch.empty(nseq, C, K, dtype=torch.bfloat16, device=x.device)
     out = torch.empty(B, L, C, dtype=torch.bfloat16, device=x.device)
-    _lib.call("gdn_conv_prefill_rows", _lib.ptr(xt), xt.stride(1), _lib.ptr(w), _lib.ptr(bias),
+    _lib.call("gdn_conv_prefill_rows", _lib.ptr(xt), xs, _lib.ptr(w), _lib.ptr(bias),
               _lib.ptr(history), _lib.ptr(out), _lib.ptr(state), _lib.ptr(rows), n_rows, B * L, _lib.ptr(cu),
               nseq, seq_len, C, K, _lib.stream_of(x))
     return out.transpose(1, 2), state
@@ -395,14 +398,11 @@ def gdn_prefill_core(mixed_qkv, z, a, b, conv_weight, A_log, dt_bias, norm_weigh
         cu, chunk0, nseq, seq_len, total_chunks = vl.cu, vl.seq_chunk0, vl.nseq, vl.max_len, vl.total_chunks
     else:
         cu, chunk0, nseq, seq_len, total_chunks = None, None, 1, T, (T + CHUNK - 1) // CHUNK
-    x = mixed_qkv
-    if x.stride(1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
-        x = x.contiguous()
+    x, xs = _lib.dense_rows(mixed_qkv)
     z2 = z if z.dim() == 2 else z.reshape(T, -1)
     if z2.dtype != torch.bfloat16 or z2.shape[0] != T or z2.shape[1] < Hv * D:
         raise ValueError(f"gdn_prefill_core: z must be bf16 [{T}, >= {Hv * D}]")
-    if z2.stride(1) != 1 or z2.stride(0) % 8 or z2.data_ptr() % 16:
-        z2 = z2.contiguous()
+    z2, zs = _lib.dense_rows(z2)
     if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
         raise TypeError(f"gdn_prefill_core: a and b must be bfloat16 (got {a.dtype}, {b.dtype})")
     if a.numel() != T * Hv or b.numel() != T * Hv:
@@ -414,7 +414,10 @@ def gdn_prefill_core(mixed_qkv, z, a, b, conv_weight, A_log, dt_bias, norm_weigh
         raise ValueError(f"gdn_prefill_core: conv_bias must hold C={C} values (got {conv_bias.numel()})")
     a2 = a if a.dim() == 2 else a.reshape(T, Hv)
     b2 = b if b.dim() == 2 else b.reshape(T, Hv)
-    if a2.stride() != b2.stride() or a2.stride(-1) != 1:
+    if T > 1 and (a2.stride() != b2.stride() or a2.stride(-1) != 1):
+        a2, b2 = a2.contiguous(), b2.contiguous()
+    ab_rs = a2.stride(0) if T > 1 else Hv  # (one row: its stride is never used)
+    if T == 1 and (a2.stride(-1) != 1 or b2.stride(-1) != 1):
         a2, b2 = a2.contiguous(), b2.contiguous()
     bias = conv_bias.to(torch.bfloat16).contiguous() if conv_bias is not None else None
     A32 = A_log if A_log.dtype == torch.float32 and A_log.is_contiguous() else A_log.to(torch.float32).contiguous()
@@ -457,8 +460,8 @@ def gdn_prefill_core(mixed_qkv, z, a, b, conv_weight, A_log, dt_bias, norm_weigh
     wbytes = int(_lib.lib().gdn_prefill_layer_workspace_bytes(T, total_chunks, nseq, Hk, Hv, D))
     work = torch.empty(max(wbytes, 1), dtype=torch.uint8, device=dev)
     p = _lib.ptr_int
-    _lib.call("gdn_prefill_layer_rows", x.data_ptr(), x.stride(0), z2.data_ptr(), z2.stride(0), a2.data_ptr(),
-              b2.data_ptr(), a2.stride(0), w.data_ptr(), p(bias), A32.data_ptr(), dt32.data_ptr(), nw.data_ptr(),
+    _lib.call("gdn_prefill_layer_rows", x.data_ptr(), xs, z2.data_ptr(), zs, a2.data_ptr(),
+              b2.data_ptr(), ab_rs, w.data_ptr(), p(bias), A32.data_ptr(), dt32.data_ptr(), nw.data_ptr(),
               _lib.dtype_code(nw), float(eps), p(hist), conv_state.data_ptr(), p(init), rec.data_ptr(),
               p(rows), n_rows, core.data_ptr(), T, p(cu), p(chunk0), total_chunks, nseq,
               seq_len, Hk, Hv, D, K, work.data_ptr(), wbytes, _lib.stream_of(mixed_qkv))

@@ -40,3 +40,20 @@ def rel_l2(a, b):
     a = a.double().cpu()
     b = b.double().cpu()
     return ((a - b).norm() / b.norm().clamp_min(1e-30)).item()
+
+
+def normal_bf16_values():
+    """Every normal bf16 value and +0 (65,025 values), in bit-pattern order.  (Left out: -0 and the
+    254 denormals, which torch's CPU conv turns into +0 -- it flushes denormals and adds to +0 -- and
+    whose SiLU is within 1e-38 of 0 either way.)"""
+    x = torch.arange(-32768, 32768, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    xf = x.float()
+    return x[torch.isfinite(xf) & ((xf.abs() >= 2.0 ** -126) | (x.view(torch.int16) == 0))]
+
+
+def assert_same_bits(got, want, inputs):
+    """got == want bit for bit; the message lists the first inputs where they differ."""
+    got, want = got.cpu().reshape(-1), want.cpu().reshape(-1)
+    bad = got.view(torch.int16) != want.view(torch.int16)
+    assert not bad.any(), (f"{int(bad.sum())} of {bad.numel()} differ; (input, got, want): "
+                           f"{list(zip(inputs.reshape(-1)[bad][:8].tolist(), got[bad][:8].tolist(), want[bad][:8].tolist()))}")

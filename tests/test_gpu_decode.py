@@ -6,7 +6,7 @@ state rel-L2 <= 1e-3, conv-state shifting and slot indexing bit-exact.
 import pytest
 import torch
 
-from conftest import rel_l2
+from conftest import assert_same_bits, normal_bf16_values, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -98,6 +98,20 @@ def test_elem_conv_update_bit_exact_state(gdn, oracle, dev):
         ulp = o_ref.float().abs().clamp_min(2 ** -126) * 2 ** -7
         assert (diff <= ulp).all(), "conv output off by more than one bf16 ulp"
         assert (diff == 0).float().mean().item() >= 0.999
+
+
+def test_elem_conv_update_silu_every_bf16_input(gdn, oracle, dev):
+    """The decode conv's SiLU is torch's, bit for bit, for every normal bf16 input (taps (0, 0, 0, 1)
+    and a zero state: the conv value is the input)."""
+    x = normal_bf16_values()
+    x = torch.cat([x, torch.zeros(-x.numel() % 8, dtype=x.dtype)])  # whole 8-channel groups
+    C, K = x.numel(), 4
+    w = torch.zeros(C, K, dtype=torch.bfloat16)
+    w[:, K - 1] = 1
+    st = torch.zeros(1, C, K, dtype=torch.bfloat16)
+    o_ref = oracle.elem_conv_update(x.reshape(1, C, 1), st.clone(), w, None)
+    o = gdn.elem_conv_update(x.reshape(1, C, 1).to(dev), st.to(dev), w.to(dev), None)
+    assert_same_bits(o, o_ref, x)
 
 
 def test_elem_conv_update_integer_kat(gdn, dev):

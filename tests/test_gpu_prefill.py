@@ -6,7 +6,7 @@ capture bit-exact; the 64x64 inverse to fp32 rounding.
 import pytest
 import torch
 
-from conftest import rel_l2
+from conftest import assert_same_bits, normal_bf16_values, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -423,6 +423,34 @@ def test_prefill_core_long_memory_heads(gdn, oracle, dev):
     for h in range(Hv):
         assert rel_l2(co[:, h], co_ref[:, h]) <= OUT_TOL, (h, rel_l2(co[:, h], co_ref[:, h]))
         assert rel_l2(rec[:, h], rec_ref[:, h]) <= STATE_TOL, (h, rel_l2(rec[:, h], rec_ref[:, h]))
+
+
+def test_conv_silu_every_bf16_input(gdn, oracle, dev):
+    """The conv's SiLU rounds to bf16 as torch does (fp32 x / (1 + e^-x), one rounding), bit for bit,
+    for every normal bf16 input: one token through the taps (0, 0, 0, 1), so the conv's bf16 output
+    before the SiLU is the input itself.  A one-ulp slip on a few inputs (x = -2^-8 and 2^-7 among
+    them) moves a fast-decaying head's final state by up to 7e-3 when it hits a sequence's last token.
+    The fused layer's prologue runs the same conv code."""
+    x = normal_bf16_values()
+    x = torch.cat([x, torch.zeros(-x.numel() % 8, dtype=x.dtype)])  # whole 8-channel groups
+    C, K = x.numel(), 4
+    w = torch.zeros(C, K, dtype=torch.bfloat16)
+    w[:, K - 1] = 1
+    out, _ = gdn.causal_conv1d_prefill(x.reshape(1, C, 1).to(dev), w.to(dev))
+    ref, _ = oracle.causal_conv1d_prefill(x.reshape(1, C, 1), w)
+    assert_same_bits(out, ref, x)
+
+
+def test_gating_every_bf16_input(gdn, oracle, dev):
+    """beta = sigmoid(b) rounds to bf16 as torch does, bit for bit, for every normal bf16 b (b = -2^-8
+    and 2^-7 lie within an fp32 ulp of a bf16 rounding midpoint)."""
+    b = normal_bf16_values()
+    b = b[:b.numel() - b.numel() % 15].reshape(-1, 15)
+    a = torch.zeros_like(b)
+    zeros = torch.zeros(15)
+    beta_ref, _ = oracle.gdn_gating(a, b, zeros, zeros)
+    beta, _ = gdn.gdn_gating(a.to(dev), b.to(dev), zeros.to(dev), zeros.to(dev))
+    assert_same_bits(beta, beta_ref, b)
 
 
 def test_gating(gdn, oracle, dev):
