@@ -57,12 +57,12 @@ __device__ __forceinline__ float softplus_f(float x) { return x > 20.0f ? x : lo
 // evaluation in double rounds to the same fp32 value.  A one-ulp slip of the fp32 value flips the
 // bf16 result for a handful of inputs (x = -2^-8 and 2^-7 among them), and a flipped conv output or
 // beta of a sequence's last token moves a fast-decaying head's final state by up to 7e-3.
-__device__ __noinline__ static float silu_exact(float x) {
+__device__ __forceinline__ float silu_exact(float x) {
   if (x < -88.72283935546875f) return x / __builtin_huge_valf();
   const double xd = x;
   return (float)(xd / (1.0 + exp(-xd)));
 }
-__device__ __noinline__ static float sigmoid_exact(float x) {
+__device__ __forceinline__ float sigmoid_exact(float x) {
   if (x < -88.72283935546875f) return 0.f;  // 1 / (1 + inf)
   return (float)(1.0 / (1.0 + exp(-(double)x)));
 }

@@ -1576,15 +1576,19 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
 // ============================================================================================
 // Causal depthwise conv prefill + SiLU with decode-state capture.
 // ============================================================================================
-// One thread per (run of kConvRun consecutive packed tokens, 8 channels): it loads the input rows
-// p0-K+1 .. p0+kConvRun-1 once with 16-byte reads and slides the K-tap window over them (rows before a
-// token's sequence come from the sequence's history row [C, K], x_{-j} = history[K - j], or are
-// zero), then writes 8 outputs per token with one 16-byte store.  A workgroup covers one token run
-// and 2048 channels, so the sequence walk is uniform across it.  Numerics of F.conv1d on bf16: fp32
-// accumulation of the K products (+ bias), one bf16 rounding, SiLU, bf16.  The decode conv state a
-// sequence leaves (its last K inputs) is written afterwards by conv_state_capture_kernel, so the
-// history may be the same slot rows the state goes to.
+// One thread per (run of kConvRun consecutive packed tokens, kConvCh channels): it loads the input
+// rows p0-K+1 .. p0+kConvRun-1 once with 8-byte reads and slides the K-tap window over them (rows
+// before a token's sequence come from the sequence's history row [C, K], x_{-j} = history[K - j], or
+// are zero), then writes kConvCh outputs per token with one 8-byte store.  A workgroup covers one
+// token run and 1024 channels, so the sequence walk is uniform across it.  Numerics of F.conv1d on
+// bf16: fp32 accumulation of the K products (+ bias), one bf16 rounding, SiLU, bf16.  The conv is
+// VALU-bound at the device copy rate, so each input row is unpacked to fp32 once and slides through
+// the window (4 channels a thread keep the window in registers at 4 waves per SIMD).  The decode conv
+// state a sequence leaves (its last K inputs) is written afterwards by conv_state_capture_kernel, so
+// the history may be the same slot rows the state goes to.
 constexpr int kConvRun = 8;
+constexpr int kConvCh = 4;
+typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ int find_seq(const int32_t* cu, int nseq, int64_t p) {
   int lo = 0, hi = nseq - 1;  // last sequence whose start <= p (skips empty ones)
   while (lo < hi) {
@@ -1595,21 +1599,21 @@ __device__ __forceinline__ int find_seq(const int32_t* cu, int nseq, int64_t p) 
   return lo;
 }
 
-// Eight channels of one token: bf16(bias + sum_r x_r w_r) in fp32 (F.conv1d's order), SiLU, bf16.
+// kConvCh channels of one token: bf16(bias + sum_r x_r w_r) in fp32 (F.conv1d's order), SiLU, bf16.
 template <int K>
-__device__ __forceinline__ void conv_out8(const float (&f)[K][8], const float (&wf)[K][8], const float (&bv)[8],
-                                          uint16_t* __restrict__ dst) {
-  float cv[8];
+__device__ __forceinline__ void conv_out(const float (&f)[K][kConvCh], const float (&wf)[K][kConvCh],
+                                         const float (&bv)[kConvCh], uint16_t* __restrict__ dst) {
+  float cv[kConvCh];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
+  for (int e = 0; e < kConvCh; ++e) {
     float acc = bv[e];
 #pragma unroll
     for (int r = 0; r < K; ++r) acc += f[r][e] * wf[r][e];
     cv[e] = rbf(acc);
   }
-  uint16_t o[8];
-  silu_bf16_n<8>(cv, o);
-  *reinterpret_cast<u16x8*>(dst) = u16x8{o[0], o[1], o[2], o[3], o[4], o[5], o[6], o[7]};
+  uint16_t o[kConvCh];
+  silu_bf16_n<kConvCh>(cv, o);
+  *reinterpret_cast<u16x4*>(dst) = u16x4{o[0], o[1], o[2], o[3]};
 }
 
 // The work of one conv workgroup: token run item / nblk, channel block item % nblk.
@@ -1619,41 +1623,61 @@ __device__ __forceinline__ void conv_run(int64_t item, int nblk, const uint16_t*
                                          const uint16_t* __restrict__ history, const int32_t* __restrict__ rows,
                                          int n_rows, uint16_t* __restrict__ out, int64_t total_tokens,
                                          const int32_t* __restrict__ cu, int nseq, int seq_len, int C) {
-  const int cg = (int)(item % nblk) * blockDim.x + threadIdx.x;  // 8-channel group
+  const int cg = (int)(item % nblk) * blockDim.x + threadIdx.x;  // channel group
   const int64_t p0 = item / nblk * kConvRun;
-  if (8 * cg >= C) return;
-  const int c0 = 8 * cg;
+  if (kConvCh * cg >= C) return;
+  const int c0 = kConvCh * cg;
   const int nrun = total_tokens - p0 < kConvRun ? (int)(total_tokens - p0) : kConvRun;
   // rows p0-K+1 .. p0+nrun-1 (only those inside [0, total_tokens) are read)
-  u16x8 xr[kConvRun + K - 1];
-  const u16x8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+  u16x4 xr[kConvRun + K - 1];
+  const u16x4 zero = {0, 0, 0, 0};
 #pragma unroll
   for (int i = 0; i < kConvRun + K - 1; ++i) {
     const int64_t tok = p0 - (K - 1) + i;
-    xr[i] = (tok >= 0 && i < nrun + K - 1) ? *reinterpret_cast<const u16x8*>(x + tok * x_stride + c0) : zero;
+    xr[i] = (tok >= 0 && i < nrun + K - 1) ? *reinterpret_cast<const u16x4*>(x + tok * x_stride + c0) : zero;
   }
-  float wf[K][8];  // weight[c0 + e][r] -> wf[r][e]
+  float wf[K][kConvCh];  // weight[c0 + e][r] -> wf[r][e]
   {
-    const u16x8* wp = reinterpret_cast<const u16x8*>(weight + (int64_t)c0 * K);  // 8 K contiguous values
-    uint16_t w[8 * K];
+    const u16x4* wp = reinterpret_cast<const u16x4*>(weight + (int64_t)c0 * K);  // kConvCh K contiguous values
+    uint16_t w[kConvCh * K];
 #pragma unroll
     for (int i = 0; i < K; ++i) {
-      const u16x8 v = wp[i];
+      const u16x4 v = wp[i];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) w[8 * i + e] = v[e];
+      for (int e = 0; e < kConvCh; ++e) w[kConvCh * i + e] = v[e];
     }
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
+    for (int e = 0; e < kConvCh; ++e)
 #pragma unroll
       for (int r = 0; r < K; ++r) wf[r][e] = bf2f(w[e * K + r]);
   }
-  float bv[8];
+  float bv[kConvCh];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) bv[e] = bias ? bf2f(bias[c0 + e]) : 0.f;
+  for (int e = 0; e < kConvCh; ++e) bv[e] = bias ? bf2f(bias[c0 + e]) : 0.f;
   // sequence of p0, then walk forward (uniform across the workgroup)
   int s = cu ? find_seq(cu, nseq, p0) : (int)(p0 / seq_len);
   int64_t s_lo = cu ? (int64_t)cu[s] : (int64_t)s * seq_len;
   int64_t s_hi = cu ? (int64_t)cu[s + 1] : s_lo + seq_len;
+  if (nrun == kConvRun && p0 - (K - 1) >= s_lo && p0 + kConvRun <= s_hi) {
+    // All tokens of the run in one sequence, at least K - 1 past its start (every run of a sequence
+    // but its first one or two): every window row is an input row.
+    float f[K][kConvCh];
+#pragma unroll
+    for (int r = 1; r < K; ++r)
+#pragma unroll
+      for (int e = 0; e < kConvCh; ++e) f[r][e] = bf2f(xr[r - 1][e]);
+#pragma unroll
+    for (int i = 0; i < kConvRun; ++i) {
+#pragma unroll
+      for (int r = 0; r + 1 < K; ++r)
+#pragma unroll
+        for (int e = 0; e < kConvCh; ++e) f[r][e] = f[r + 1][e];
+#pragma unroll
+      for (int e = 0; e < kConvCh; ++e) f[K - 1][e] = bf2f(xr[i + K - 1][e]);
+      conv_out<K>(f, wf, bv, out + (p0 + i) * (int64_t)C + c0);
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < kConvRun; ++i) {
     if (i >= nrun) break;  // (uniform: the last run of the batch)
@@ -1663,7 +1687,7 @@ __device__ __forceinline__ void conv_run(int64_t item, int nblk, const uint16_t*
       s_lo = cu ? (int64_t)cu[s] : (int64_t)s * seq_len;
       s_hi = cu ? (int64_t)cu[s + 1] : s_lo + seq_len;
     }
-    u16x8 win[K];
+    u16x4 win[K];
     if (p - (K - 1) >= s_lo) {
 #pragma unroll
       for (int r = 0; r < K; ++r) win[r] = xr[i + r];
@@ -1677,17 +1701,17 @@ __device__ __forceinline__ void conv_run(int64_t item, int nblk, const uint16_t*
         } else {
           const int back = (int)(s_lo - tok);  // 1..K-1
 #pragma unroll
-          for (int e = 0; e < 8; ++e)
+          for (int e = 0; e < kConvCh; ++e)
             win[r][e] = hrow >= 0 ? history[((int64_t)hrow * C + c0 + e) * K + (K - back)] : (uint16_t)0;
         }
       }
     }
-    float f[K][8];
+    float f[K][kConvCh];
 #pragma unroll
     for (int r = 0; r < K; ++r)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) f[r][e] = bf2f(win[r][e]);
-    conv_out8<K>(f, wf, bv, out + p * (int64_t)C + c0);
+      for (int e = 0; e < kConvCh; ++e) f[r][e] = bf2f(win[r][e]);
+    conv_out<K>(f, wf, bv, out + p * (int64_t)C + c0);
   }
 }
 // Workgroup b covers item xcd_range_item(b).  The 8 XCDs take workgroups b % 8 in turn; the remap
@@ -2197,7 +2221,7 @@ extern "C" int gdn_conv_prefill_rows(const void* x, int64_t x_stride, const void
                 "gdn_conv_prefill: C and the row stride must be multiples of 8 with 16-byte aligned rows");
     GDN_REQUIRE(total_tokens < (1ll << 31), "gdn_conv_prefill: too many tokens");
     GDN_REQUIRE(aligned(weight, 16), "gdn_conv_prefill: weight must be 16-byte aligned");
-    const int nblk = (C / 8 + 255) / 256;
+    const int nblk = (C / kConvCh + 255) / 256;
     const int64_t nwg = (int64_t)nblk * ((total_tokens + kConvRun - 1) / kConvRun);
     GDN_REQUIRE(nwg < (1ll << 31), "gdn_conv_prefill: grid too large");
     const unsigned grid = (unsigned)nwg;
@@ -2345,7 +2369,7 @@ extern "C" int gdn_prefill_layer_rows(const void* mixed, int64_t mixed_stride, c
   P.nseq = nseq;
   P.seq_len = seq_len;
   P.C = C;
-  P.nblk = (C / 8 + 255) / 256;
+  P.nblk = (C / kConvCh + 255) / 256;
   P.n_conv = (int64_t)P.nblk * ((total_tokens + kConvRun - 1) / kConvRun);
   P.state = (uint16_t*)conv_state;
   P.n_cap = cap_fused ? ((int64_t)nseq * C + 255) / 256 : 0;
