@@ -226,6 +226,25 @@ __device__ __forceinline__ bf16x8 pack_acc_bf16(f32x4 a, f32x4 b) {
   const u32x4 u = {w0, w1, w2, w3};
   return __builtin_bit_cast(bf16x8, u);
 }
+// x = hi + lo with hi = bf16(x), lo = bf16(x - hi): 8 accumulator values (two tiles) as two k-slot
+// ordered bf16 fragments; hi + lo carries about 16 significant bits.
+__device__ __forceinline__ bf16x8 lo_bf16(f32x4 a, f32x4 b, bf16x8 hi) {
+  const u32x4v h = __builtin_bit_cast(u32x4v, hi);
+  f32x4 ra, rb;
+  ra[0] = a[0] - __uint_as_float(h[0] << 16);
+  ra[1] = a[1] - __uint_as_float(h[0] & 0xffff0000u);
+  ra[2] = a[2] - __uint_as_float(h[1] << 16);
+  ra[3] = a[3] - __uint_as_float(h[1] & 0xffff0000u);
+  rb[0] = b[0] - __uint_as_float(h[2] << 16);
+  rb[1] = b[1] - __uint_as_float(h[2] & 0xffff0000u);
+  rb[2] = b[2] - __uint_as_float(h[3] << 16);
+  rb[3] = b[3] - __uint_as_float(h[3] & 0xffff0000u);
+  return pack_acc_bf16(ra, rb);
+}
+__device__ __forceinline__ void split_bf16(f32x4 a, f32x4 b, bf16x8& hi, bf16x8& lo) {
+  hi = pack_acc_bf16(a, b);
+  lo = lo_bf16(a, b, hi);
+}
 __device__ __forceinline__ bf16x8 lds_frag(const uint8_t* base, int f, int lane) {
   return *reinterpret_cast<const bf16x8*>(base + f * ws::FRAG + lane * 16);
 }
@@ -245,12 +264,22 @@ constexpr float kNegligibleLog = -44.3614f;  // ln(2^-64): a segment map A_j thi
 // part is lost in the rounding the chain makes anyway (unless the state shrank by more than 2^7 over
 // the warm-up: new tokens contributing under 1/128 of the state they replace).
 constexpr float kWarmLog = -11.0904f;        // ln(2^-16)
-// A chunk whose decay over its tokens is slight (e^{G_last} above e^-2) passes most of the state it
-// receives on: the bf16 rounding of the W S operands then accumulates over many chunks (to 1e-3 of
-// the state over 8192 tokens of decay ~0.002 a token).  Such a chunk forms -W and the state as
-// bf16 hi + lo pairs and takes W S = Wh Sh + Wh Sl + Wl Sh (about 16 significant bits); a chunk with
-// faster decay forgets that rounding within a few chunks and keeps the single bf16 product.
-constexpr float kPreciseGl = 0.135335283f;   // e^-2
+// A chunk whose decay over its tokens is slight (e^{G_last} above e^-4) passes much of the state it
+// receives on: the bf16 rounding of the W S operands then accumulates over the chunks (to 1e-3 of
+// the state over 8192 tokens of decay ~0.002 a token), or, from a large initial state that decays
+// to a small one, weighs against the small one (1.3e-3 for one chunk at e^{G_last} = 0.13 from a
+// state 8x the final one).  Such a chunk forms -W and the state as bf16 hi + lo pairs and takes
+// W S = Wh Sh + Wh Sl + Wl Sh (about 16 significant bits); a chunk with faster decay forgets that
+// rounding within a chunk or two and keeps the single bf16 product.
+constexpr float kPreciseGl = 0.0183156389f;  // e^-4
+// T diag(beta) (the inverse kernel's record) also enters U and W as hi + lo in such a chunk and in a
+// sequence's last chunk.  With a head's keys sharing a large common part (a conv bias, say) the bf16
+// rounding of the record alone moved states by 1e-3 to 2e-3 relative: in a long-memory head it builds
+// up over the chunks, and in a fast-decaying head the last chunk's U makes most of the final state
+// (5e-6 with the lo part; chunks of faster decay are forgotten before they matter).  The inverse
+// kernel writes the lo part of every chunk whose G_last is above -4.5 -- a margin on the output
+// pass's test, which scans the same g values the same way -- and of every sequence's last chunk.
+constexpr float kLoRecordLog = -4.5f;
 constexpr int kTrans = 2 * pf::D * pf::D;    // floats per (slot, head): A, then B
 }  // namespace sg
 
@@ -384,10 +413,13 @@ typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
 namespace tf {
 constexpr int FRAGS = 6;                      // lower fragments of T diag(beta)
 __device__ __forceinline__ int fid(int w, int s) { return w < 2 ? w : 2 * w - 2 + s; }
-// In memory a record is 5 KiB: fragments 0 = (0, 0) and 3 = (2, 1) straddle the diagonal, their
-// second 16-column block is zero, and they keep only the first 8 bytes of each lane (512 B); the
-// other four keep 16 bytes a lane.  Byte offsets 0, 512, 1536, 2560, 3072, 4096.
-constexpr int BYTES = 5 * ws::FRAG;
+// In memory the bf16 hi part is 5 KiB: fragments 0 = (0, 0) and 3 = (2, 1) straddle the diagonal,
+// their second 16-column block is zero, and they keep only the first 8 bytes of each lane (512 B);
+// the other four keep 16 bytes a lane.  Byte offsets 0, 512, 1536, 2560, 3072, 4096.  The lo part
+// (T diag(beta) - hi, rounded to bf16) follows in the same layout, written only for a chunk of slight
+// decay and a sequence's last chunk (sg::kLoRecordLog).
+constexpr int HALF = 5 * ws::FRAG;
+constexpr int BYTES = 2 * HALF;
 __host__ __device__ __forceinline__ constexpr bool half(int f) { return f == 0 || f == 3; }
 __host__ __device__ __forceinline__ constexpr int offset(int f) {
   return f * ws::FRAG - (f >= 1 ? ws::FRAG / 2 : 0) - (f >= 4 ? ws::FRAG / 2 : 0);
@@ -554,6 +586,7 @@ __global__ __launch_bounds__(pf::NT, 2) void inv_kernel(const uint16_t* __restri
     }
   f32x4 TT[10];
   reg_inv64(XT, Xd, TT, strp[w], lane);
+  const bool lo_rec = sdec[w][0][CH - 1] > sg::kLoRecordLog || cp.c + 1 == tab.nch(cp.seq);  // (wave-uniform)
   // fragments (w', s), s <= w' / 2: element e of lane (i, g) = T[16 w' + i][j] beta_j with
   // j = 32 s + kpos(8 g + e), kpos(8 g + e) = 16 (e >> 2) + 4 g + (e & 3): blocks 2s (e < 4) and 2s + 1
   uint8_t* dst = tfrag + ((int64_t)slot * Hv + h) * tf::BYTES;
@@ -566,11 +599,20 @@ __global__ __launch_bounds__(pf::NT, 2) void inv_kernel(const uint16_t* __restri
       const f32x4 t0 = TT[tri(wt, 2 * s)], t1 = 2 * s + 1 <= wt ? TT[tri(wt, 2 * s + 1 <= wt ? 2 * s + 1 : 0)] : z;
       const int f = tf::fid(wt, s);
       typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-      const u32x4 pk = __builtin_bit_cast(u32x4, pack_acc_bf16(t0 * Br[2 * s], t1 * Br[2 * s + 1]));
+      const f32x4 a0 = t0 * Br[2 * s], a1 = t1 * Br[2 * s + 1];
+      const bf16x8 hb = pack_acc_bf16(a0, a1);
+      const u32x4 pk = __builtin_bit_cast(u32x4, hb);
       if (tf::half(f))  // the second block (e >= 4) is zero: 8 bytes a lane
         *reinterpret_cast<u32x2v*>(dst + tf::offset(f) + lane * 8) = u32x2v{pk[0], pk[1]};
       else
         *reinterpret_cast<u32x4*>(dst + tf::offset(f) + lane * 16) = pk;
+      if (lo_rec) {
+        const u32x4 pl = __builtin_bit_cast(u32x4, lo_bf16(a0, a1, hb));
+        if (tf::half(f))
+          *reinterpret_cast<u32x2v*>(dst + tf::HALF + tf::offset(f) + lane * 8) = u32x2v{pl[0], pl[1]};
+        else
+          *reinterpret_cast<u32x4*>(dst + tf::HALF + tf::offset(f) + lane * 16) = pl;
+      }
     }
   // the last chunk of a segment with a successor: that transition slot's warm-up length
   const int nch = tab.nch(cp.seq);
@@ -647,6 +689,7 @@ struct alignas(16) SegOps {
   uint8_t wn[16 * ws::FRAG];          // -W fragments [tb 4][j 4] (the bf16 hi part in a precise chunk)
   uint8_t wl[16 * ws::FRAG];          // the lo part of -W in a precise chunk
   uint8_t qk[tf::FRAGS * ws::FRAG];   // QK fragments of the lower blocks, index tf::fid(tb, j)
+  uint8_t tl[tf::FRAGS * ws::FRAG];   // the lo part of T diag(beta) in a precise chunk, index tf::fid(tb, k)
 };
 struct SegSmem {
   SegBuf buf[2];
@@ -677,7 +720,7 @@ constexpr int kALd = pf::D + 4;  // row pitch (floats) of A_j's row-major LDS co
 // base plus a 32-bit lane offset.
 struct LocIn {
   u16x8 kr[4], vr[4], qr[4];
-  bf16x8 tb[2];
+  bf16x8 tb[2], tl[2];  // T diag(beta) fragments: bf16 hi, and lo (written for chunks of slight decay only)
   f32x4 kn;  // the inverse kernel's l2norm factors of K rows 4 tq .. 4 tq + 3
   float graw;
 };
@@ -720,8 +763,10 @@ __device__ __forceinline__ void loc_load(LocIn& L, int64_t t0, int len, int kh, 
       const int f = tf::fid(w, s);
       const bool hf = tf::half(f);
       u32x4 x = *reinterpret_cast<const u32x4*>(tfr + (uint32_t)(tf::offset(f) + lane * (hf ? 8 : 16)));
-      if (hf) x[2] = x[3] = 0u;
+      u32x4 y = *reinterpret_cast<const u32x4*>(tfr + (uint32_t)(tf::HALF + tf::offset(f) + lane * (hf ? 8 : 16)));
+      if (hf) x[2] = x[3] = y[2] = y[3] = 0u;
       L.tb[s] = __builtin_bit_cast(bf16x8, x);
+      L.tl[s] = __builtin_bit_cast(bf16x8, y);
     }
   }
   if (kNeedQ && (kPart < 0 || kPart == 2)) {  // a warm-up chunk (no outputs) reads one row for all lanes:
@@ -739,25 +784,6 @@ __device__ __forceinline__ void loc_load(LocIn& L, int64_t t0, int len, int kh, 
     L.graw = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(knc) + (pf::CH + lane) * 4u);
 }
 
-// x = hi + lo with hi = bf16(x), lo = bf16(x - hi): 8 accumulator values (two tiles) as two k-slot
-// ordered bf16 fragments; hi + lo carries about 16 significant bits.
-__device__ __forceinline__ bf16x8 lo_bf16(f32x4 a, f32x4 b, bf16x8 hi) {
-  const u32x4v h = __builtin_bit_cast(u32x4v, hi);
-  f32x4 ra, rb;
-  ra[0] = a[0] - __uint_as_float(h[0] << 16);
-  ra[1] = a[1] - __uint_as_float(h[0] & 0xffff0000u);
-  ra[2] = a[2] - __uint_as_float(h[1] << 16);
-  ra[3] = a[3] - __uint_as_float(h[1] & 0xffff0000u);
-  rb[0] = b[0] - __uint_as_float(h[2] << 16);
-  rb[1] = b[1] - __uint_as_float(h[2] & 0xffff0000u);
-  rb[2] = b[2] - __uint_as_float(h[3] << 16);
-  rb[3] = b[3] - __uint_as_float(h[3] & 0xffff0000u);
-  return pack_acc_bf16(ra, rb);
-}
-__device__ __forceinline__ void split_bf16(f32x4 a, f32x4 b, bf16x8& hi, bf16x8& lo) {
-  hi = pack_acc_bf16(a, b);
-  lo = lo_bf16(a, b, hi);
-}
 // Whether a chunk's W S runs in hi + lo (its e^{G_last} above e^-2), read as a wave-uniform value so
 // that the two forms are a scalar branch.  The local and chain waves read the same LDS word.
 __device__ __forceinline__ bool chunk_precise(const SegBuf& B) {
@@ -837,12 +863,12 @@ __device__ __forceinline__ void loc_phase1(SegBuf& B, const LocIn& in, int len, 
 // 32 s + 16 (e >> 2) + 4 g + (e & 3)).
 template <int W, bool kNeedQ>
 __device__ __forceinline__ void loc_phase2(const SegBuf& B, SegOps& P, const bf16x8 (&qf)[4], const bf16x8 (&tbu)[2],
-                                           bool q_on) {
+                                           const bf16x8 (&tlu)[2], bool q_on, bool last) {
   using namespace pf;
   int t;
   asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"((int)threadIdx.x));
   const int lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
-  const bool precise = chunk_precise(B);
+  const bool precise = chunk_precise(B), tlo = precise || last;
   bf16x8 tbe[2], tbl[2];  // T diag(beta e^G), and in a precise chunk the lo part of its fp32 value
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
@@ -851,14 +877,28 @@ __device__ __forceinline__ void loc_phase2(const SegBuf& B, SegOps& P, const bf1
     const f32x4 e1 = *reinterpret_cast<const f32x4*>(&B.eg[32 * s + 16 + 4 * g4]);
     const u32x4v u = __builtin_bit_cast(u32x4v, tbu[s]);
     f32x4 a, b;
-    a[0] = __uint_as_float(u[0] << 16) * e0[0];
-    a[1] = __uint_as_float(u[0] & 0xffff0000u) * e0[1];
-    a[2] = __uint_as_float(u[1] << 16) * e0[2];
-    a[3] = __uint_as_float(u[1] & 0xffff0000u) * e0[3];
-    b[0] = __uint_as_float(u[2] << 16) * e1[0];
-    b[1] = __uint_as_float(u[2] & 0xffff0000u) * e1[1];
-    b[2] = __uint_as_float(u[3] << 16) * e1[2];
-    b[3] = __uint_as_float(u[3] & 0xffff0000u) * e1[3];
+    a[0] = __uint_as_float(u[0] << 16);
+    a[1] = __uint_as_float(u[0] & 0xffff0000u);
+    a[2] = __uint_as_float(u[1] << 16);
+    a[3] = __uint_as_float(u[1] & 0xffff0000u);
+    b[0] = __uint_as_float(u[2] << 16);
+    b[1] = __uint_as_float(u[2] & 0xffff0000u);
+    b[2] = __uint_as_float(u[3] << 16);
+    b[3] = __uint_as_float(u[3] & 0xffff0000u);
+    if (tlo) {  // T diag(beta) = hi + lo; its lo fragments go to the chain for U as well
+      const u32x4v l = __builtin_bit_cast(u32x4v, tlu[s]);
+      a[0] += __uint_as_float(l[0] << 16);
+      a[1] += __uint_as_float(l[0] & 0xffff0000u);
+      a[2] += __uint_as_float(l[1] << 16);
+      a[3] += __uint_as_float(l[1] & 0xffff0000u);
+      b[0] += __uint_as_float(l[2] << 16);
+      b[1] += __uint_as_float(l[2] & 0xffff0000u);
+      b[2] += __uint_as_float(l[3] << 16);
+      b[3] += __uint_as_float(l[3] & 0xffff0000u);
+      *reinterpret_cast<bf16x8*>(P.tl + tf::fid(W, s) * ws::FRAG + lane * 16) = tlu[s];
+    }
+    a *= e0;
+    b *= e1;
     tbe[s] = pack_acc_bf16(a, b);
     if (precise) tbl[s] = lo_bf16(a, b, tbe[s]);
   }
@@ -1024,7 +1064,7 @@ __device__ __forceinline__ void norm_store(const NormIn& N, const float (&wt)[8]
 // from the hi + lo parts of -W and of the state; block j's state parts are formed in its step and
 // its -W lo fragments requested there (behind the hi products), which keeps the registers of the
 // fast form.
-template <bool kUseU, bool kOut, bool kSplitLate, bool kPrecise>
+template <bool kUseU, bool kOut, bool kSplitLate, bool kPrecise, bool kTlo>
 __device__ __forceinline__ void chain_part1(const SegBuf& B, const SegOps& P, ChainRegs& R, int wc, int lane_in) {
   using namespace pf;
   int lane;
@@ -1064,7 +1104,7 @@ __device__ __forceinline__ void chain_part1(const SegBuf& B, const SegOps& P, Ch
   for (int sl = 0; sl < 2; ++sl)
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb) acc[sl][tb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (kUseU) {  // U = T diag(beta) V, token tile tb, k-blocks kb <= tb / 2
+  if (kUseU) {  // U = T diag(beta) V, token tile tb, k-blocks kb <= tb / 2 (kTlo: T's hi and lo parts)
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -1073,6 +1113,17 @@ __device__ __forceinline__ void chain_part1(const SegBuf& B, const SegOps& P, Ch
           acc[0][tb] = mma(ft[tf::fid(tb, kb)], vf[kb][0], acc[0][tb]);
           acc[1][tb] = mma(ft[tf::fid(tb, kb)], vf[kb][1], acc[1][tb]);
         }
+    if (kTlo) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb)
+          if (2 * kb <= tb) {
+            const bf16x8 fl = lds_frag(P.tl, tf::fid(tb, kb), lane);
+            acc[0][tb] = mma(fl, vf[kb][0], acc[0][tb]);
+            acc[1][tb] = mma(fl, vf[kb][1], acc[1][tb]);
+          }
+    }
   }
   // o^T tile by tile: lane (c, g) of O[tb][sl] holds o[16 tb + c][16 n + 4 g .. 4 g + 3]
   f32x4 O[4][2];
@@ -1284,6 +1335,7 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
   const int w0 = (kPass == 0 && warm_path) ? warm[(int64_t)slot * Hv + h] : 0;
   const int cb0 = c_begin - w0, ntot = n + w0;
   const int chunk_slot0 = tab.first_chunk(s) + cb0;
+  const int last_c = cb0 + ntot == nch_s ? ntot - 1 : -1;  // the sequence's last chunk, if in this walk
   auto tfr = [&](int c) { return tfrag + ((int64_t)(chunk_slot0 + c) * Hv + h) * tf::BYTES; };
   auto chunk_t0 = [&](int c) { return t_seq + (int64_t)(cb0 + c) * CH; };
   auto chunk_len = [&](int c) { return Ls - (cb0 + c) * CH < CH ? Ls - (cb0 + c) * CH : CH; };
@@ -1294,18 +1346,18 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     // unrolled by two so that each set keeps its registers; every load in it is unconditional (past
     // the end the last chunk is requested again, unused), which keeps the wait counts exact.
     LocIn ia, ib;
-    bf16x8 qf[4], tbu[2];
+    bf16x8 qf[4], tbu[2], tlu[2];
     auto load = [&](LocIn& L, int c, auto part) __attribute__((always_inline)) {
       loc_load<need_q, decltype(part)::value>(L, chunk_t0(c), chunk_len(c), kh, h, k, (uint32_t)ks, q, (uint32_t)qs, v,
                                               (uint32_t)vs, tfr(c),
                                               knorm + ((int64_t)(chunk_slot0 + c) * Hv + h) * (2 * CH), c >= w0);
     };
-    auto phase2 = [&](const SegBuf& B, bool q_on) __attribute__((always_inline)) {
+    auto phase2 = [&](const SegBuf& B, bool q_on, bool last) __attribute__((always_inline)) {
       switch (w) {
-        case 0: loc_phase2<0, need_q>(B, sm.ops, qf, tbu, q_on); break;
-        case 1: loc_phase2<1, need_q>(B, sm.ops, qf, tbu, q_on); break;
-        case 2: loc_phase2<2, need_q>(B, sm.ops, qf, tbu, q_on); break;
-        default: loc_phase2<3, need_q>(B, sm.ops, qf, tbu, q_on); break;
+        case 0: loc_phase2<0, need_q>(B, sm.ops, qf, tbu, tlu, q_on, last); break;
+        case 1: loc_phase2<1, need_q>(B, sm.ops, qf, tbu, tlu, q_on, last); break;
+        case 2: loc_phase2<2, need_q>(B, sm.ops, qf, tbu, tlu, q_on, last); break;
+        default: loc_phase2<3, need_q>(B, sm.ops, qf, tbu, tlu, q_on, last); break;
       }
     };
     // the stores of chunk j's outputs (j >= w0); the gated norm's weight of columns 8 fb .. 8 fb + 7
@@ -1351,10 +1403,12 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
       }
       tbu[0] = cur.tb[0];
       tbu[1] = cur.tb[1];
+      tlu[0] = cur.tl[0];
+      tlu[1] = cur.tl[1];
       if (kPass == 0) norm_out(c - 1);
       if (kNorm) norm_req_z(c);
       lds_barrier();
-      phase2(sm.buf[(c + 1) & 1], c + 1 >= w0);
+      phase2(sm.buf[(c + 1) & 1], c + 1 >= w0, c + 1 == last_c);
       lds_barrier();
     };
     if (combine_steps > 0) {
@@ -1396,9 +1450,11 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
       loc_phase1<need_q>(sm.buf[0], ia, chunk_len(0), use_l2, w0 == 0, qf);
       tbu[0] = ia.tb[0];
       tbu[1] = ia.tb[1];
+      tlu[0] = ia.tl[0];
+      tlu[1] = ia.tl[1];
     }
     lds_barrier();
-    if (ntot > 0) phase2(sm.buf[0], w0 == 0);
+    if (ntot > 0) phase2(sm.buf[0], w0 == 0, last_c == 0);
     lds_barrier();
     int c = 0;
     for (; c + 2 < ntot; c += 2) {
@@ -1507,15 +1563,16 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
       const SegBuf& B = sm.buf[c & 1];
       constexpr bool late = kNorm == 0;
       const bool precise = chunk_precise(B);
-      if (kPass == 0 && c >= w0) {
-        if (precise) chain_part1<true, true, late, true>(B, sm.ops, R, wc, lane);
-        else chain_part1<true, true, late, false>(B, sm.ops, R, wc, lane);
-      } else if (mode != kSegA) {
-        if (precise) chain_part1<true, false, late, true>(B, sm.ops, R, wc, lane);
-        else chain_part1<true, false, late, false>(B, sm.ops, R, wc, lane);
-      } else {
-        if (precise) chain_part1<false, false, late, true>(B, sm.ops, R, wc, lane);
-        else chain_part1<false, false, late, false>(B, sm.ops, R, wc, lane);
+      if (kPass == 0 && c >= w0) {  // (a precise chunk takes T's lo part; otherwise only the sequence's last)
+        if (precise) chain_part1<true, true, late, true, true>(B, sm.ops, R, wc, lane);
+        else if (c == last_c) chain_part1<true, true, late, false, true>(B, sm.ops, R, wc, lane);
+        else chain_part1<true, true, late, false, false>(B, sm.ops, R, wc, lane);
+      } else if (mode != kSegA) {  // (no chunk here is a sequence's last with outputs)
+        if (precise) chain_part1<true, false, late, true, true>(B, sm.ops, R, wc, lane);
+        else chain_part1<true, false, late, false, false>(B, sm.ops, R, wc, lane);
+      } else {  // (no U)
+        if (precise) chain_part1<false, false, late, true, false>(B, sm.ops, R, wc, lane);
+        else chain_part1<false, false, late, false, false>(B, sm.ops, R, wc, lane);
       }
       lds_barrier();
       chain_part2<late>(B, R, lane);

@@ -157,7 +157,8 @@ int gdn_chunk_prefill_generic(const void* q, int64_t q_stride, const void* k, in
  * sequences and Hv value heads (-1 for bad sizes): the segment table and flags (a few bytes per
  * sequence and per segment), the fp32 transition maps of the segments that have a successor (at
  * most 32 MiB: sequences are cut into segments so that at most about 256 (segment, value head)
- * items exist) and the intra-chunk inverse's output (5.5 KiB per (chunk, value head)).
+ * items exist) and the intra-chunk inverse's output (10.5 KiB per (chunk, value head): T diag(beta) as
+ * bf16 hi + lo, and the K row factors and g).
  */
 int64_t gdn_chunk_prefill_workspace_bytes(int64_t total_chunks, int nseq, int Hv);
 
@@ -277,11 +278,11 @@ int gdn_chunk_prefill_rows_gated(const void* q, int64_t q_stride, const void* k,
  * workspace is a static device array of GDN_NOALLOC_SCRATCH_BYTES (256 MiB) that the library holds on
  * every GPU it runs on until the process ends.  A call whose
  * gdn_chunk_prefill_workspace_bytes(total_chunks, nseq, Hv) exceeds it is rejected with GDN_EINVAL
- * before any launch (the workspace is at most about 32 MiB plus 5.5 KiB per (chunk, value head): 256 MiB
- * holds e.g. 81,920 tokens at Hv = 32).  Every
+ * before any launch (the workspace is at most about 32 MiB plus 10.5 KiB per (chunk, value head): 256 MiB
+ * holds e.g. 44,416 tokens at Hv = 32).  Every
  * call on one GPU shares that GPU's array: calls that overlap on one GPU (other streams, other host
  * threads) race and give wrong results -- order them on one stream.  The array needs no clearing
- * (every record a call reads, the same call writes first).
+ * (every record a call uses, the same call writes first).
  * No counterpart in the reference: for callers that cannot allocate (code under HIP graph capture,
  * serving loops, harnesses that forbid hipMalloc).
  */

@@ -391,16 +391,16 @@ def gdn_prefill_core(mixed_qkv, z, a, b, conv_weight, A_log, dt_bias, norm_weigh
         mixed, cstate = causal_conv1d_prefill(x, conv_weight, conv_bias, hist)
         mixed = mixed.transpose(1, 2)
         query, key, value = torch.split(mixed, [kd, kd, num_v_heads * head_dim], dim=-1)
-        query = query.reshape(1, L, -1, head_dim)
-        key = key.reshape(1, L, -1, head_dim)
-        value = value.reshape(1, L, -1, head_dim)
+        query = query.reshape(1, L, num_k_heads, head_dim)
+        key = key.reshape(1, L, num_k_heads, head_dim)
+        value = value.reshape(1, L, num_v_heads, head_dim)
         beta, g = gdn_gating(a[lo:hi].unsqueeze(0), b[lo:hi].unsqueeze(0), A_log, dt_bias)
         query, key = expand_key_heads(query, r), expand_key_heads(key, r)
         init = None if initial_state is None else initial_state[s:s + 1]
         core, last = chunk_gated_delta_rule_v2(query, key, value, g, beta, chunk_size, init, True, True)
         core = gated_rmsnorm(core.reshape(-1, head_dim), z[lo:hi].reshape(-1, head_dim),
                              norm_weight, eps)
-        cores.append(core.reshape(L, -1))
+        cores.append(core.reshape(L, num_v_heads * head_dim))
         convs.append(cstate.to(mixed_qkv.dtype))
         recs.append(last)
     return torch.cat(cores, 0), torch.cat(convs, 0), torch.cat(recs, 0)

@@ -188,3 +188,31 @@ def test_gating_matches_transformers_layer(oracle):
         g_ref = -m.A_log.float().exp() * torch.nn.functional.softplus(a.float() + m.dt_bias)
         beta, g = oracle.gdn_gating(a, b, m.A_log, m.dt_bias)
     assert torch.equal(beta, beta_ref) and torch.equal(g, g_ref)
+
+
+def test_prefill_core_empty_prompt(oracle):
+    """An empty prompt in a packed batch: no outputs, its conv state is its history and its recurrent
+    state its initial state, bit for bit; the prompts around it are unchanged by its presence."""
+    D, Hk, Hv, K = 16, 2, 4, 4
+    C = (2 * Hk + Hv) * D
+    g_ = torch.Generator().manual_seed(5)
+    lens = [7, 0, 20]
+    T = sum(lens)
+    mixed = torch.randn(T, C, generator=g_).to(torch.bfloat16)
+    z = torch.randn(T, Hv * D, generator=g_).to(torch.bfloat16)
+    a = torch.randn(T, Hv, generator=g_).to(torch.bfloat16)
+    b = torch.randn(T, Hv, generator=g_).to(torch.bfloat16)
+    cw = (0.5 * torch.randn(C, K, generator=g_)).to(torch.bfloat16)
+    A_log, dt, nw = torch.randn(Hv, generator=g_), torch.randn(Hv, generator=g_), torch.ones(D)
+    hist = torch.randn(3, C, K, generator=g_).to(torch.bfloat16)
+    s0 = 0.1 * torch.randn(3, Hv, D, D, generator=g_)
+    cu = torch.tensor([0, 7, 7, 27], dtype=torch.int32)
+    core, conv, rec = oracle.gdn_prefill_core(mixed, z, a, b, cw, A_log, dt, nw, Hk, Hv, D, cu_seqlens=cu,
+                                              conv_history=hist, initial_state=s0)
+    assert core.shape == (T, Hv * D)
+    assert torch.equal(conv[1], hist[1]) and torch.equal(rec[1], s0[1])
+    keep = torch.tensor([0, 2])
+    cu2 = torch.tensor([0, 7, 27], dtype=torch.int32)
+    core2, conv2, rec2 = oracle.gdn_prefill_core(mixed, z, a, b, cw, A_log, dt, nw, Hk, Hv, D, cu_seqlens=cu2,
+                                                 conv_history=hist[keep], initial_state=s0[keep])
+    assert torch.equal(core, core2) and torch.equal(conv[keep], conv2) and torch.equal(rec[keep], rec2)

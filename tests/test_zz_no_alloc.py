@@ -58,7 +58,7 @@ def test_noalloc_prefill_matches_workspace_entry_point(gdn, dev):
         o, f = _call(L, "gdn_chunk_prefill_noalloc", q, k, v, g, beta, s0, cu, c0, total, Hk, Hv)
         torch.cuda.synchronize()
         assert torch.equal(o, o_ref) and torch.equal(f, f_ref), f"lens {lens}"
-    # beyond the scratch (5.5 KiB of inverse records per (chunk, value head)): refused on the host
+    # beyond the scratch (10.5 KiB of inverse records per (chunk, value head)): refused on the host
     # before any launch
     with pytest.raises(L.GDNError, match="static scratch holds"):
         _call(L, "gdn_chunk_prefill_noalloc", q, k, v, g, beta, s0, cu, c0, 20_000, Hk, Hv)
