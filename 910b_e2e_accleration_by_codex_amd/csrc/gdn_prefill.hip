@@ -272,13 +272,14 @@ constexpr float kWarmLog = -11.0904f;        // ln(2^-16)
 // W S = Wh Sh + Wh Sl + Wl Sh (about 16 significant bits); a chunk with faster decay forgets that
 // rounding within a chunk or two and keeps the single bf16 product.
 constexpr float kPreciseGl = 0.0183156389f;  // e^-4
-// T diag(beta) (the inverse kernel's record) also enters U and W as hi + lo in such a chunk and in a
-// sequence's last chunk.  With a head's keys sharing a large common part (a conv bias, say) the bf16
-// rounding of the record alone moved states by 1e-3 to 2e-3 relative: in a long-memory head it builds
-// up over the chunks, and in a fast-decaying head the last chunk's U makes most of the final state
-// (5e-6 with the lo part; chunks of faster decay are forgotten before they matter).  The inverse
-// kernel writes the lo part of every chunk whose G_last is above -4.5 -- a margin on the output
-// pass's test, which scans the same g values the same way -- and of every sequence's last chunk.
+// T diag(beta) (the inverse kernel's record) enters U and W as bf16 hi + lo in every chunk whose part
+// of the final state is not negligible: a precise chunk, and one after which the decay up to the
+// sequence's end sums to more than -4.5 (a sequence's last chunk, and the one before a short last
+// chunk).  With a head's keys sharing a large common part (a conv bias, say), or beta in fp32 (a
+// non-bf16 diagonal), the record's bf16 rounding alone moved states by 1e-3 to 2e-3 relative: in a
+// long-memory head it builds up over the chunks, in a fast-decaying head the last chunks' U make most
+// of the final state.  The inverse kernel decides, writes the lo part and sets a flag in the chunk's
+// second record; the output pass follows the flag.
 constexpr float kLoRecordLog = -4.5f;
 constexpr int kTrans = 2 * pf::D * pf::D;    // floats per (slot, head): A, then B
 }  // namespace sg
@@ -410,14 +411,20 @@ __global__ __launch_bounds__(256) void seg_table_kernel(const int32_t* __restric
 // columns scaled by e^G, K (W = T diag(beta e^G) K).  One wave owns one (chunk, value head) and
 // keeps everything in registers: no LDS round trips of intermediate products and no barriers.
 typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+// The inverse kernel's second record per (chunk, value head): the K rows' l2norm factors, the chunk's
+// g values (both fp32, by token) and a flag word (nonzero: the T record's lo part was written).
+namespace kr {
+constexpr int FLAG = 2 * pf::CH;      // float index of the flag word
+constexpr int FLOATS = 2 * pf::CH + 4;  // 528 bytes: 16-byte aligned records
+}  // namespace kr
 namespace tf {
 constexpr int FRAGS = 6;                      // lower fragments of T diag(beta)
 __device__ __forceinline__ int fid(int w, int s) { return w < 2 ? w : 2 * w - 2 + s; }
 // In memory the bf16 hi part is 5 KiB: fragments 0 = (0, 0) and 3 = (2, 1) straddle the diagonal,
 // their second 16-column block is zero, and they keep only the first 8 bytes of each lane (512 B);
 // the other four keep 16 bytes a lane.  Byte offsets 0, 512, 1536, 2560, 3072, 4096.  The lo part
-// (T diag(beta) - hi, rounded to bf16) follows in the same layout, written only for a chunk of slight
-// decay and a sequence's last chunk (sg::kLoRecordLog).
+// (T diag(beta) - hi, rounded to bf16) follows in the same layout, written only where the flag in the
+// chunk's second record (kr::FLAG) is set.
 constexpr int HALF = 5 * ws::FRAG;
 constexpr int BYTES = 2 * HALF;
 __host__ __device__ __forceinline__ constexpr bool half(int f) { return f == 0 || f == 3; }
@@ -457,6 +464,20 @@ __device__ int chunk_warm(const float* __restrict__ g, const BetaT* __restrict__
     }
   }
   return 0;
+}
+
+// Whether the summed g of tokens t_from .. t_end - 1 (one head) stays above thr: the decay a chunk's
+// contribution to the state still meets before its sequence ends (one wave, 64 tokens a step, stopping
+// as soon as the sum falls below thr).
+__device__ bool tail_decay_above(const float* __restrict__ g, int Hv, int h, int64_t t_from, int64_t t_end, float thr) {
+  const int lane = threadIdx.x & 63;
+  float acc = 0.f;
+  for (int64_t t0 = t_from; t0 < t_end; t0 += 64) {
+    const int64_t tok = t0 + lane;
+    acc += wave_sum_fast(tok < t_end ? g[tok * Hv + h] : 0.f);
+    if (!(acc > thr)) return false;
+  }
+  return true;
 }
 
 // Workgroup order -> item order.  The 8 XCDs take workgroups b % 8 in turn; this bijection on [0, n),
@@ -532,7 +553,7 @@ __global__ __launch_bounds__(pf::NT, 2) void inv_kernel(const uint16_t* __restri
         for (int s = 0; s < 4; ++s) kf[tt][s] = scale_bf16(kf[tt][s], invc[tt]);
       }
     }
-    float* rec = knorm + ((int64_t)slot * Hv + h) * (2 * CH);
+    float* rec = knorm + ((int64_t)slot * Hv + h) * kr::FLOATS;
     if (use_l2) rec[lane] = mine;
     rec[CH + lane] = graw;  // the chunk's g of this head, contiguous for the segment kernel
   }
@@ -586,7 +607,14 @@ __global__ __launch_bounds__(pf::NT, 2) void inv_kernel(const uint16_t* __restri
     }
   f32x4 TT[10];
   reg_inv64(XT, Xd, TT, strp[w], lane);
-  const bool lo_rec = sdec[w][0][CH - 1] > sg::kLoRecordLog || cp.c + 1 == tab.nch(cp.seq);  // (wave-uniform)
+  // (the output pass's own test for a precise chunk is part of it, on the same G_last, so a precise
+  // chunk always has its lo part)
+  const float Gl = sdec[w][0][CH - 1];  // G_last (wave-uniform)
+  bool lo_rec = __expf(Gl) > sg::kPreciseGl || Gl > sg::kLoRecordLog;
+  if (!lo_rec)
+    lo_rec = tail_decay_above(g, Hv, h, cp.t0 + cp.len, tab.start(cp.seq) + tab.len(cp.seq), sg::kLoRecordLog);
+  if (lane == 0)
+    reinterpret_cast<int*>(knorm)[((int64_t)slot * Hv + h) * kr::FLOATS + kr::FLAG] = lo_rec ? 1 : 0;
   // fragments (w', s), s <= w' / 2: element e of lane (i, g) = T[16 w' + i][j] beta_j with
   // j = 32 s + kpos(8 g + e), kpos(8 g + e) = 16 (e >> 2) + 4 g + (e & 3): blocks 2s (e < 4) and 2s + 1
   uint8_t* dst = tfrag + ((int64_t)slot * Hv + h) * tf::BYTES;
@@ -681,6 +709,7 @@ struct alignas(16) SegBuf {
   float eg[pf::CH];               // e^{G_t}
   float egs[pf::CH];              // scale e^{G_t}
   float gl;                       // e^{G_last}
+  int lof;                        // T diag(beta)'s lo part is in the chunk's record (and the chain takes it)
 };
 // The operands the local waves form after the step's first barrier and the chain reads before the
 // next step's first barrier (-W and QK) are single: the local waves write chunk c + 1's while the
@@ -723,6 +752,7 @@ struct LocIn {
   bf16x8 tb[2], tl[2];  // T diag(beta) fragments: bf16 hi, and lo (written for chunks of slight decay only)
   f32x4 kn;  // the inverse kernel's l2norm factors of K rows 4 tq .. 4 tq + 3
   float graw;
+  int lof;   // the T record's lo part was written
 };
 // Parts of a chunk's loads, and of phase 1 (kPart < 0: all): 0 the K rows and their l2norm factors,
 // 1 the V rows and the T diag(beta) fragments, 2 the q rows, 3 the g values.  The chunk loop
@@ -732,7 +762,8 @@ template <bool kNeedQ, int kPart = -1>
 __device__ __forceinline__ void loc_load(LocIn& L, int64_t t0, int len, int kh, int h,
                                          const uint16_t* __restrict__ k, uint32_t ks, const uint16_t* __restrict__ q,
                                          uint32_t qs, const uint16_t* __restrict__ v, uint32_t vs,
-                                         const uint8_t* __restrict__ tfr, const float* __restrict__ knc, bool q_on) {
+                                         const uint8_t* __restrict__ tfr, const float* __restrict__ knc, bool q_on,
+                                         bool want_lo) {
   using namespace pf;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const uint32_t tq = t >> 4, fb = t & 15;
@@ -763,7 +794,9 @@ __device__ __forceinline__ void loc_load(LocIn& L, int64_t t0, int len, int kh, 
       const int f = tf::fid(w, s);
       const bool hf = tf::half(f);
       u32x4 x = *reinterpret_cast<const u32x4*>(tfr + (uint32_t)(tf::offset(f) + lane * (hf ? 8 : 16)));
-      u32x4 y = *reinterpret_cast<const u32x4*>(tfr + (uint32_t)(tf::HALF + tf::offset(f) + lane * (hf ? 8 : 16)));
+      // the lo half where the chunk's flag says it was written, else the hi half again (the same
+      // loads, from lines just read: every path issues the same instructions)
+      u32x4 y = *reinterpret_cast<const u32x4*>(tfr + (uint32_t)((want_lo ? tf::HALF : 0) + tf::offset(f) + lane * (hf ? 8 : 16)));
       if (hf) x[2] = x[3] = y[2] = y[3] = 0u;
       L.tb[s] = __builtin_bit_cast(bf16x8, x);
       L.tl[s] = __builtin_bit_cast(bf16x8, y);
@@ -781,7 +814,10 @@ __device__ __forceinline__ void loc_load(LocIn& L, int64_t t0, int len, int kh, 
     }
   }
   if (kPart < 0 || kPart == 3)  // g of token `lane` (the last token's past the end), from the inverse kernel's record
+  {
     L.graw = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(knc) + (pf::CH + lane) * 4u);
+    L.lof = *reinterpret_cast<const int*>(reinterpret_cast<const char*>(knc) + kr::FLAG * 4u);
+  }
 }
 
 // Whether a chunk's W S runs in hi + lo (its e^{G_last} above e^-2), read as a wave-uniform value so
@@ -789,6 +825,8 @@ __device__ __forceinline__ void loc_load(LocIn& L, int64_t t0, int len, int kh, 
 __device__ __forceinline__ bool chunk_precise(const SegBuf& B) {
   return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(B.gl))) > sg::kPreciseGl;
 }
+// Whether the chunk takes T diag(beta) as hi + lo (the inverse kernel's flag), wave-uniform.
+__device__ __forceinline__ bool chunk_tlo(const SegBuf& B) { return __builtin_amdgcn_readfirstlane(B.lof) != 0; }
 
 // Local phase 1 (wave w < 4): K rows (masked, l2-normalised when asked), V rows and the T diag(beta)
 // fragments into the buffer, the q fragments (masked, l2-normalised when asked; kept in qf for
@@ -852,7 +890,10 @@ __device__ __forceinline__ void loc_phase1(SegBuf& B, const LocIn& in, int len, 
     B.dec[lane] = __expf(gl - G);
     B.eg[lane] = eg;
     B.egs[lane] = kScale * eg;
-    if (lane == 0) B.gl = __expf(gl);
+    if (lane == 0) {
+      B.gl = __expf(gl);
+      B.lof = in.lof;
+    }
   }
 }
 
@@ -863,12 +904,12 @@ __device__ __forceinline__ void loc_phase1(SegBuf& B, const LocIn& in, int len, 
 // 32 s + 16 (e >> 2) + 4 g + (e & 3)).
 template <int W, bool kNeedQ>
 __device__ __forceinline__ void loc_phase2(const SegBuf& B, SegOps& P, const bf16x8 (&qf)[4], const bf16x8 (&tbu)[2],
-                                           const bf16x8 (&tlu)[2], bool q_on, bool last) {
+                                           const bf16x8 (&tlu)[2], bool q_on) {
   using namespace pf;
   int t;
   asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"((int)threadIdx.x));
   const int lane = t & 63, c16 = lane & 15, g4 = lane >> 4;
-  const bool precise = chunk_precise(B), tlo = precise || last;
+  const bool precise = chunk_precise(B), tlo = chunk_tlo(B);
   bf16x8 tbe[2], tbl[2];  // T diag(beta e^G), and in a precise chunk the lo part of its fp32 value
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
@@ -1335,7 +1376,6 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
   const int w0 = (kPass == 0 && warm_path) ? warm[(int64_t)slot * Hv + h] : 0;
   const int cb0 = c_begin - w0, ntot = n + w0;
   const int chunk_slot0 = tab.first_chunk(s) + cb0;
-  const int last_c = cb0 + ntot == nch_s ? ntot - 1 : -1;  // the sequence's last chunk, if in this walk
   auto tfr = [&](int c) { return tfrag + ((int64_t)(chunk_slot0 + c) * Hv + h) * tf::BYTES; };
   auto chunk_t0 = [&](int c) { return t_seq + (int64_t)(cb0 + c) * CH; };
   auto chunk_len = [&](int c) { return Ls - (cb0 + c) * CH < CH ? Ls - (cb0 + c) * CH : CH; };
@@ -1347,17 +1387,24 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     // the end the last chunk is requested again, unused), which keeps the wait counts exact.
     LocIn ia, ib;
     bf16x8 qf[4], tbu[2], tlu[2];
-    auto load = [&](LocIn& L, int c, auto part) __attribute__((always_inline)) {
+    auto load = [&](LocIn& L, int c, auto part, bool want_lo) __attribute__((always_inline)) {
       loc_load<need_q, decltype(part)::value>(L, chunk_t0(c), chunk_len(c), kh, h, k, (uint32_t)ks, q, (uint32_t)qs, v,
                                               (uint32_t)vs, tfr(c),
-                                              knorm + ((int64_t)(chunk_slot0 + c) * Hv + h) * (2 * CH), c >= w0);
+                                              knorm + ((int64_t)(chunk_slot0 + c) * Hv + h) * kr::FLOATS, c >= w0,
+                                              want_lo);
     };
-    auto phase2 = [&](const SegBuf& B, bool q_on, bool last) __attribute__((always_inline)) {
+    // chunk c's lo flag (the inverse kernel's): read a step before the chunk's own loads need it
+    auto lo_flag = [&](int c) __attribute__((always_inline)) {
+      const int cc = c < ntot ? c : ntot - 1;
+      return reinterpret_cast<const int*>(knorm)[((int64_t)(chunk_slot0 + cc) * Hv + h) * kr::FLOATS + kr::FLAG] != 0;
+    };
+    bool lof_next = false;  // chunk c + 2's flag in step c
+    auto phase2 = [&](const SegBuf& B, bool q_on) __attribute__((always_inline)) {
       switch (w) {
-        case 0: loc_phase2<0, need_q>(B, sm.ops, qf, tbu, tlu, q_on, last); break;
-        case 1: loc_phase2<1, need_q>(B, sm.ops, qf, tbu, tlu, q_on, last); break;
-        case 2: loc_phase2<2, need_q>(B, sm.ops, qf, tbu, tlu, q_on, last); break;
-        default: loc_phase2<3, need_q>(B, sm.ops, qf, tbu, tlu, q_on, last); break;
+        case 0: loc_phase2<0, need_q>(B, sm.ops, qf, tbu, tlu, q_on); break;
+        case 1: loc_phase2<1, need_q>(B, sm.ops, qf, tbu, tlu, q_on); break;
+        case 2: loc_phase2<2, need_q>(B, sm.ops, qf, tbu, tlu, q_on); break;
+        default: loc_phase2<3, need_q>(B, sm.ops, qf, tbu, tlu, q_on); break;
       }
     };
     // the stores of chunk j's outputs (j >= w0); the gated norm's weight of columns 8 fb .. 8 fb + 7
@@ -1383,21 +1430,23 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
                                                           // chunk c + 1's V rows replace them
       {  // chunk c + 2's load parts interleaved with chunk c + 1's phase-1 parts
         const int cn = c + 2 < ntot ? c + 2 : ntot - 1;
+        const bool want_lo = lof_next;
+        lof_next = lo_flag(c + 3);
         SegBuf& B1 = sm.buf[(c + 1) & 1];
         const int len1 = chunk_len(c + 1);
-        load(nxt, cn, std::integral_constant<int, 0>{});
+        load(nxt, cn, std::integral_constant<int, 0>{}, want_lo);
         __builtin_amdgcn_sched_barrier(0);
         loc_phase1<need_q, 0>(B1, cur, len1, use_l2, c + 1 >= w0, qf);
         __builtin_amdgcn_sched_barrier(0);
-        load(nxt, cn, std::integral_constant<int, 1>{});
+        load(nxt, cn, std::integral_constant<int, 1>{}, want_lo);
         __builtin_amdgcn_sched_barrier(0);
         loc_phase1<need_q, 1>(B1, cur, len1, use_l2, c + 1 >= w0, qf);
         __builtin_amdgcn_sched_barrier(0);
-        load(nxt, cn, std::integral_constant<int, 2>{});
+        load(nxt, cn, std::integral_constant<int, 2>{}, want_lo);
         __builtin_amdgcn_sched_barrier(0);
         loc_phase1<need_q, 2>(B1, cur, len1, use_l2, c + 1 >= w0, qf);
         __builtin_amdgcn_sched_barrier(0);
-        load(nxt, cn, std::integral_constant<int, 3>{});
+        load(nxt, cn, std::integral_constant<int, 3>{}, want_lo);
         __builtin_amdgcn_sched_barrier(0);
         loc_phase1<need_q, 3>(B1, cur, len1, use_l2, c + 1 >= w0, qf);
       }
@@ -1408,7 +1457,7 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
       if (kPass == 0) norm_out(c - 1);
       if (kNorm) norm_req_z(c);
       lds_barrier();
-      phase2(sm.buf[(c + 1) & 1], c + 1 >= w0, c + 1 == last_c);
+      phase2(sm.buf[(c + 1) & 1], c + 1 >= w0);
       lds_barrier();
     };
     if (combine_steps > 0) {
@@ -1445,8 +1494,9 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     }
     if (ntot > 0) {
       if (kNorm) norm_req_z(-1);  // unused: every step then finds one z request in flight
-      load(ia, 0, std::integral_constant<int, -1>{});
-      load(ib, ntot > 1 ? 1 : 0, std::integral_constant<int, -1>{});
+      load(ia, 0, std::integral_constant<int, -1>{}, lo_flag(0));
+      load(ib, ntot > 1 ? 1 : 0, std::integral_constant<int, -1>{}, lo_flag(1));
+      lof_next = lo_flag(2);
       loc_phase1<need_q>(sm.buf[0], ia, chunk_len(0), use_l2, w0 == 0, qf);
       tbu[0] = ia.tb[0];
       tbu[1] = ia.tb[1];
@@ -1454,7 +1504,7 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
       tlu[1] = ia.tl[1];
     }
     lds_barrier();
-    if (ntot > 0) phase2(sm.buf[0], w0 == 0, last_c == 0);
+    if (ntot > 0) phase2(sm.buf[0], w0 == 0);
     lds_barrier();
     int c = 0;
     for (; c + 2 < ntot; c += 2) {
@@ -1562,13 +1612,14 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     for (int c = 0; c < ntot; ++c) {
       const SegBuf& B = sm.buf[c & 1];
       constexpr bool late = kNorm == 0;
-      const bool precise = chunk_precise(B);
-      if (kPass == 0 && c >= w0) {  // (a precise chunk takes T's lo part; otherwise only the sequence's last)
+      const bool precise = chunk_precise(B), tlo = chunk_tlo(B);  // (a precise chunk has tlo)
+      if (kPass == 0 && c >= w0) {
         if (precise) chain_part1<true, true, late, true, true>(B, sm.ops, R, wc, lane);
-        else if (c == last_c) chain_part1<true, true, late, false, true>(B, sm.ops, R, wc, lane);
+        else if (tlo) chain_part1<true, true, late, false, true>(B, sm.ops, R, wc, lane);
         else chain_part1<true, true, late, false, false>(B, sm.ops, R, wc, lane);
-      } else if (mode != kSegA) {  // (no chunk here is a sequence's last with outputs)
+      } else if (mode != kSegA) {
         if (precise) chain_part1<true, false, late, true, true>(B, sm.ops, R, wc, lane);
+        else if (tlo) chain_part1<true, false, late, false, true>(B, sm.ops, R, wc, lane);
         else chain_part1<true, false, late, false, false>(B, sm.ops, R, wc, lane);
       } else {  // (no U)
         if (precise) chain_part1<false, false, late, true, false>(B, sm.ops, R, wc, lane);
@@ -1991,7 +2042,7 @@ SegLayout seg_layout(int64_t total_chunks, int nseq, int Hv) {
   l.off_trans = l.off_warm + up(l.nslots * Hv * 4);
   l.off_tfrag = l.off_trans + l.nslots * Hv * (int64_t)sg::kTrans * 4;
   l.off_knorm = l.off_tfrag + total_chunks * Hv * (int64_t)tf::BYTES;
-  l.bytes = l.off_knorm + total_chunks * Hv * (int64_t)(2 * pf::CH * 4);
+  l.bytes = l.off_knorm + total_chunks * Hv * (int64_t)(kr::FLOATS * 4);
   return l;
 }
 }  // namespace
@@ -2128,7 +2179,7 @@ __global__ __launch_bounds__(256) void inv_records_expand_kernel(const uint8_t* 
     }
     row[j] = x;
   }
-  if (factor_out) factor_out[item * 64 + lane] = knorm[item * 2 * pf::CH + lane];
+  if (factor_out) factor_out[item * 64 + lane] = knorm[item * kr::FLOATS + lane];
 }
 
 extern "C" int gdn_chunk_prefill_rows(const void* q, int64_t q_stride, const void* k, int64_t k_stride,

@@ -158,7 +158,7 @@ int gdn_chunk_prefill_generic(const void* q, int64_t q_stride, const void* k, in
  * sequence and per segment), the fp32 transition maps of the segments that have a successor (at
  * most 32 MiB: sequences are cut into segments so that at most about 256 (segment, value head)
  * items exist) and the intra-chunk inverse's output (10.5 KiB per (chunk, value head): T diag(beta) as
- * bf16 hi + lo, and the K row factors and g).
+ * bf16 hi + lo, the K row factors, g and a flag).
  */
 int64_t gdn_chunk_prefill_workspace_bytes(int64_t total_chunks, int nseq, int Hv);
 
