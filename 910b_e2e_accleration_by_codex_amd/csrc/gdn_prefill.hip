@@ -468,11 +468,15 @@ __device__ int chunk_warm(const float* __restrict__ g, const BetaT* __restrict__
 
 // Whether the summed g of tokens t_from .. t_end - 1 (one head) stays above thr: the decay a chunk's
 // contribution to the state still meets before its sequence ends (one wave, 64 tokens a step, stopping
-// as soon as the sum falls below thr).
-__device__ bool tail_decay_above(const float* __restrict__ g, int Hv, int h, int64_t t_from, int64_t t_end, float thr) {
+// as soon as the sum falls below thr).  The caller loads the first step's g (this lane's token
+// t_from + lane, 0 past t_end) with its other loads: in a fast-decaying head that step decides.
+__device__ bool tail_decay_above(const float* __restrict__ g, int Hv, int h, int64_t t_from, int64_t t_end, float thr,
+                                 float g_first) {
   const int lane = threadIdx.x & 63;
-  float acc = 0.f;
-  for (int64_t t0 = t_from; t0 < t_end; t0 += 64) {
+  if (t_from >= t_end) return true;
+  float acc = wave_sum_fast(g_first);
+  if (!(acc > thr)) return false;
+  for (int64_t t0 = t_from + 64; t0 < t_end; t0 += 64) {
     const int64_t tok = t0 + lane;
     acc += wave_sum_fast(tok < t_end ? g[tok * Hv + h] : 0.f);
     if (!(acc > thr)) return false;
@@ -527,6 +531,9 @@ __global__ __launch_bounds__(pf::NT, 2) void inv_kernel(const uint16_t* __restri
   const int tok = lane < cp.len ? lane : cp.len - 1;
   const float graw = g[(cp.t0 + tok) * Hv + h];
   const float braw = Elem<BetaT>::load(beta + (cp.t0 + tok) * Hv + h);
+  // the first 64 tokens after the chunk (same sequence): the tail decay's first step
+  const int64_t t_tail = cp.t0 + cp.len, t_end = tab.start(cp.seq) + tab.len(cp.seq);
+  const float gtail = t_tail + lane < t_end ? g[(t_tail + lane) * Hv + h] : 0.f;
   // rows past the chunk's end are zero; with use_l2, each row's l2norm factor bf16(rsqrt(...)) with
   // torch's bf16 op rounding (a row sits in the lanes c, c + 16, c + 32, c + 48), and the rows
   // scaled by it and rounded to bf16: the reference's normalised rows, bit for bit, as the segment
@@ -612,7 +619,7 @@ __global__ __launch_bounds__(pf::NT, 2) void inv_kernel(const uint16_t* __restri
   const float Gl = sdec[w][0][CH - 1];  // G_last (wave-uniform)
   bool lo_rec = __expf(Gl) > sg::kPreciseGl || Gl > sg::kLoRecordLog;
   if (!lo_rec)
-    lo_rec = tail_decay_above(g, Hv, h, cp.t0 + cp.len, tab.start(cp.seq) + tab.len(cp.seq), sg::kLoRecordLog);
+    lo_rec = tail_decay_above(g, Hv, h, t_tail, t_end, sg::kLoRecordLog, gtail);
   if (lane == 0)
     reinterpret_cast<int*>(knorm)[((int64_t)slot * Hv + h) * kr::FLOATS + kr::FLAG] = lo_rec ? 1 : 0;
   // fragments (w', s), s <= w' / 2: element e of lane (i, g) = T[16 w' + i][j] beta_j with
