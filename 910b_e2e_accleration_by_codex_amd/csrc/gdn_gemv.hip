@@ -13,6 +13,9 @@
 //     workgroup is 4 waves.  When N alone gives too few waves to fill the chip, K is split over
 //     blockIdx.y and fp32 partial sums go through a workspace and a small reduction kernel.
 //   * each wave keeps PF k steps of loads in flight ahead of its MFMAs (a ring of register buffers).
+//   * W is read once per step: its loads are non-temporal, so the stream does not evict what the
+//     step keeps (x, the partial sums, the states of the other kernels); measured 3-7% faster per
+//     projection than cached loads at the 27B decode shapes.
 #include "gdn_device.h"
 #include "gdn_internal.h"
 
@@ -34,6 +37,10 @@ struct Frag4 {
 __device__ __forceinline__ void load4(Frag4& f, const uint16_t* p) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) f.v[j] = *reinterpret_cast<const u16x8*>(p + 8 * j);
+}
+__device__ __forceinline__ void load4_nt(Frag4& f, const uint16_t* p) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) f.v[j] = __builtin_nontemporal_load(reinterpret_cast<const u16x8*>(p + 8 * j));
 }
 }  // namespace gv
 
@@ -79,9 +86,9 @@ __global__ __launch_bounds__(64 * gv::WAVES) void decode_linear_kernel(
       if (PACKED) {  // block (tile, s): 4 fragments of 64 lanes x 16 bytes, fragment j contiguous
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          a[buf][t].v[j] = *reinterpret_cast<const u16x8*>(wrow[t] + s * (KSTEP * 16) + j * 512);
+          a[buf][t].v[j] = __builtin_nontemporal_load(reinterpret_cast<const u16x8*>(wrow[t] + s * (KSTEP * 16) + j * 512));
       } else {
-        load4(a[buf][t], wrow[t] + k);
+        load4_nt(a[buf][t], wrow[t] + k);
       }
     }
     if (xrow) load4(b[buf], xp + k);
