@@ -1616,10 +1616,14 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     }
     lds_barrier();
     lds_barrier();
+    // chunk c's forms (precise: W S in hi + lo; tlo: T diag(beta) in hi + lo, also set for every
+    // precise chunk), read from its buffer a step ahead: after the barrier that completes the buffer,
+    // so the step starts without waiting on LDS
+    bool precise_n = ntot > 0 && chunk_precise(sm.buf[0]), tlo_n = ntot > 0 && chunk_tlo(sm.buf[0]);
     for (int c = 0; c < ntot; ++c) {
       const SegBuf& B = sm.buf[c & 1];
       constexpr bool late = kNorm == 0;
-      const bool precise = chunk_precise(B), tlo = chunk_tlo(B);  // (a precise chunk has tlo)
+      const bool precise = precise_n, tlo = tlo_n;
       if (kPass == 0 && c >= w0) {
         if (precise) chain_part1<true, true, late, true, true>(B, sm.ops, R, wc, lane);
         else if (tlo) chain_part1<true, true, late, false, true>(B, sm.ops, R, wc, lane);
@@ -1633,6 +1637,10 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
         else chain_part1<false, false, late, false, false>(B, sm.ops, R, wc, lane);
       }
       lds_barrier();
+      if (c + 1 < ntot) {  // chunk c + 1's buffer is complete at this barrier
+        precise_n = chunk_precise(sm.buf[(c + 1) & 1]);
+        tlo_n = chunk_tlo(sm.buf[(c + 1) & 1]);
+      }
       chain_part2<late>(B, R, lane);
       lds_barrier();
     }
