@@ -1011,8 +1011,7 @@ __device__ __forceinline__ void loc_phase2(const SegBuf& B, SegOps& P, const bf1
 // 16-column slices (n = 2 w' + sl), S[sl][i][r] = S[16 i + 4 g + r][16 n + c].
 struct ChainRegs {
   f32x4 S[2][8];
-  bf16x8 hi[2][2], lo[2][2];  // DEC vn, split (by part 1, or by part 2 from vn)
-  f32x4 vn[2][4];             // vn carried from part 1 to part 2 when part 2 splits it
+  bf16x8 hi[2][2], lo[2][2];  // DEC vn, split by part 1 for part 2
 };
 // DEC vn -> hi + lo bf16 (the k-slot ordered B fragments of the update).
 __device__ __forceinline__ void dec_split(const SegBuf& B, f32x4 (&vn)[2][4], ChainRegs& R, int g4) {
@@ -1106,13 +1105,13 @@ __device__ __forceinline__ void norm_store(const NormIn& N, const float (&wt)[8]
 }
 // Chain part 1 for one chunk: U (fp32, from the inverse kernel's T diag(beta) fragments and the V
 // rows), vn = U - W S, the outputs o = diag(scale e^G) Q S + QK vn (kOut: left in bf16 in the V tile
-// for the local waves to store), and DEC vn split for part 2 (kSplitLate: vn itself, split by part 2).  W S and Q S share the loop over the state's k-blocks j
+// for the local waves to store), and DEC vn split for part 2.  W S and Q S share the loop over the state's k-blocks j
 // (16 independent accumulators); the LDS fragments of block j + 1 are requested before the products
 // of block j, so their latency hides behind those products.  kPrecise: W S = Wh Sh + Wh Sl + Wl Sh
 // from the hi + lo parts of -W and of the state; block j's state parts are formed in its step and
 // its -W lo fragments requested there (behind the hi products), which keeps the registers of the
 // fast form.
-template <bool kUseU, bool kOut, bool kSplitLate, bool kPrecise, bool kTlo>
+template <bool kUseU, bool kOut, bool kPrecise, bool kTlo>
 __device__ __forceinline__ void chain_part1(const SegBuf& B, const SegOps& P, ChainRegs& R, int wc, int lane_in) {
   using namespace pf;
   int lane;
@@ -1254,22 +1253,15 @@ __device__ __forceinline__ void chain_part1(const SegBuf& B, const SegOps& P, Ch
         *reinterpret_cast<u32x2v*>(vrow + 16 * tb * LDK + 16 * sl) = pk;
       }
   }
-  if (kSplitLate) {
-#pragma unroll
-    for (int sl = 0; sl < 2; ++sl)
-#pragma unroll
-      for (int tb = 0; tb < 4; ++tb) R.vn[sl][tb] = acc[sl][tb];
-  } else {
-    dec_split(B, acc, R, g4);
-  }
+  // DEC vn is split here, not in part 2: the chain has slack in the step's first half, where the
+  // local waves (phase 1, the outputs' stores or the gated norm) take longer, and none in the
+  // second (T=8192: 1-2% faster than splitting in part 2, 1.4% slower when every chunk takes W S in
+  // hi + lo)
+  dec_split(B, acc, R, g4);
 }
 // Chain part 2: S' = e^{G_last} S + K^T (DEC vn), K^T straight from the K rows (exact in bf16).  For
 // each token half j the hi terms of all 16 accumulators go first, then the lo terms; the K^T
-// fragments of half 1 are requested before the products of half 0.  kSplitLate: DEC vn is formed and
-// split here, while the K^T fragments arrive (the step's first half then holds less of the chain's
-// work: the choice for the output pass without the fused norm, whose local waves finish the first
-// half earlier than the chain).
-template <bool kSplitLate>
+// fragments of half 1 are requested before the products of half 0.
 __device__ __forceinline__ void chain_part2(const SegBuf& B, ChainRegs& R, int lane_in) {
   using namespace pf;
   int lane;
@@ -1280,7 +1272,6 @@ __device__ __forceinline__ void chain_part2(const SegBuf& B, ChainRegs& R, int l
   for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int i = 0; i < 8; ++i) kt[j][i] = __builtin_bit_cast(bf16x8, frag_tr_kperm(B.K, LDK, 32 * j, 16 * i, lane));
-  if (kSplitLate) dec_split(B, R.vn, R, lane >> 4);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -1622,26 +1613,25 @@ __global__ __launch_bounds__(sg::NT, 1) void seg_kernel(
     bool precise_n = ntot > 0 && chunk_precise(sm.buf[0]), tlo_n = ntot > 0 && chunk_tlo(sm.buf[0]);
     for (int c = 0; c < ntot; ++c) {
       const SegBuf& B = sm.buf[c & 1];
-      constexpr bool late = kNorm == 0;
       const bool precise = precise_n, tlo = tlo_n;
       if (kPass == 0 && c >= w0) {
-        if (precise) chain_part1<true, true, late, true, true>(B, sm.ops, R, wc, lane);
-        else if (tlo) chain_part1<true, true, late, false, true>(B, sm.ops, R, wc, lane);
-        else chain_part1<true, true, late, false, false>(B, sm.ops, R, wc, lane);
+        if (precise) chain_part1<true, true, true, true>(B, sm.ops, R, wc, lane);
+        else if (tlo) chain_part1<true, true, false, true>(B, sm.ops, R, wc, lane);
+        else chain_part1<true, true, false, false>(B, sm.ops, R, wc, lane);
       } else if (mode != kSegA) {
-        if (precise) chain_part1<true, false, late, true, true>(B, sm.ops, R, wc, lane);
-        else if (tlo) chain_part1<true, false, late, false, true>(B, sm.ops, R, wc, lane);
-        else chain_part1<true, false, late, false, false>(B, sm.ops, R, wc, lane);
+        if (precise) chain_part1<true, false, true, true>(B, sm.ops, R, wc, lane);
+        else if (tlo) chain_part1<true, false, false, true>(B, sm.ops, R, wc, lane);
+        else chain_part1<true, false, false, false>(B, sm.ops, R, wc, lane);
       } else {  // (no U)
-        if (precise) chain_part1<false, false, late, true, false>(B, sm.ops, R, wc, lane);
-        else chain_part1<false, false, late, false, false>(B, sm.ops, R, wc, lane);
+        if (precise) chain_part1<false, false, true, false>(B, sm.ops, R, wc, lane);
+        else chain_part1<false, false, false, false>(B, sm.ops, R, wc, lane);
       }
       lds_barrier();
       if (c + 1 < ntot) {  // chunk c + 1's buffer is complete at this barrier
         precise_n = chunk_precise(sm.buf[(c + 1) & 1]);
         tlo_n = chunk_tlo(sm.buf[(c + 1) & 1]);
       }
-      chain_part2<late>(B, R, lane);
+      chain_part2(B, R, lane);
       lds_barrier();
     }
     // the state after the segment
