@@ -667,8 +667,9 @@ __global__ __launch_bounds__(pf::NT, 2) void inv_kernel(const uint16_t* __restri
 // described above in LDS (K and q masked and l2-normalised, the decay, Q K^T, -W from the K rows and
 // the inverse kernel's T diag(beta) scaled by e^G) and store the previous chunk's outputs, and its 4
 // chain waves advance 32 columns of the fp32 state each and leave their outputs in LDS.  Only the
-// inverse kernel's records (5 KiB of T fragments and 512 B of K row factors and g per (chunk, value
-// head)) pass through memory besides the inputs and outputs.
+// inverse kernel's records (5 KiB of T fragments, 5 KiB more for their lo parts where a chunk's flag
+// is set, and 528 B of K row factors, g and the flag per (chunk, value head)) pass through memory
+// besides the inputs and outputs.
 // A segment other than the first of its sequence needs its true initial state: the state after
 // segment j is S_{j+1} = A_j S_j + B_j, with A_j the segment's linear map (the chain run from the
 // identity with U = 0) and B_j its affine part (run from zero).  A summary pass computes A_j and
@@ -2030,9 +2031,9 @@ int64_t seg_len(int64_t total_chunks, int nseq, int Hv) {
 // segment), the transition flags (int32 per (slot,
 // value head)), the warm-up lengths (int32 per (slot, value head)), the transition slots (128 KiB per
 // (slot, value head): A's bf16 hi + lo fragments, then B in fp32; layout in namespace tr), the
-// inverse kernel's fragments (5 KiB per (chunk, value head)) and its
-// records of 64 K l2norm factors then the chunk's 64 g values (fp32, 512 B per (chunk, value head)),
-// each part 256-byte aligned.
+// inverse kernel's fragments (10 KiB per (chunk, value head): the bf16 hi half, then the lo half) and
+// its records of 64 K l2norm factors, the chunk's 64 g values and the lo flag (528 B per (chunk, value
+// head)), each part 256-byte aligned.
 struct SegLayout {
   int64_t L, nslots, off_order, off_flags, off_warm, off_trans, off_tfrag, off_knorm, bytes;
 };
