@@ -186,15 +186,6 @@ __device__ __forceinline__ float l2norm_inv(float ss) {
   y = y * (1.5f - 0.5f * x * y * y);
   return rbf(y);
 }
-__device__ __forceinline__ void l2norm_rows4(u16x8* x) {
-  float ss[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) ss[i] = sumsq_bf16(x[i], 0.f);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) ss[i] = row16_sum(ss[i]);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) x[i] = scale_bf16(x[i], l2norm_inv(ss[i]));
-}
 
 // A-fragment of a bf16 [rows, ld] tile in k-slot order (two 8-byte reads).
 __device__ __forceinline__ bf16x8 frag_kperm(const uint16_t* base, int ld, int row0, int k0, int lane) {
